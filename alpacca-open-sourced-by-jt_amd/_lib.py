@@ -1,0 +1,131 @@
+"""ctypes binding of libalpx.so (the gfx950 attention library).
+
+The library is built in-tree by ``csrc/Makefile`` (``__graft_entry__.build``)
+and loaded from this directory.  There is no fallback: if the library or a
+gfx950 device is missing, every entry point raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libalpx.so")
+ABI_VERSION = 1
+
+F32, F16, BF16 = 0, 1, 2
+OK, EINVAL, EUNSUPPORTED, EHIP, ERANGE = 0, -1, -2, -3, -4
+
+_c_int, _c_i64, _c_ptr, _c_size = ctypes.c_int, ctypes.c_int64, ctypes.c_void_p, ctypes.c_size_t
+_c_float = ctypes.c_float
+
+# name -> (restype, argtypes); mirrors include/alpx.h
+SIGNATURES = {
+    "alpx_abi_version": (_c_int, []),
+    "alpx_last_error": (ctypes.c_char_p, []),
+    "alpx_device_arch": (_c_int, [_c_int, ctypes.c_char_p, _c_int]),
+    "alpx_kv_append": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_int, _c_int,
+                                _c_int, _c_int, _c_int, _c_i64, _c_ptr, _c_ptr]),
+    "alpx_decode_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int]),
+    "alpx_decode_gqa": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr,
+                                 _c_ptr, _c_size, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                 _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_float,
+                                 _c_int, _c_int, _c_ptr]),
+    "alpx_sigmoid_gate": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_i64, _c_int, _c_int, _c_ptr]),
+}
+
+
+class AlpxUnavailable(RuntimeError):
+    """The library is not built, fails to load, or no gfx950 device exists."""
+
+
+class AlpxError(RuntimeError):
+    """A HIP runtime failure reported by the library."""
+
+    def __init__(self, message: str, status: int) -> None:
+        super().__init__(message)
+        self.status = status
+
+
+class AlpxUnsupported(ValueError):
+    """Shape/dtype outside what the kernels cover (status ALPX_EUNSUPPORTED)."""
+
+
+_lib = None
+
+
+def lib():
+    """Load libalpx.so once, bind every signature and check the ABI version."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise AlpxUnavailable(
+            f"{LIB_PATH} is not built (run __graft_entry__.build() or make -C csrc)")
+    try:
+        handle = ctypes.CDLL(LIB_PATH)
+    except OSError as exc:  # pragma: no cover - depends on the image
+        raise AlpxUnavailable(f"cannot load {LIB_PATH}: {exc}") from exc
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    version = handle.alpx_abi_version()
+    if version != ABI_VERSION:
+        raise AlpxUnavailable(f"libalpx ABI {version} != expected {ABI_VERSION}")
+    _lib = handle
+    return handle
+
+
+def last_error() -> str:
+    return lib().alpx_last_error().decode("utf-8", "replace")
+
+
+def check(status: int) -> None:
+    """Map a library status to the reference's exception types."""
+    if status == OK:
+        return
+    message = last_error()
+    if status in (EINVAL, ERANGE):
+        raise ValueError(message)
+    if status == EUNSUPPORTED:
+        raise AlpxUnsupported(message)
+    raise AlpxError(message, status)
+
+
+def device_arch(index: int) -> str:
+    buf = ctypes.create_string_buffer(256)
+    check(lib().alpx_device_arch(int(index), buf, len(buf)))
+    return buf.value.decode()
+
+
+def dtype_code(torch, dtype) -> int:
+    if dtype == torch.float32:
+        return F32
+    if dtype == torch.float16:
+        return F16
+    if dtype == torch.bfloat16:
+        return BF16
+    raise TypeError(f"unsupported dtype {dtype}")
+
+
+def stream_handle(torch, device) -> int:
+    """hipStream_t of torch's current stream on ``device``."""
+    return int(torch.cuda.current_stream(device).cuda_stream)
+
+
+_workspaces: dict = {}
+
+
+def workspace(torch, device, nbytes: int):
+    """A grow-only scratch buffer per device, owned by this module.
+
+    Calls that share it are ordered on one stream (the reference's
+    one-caller-at-a-time contract, serve.py:326)."""
+    key = str(device)
+    buf = _workspaces.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+        _workspaces[key] = buf
+    return buf

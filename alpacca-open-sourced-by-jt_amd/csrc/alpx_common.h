@@ -1,0 +1,72 @@
+// Shared device/host helpers for the gfx950 attention library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/alpx.h"
+
+namespace alpx {
+
+typedef _Float16 f16_t;
+typedef __bf16 bf16_t;
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// log2(e): scores are kept in the base-2 domain so the softmax uses the
+// hardware exp2 (v_exp_f32) directly.
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(f16_t x) { return static_cast<float>(x); }
+__device__ __forceinline__ float to_f32(bf16_t x) { return static_cast<float>(x); }
+
+template <typename T> __device__ __forceinline__ T from_f32(float x);
+template <> __device__ __forceinline__ float from_f32<float>(float x) { return x; }
+template <> __device__ __forceinline__ f16_t from_f32<f16_t>(float x) { return static_cast<f16_t>(x); }
+template <> __device__ __forceinline__ bf16_t from_f32<bf16_t>(float x) { return static_cast<bf16_t>(x); }
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Stable two-branch logistic function: never overflows for finite x.
+__device__ __forceinline__ float stable_sigmoid(float x) {
+  if (x >= 0.0f) {
+    float z = __expf(-x);
+    return 1.0f / (1.0f + z);
+  }
+  float z = __expf(x);
+  return z / (1.0f + z);
+}
+
+// Vector of 8 16-bit elements of type T, the MFMA k=32 operand of one lane.
+template <typename T> struct Vec8;
+template <> struct Vec8<f16_t> { typedef f16x8 type; };
+template <> struct Vec8<bf16_t> { typedef bf16x8 type; };
+
+__device__ __forceinline__ f32x4 mfma16x16x32(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+inline size_t dtype_size(int dtype) {
+  return dtype == ALPX_F32 ? 4 : 2;
+}
+
+inline bool dtype_ok(int dtype) {
+  return dtype == ALPX_F32 || dtype == ALPX_F16 || dtype == ALPX_BF16;
+}
+
+// Host-side error slot shared by every entry point (abi.hip).
+int fail(int status, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int check_launch(const char* what);
+
+}  // namespace alpx

@@ -1,0 +1,552 @@
+// Split-K flash-decode for single-token GQA attention, plus the combine pass.
+//
+// Pass 1 (split): the cache rows of one (sequence, kv head) are cut into
+// chunks; every chunk is one "slot" owned by one wavefront, which streams its
+// rows once and produces an online-softmax partial (running max m in the
+// base-2 domain, running sum l, unnormalised accumulator acc[Dv]) for every
+// query head of the GQA group.  K and V are read exactly once per group, so
+// the 4 (Llama-3-8B) or 8 (Qwen3.5) query heads of a group share each byte.
+//
+//  * fp16/bf16, head_dim 64/128/256 (decode_split_mfma): each wavefront takes
+//    32 rows per step.  K rows are loaded with 128-bit loads straight into
+//    the A operand of v_mfma_f32_16x16x32_{f16,bf16} (S^T = K Q^T: 16 rows x
+//    16 query heads per instruction), so scores need no cross-lane dot-product
+//    reduction.  V rows are loaded with 128-bit loads, staged in a per-wave
+//    LDS tile and read back transposed as the A operand of O^T = V^T P^T, so
+//    the probabilities never leave the registers the score MFMA wrote them
+//    to.  The softmax max is a 2-step cross-lane (xor 16, xor 32) reduction.
+//  * everything else (fp32, odd head dims, unaligned caches):
+//    decode_split_generic, one wavefront per slot, VALU dot products.
+//
+// Pass 2 (combine): per (sequence, query head), merge the slot partials with
+// weights 2^(m_s - M), divide by the merged sum, apply the optional sigmoid
+// output gate, and store in the output dtype.
+#include <math.h>
+
+#include "alpx_common.h"
+
+namespace alpx {
+namespace {
+
+constexpr int kTile = 32;   // rows per wavefront step (MFMA path)
+constexpr int kWaves = 4;   // wavefronts (= slots) per block (MFMA path)
+constexpr int kGenericTile = 64;
+constexpr int kMaxSlots = 2048;
+
+struct DecodeArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const int32_t* seq_lens;
+  const void* gate;
+  void* out;
+  float* part_m;    // [B][Hq][nsplit]
+  float* part_l;    // [B][Hq][nsplit]
+  float* part_acc;  // [B][Hq][nsplit][Dv]
+  int64_t ks_pos, ks_b, ks_h, vs_pos, vs_b, vs_h;
+  int length;
+  int batch, q_heads, kv_heads, group, key_dim, value_dim;
+  int head_chunks;  // ceil(group / 16): 16 query heads per MFMA column block
+  int nsplit;       // partial slots per (b, h)
+  int chunk;        // rows per slot
+  float scale_log2; // softmax scale * log2(e)
+};
+
+__device__ __forceinline__ int seq_len(const DecodeArgs& a, int b) {
+  if (a.seq_lens == nullptr) return a.length;
+  int n = a.seq_lens[b];
+  n = n < 0 ? 0 : n;
+  return n > a.length ? a.length : n;
+}
+
+__device__ __forceinline__ void wave_sync_lds() {
+  // LDS operations of one wavefront complete in issue order; this only
+  // stops the compiler from moving LDS accesses across the point.
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// ------------------------------------------------------------ MFMA split
+
+template <typename T, int D>
+__global__ void __launch_bounds__(256)
+decode_split_mfma(DecodeArgs a) {
+  typedef typename Vec8<T>::type V8;
+  constexpr int kStride = D + 8;          // LDS row stride (elements), 16-byte aligned rows
+  constexpr int kUnits = D / 8;           // 16-byte units per row
+  constexpr int kVIters = kTile * kUnits / 64;
+  __shared__ __attribute__((aligned(16))) T vtile[kWaves][kTile * kStride];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int b = blockIdx.z;
+  const int hc = blockIdx.y % a.head_chunks;
+  const int kvh = blockIdx.y / a.head_chunks;
+  const int slot = blockIdx.x * kWaves + wave;
+  const int len = seq_len(a, b);
+  const int start = slot * a.chunk;
+  const int end = min(start + a.chunk, len);
+  const int hl = lane & 15;  // query-head column (N index) of this lane
+  const int quad = lane >> 4;
+  const int g_in = hc * 16 + hl;
+  const bool head_ok = g_in < a.group;
+  const int h = kvh * a.group + (head_ok ? g_in : 0);
+
+  // B operand of S^T = K Q^T: lane holds Q[h][32 ks + 8 quad + 0..7].
+  V8 qv[D / 32];
+  {
+    const T* qp = (const T*)a.q + ((int64_t)b * a.q_heads + h) * D + 8 * quad;
+#pragma unroll
+    for (int ks = 0; ks < D / 32; ++ks) {
+      V8 x = *(const V8*)(qp + 32 * ks);
+      qv[ks] = head_ok ? x : (V8){};
+    }
+  }
+
+  f32x4 o[D / 16];  // O^T[d = 16 mb + 4 quad + i][head hl]
+#pragma unroll
+  for (int mb = 0; mb < D / 16; ++mb) o[mb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY;
+  float l = 0.f;
+
+  const T* kbase = (const T*)a.k + (int64_t)b * a.ks_b + (int64_t)kvh * a.ks_h;
+  const T* vbase = (const T*)a.v + (int64_t)b * a.vs_b + (int64_t)kvh * a.vs_h;
+  T* lds = vtile[wave];
+
+  for (int p0 = start; p0 < end; p0 += kTile) {
+    const int last = end - 1;
+    // K rows -> MFMA A operand: lane holds K[p0 + 16 blk + hl][32 ks + 8 quad + 0..7].
+    V8 kr[2][D / 32];
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk) {
+      const int pos = min(p0 + 16 * blk + hl, last);
+      const T* row = kbase + (int64_t)pos * a.ks_pos + 8 * quad;
+#pragma unroll
+      for (int ks = 0; ks < D / 32; ++ks) kr[blk][ks] = *(const V8*)(row + 32 * ks);
+    }
+    // V rows, 16 bytes per lane, row-major into registers.
+    V8 vr[kVIters];
+#pragma unroll
+    for (int it = 0; it < kVIters; ++it) {
+      const int u = it * 64 + lane;
+      const int r = u / kUnits;
+      const int c = u - r * kUnits;
+      const int pos = min(p0 + r, last);
+      vr[it] = *(const V8*)(vbase + (int64_t)pos * a.vs_pos + 8 * c);
+    }
+    // Scores for 32 rows x 16 heads: lane holds S[pos = p0 + 16 blk + 4 quad + i][hl].
+    f32x4 s[2];
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk) {
+      s[blk] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < D / 32; ++ks) s[blk] = mfma16x16x32(kr[blk][ks], qv[ks], s[blk]);
+    }
+    // Stage V in LDS (row-major, padded rows).
+#pragma unroll
+    for (int it = 0; it < kVIters; ++it) {
+      const int u = it * 64 + lane;
+      const int r = u / kUnits;
+      const int c = u - r * kUnits;
+      *(V8*)(lds + r * kStride + 8 * c) = vr[it];
+    }
+    // Online softmax (base 2).  Slot j of this lane is row 16 (j/4) + 4 quad + j%4.
+    float sv[8];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int pos = p0 + 16 * (j >> 2) + 4 * quad + (j & 3);
+      const float x = pos < end ? s[j >> 2][j & 3] * a.scale_log2 : -INFINITY;
+      sv[j] = x;
+      mx = fmaxf(mx, x);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float mn = fmaxf(m, mx);  // finite: every step holds at least one live row
+    const float alpha = fast_exp2(m - mn);
+    V8 pv;
+    float ps = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float p = fast_exp2(sv[j] - mn);
+      ps += p;
+      pv[j] = from_f32<T>(p);
+    }
+    l = l * alpha + ps;
+    m = mn;
+#pragma unroll
+    for (int mb = 0; mb < D / 16; ++mb) o[mb] *= alpha;
+    wave_sync_lds();
+    // O^T += V^T P^T: A operand lane holds V[row(quad, j)][16 mb + hl], j = 0..7.
+#pragma unroll
+    for (int mb = 0; mb < D / 16; ++mb) {
+      V8 va;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int r = 16 * (j >> 2) + 4 * quad + (j & 3);
+        va[j] = lds[r * kStride + 16 * mb + hl];
+      }
+      o[mb] = mfma16x16x32(va, pv, o[mb]);
+    }
+    wave_sync_lds();
+  }
+
+  l += __shfl_xor(l, 16);
+  l += __shfl_xor(l, 32);
+  if (head_ok) {
+    const int64_t pidx = ((int64_t)b * a.q_heads + h) * a.nsplit + slot;
+    if (quad == 0) {
+      a.part_m[pidx] = m;
+      a.part_l[pidx] = l;
+    }
+    float* pa = a.part_acc + pidx * D + 4 * quad;
+#pragma unroll
+    for (int mb = 0; mb < D / 16; ++mb) *(f32x4*)(pa + 16 * mb) = o[mb];
+  }
+}
+
+// ------------------------------------------------------------ generic split
+
+template <typename T>
+__global__ void __launch_bounds__(64)
+decode_split_generic(DecodeArgs a) {
+  __shared__ float qs[16][256];
+  __shared__ float ps[kGenericTile][17];
+  const int lane = threadIdx.x;
+  const int b = blockIdx.z;
+  const int hc = blockIdx.y % a.head_chunks;
+  const int kvh = blockIdx.y / a.head_chunks;
+  const int slot = blockIdx.x;
+  const int len = seq_len(a, b);
+  const int start = slot * a.chunk;
+  const int end = min(start + a.chunk, len);
+  const int D = a.key_dim, DV = a.value_dim;
+  int gcount = a.group - hc * 16;
+  gcount = gcount > 16 ? 16 : gcount;
+  const int h0 = kvh * a.group + hc * 16;
+
+  for (int i = lane; i < gcount * D; i += 64) {
+    const int hh = i / D;
+    const int d = i - hh * D;
+    qs[hh][d] = to_f32(((const T*)a.q)[((int64_t)b * a.q_heads + h0 + hh) * D + d]);
+  }
+  __syncthreads();
+
+  float m[16], l[16], acc[16][4];
+#pragma unroll
+  for (int hh = 0; hh < 16; ++hh) {
+    m[hh] = -INFINITY;
+    l[hh] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[hh][e] = 0.f;
+  }
+  const T* kbase = (const T*)a.k + (int64_t)b * a.ks_b + (int64_t)kvh * a.ks_h;
+  const T* vbase = (const T*)a.v + (int64_t)b * a.vs_b + (int64_t)kvh * a.vs_h;
+
+  for (int p0 = start; p0 < end; p0 += kGenericTile) {
+    const int pos = p0 + lane;
+    const bool live = pos < end;
+    float s[16];
+#pragma unroll
+    for (int hh = 0; hh < 16; ++hh) s[hh] = 0.f;
+    if (live) {
+      const T* row = kbase + (int64_t)pos * a.ks_pos;
+      for (int d = 0; d < D; ++d) {
+        const float kv = to_f32(row[d]);
+#pragma unroll
+        for (int hh = 0; hh < 16; ++hh)
+          if (hh < gcount) s[hh] += qs[hh][d] * kv;
+      }
+    }
+#pragma unroll
+    for (int hh = 0; hh < 16; ++hh) {
+      if (hh >= gcount) continue;
+      const float x = live ? s[hh] * a.scale_log2 : -INFINITY;
+      float mx = x;
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+      const float mn = fmaxf(m[hh], mx);
+      const float alpha = fast_exp2(m[hh] - mn);
+      const float p = fast_exp2(x - mn);
+      l[hh] = l[hh] * alpha + p;
+      m[hh] = mn;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[hh][e] *= alpha;
+      ps[lane][hh] = p;
+    }
+    __syncthreads();
+    const int n = min(kGenericTile, end - p0);
+    for (int j = 0; j < n; ++j) {
+      const T* vrow = vbase + (int64_t)(p0 + j) * a.vs_pos;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int d = lane + 64 * e;
+        if (d < DV) {
+          const float vv = to_f32(vrow[d]);
+#pragma unroll
+          for (int hh = 0; hh < 16; ++hh)
+            if (hh < gcount) acc[hh][e] += ps[j][hh] * vv;
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int hh = 0; hh < 16; ++hh) {
+    if (hh >= gcount) continue;
+    float lt = l[hh];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) lt += __shfl_xor(lt, off);
+    const int64_t pidx = ((int64_t)b * a.q_heads + h0 + hh) * a.nsplit + slot;
+    if (lane == 0) {
+      a.part_m[pidx] = m[hh];
+      a.part_l[pidx] = lt;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int d = lane + 64 * e;
+      if (d < DV) a.part_acc[pidx * DV + d] = acc[hh][e];
+    }
+  }
+}
+
+// ------------------------------------------------------------ combine
+
+template <typename T, typename TO>
+__global__ void __launch_bounds__(256)
+decode_combine(DecodeArgs a) {
+  __shared__ float w[kMaxSlots];
+  __shared__ float red[256];
+  const int bh = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int ns = a.nsplit;
+  const float* pm = a.part_m + (int64_t)bh * ns;
+  const float* pl = a.part_l + (int64_t)bh * ns;
+
+  float mx = -INFINITY;
+  for (int s = tid; s < ns; s += blockDim.x) mx = fmaxf(mx, pm[s]);
+  red[tid] = mx;
+  __syncthreads();
+  for (int off = blockDim.x / 2; off > 0; off >>= 1) {
+    if (tid < off) red[tid] = fmaxf(red[tid], red[tid + off]);
+    __syncthreads();
+  }
+  const float M = red[0];
+  __syncthreads();
+  float lsum = 0.f;
+  for (int s = tid; s < ns; s += blockDim.x) {
+    const float ws = (M == -INFINITY) ? 0.f : fast_exp2(pm[s] - M);
+    w[s] = ws;
+    lsum += pl[s] * ws;
+  }
+  red[tid] = lsum;
+  __syncthreads();
+  for (int off = blockDim.x / 2; off > 0; off >>= 1) {
+    if (tid < off) red[tid] += red[tid + off];
+    __syncthreads();
+  }
+  const float L = red[0];
+  const float inv = L > 0.f ? 1.0f / L : 0.f;
+  const int DV = a.value_dim;
+  const float* pa = a.part_acc + (int64_t)bh * ns * DV;
+  for (int d = tid; d < DV; d += blockDim.x) {
+    float accv = 0.f;
+    for (int s = 0; s < ns; ++s) accv += pa[(int64_t)s * DV + d] * w[s];
+    float r = accv * inv;
+    if (a.gate != nullptr) r *= stable_sigmoid(to_f32(((const T*)a.gate)[(int64_t)bh * DV + d]));
+    ((TO*)a.out)[(int64_t)bh * DV + d] = from_f32<TO>(r);
+  }
+}
+
+// ------------------------------------------------------------ planning
+
+struct Plan {
+  int nsplit;   // slots per (b, h) == partial count
+  int chunk;    // rows per slot
+  int grid_x;   // blocks along the split axis
+};
+
+int target_slots() {
+  static int value = -1;
+  if (value < 0) {
+    const char* env = getenv("ALPX_DECODE_SLOTS");
+    value = env ? atoi(env) : 0;
+    if (value <= 0) value = 3072;
+  }
+  return value;
+}
+
+Plan plan_split(int batch, int kv_heads, int head_chunks, int length, bool mfma) {
+  Plan p;
+  const int unit = mfma ? kTile : kGenericTile;
+  const int per_block = mfma ? kWaves : 1;
+  const int pairs = batch * kv_heads * head_chunks;
+  int want = (target_slots() + pairs - 1) / pairs;
+  const int max_slots = (length + unit - 1) / unit;
+  if (want > max_slots) want = max_slots;
+  if (want < 1) want = 1;
+  int chunk = (length + want - 1) / want;
+  chunk = ((chunk + unit - 1) / unit) * unit;
+  if (chunk < unit) chunk = unit;
+  int slots = (length + chunk - 1) / chunk;
+  if (slots < 1) slots = 1;
+  while (((slots + per_block - 1) / per_block) * per_block > kMaxSlots) {
+    chunk += unit;
+    slots = (length + chunk - 1) / chunk;
+  }
+  p.grid_x = (slots + per_block - 1) / per_block;
+  p.nsplit = p.grid_x * per_block;
+  p.chunk = chunk;
+  return p;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+size_t workspace_for(int batch, int q_heads, int value_dim, int nsplit) {
+  const size_t n = (size_t)batch * q_heads * nsplit;
+  return 2 * align256(n * sizeof(float)) + align256(n * value_dim * sizeof(float));
+}
+
+template <typename T>
+int launch_split(bool mfma, int D, const DecodeArgs& a, dim3 grid, hipStream_t s) {
+  if (mfma) {
+    if constexpr (sizeof(T) == 2) {
+      switch (D) {
+        case 64:
+          hipLaunchKernelGGL((decode_split_mfma<T, 64>), grid, dim3(256), 0, s, a);
+          return check_launch("decode_split_mfma<64>");
+        case 128:
+          hipLaunchKernelGGL((decode_split_mfma<T, 128>), grid, dim3(256), 0, s, a);
+          return check_launch("decode_split_mfma<128>");
+        case 256:
+          hipLaunchKernelGGL((decode_split_mfma<T, 256>), grid, dim3(256), 0, s, a);
+          return check_launch("decode_split_mfma<256>");
+      }
+    }
+    return fail(ALPX_EUNSUPPORTED, "decode: no MFMA kernel for head_dim %d", D);
+  }
+  hipLaunchKernelGGL((decode_split_generic<T>), grid, dim3(64), 0, s, a);
+  return check_launch("decode_split_generic");
+}
+
+template <typename T>
+int launch_combine(int out_dtype, const DecodeArgs& a, hipStream_t s) {
+  dim3 grid(a.batch * a.q_heads);
+  dim3 block(a.value_dim > 128 ? 256 : 128);
+  switch (out_dtype) {
+    case ALPX_F32:
+      hipLaunchKernelGGL((decode_combine<T, float>), grid, block, 0, s, a);
+      break;
+    case ALPX_F16:
+      hipLaunchKernelGGL((decode_combine<T, f16_t>), grid, block, 0, s, a);
+      break;
+    default:
+      hipLaunchKernelGGL((decode_combine<T, bf16_t>), grid, block, 0, s, a);
+      break;
+  }
+  return check_launch("decode_combine");
+}
+
+}  // namespace
+}  // namespace alpx
+
+extern "C" size_t alpx_decode_workspace_bytes(int batch, int q_heads, int kv_heads,
+                                              int value_dim, int max_len) {
+  using namespace alpx;
+  if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || value_dim <= 0 || max_len <= 0 ||
+      q_heads % kv_heads != 0)
+    return 0;
+  const int group = q_heads / kv_heads;
+  const int hc = (group + 15) / 16;
+  const Plan pm = plan_split(batch, kv_heads, hc, max_len, true);
+  const Plan pg = plan_split(batch, kv_heads, hc, max_len, false);
+  const int ns = pm.nsplit > pg.nsplit ? pm.nsplit : pg.nsplit;
+  return workspace_for(batch, q_heads, value_dim, ns);
+}
+
+extern "C" int alpx_decode_gqa(const void* q, const void* key_cache, const void* value_cache,
+                               const int32_t* seq_lens, int length, const void* gate, void* out,
+                               void* workspace, size_t workspace_bytes, int batch, int q_heads,
+                               int kv_heads, int key_dim, int value_dim, int64_t k_pos_stride,
+                               int64_t k_batch_stride, int64_t k_head_stride,
+                               int64_t v_pos_stride, int64_t v_batch_stride,
+                               int64_t v_head_stride, float scale, int dtype, int out_dtype,
+                               void* stream) {
+  using namespace alpx;
+  if (!q || !key_cache || !value_cache || !out || !workspace)
+    return fail(ALPX_EINVAL, "alpx_decode_gqa: null buffer");
+  if (!dtype_ok(dtype) || !dtype_ok(out_dtype))
+    return fail(ALPX_EINVAL, "alpx_decode_gqa: unknown dtype");
+  if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || key_dim <= 0 || value_dim <= 0)
+    return fail(ALPX_EINVAL, "alpx_decode_gqa: sizes must be positive");
+  if (length <= 0) return fail(ALPX_EINVAL, "attention cache length must be a positive integer");
+  if (q_heads % kv_heads != 0)
+    return fail(ALPX_EINVAL, "attention query heads must be a multiple of KV heads");
+  if (!(scale > 0.0f) || !isfinite(scale))
+    return fail(ALPX_EINVAL, "attention scale must be positive and finite");
+  if (key_dim > 256 || value_dim > 256)
+    return fail(ALPX_EUNSUPPORTED, "alpx_decode_gqa: head dims above 256 are not supported");
+
+  const int group = q_heads / kv_heads;
+  const int hc = (group + 15) / 16;
+  const size_t es = dtype_size(dtype);
+  const uintptr_t align = (uintptr_t)q | (uintptr_t)key_cache | (uintptr_t)value_cache |
+                          (uintptr_t)(k_pos_stride * es) | (uintptr_t)(k_batch_stride * es) |
+                          (uintptr_t)(k_head_stride * es) | (uintptr_t)(v_pos_stride * es) |
+                          (uintptr_t)(v_batch_stride * es) | (uintptr_t)(v_head_stride * es);
+  const bool mfma = dtype != ALPX_F32 && key_dim == value_dim &&
+                    (key_dim == 64 || key_dim == 128 || key_dim == 256) && (align & 15) == 0 &&
+                    getenv("ALPX_DECODE_GENERIC") == nullptr;
+  const Plan p = plan_split(batch, kv_heads, hc, length, mfma);
+  const size_t need = workspace_for(batch, q_heads, value_dim, p.nsplit);
+  if (workspace_bytes < need)
+    return fail(ALPX_EINVAL, "alpx_decode_gqa: workspace holds %zu bytes, needs %zu",
+                workspace_bytes, need);
+
+  DecodeArgs a;
+  a.q = q;
+  a.k = key_cache;
+  a.v = value_cache;
+  a.seq_lens = seq_lens;
+  a.gate = gate;
+  a.out = out;
+  const size_t n = (size_t)batch * q_heads * p.nsplit;
+  char* ws = (char*)workspace;
+  a.part_m = (float*)ws;
+  a.part_l = (float*)(ws + align256(n * sizeof(float)));
+  a.part_acc = (float*)(ws + 2 * align256(n * sizeof(float)));
+  a.ks_pos = k_pos_stride;
+  a.ks_b = k_batch_stride;
+  a.ks_h = k_head_stride;
+  a.vs_pos = v_pos_stride;
+  a.vs_b = v_batch_stride;
+  a.vs_h = v_head_stride;
+  a.length = length;
+  a.batch = batch;
+  a.q_heads = q_heads;
+  a.kv_heads = kv_heads;
+  a.group = group;
+  a.key_dim = key_dim;
+  a.value_dim = value_dim;
+  a.head_chunks = hc;
+  a.nsplit = p.nsplit;
+  a.chunk = p.chunk;
+  a.scale_log2 = scale * kLog2e;
+
+  hipStream_t s = (hipStream_t)stream;
+  dim3 grid(p.grid_x, kv_heads * hc, batch);
+  int rc;
+  switch (dtype) {
+    case ALPX_F32: rc = launch_split<float>(false, key_dim, a, grid, s); break;
+    case ALPX_F16: rc = launch_split<f16_t>(mfma, key_dim, a, grid, s); break;
+    default: rc = launch_split<bf16_t>(mfma, key_dim, a, grid, s); break;
+  }
+  if (rc != ALPX_OK) return rc;
+  switch (dtype) {
+    case ALPX_F32: return launch_combine<float>(out_dtype, a, s);
+    case ALPX_F16: return launch_combine<f16_t>(out_dtype, a, s);
+    default: return launch_combine<bf16_t>(out_dtype, a, s);
+  }
+}

@@ -1,0 +1,384 @@
+"""Drop-in for alpaccaroo's ``Qwen35RocmOps`` attention/recurrence surface.
+
+Mirrors ``alpaccaroo/qwen35_rocm_ops.py`` (class ``Qwen35RocmOps``,
+qwen35_rocm_ops.py:89-589): same method names, argument order, tensor
+layouts, return conventions and exception types for the hot path:
+
+* ``initialize_attention_workspace`` -> caches ``[capacity, batch, kv_heads,
+  dim]`` (qwen35_rocm_ops.py:214-238)
+* ``initialize_recurrent_workspace`` -> conv history + delta state
+  ``[batch, value_heads, value, key]`` (qwen35_rocm_ops.py:186-212)
+* ``attention_append_`` (qwen35_rocm_ops.py:475-500)
+* ``online_attention`` (qwen35_rocm_ops.py:502-564)
+* ``append_online_attention_`` (qwen35_rocm_ops.py:566-589)
+* ``sigmoid_gate`` (qwen35_rocm_ops.py:286-290)
+* ``gated_delta_net_step_`` (qwen35_rocm_ops.py:362-407)
+* ``state_copy`` / ``state_restore_`` (qwen35_rocm_ops.py:240-249)
+
+Differences, all extensions that keep the base signatures:
+
+* float16 and bfloat16 buffers are accepted next to float32 (the reference
+  is float32-only, qwen35_rocm_ops.py:153-158); arithmetic is fp32;
+* ``online_attention`` takes optional ``seq_lens`` (ragged batch),
+  ``gate`` (fused sigmoid output gate) and ``out_dtype``;
+* the capability check qualifies a gfx950 (MI355X) device and the built
+  library instead of the reference's gfx1151 APU gate.
+
+Every method runs in the HIP library (libalpx.so) through its C-ABI; there
+is no PyTorch compute fallback.
+"""
+
+from __future__ import annotations
+
+import importlib
+import math
+from dataclasses import dataclass
+from typing import Any, Sequence
+
+from . import _lib, _ops
+
+
+class Qwen35RocmUnavailable(RuntimeError):
+    """Raised when the gfx950 path cannot be used (qwen35_rocm.py:43-53)."""
+
+    def __init__(self, message: str, *, diagnostics=None) -> None:
+        super().__init__(message)
+        self.diagnostics = None if diagnostics is None else dict(diagnostics)
+
+
+@dataclass(frozen=True)
+class RocmCapability:
+    available: bool
+    reason: str
+    device_index: int | None = None
+    gcn_arch_name: str | None = None
+
+
+TARGET_GFX = "gfx950"
+
+
+def rocm_capability(device_index: int | None = None) -> RocmCapability:
+    """Fail-closed check: PyTorch-ROCm, a visible gfx950 device, libalpx."""
+    try:
+        torch = importlib.import_module("torch")
+    except Exception as exc:  # pragma: no cover
+        return RocmCapability(False, f"PyTorch is not importable: {exc}")
+    if getattr(torch.version, "hip", None) is None:
+        return RocmCapability(False, "PyTorch is not a ROCm build")
+    if not torch.cuda.is_available():
+        return RocmCapability(False, "no HIP device is visible")
+    index = torch.cuda.current_device() if device_index is None else int(device_index)
+    try:
+        arch = _lib.device_arch(index)
+    except Exception as exc:
+        return RocmCapability(False, f"libalpx unavailable: {exc}", index)
+    if arch.split(":")[0] != TARGET_GFX:
+        return RocmCapability(False, f"device {index} is {arch}, not {TARGET_GFX}", index, arch)
+    return RocmCapability(True, "ok", index, arch)
+
+
+def _positive_integer(name: str, value: int) -> int:
+    if isinstance(value, bool) or not isinstance(value, int) or value <= 0:
+        raise ValueError(f"{name} must be a positive integer")
+    return value
+
+
+def _nonnegative_integer(name: str, value: int) -> int:
+    if isinstance(value, bool) or not isinstance(value, int) or value < 0:
+        raise ValueError(f"{name} must be a non-negative integer")
+    return value
+
+
+def _positive_finite(name: str, value: float) -> float:
+    value = float(value)
+    if not math.isfinite(value) or value <= 0.0:
+        raise ValueError(f"{name} must be positive and finite")
+    return value
+
+
+def _shape(tensor: Any) -> tuple[int, ...]:
+    return tuple(int(value) for value in tensor.shape)
+
+
+def _tensor_descriptor(tensor: Any) -> dict[str, Any]:
+    device = tensor.device
+    index = getattr(device, "index", None)
+    return {
+        "shape": list(_shape(tensor)),
+        "dtype": str(tensor.dtype),
+        "device": f"{device.type}:{0 if index is None else index}",
+        "contiguous": bool(tensor.is_contiguous()),
+    }
+
+
+@dataclass(frozen=True)
+class RocmRecurrentWorkspace:
+    """Zero-initialized recurrent state on the device (qwen35_rocm_ops.py:57-70)."""
+
+    convolution_history: Any
+    delta_state: Any
+
+    def descriptor(self) -> dict[str, Any]:
+        return {
+            "convolution_history": _tensor_descriptor(self.convolution_history),
+            "delta_state": _tensor_descriptor(self.delta_state),
+            "delta_state_orientation": "batch,value_head,value,key",
+            "initialization": "deterministic-zero",
+        }
+
+
+@dataclass(frozen=True)
+class RocmAttentionWorkspace:
+    """Preallocated K/V capacity; the chain owns the logical length
+    (qwen35_rocm_ops.py:73-86)."""
+
+    key_cache: Any
+    value_cache: Any
+
+    def descriptor(self) -> dict[str, Any]:
+        return {
+            "key_cache": _tensor_descriptor(self.key_cache),
+            "value_cache": _tensor_descriptor(self.value_cache),
+            "layout": "capacity,batch,kv_head,head_dimension",
+            "initialization": "deterministic-zero",
+        }
+
+
+class Qwen35RocmOps:
+    """gfx950 implementation of the Qwen35 attention/recurrence boundaries."""
+
+    def __init__(self, *, device_index: int | None = None, _torch: Any | None = None,
+                 _capability: RocmCapability | None = None) -> None:
+        capability = rocm_capability(device_index) if _capability is None else _capability
+        if not capability.available:
+            raise Qwen35RocmUnavailable(capability.reason)
+        selected = capability.device_index if device_index is None else device_index
+        if selected is None:
+            raise Qwen35RocmUnavailable("ROCm capability has no target device index")
+        _nonnegative_integer("device_index", selected)
+        if capability.device_index is not None and selected != capability.device_index:
+            raise ValueError(
+                f"device_index {selected} differs from qualified target "
+                f"{capability.device_index}")
+        self.torch = importlib.import_module("torch") if _torch is None else _torch
+        self.capability = capability
+        self.device_index = selected
+        self.device = f"cuda:{selected}"
+
+    def descriptor(self) -> dict[str, Any]:
+        return {
+            "backend": "hip-gfx950-libalpx",
+            "device": self.device,
+            "gcn_arch_name": self.capability.gcn_arch_name,
+            "tensor_dtype": "float32|float16|bfloat16",
+            "host_transfer_api": False,
+            "state_orientation": "batch,value_head,value,key",
+            "recurrent_key_mapping": "value_head % key_head_count",
+            "attention_key_mapping": "contiguous-query-head-groups",
+            "attention_algorithm": "split-k-online-softmax",
+            "supported_attention_head_dimensions": "1..256",
+        }
+
+    # ------------------------------------------------------------ validation
+
+    def _tensor(self, value: Any, name: str, *, dimensions: int | None = None,
+                allow_integer: bool = False) -> Any:
+        """Contract check of qwen35_rocm_ops.py:134-165, widened to fp16/bf16."""
+        torch = self.torch
+        if not torch.is_tensor(value):
+            raise TypeError(f"{name} must be a PyTorch tensor")
+        device = value.device
+        if getattr(device, "type", None) != "cuda":
+            raise TypeError(f"{name} must remain on the ROCm device")
+        index = getattr(device, "index", None)
+        if index not in (None, self.device_index):
+            raise ValueError(f"{name} is on device {index}, expected {self.device_index}")
+        valid = (torch.float32, torch.float16, torch.bfloat16)
+        if allow_integer:
+            valid = valid + (torch.int64, torch.int32)
+        if value.dtype not in valid:
+            expected = "float32, float16 or bfloat16"
+            raise TypeError(f"{name} must use {expected}" + (" or int" if allow_integer else ""))
+        if dimensions is not None and len(value.shape) != dimensions:
+            raise ValueError(f"{name} has {_shape(value)}, expected {dimensions} dimensions")
+        if not value.is_contiguous():
+            raise ValueError(f"{name} must be contiguous")
+        return value
+
+    @staticmethod
+    def _same_shape(left: Any, right: Any, what: str) -> None:
+        if _shape(left) != _shape(right):
+            raise ValueError(f"{what} shapes differ: {_shape(left)} != {_shape(right)}")
+
+    @staticmethod
+    def _same_dtype(what: str, *tensors: Any) -> None:
+        dtypes = {t.dtype for t in tensors}
+        if len(dtypes) != 1:
+            raise TypeError(f"{what} tensors must share one dtype, got {sorted(map(str, dtypes))}")
+
+    # ------------------------------------------------------------ workspaces
+
+    def zeros(self, shape: Sequence[int], dtype: Any = None) -> Any:
+        normalized = tuple(_positive_integer("workspace dimension", v) for v in shape)
+        if not normalized:
+            raise ValueError("workspace shape cannot be empty")
+        dtype = self.torch.float32 if dtype is None else dtype
+        return self.torch.zeros(normalized, dtype=dtype, device=self.device)
+
+    def initialize_recurrent_workspace(self, *, batch_size: int, convolution_kernel: int,
+                                       convolution_channels: int, value_heads: int,
+                                       value_dimension: int,
+                                       key_dimension: int) -> RocmRecurrentWorkspace:
+        batch = _positive_integer("batch_size", batch_size)
+        kernel = _positive_integer("convolution_kernel", convolution_kernel)
+        channels = _positive_integer("convolution_channels", convolution_channels)
+        heads = _positive_integer("value_heads", value_heads)
+        value_width = _positive_integer("value_dimension", value_dimension)
+        key_width = _positive_integer("key_dimension", key_dimension)
+        history = self.torch.zeros((batch, kernel - 1, channels), dtype=self.torch.float32,
+                                   device=self.device)
+        state = self.torch.zeros((batch, heads, value_width, key_width),
+                                 dtype=self.torch.float32, device=self.device)
+        return RocmRecurrentWorkspace(history, state)
+
+    def initialize_attention_workspace(self, *, capacity: int, batch_size: int, kv_heads: int,
+                                       key_dimension: int, value_dimension: int,
+                                       dtype: Any = None) -> RocmAttentionWorkspace:
+        length = _positive_integer("capacity", capacity)
+        batch = _positive_integer("batch_size", batch_size)
+        heads = _positive_integer("kv_heads", kv_heads)
+        key_width = _positive_integer("key_dimension", key_dimension)
+        value_width = _positive_integer("value_dimension", value_dimension)
+        dtype = self.torch.float32 if dtype is None else dtype
+        keys = self.torch.zeros((length, batch, heads, key_width), dtype=dtype, device=self.device)
+        values = self.torch.zeros((length, batch, heads, value_width), dtype=dtype,
+                                  device=self.device)
+        return RocmAttentionWorkspace(keys, values)
+
+    def state_copy(self, source: Any) -> Any:
+        source = self._tensor(source, "state source")
+        return source.clone()
+
+    def state_restore_(self, target: Any, snapshot: Any) -> Any:
+        target = self._tensor(target, "state target")
+        snapshot = self._tensor(snapshot, "state snapshot")
+        self._same_shape(target, snapshot, "state restore")
+        target.copy_(snapshot)
+        return target
+
+    # ------------------------------------------------------------ attention
+
+    def attention_append_(self, key_cache: Any, value_cache: Any, position: int, key: Any,
+                          value: Any) -> int:
+        key_cache = self._tensor(key_cache, "attention key cache", dimensions=4)
+        value_cache = self._tensor(value_cache, "attention value cache", dimensions=4)
+        key = self._tensor(key, "attention key", dimensions=3)
+        value = self._tensor(value, "attention value", dimensions=3)
+        position = _nonnegative_integer("attention cache position", position)
+        if int(key_cache.shape[0]) != int(value_cache.shape[0]):
+            raise ValueError("attention K/V cache capacities differ")
+        if position >= int(key_cache.shape[0]):
+            raise ValueError("attention cache position exceeds capacity")
+        if _shape(key_cache)[1:3] != _shape(value_cache)[1:3]:
+            raise ValueError("attention K/V cache batch and head axes differ")
+        if _shape(key) != _shape(key_cache)[1:]:
+            raise ValueError("attention key does not match cache token shape")
+        if _shape(value) != _shape(value_cache)[1:]:
+            raise ValueError("attention value does not match cache token shape")
+        self._same_dtype("attention append", key_cache, value_cache, key, value)
+        _ops.kv_append(key_cache, value_cache, key.unsqueeze(0), value.unsqueeze(0),
+                       position=position)
+        return position + 1
+
+    def attention_append_rows_(self, key_cache: Any, value_cache: Any, key: Any, value: Any, *,
+                               position: int | None = None, positions: Any = None) -> None:
+        """Multi-token / ragged append (extension): ``key [T, B, Hkv, D]``
+        rows land at ``position + t`` or, per sequence, ``positions[b] + t``."""
+        key_cache = self._tensor(key_cache, "attention key cache", dimensions=4)
+        value_cache = self._tensor(value_cache, "attention value cache", dimensions=4)
+        key = self._tensor(key, "attention key rows", dimensions=4)
+        value = self._tensor(value, "attention value rows", dimensions=4)
+        if _shape(key)[1:] != _shape(key_cache)[1:] or _shape(value)[1:] != _shape(value_cache)[1:]:
+            raise ValueError("attention rows do not match cache token shape")
+        if int(key.shape[0]) != int(value.shape[0]):
+            raise ValueError("attention K/V row counts differ")
+        self._same_dtype("attention append", key_cache, value_cache, key, value)
+        tokens = int(key.shape[0])
+        capacity = int(key_cache.shape[0])
+        if positions is None:
+            position = _nonnegative_integer("attention cache position", position)
+            if position + tokens > capacity:
+                raise ValueError("attention cache position exceeds capacity")
+        elif not self.torch.is_tensor(positions) or positions.device.type != "cuda":
+            host = [int(p) for p in positions]
+            if len(host) != int(key_cache.shape[1]):
+                raise ValueError("positions must have one entry per sequence")
+            if any(p < 0 or p + tokens > capacity for p in host):
+                raise ValueError("attention cache position exceeds capacity")
+            positions = self.torch.tensor(host, dtype=self.torch.int32, device=self.device)
+        _ops.kv_append(key_cache, value_cache, key, value, position=position, positions=positions)
+
+    def online_attention(self, query: Any, key_cache: Any, value_cache: Any, *, length: int,
+                         scale: float | None = None, seq_lens: Any = None, gate: Any = None,
+                         out_dtype: Any = None) -> Any:
+        query = self._tensor(query, "attention query", dimensions=3)
+        key_cache = self._tensor(key_cache, "attention key cache", dimensions=4)
+        value_cache = self._tensor(value_cache, "attention value cache", dimensions=4)
+        length = _positive_integer("attention cache length", length)
+        capacity, batch, kv_heads, key_width = _shape(key_cache)
+        value_shape = _shape(value_cache)
+        if length > capacity:
+            raise ValueError("attention cache length exceeds capacity")
+        if value_shape[:3] != (capacity, batch, kv_heads):
+            raise ValueError("attention K/V cache capacity, batch, or heads differ")
+        query_batch, query_heads, query_width = _shape(query)
+        if query_batch != batch or query_width != key_width:
+            raise ValueError("attention query does not match K cache batch/head width")
+        if kv_heads <= 0 or query_heads % kv_heads:
+            raise ValueError("attention query heads must be a multiple of KV heads")
+        scale_value = (1.0 / math.sqrt(key_width) if scale is None
+                       else _positive_finite("attention scale", scale))
+        self._same_dtype("attention", query, key_cache, value_cache)
+        if gate is not None:
+            gate = self._tensor(gate, "sigmoid-gate logits", dimensions=3)
+            if _shape(gate) != (batch, query_heads, value_shape[3]):
+                raise ValueError("sigmoid-gate logits must match the attention output")
+            self._same_dtype("attention gate", query, gate)
+        if seq_lens is not None:
+            if not self.torch.is_tensor(seq_lens) or seq_lens.device.type != "cuda":
+                host = [int(n) for n in seq_lens]
+                if len(host) != batch or any(n < 1 or n > length for n in host):
+                    raise ValueError("seq_lens must hold one length in [1, length] per sequence")
+                seq_lens = self.torch.tensor(host, dtype=self.torch.int32, device=self.device)
+            elif _shape(seq_lens) != (batch,):
+                raise ValueError("seq_lens must hold one length per sequence")
+        c, b, h = batch * kv_heads * key_width, kv_heads * key_width, key_width
+        cv, bv, hv = batch * kv_heads * value_shape[3], kv_heads * value_shape[3], value_shape[3]
+        return _ops.decode(query, key_cache, value_cache, length=length, k_strides=(c, b, h),
+                           v_strides=(cv, bv, hv), batch=batch, kv_heads=kv_heads,
+                           seq_lens=seq_lens, gate=gate, scale=scale_value,
+                           out_dtype=out_dtype)
+
+    def append_online_attention_(self, query: Any, key: Any, value: Any, key_cache: Any,
+                                 value_cache: Any, *, position: int,
+                                 scale: float | None = None) -> tuple[Any, int]:
+        length = self.attention_append_(key_cache, value_cache, position, key, value)
+        return (self.online_attention(query, key_cache, value_cache, length=length,
+                                      scale=scale), length)
+
+    def sigmoid_gate(self, values: Any, gate: Any) -> Any:
+        values = self._tensor(values, "sigmoid-gate values")
+        gate = self._tensor(gate, "sigmoid-gate logits")
+        self._same_shape(values, gate, "sigmoid gate")
+        self._same_dtype("sigmoid gate", values, gate)
+        return _ops.sigmoid_gate(values, gate)
+
+
+__all__ = [
+    "Qwen35RocmOps",
+    "Qwen35RocmUnavailable",
+    "RocmAttentionWorkspace",
+    "RocmCapability",
+    "RocmRecurrentWorkspace",
+    "rocm_capability",
+]

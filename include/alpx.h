@@ -1,0 +1,135 @@
+/*
+ * alpx.h -- C-ABI of the MI355X (gfx950) attention library libalpx.so.
+ *
+ * The library replaces the attention hot path of alpaccaroo: KV-cache
+ * append, GQA decode attention (with the optional Qwen3.5 sigmoid output
+ * gate), causal prefill attention and the Qwen3.5 gated delta-rule (GDN)
+ * recurrence.  Each entry point cites the reference interface it stands
+ * behind (paths relative to the reference's alpaccaroo/ package).
+ *
+ * Conventions
+ *  - Every pointer is a device pointer unless stated otherwise; the caller
+ *    owns all buffers (caches, state, outputs, workspace).
+ *  - Element strides are in ELEMENTS, not bytes.  The innermost (head
+ *    dimension) axis is always contiguous.
+ *  - `stream` is a hipStream_t (NULL = the legacy default stream).  Calls
+ *    are asynchronous: they enqueue kernels and return.
+ *  - Return value: ALPX_OK (0) or a negative status; the message of the
+ *    last failing call on this host thread is alpx_last_error().
+ *    Arguments are validated before anything is enqueued, so a failing
+ *    call leaves every buffer untouched.
+ *  - One caller at a time per stream; calls on one GPU that share a
+ *    workspace must be ordered (same stream), as in the reference's
+ *    single-generation lock (serve.py:326).
+ */
+#ifndef ALPX_H
+#define ALPX_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ALPX_ABI_VERSION 1
+
+/* Element types (the reference's ROCm ops are float32 only,
+ * qwen35_rocm_ops.py:153-158; fp16/bf16 are this library's extension). */
+enum alpx_dtype { ALPX_F32 = 0, ALPX_F16 = 1, ALPX_BF16 = 2 };
+
+enum alpx_status {
+  ALPX_OK = 0,
+  ALPX_EINVAL = -1,       /* contract violation: maps to ValueError/TypeError */
+  ALPX_EUNSUPPORTED = -2, /* shape/dtype outside what the kernels cover */
+  ALPX_EHIP = -3,         /* HIP runtime error (launch, device query) */
+  ALPX_ERANGE = -4        /* position/length outside the cache capacity */
+};
+
+/* ABI version of the loaded library (must equal ALPX_ABI_VERSION). */
+int alpx_abi_version(void);
+
+/* Message of the last failing call on the calling host thread ("" if none). */
+const char* alpx_last_error(void);
+
+/* gcnArchName of `device` (e.g. "gfx950:sramecc+:xnack-") into a host buffer. */
+int alpx_device_arch(int device, char* buf, int buf_len);
+
+/*
+ * KV-cache append.
+ * Replaces Qwen35RocmOps.attention_append_ (qwen35_rocm_ops.py:475-500),
+ * qwen35_cuda._kv_append (qwen35_cuda.py:1001-1012), the llama-class cache
+ * writes cache_k[li][pos0:pos0+n] = k (model.py:1335-1337, :1431-1432) and
+ * FullAttentionState.append (memory.py:419-428).
+ *
+ * Caches are [capacity, batch, kv_heads, key_dim|value_dim]; key/value are
+ * `tokens` rows [tokens, batch, kv_heads, key_dim|value_dim], contiguous.
+ * Row (t, b) is written to cache row positions[b] + t when `positions`
+ * (device int32 [batch]) is given, else to position + t.  The copy is
+ * bit-exact.  With `positions` == NULL the call fails with ALPX_ERANGE
+ * unless position + tokens <= capacity; with device `positions` the host
+ * cannot see them, and rows that would fall outside [0, capacity) are
+ * skipped by the kernel (never written out of bounds).
+ */
+int alpx_kv_append(void* key_cache, void* value_cache, const void* key, const void* value,
+                   int dtype, int64_t capacity, int batch, int kv_heads, int key_dim,
+                   int value_dim, int tokens, int64_t position, const int32_t* positions,
+                   void* stream);
+
+/*
+ * Workspace size in bytes needed by alpx_decode_gqa for these sizes
+ * (split-K partials: running max, running sum and the unnormalised
+ * accumulator per query head and split).
+ */
+size_t alpx_decode_workspace_bytes(int batch, int q_heads, int kv_heads, int value_dim,
+                                   int max_len);
+
+/*
+ * Single-token GQA decode attention (split-K flash-decode + combine).
+ * Replaces kernels.attention_decode (kernels.py:1183-1200),
+ * Model._attention_np (model.py:1231-1252),
+ * qwen35_kernels.qwen35_full_attention_decode (qwen35_kernels.py:363-392),
+ * Qwen35RocmOps.online_attention (qwen35_rocm_ops.py:502-564) and, with
+ * `gate`, the sigmoid output gate of Qwen35Model._attention
+ * (qwen35_runtime.py:653-660; Qwen35RocmOps.sigmoid_gate,
+ * qwen35_rocm_ops.py:286-290).
+ *
+ *   out[b, h, :] = softmax_j(scale * q[b, h] . K[j, b, h // G]) . V[j, b, h // G]
+ *                  (* sigmoid(gate[b, h, :]) when gate != NULL)
+ * over cache rows j < len_b, where G = q_heads / kv_heads (contiguous
+ * grouping) and len_b = seq_lens[b] (device int32 [batch], ragged
+ * extension) or `length` when seq_lens == NULL.  Device lengths are
+ * clamped to [0, length]; a sequence of length 0 yields zeros.
+ *
+ * q [batch, q_heads, key_dim] and gate/out [batch, q_heads, value_dim] are
+ * contiguous.  K element (j, b, h, d) is at
+ * key_cache[j*k_pos_stride + b*k_batch_stride + h*k_head_stride + d]
+ * (likewise V with the v_* strides): [capacity, batch, kv_heads, D] is the
+ * ROCm workspace layout, (t, kv_heads, D) with batch 1 the llama layout.
+ * q, K, V and gate use `dtype`; out uses `out_dtype`; arithmetic is fp32.
+ * workspace must hold alpx_decode_workspace_bytes(batch, q_heads,
+ * kv_heads, value_dim, length) bytes and is scratch (no initial contents).
+ */
+int alpx_decode_gqa(const void* q, const void* key_cache, const void* value_cache,
+                    const int32_t* seq_lens, int length, const void* gate, void* out,
+                    void* workspace, size_t workspace_bytes, int batch, int q_heads,
+                    int kv_heads, int key_dim, int value_dim, int64_t k_pos_stride,
+                    int64_t k_batch_stride, int64_t k_head_stride, int64_t v_pos_stride,
+                    int64_t v_batch_stride, int64_t v_head_stride, float scale, int dtype,
+                    int out_dtype, void* stream);
+
+/*
+ * Sigmoid output gate: out[i] = values[i] * sigmoid(gate[i]) for i < n, with
+ * the stable two-branch sigmoid of tensor.stable_sigmoid (tensor.py:123-129).
+ * Replaces Qwen35RocmOps.sigmoid_gate (qwen35_rocm_ops.py:286-290) and
+ * qwen35_cuda._sigmoid_gate (qwen35_cuda.py:953-963).  values/gate use
+ * `dtype`, out uses `out_dtype`; out may alias values when the dtypes match.
+ */
+int alpx_sigmoid_gate(const void* values, const void* gate, void* out, int64_t n, int dtype,
+                      int out_dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ALPX_H */

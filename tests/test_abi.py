@@ -1,0 +1,87 @@
+"""CPU checks of the C-ABI boundary: the library loads, exports every symbol
+the header declares, and rejects contract violations before touching the
+GPU (no compute calls are made here)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "alpx.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(alpx_\w+)\s*\(", text)))
+
+
+def test_header_symbols_exported(pkg):
+    lib = pkg._lib.lib()
+    names = _declared()
+    assert "alpx_decode_gqa" in names and "alpx_kv_append" in names
+    for name in names:
+        assert hasattr(lib, name), name
+        assert name in pkg._lib.SIGNATURES, f"{name} has no ctypes signature"
+    assert lib.alpx_abi_version() == pkg._lib.ABI_VERSION
+
+
+def test_header_abi_version_matches_binding(pkg):
+    m = re.search(r"#define ALPX_ABI_VERSION (\d+)", open(HEADER).read())
+    assert int(m.group(1)) == pkg._lib.ABI_VERSION
+
+
+def test_null_buffers_rejected_without_gpu(pkg):
+    lib = pkg._lib.lib()
+    rc = lib.alpx_kv_append(None, None, None, None, 0, 8, 1, 1, 4, 4, 1, 0, None, None)
+    assert rc == pkg._lib.EINVAL and "null" in pkg._lib.last_error()
+    rc = lib.alpx_decode_gqa(None, None, None, None, 4, None, None, None, 0, 1, 4, 2, 64, 64,
+                             128, 0, 64, 128, 0, 64, 0.125, 0, 0, None)
+    assert rc == pkg._lib.EINVAL
+    with pytest.raises(ValueError):
+        pkg._lib.check(rc)
+
+
+def test_range_and_shape_errors_without_gpu(pkg):
+    lib = pkg._lib.lib()
+    fake = ctypes.c_void_p(256)  # never dereferenced: validation fails first
+    rc = lib.alpx_kv_append(fake, fake, fake, fake, 1, 8, 1, 1, 4, 4, 2, 7, None, None)
+    assert rc == pkg._lib.ERANGE and "exceeds capacity" in pkg._lib.last_error()
+    rc = lib.alpx_decode_gqa(fake, fake, fake, None, 4, None, fake, fake, 1 << 20, 1, 6, 4, 64,
+                             64, 256, 0, 64, 256, 0, 64, 0.125, 1, 1, None)
+    assert rc == pkg._lib.EINVAL and "multiple of KV heads" in pkg._lib.last_error()
+    rc = lib.alpx_decode_gqa(fake, fake, fake, None, 4, None, fake, fake, 16, 1, 8, 4, 64,
+                             64, 256, 0, 64, 256, 0, 64, 0.125, 1, 1, None)
+    assert rc == pkg._lib.EINVAL and "workspace" in pkg._lib.last_error()
+    rc = lib.alpx_decode_gqa(fake, fake, fake, None, 4, None, fake, fake, 1 << 20, 1, 8, 4,
+                             512, 512, 256, 0, 64, 256, 0, 64, 0.125, 1, 1, None)
+    assert rc == pkg._lib.EUNSUPPORTED
+
+
+def test_decode_workspace_sizes(pkg):
+    lib = pkg._lib.lib()
+    assert lib.alpx_decode_workspace_bytes(16, 32, 8, 128, 8192) > 0
+    assert lib.alpx_decode_workspace_bytes(16, 30, 8, 128, 8192) == 0  # not a multiple
+    # grows with the number of partial slots, never below the 1-slot size
+    one = 3 * 256
+    assert lib.alpx_decode_workspace_bytes(1, 1, 1, 64, 1) >= one
+
+
+def test_facade_validation_mirrors_reference(pkg):
+    import importlib
+
+    import torch
+    m = importlib.import_module(pkg.__name__ + ".qwen35_rocm_ops")
+    cap = m.RocmCapability(True, "injected", 0, "gfx950")
+    ops = m.Qwen35RocmOps(_capability=cap)
+    t = torch.zeros(2, 2, 2)
+    with pytest.raises(TypeError, match="must remain on the ROCm device"):
+        ops.attention_append_(torch.zeros(4, 2, 2, 2), torch.zeros(4, 2, 2, 2), 0, t, t)
+    with pytest.raises(TypeError, match="must be a PyTorch tensor"):
+        ops.online_attention([1.0], t, t, length=1)
+    with pytest.raises(m.Qwen35RocmUnavailable):
+        m.Qwen35RocmOps(_capability=m.RocmCapability(False, "no device"))
+    with pytest.raises(ValueError, match="positive integer"):
+        ops.zeros((0, 2))
