@@ -33,7 +33,25 @@ SIGNATURES = {
                                  _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_float,
                                  _c_int, _c_int, _c_ptr]),
     "alpx_sigmoid_gate": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_i64, _c_int, _c_int, _c_ptr]),
+    "alpx_timing_enable": (_c_int, [_c_int]),
+    "alpx_timing_read": (_c_int, [_c_int, ctypes.POINTER(ctypes.c_double),
+                                  ctypes.POINTER(ctypes.c_int64)]),
 }
+
+# alpx_timed_kernel ids
+T_KV_APPEND, T_DECODE, T_DECODE_COMBINE, T_PREFILL, T_GDN_CHUNK, T_GDN_STEP, T_AUX = range(7)
+
+
+def timing_enable(on: bool) -> None:
+    check(lib().alpx_timing_enable(1 if on else 0))
+
+
+def timing_read(kernel: int) -> tuple[float, int]:
+    """(summed milliseconds, launches) recorded for ``kernel`` since enable."""
+    total = ctypes.c_double()
+    count = ctypes.c_int64()
+    check(lib().alpx_timing_read(int(kernel), ctypes.byref(total), ctypes.byref(count)))
+    return total.value, count.value
 
 
 class AlpxUnavailable(RuntimeError):
@@ -119,13 +137,12 @@ _workspaces: dict = {}
 
 
 def workspace(torch, device, nbytes: int):
-    """A grow-only scratch buffer per device, owned by this module.
-
+    """A grow-only scratch workspace per device, owned by this module.
     Calls that share it are ordered on one stream (the reference's
     one-caller-at-a-time contract, serve.py:326)."""
     key = str(device)
     buf = _workspaces.get(key)
     if buf is None or buf.numel() < nbytes:
-        buf = torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+        buf = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device)
         _workspaces[key] = buf
     return buf

@@ -27,6 +27,30 @@ int check_launch(const char* what) {
   return ALPX_OK;
 }
 
+int resident_blocks(const void* kernel, int block, size_t lds) {
+  struct Entry {
+    const void* kernel;
+    int device;
+    int value;
+  };
+  static thread_local Entry cache[32];
+  static thread_local int used = 0;
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess) device = 0;
+  for (int i = 0; i < used; ++i)
+    if (cache[i].kernel == kernel && cache[i].device == device) return cache[i].value;
+  int per_cu = 0, cus = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, lds) != hipSuccess ||
+      per_cu <= 0)
+    per_cu = 1;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+      cus <= 0)
+    cus = 256;
+  const int value = per_cu * cus;
+  if (used < 32) cache[used++] = {kernel, device, value};
+  return value;
+}
+
 }  // namespace alpx
 
 extern "C" {

@@ -57,6 +57,30 @@ __device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+// gfx950 transposing LDS read (ds_read_b64_tr_b16).  Within each group of
+// 16 lanes, lane i = 4k + q supplies the address of 4 consecutive 16-bit
+// elements (row R_k, columns C + 4q .. C + 4q + 3 of a row-major tile);
+// lane j of the group receives column C + j of rows R_0 .. R_3.  Used to
+// read a row-major [row][col] LDS tile as MFMA operands that need 4
+// consecutive rows of one column per lane.
+__device__ __forceinline__ f16x4 lds_read_tr4(const f16_t* p) {
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4*)(p));
+  return __builtin_bit_cast(f16x4, v);
+}
+__device__ __forceinline__ bf16x4 lds_read_tr4(const bf16_t* p) {
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4*)(p));
+  return __builtin_bit_cast(bf16x4, v);
+}
+
+// Blocks of `kernel` (with `block` threads, `lds` dynamic bytes) that fit on
+// one CU at once, times the CU count of the current device (cached per
+// kernel and device).
+int resident_blocks(const void* kernel, int block, size_t lds);
+
 inline size_t dtype_size(int dtype) {
   return dtype == ALPX_F32 ? 4 : 2;
 }

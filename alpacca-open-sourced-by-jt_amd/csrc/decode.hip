@@ -1,29 +1,35 @@
 // Split-K flash-decode for single-token GQA attention, plus the combine pass.
 //
 // Pass 1 (split): the cache rows of one (sequence, kv head) are cut into
-// chunks; every chunk is one "slot" owned by one wavefront, which streams its
-// rows once and produces an online-softmax partial (running max m in the
-// base-2 domain, running sum l, unnormalised accumulator acc[Dv]) for every
-// query head of the GQA group.  K and V are read exactly once per group, so
-// the 4 (Llama-3-8B) or 8 (Qwen3.5) query heads of a group share each byte.
+// chunks, one per block; each block streams its rows once and produces an
+// online-softmax partial (running max m in the base-2 domain, running sum l,
+// unnormalised accumulator acc[Dv]) for every query head of the GQA group.
+// K and V are read exactly once per group, so the 4 (Llama-3-8B) or 8
+// (Qwen3.5) query heads of a group share each byte.  The grid is sized from
+// the occupancy API so that all blocks are resident in a single round.
 //
-//  * fp16/bf16, head_dim 64/128/256 (decode_split_mfma): each wavefront takes
-//    32 rows per step.  K rows are loaded with 128-bit loads straight into
-//    the A operand of v_mfma_f32_16x16x32_{f16,bf16} (S^T = K Q^T: 16 rows x
-//    16 query heads per instruction), so scores need no cross-lane dot-product
-//    reduction.  V rows are loaded with 128-bit loads, staged in a per-wave
-//    LDS tile and read back transposed as the A operand of O^T = V^T P^T, so
-//    the probabilities never leave the registers the score MFMA wrote them
-//    to.  The softmax max is a 2-step cross-lane (xor 16, xor 32) reduction.
+//  * fp16/bf16, head_dim 64/128/256 (decode_split_mfma): 4 wavefronts per
+//    block, 32 rows per wave step.  K rows are loaded with 128-bit loads
+//    straight into the A operand of v_mfma_f32_16x16x32_{f16,bf16}
+//    (S^T = K Q^T: 16 rows x 16 query heads per instruction), so scores need
+//    no cross-lane dot-product reduction.  V rows are loaded with 128-bit
+//    loads, staged in a per-wave LDS tile and read back with transposing LDS
+//    reads as the A operand of O^T = V^T P^T, so the probabilities never
+//    leave the registers the score MFMA wrote them to.  The softmax max is a
+//    2-step cross-lane (xor 16, xor 32) reduction.
 //  * everything else (fp32, odd head dims, unaligned caches):
-//    decode_split_generic, one wavefront per slot, VALU dot products.
+//    decode_split_generic, one wavefront per block, VALU dot products.
 //
-// Pass 2 (combine): per (sequence, query head), merge the slot partials with
-// weights 2^(m_s - M), divide by the merged sum, apply the optional sigmoid
-// output gate, and store in the output dtype.
+// Pass 2 (combine): per (sequence, query head, 64 output columns), merge the
+// block partials with weights 2^(m_s - M), divide by the merged sum, apply
+// the optional sigmoid output gate and store in the output dtype.  (A
+// single-launch variant where the last block of a group merges was measured
+// 2.4x slower: the device-scope release/acquire fences it needs write back
+// and invalidate the XCD L2 in every block.)
 #include <math.h>
 
 #include "alpx_common.h"
+#include "timing.h"
 
 namespace alpx {
 namespace {
@@ -69,24 +75,39 @@ __device__ __forceinline__ void wave_sync_lds() {
 
 // ------------------------------------------------------------ MFMA split
 
+template <typename T> struct Vec4;
+template <> struct Vec4<f16_t> { typedef f16x4 type; };
+template <> struct Vec4<bf16_t> { typedef bf16x4 type; };
+
+// One block = 4 wavefronts sharing one chunk of rows of one (sequence, kv
+// head, 16-head column block).  Wave w takes the 32-row tiles w, w+4, ...;
+// the next tile's K/V loads are issued before the current tile's softmax and
+// PV so every wave keeps a tile in flight.  At the end the four waves' online
+// softmax states are merged through LDS into one partial per block.
 template <typename T, int D>
 __global__ void __launch_bounds__(256)
 decode_split_mfma(DecodeArgs a) {
   typedef typename Vec8<T>::type V8;
+  typedef typename Vec4<T>::type V4;
   constexpr int kStride = D + 8;          // LDS row stride (elements), 16-byte aligned rows
   constexpr int kUnits = D / 8;           // 16-byte units per row
   constexpr int kVIters = kTile * kUnits / 64;
-  __shared__ __attribute__((aligned(16))) T vtile[kWaves][kTile * kStride];
+  constexpr int kTileElems = kTile * kStride;
+  constexpr int kMergeO = (kWaves - 1) * (D / 16) * 64 * 4;   // floats
+  constexpr int kMergeFloats = kMergeO + 2 * (kWaves - 1) * 64;
+  constexpr int kTileBytes = kWaves * kTileElems * (int)sizeof(T);
+  constexpr int kLdsBytes = kTileBytes > kMergeFloats * 4 ? kTileBytes : kMergeFloats * 4;
+  __shared__ __attribute__((aligned(16))) char smem[kLdsBytes];
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int b = blockIdx.z;
   const int hc = blockIdx.y % a.head_chunks;
   const int kvh = blockIdx.y / a.head_chunks;
-  const int slot = blockIdx.x * kWaves + wave;
   const int len = seq_len(a, b);
-  const int start = slot * a.chunk;
+  const int start = blockIdx.x * a.chunk;
   const int end = min(start + a.chunk, len);
+  const int last = end - 1;
   const int hl = lane & 15;  // query-head column (N index) of this lane
   const int quad = lane >> 4;
   const int g_in = hc * 16 + hl;
@@ -110,31 +131,32 @@ decode_split_mfma(DecodeArgs a) {
   float m = -INFINITY;
   float l = 0.f;
 
-  const T* kbase = (const T*)a.k + (int64_t)b * a.ks_b + (int64_t)kvh * a.ks_h;
+  const T* kbase = (const T*)a.k + (int64_t)b * a.ks_b + (int64_t)kvh * a.ks_h + 8 * quad;
   const T* vbase = (const T*)a.v + (int64_t)b * a.vs_b + (int64_t)kvh * a.vs_h;
-  T* lds = vtile[wave];
+  T* lds = (T*)smem + wave * kTileElems;
 
-  for (int p0 = start; p0 < end; p0 += kTile) {
-    const int last = end - 1;
-    // K rows -> MFMA A operand: lane holds K[p0 + 16 blk + hl][32 ks + 8 quad + 0..7].
-    V8 kr[2][D / 32];
+  V8 kr[2][D / 32];   // K rows -> A operand: K[p0 + 16 blk + hl][32 ks + 8 quad + 0..7]
+  V8 vr[kVIters];     // V rows, 16 bytes per lane, row-major
+  auto load_tile = [&](int p) {
 #pragma unroll
     for (int blk = 0; blk < 2; ++blk) {
-      const int pos = min(p0 + 16 * blk + hl, last);
-      const T* row = kbase + (int64_t)pos * a.ks_pos + 8 * quad;
+      const T* row = kbase + (int64_t)min(p + 16 * blk + hl, last) * a.ks_pos;
 #pragma unroll
       for (int ks = 0; ks < D / 32; ++ks) kr[blk][ks] = *(const V8*)(row + 32 * ks);
     }
-    // V rows, 16 bytes per lane, row-major into registers.
-    V8 vr[kVIters];
 #pragma unroll
     for (int it = 0; it < kVIters; ++it) {
       const int u = it * 64 + lane;
       const int r = u / kUnits;
       const int c = u - r * kUnits;
-      const int pos = min(p0 + r, last);
-      vr[it] = *(const V8*)(vbase + (int64_t)pos * a.vs_pos + 8 * c);
+      vr[it] = *(const V8*)(vbase + (int64_t)min(p + r, last) * a.vs_pos + 8 * c);
     }
+  };
+
+  int p0 = start + kTile * wave;
+  if (p0 < end) load_tile(p0);
+  while (p0 < end) {
+    const int pn = p0 + kTile * kWaves;
     // Scores for 32 rows x 16 heads: lane holds S[pos = p0 + 16 blk + 4 quad + i][hl].
     f32x4 s[2];
 #pragma unroll
@@ -143,7 +165,7 @@ decode_split_mfma(DecodeArgs a) {
 #pragma unroll
       for (int ks = 0; ks < D / 32; ++ks) s[blk] = mfma16x16x32(kr[blk][ks], qv[ks], s[blk]);
     }
-    // Stage V in LDS (row-major, padded rows).
+    // Stage V in LDS (row-major, padded rows), then prefetch the next tile.
 #pragma unroll
     for (int it = 0; it < kVIters; ++it) {
       const int u = it * 64 + lane;
@@ -151,6 +173,7 @@ decode_split_mfma(DecodeArgs a) {
       const int c = u - r * kUnits;
       *(V8*)(lds + r * kStride + 8 * c) = vr[it];
     }
+    if (pn < end) load_tile(pn);
     // Online softmax (base 2).  Slot j of this lane is row 16 (j/4) + 4 quad + j%4.
     float sv[8];
     float mx = -INFINITY;
@@ -163,7 +186,7 @@ decode_split_mfma(DecodeArgs a) {
     }
     mx = fmaxf(mx, __shfl_xor(mx, 16));
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float mn = fmaxf(m, mx);  // finite: every step holds at least one live row
+    const float mn = fmaxf(m, mx);  // finite: every tile holds at least one live row
     const float alpha = fast_exp2(m - mn);
     V8 pv;
     float ps = 0.f;
@@ -178,31 +201,67 @@ decode_split_mfma(DecodeArgs a) {
 #pragma unroll
     for (int mb = 0; mb < D / 16; ++mb) o[mb] *= alpha;
     wave_sync_lds();
-    // O^T += V^T P^T: A operand lane holds V[row(quad, j)][16 mb + hl], j = 0..7.
+    // O^T += V^T P^T.  A operand: lane holds V[row(quad, j)][16 mb + hl], j = 0..7,
+    // gathered with two transposing reads of 4 rows (16 h + 4 quad + 0..3) each.
+    const int tr_row = 4 * quad + (hl >> 2);
+    const int tr_col = 4 * (hl & 3);
 #pragma unroll
     for (int mb = 0; mb < D / 16; ++mb) {
-      V8 va;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int r = 16 * (j >> 2) + 4 * quad + (j & 3);
-        va[j] = lds[r * kStride + 16 * mb + hl];
-      }
+      const V4 lo = lds_read_tr4(lds + tr_row * kStride + 16 * mb + tr_col);
+      const V4 hi = lds_read_tr4(lds + (16 + tr_row) * kStride + 16 * mb + tr_col);
+      const V8 va = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
       o[mb] = mfma16x16x32(va, pv, o[mb]);
     }
     wave_sync_lds();
+    p0 = pn;
   }
 
+  // Merge the four waves' states (same lane layout) into wave 0.
   l += __shfl_xor(l, 16);
   l += __shfl_xor(l, 32);
-  if (head_ok) {
-    const int64_t pidx = ((int64_t)b * a.q_heads + h) * a.nsplit + slot;
-    if (quad == 0) {
-      a.part_m[pidx] = m;
-      a.part_l[pidx] = l;
-    }
-    float* pa = a.part_acc + pidx * D + 4 * quad;
+  __syncthreads();
+  float* mf = (float*)smem;
+  float* mm = mf + kMergeO;
+  float* ml = mm + (kWaves - 1) * 64;
+  if (wave > 0) {
 #pragma unroll
-    for (int mb = 0; mb < D / 16; ++mb) *(f32x4*)(pa + 16 * mb) = o[mb];
+    for (int mb = 0; mb < D / 16; ++mb)
+      *(f32x4*)(mf + (((wave - 1) * (D / 16) + mb) * 64 + lane) * 4) = o[mb];
+    mm[(wave - 1) * 64 + lane] = m;
+    ml[(wave - 1) * 64 + lane] = l;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    float mw[kWaves - 1];
+    float M = m;
+#pragma unroll
+    for (int w = 0; w < kWaves - 1; ++w) {
+      mw[w] = mm[w * 64 + lane];
+      M = fmaxf(M, mw[w]);
+    }
+    const bool any = M != -INFINITY;
+    const float c0 = any ? fast_exp2(m - M) : 0.f;
+    float L = l * c0;
+#pragma unroll
+    for (int mb = 0; mb < D / 16; ++mb) o[mb] *= c0;
+#pragma unroll
+    for (int w = 0; w < kWaves - 1; ++w) {
+      const float cw = any ? fast_exp2(mw[w] - M) : 0.f;
+      L += ml[w * 64 + lane] * cw;
+#pragma unroll
+      for (int mb = 0; mb < D / 16; ++mb)
+        o[mb] += cw * *(const f32x4*)(mf + ((w * (D / 16) + mb) * 64 + lane) * 4);
+    }
+    if (head_ok) {
+      const int64_t pidx = ((int64_t)b * a.q_heads + h) * a.nsplit + blockIdx.x;
+      if (quad == 0) {
+        a.part_m[pidx] = M;
+        a.part_l[pidx] = L;
+      }
+      float* pa = a.part_acc + pidx * D + 4 * quad;
+#pragma unroll
+      for (int mb = 0; mb < D / 16; ++mb) *(f32x4*)(pa + 16 * mb) = o[mb];
+    }
   }
 }
 
@@ -314,90 +373,78 @@ decode_split_generic(DecodeArgs a) {
 
 // ------------------------------------------------------------ combine
 
+// Pass 2: block (b*Hq + h, 64-column slice) merges the split partials of one
+// query head for 64 output columns.  Every thread derives the merged max M
+// and sum L from the (few) partial (m, l) pairs; the four waves each sum a
+// quarter of the partials with independent loads and reduce through LDS.
 template <typename T, typename TO>
 __global__ void __launch_bounds__(256)
 decode_combine(DecodeArgs a) {
-  __shared__ float w[kMaxSlots];
-  __shared__ float red[256];
-  const int bh = blockIdx.x;
-  const int tid = threadIdx.x;
-  const int ns = a.nsplit;
-  const float* pm = a.part_m + (int64_t)bh * ns;
-  const float* pl = a.part_l + (int64_t)bh * ns;
-
-  float mx = -INFINITY;
-  for (int s = tid; s < ns; s += blockDim.x) mx = fmaxf(mx, pm[s]);
-  red[tid] = mx;
-  __syncthreads();
-  for (int off = blockDim.x / 2; off > 0; off >>= 1) {
-    if (tid < off) red[tid] = fmaxf(red[tid], red[tid + off]);
-    __syncthreads();
-  }
-  const float M = red[0];
-  __syncthreads();
-  float lsum = 0.f;
-  for (int s = tid; s < ns; s += blockDim.x) {
-    const float ws = (M == -INFINITY) ? 0.f : fast_exp2(pm[s] - M);
-    w[s] = ws;
-    lsum += pl[s] * ws;
-  }
-  red[tid] = lsum;
-  __syncthreads();
-  for (int off = blockDim.x / 2; off > 0; off >>= 1) {
-    if (tid < off) red[tid] += red[tid + off];
-    __syncthreads();
-  }
-  const float L = red[0];
-  const float inv = L > 0.f ? 1.0f / L : 0.f;
+  __shared__ float red[kWaves][64];
+  const int64_t bh = blockIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int d = blockIdx.y * 64 + lane;
   const int DV = a.value_dim;
-  const float* pa = a.part_acc + (int64_t)bh * ns * DV;
-  for (int d = tid; d < DV; d += blockDim.x) {
-    float accv = 0.f;
-    for (int s = 0; s < ns; ++s) accv += pa[(int64_t)s * DV + d] * w[s];
-    float r = accv * inv;
-    if (a.gate != nullptr) r *= stable_sigmoid(to_f32(((const T*)a.gate)[(int64_t)bh * DV + d]));
-    ((TO*)a.out)[(int64_t)bh * DV + d] = from_f32<TO>(r);
+  const int ns = a.nsplit;
+  const float* pm = a.part_m + bh * ns;
+  const float* pl = a.part_l + bh * ns;
+  float M = -INFINITY;
+  for (int s = 0; s < ns; ++s) M = fmaxf(M, pm[s]);
+  float acc0 = 0.f, acc1 = 0.f;
+  if (d < DV && M != -INFINITY) {
+    const float* pa = a.part_acc + bh * ns * DV + d;
+    int s = wave;
+    for (; s + kWaves < ns; s += 2 * kWaves) {
+      const float x0 = pa[(int64_t)s * DV];
+      const float x1 = pa[(int64_t)(s + kWaves) * DV];
+      acc0 += x0 * fast_exp2(pm[s] - M);
+      acc1 += x1 * fast_exp2(pm[s + kWaves] - M);
+    }
+    if (s < ns) acc0 += pa[(int64_t)s * DV] * fast_exp2(pm[s] - M);
   }
+  red[wave][lane] = acc0 + acc1;
+  __syncthreads();
+  if (wave != 0 || d >= DV) return;
+  float L = 0.f;
+  if (M != -INFINITY)
+    for (int s = 0; s < ns; ++s) L += pl[s] * fast_exp2(pm[s] - M);
+  const float acc = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
+  float r = L > 0.f ? acc / L : 0.f;
+  if (a.gate != nullptr) r *= stable_sigmoid(to_f32(((const T*)a.gate)[bh * DV + d]));
+  ((TO*)a.out)[bh * DV + d] = from_f32<TO>(r);
 }
 
 // ------------------------------------------------------------ planning
 
 struct Plan {
-  int nsplit;   // slots per (b, h) == partial count
-  int chunk;    // rows per slot
-  int grid_x;   // blocks along the split axis
+  int nsplit;   // partials per (b, h) == blocks along the split axis
+  int chunk;    // rows per block
 };
 
-int target_slots() {
-  static int value = -1;
-  if (value < 0) {
-    const char* env = getenv("ALPX_DECODE_SLOTS");
-    value = env ? atoi(env) : 0;
-    if (value <= 0) value = 3072;
-  }
-  return value;
+// Upper bound on partials per (b, h) for a cache of `length` rows; every
+// plan stays within it, so the workspace size does not depend on the device.
+int max_slots(int length) {
+  int n = (length + kGenericTile - 1) / kGenericTile;
+  return n < kMaxSlots ? (n < 1 ? 1 : n) : kMaxSlots;
 }
 
-Plan plan_split(int batch, int kv_heads, int head_chunks, int length, bool mfma) {
-  Plan p;
-  const int unit = mfma ? kTile : kGenericTile;
-  const int per_block = mfma ? kWaves : 1;
-  const int pairs = batch * kv_heads * head_chunks;
-  int want = (target_slots() + pairs - 1) / pairs;
-  const int max_slots = (length + unit - 1) / unit;
-  if (want > max_slots) want = max_slots;
+// Size the split so the whole grid is resident at once (one round of blocks
+// over the device), with each block's chunk a whole number of wave tiles.
+Plan plan_split(int pairs, int length, int resident, int unit) {
+  int want = (resident + pairs - 1) / pairs;
+  const int most = (length + unit - 1) / unit;
+  if (want > most) want = most;
   if (want < 1) want = 1;
   int chunk = (length + want - 1) / want;
   chunk = ((chunk + unit - 1) / unit) * unit;
-  if (chunk < unit) chunk = unit;
-  int slots = (length + chunk - 1) / chunk;
-  if (slots < 1) slots = 1;
-  while (((slots + per_block - 1) / per_block) * per_block > kMaxSlots) {
+  int n = (length + chunk - 1) / chunk;
+  while (n > max_slots(length)) {
     chunk += unit;
-    slots = (length + chunk - 1) / chunk;
+    n = (length + chunk - 1) / chunk;
   }
-  p.grid_x = (slots + per_block - 1) / per_block;
-  p.nsplit = p.grid_x * per_block;
+  Plan p;
+  p.nsplit = n;
   p.chunk = chunk;
   return p;
 }
@@ -410,43 +457,44 @@ size_t workspace_for(int batch, int q_heads, int value_dim, int nsplit) {
 }
 
 template <typename T>
-int launch_split(bool mfma, int D, const DecodeArgs& a, dim3 grid, hipStream_t s) {
+const void* split_kernel(bool mfma, int D) {
   if (mfma) {
     if constexpr (sizeof(T) == 2) {
       switch (D) {
-        case 64:
-          hipLaunchKernelGGL((decode_split_mfma<T, 64>), grid, dim3(256), 0, s, a);
-          return check_launch("decode_split_mfma<64>");
-        case 128:
-          hipLaunchKernelGGL((decode_split_mfma<T, 128>), grid, dim3(256), 0, s, a);
-          return check_launch("decode_split_mfma<128>");
-        case 256:
-          hipLaunchKernelGGL((decode_split_mfma<T, 256>), grid, dim3(256), 0, s, a);
-          return check_launch("decode_split_mfma<256>");
+        case 64: return (const void*)decode_split_mfma<T, 64>;
+        case 128: return (const void*)decode_split_mfma<T, 128>;
+        case 256: return (const void*)decode_split_mfma<T, 256>;
       }
     }
-    return fail(ALPX_EUNSUPPORTED, "decode: no MFMA kernel for head_dim %d", D);
+    return nullptr;
   }
-  hipLaunchKernelGGL((decode_split_generic<T>), grid, dim3(64), 0, s, a);
-  return check_launch("decode_split_generic");
+  return (const void*)decode_split_generic<T>;
 }
 
 template <typename T>
 int launch_combine(int out_dtype, const DecodeArgs& a, hipStream_t s) {
-  dim3 grid(a.batch * a.q_heads);
-  dim3 block(a.value_dim > 128 ? 256 : 128);
+  dim3 grid(a.batch * a.q_heads, (a.value_dim + 63) / 64);
   switch (out_dtype) {
     case ALPX_F32:
-      hipLaunchKernelGGL((decode_combine<T, float>), grid, block, 0, s, a);
+      hipLaunchKernelGGL((decode_combine<T, float>), grid, dim3(256), 0, s, a);
       break;
     case ALPX_F16:
-      hipLaunchKernelGGL((decode_combine<T, f16_t>), grid, block, 0, s, a);
+      hipLaunchKernelGGL((decode_combine<T, f16_t>), grid, dim3(256), 0, s, a);
       break;
     default:
-      hipLaunchKernelGGL((decode_combine<T, bf16_t>), grid, block, 0, s, a);
+      hipLaunchKernelGGL((decode_combine<T, bf16_t>), grid, dim3(256), 0, s, a);
       break;
   }
   return check_launch("decode_combine");
+}
+
+template <typename T>
+int launch_split(const void* kernel, bool mfma, const DecodeArgs& a, dim3 grid, hipStream_t s) {
+  void* args[] = {(void*)&a};
+  hipError_t err = hipLaunchKernel(kernel, grid, dim3(mfma ? 256 : 64), args, 0, s);
+  if (err != hipSuccess)
+    return fail(ALPX_EHIP, "decode split launch failed: %s", hipGetErrorString(err));
+  return check_launch("decode_split");
 }
 
 }  // namespace
@@ -458,12 +506,7 @@ extern "C" size_t alpx_decode_workspace_bytes(int batch, int q_heads, int kv_hea
   if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || value_dim <= 0 || max_len <= 0 ||
       q_heads % kv_heads != 0)
     return 0;
-  const int group = q_heads / kv_heads;
-  const int hc = (group + 15) / 16;
-  const Plan pm = plan_split(batch, kv_heads, hc, max_len, true);
-  const Plan pg = plan_split(batch, kv_heads, hc, max_len, false);
-  const int ns = pm.nsplit > pg.nsplit ? pm.nsplit : pg.nsplit;
-  return workspace_for(batch, q_heads, value_dim, ns);
+  return workspace_for(batch, q_heads, value_dim, max_slots(max_len));
 }
 
 extern "C" int alpx_decode_gqa(const void* q, const void* key_cache, const void* value_cache,
@@ -499,11 +542,21 @@ extern "C" int alpx_decode_gqa(const void* q, const void* key_cache, const void*
   const bool mfma = dtype != ALPX_F32 && key_dim == value_dim &&
                     (key_dim == 64 || key_dim == 128 || key_dim == 256) && (align & 15) == 0 &&
                     getenv("ALPX_DECODE_GENERIC") == nullptr;
-  const Plan p = plan_split(batch, kv_heads, hc, length, mfma);
-  const size_t need = workspace_for(batch, q_heads, value_dim, p.nsplit);
+  const size_t need = workspace_for(batch, q_heads, value_dim, max_slots(length));
   if (workspace_bytes < need)
     return fail(ALPX_EINVAL, "alpx_decode_gqa: workspace holds %zu bytes, needs %zu",
                 workspace_bytes, need);
+
+  const void* kernel = nullptr;
+  switch (dtype) {
+    case ALPX_F32: kernel = split_kernel<float>(false, key_dim); break;
+    case ALPX_F16: kernel = split_kernel<f16_t>(mfma, key_dim); break;
+    default: kernel = split_kernel<bf16_t>(mfma, key_dim); break;
+  }
+  if (kernel == nullptr) return fail(ALPX_EUNSUPPORTED, "decode: no kernel for this shape");
+  const int unit = mfma ? kTile * kWaves : kGenericTile;
+  const Plan p = plan_split(batch * kv_heads * hc, length,
+                            resident_blocks(kernel, mfma ? 256 : 64, 0), unit);
 
   DecodeArgs a;
   a.q = q;
@@ -536,14 +589,14 @@ extern "C" int alpx_decode_gqa(const void* q, const void* key_cache, const void*
   a.scale_log2 = scale * kLog2e;
 
   hipStream_t s = (hipStream_t)stream;
-  dim3 grid(p.grid_x, kv_heads * hc, batch);
+  dim3 grid(p.nsplit, kv_heads * hc, batch);
   int rc;
-  switch (dtype) {
-    case ALPX_F32: rc = launch_split<float>(false, key_dim, a, grid, s); break;
-    case ALPX_F16: rc = launch_split<f16_t>(mfma, key_dim, a, grid, s); break;
-    default: rc = launch_split<bf16_t>(mfma, key_dim, a, grid, s); break;
+  {
+    TimedRegion timed(ALPX_T_DECODE, s);
+    rc = launch_split<float>(kernel, mfma, a, grid, s);
   }
   if (rc != ALPX_OK) return rc;
+  TimedRegion timed(ALPX_T_DECODE_COMBINE, s);
   switch (dtype) {
     case ALPX_F32: return launch_combine<float>(out_dtype, a, s);
     case ALPX_F16: return launch_combine<f16_t>(out_dtype, a, s);

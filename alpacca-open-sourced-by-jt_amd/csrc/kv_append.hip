@@ -7,6 +7,7 @@
 // head_dim 128 moves 16 bytes per lane with fully coalesced reads and
 // writes.  K and V travel in one launch (blockIdx.y selects the tensor).
 #include "alpx_common.h"
+#include "timing.h"
 
 namespace alpx {
 namespace {
@@ -70,6 +71,7 @@ extern "C" int alpx_kv_append(void* key_cache, void* value_cache, const void* ke
       return fail(ALPX_ERANGE, "attention cache position exceeds capacity (%lld + %d > %lld)",
                   (long long)position, tokens, (long long)capacity);
   }
+  TimedRegion timed(ALPX_T_KV_APPEND, (hipStream_t)stream);
   const int64_t es = (int64_t)dtype_size(dtype);
   const int64_t kb = (int64_t)kv_heads * key_dim * es;
   const int64_t vb = (int64_t)kv_heads * value_dim * es;

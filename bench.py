@@ -1,0 +1,225 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X attention path; prints ONE JSON line.
+
+Headline (``value``): GQA decode attention at 8K context -- BASELINE config
+C2, uniform-8192 variant: 16 sequences x 8192 cached rows, 32 query / 8 KV
+heads, head_dim 128, fp16 cache in the ROCm layout [8192, 16, 8, 128] --
+reported as algorithmic HBM GB/s (K + V bytes of every valid row, plus q and
+o) per decode step, whole step (split + combine) timed.  ``roofline`` covers
+the dominant kernel (the split-K pass), timed with HIP events recorded by
+the library on its launch stream over the timed region.  ``extra`` carries
+the other configs (C1 fp32 decode, C4 gated bf16 decode, ...).
+``cpu_baseline`` times the NumPy oracle (the reference's two-pass llama
+algorithm, fp32) on the same C2 workload on this host.
+
+Inputs are synthetic N(0, 1) (seeded), generated on the device.
+"""
+
+from __future__ import annotations
+
+import argparse
+import importlib
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+PACKAGE = "alpacca-open-sourced-by-jt_amd"
+
+METRIC = ("decode attn HBM GB/s (% of peak) @8K ctx; "
+          "prefill attn TFLOP/s (% MFMA peak)")
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def _mod(name):
+    return importlib.import_module(f"{PACKAGE}.{name}")
+
+
+def _timed_steps(torch, fn, steps, warmup):
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps * 1e3
+
+
+def _kernel_avg_ms(lib, kernel):
+    total, count = lib.timing_read(kernel)
+    return (total / count) if count else float("nan")
+
+
+def bench_decode(torch, ops, lib, *, batch, ctx, hq, hkv, d, dtype, gate, steps, warmup,
+                 seed):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    dev = torch.device("cuda")
+    q = torch.randn((batch, hq, d), generator=g, device=dev).to(dtype)
+    K = torch.randn((ctx, batch, hkv, d), generator=g, device=dev).to(dtype)
+    V = torch.randn((ctx, batch, hkv, d), generator=g, device=dev).to(dtype)
+    gt = torch.randn((batch, hq, d), generator=g, device=dev).to(dtype) if gate else None
+    fn = lambda: ops.online_attention(q, K, V, length=ctx, gate=gt)  # noqa: E731
+    # Timed region 1: the K steps as a caller runs them (value, ms_per_step).
+    ms = _timed_steps(torch, fn, steps, warmup)
+    # Timed region 2: the same K steps with the library's HIP-event brackets
+    # on the launch stream, for per-kernel durations (roofline).  Event
+    # records cost a few microseconds each, so region 1 excludes them.
+    lib.timing_enable(True)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    ev_ms = (time.perf_counter() - t0) / steps * 1e3
+    split_ms = _kernel_avg_ms(lib, lib.T_DECODE)
+    comb_ms = _kernel_avg_ms(lib, lib.T_DECODE_COMBINE)
+    lib.timing_enable(False)
+    es = q.element_size()
+    kv_bytes = 2 * ctx * batch * hkv * d * es
+    q_bytes = batch * hq * d * es
+    step_bytes = kv_bytes + q_bytes * (3 if gate else 2)  # + gate + o
+    return {
+        "ms_per_step": ms,
+        "gbs": step_bytes / (ms * 1e-3) / 1e9,
+        "split_ms": split_ms,
+        "combine_ms": comb_ms,
+        "ms_per_step_with_events": ev_ms,
+        "split_alg_bytes": kv_bytes + q_bytes,
+        "split_gbs": (kv_bytes + q_bytes) / (split_ms * 1e-3) / 1e9,
+        "step_bytes": step_bytes,
+        "tensors": (q, K, V),
+    }
+
+
+def cpu_baseline_c2(q, K, V, batch, hkv, d, budget_s=12.0):
+    """Time the oracle's two-pass llama decode (fp32, model.py:1246-1252) on
+    the C2 workload; returns GB/s of algorithmic bytes and the sample."""
+    import numpy as np
+    from oracle import attention as A
+    try:
+        from threadpoolctl import threadpool_info
+        blas = [i for i in threadpool_info() if i.get("user_api") == "blas"]
+        cores = max(int(i.get("num_threads", 1)) for i in blas) if blas else 1
+    except Exception:  # pragma: no cover
+        cores = 1
+    qh = q.float().cpu().numpy()
+    # llama layout: one contiguous (t, n_kv, hd) fp32 cache per sequence
+    Kh = [np.ascontiguousarray(K[:, b].float().cpu().numpy()) for b in range(batch)]
+    Vh = [np.ascontiguousarray(V[:, b].float().cpu().numpy()) for b in range(batch)]
+    group = qh.shape[1] // hkv
+    scale = 1.0 / math.sqrt(d)
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < 3 or (time.perf_counter() - t_start < budget_s and len(times) < 50):
+        t0 = time.perf_counter()
+        for b in range(batch):
+            A.attention_decode_twopass(qh[b], Kh[b], Vh[b], group, scale, acc=np.float32)
+        times.append(time.perf_counter() - t0)
+    step_s = statistics.median(times)
+    es = 2  # algorithmic bytes are counted at the workload's fp16 storage size
+    ctx = Kh[0].shape[0]
+    step_bytes = 2 * ctx * batch * hkv * d * es + 2 * qh.size * es
+    return {
+        "value": step_bytes / step_s / 1e9,
+        "unit": "GB/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": (f"full C2 uniform-8192 step (16 sequences, NumPy two-pass fp32 "
+                   f"oracle), median of {len(times)} runs, {step_s * 1e3:.1f} ms/step"),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only-headline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
+              "(the path has no multi-GPU component in this build)", file=sys.stderr)
+        return 2
+
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    lib = _mod("_lib")
+    ops = _mod("qwen35_rocm_ops").Qwen35RocmOps()
+    steps, warmup = args.steps, args.warmup
+
+    # headline: C2 uniform-8192 fp16
+    c2 = bench_decode(torch, ops, lib, batch=16, ctx=8192, hq=32, hkv=8, d=128,
+                      dtype=torch.float16, gate=False, steps=steps, warmup=warmup, seed=2)
+    extra = {}
+    if not args.only_headline:
+        c4 = bench_decode(torch, ops, lib, batch=4, ctx=32768, hq=16, hkv=2, d=256,
+                          dtype=torch.bfloat16, gate=True, steps=steps, warmup=warmup, seed=4)
+        c4.pop("tensors")
+        extra["c4_gated_decode_bf16_32k"] = {
+            "gbs": round(c4["gbs"], 1), "frac_hbm": round(c4["gbs"] / HBM_PEAK_GBS, 4),
+            "ms_per_step": round(c4["ms_per_step"], 4),
+            "split_kernel_gbs": round(c4["split_gbs"], 1),
+            "split_ms": round(c4["split_ms"], 4), "combine_ms": round(c4["combine_ms"], 4)}
+        c1 = bench_decode(torch, ops, lib, batch=1, ctx=512, hq=32, hkv=8, d=64,
+                          dtype=torch.float32, gate=False, steps=steps, warmup=warmup, seed=1)
+        c1.pop("tensors")
+        extra["c1_decode_fp32_512"] = {
+            "us_per_step": round(c1["ms_per_step"] * 1e3, 2),
+            "split_us": round(c1["split_ms"] * 1e3, 2),
+            "combine_us": round(c1["combine_ms"] * 1e3, 2)}
+    extra["c2_combine_ms"] = round(c2["combine_ms"], 5)
+
+    cpu = None
+    if not args.no_cpu:
+        q, K, V = c2["tensors"]
+        cpu = cpu_baseline_c2(q, K, V, 16, 8, 128)
+    c2.pop("tensors")
+
+    line = {
+        "metric": METRIC,
+        "value": round(c2["gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(c2["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic N(0,1), seeded, generated on device",
+        "config": {
+            "workload": "C2 GQA decode, uniform 8192-row fp16 cache, 16 seqs, 32q/8kv heads, "
+                        "head_dim 128, ROCm layout [8192,16,8,128], split-K + combine",
+            "batch": 16, "ctx": 8192, "q_heads": 32, "kv_heads": 8, "head_dim": 128,
+            "frac_of_hbm_peak": round(c2["gbs"] / HBM_PEAK_GBS, 4),
+        },
+        "roofline": {
+            "kernel": "decode_split_mfma<f16,128>",
+            "bound": "hbm",
+            "achieved": round(c2["split_gbs"], 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(c2["split_gbs"] / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "avg_launch_ms": round(c2["split_ms"], 5),
+            "alg_bytes_per_launch": c2["split_alg_bytes"],
+        },
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -108,7 +108,9 @@ size_t alpx_decode_workspace_bytes(int batch, int q_heads, int kv_heads, int val
  * ROCm workspace layout, (t, kv_heads, D) with batch 1 the llama layout.
  * q, K, V and gate use `dtype`; out uses `out_dtype`; arithmetic is fp32.
  * workspace must hold alpx_decode_workspace_bytes(batch, q_heads,
- * kv_heads, value_dim, length) bytes and is scratch (no initial contents).
+ * kv_heads, value_dim, length) bytes; it is scratch (no initial contents
+ * needed).  Calls sharing a workspace must be ordered on one stream.  One
+ * call is two kernel launches: the split pass and the combine pass.
  */
 int alpx_decode_gqa(const void* q, const void* key_cache, const void* value_cache,
                     const int32_t* seq_lens, int length, const void* gate, void* out,
@@ -127,6 +129,27 @@ int alpx_decode_gqa(const void* q, const void* key_cache, const void* value_cach
  */
 int alpx_sigmoid_gate(const void* values, const void* gate, void* out, int64_t n, int dtype,
                       int out_dtype, void* stream);
+
+/*
+ * Kernel timing (measurement support, no reference counterpart: it serves
+ * the roofline measurement of bench.py).  While enabled, each entry point
+ * records a pair of HIP events on its launch stream around the kernel named
+ * by `kernel` below; alpx_timing_read synchronises the recorded events and
+ * returns the summed duration and launch count.  alpx_timing_enable clears
+ * the totals.  Timing adds two event records per launch.
+ */
+enum alpx_timed_kernel {
+  ALPX_T_KV_APPEND = 0,
+  ALPX_T_DECODE = 1,
+  ALPX_T_DECODE_COMBINE = 2,
+  ALPX_T_PREFILL = 3,
+  ALPX_T_GDN_CHUNK = 4,
+  ALPX_T_GDN_STEP = 5,
+  ALPX_T_AUX = 6
+};
+#define ALPX_TIMING_KERNELS 7
+int alpx_timing_enable(int enable);
+int alpx_timing_read(int kernel, double* total_ms, int64_t* launches);
 
 #ifdef __cplusplus
 }
