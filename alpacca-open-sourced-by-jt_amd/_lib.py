@@ -33,6 +33,10 @@ SIGNATURES = {
                                  _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_float,
                                  _c_int, _c_int, _c_ptr]),
     "alpx_sigmoid_gate": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_i64, _c_int, _c_int, _c_ptr]),
+    "alpx_prefill_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int]),
+    "alpx_prefill_causal": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_size, _c_int,
+                                     _c_int, _c_int, _c_int, _c_int, _c_int, _c_i64, _c_i64,
+                                     _c_i64, _c_int, _c_i64, _c_float, _c_int, _c_int, _c_ptr]),
     "alpx_timing_enable": (_c_int, [_c_int]),
     "alpx_timing_read": (_c_int, [_c_int, ctypes.POINTER(ctypes.c_double),
                                   ctypes.POINTER(ctypes.c_int64)]),

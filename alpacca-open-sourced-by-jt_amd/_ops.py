@@ -79,3 +79,50 @@ def sigmoid_gate(values, gate, out_dtype=None):
         _lib.stream_handle(torch, values.device))
     _lib.check(rc)
     return out
+
+
+def prefill(q, key, value, *, pos0, scale=None, window=0, kv_start=0, kv_tokens=None,
+            k_pos_stride=None, v_pos_stride=None, out_dtype=None, out=None):
+    """Causal GQA prefill.  ``q [T, Hq, D]`` contiguous; ``key``/``value``
+    cache rows ``j < kv_tokens`` of ``kv_heads`` heads, row stride given in
+    elements (default: contiguous ``[T_kv, Hkv, D]``).  Returns
+    ``[T, Hq, Dv]``."""
+    torch = _torch()
+    q_tokens, q_heads, key_dim = (int(x) for x in q.shape)
+    kv_heads = int(key.shape[-2])
+    value_dim = int(value.shape[-1])
+    if kv_tokens is None:
+        kv_tokens = int(key.shape[0])
+    if k_pos_stride is None:
+        k_pos_stride = kv_heads * key_dim
+    if v_pos_stride is None:
+        v_pos_stride = kv_heads * value_dim
+    if scale is None:
+        scale = 1.0 / math.sqrt(key_dim)
+    out_dtype = q.dtype if out_dtype is None else out_dtype
+    if out is None:
+        out = torch.empty((q_tokens, q_heads, value_dim), dtype=out_dtype, device=q.device)
+    L = _lib.lib()
+    nbytes = L.alpx_prefill_workspace_bytes(q_tokens, q_heads, kv_heads, value_dim, kv_tokens)
+    if nbytes == 0:
+        raise ValueError("invalid prefill sizes")
+    # only the split-K fallback (fp32, odd shapes) touches the workspace
+    fast = (q.dtype != torch.float32 and key_dim == value_dim and key_dim in (64, 128, 256))
+    ws = None if fast else _lib.workspace(torch, q.device, nbytes)
+    rc = L.alpx_prefill_causal(
+        q.data_ptr(), key.data_ptr(), value.data_ptr(), out.data_ptr(),
+        None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(),
+        q_tokens, int(kv_tokens), q_heads, kv_heads, key_dim, value_dim, int(k_pos_stride),
+        int(v_pos_stride), int(pos0), int(window), int(kv_start), float(scale),
+        _lib.dtype_code(torch, q.dtype), _lib.dtype_code(torch, out.dtype),
+        _lib.stream_handle(torch, q.device))
+    if rc == _lib.EINVAL and ws is None:  # unaligned rows fell back: retry with workspace
+        ws = _lib.workspace(torch, q.device, nbytes)
+        rc = L.alpx_prefill_causal(
+            q.data_ptr(), key.data_ptr(), value.data_ptr(), out.data_ptr(), ws.data_ptr(),
+            ws.numel(), q_tokens, int(kv_tokens), q_heads, kv_heads, key_dim, value_dim,
+            int(k_pos_stride), int(v_pos_stride), int(pos0), int(window), int(kv_start),
+            float(scale), _lib.dtype_code(torch, q.dtype), _lib.dtype_code(torch, out.dtype),
+            _lib.stream_handle(torch, q.device))
+    _lib.check(rc)
+    return out

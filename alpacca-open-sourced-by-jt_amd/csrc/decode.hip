@@ -29,6 +29,7 @@
 #include <math.h>
 
 #include "alpx_common.h"
+#include "decode_internal.h"
 #include "timing.h"
 
 namespace alpx {
@@ -38,31 +39,28 @@ constexpr int kTile = 32;   // rows per wavefront step (MFMA path)
 constexpr int kWaves = 4;   // wavefronts (= slots) per block (MFMA path)
 constexpr int kGenericTile = 64;
 constexpr int kMaxSlots = 2048;
+constexpr int kMaxResident = 8192;  // upper bound on resident blocks any plan assumes
 
-struct DecodeArgs {
-  const void* q;
-  const void* k;
-  const void* v;
-  const int32_t* seq_lens;
-  const void* gate;
-  void* out;
-  float* part_m;    // [B][Hq][nsplit]
-  float* part_l;    // [B][Hq][nsplit]
-  float* part_acc;  // [B][Hq][nsplit][Dv]
-  int64_t ks_pos, ks_b, ks_h, vs_pos, vs_b, vs_h;
-  int length;
-  int batch, q_heads, kv_heads, group, key_dim, value_dim;
-  int head_chunks;  // ceil(group / 16): 16 query heads per MFMA column block
-  int nsplit;       // partial slots per (b, h)
-  int chunk;        // rows per slot
-  float scale_log2; // softmax scale * log2(e)
-};
 
+// Rows [seq_lo, seq_len) of sequence b are attended.  Decode: [0, len_b).
+// Causal mode (prefill through this path): "sequence" b is query token b at
+// absolute position causal_pos0 + b; cache row j sits at kv_start + j and is
+// visible iff kv_start + j <= pos and, with a window, > pos - window.
 __device__ __forceinline__ int seq_len(const DecodeArgs& a, int b) {
-  if (a.seq_lens == nullptr) return a.length;
-  int n = a.seq_lens[b];
+  int64_t n;
+  if (a.causal_pos0 >= 0)
+    n = a.causal_pos0 + b + 1 - a.kv_start;
+  else
+    n = a.seq_lens == nullptr ? a.length : a.seq_lens[b];
   n = n < 0 ? 0 : n;
-  return n > a.length ? a.length : n;
+  return (int)(n > a.length ? a.length : n);
+}
+
+__device__ __forceinline__ int seq_lo(const DecodeArgs& a, int b, int hi) {
+  if (a.causal_pos0 < 0 || a.window <= 0) return 0;
+  int64_t n = a.causal_pos0 + b - a.window + 1 - a.kv_start;
+  n = n < 0 ? 0 : n;
+  return (int)(n > hi ? hi : n);
 }
 
 __device__ __forceinline__ void wave_sync_lds() {
@@ -74,10 +72,6 @@ __device__ __forceinline__ void wave_sync_lds() {
 }
 
 // ------------------------------------------------------------ MFMA split
-
-template <typename T> struct Vec4;
-template <> struct Vec4<f16_t> { typedef f16x4 type; };
-template <> struct Vec4<bf16_t> { typedef bf16x4 type; };
 
 // One block = 4 wavefronts sharing one chunk of rows of one (sequence, kv
 // head, 16-head column block).  Wave w takes the 32-row tiles w, w+4, ...;
@@ -105,8 +99,8 @@ decode_split_mfma(DecodeArgs a) {
   const int hc = blockIdx.y % a.head_chunks;
   const int kvh = blockIdx.y / a.head_chunks;
   const int len = seq_len(a, b);
-  const int start = blockIdx.x * a.chunk;
-  const int end = min(start + a.chunk, len);
+  const int start = max(blockIdx.x * a.chunk, seq_lo(a, b, len));
+  const int end = min(blockIdx.x * a.chunk + a.chunk, len);
   const int last = end - 1;
   const int hl = lane & 15;  // query-head column (N index) of this lane
   const int quad = lane >> 4;
@@ -278,8 +272,8 @@ decode_split_generic(DecodeArgs a) {
   const int kvh = blockIdx.y / a.head_chunks;
   const int slot = blockIdx.x;
   const int len = seq_len(a, b);
-  const int start = slot * a.chunk;
-  const int end = min(start + a.chunk, len);
+  const int start = max(slot * a.chunk, seq_lo(a, b, len));
+  const int end = min(slot * a.chunk + a.chunk, len);
   const int D = a.key_dim, DV = a.value_dim;
   int gcount = a.group - hc * 16;
   gcount = gcount > 16 ? 16 : gcount;
@@ -432,6 +426,7 @@ int max_slots(int length) {
 // Size the split so the whole grid is resident at once (one round of blocks
 // over the device), with each block's chunk a whole number of wave tiles.
 Plan plan_split(int pairs, int length, int resident, int unit) {
+  if (resident > kMaxResident) resident = kMaxResident;
   int want = (resident + pairs - 1) / pairs;
   const int most = (length + unit - 1) / unit;
   if (want > most) want = most;
@@ -450,6 +445,12 @@ Plan plan_split(int pairs, int length, int resident, int unit) {
 }
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+int slot_bound(int pairs, int length) {
+  const int by_device = (kMaxResident + pairs - 1) / pairs;
+  const int by_len = max_slots(length);
+  return by_device < by_len ? by_device : by_len;
+}
 
 size_t workspace_for(int batch, int q_heads, int value_dim, int nsplit) {
   const size_t n = (size_t)batch * q_heads * nsplit;
@@ -506,8 +507,65 @@ extern "C" size_t alpx_decode_workspace_bytes(int batch, int q_heads, int kv_hea
   if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || value_dim <= 0 || max_len <= 0 ||
       q_heads % kv_heads != 0)
     return 0;
-  return workspace_for(batch, q_heads, value_dim, max_slots(max_len));
+  const int hc = (q_heads / kv_heads + 15) / 16;
+  return workspace_for(batch, q_heads, value_dim, slot_bound(batch * kv_heads * hc, max_len));
 }
+
+namespace alpx {
+
+size_t decode_workspace(int batch, int q_heads, int kv_heads, int value_dim, int length) {
+  const int hc = (q_heads / kv_heads + 15) / 16;
+  return workspace_for(batch, q_heads, value_dim, slot_bound(batch * kv_heads * hc, length));
+}
+
+int run_decode(DecodeArgs a, int dtype, int out_dtype, void* workspace, size_t workspace_bytes,
+               hipStream_t s, int split_timer, int combine_timer) {
+  const size_t es = dtype_size(dtype);
+  const uintptr_t align = (uintptr_t)a.q | (uintptr_t)a.k | (uintptr_t)a.v |
+                          (uintptr_t)(a.ks_pos * es) | (uintptr_t)(a.ks_b * es) |
+                          (uintptr_t)(a.ks_h * es) | (uintptr_t)(a.vs_pos * es) |
+                          (uintptr_t)(a.vs_b * es) | (uintptr_t)(a.vs_h * es);
+  const int D = a.key_dim;
+  const bool mfma = dtype != ALPX_F32 && D == a.value_dim && (D == 64 || D == 128 || D == 256) &&
+                    (align & 15) == 0 && getenv("ALPX_DECODE_GENERIC") == nullptr;
+  const size_t need = decode_workspace(a.batch, a.q_heads, a.kv_heads, a.value_dim, a.length);
+  if (workspace_bytes < need)
+    return fail(ALPX_EINVAL, "decode workspace holds %zu bytes, needs %zu", workspace_bytes,
+                need);
+  const void* kernel = nullptr;
+  switch (dtype) {
+    case ALPX_F32: kernel = split_kernel<float>(false, D); break;
+    case ALPX_F16: kernel = split_kernel<f16_t>(mfma, D); break;
+    default: kernel = split_kernel<bf16_t>(mfma, D); break;
+  }
+  if (kernel == nullptr) return fail(ALPX_EUNSUPPORTED, "decode: no kernel for this shape");
+  const int unit = mfma ? kTile * kWaves : kGenericTile;
+  a.head_chunks = (a.group + 15) / 16;
+  const Plan p = plan_split(a.batch * a.kv_heads * a.head_chunks, a.length,
+                            resident_blocks(kernel, mfma ? 256 : 64, 0), unit);
+  const size_t n = (size_t)a.batch * a.q_heads * p.nsplit;
+  char* ws = (char*)workspace;
+  a.part_m = (float*)ws;
+  a.part_l = (float*)(ws + align256(n * sizeof(float)));
+  a.part_acc = (float*)(ws + 2 * align256(n * sizeof(float)));
+  a.nsplit = p.nsplit;
+  a.chunk = p.chunk;
+  dim3 grid(p.nsplit, a.kv_heads * a.head_chunks, a.batch);
+  int rc;
+  {
+    TimedRegion timed(split_timer, s);
+    rc = launch_split<float>(kernel, mfma, a, grid, s);
+  }
+  if (rc != ALPX_OK) return rc;
+  TimedRegion timed(combine_timer, s);
+  switch (dtype) {
+    case ALPX_F32: return launch_combine<float>(out_dtype, a, s);
+    case ALPX_F16: return launch_combine<f16_t>(out_dtype, a, s);
+    default: return launch_combine<bf16_t>(out_dtype, a, s);
+  }
+}
+
+}  // namespace alpx
 
 extern "C" int alpx_decode_gqa(const void* q, const void* key_cache, const void* value_cache,
                                const int32_t* seq_lens, int length, const void* gate, void* out,
@@ -531,75 +589,30 @@ extern "C" int alpx_decode_gqa(const void* q, const void* key_cache, const void*
     return fail(ALPX_EINVAL, "attention scale must be positive and finite");
   if (key_dim > 256 || value_dim > 256)
     return fail(ALPX_EUNSUPPORTED, "alpx_decode_gqa: head dims above 256 are not supported");
-
-  const int group = q_heads / kv_heads;
-  const int hc = (group + 15) / 16;
-  const size_t es = dtype_size(dtype);
-  const uintptr_t align = (uintptr_t)q | (uintptr_t)key_cache | (uintptr_t)value_cache |
-                          (uintptr_t)(k_pos_stride * es) | (uintptr_t)(k_batch_stride * es) |
-                          (uintptr_t)(k_head_stride * es) | (uintptr_t)(v_pos_stride * es) |
-                          (uintptr_t)(v_batch_stride * es) | (uintptr_t)(v_head_stride * es);
-  const bool mfma = dtype != ALPX_F32 && key_dim == value_dim &&
-                    (key_dim == 64 || key_dim == 128 || key_dim == 256) && (align & 15) == 0 &&
-                    getenv("ALPX_DECODE_GENERIC") == nullptr;
-  const size_t need = workspace_for(batch, q_heads, value_dim, max_slots(length));
-  if (workspace_bytes < need)
-    return fail(ALPX_EINVAL, "alpx_decode_gqa: workspace holds %zu bytes, needs %zu",
-                workspace_bytes, need);
-
-  const void* kernel = nullptr;
-  switch (dtype) {
-    case ALPX_F32: kernel = split_kernel<float>(false, key_dim); break;
-    case ALPX_F16: kernel = split_kernel<f16_t>(mfma, key_dim); break;
-    default: kernel = split_kernel<bf16_t>(mfma, key_dim); break;
-  }
-  if (kernel == nullptr) return fail(ALPX_EUNSUPPORTED, "decode: no kernel for this shape");
-  const int unit = mfma ? kTile * kWaves : kGenericTile;
-  const Plan p = plan_split(batch * kv_heads * hc, length,
-                            resident_blocks(kernel, mfma ? 256 : 64, 0), unit);
-
-  DecodeArgs a;
+  DecodeArgs a = {};
   a.q = q;
   a.k = key_cache;
   a.v = value_cache;
   a.seq_lens = seq_lens;
   a.gate = gate;
   a.out = out;
-  const size_t n = (size_t)batch * q_heads * p.nsplit;
-  char* ws = (char*)workspace;
-  a.part_m = (float*)ws;
-  a.part_l = (float*)(ws + align256(n * sizeof(float)));
-  a.part_acc = (float*)(ws + 2 * align256(n * sizeof(float)));
   a.ks_pos = k_pos_stride;
   a.ks_b = k_batch_stride;
   a.ks_h = k_head_stride;
   a.vs_pos = v_pos_stride;
   a.vs_b = v_batch_stride;
   a.vs_h = v_head_stride;
+  a.causal_pos0 = -1;
+  a.kv_start = 0;
+  a.window = 0;
   a.length = length;
   a.batch = batch;
   a.q_heads = q_heads;
   a.kv_heads = kv_heads;
-  a.group = group;
+  a.group = q_heads / kv_heads;
   a.key_dim = key_dim;
   a.value_dim = value_dim;
-  a.head_chunks = hc;
-  a.nsplit = p.nsplit;
-  a.chunk = p.chunk;
   a.scale_log2 = scale * kLog2e;
-
-  hipStream_t s = (hipStream_t)stream;
-  dim3 grid(p.nsplit, kv_heads * hc, batch);
-  int rc;
-  {
-    TimedRegion timed(ALPX_T_DECODE, s);
-    rc = launch_split<float>(kernel, mfma, a, grid, s);
-  }
-  if (rc != ALPX_OK) return rc;
-  TimedRegion timed(ALPX_T_DECODE_COMBINE, s);
-  switch (dtype) {
-    case ALPX_F32: return launch_combine<float>(out_dtype, a, s);
-    case ALPX_F16: return launch_combine<f16_t>(out_dtype, a, s);
-    default: return launch_combine<bf16_t>(out_dtype, a, s);
-  }
+  return run_decode(a, dtype, out_dtype, workspace, workspace_bytes, (hipStream_t)stream,
+                    ALPX_T_DECODE, ALPX_T_DECODE_COMBINE);
 }

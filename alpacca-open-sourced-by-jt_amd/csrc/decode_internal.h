@@ -1,0 +1,41 @@
+// Split-K decode machinery shared by the decode and prefill entry points.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace alpx {
+
+struct DecodeArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const int32_t* seq_lens;
+  const void* gate;
+  void* out;
+  float* part_m;    // [B][Hq][nsplit]
+  float* part_l;    // [B][Hq][nsplit]
+  float* part_acc;  // [B][Hq][nsplit][Dv]
+  int64_t ks_pos, ks_b, ks_h, vs_pos, vs_b, vs_h;
+  int64_t causal_pos0;  // < 0: decode; >= 0: row b is query token b at this + b
+  int64_t kv_start;     // absolute position of cache row 0 (causal mode)
+  int window;           // > 0: sliding window (causal mode)
+  int length;
+  int batch, q_heads, kv_heads, group, key_dim, value_dim;
+  int head_chunks;  // ceil(group / 16): 16 query heads per MFMA column block
+  int nsplit;       // partial slots per (b, h)
+  int chunk;        // rows per slot
+  float scale_log2; // softmax scale * log2(e)
+};
+
+// Bytes of split partials for `batch` rows of `q_heads` heads over `length`
+// cache rows.
+size_t decode_workspace(int batch, int q_heads, int kv_heads, int value_dim, int length);
+
+// Plans and launches split + combine for fully described args (pointers,
+// strides, sizes, causal fields, scale_log2); fills the partial pointers,
+// nsplit and chunk.  Validation is the caller's job.
+int run_decode(DecodeArgs a, int dtype, int out_dtype, void* workspace, size_t workspace_bytes,
+               hipStream_t stream, int split_timer, int combine_timer);
+
+}  // namespace alpx

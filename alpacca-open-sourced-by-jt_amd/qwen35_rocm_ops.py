@@ -366,6 +366,61 @@ class Qwen35RocmOps:
         return (self.online_attention(query, key_cache, value_cache, length=length,
                                       scale=scale), length)
 
+    def attention_prefill(self, query: Any, key_cache: Any, value_cache: Any, *,
+                          position: int, batch_index: int = 0, scale: float | None = None,
+                          window: int = 0, out_dtype: Any = None) -> Any:
+        """Causal prefill over the ROCm cache layout (extension): query
+        ``[T, Hq, D]`` of sequence ``batch_index`` at positions
+        ``position .. position + T - 1`` attends to its cache rows
+        ``0 .. position + t`` (``qwen35_full_attention_prefill`` semantics,
+        qwen35_kernels.py:395-411, with prefix_length = position)."""
+        query = self._tensor(query, "prefill query", dimensions=3)
+        key_cache = self._tensor(key_cache, "attention key cache", dimensions=4)
+        value_cache = self._tensor(value_cache, "attention value cache", dimensions=4)
+        position = _nonnegative_integer("attention cache position", position)
+        batch_index = _nonnegative_integer("batch_index", batch_index)
+        window = _nonnegative_integer("window", window)
+        capacity, batch, kv_heads, key_width = _shape(key_cache)
+        value_shape = _shape(value_cache)
+        tokens, query_heads, query_width = _shape(query)
+        if value_shape[:3] != (capacity, batch, kv_heads):
+            raise ValueError("attention K/V cache capacity, batch, or heads differ")
+        if batch_index >= batch:
+            raise ValueError("batch_index exceeds the cache batch")
+        if position + tokens > capacity:
+            raise ValueError("attention cache position exceeds capacity")
+        if query_width != key_width:
+            raise ValueError("prefill query does not match K cache head width")
+        if query_heads % kv_heads:
+            raise ValueError("attention query heads must be a multiple of KV heads")
+        self._same_dtype("prefill", query, key_cache, value_cache)
+        scale_value = (1.0 / math.sqrt(key_width) if scale is None
+                       else _positive_finite("attention scale", scale))
+        return _ops.prefill(query, key_cache[0, batch_index], value_cache[0, batch_index],
+                            pos0=position, scale=scale_value, window=window,
+                            kv_tokens=position + tokens,
+                            k_pos_stride=batch * kv_heads * key_width,
+                            v_pos_stride=batch * kv_heads * value_shape[3],
+                            out_dtype=out_dtype)
+
+    def append_prefill_attention_(self, query: Any, key: Any, value: Any, key_cache: Any,
+                                  value_cache: Any, *, position: int,
+                                  scale: float | None = None) -> tuple[Any, int]:
+        """Prefill-chunk form of ``append_online_attention_`` for a batch-1
+        cache (extension): append ``key/value [T, Hkv, D]`` at ``position``
+        (bit-exact), then causal prefill attention of ``query [T, Hq, D]``.
+        Returns ``(output [T, Hq, Dv], position + T)``."""
+        key_cache = self._tensor(key_cache, "attention key cache", dimensions=4)
+        if int(key_cache.shape[1]) != 1:
+            raise ValueError("append_prefill_attention_ needs a batch-1 cache")
+        key = self._tensor(key, "attention key rows", dimensions=3)
+        value = self._tensor(value, "attention value rows", dimensions=3)
+        self.attention_append_rows_(key_cache, value_cache, key.unsqueeze(1),
+                                    value.unsqueeze(1), position=position)
+        out = self.attention_prefill(query, key_cache, value_cache, position=position,
+                                     scale=scale)
+        return out, position + int(key.shape[0])
+
     def sigmoid_gate(self, values: Any, gate: Any) -> Any:
         values = self._tensor(values, "sigmoid-gate values")
         gate = self._tensor(gate, "sigmoid-gate logits")

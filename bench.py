@@ -97,6 +97,30 @@ def bench_decode(torch, ops, lib, *, batch, ctx, hq, hkv, d, dtype, gate, steps,
     }
 
 
+def bench_prefill(torch, ops, lib, *, steps, warmup, seed=3):
+    """C3: causal prefill of a 2048-token bf16 chunk whose K/V were appended
+    at rows 2048..4095 of a [4096, 1, 8, 128] cache; 32 query heads.  The
+    step is the prefill attention call; FLOPs count causal-valid pairs only."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    dev = torch.device("cuda")
+    tq, prefix, hq, hkv, d = 2048, 2048, 32, 8, 128
+    K = torch.randn((prefix + tq, 1, hkv, d), generator=g, device=dev).to(torch.bfloat16)
+    V = torch.randn((prefix + tq, 1, hkv, d), generator=g, device=dev).to(torch.bfloat16)
+    q = torch.randn((tq, hq, d), generator=g, device=dev).to(torch.bfloat16)
+    fn = lambda: ops.attention_prefill(q, K, V, position=prefix)  # noqa: E731
+    ms = _timed_steps(torch, fn, steps, warmup)
+    lib.timing_enable(True)
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    k_ms = _kernel_avg_ms(lib, lib.T_PREFILL)
+    lib.timing_enable(False)
+    pairs = sum(prefix + i + 1 for i in range(tq))  # 6,292,480
+    flops = 4 * d * hq * pairs                      # QK^T and PV, 2 FLOP per MAC
+    return {"ms_per_step": ms, "kernel_ms": k_ms, "flops": flops,
+            "tflops": flops / (ms * 1e-3) / 1e12, "kernel_tflops": flops / (k_ms * 1e-3) / 1e12}
+
+
 def cpu_baseline_c2(q, K, V, batch, hkv, d, budget_s=12.0):
     """Time the oracle's two-pass llama decode (fp32, model.py:1246-1252) on
     the C2 workload; returns GB/s of algorithmic bytes and the sample."""
@@ -169,6 +193,14 @@ def main() -> int:
             "ms_per_step": round(c4["ms_per_step"], 4),
             "split_kernel_gbs": round(c4["split_gbs"], 1),
             "split_ms": round(c4["split_ms"], 4), "combine_ms": round(c4["combine_ms"], 4)}
+        c3 = bench_prefill(torch, ops, lib, steps=steps, warmup=warmup)
+        extra["c3_prefill_bf16_2k_on_2k"] = {
+            "tflops": round(c3["tflops"], 1),
+            "frac_mfma_bf16": round(c3["tflops"] / BF16_PEAK_TFLOPS, 4),
+            "ms_per_step": round(c3["ms_per_step"], 4),
+            "kernel_ms": round(c3["kernel_ms"], 4),
+            "kernel_tflops": round(c3["kernel_tflops"], 1),
+            "flops_per_step": c3["flops"]}
         c1 = bench_decode(torch, ops, lib, batch=1, ctx=512, hq=32, hkv=8, d=64,
                           dtype=torch.float32, gate=False, steps=steps, warmup=warmup, seed=1)
         c1.pop("tensors")

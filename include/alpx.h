@@ -121,6 +121,39 @@ int alpx_decode_gqa(const void* q, const void* key_cache, const void* value_cach
                     int out_dtype, void* stream);
 
 /*
+ * Workspace bytes alpx_prefill_causal may need (only its fallback path, for
+ * fp32 or unsupported shapes, uses it).
+ */
+size_t alpx_prefill_workspace_bytes(int q_tokens, int q_heads, int kv_heads, int value_dim,
+                                    int kv_tokens);
+
+/*
+ * Causal (optionally sliding-window) GQA prefill attention.
+ * Replaces Model._attention_batch_np (model.py:1254-1272), its windowed form
+ * _attention_batch_window_np (model.py:1567-1592), the device seam
+ * cuda.attention_batch (cuda.py:1186-1244) and
+ * qwen35_kernels.qwen35_full_attention_prefill (qwen35_kernels.py:395-411).
+ *
+ * q [q_tokens, q_heads, key_dim] and out [q_tokens, q_heads, value_dim] are
+ * contiguous; cache row j of head h is key[j*k_pos_stride + h*key_dim + d]
+ * (value likewise), so a (t, kv_heads, D) cache has k_pos_stride =
+ * kv_heads*key_dim and one sequence of a [C, B, Hkv, D] cache is the base
+ * pointer b*Hkv*D with k_pos_stride = B*Hkv*D.  Query token t sits at
+ * absolute position q_pos0 + t, cache row j at kv_start + j; t sees row j
+ * iff kv_start + j <= q_pos0 + t and (window == 0 or kv_start + j >
+ * q_pos0 + t - window).  A row that sees no key yields zeros (the device
+ * seam's convention, cuda.py:572-577).  Scale is usually 1/sqrt(key_dim).
+ * fp16/bf16 with key_dim == value_dim in {64, 128, 256} and 16-byte aligned
+ * rows run the MFMA flash kernel (no workspace); anything else runs the
+ * split-K machinery and needs alpx_prefill_workspace_bytes of workspace.
+ */
+int alpx_prefill_causal(const void* q, const void* key, const void* value, void* out,
+                        void* workspace, size_t workspace_bytes, int q_tokens, int kv_tokens,
+                        int q_heads, int kv_heads, int key_dim, int value_dim,
+                        int64_t k_pos_stride, int64_t v_pos_stride, int64_t q_pos0, int window,
+                        int64_t kv_start, float scale, int dtype, int out_dtype, void* stream);
+
+/*
  * Sigmoid output gate: out[i] = values[i] * sigmoid(gate[i]) for i < n, with
  * the stable two-branch sigmoid of tensor.stable_sigmoid (tensor.py:123-129).
  * Replaces Qwen35RocmOps.sigmoid_gate (qwen35_rocm_ops.py:286-290) and
