@@ -37,6 +37,12 @@ SIGNATURES = {
     "alpx_prefill_causal": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_size, _c_int,
                                      _c_int, _c_int, _c_int, _c_int, _c_int, _c_i64, _c_i64,
                                      _c_i64, _c_int, _c_i64, _c_float, _c_int, _c_int, _c_ptr]),
+    "alpx_gdn_step": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int,
+                               _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_ptr]),
+    "alpx_gdn_chunk_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int]),
+    "alpx_gdn_chunk_prefill": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
+                                        _c_ptr, _c_size, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                        _c_int, _c_int, _c_int, _c_ptr]),
     "alpx_timing_enable": (_c_int, [_c_int]),
     "alpx_timing_read": (_c_int, [_c_int, ctypes.POINTER(ctypes.c_double),
                                   ctypes.POINTER(ctypes.c_int64)]),

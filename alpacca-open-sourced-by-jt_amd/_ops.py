@@ -126,3 +126,42 @@ def prefill(q, key, value, *, pos0, scale=None, window=0, kv_start=0, kv_tokens=
             _lib.stream_handle(torch, q.device))
     _lib.check(rc)
     return out
+
+
+def gdn_step(state, q, k, v, beta, log_decay, out_dtype=None):
+    """One GDN decode step in place on ``state [B, Hv, Dv, Dk]`` (fp32);
+    q/k ``[B, Hk, Dk]``, v ``[B, Hv, Dv]``, beta/log_decay ``[B, Hv]`` fp32.
+    Returns ``[B, Hv, Dv]``."""
+    torch = _torch()
+    bsz, hv, dv, dk = (int(x) for x in state.shape)
+    hk = int(q.shape[1])
+    out = torch.empty((bsz, hv, dv), dtype=q.dtype if out_dtype is None else out_dtype,
+                      device=state.device)
+    rc = _lib.lib().alpx_gdn_step(
+        state.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(),
+        log_decay.data_ptr(), out.data_ptr(), bsz, hk, hv, dk, dv,
+        _lib.dtype_code(torch, q.dtype), _lib.dtype_code(torch, out.dtype),
+        _lib.stream_handle(torch, state.device))
+    _lib.check(rc)
+    return out
+
+
+def gdn_chunk(state, q, k, v, beta, log_decay, out_dtype=None):
+    """GDN over ``T`` tokens in place on ``state``; q/k ``[B, T, Hk, Dk]``,
+    v ``[B, T, Hv, Dv]``, beta/log_decay ``[B, T, Hv]`` fp32.  Returns
+    ``[B, T, Hv, Dv]``."""
+    torch = _torch()
+    bsz, hv, dv, dk = (int(x) for x in state.shape)
+    tokens, hk = int(q.shape[1]), int(q.shape[2])
+    out = torch.empty((bsz, tokens, hv, dv), dtype=q.dtype if out_dtype is None else out_dtype,
+                      device=state.device)
+    L = _lib.lib()
+    nbytes = L.alpx_gdn_chunk_workspace_bytes(bsz, tokens, hv, dk)
+    ws = _lib.workspace(torch, state.device, nbytes)
+    rc = L.alpx_gdn_chunk_prefill(
+        state.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(),
+        log_decay.data_ptr(), out.data_ptr(), ws.data_ptr(), ws.numel(), bsz, tokens, hk, hv,
+        dk, dv, _lib.dtype_code(torch, q.dtype), _lib.dtype_code(torch, out.dtype),
+        _lib.stream_handle(torch, state.device))
+    _lib.check(rc)
+    return out

@@ -4,6 +4,9 @@ Same names, argument order and layouts as the reference (qwen35_kernels.py):
 
 * ``qwen35_full_attention_decode(queries [Hq, D], keys [T, Hkv, D],
   values [T, Hkv, Dv]) -> [Hq, Dv]`` (qwen35_kernels.py:363-392)
+* ``qwen35_gdn_step(state [Hv, Dv, Dk], queries [Hk, Dk], keys [Hk, Dk],
+  values [Hv, Dv], beta [Hv], log_decay [Hv]) -> [Hv, Dv]``, updating the
+  state in place (qwen35_kernels.py:310-332)
 * ``qwen35_full_attention_prefill(queries [Tq, Hq, D], keys, values,
   prefix_length=0) -> [Tq, Hq, Dv]``: token t attends to cache rows
   ``0 .. prefix_length + t`` (qwen35_kernels.py:395-411)
@@ -61,5 +64,29 @@ def qwen35_full_attention_prefill(queries, keys, values, prefix_length: int = 0)
     return _host.to_host(out) if host else out
 
 
+def qwen35_gdn_step(state_matrix, queries, keys, values, beta, log_decay):
+    torch = _host.torch_mod()
+    host = _host.is_host(state_matrix)
+    if host:
+        import numpy as np
+        if not (isinstance(state_matrix, np.ndarray) and state_matrix.dtype == np.float32
+                and state_matrix.flags.c_contiguous):
+            raise ValueError("state must be a contiguous float32 NumPy array (updated in place)")
+    S = _host.to_device(state_matrix, torch.float32)
+    q = _host.to_device(queries, torch.float32)
+    k = _host.to_device(keys, torch.float32)
+    v = _host.to_device(values, torch.float32)
+    b = _host.to_device(beta, torch.float32)
+    g = _host.to_device(log_decay, torch.float32)
+    out = _ops.gdn_step(S.unsqueeze(0), q.unsqueeze(0), k.unsqueeze(0), v.unsqueeze(0),
+                        b.unsqueeze(0), g.unsqueeze(0))[0]
+    if host:
+        state_matrix[...] = S.cpu().numpy()
+        return _host.to_host(out)
+    if S.data_ptr() != state_matrix.data_ptr():
+        state_matrix.copy_(S)
+    return out
+
+
 __all__ = ["available", "backend_name", "qwen35_full_attention_decode",
-           "qwen35_full_attention_prefill"]
+           "qwen35_full_attention_prefill", "qwen35_gdn_step"]

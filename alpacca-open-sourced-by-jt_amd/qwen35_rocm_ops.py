@@ -421,6 +421,55 @@ class Qwen35RocmOps:
                                      scale=scale)
         return out, position + int(key.shape[0])
 
+    # ------------------------------------------------------------ recurrence
+
+    def _gdn_checks(self, state, query, key, value, beta, log_decay, *, chunk):
+        dims = 4 if chunk else 3
+        state = self._tensor(state, "GDN state", dimensions=4)
+        query = self._tensor(query, "GDN query", dimensions=dims)
+        key = self._tensor(key, "GDN key", dimensions=dims)
+        value = self._tensor(value, "GDN value", dimensions=dims)
+        beta = self._tensor(beta, "GDN beta", dimensions=dims - 1)
+        log_decay = self._tensor(log_decay, "GDN log decay", dimensions=dims - 1)
+        torch = self.torch
+        if state.dtype != torch.float32:
+            raise TypeError("GDN state must use float32")
+        if beta.dtype != torch.float32 or log_decay.dtype != torch.float32:
+            raise TypeError("GDN beta and log decay must use float32")
+        self._same_dtype("GDN", query, key, value)
+        batch, value_heads, value_width, key_width = _shape(state)
+        lead = _shape(query)[:-2]
+        if _shape(query) != _shape(key):
+            raise ValueError("GDN query and key shapes must agree")
+        if lead[0] != batch or _shape(query)[-1] != key_width:
+            raise ValueError("GDN query/key must match state batch and key dimension")
+        key_heads = int(query.shape[-2])
+        if key_heads <= 0 or value_heads % key_heads:
+            raise ValueError("GDN value heads must be a multiple of key heads")
+        if _shape(value) != lead + (value_heads, value_width):
+            raise ValueError("GDN value must match state batch/value-head/value axes")
+        if _shape(beta) != lead + (value_heads,):
+            raise ValueError("GDN beta must match batch and value heads")
+        if _shape(log_decay) != lead + (value_heads,):
+            raise ValueError("GDN log decay must match batch and value heads")
+        return state, query, key, value, beta, log_decay
+
+    def gated_delta_net_step_(self, state: Any, query: Any, key: Any, value: Any, beta: Any,
+                              log_decay: Any) -> Any:
+        """One GDN step in place on ``state [B, Hv, Dv, Dk]``
+        (qwen35_rocm_ops.py:362-407); value head h reads key head h % Hk."""
+        args = self._gdn_checks(state, query, key, value, beta, log_decay, chunk=False)
+        return _ops.gdn_step(*args)
+
+    def gated_delta_net_chunk_(self, state: Any, query: Any, key: Any, value: Any, beta: Any,
+                               log_decay: Any, *, out_dtype: Any = None) -> Any:
+        """GDN over a prefill chunk (extension): query/key ``[B, T, Hk, Dk]``,
+        value ``[B, T, Hv, Dv]``, beta/log_decay ``[B, T, Hv]``; the state is
+        advanced in place exactly as T calls of ``gated_delta_net_step_``
+        would, computed in 64-token chunks.  Returns ``[B, T, Hv, Dv]``."""
+        args = self._gdn_checks(state, query, key, value, beta, log_decay, chunk=True)
+        return _ops.gdn_chunk(*args, out_dtype=out_dtype)
+
     def sigmoid_gate(self, values: Any, gate: Any) -> Any:
         values = self._tensor(values, "sigmoid-gate values")
         gate = self._tensor(gate, "sigmoid-gate logits")

@@ -121,6 +121,53 @@ def bench_prefill(torch, ops, lib, *, steps, warmup, seed=3):
             "tflops": flops / (ms * 1e-3) / 1e12, "kernel_tflops": flops / (k_ms * 1e-3) / 1e12}
 
 
+def bench_gdn(torch, ops, lib, *, steps, warmup, seed=5):
+    """C5: gated delta rule, 16 q/k heads, 32 v heads, Dk = Dv = 128, fp32
+    state; a 1024-token chunked prefill, then 256 single-token decode steps.
+    Prefill FLOPs follow the chunked form (2 C^2 (3 Dk + 2 Dv) + 6 C Dk Dv per
+    head-chunk); decode bytes are the state read + write plus q/k/v/o."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    dev = torch.device("cuda")
+    T, hk, hv, dk, dv, C = 1024, 16, 32, 128, 128, 64
+    q = torch.nn.functional.normalize(torch.randn((1, T, hk, dk), generator=g, device=dev), dim=-1)
+    k = torch.nn.functional.normalize(torch.randn((1, T, hk, dk), generator=g, device=dev), dim=-1)
+    q, k = q.to(torch.bfloat16), k.to(torch.bfloat16)
+    v = torch.randn((1, T, hv, dv), generator=g, device=dev).to(torch.bfloat16)
+    beta = torch.sigmoid(torch.randn((1, T, hv), generator=g, device=dev))
+    a = torch.rand((hv,), generator=g, device=dev) * 2 - 1
+    gl = (-torch.exp(a) * torch.nn.functional.softplus(
+        torch.randn((1, T, hv), generator=g, device=dev))).contiguous()
+    S = torch.zeros((1, hv, dv, dk), dtype=torch.float32, device=dev)
+    fn = lambda: ops.gated_delta_net_chunk_(S, q, k, v, beta, gl)  # noqa: E731
+    ms = _timed_steps(torch, fn, steps, warmup)
+    lib.timing_enable(True)
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    k_ms = _kernel_avg_ms(lib, lib.T_GDN_CHUNK)
+    lib.timing_enable(False)
+    head_chunks = hv * (T // C)
+    flops = head_chunks * (2 * C * C * (3 * dk + 2 * dv) + 6 * C * dk * dv)
+    # decode: 256 steps on the carried state
+    q1, k1, v1 = q[:, 0].contiguous(), k[:, 0].contiguous(), v[:, 0].contiguous()
+    b1, g1 = beta[:, 0].contiguous(), gl[:, 0].contiguous()
+    step = lambda: ops.gated_delta_net_step_(S, q1, k1, v1, b1, g1)  # noqa: E731
+    n_dec = 256
+    dec_ms = _timed_steps(torch, step, n_dec, 16)
+    lib.timing_enable(True)
+    for _ in range(n_dec):
+        step()
+    torch.cuda.synchronize()
+    dk_ms = _kernel_avg_ms(lib, lib.T_GDN_STEP)
+    lib.timing_enable(False)
+    step_bytes = 2 * hv * dv * dk * 4 + (2 * hk * dk + 2 * hv * dv) * 2
+    return {"prefill_ms": ms, "prefill_kernel_ms": k_ms, "prefill_flops": flops,
+            "prefill_tflops": flops / (k_ms * 1e-3) / 1e12,
+            "decode_us_per_step": dec_ms * 1e3, "decode_kernel_us": dk_ms * 1e3,
+            "decode_step_bytes": step_bytes,
+            "decode_kernel_gbs": step_bytes / (dk_ms * 1e-3) / 1e9}
+
+
 def cpu_baseline_c2(q, K, V, batch, hkv, d, budget_s=12.0):
     """Time the oracle's two-pass llama decode (fp32, model.py:1246-1252) on
     the C2 workload; returns GB/s of algorithmic bytes and the sample."""
@@ -201,6 +248,17 @@ def main() -> int:
             "kernel_ms": round(c3["kernel_ms"], 4),
             "kernel_tflops": round(c3["kernel_tflops"], 1),
             "flops_per_step": c3["flops"]}
+        c5 = bench_gdn(torch, ops, lib, steps=steps, warmup=warmup)
+        extra["c5_gdn_bf16"] = {
+            "prefill_1024_ms": round(c5["prefill_ms"], 4),
+            "prefill_kernel_ms": round(c5["prefill_kernel_ms"], 4),
+            "prefill_kernel_tflops": round(c5["prefill_tflops"], 1),
+            "prefill_frac_mfma_bf16": round(c5["prefill_tflops"] / BF16_PEAK_TFLOPS, 4),
+            "prefill_flops_chunked": c5["prefill_flops"],
+            "decode_us_per_step": round(c5["decode_us_per_step"], 2),
+            "decode_kernel_us": round(c5["decode_kernel_us"], 2),
+            "decode_kernel_gbs": round(c5["decode_kernel_gbs"], 1),
+            "decode_frac_hbm": round(c5["decode_kernel_gbs"] / HBM_PEAK_GBS, 4)}
         c1 = bench_decode(torch, ops, lib, batch=1, ctx=512, hq=32, hkv=8, d=64,
                           dtype=torch.float32, gate=False, steps=steps, warmup=warmup, seed=1)
         c1.pop("tensors")

@@ -154,6 +154,46 @@ int alpx_prefill_causal(const void* q, const void* key, const void* value, void*
                         int64_t kv_start, float scale, int dtype, int out_dtype, void* stream);
 
 /*
+ * Gated delta-rule (GDN) decode step, in place on the state.
+ * Replaces Qwen35RocmOps.gated_delta_net_step_ (qwen35_rocm_ops.py:362-407),
+ * qwen35_kernels.qwen35_gdn_step (qwen35_kernels.py:310-332) and
+ * qwen35_cuda._gdn_step/_gdn_step_out (qwen35_cuda.py:239-293).
+ *
+ * state [batch, value_heads, value_dim, key_dim] fp32 (row-major value x
+ * key, qwen35_ops.py:318-323); q, k [batch, key_heads, key_dim]; v and out
+ * [batch, value_heads, value_dim]; beta and log_decay [batch, value_heads]
+ * fp32.  Value head h reads key head h % key_heads (qwen35_ops.py:275-285):
+ *   S <- exp(g) S; p = S k; S <- S + beta (v - p) k^T; out = S q / sqrt(key_dim)
+ * q/k/v use `dtype`, out `out_dtype`; arithmetic is fp32.  key_dim <= 256.
+ */
+int alpx_gdn_step(float* state, const void* q, const void* k, const void* v, const float* beta,
+                  const float* log_decay, void* out, int batch, int key_heads, int value_heads,
+                  int key_dim, int value_dim, int dtype, int out_dtype, void* stream);
+
+/* Workspace bytes for alpx_gdn_chunk_prefill (chunked path). */
+size_t alpx_gdn_chunk_workspace_bytes(int batch, int tokens, int value_heads, int key_dim);
+
+/*
+ * GDN over a `tokens`-long prefill, in place on the state: the same result
+ * as `tokens` calls of alpx_gdn_step (the reference's only form, the
+ * token-sequential scan of qwen35_ops.gated_delta_net_scan,
+ * qwen35_ops.py:373-403, and Qwen35Model.prefill_state,
+ * qwen35_runtime.py:777-810), computed in chunks of 64 tokens.
+ *
+ * q, k [batch, tokens, key_heads, key_dim]; v and out [batch, tokens,
+ * value_heads, value_dim]; beta, log_decay [batch, tokens, value_heads] fp32;
+ * state as in alpx_gdn_step.  bf16 inputs with key_dim in {64, 128, 256},
+ * value_dim a multiple of 16 and 16-byte aligned rows run the chunked
+ * MFMA kernels (workspace of alpx_gdn_chunk_workspace_bytes needed);
+ * anything else runs the step kernel token by token (workspace unused).
+ */
+int alpx_gdn_chunk_prefill(float* state, const void* q, const void* k, const void* v,
+                           const float* beta, const float* log_decay, void* out, void* workspace,
+                           size_t workspace_bytes, int batch, int tokens, int key_heads,
+                           int value_heads, int key_dim, int value_dim, int dtype, int out_dtype,
+                           void* stream);
+
+/*
  * Sigmoid output gate: out[i] = values[i] * sigmoid(gate[i]) for i < n, with
  * the stable two-branch sigmoid of tensor.stable_sigmoid (tensor.py:123-129).
  * Replaces Qwen35RocmOps.sigmoid_gate (qwen35_rocm_ops.py:286-290) and
