@@ -1,7 +1,7 @@
 // Causal (optionally windowed) GQA prefill attention.
 //
 // fp16/bf16 with head_dim 64/128/256 (prefill_mfma): a flash-attention
-// forward pass on v_mfma_f32_16x16x32_{f16,bf16}.  A block owns 64*NQB query
+// forward pass on v_mfma_f32_16x16x32_{f16,bf16}.  A block owns 16*NQB query
 // columns per wave x 4 waves, where a column is one (token, query head) pair
 // of one kv head's GQA group, so every K/V tile staged in LDS serves all the
 // group's heads.  Per 64-key (32 for head_dim 256) tile each wave computes
@@ -12,8 +12,9 @@
 // from the row-major LDS tile with transposing reads.  K/V tiles are double
 // buffered: the next tile's global loads are in flight while the current
 // tile is multiplied.  Tiles entirely above the diagonal are never loaded;
-// tiles entirely above one wave's diagonal are skipped by that wave.  The
-// latest (most expensive) column tiles are launched first.
+// tiles entirely above one wave's diagonal are skipped by that wave.  Blocks
+// are mapped so that one kv head's blocks share one XCD (and its L2), with
+// the latest (most expensive) column tiles launched first.
 //
 // Everything else (fp32, odd head dims, unaligned rows) runs the split-K
 // decode machinery in causal mode: query token t is a "sequence" whose
@@ -38,17 +39,52 @@ struct PrefillArgs {
   int64_t kv_start;        // absolute position of cache row 0
   int window;              // > 0: row at p sees keys in (p - window, p]
   int q_tokens, kv_tokens, q_heads, kv_heads, group;
-  int col_tiles;           // column tiles along blockIdx.x
+  int col_tiles;           // column tiles per kv head
+  int per_xcd;             // work items per XCD slice of the grid
   float scale_log2;
 };
+
+constexpr int kXcds = 8;  // MI355X: workgroup b is dispatched to XCD b % 8
+
+// XCD-aware work mapping.  Work items (kv head, column tile) are ordered
+// kv-head-major, heaviest column tile first, and cut into 8 contiguous
+// slices, slice x running on XCD x, so the blocks of one kv head share one
+// XCD's L2 and its K/V tiles are fetched from HBM once instead of once per
+// XCD.  Inside a slice the first half of the dispatch order takes the heavy
+// items in descending order and the second half the light items in
+// ascending order, so the two blocks that share a CU (dispatched one slice
+// pass apart) carry a heavy and a light tile.
+__device__ __forceinline__ bool prefill_work(const PrefillArgs& a, int& kvh, int& ctile) {
+  const int b = blockIdx.x;
+  const int j = b / kXcds;
+  const int half = (a.per_xcd + 1) / 2;
+  const int rank = j < half ? j : a.per_xcd - 1 - (j - half);
+  const int item = (b % kXcds) * a.per_xcd + rank;
+  if (item >= a.kv_heads * a.col_tiles) return false;
+  kvh = item / a.col_tiles;
+  ctile = a.col_tiles - 1 - (item - kvh * a.col_tiles);
+  return true;
+}
+
+// Scores are compared in the raw (unscaled) domain; the running max of a
+// column is only moved when a tile's max exceeds it by more than
+// kRescale / (scale log2 e), i.e. p = 2^((s - m) scale log2 e) stays <= 2^8.
+// O and l share the stale scale, so the result is exact; the rescale
+// multiplies (64 per tile) are skipped on almost every tile.
+constexpr float kRescale = 8.0f;
 
 template <typename T, typename TO, int D, int BK, int NQB>
 __global__ void __launch_bounds__(256, 2)
 prefill_mfma(PrefillArgs a) {
   typedef typename Vec8<T>::type V8;
   typedef typename Vec4<T>::type V4;
-  constexpr int kStride = D + 8;          // LDS row stride (elements), 16-byte aligned rows
-  constexpr int kTileElems = BK * kStride;
+  // LDS row strides (elements).  K rows are read 16 B per lane, 16 rows at a
+  // time: a 16-byte bank shift per row keeps 8 consecutive rows on distinct
+  // banks.  V rows are read by 4-row transposing reads of 32 B per row: a
+  // 32-byte shift keeps those 4 rows on distinct banks.
+  constexpr int kStride = D + 8;
+  constexpr int kVStride = D + 16;
+  constexpr int kTileElems = BK * kVStride;
   constexpr int kUnits = D / 8;           // 16-byte units per row
   constexpr int kUPT = BK * kUnits / 256; // units per thread per tensor per tile
   constexpr int KB = BK / 16;
@@ -62,13 +98,14 @@ prefill_mfma(PrefillArgs a) {
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hl = lane & 15;
   const int quad = lane >> 4;
-  const int kvh = blockIdx.y;
+  int kvh, ctile;
+  if (!prefill_work(a, kvh, ctile)) return;
   const int G = a.group;
   const int cols = a.q_tokens * G;
-  const int col0 = (a.col_tiles - 1 - (int)blockIdx.x) * kCols;  // heaviest tiles first
+  const int col0 = ctile * kCols;
   const int wcol0 = col0 + kWaveCols * wave;
 
   int tok[NQB], hq[NQB];
@@ -81,20 +118,18 @@ prefill_mfma(PrefillArgs a) {
     tok[qb] = cc / G;
     hq[qb] = kvh * G + (cc - tok[qb] * G);
   }
+  // Positions relative to the first cache row: key j is visible to query
+  // token t iff j <= rel0 + t (and j > rel0 + t - window).
+  const int rel0 = (int)(a.pos0 - a.kv_start);
   const int bt_first = col0 / G;
   const int bt_last = (min(col0 + kCols, cols) - 1) / G;
   const int wt_first = min(wcol0, cols - 1) / G;
   const int wt_last = (min(wcol0 + kWaveCols, cols) - 1) / G;
 
   // Key rows [lo, hi) that any column of the block can see.
-  int64_t h64 = a.pos0 + bt_last + 1 - a.kv_start;
-  const int hi = (int)(h64 < 0 ? 0 : (h64 > a.kv_tokens ? a.kv_tokens : h64));
+  const int hi = max(0, min(a.kv_tokens, rel0 + bt_last + 1));
   int lo = 0;
-  if (a.window > 0) {
-    int64_t l64 = a.pos0 + bt_first - a.window + 1 - a.kv_start;
-    lo = (int)(l64 < 0 ? 0 : (l64 > hi ? hi : l64));
-    lo = lo / BK * BK;
-  }
+  if (a.window > 0) lo = min(hi, max(0, rel0 + bt_first - a.window + 1)) / BK * BK;
 
   // B operand of S^T = K Q^T: lane holds Q[column][32 ks + 8 quad + 0..7].
   V8 qv[NQB][KS];
@@ -117,19 +152,38 @@ prefill_mfma(PrefillArgs a) {
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) o[qb][mb] = (f32x4){0.f, 0.f, 0.f, 0.f};
   }
+  const float c2 = a.scale_log2;
+  const float thr = kRescale / c2;
 
   const T* kg = (const T*)a.k + (int64_t)kvh * D;
   const T* vg = (const T*)a.v + (int64_t)kvh * D;
+  int urow[kUPT], kofs[kUPT], vofs[kUPT];
+#pragma unroll
+  for (int u = 0; u < kUPT; ++u) {
+    const int idx = u * 256 + tid;
+    urow[u] = idx / kUnits;
+    const int c = idx - urow[u] * kUnits;
+    kofs[u] = urow[u] * (int)a.ks_pos + 8 * c;
+    vofs[u] = urow[u] * (int)a.vs_pos + 8 * c;
+  }
   V8 kreg[kUPT], vreg[kUPT];
   auto gload = [&](int k0) {
+    const T* kt = kg + (int64_t)k0 * a.ks_pos;
+    const T* vt = vg + (int64_t)k0 * a.vs_pos;
+    if (k0 + BK <= hi) {
 #pragma unroll
-    for (int u = 0; u < kUPT; ++u) {
-      const int idx = u * 256 + tid;
-      const int r = idx / kUnits;
-      const int c = idx - r * kUnits;
-      const int64_t key = min(k0 + r, hi - 1);
-      kreg[u] = *(const V8*)(kg + key * a.ks_pos + 8 * c);
-      vreg[u] = *(const V8*)(vg + key * a.vs_pos + 8 * c);
+      for (int u = 0; u < kUPT; ++u) {
+        kreg[u] = *(const V8*)(kt + kofs[u]);
+        vreg[u] = *(const V8*)(vt + vofs[u]);
+      }
+    } else {  // last partial tile: clamp rows to hi - 1
+      const int lim = hi - 1 - k0;
+#pragma unroll
+      for (int u = 0; u < kUPT; ++u) {
+        const int over = max(urow[u] - lim, 0);
+        kreg[u] = *(const V8*)(kt + kofs[u] - over * (int)a.ks_pos);
+        vreg[u] = *(const V8*)(vt + vofs[u] - over * (int)a.vs_pos);
+      }
     }
   };
   auto lstore = [&](int buf) {
@@ -138,10 +192,10 @@ prefill_mfma(PrefillArgs a) {
 #pragma unroll
     for (int u = 0; u < kUPT; ++u) {
       const int idx = u * 256 + tid;
-      const int r = idx / kUnits;
+      const int r = urow[u];
       const int c = idx - r * kUnits;
       *(V8*)(Kd + r * kStride + 8 * c) = kreg[u];
-      *(V8*)(Vd + r * kStride + 8 * c) = vreg[u];
+      *(V8*)(Vd + r * kVStride + 8 * c) = vreg[u];
     }
   };
 
@@ -156,19 +210,25 @@ prefill_mfma(PrefillArgs a) {
   for (int k0 = lo; k0 < hi; k0 += BK) {
     const bool next = k0 + BK < hi;
     if (next) gload(k0 + BK);
-    const int64_t kp0 = k0 + a.kv_start;  // absolute position of the tile's first key
-    const bool skip = kp0 > a.pos0 + wt_last ||
-                      (a.window > 0 && kp0 + BK - 1 <= a.pos0 + wt_first - a.window);
+    const bool skip = k0 > rel0 + wt_last ||
+                      (a.window > 0 && k0 + BK - 1 <= rel0 + wt_first - a.window);
     if (!skip) {
+      // The mask is needed only on tiles that straddle a row's diagonal or
+      // window edge, or run past the last row; the branch is wave-uniform.
+      const bool need_mask = k0 + BK - 1 > rel0 + wt_first || k0 + BK > hi ||
+                             (a.window > 0 && k0 <= rel0 + wt_last - a.window);
       const T* Ks = smem + 2 * buf * kTileElems;
       const T* Vs = Ks + kTileElems;
       f32x4 sc[KB][NQB];
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
+      for (int kb = 0; kb < KB; ++kb) {
+        const V8 ka = *(const V8*)(Ks + (16 * kb + hl) * kStride + 8 * quad);
 #pragma unroll
-        for (int qb = 0; qb < NQB; ++qb) sc[kb][qb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+        for (int qb = 0; qb < NQB; ++qb)
+          sc[kb][qb] = mfma16x16x32(ka, qv[qb][0], (f32x4){0.f, 0.f, 0.f, 0.f});
+      }
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
+      for (int ks = 1; ks < KS; ++ks) {
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
           const V8 ka = *(const V8*)(Ks + (16 * kb + hl) * kStride + 32 * ks + 8 * quad);
@@ -176,56 +236,61 @@ prefill_mfma(PrefillArgs a) {
           for (int qb = 0; qb < NQB; ++qb) sc[kb][qb] = mfma16x16x32(ka, qv[qb][ks], sc[kb][qb]);
         }
       }
-      const bool need_mask = kp0 + BK - 1 > a.pos0 + wt_first || k0 + BK > hi ||
-                             (a.window > 0 && kp0 <= a.pos0 + wt_last - a.window);
+      if (__builtin_expect(need_mask, 0)) {
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) {
+          const int qrel = rel0 + tok[qb];
+#pragma unroll
+          for (int kb = 0; kb < KB; ++kb) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int key = k0 + 16 * kb + 4 * quad + i;
+              const bool ok = key < hi && key <= qrel && (a.window <= 0 || key > qrel - a.window);
+              sc[kb][qb][i] = ok ? sc[kb][qb][i] : -INFINITY;
+            }
+          }
+        }
+      }
       V8 pv[KK][NQB];
 #pragma unroll
       for (int qb = 0; qb < NQB; ++qb) {
-        const int64_t qpos = a.pos0 + tok[qb];
-        float x[KB][4];
-        float mx = -INFINITY;
+        float mx = sc[0][qb][0];
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb) {
+        for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            float v = sc[kb][qb][i] * a.scale_log2;
-            if (need_mask) {
-              const int key = k0 + 16 * kb + 4 * quad + i;
-              const int64_t kp = key + a.kv_start;
-              const bool ok = key < hi && kp <= qpos && (a.window <= 0 || kp > qpos - a.window);
-              v = ok ? v : -INFINITY;
-            }
-            x[kb][i] = v;
-            mx = fmaxf(mx, v);
-          }
-        }
+          for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[kb][qb][i]);
         mx = fmaxf(mx, __shfl_xor(mx, 16));
         mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float mn = fmaxf(m[qb], mx);
-        const float mu = mn == -INFINITY ? 0.f : mn;
-        const float alpha = fast_exp2(m[qb] - mu);
+        const bool grow = mx > m[qb] + thr;
+        if (__ballot(grow) != 0) {  // rare: move the reference max and rescale
+          const float mn = grow ? mx : m[qb];
+          const float alpha = m[qb] == -INFINITY ? 0.f : fast_exp2((m[qb] - mn) * c2);
+          l[qb] *= alpha;
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb) o[qb][mb] *= alpha;
+          m[qb] = mn;
+        }
+        const float mc = m[qb] == -INFINITY ? 0.f : m[qb] * c2;
         float ps = 0.f;
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float p = fast_exp2(x[kb][i] - mu);
+            const float p = fast_exp2(__builtin_fmaf(sc[kb][qb][i], c2, -mc));
             ps += p;
             pv[kb >> 1][qb][4 * (kb & 1) + i] = from_f32<T>(p);
           }
         }
-        l[qb] = l[qb] * alpha + ps;
-        m[qb] = mn;
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb) o[qb][mb] *= alpha;
+        l[qb] += ps;
       }
       // O^T += V^T P^T; rows 32 kk + 16 h + 4 quad + 0..3 via transposing reads.
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) {
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) {
-          const V4 v0 = lds_read_tr4(Vs + (32 * kk + tr_row) * kStride + 16 * mb + tr_col);
-          const V4 v1 = lds_read_tr4(Vs + (32 * kk + 16 + tr_row) * kStride + 16 * mb + tr_col);
+          const V4 v0 = lds_read_tr4(Vs + (32 * kk + tr_row) * kVStride + 16 * mb + tr_col);
+          const V4 v1 = lds_read_tr4(Vs + (32 * kk + 16 + tr_row) * kVStride + 16 * mb + tr_col);
           const V8 va = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
           for (int qb = 0; qb < NQB; ++qb) o[qb][mb] = mfma16x16x32(va, pv[kk][qb], o[qb][mb]);
@@ -315,7 +380,10 @@ extern "C" int alpx_prefill_causal(const void* q, const void* key, const void* v
   const bool mfma = dtype != ALPX_F32 && key_dim == value_dim &&
                     (key_dim == 64 || key_dim == 128 || key_dim == 256) && (align & 15) == 0 &&
                     getenv("ALPX_PREFILL_GENERIC") == nullptr;
-  if (mfma) {
+  // the MFMA kernel forms per-tile row offsets in 32 bits
+  const bool offsets_fit = k_pos_stride * 256 < (int64_t)1 << 31 && v_pos_stride * 256 < (int64_t)1 << 31 &&
+                           q_pos0 - kv_start < ((int64_t)1 << 30) && q_pos0 - kv_start > -((int64_t)1 << 30);
+  if (mfma && offsets_fit) {
     const void* kernel = nullptr;
     if (dtype == ALPX_F16)
       kernel = pick_kernel_out<f16_t>(key_dim, out_dtype);
@@ -339,11 +407,12 @@ extern "C" int alpx_prefill_causal(const void* q, const void* key, const void* v
     const int cols_per_block = key_dim == 256 ? 64 : 128;
     const int64_t cols = (int64_t)q_tokens * group;
     a.col_tiles = (int)((cols + cols_per_block - 1) / cols_per_block);
+    const int64_t items = (int64_t)a.col_tiles * kv_heads;
+    a.per_xcd = (int)((items + kXcds - 1) / kXcds);
     a.scale_log2 = scale * kLog2e;
     TimedRegion timed(ALPX_T_PREFILL, s);
     void* args[] = {(void*)&a};
-    hipError_t err =
-        hipLaunchKernel(kernel, dim3(a.col_tiles, kv_heads), dim3(256), args, 0, s);
+    hipError_t err = hipLaunchKernel(kernel, dim3(a.per_xcd * kXcds), dim3(256), args, 0, s);
     if (err != hipSuccess)
       return fail(ALPX_EHIP, "prefill launch failed: %s", hipGetErrorString(err));
     return check_launch("prefill_mfma");

@@ -213,6 +213,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only-headline", action="store_true")
+    ap.add_argument("--workloads", default="c4,c3,c5,c1",
+                    help="comma list of secondary workloads to run (c1, c3, c4, c5)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
@@ -231,7 +233,8 @@ def main() -> int:
     c2 = bench_decode(torch, ops, lib, batch=16, ctx=8192, hq=32, hkv=8, d=128,
                       dtype=torch.float16, gate=False, steps=steps, warmup=warmup, seed=2)
     extra = {}
-    if not args.only_headline:
+    wl = set() if args.only_headline else set(args.workloads.split(","))
+    if "c4" in wl:
         c4 = bench_decode(torch, ops, lib, batch=4, ctx=32768, hq=16, hkv=2, d=256,
                           dtype=torch.bfloat16, gate=True, steps=steps, warmup=warmup, seed=4)
         c4.pop("tensors")
@@ -240,6 +243,7 @@ def main() -> int:
             "ms_per_step": round(c4["ms_per_step"], 4),
             "split_kernel_gbs": round(c4["split_gbs"], 1),
             "split_ms": round(c4["split_ms"], 4), "combine_ms": round(c4["combine_ms"], 4)}
+    if "c3" in wl:
         c3 = bench_prefill(torch, ops, lib, steps=steps, warmup=warmup)
         extra["c3_prefill_bf16_2k_on_2k"] = {
             "tflops": round(c3["tflops"], 1),
@@ -248,6 +252,7 @@ def main() -> int:
             "kernel_ms": round(c3["kernel_ms"], 4),
             "kernel_tflops": round(c3["kernel_tflops"], 1),
             "flops_per_step": c3["flops"]}
+    if "c5" in wl:
         c5 = bench_gdn(torch, ops, lib, steps=steps, warmup=warmup)
         extra["c5_gdn_bf16"] = {
             "prefill_1024_ms": round(c5["prefill_ms"], 4),
@@ -259,6 +264,7 @@ def main() -> int:
             "decode_kernel_us": round(c5["decode_kernel_us"], 2),
             "decode_kernel_gbs": round(c5["decode_kernel_gbs"], 1),
             "decode_frac_hbm": round(c5["decode_kernel_gbs"] / HBM_PEAK_GBS, 4)}
+    if "c1" in wl:
         c1 = bench_decode(torch, ops, lib, batch=1, ctx=512, hq=32, hkv=8, d=64,
                           dtype=torch.float32, gate=False, steps=steps, warmup=warmup, seed=1)
         c1.pop("tensors")
