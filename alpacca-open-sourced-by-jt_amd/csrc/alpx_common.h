@@ -80,6 +80,13 @@ __device__ __forceinline__ bf16x4 lds_read_tr4(const bf16_t* p) {
   return __builtin_bit_cast(bf16x4, v);
 }
 
+// Raw buffer resource over `bytes` bytes at `base` (loads past the end read
+// zero instead of touching memory).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+
 // Blocks of `kernel` (with `block` threads, `lds` dynamic bytes) that fit on
 // one CU at once, times the CU count of the current device (cached per
 // kernel and device).

@@ -157,33 +157,30 @@ prefill_mfma(PrefillArgs a) {
 
   const T* kg = (const T*)a.k + (int64_t)kvh * D;
   const T* vg = (const T*)a.v + (int64_t)kvh * D;
-  int urow[kUPT], kofs[kUPT], vofs[kUPT];
+  // Tile loads are raw buffer loads: a per-tile scalar resource (base = row
+  // k0) plus per-thread constant byte offsets, so no per-tile vector address
+  // arithmetic.  Rows at or past kv_tokens read as zero (masked anyway).
+  int urow[kUPT];
+  uint32_t kofs[kUPT], vofs[kUPT];
 #pragma unroll
   for (int u = 0; u < kUPT; ++u) {
     const int idx = u * 256 + tid;
     urow[u] = idx / kUnits;
     const int c = idx - urow[u] * kUnits;
-    kofs[u] = urow[u] * (int)a.ks_pos + 8 * c;
-    vofs[u] = urow[u] * (int)a.vs_pos + 8 * c;
+    kofs[u] = (uint32_t)((urow[u] * a.ks_pos + 8 * c) * (int64_t)sizeof(T));
+    vofs[u] = (uint32_t)((urow[u] * a.vs_pos + 8 * c) * (int64_t)sizeof(T));
   }
   V8 kreg[kUPT], vreg[kUPT];
   auto gload = [&](int k0) {
-    const T* kt = kg + (int64_t)k0 * a.ks_pos;
-    const T* vt = vg + (int64_t)k0 * a.vs_pos;
-    if (k0 + BK <= hi) {
+    const uint32_t rows = (uint32_t)(a.kv_tokens - k0);
+    const __amdgpu_buffer_rsrc_t kr =
+        buffer_rsrc(kg + (int64_t)k0 * a.ks_pos, (uint32_t)(rows * a.ks_pos * sizeof(T)));
+    const __amdgpu_buffer_rsrc_t vr =
+        buffer_rsrc(vg + (int64_t)k0 * a.vs_pos, (uint32_t)(rows * a.vs_pos * sizeof(T)));
 #pragma unroll
-      for (int u = 0; u < kUPT; ++u) {
-        kreg[u] = *(const V8*)(kt + kofs[u]);
-        vreg[u] = *(const V8*)(vt + vofs[u]);
-      }
-    } else {  // last partial tile: clamp rows to hi - 1
-      const int lim = hi - 1 - k0;
-#pragma unroll
-      for (int u = 0; u < kUPT; ++u) {
-        const int over = max(urow[u] - lim, 0);
-        kreg[u] = *(const V8*)(kt + kofs[u] - over * (int)a.ks_pos);
-        vreg[u] = *(const V8*)(vt + vofs[u] - over * (int)a.vs_pos);
-      }
+    for (int u = 0; u < kUPT; ++u) {
+      kreg[u] = __builtin_bit_cast(V8, __builtin_amdgcn_raw_buffer_load_b128(kr, kofs[u], 0, 0));
+      vreg[u] = __builtin_bit_cast(V8, __builtin_amdgcn_raw_buffer_load_b128(vr, vofs[u], 0, 0));
     }
   };
   auto lstore = [&](int buf) {
@@ -381,7 +378,8 @@ extern "C" int alpx_prefill_causal(const void* q, const void* key, const void* v
                     (key_dim == 64 || key_dim == 128 || key_dim == 256) && (align & 15) == 0 &&
                     getenv("ALPX_PREFILL_GENERIC") == nullptr;
   // the MFMA kernel forms per-tile row offsets in 32 bits
-  const bool offsets_fit = k_pos_stride * 256 < (int64_t)1 << 31 && v_pos_stride * 256 < (int64_t)1 << 31 &&
+  const bool offsets_fit = (int64_t)kv_tokens * k_pos_stride * (int64_t)es < ((int64_t)1 << 31) &&
+                           (int64_t)kv_tokens * v_pos_stride * (int64_t)es < ((int64_t)1 << 31) &&
                            q_pos0 - kv_start < ((int64_t)1 << 30) && q_pos0 - kv_start > -((int64_t)1 << 30);
   if (mfma && offsets_fit) {
     const void* kernel = nullptr;
