@@ -11,7 +11,8 @@ import ctypes
 import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libalpx.so")
+# ALPX_LIBRARY overrides the in-tree build (e.g. to compare two builds).
+LIB_PATH = os.environ.get("ALPX_LIBRARY") or os.path.join(_HERE, "libalpx.so")
 ABI_VERSION = 1
 
 F32, F16, BF16 = 0, 1, 2
