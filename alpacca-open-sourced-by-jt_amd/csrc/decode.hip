@@ -372,43 +372,71 @@ decode_split_generic(DecodeArgs a) {
 // ------------------------------------------------------------ combine
 
 // Pass 2: block (b*Hq + h, 64-column slice) merges the split partials of one
-// query head for 64 output columns.  Every thread derives the merged max M
-// and sum L from the (few) partial (m, l) pairs; the four waves each sum a
-// quarter of the partials with independent loads and reduce through LDS.
+// query head for 64 output columns.  Wave w folds slots w, w+4, ... into an
+// online (m, l, acc) state; each group of four slots has its max, sum and
+// partial loads issued together (none depends on the running max), so the
+// kernel pays about one memory round trip.  The four wave states are then
+// merged through LDS by wave 0.
 template <typename T, typename TO>
 __global__ void __launch_bounds__(256)
 decode_combine(DecodeArgs a) {
-  __shared__ float red[kWaves][64];
+  constexpr int kGroup = 4;
+  __shared__ float red[3][kWaves - 1][64];
   const int64_t bh = blockIdx.x;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int d = blockIdx.y * 64 + lane;
   const int DV = a.value_dim;
+  const int d = blockIdx.y * 64 + lane;
+  const int dc = d < DV ? d : DV - 1;
   const int ns = a.nsplit;
   const float* pm = a.part_m + bh * ns;
   const float* pl = a.part_l + bh * ns;
-  float M = -INFINITY;
-  for (int s = 0; s < ns; ++s) M = fmaxf(M, pm[s]);
-  float acc0 = 0.f, acc1 = 0.f;
-  if (d < DV && M != -INFINITY) {
-    const float* pa = a.part_acc + bh * ns * DV + d;
-    int s = wave;
-    for (; s + kWaves < ns; s += 2 * kWaves) {
-      const float x0 = pa[(int64_t)s * DV];
-      const float x1 = pa[(int64_t)(s + kWaves) * DV];
-      acc0 += x0 * fast_exp2(pm[s] - M);
-      acc1 += x1 * fast_exp2(pm[s + kWaves] - M);
+  const float* pa = a.part_acc + bh * ns * DV + dc;
+  float m = -INFINITY, l = 0.f, acc = 0.f;
+  for (int s0 = wave; s0 < ns; s0 += kGroup * kWaves) {
+    float xm[kGroup], xl[kGroup], xa[kGroup];
+#pragma unroll
+    for (int u = 0; u < kGroup; ++u) {
+      const int s = s0 + u * kWaves;
+      const bool ok = s < ns;
+      xm[u] = ok ? pm[s] : -INFINITY;
+      xl[u] = ok ? pl[s] : 0.f;
+      xa[u] = ok ? pa[(int64_t)s * DV] : 0.f;
     }
-    if (s < ns) acc0 += pa[(int64_t)s * DV] * fast_exp2(pm[s] - M);
+#pragma unroll
+    for (int u = 0; u < kGroup; ++u) {
+      const float mn = fmaxf(m, xm[u]);
+      if (mn == -INFINITY) continue;  // nothing live yet
+      const float c_old = fast_exp2(m - mn);
+      const float c_new = fast_exp2(xm[u] - mn);
+      l = l * c_old + xl[u] * c_new;
+      acc = acc * c_old + xa[u] * c_new;
+      m = mn;
+    }
   }
-  red[wave][lane] = acc0 + acc1;
+  if (wave > 0) {
+    red[0][wave - 1][lane] = m;
+    red[1][wave - 1][lane] = l;
+    red[2][wave - 1][lane] = acc;
+  }
   __syncthreads();
   if (wave != 0 || d >= DV) return;
-  float L = 0.f;
-  if (M != -INFINITY)
-    for (int s = 0; s < ns; ++s) L += pl[s] * fast_exp2(pm[s] - M);
-  const float acc = (red[0][lane] + red[1][lane]) + (red[2][lane] + red[3][lane]);
-  float r = L > 0.f ? acc / L : 0.f;
+  float M = m;
+#pragma unroll
+  for (int w = 0; w < kWaves - 1; ++w) M = fmaxf(M, red[0][w][lane]);
+  float L = 0.f, A = 0.f;
+  if (M != -INFINITY) {
+    const float c0 = fast_exp2(m - M);
+    L = l * c0;
+    A = acc * c0;
+#pragma unroll
+    for (int w = 0; w < kWaves - 1; ++w) {
+      const float cw = fast_exp2(red[0][w][lane] - M);
+      L += red[1][w][lane] * cw;
+      A += red[2][w][lane] * cw;
+    }
+  }
+  float r = L > 0.f ? A / L : 0.f;
   if (a.gate != nullptr) r *= stable_sigmoid(to_f32(((const T*)a.gate)[bh * DV + d]));
   ((TO*)a.out)[bh * DV + d] = from_f32<TO>(r);
 }
