@@ -12,6 +12,12 @@ the other configs (C1 fp32 decode, C4 gated bf16 decode, ...).
 ``cpu_baseline`` times the NumPy oracle (the reference's two-pass llama
 algorithm, fp32) on the same C2 workload on this host.
 
+``roofline.traffic`` (HBM bytes per split launch) comes from two rocprofv3
+counter runs of ``bench.py --pmc-probe`` (FETCH_SIZE, then WRITE_SIZE), each
+scaled by what the counter reads for a plain copy of known size in the same
+run; ``bench.py --traffic-summary FETCH_DIR WRITE_DIR`` turns the two runs
+into the summary under profiles/ that this script reads.
+
 Inputs are synthetic N(0, 1) (seeded), generated on the device.
 """
 
@@ -35,6 +41,10 @@ METRIC = ("decode attn HBM GB/s (% of peak) @8K ctx; "
           "prefill attn TFLOP/s (% MFMA peak)")
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "pmc_traffic_decode_split_c2_f16.md")
+C2_SHAPE = dict(batch=16, ctx=8192, hq=32, hkv=8, d=128)
+SPLIT_KERNEL = "decode_split_mfma"
+COPY_KERNEL = "kv_append_kernel"
 
 
 def _mod(name):
@@ -206,6 +216,110 @@ def cpu_baseline_c2(q, K, V, batch, hkv, d, budget_s=12.0):
     }
 
 
+def _c2_tensors(torch, seed=2):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    b, c, hq, hkv, d = (C2_SHAPE[k] for k in ("batch", "ctx", "hq", "hkv", "d"))
+    q = torch.randn((b, hq, d), generator=g, device="cuda").half()
+    K = torch.randn((c, b, hkv, d), generator=g, device="cuda").half()
+    V = torch.randn((c, b, hkv, d), generator=g, device="cuda").half()
+    return q, K, V
+
+
+def pmc_probe(torch, ops, steps) -> int:
+    """Workload for the counter runs: 3 plain copies of known size (the
+    library's append kernel writing a whole C2-sized K and V cache: it reads
+    and writes 2 x 268,435,456 bytes per launch), then ``steps`` C2 decode
+    steps.  Prints the copy's byte count for the summary step."""
+    q, K, V = _c2_tensors(torch)
+    Kc, Vc = torch.empty_like(K), torch.empty_like(V)
+    ops_mod = _mod("_ops")
+    for _ in range(3):
+        ops_mod.kv_append(Kc, Vc, K, V, position=0)
+    for _ in range(steps):
+        ops.online_attention(q, K, V, length=C2_SHAPE["ctx"])
+    torch.cuda.synchronize()
+    copy_bytes = 2 * K.numel() * K.element_size()
+    print(json.dumps({"copy_kernel": COPY_KERNEL, "copy_read_bytes": copy_bytes,
+                      "copy_write_bytes": copy_bytes, "split_kernel": SPLIT_KERNEL,
+                      "decode_steps": steps}))
+    return 0
+
+
+def _counter_means(run_dir, counter):
+    """Mean per-dispatch value of ``counter`` for the copy and split kernels
+    in one rocprofv3 CSV run directory (rows of one dispatch are summed)."""
+    import csv
+    import glob
+    files = glob.glob(os.path.join(run_dir, "**", "*counter_collection.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no counter_collection.csv under {run_dir}")
+    per = {COPY_KERNEL: {}, SPLIT_KERNEL: {}}
+    for f in files:
+        with open(f, newline="") as fh:
+            for r in csv.DictReader(fh):
+                if r["Counter_Name"] != counter:
+                    continue
+                for key, acc in per.items():
+                    if key in r["Kernel_Name"]:
+                        did = (f, r["Dispatch_Id"])
+                        acc[did] = acc.get(did, 0.0) + float(r["Counter_Value"])
+    out = {}
+    for key, acc in per.items():
+        if not acc:
+            raise SystemExit(f"{counter}: no dispatch of {key} in {run_dir}")
+        out[key] = (statistics.mean(acc.values()), len(acc))
+    return out
+
+
+def traffic_summary(fetch_dir, write_dir) -> int:
+    """Print the profiles/ summary (markdown) from the two counter runs."""
+    copy_bytes = 2 * C2_SHAPE["ctx"] * C2_SHAPE["batch"] * C2_SHAPE["hkv"] * C2_SHAPE["d"] * 2
+    fetch = _counter_means(fetch_dir, "FETCH_SIZE")
+    write = _counter_means(write_dir, "WRITE_SIZE")
+    f_scale = copy_bytes / (fetch[COPY_KERNEL][0] * 1024.0)
+    w_scale = copy_bytes / (write[COPY_KERNEL][0] * 1024.0)
+    fetch_b = fetch[SPLIT_KERNEL][0] * 1024.0 * f_scale
+    write_b = write[SPLIT_KERNEL][0] * 1024.0 * w_scale
+    b, c, hq, hkv, d = (C2_SHAPE[k] for k in ("batch", "ctx", "hq", "hkv", "d"))
+    alg = 2 * c * b * hkv * d * 2 + b * hq * d * 2
+    rec = {"kernel": SPLIT_KERNEL + "<f16,128>", "workload": "C2 uniform 8192, fp16",
+           "traffic_bytes_per_launch": round(fetch_b + write_b),
+           "fetch_bytes_per_launch": round(fetch_b), "write_bytes_per_launch": round(write_b),
+           "alg_bytes_per_launch": alg,
+           "traffic_over_alg": round((fetch_b + write_b) / alg, 4),
+           "fetch_scale": round(f_scale, 5), "write_scale": round(w_scale, 5)}
+    print("# HBM traffic of the decode split kernel (C2 uniform-8192, fp16)\n")
+    print("Counter runs (one rocprofv3 run per counter, from the repository root):\n")
+    print("```")
+    for ctr, dname in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        print(f"rocprofv3 --pmc {ctr} --output-format csv -d {dname} -o run -- "
+              "python3 bench.py --pmc-probe")
+    print(f"python3 bench.py --traffic-summary {fetch_dir} {write_dir}")
+    print("```\n")
+    print("| kernel | counter | mean KiB / dispatch | dispatches |")
+    print("|---|---|---|---|")
+    for ctr, res in (("FETCH_SIZE", fetch), ("WRITE_SIZE", write)):
+        for key in (COPY_KERNEL, SPLIT_KERNEL):
+            print(f"| {key} | {ctr} | {res[key][0]:.1f} | {res[key][1]} |")
+    print(f"\nCalibration: the copy moves {copy_bytes} bytes each way per launch; "
+          f"scale = known bytes / (counter KiB x 1024): fetch {f_scale:.4f}, "
+          f"write {w_scale:.4f}.\n")
+    print("traffic_json: " + json.dumps(rec))
+    return 0
+
+
+def _measured_traffic():
+    """Bytes per split launch from the committed counter summary, or None."""
+    try:
+        with open(TRAFFIC_FILE) as fh:
+            for line in fh:
+                if line.startswith("traffic_json: "):
+                    return json.loads(line[len("traffic_json: "):])
+    except OSError:
+        return None
+    return None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -215,7 +329,13 @@ def main() -> int:
     ap.add_argument("--only-headline", action="store_true")
     ap.add_argument("--workloads", default="c4,c3,c5,c1",
                     help="comma list of secondary workloads to run (c1, c3, c4, c5)")
+    ap.add_argument("--pmc-probe", action="store_true",
+                    help="run the counter-run workload (copy calibration + C2 steps)")
+    ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="summarise two rocprofv3 counter runs of --pmc-probe")
     args = ap.parse_args()
+    if args.traffic_summary:
+        return traffic_summary(*args.traffic_summary)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
               "(the path has no multi-GPU component in this build)", file=sys.stderr)
@@ -228,6 +348,8 @@ def main() -> int:
     lib = _mod("_lib")
     ops = _mod("qwen35_rocm_ops").Qwen35RocmOps()
     steps, warmup = args.steps, args.warmup
+    if args.pmc_probe:
+        return pmc_probe(torch, ops, 5)
 
     # headline: C2 uniform-8192 fp16
     c2 = bench_decode(torch, ops, lib, batch=16, ctx=8192, hq=32, hkv=8, d=128,
@@ -280,6 +402,12 @@ def main() -> int:
         cpu = cpu_baseline_c2(q, K, V, 16, 8, 128)
     c2.pop("tensors")
 
+    traffic = _measured_traffic()
+    if traffic:
+        extra["traffic_source"] = {k: traffic[k] for k in (
+            "fetch_bytes_per_launch", "write_bytes_per_launch", "traffic_over_alg",
+            "fetch_scale", "write_scale")}
+        extra["traffic_source"]["file"] = os.path.relpath(TRAFFIC_FILE, ROOT)
     line = {
         "metric": METRIC,
         "value": round(c2["gbs"], 2),
@@ -306,7 +434,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(c2["split_gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": traffic["traffic_bytes_per_launch"] if traffic else None,
             "avg_launch_ms": round(c2["split_ms"], 5),
             "alg_bytes_per_launch": c2["split_alg_bytes"],
         },
