@@ -140,7 +140,12 @@ def dtype_code(torch, dtype) -> int:
 
 
 def stream_handle(torch, device) -> int:
-    """hipStream_t of torch's current stream on ``device``."""
+    """hipStream_t of torch's current stream on ``device``.  Uses torch's raw
+    stream query (no Stream object per call) when this torch build has it."""
+    raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+    if raw is not None:
+        index = device.index if hasattr(device, "index") else device
+        return int(raw(torch.cuda.current_device() if index is None else int(index)))
     return int(torch.cuda.current_stream(device).cuda_stream)
 
 

@@ -52,7 +52,33 @@ struct GdnArgs {
 
 // ------------------------------------------------------------ decode step
 
-template <typename T, typename TO>
+// A 32-lane half-wave updates kStepRows state rows; lane `lane` owns columns
+// 4 lane + 128 e + 0..3 (e < NV, NV = ceil(Dk / 128)).  Every load is issued
+// unconditionally from a clamped address and zeroed afterwards when out of
+// range, so the whole working set (q, k, v, beta, g and the state rows) is in
+// flight at once; a predicated load would be compiled as a branch with a
+// wait after each load.  VEC: Dk % 4 == 0 and aligned rows, so each group of
+// four columns is one vector load.
+constexpr int kStepRows = 2;
+
+template <typename T, bool VEC>
+__device__ __forceinline__ void load4(const T* p, int c, int n, float (&x)[4]) {
+  if constexpr (VEC) {
+    typedef typename Vec4<T>::type V4;
+    const bool ok = c < n;
+    const V4 v = *(const V4*)(p + (ok ? c : 0));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) x[j] = ok ? to_f32(v[j]) : 0.f;
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float v = to_f32(p[min(c + j, n - 1)]);
+      x[j] = c + j < n ? v : 0.f;
+    }
+  }
+}
+
+template <typename T, typename TO, int NV, bool VEC>
 __global__ void __launch_bounds__(256)
 gdn_step_kernel(GdnArgs a) {
   const int lane = threadIdx.x & 31;
@@ -61,66 +87,82 @@ gdn_step_kernel(GdnArgs a) {
   const int b = blockIdx.z;
   const int kh = h % a.Hk;
   const int Dk = a.Dk;
+  const int Dv = a.Dv;
+  const int64_t bh = (int64_t)b * a.Hv + h;
   const T* kp = (const T*)a.k + ((int64_t)b * a.Hk + kh) * Dk;
   const T* qp = (const T*)a.q + ((int64_t)b * a.Hk + kh) * Dk;
-  float kk[8], qq[8];
+  const int r0 = (blockIdx.x * 8 + hw) * kStepRows;
+
+  float kk[NV][4], qq[NV][4], s[kStepRows][NV][4], vv[kStepRows];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const int c = lane + 32 * e;
-    kk[e] = c < Dk ? to_f32(kp[c]) : 0.f;
-    qq[e] = c < Dk ? to_f32(qp[c]) : 0.f;
+  for (int e = 0; e < NV; ++e) {
+    load4<T, VEC>(kp, 4 * lane + 128 * e, Dk, kk[e]);
+    load4<T, VEC>(qp, 4 * lane + 128 * e, Dk, qq[e]);
   }
-  const int64_t bh = (int64_t)b * a.Hv + h;
-  const float decay = expf(a.g[bh]);
-  const float beta = a.beta[bh];
-  const T* vp = (const T*)a.v + bh * a.Dv;
-  // 4 rows per half-wave, interleaved for independent reductions in flight
-  const int r0 = blockIdx.x * 32 + hw * 4;
-  float s[4][8];
-  float p[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int r = r0 + j;
-    float* row = a.state + (bh * a.Dv + (r < a.Dv ? r : 0)) * Dk;
+  for (int j = 0; j < kStepRows; ++j) {
+    const int r = min(r0 + j, Dv - 1);
+    const float* row = a.state + (bh * Dv + r) * Dk;
+#pragma unroll
+    for (int e = 0; e < NV; ++e) load4<float, VEC>(row, 4 * lane + 128 * e, Dk, s[j][e]);
+    vv[j] = to_f32(((const T*)a.v)[bh * Dv + r]);
+  }
+  const float decay = __expf(a.g[bh]);
+  const float beta = a.beta[bh];
+
+  float p[kStepRows];
+#pragma unroll
+  for (int j = 0; j < kStepRows; ++j) {
     p[j] = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int c = lane + 32 * e;
-      s[j][e] = (c < Dk && r < a.Dv) ? row[c] * decay : 0.f;
-      p[j] += s[j][e] * kk[e];
-    }
+    for (int e = 0; e < NV; ++e)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        s[j][e][c] *= decay;
+        p[j] += s[j][e][c] * kk[e][c];
+      }
   }
 #pragma unroll
   for (int off = 16; off >= 1; off >>= 1)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) p[j] += __shfl_xor(p[j], off, 32);
-  float o[4];
+    for (int j = 0; j < kStepRows; ++j) p[j] += __shfl_xor(p[j], off, 32);
+  float o[kStepRows];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int r = r0 + j;
-    const float delta = r < a.Dv ? beta * (to_f32(vp[r]) - p[j]) : 0.f;
+  for (int j = 0; j < kStepRows; ++j) {
+    const float delta = beta * (vv[j] - p[j]);
     o[j] = 0.f;
-    float* row = a.state + (bh * a.Dv + (r < a.Dv ? r : 0)) * Dk;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int c = lane + 32 * e;
-      s[j][e] += delta * kk[e];
-      o[j] += s[j][e] * qq[e];
-      if (c < Dk && r < a.Dv) row[c] = s[j][e];
+    for (int e = 0; e < NV; ++e)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        s[j][e][c] += delta * kk[e][c];
+        o[j] += s[j][e][c] * qq[e][c];
+      }
+  }
+#pragma unroll
+  for (int j = 0; j < kStepRows; ++j) {
+    const int r = r0 + j;
+    if (r >= Dv) break;
+    float* row = a.state + (bh * Dv + r) * Dk;
+#pragma unroll
+    for (int e = 0; e < NV; ++e) {
+      const int c0 = 4 * lane + 128 * e;
+      if constexpr (VEC) {
+        if (c0 < Dk) *(f32x4*)(row + c0) = (f32x4){s[j][e][0], s[j][e][1], s[j][e][2], s[j][e][3]};
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          if (c0 + c < Dk) row[c0 + c] = s[j][e][c];
+      }
     }
   }
 #pragma unroll
   for (int off = 16; off >= 1; off >>= 1)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) o[j] += __shfl_xor(o[j], off, 32);
-  if (lane < 4) {
-    // lane j writes row r0 + j (selects o[j] without dynamic indexing)
-    float oj = o[0];
-    if (lane == 1) oj = o[1];
-    if (lane == 2) oj = o[2];
-    if (lane == 3) oj = o[3];
-    const int r = r0 + lane;
-    if (r < a.Dv) ((TO*)a.out)[bh * a.Dv + r] = from_f32<TO>(oj * a.scale);
+    for (int j = 0; j < kStepRows; ++j) o[j] += __shfl_xor(o[j], off, 32);
+  if (lane < kStepRows && r0 + lane < Dv) {
+    const float oj = lane == 0 ? o[0] : o[1];
+    ((TO*)a.out)[bh * Dv + r0 + lane] = from_f32<TO>(oj * a.scale);
   }
 }
 
@@ -507,19 +549,33 @@ int launch_chunk_dk(const GdnArgs& a, hipStream_t s) {
   }
 }
 
+template <typename T, typename TO, int NV>
+void launch_step_nv(const GdnArgs& a, bool vec, dim3 grid, hipStream_t s) {
+  if (vec)
+    hipLaunchKernelGGL((gdn_step_kernel<T, TO, NV, true>), grid, dim3(256), 0, s, a);
+  else
+    hipLaunchKernelGGL((gdn_step_kernel<T, TO, NV, false>), grid, dim3(256), 0, s, a);
+}
+
+template <typename T, typename TO>
+void launch_step_to(const GdnArgs& a, bool vec, dim3 grid, hipStream_t s) {
+  if (a.Dk > 128)
+    launch_step_nv<T, TO, 2>(a, vec, grid, s);
+  else
+    launch_step_nv<T, TO, 1>(a, vec, grid, s);
+}
+
 template <typename T>
 int launch_step(const GdnArgs& a, int out_dtype, hipStream_t s) {
-  dim3 grid((a.Dv + 31) / 32, a.Hv, a.B);
+  static_assert(kStepRows == 2, "output lane select assumes two rows per half-wave");
+  const dim3 grid((a.Dv + 8 * kStepRows - 1) / (8 * kStepRows), a.Hv, a.B);
+  const size_t vec_align = 4 * sizeof(T);
+  const bool vec = a.Dk % 4 == 0 && (uintptr_t)a.state % 16 == 0 &&
+                   (uintptr_t)a.q % vec_align == 0 && (uintptr_t)a.k % vec_align == 0;
   switch (out_dtype) {
-    case ALPX_F32:
-      hipLaunchKernelGGL((gdn_step_kernel<T, float>), grid, dim3(256), 0, s, a);
-      break;
-    case ALPX_F16:
-      hipLaunchKernelGGL((gdn_step_kernel<T, f16_t>), grid, dim3(256), 0, s, a);
-      break;
-    default:
-      hipLaunchKernelGGL((gdn_step_kernel<T, bf16_t>), grid, dim3(256), 0, s, a);
-      break;
+    case ALPX_F32: launch_step_to<T, float>(a, vec, grid, s); break;
+    case ALPX_F16: launch_step_to<T, f16_t>(a, vec, grid, s); break;
+    default: launch_step_to<T, bf16_t>(a, vec, grid, s); break;
   }
   return check_launch("gdn_step");
 }

@@ -164,6 +164,9 @@ class Qwen35RocmOps:
         self.capability = capability
         self.device_index = selected
         self.device = f"cuda:{selected}"
+        t = self.torch
+        self._float_dtypes = frozenset((t.float32, t.float16, t.bfloat16))
+        self._int_dtypes = self._float_dtypes | {t.int64, t.int32}
 
     def descriptor(self) -> dict[str, Any]:
         return {
@@ -185,21 +188,17 @@ class Qwen35RocmOps:
                 allow_integer: bool = False) -> Any:
         """Contract check of qwen35_rocm_ops.py:134-165, widened to fp16/bf16."""
         torch = self.torch
-        if not torch.is_tensor(value):
+        if not isinstance(value, torch.Tensor):
             raise TypeError(f"{name} must be a PyTorch tensor")
-        device = value.device
-        if getattr(device, "type", None) != "cuda":
+        if not value.is_cuda:
             raise TypeError(f"{name} must remain on the ROCm device")
-        index = getattr(device, "index", None)
-        if index not in (None, self.device_index):
+        index = value.get_device()
+        if index != self.device_index:
             raise ValueError(f"{name} is on device {index}, expected {self.device_index}")
-        valid = (torch.float32, torch.float16, torch.bfloat16)
-        if allow_integer:
-            valid = valid + (torch.int64, torch.int32)
-        if value.dtype not in valid:
+        if value.dtype not in (self._int_dtypes if allow_integer else self._float_dtypes):
             expected = "float32, float16 or bfloat16"
             raise TypeError(f"{name} must use {expected}" + (" or int" if allow_integer else ""))
-        if dimensions is not None and len(value.shape) != dimensions:
+        if dimensions is not None and value.dim() != dimensions:
             raise ValueError(f"{name} has {_shape(value)}, expected {dimensions} dimensions")
         if not value.is_contiguous():
             raise ValueError(f"{name} must be contiguous")
