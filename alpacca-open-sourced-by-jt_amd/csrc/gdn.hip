@@ -365,6 +365,35 @@ gdn_prep(GdnArgs a) {
 
 // ------------------------------------------------------------ phase B
 
+// Block -> (16-row state slice, value head, batch).  Consecutive block ids
+// run on consecutive XCDs, so the ids are permuted to give the slices of one
+// head neighbouring positions on one XCD: they read the same per-chunk
+// workspace (Ub, M, W) and share that XCD's L2.
+__device__ __forceinline__ void apply_block(const GdnArgs& a, int& slice, int& h, int& b) {
+  const int slices = a.Dv / 16;
+  const int n = slices * a.Hv * a.B;
+  int L = blockIdx.x;
+  if (n % 8 == 0) L = (L % 8) * (n / 8) + L / 8;
+  slice = L % slices;
+  const int rest = L / slices;
+  h = rest % a.Hv;
+  b = rest / a.Hv;
+}
+
+// Global inputs of one chunk for one thread: its share of the K/Q/V rows
+// and decays (staged in LDS) and the rows of W, Ub and M its lane feeds to
+// the MFMAs as A operands.
+template <int DK>
+struct ApplyIn {
+  static constexpr int kUnitsPerThread = kC * (DK / 8) / 256;
+  bf16x8 k[kUnitsPerThread], q[kUnitsPerThread];
+  bf16x8 v;
+  float g;
+  float w[DK / 32][8];
+  float u[2][8];
+  float m[2][8];
+};
+
 template <typename TO, int DK>
 __global__ void __launch_bounds__(256)
 gdn_apply(GdnArgs a) {
@@ -372,6 +401,12 @@ gdn_apply(GdnArgs a) {
   constexpr int kSF = DK + 4;
   constexpr int kDF = kC + 4;
   constexpr int KS = DK / 32;
+  // DK <= 128: the next chunk's inputs are fetched while this chunk computes.
+  // DK = 256 has no registers for a second set; its fetch is issued at the
+  // end of the previous chunk (one exposed latency per chunk).
+  constexpr bool kAhead = DK <= 128;
+  constexpr int kUnits = DK / 8;
+  constexpr int kUPT = ApplyIn<DK>::kUnitsPerThread;
   __shared__ __attribute__((aligned(16))) bf16_t Ks[kC * kS];
   __shared__ __attribute__((aligned(16))) bf16_t Qs[kC * kS];
   __shared__ __attribute__((aligned(16))) bf16_t Vs[kC * 24];  // [t][16 rows] + pad
@@ -381,7 +416,9 @@ gdn_apply(GdnArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hl = lane & 15, quad = lane >> 4;
-  const int r0 = blockIdx.x * 16, h = blockIdx.y, b = blockIdx.z;
+  int slice, h, b;
+  apply_block(a, slice, h, b);
+  const int r0 = slice * 16;
   const int kh = h % a.Hk;
   const int64_t bh = (int64_t)b * a.Hv + h;
   float* sg = a.state + (bh * a.Dv + r0) * DK;
@@ -391,39 +428,76 @@ gdn_apply(GdnArgs a) {
   }
   const int tr_row = 4 * quad + (hl >> 2);
   const int tr_col = 4 * (hl & 3);
-  constexpr int kUnits = DK / 8;
+  const int trow = 16 * wave + hl;  // A-operand row of this lane
 
-  for (int c = 0; c < a.nchunks; ++c) {
+  // Every load is unconditional (rows past the end read a clamped row and
+  // are zeroed), so one fetch puts all of a chunk's inputs in flight.
+  auto fetch = [&](ApplyIn<DK>& in, int c) {
     const int t0 = c * kC;
-    const float* ws = a.ws + (bh * a.nchunks + c) * ws_per_chunk(DK);
-    const float* wG = ws;
-    const float* wU = ws + kC;
-    const float* wM = wU + kC * kC;
-    const float* wW = wM + kC * kC;
 #pragma unroll
-    for (int u = 0; u < kC * kUnits / 256; ++u) {
+    for (int u = 0; u < kUPT; ++u) {
       const int idx = u * 256 + tid;
       const int r = idx / kUnits, cc = idx - (idx / kUnits) * kUnits;
       const int t = t0 + r;
-      bf16x8 kv = {}, qv = {};
-      if (t < a.T) {
-        const int64_t off = (((int64_t)b * a.T + t) * a.Hk + kh) * DK + 8 * cc;
-        kv = *(const bf16x8*)((const bf16_t*)a.k + off);
-        qv = *(const bf16x8*)((const bf16_t*)a.q + off);
+      const int64_t off =
+          (((int64_t)b * a.T + min(t, a.T - 1)) * a.Hk + kh) * DK + 8 * cc;
+      const bf16x8 kv = *(const bf16x8*)((const bf16_t*)a.k + off);
+      const bf16x8 qv = *(const bf16x8*)((const bf16_t*)a.q + off);
+      in.k[u] = t < a.T ? kv : (bf16x8){};
+      in.q[u] = t < a.T ? qv : (bf16x8){};
+    }
+    {
+      const int t = (tid & 127) >> 1, half = tid & 1;
+      const bf16x8 vv = *(const bf16x8*)((const bf16_t*)a.v +
+                                         (((int64_t)b * a.T + min(t0 + t, a.T - 1)) * a.Hv + h) *
+                                             a.Dv + r0 + 8 * half);
+      in.v = t0 + t < a.T ? vv : (bf16x8){};
+    }
+    const float* ws = a.ws + (bh * a.nchunks + c) * ws_per_chunk(DK);
+    const float* wU = ws + kC;
+    const float* wM = wU + kC * kC;
+    const float* wW = wM + kC * kC;
+    in.g = ws[tid & (kC - 1)];
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const f32x4 x0 = *(const f32x4*)(wW + trow * DK + 32 * ks + 8 * quad);
+      const f32x4 x1 = *(const f32x4*)(wW + trow * DK + 32 * ks + 8 * quad + 4);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        in.w[ks][j] = x0[j];
+        in.w[ks][4 + j] = x1[j];
       }
-      *(bf16x8*)(Ks + r * kS + 8 * cc) = kv;
-      *(bf16x8*)(Qs + r * kS + 8 * cc) = qv;
     }
-    if (tid < kC * 2) {  // V slice: 64 rows x 16 values as 2 x 8
-      const int t = tid >> 1, half = tid & 1;
-      bf16x8 vv = {};
-      if (t0 + t < a.T)
-        vv = *(const bf16x8*)((const bf16_t*)a.v +
-                              (((int64_t)b * a.T + t0 + t) * a.Hv + h) * a.Dv + r0 + 8 * half);
-      *(bf16x8*)(Vs + t * 24 + 8 * half) = vv;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) in.u[ks][j] = wU[trow * kC + 32 * ks + tr_slot(quad, j)];
+      const f32x4 x0 = *(const f32x4*)(wM + trow * kC + 32 * ks + 8 * quad);
+      const f32x4 x1 = *(const f32x4*)(wM + trow * kC + 32 * ks + 8 * quad + 4);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        in.m[ks][j] = x0[j];
+        in.m[ks][4 + j] = x1[j];
+      }
     }
-    if (tid < kC) Gs[tid] = wG[tid];
+  };
+
+  ApplyIn<DK> nxt;
+  fetch(nxt, 0);
+  for (int c = 0; c < a.nchunks; ++c) {
+    const int t0 = c * kC;
+    const ApplyIn<DK> cur = nxt;
+#pragma unroll
+    for (int u = 0; u < kUPT; ++u) {
+      const int idx = u * 256 + tid;
+      const int r = idx / kUnits, cc = idx - (idx / kUnits) * kUnits;
+      *(bf16x8*)(Ks + r * kS + 8 * cc) = cur.k[u];
+      *(bf16x8*)(Qs + r * kS + 8 * cc) = cur.q[u];
+    }
+    if (tid < kC * 2) *(bf16x8*)(Vs + (tid >> 1) * 24 + 8 * (tid & 1)) = cur.v;
+    if (tid < kC) Gs[tid] = cur.g;
     __syncthreads();
+    if (kAhead && c + 1 < a.nchunks) fetch(nxt, c + 1);
 
     // S^T operand (B: k = d, n = state row): lane holds S[hl][32 ks + 8 quad + 0..7].
     bf16x8 shi[KS], slo[KS];
@@ -431,12 +505,11 @@ gdn_apply(GdnArgs a) {
     for (int ks = 0; ks < KS; ++ks) split8(Ss + hl * kSF + 32 * ks + 8 * quad, shi[ks], slo[ks]);
 
     // (1) Delta rows 16w.. = Ub V - W S^T
-    const int trow = 16 * wave + hl;  // A-operand row of this lane
     f32x4 ws_acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       bf16x8 whi, wlo;
-      split8(wW + trow * DK + 32 * ks + 8 * quad, whi, wlo);
+      split8(cur.w[ks], whi, wlo);
       ws_acc = mfma16x16x32(whi, shi[ks], ws_acc);
       ws_acc = mfma16x16x32(whi, slo[ks], ws_acc);
       ws_acc = mfma16x16x32(wlo, shi[ks], ws_acc);
@@ -444,23 +517,17 @@ gdn_apply(GdnArgs a) {
     f32x4 uv = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      float x[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) x[j] = wU[trow * kC + 32 * ks + tr_slot(quad, j)];
       bf16x8 uhi, ulo;
-      split8(x, uhi, ulo);
+      split8(cur.u[ks], uhi, ulo);
       const bf16x4 v0 = lds_read_tr4(Vs + (32 * ks + tr_row) * 24 + tr_col);
       const bf16x4 v1 = lds_read_tr4(Vs + (32 * ks + 16 + tr_row) * 24 + tr_col);
       const bf16x8 vb = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
       uv = mfma16x16x32(uhi, vb, uv);
       uv = mfma16x16x32(ulo, vb, uv);
     }
-    f32x4 delta;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      delta[r] = uv[r] - ws_acc[r];
-      Dt[hl * kDF + 16 * wave + 4 * quad + r] = delta[r];  // Delta^T[state row][t]
-    }
+    for (int r = 0; r < 4; ++r)
+      Dt[hl * kDF + 16 * wave + 4 * quad + r] = uv[r] - ws_acc[r];  // Delta^T[state row][t]
     // (2a) Q S^T for the output rows of this wave
     f32x4 qs = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -476,7 +543,7 @@ gdn_apply(GdnArgs a) {
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       bf16x8 mhi, mlo, dhi, dlo;
-      split8(wM + trow * kC + 32 * ks + 8 * quad, mhi, mlo);
+      split8(cur.m[ks], mhi, mlo);
       split8(Dt + hl * kDF + 32 * ks + 8 * quad, dhi, dlo);
       md = mfma16x16x32(mhi, dhi, md);
       md = mfma16x16x32(mhi, dlo, md);
@@ -523,6 +590,7 @@ gdn_apply(GdnArgs a) {
         *sp = gl * *sp + acc[r];
       }
     }
+    if (!kAhead && c + 1 < a.nchunks) fetch(nxt, c + 1);
     __syncthreads();
   }
   for (int idx = tid; idx < 16 * DK; idx += 256) {
@@ -536,7 +604,7 @@ int launch_chunk(const GdnArgs& a, hipStream_t s) {
   hipLaunchKernelGGL((gdn_prep<DK>), dim3(a.nchunks, a.Hv, a.B), dim3(256), 0, s, a);
   int rc = check_launch("gdn_prep");
   if (rc != ALPX_OK) return rc;
-  hipLaunchKernelGGL((gdn_apply<TO, DK>), dim3(a.Dv / 16, a.Hv, a.B), dim3(256), 0, s, a);
+  hipLaunchKernelGGL((gdn_apply<TO, DK>), dim3(a.Dv / 16 * a.Hv * a.B), dim3(256), 0, s, a);
   return check_launch("gdn_apply");
 }
 

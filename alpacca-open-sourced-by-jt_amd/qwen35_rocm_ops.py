@@ -97,7 +97,10 @@ def _positive_finite(name: str, value: float) -> float:
 
 
 def _shape(tensor: Any) -> tuple[int, ...]:
-    return tuple(int(value) for value in tensor.shape)
+    shape = tensor.shape
+    if isinstance(shape, tuple):  # torch.Size: already a tuple of ints
+        return shape
+    return tuple(int(value) for value in shape)
 
 
 def _tensor_descriptor(tensor: Any) -> dict[str, Any]:

@@ -355,7 +355,7 @@ def main() -> int:
     c2 = bench_decode(torch, ops, lib, batch=16, ctx=8192, hq=32, hkv=8, d=128,
                       dtype=torch.float16, gate=False, steps=steps, warmup=warmup, seed=2)
     extra = {}
-    wl = set() if args.only_headline else set(args.workloads.split(","))
+    wl = set(args.workloads.split(",")) if not args.only_headline or "--workloads" in " ".join(sys.argv) else set()
     if "c4" in wl:
         c4 = bench_decode(torch, ops, lib, batch=4, ctx=32768, hq=16, hkv=2, d=256,
                           dtype=torch.bfloat16, gate=True, steps=steps, warmup=warmup, seed=4)
