@@ -18,7 +18,9 @@
 //    16x16 forward substitution plus block recursion; Ub = T diag(beta);
 //    W = T diag(beta exp(Gc)) K.  K K^T and Q K^T run on bf16 MFMA (exact
 //    products of bf16 inputs, fp32 sums); W on bf16 MFMA with T split into
-//    hi + lo bf16 parts.
+//    hi + lo bf16 parts.  Ub, M and W are stored already split into hi and
+//    lo bf16 planes (the same bytes as fp32), Gc in base 2, so phase B
+//    loads MFMA operands directly.
 //  phase B, gdn_apply, one block per (sequence, head, 16 state rows),
 //    sequential over chunks with the 16 x Dk state slice resident in LDS:
 //    Delta = Ub V - W S^T;  O = (diag(exp Gc) Q S^T + M Delta) / sqrt(Dk);
@@ -184,6 +186,40 @@ __device__ __forceinline__ int tr_slot(int quad, int j) { return 16 * (j >> 2) +
 
 __host__ __device__ inline int64_t ws_per_chunk(int Dk) { return kC + 2 * kC * kC + (int64_t)kC * Dk; }
 
+// Per-chunk workspace, in order: Gc * log2(e) [kC] fp32, then hi and lo bf16
+// planes of Ub [kC x kC], M [kC x kC] and W [kC x Dk].  Ub's columns are
+// stored in operand order: position 32 ks + 8 quad + j of a row holds
+// column 32 ks + tr_slot(quad, j), so one 16-byte load gives a lane its
+// A operand for the transposing read of V.
+struct ChunkWs {
+  float* g;
+  bf16_t *u_hi, *u_lo, *m_hi, *m_lo, *w_hi, *w_lo;
+};
+
+__device__ __forceinline__ ChunkWs chunk_ws(float* base, int dk) {
+  ChunkWs w;
+  w.g = base;
+  w.u_hi = (bf16_t*)(base + kC);
+  w.u_lo = w.u_hi + kC * kC;
+  w.m_hi = w.u_lo + kC * kC;
+  w.m_lo = w.m_hi + kC * kC;
+  w.w_hi = w.m_lo + kC * kC;
+  w.w_lo = w.w_hi + kC * dk;
+  return w;
+}
+
+// Column i of Ub -> its position in the operand-ordered row.
+__device__ __forceinline__ int u_pos(int i) {
+  const int ks = i >> 5, r = i & 31;
+  return 32 * ks + 8 * ((r & 15) >> 2) + 4 * (r >> 4) + (r & 3);
+}
+
+__device__ __forceinline__ void store_split(bf16_t* hi, bf16_t* lo, int idx, float v) {
+  const bf16_t h = static_cast<bf16_t>(v);
+  hi[idx] = h;
+  lo[idx] = static_cast<bf16_t>(v - static_cast<float>(h));
+}
+
 // ------------------------------------------------------------ phase A
 
 template <int DK>
@@ -235,12 +271,8 @@ gdn_prep(GdnArgs a) {
   }
   __syncthreads();
 
-  float* ws = a.ws + (((int64_t)b * a.Hv + h) * a.nchunks + c) * ws_per_chunk(DK);
-  float* wG = ws;
-  float* wU = ws + kC;
-  float* wM = wU + kC * kC;
-  float* wW = wM + kC * kC;
-  if (tid < kC) wG[tid] = Gs[tid];
+  const ChunkWs out = chunk_ws(a.ws + (((int64_t)b * a.Hv + h) * a.nchunks + c) * ws_per_chunk(DK), DK);
+  if (tid < kC) out.g[tid] = Gs[tid] * 1.4426950408889634f;
 
   // K K^T and Q K^T: wave w computes rows 16w..16w+15.
   {
@@ -266,7 +298,7 @@ gdn_prep(GdnArgs a) {
         const int i = 16 * ib + hl;
         const float dec = i <= t ? expf(Gs[t] - Gs[i]) : 0.f;
         Bm[t * kF + i] = i < t ? Bs[t] * dec * kk[ib][r] : 0.f;
-        wM[t * kC + i] = dec * qk[ib][r];
+        store_split(out.m_hi, out.m_lo, t * kC + i, dec * qk[ib][r]);
       }
     }
   }
@@ -329,7 +361,7 @@ gdn_prep(GdnArgs a) {
   // Ub = T diag(beta)
   for (int idx = tid; idx < kC * kC; idx += 256) {
     const int t = idx / kC, i = idx - (idx / kC) * kC;
-    wU[idx] = Tm[t * kF + i] * Bs[i];
+    store_split(out.u_hi, out.u_lo, t * kC + u_pos(i), Tm[t * kF + i] * Bs[i]);
   }
   // W = T diag(beta exp(Gc)) K: wave w computes rows 16w..16w+15.
   {
@@ -358,7 +390,8 @@ gdn_prep(GdnArgs a) {
         acc = mfma16x16x32(alo[ks], kb, acc);
       }
 #pragma unroll
-      for (int r = 0; r < 4; ++r) wW[(16 * wave + 4 * quad + r) * DK + 16 * nb + hl] = acc[r];
+      for (int r = 0; r < 4; ++r)
+        store_split(out.w_hi, out.w_lo, (16 * wave + 4 * quad + r) * DK + 16 * nb + hl, acc[r]);
     }
   }
 }
@@ -389,9 +422,9 @@ struct ApplyIn {
   bf16x8 k[kUnitsPerThread], q[kUnitsPerThread];
   bf16x8 v;
   float g;
-  float w[DK / 32][8];
-  float u[2][8];
-  float m[2][8];
+  bf16x8 w_hi[DK / 32], w_lo[DK / 32];
+  bf16x8 u_hi[2], u_lo[2];
+  bf16x8 m_hi[2], m_lo[2];
 };
 
 template <typename TO, int DK>
@@ -453,32 +486,19 @@ gdn_apply(GdnArgs a) {
                                              a.Dv + r0 + 8 * half);
       in.v = t0 + t < a.T ? vv : (bf16x8){};
     }
-    const float* ws = a.ws + (bh * a.nchunks + c) * ws_per_chunk(DK);
-    const float* wU = ws + kC;
-    const float* wM = wU + kC * kC;
-    const float* wW = wM + kC * kC;
-    in.g = ws[tid & (kC - 1)];
+    const ChunkWs w = chunk_ws(a.ws + (bh * a.nchunks + c) * ws_per_chunk(DK), DK);
+    in.g = w.g[tid & (kC - 1)];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      const f32x4 x0 = *(const f32x4*)(wW + trow * DK + 32 * ks + 8 * quad);
-      const f32x4 x1 = *(const f32x4*)(wW + trow * DK + 32 * ks + 8 * quad + 4);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        in.w[ks][j] = x0[j];
-        in.w[ks][4 + j] = x1[j];
-      }
+      in.w_hi[ks] = *(const bf16x8*)(w.w_hi + trow * DK + 32 * ks + 8 * quad);
+      in.w_lo[ks] = *(const bf16x8*)(w.w_lo + trow * DK + 32 * ks + 8 * quad);
     }
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) in.u[ks][j] = wU[trow * kC + 32 * ks + tr_slot(quad, j)];
-      const f32x4 x0 = *(const f32x4*)(wM + trow * kC + 32 * ks + 8 * quad);
-      const f32x4 x1 = *(const f32x4*)(wM + trow * kC + 32 * ks + 8 * quad + 4);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        in.m[ks][j] = x0[j];
-        in.m[ks][4 + j] = x1[j];
-      }
+      in.u_hi[ks] = *(const bf16x8*)(w.u_hi + trow * kC + 32 * ks + 8 * quad);
+      in.u_lo[ks] = *(const bf16x8*)(w.u_lo + trow * kC + 32 * ks + 8 * quad);
+      in.m_hi[ks] = *(const bf16x8*)(w.m_hi + trow * kC + 32 * ks + 8 * quad);
+      in.m_lo[ks] = *(const bf16x8*)(w.m_lo + trow * kC + 32 * ks + 8 * quad);
     }
   };
 
@@ -508,22 +528,18 @@ gdn_apply(GdnArgs a) {
     f32x4 ws_acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      bf16x8 whi, wlo;
-      split8(cur.w[ks], whi, wlo);
-      ws_acc = mfma16x16x32(whi, shi[ks], ws_acc);
-      ws_acc = mfma16x16x32(whi, slo[ks], ws_acc);
-      ws_acc = mfma16x16x32(wlo, shi[ks], ws_acc);
+      ws_acc = mfma16x16x32(cur.w_hi[ks], shi[ks], ws_acc);
+      ws_acc = mfma16x16x32(cur.w_hi[ks], slo[ks], ws_acc);
+      ws_acc = mfma16x16x32(cur.w_lo[ks], shi[ks], ws_acc);
     }
     f32x4 uv = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      bf16x8 uhi, ulo;
-      split8(cur.u[ks], uhi, ulo);
       const bf16x4 v0 = lds_read_tr4(Vs + (32 * ks + tr_row) * 24 + tr_col);
       const bf16x4 v1 = lds_read_tr4(Vs + (32 * ks + 16 + tr_row) * 24 + tr_col);
       const bf16x8 vb = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
-      uv = mfma16x16x32(uhi, vb, uv);
-      uv = mfma16x16x32(ulo, vb, uv);
+      uv = mfma16x16x32(cur.u_hi[ks], vb, uv);
+      uv = mfma16x16x32(cur.u_lo[ks], vb, uv);
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r)
@@ -542,23 +558,22 @@ gdn_apply(GdnArgs a) {
     f32x4 md = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      bf16x8 mhi, mlo, dhi, dlo;
-      split8(cur.m[ks], mhi, mlo);
+      bf16x8 dhi, dlo;
       split8(Dt + hl * kDF + 32 * ks + 8 * quad, dhi, dlo);
-      md = mfma16x16x32(mhi, dhi, md);
-      md = mfma16x16x32(mhi, dlo, md);
-      md = mfma16x16x32(mlo, dhi, md);
+      md = mfma16x16x32(cur.m_hi[ks], dhi, md);
+      md = mfma16x16x32(cur.m_hi[ks], dlo, md);
+      md = mfma16x16x32(cur.m_lo[ks], dhi, md);
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int t = 16 * wave + 4 * quad + r;
       if (t0 + t < a.T) {
-        const float o = (expf(Gs[t]) * qs[r] + md[r]) * a.scale;
+        const float o = (fast_exp2(Gs[t]) * qs[r] + md[r]) * a.scale;
         ((TO*)a.out)[(((int64_t)b * a.T + t0 + t) * a.Hv + h) * a.Dv + r0 + hl] = from_f32<TO>(o);
       }
     }
 
-    // (3) S <- exp(Gc_last) S + (diag(exp(Gc_last - Gc)) Delta)^T K
+    // (3) S <- exp(Gc_last) S + (diag(exp(Gc_last - Gc)) Delta)^T K  (Gs is in base 2)
     const float glast = Gs[kC - 1];
     bf16x8 dthi[2], dtlo[2];
 #pragma unroll
@@ -567,11 +582,11 @@ gdn_apply(GdnArgs a) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int t = 32 * ks + tr_slot(quad, j);
-        x[j] = Dt[hl * kDF + t] * expf(glast - Gs[t]);
+        x[j] = Dt[hl * kDF + t] * fast_exp2(glast - Gs[t]);
       }
       split8(x, dthi[ks], dtlo[ks]);
     }
-    const float gl = expf(glast);
+    const float gl = fast_exp2(glast);
 #pragma unroll
     for (int nq = 0; nq < DK / 64; ++nq) {
       const int nb = wave + 4 * nq;
