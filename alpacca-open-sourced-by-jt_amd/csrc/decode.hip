@@ -74,9 +74,15 @@ __device__ __forceinline__ void wave_sync_lds() {
 // ------------------------------------------------------------ MFMA split
 
 // One block = 4 wavefronts sharing one chunk of rows of one (sequence, kv
-// head, 16-head column block).  Wave w takes the 32-row tiles w, w+4, ...;
-// the next tile's K/V loads are issued before the current tile's softmax and
-// PV so every wave keeps a tile in flight.  At the end the four waves' online
+// head, 16-head column block).  Wave w takes the 32-row tiles w, w+4, ...
+// K and V rows are fetched row-major (16 lanes cover one 256-byte row at
+// head_dim 128), so every 128-byte line is consumed by the instruction that
+// fetches it; both tiles are staged in the wave's LDS slot, K read back as
+// MFMA A operands, V with transposing reads.  V loads carry the nontemporal
+// hint (V is read once per step); measured on C2, the hint on V alone gives
+// the best rate, and adding it to K lowers it.
+// The next tile's loads are issued as soon as the current tile is staged,
+// so every wave keeps a tile in flight.  At the end the four waves' online
 // softmax states are merged through LDS into one partial per block.
 template <typename T, int D>
 __global__ void __launch_bounds__(256)
@@ -85,11 +91,11 @@ decode_split_mfma(DecodeArgs a) {
   typedef typename Vec4<T>::type V4;
   constexpr int kStride = D + 8;          // LDS row stride (elements), 16-byte aligned rows
   constexpr int kUnits = D / 8;           // 16-byte units per row
-  constexpr int kVIters = kTile * kUnits / 64;
+  constexpr int kIters = kTile * kUnits / 64;
   constexpr int kTileElems = kTile * kStride;
   constexpr int kMergeO = (kWaves - 1) * (D / 16) * 64 * 4;   // floats
   constexpr int kMergeFloats = kMergeO + 2 * (kWaves - 1) * 64;
-  constexpr int kTileBytes = kWaves * kTileElems * (int)sizeof(T);
+  constexpr int kTileBytes = 2 * kWaves * kTileElems * (int)sizeof(T);
   constexpr int kLdsBytes = kTileBytes > kMergeFloats * 4 ? kTileBytes : kMergeFloats * 4;
   __shared__ __attribute__((aligned(16))) char smem[kLdsBytes];
 
@@ -125,29 +131,22 @@ decode_split_mfma(DecodeArgs a) {
   float m = -INFINITY;
   float l = 0.f;
 
-  const T* kbase = (const T*)a.k + (int64_t)b * a.ks_b + (int64_t)kvh * a.ks_h + 8 * quad;
+  const T* kbase = (const T*)a.k + (int64_t)b * a.ks_b + (int64_t)kvh * a.ks_h;
   const T* vbase = (const T*)a.v + (int64_t)b * a.vs_b + (int64_t)kvh * a.vs_h;
-  T* lds = (T*)smem + wave * kTileElems;
+  T* ldsk = (T*)smem + 2 * wave * kTileElems;
+  T* ldsv = ldsk + kTileElems;
 
-  V8 kr[2][D / 32];   // K rows -> A operand: K[p0 + 16 blk + hl][32 ks + 8 quad + 0..7]
-  V8 vr[kVIters];     // V rows, 16 bytes per lane, row-major
+  V8 kr[kIters];  // K rows, 16 bytes per lane, row-major
+  V8 vr[kIters];  // V rows, same layout
   auto load_tile = [&](int p) {
 #pragma unroll
-    for (int blk = 0; blk < 2; ++blk) {
-      const T* row = kbase + (int64_t)min(p + 16 * blk + hl, last) * a.ks_pos;
-#pragma unroll
-      for (int ks = 0; ks < D / 32; ++ks) kr[blk][ks] = *(const V8*)(row + 32 * ks);
-    }
-#pragma unroll
-    for (int it = 0; it < kVIters; ++it) {
+    for (int it = 0; it < kIters; ++it) {
       const int u = it * 64 + lane;
       const int r = u / kUnits;
       const int c = u - r * kUnits;
-      // V rows are read once per step: a nontemporal load keeps them from
-      // displacing K lines and queries in L2 (measured: +15% step rate at
-      // D=128, neutral at D=256; the same hint on K loads is slower).
-      vr[it] = __builtin_nontemporal_load(
-          (const V8*)(vbase + (int64_t)min(p + r, last) * a.vs_pos + 8 * c));
+      const int row = min(p + r, last);
+      kr[it] = *(const V8*)(kbase + (int64_t)row * a.ks_pos + 8 * c);
+      vr[it] = __builtin_nontemporal_load((const V8*)(vbase + (int64_t)row * a.vs_pos + 8 * c));
     }
   };
 
@@ -155,23 +154,28 @@ decode_split_mfma(DecodeArgs a) {
   if (p0 < end) load_tile(p0);
   while (p0 < end) {
     const int pn = p0 + kTile * kWaves;
+    // Stage K and V in LDS (row-major, padded rows), then prefetch the next tile.
+#pragma unroll
+    for (int it = 0; it < kIters; ++it) {
+      const int u = it * 64 + lane;
+      const int r = u / kUnits;
+      const int c = u - r * kUnits;
+      *(V8*)(ldsk + r * kStride + 8 * c) = kr[it];
+      *(V8*)(ldsv + r * kStride + 8 * c) = vr[it];
+    }
+    if (pn < end) load_tile(pn);
+    wave_sync_lds();
     // Scores for 32 rows x 16 heads: lane holds S[pos = p0 + 16 blk + 4 quad + i][hl].
     f32x4 s[2];
 #pragma unroll
     for (int blk = 0; blk < 2; ++blk) {
       s[blk] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ks = 0; ks < D / 32; ++ks) s[blk] = mfma16x16x32(kr[blk][ks], qv[ks], s[blk]);
+      for (int ks = 0; ks < D / 32; ++ks) {
+        const V8 ka = *(const V8*)(ldsk + (16 * blk + hl) * kStride + 32 * ks + 8 * quad);
+        s[blk] = mfma16x16x32(ka, qv[ks], s[blk]);
+      }
     }
-    // Stage V in LDS (row-major, padded rows), then prefetch the next tile.
-#pragma unroll
-    for (int it = 0; it < kVIters; ++it) {
-      const int u = it * 64 + lane;
-      const int r = u / kUnits;
-      const int c = u - r * kUnits;
-      *(V8*)(lds + r * kStride + 8 * c) = vr[it];
-    }
-    if (pn < end) load_tile(pn);
     // Online softmax (base 2).  Slot j of this lane is row 16 (j/4) + 4 quad + j%4.
     float sv[8];
     float mx = -INFINITY;
@@ -198,15 +202,14 @@ decode_split_mfma(DecodeArgs a) {
     m = mn;
 #pragma unroll
     for (int mb = 0; mb < D / 16; ++mb) o[mb] *= alpha;
-    wave_sync_lds();
     // O^T += V^T P^T.  A operand: lane holds V[row(quad, j)][16 mb + hl], j = 0..7,
     // gathered with two transposing reads of 4 rows (16 h + 4 quad + 0..3) each.
     const int tr_row = 4 * quad + (hl >> 2);
     const int tr_col = 4 * (hl & 3);
 #pragma unroll
     for (int mb = 0; mb < D / 16; ++mb) {
-      const V4 lo = lds_read_tr4(lds + tr_row * kStride + 16 * mb + tr_col);
-      const V4 hi = lds_read_tr4(lds + (16 + tr_row) * kStride + 16 * mb + tr_col);
+      const V4 lo = lds_read_tr4(ldsv + tr_row * kStride + 16 * mb + tr_col);
+      const V4 hi = lds_read_tr4(ldsv + (16 + tr_row) * kStride + 16 * mb + tr_col);
       const V8 va = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
       o[mb] = mfma16x16x32(va, pv, o[mb]);
     }
