@@ -55,6 +55,10 @@ template <> struct Vec4<f16_t> { typedef f16x4 type; };
 template <> struct Vec4<bf16_t> { typedef bf16x4 type; };
 template <> struct Vec4<float> { typedef f32x4 type; };
 
+// 16x16x4 fp32: lane l supplies A[l % 16][l / 16] and B[l / 16][l % 16].
+__device__ __forceinline__ f32x4 mfma16x16x4(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
 __device__ __forceinline__ f32x4 mfma16x16x32(f16x8 a, f16x8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }

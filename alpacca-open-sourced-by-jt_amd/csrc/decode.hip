@@ -39,6 +39,8 @@ constexpr int kTile = 32;   // rows per wavefront step (MFMA path)
 constexpr int kWaves = 4;   // wavefronts (= slots) per block (MFMA path)
 constexpr int kGenericTile = 64;
 constexpr int kMaxSlots = 2048;
+// Wave tile rows of the fp32 MFMA split kernel.
+constexpr int f32_tile_rows(int d) { return d == 64 ? 32 : 16; }
 constexpr int kMaxResident = 8192;  // upper bound on resident blocks any plan assumes
 
 
@@ -71,6 +73,69 @@ __device__ __forceinline__ void wave_sync_lds() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// End of a split block: merge the four waves' online-softmax states (same
+// lane layout: O^T[d = 16 mb + 4 quad + i][head hl]) through LDS into wave
+// 0, which writes the block's partial (m, l, acc) for its live heads.
+template <int D>
+__device__ __forceinline__ void merge_waves(const DecodeArgs& a, char* smem, f32x4 (&o)[D / 16],
+                                            float m, float l, int wave, int lane, bool head_ok,
+                                            int b, int h) {
+  constexpr int kMergeO = (kWaves - 1) * (D / 16) * 64 * 4;   // floats
+  const int quad = lane >> 4;
+  l += __shfl_xor(l, 16);
+  l += __shfl_xor(l, 32);
+  __syncthreads();
+  float* mf = (float*)smem;
+  float* mm = mf + kMergeO;
+  float* ml = mm + (kWaves - 1) * 64;
+  if (wave > 0) {
+#pragma unroll
+    for (int mb = 0; mb < D / 16; ++mb)
+      *(f32x4*)(mf + (((wave - 1) * (D / 16) + mb) * 64 + lane) * 4) = o[mb];
+    mm[(wave - 1) * 64 + lane] = m;
+    ml[(wave - 1) * 64 + lane] = l;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    float mw[kWaves - 1];
+    float M = m;
+#pragma unroll
+    for (int w = 0; w < kWaves - 1; ++w) {
+      mw[w] = mm[w * 64 + lane];
+      M = fmaxf(M, mw[w]);
+    }
+    const bool any = M != -INFINITY;
+    const float c0 = any ? fast_exp2(m - M) : 0.f;
+    float L = l * c0;
+#pragma unroll
+    for (int mb = 0; mb < D / 16; ++mb) o[mb] *= c0;
+#pragma unroll
+    for (int w = 0; w < kWaves - 1; ++w) {
+      const float cw = any ? fast_exp2(mw[w] - M) : 0.f;
+      L += ml[w * 64 + lane] * cw;
+#pragma unroll
+      for (int mb = 0; mb < D / 16; ++mb)
+        o[mb] += cw * *(const f32x4*)(mf + ((w * (D / 16) + mb) * 64 + lane) * 4);
+    }
+    if (head_ok) {
+      const int64_t pidx = ((int64_t)b * a.q_heads + h) * a.nsplit + blockIdx.x;
+      if (quad == 0) {
+        a.part_m[pidx] = M;
+        a.part_l[pidx] = L;
+      }
+      float* pa = a.part_acc + pidx * D + 4 * quad;
+#pragma unroll
+      for (int mb = 0; mb < D / 16; ++mb) *(f32x4*)(pa + 16 * mb) = o[mb];
+    }
+  }
+}
+
+// Bytes of LDS a split block needs for the final merge.
+template <int D>
+constexpr int merge_lds_bytes() {
+  return 4 * ((kWaves - 1) * (D / 16) * 64 * 4 + 2 * (kWaves - 1) * 64);
+}
+
 // ------------------------------------------------------------ MFMA split
 
 // One block = 4 wavefronts sharing one chunk of rows of one (sequence, kv
@@ -93,10 +158,8 @@ decode_split_mfma(DecodeArgs a) {
   constexpr int kUnits = D / 8;           // 16-byte units per row
   constexpr int kIters = kTile * kUnits / 64;
   constexpr int kTileElems = kTile * kStride;
-  constexpr int kMergeO = (kWaves - 1) * (D / 16) * 64 * 4;   // floats
-  constexpr int kMergeFloats = kMergeO + 2 * (kWaves - 1) * 64;
   constexpr int kTileBytes = 2 * kWaves * kTileElems * (int)sizeof(T);
-  constexpr int kLdsBytes = kTileBytes > kMergeFloats * 4 ? kTileBytes : kMergeFloats * 4;
+  constexpr int kLdsBytes = kTileBytes > merge_lds_bytes<D>() ? kTileBytes : merge_lds_bytes<D>();
   __shared__ __attribute__((aligned(16))) char smem[kLdsBytes];
 
   const int lane = threadIdx.x & 63;
@@ -217,53 +280,145 @@ decode_split_mfma(DecodeArgs a) {
     p0 = pn;
   }
 
-  // Merge the four waves' states (same lane layout) into wave 0.
-  l += __shfl_xor(l, 16);
-  l += __shfl_xor(l, 32);
-  __syncthreads();
-  float* mf = (float*)smem;
-  float* mm = mf + kMergeO;
-  float* ml = mm + (kWaves - 1) * 64;
-  if (wave > 0) {
+  merge_waves<D>(a, smem, o, m, l, wave, lane, head_ok, b, h);
+}
+
+// fp32 caches: the same split structure on v_mfma_f32_16x16x4_f32 (fp32
+// products and sums; P stays fp32).  A wave tile is R rows (32 at head_dim
+// 64, 16 above, so two blocks' K and V tiles fit one CU's LDS at head_dim
+// 64 and 128).  Both reductions run in a permuted order that lets each lane
+// feed the values it already holds:
+//   S^T = K Q^T, k-step (g, j): lane (hl, quad) supplies K[row hl][16 g +
+//     4 quad + j] (one 16-byte LDS read per g) and Q[head hl][same d];
+//   O^T = V^T P^T, k-step (blk, i): lane supplies P[16 blk + 4 quad + i]
+//     [head hl] (its own score slot) and V[that row][16 mb + hl].
+template <int D, int R>
+__global__ void __launch_bounds__(256)
+decode_split_f32(DecodeArgs a) {
+  constexpr int kStride = D + 4;  // floats: rows 4 apart sit 16 banks apart
+  constexpr int kUnits = D / 4;   // 16-byte units per row
+  constexpr int kIters = R * kUnits / 64;
+  constexpr int kTileElems = R * kStride;
+  constexpr int NB = R / 16;
+  constexpr int kTileBytes = 2 * kWaves * kTileElems * 4;
+  constexpr int kLdsBytes = kTileBytes > merge_lds_bytes<D>() ? kTileBytes : merge_lds_bytes<D>();
+  static_assert(kIters >= 1 && R * kUnits % 64 == 0, "tile must split evenly over a wave");
+  __shared__ __attribute__((aligned(16))) char smem[kLdsBytes];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int b = blockIdx.z;
+  const int hc = blockIdx.y % a.head_chunks;
+  const int kvh = blockIdx.y / a.head_chunks;
+  const int len = seq_len(a, b);
+  const int start = max(blockIdx.x * a.chunk, seq_lo(a, b, len));
+  const int end = min(blockIdx.x * a.chunk + a.chunk, len);
+  const int last = end - 1;
+  const int hl = lane & 15;
+  const int quad = lane >> 4;
+  const int g_in = hc * 16 + hl;
+  const bool head_ok = g_in < a.group;
+  const int h = kvh * a.group + (head_ok ? g_in : 0);
+
+  f32x4 qv[D / 16];  // Q[h][16 g + 4 quad + 0..3]
+  {
+    const float* qp = (const float*)a.q + ((int64_t)b * a.q_heads + h) * D + 4 * quad;
+#pragma unroll
+    for (int g = 0; g < D / 16; ++g) {
+      const f32x4 x = *(const f32x4*)(qp + 16 * g);
+      qv[g] = head_ok ? x : (f32x4){0.f, 0.f, 0.f, 0.f};
+    }
+  }
+  f32x4 o[D / 16];
+#pragma unroll
+  for (int mb = 0; mb < D / 16; ++mb) o[mb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY;
+  float l = 0.f;
+
+  const float* kbase = (const float*)a.k + (int64_t)b * a.ks_b + (int64_t)kvh * a.ks_h;
+  const float* vbase = (const float*)a.v + (int64_t)b * a.vs_b + (int64_t)kvh * a.vs_h;
+  float* ldsk = (float*)smem + 2 * wave * kTileElems;
+  float* ldsv = ldsk + kTileElems;
+
+  f32x4 kr[kIters], vr[kIters];
+  auto load_tile = [&](int p) {
+#pragma unroll
+    for (int it = 0; it < kIters; ++it) {
+      const int u = it * 64 + lane;
+      const int r = u / kUnits;
+      const int c = u - r * kUnits;
+      const int row = min(p + r, last);
+      kr[it] = *(const f32x4*)(kbase + (int64_t)row * a.ks_pos + 4 * c);
+      vr[it] = __builtin_nontemporal_load((const f32x4*)(vbase + (int64_t)row * a.vs_pos + 4 * c));
+    }
+  };
+
+  int p0 = start + R * wave;
+  if (p0 < end) load_tile(p0);
+  while (p0 < end) {
+    const int pn = p0 + R * kWaves;
+#pragma unroll
+    for (int it = 0; it < kIters; ++it) {
+      const int u = it * 64 + lane;
+      const int r = u / kUnits;
+      const int c = u - r * kUnits;
+      *(f32x4*)(ldsk + r * kStride + 4 * c) = kr[it];
+      *(f32x4*)(ldsv + r * kStride + 4 * c) = vr[it];
+    }
+    if (pn < end) load_tile(pn);
+    wave_sync_lds();
+    // lane holds S[pos = p0 + 16 blk + 4 quad + i][hl]
+    f32x4 s[NB];
+#pragma unroll
+    for (int blk = 0; blk < NB; ++blk) {
+      s[blk] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int g = 0; g < D / 16; ++g) {
+        const f32x4 ka = *(const f32x4*)(ldsk + (16 * blk + hl) * kStride + 16 * g + 4 * quad);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) s[blk] = mfma16x16x4(ka[j], qv[g][j], s[blk]);
+      }
+    }
+    float sv[NB][4];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int blk = 0; blk < NB; ++blk)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int pos = p0 + 16 * blk + 4 * quad + i;
+        const float x = pos < end ? s[blk][i] * a.scale_log2 : -INFINITY;
+        sv[blk][i] = x;
+        mx = fmaxf(mx, x);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float mn = fmaxf(m, mx);  // finite: every tile holds at least one live row
+    const float alpha = fast_exp2(m - mn);
+    float ps = 0.f;
+#pragma unroll
+    for (int blk = 0; blk < NB; ++blk)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sv[blk][i] = fast_exp2(sv[blk][i] - mn);
+        ps += sv[blk][i];
+      }
+    l = l * alpha + ps;
+    m = mn;
+#pragma unroll
+    for (int mb = 0; mb < D / 16; ++mb) o[mb] *= alpha;
 #pragma unroll
     for (int mb = 0; mb < D / 16; ++mb)
-      *(f32x4*)(mf + (((wave - 1) * (D / 16) + mb) * 64 + lane) * 4) = o[mb];
-    mm[(wave - 1) * 64 + lane] = m;
-    ml[(wave - 1) * 64 + lane] = l;
+#pragma unroll
+      for (int blk = 0; blk < NB; ++blk)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float va = ldsv[(16 * blk + 4 * quad + i) * kStride + 16 * mb + hl];
+          o[mb] = mfma16x16x4(va, sv[blk][i], o[mb]);
+        }
+    wave_sync_lds();
+    p0 = pn;
   }
-  __syncthreads();
-  if (wave == 0) {
-    float mw[kWaves - 1];
-    float M = m;
-#pragma unroll
-    for (int w = 0; w < kWaves - 1; ++w) {
-      mw[w] = mm[w * 64 + lane];
-      M = fmaxf(M, mw[w]);
-    }
-    const bool any = M != -INFINITY;
-    const float c0 = any ? fast_exp2(m - M) : 0.f;
-    float L = l * c0;
-#pragma unroll
-    for (int mb = 0; mb < D / 16; ++mb) o[mb] *= c0;
-#pragma unroll
-    for (int w = 0; w < kWaves - 1; ++w) {
-      const float cw = any ? fast_exp2(mw[w] - M) : 0.f;
-      L += ml[w * 64 + lane] * cw;
-#pragma unroll
-      for (int mb = 0; mb < D / 16; ++mb)
-        o[mb] += cw * *(const f32x4*)(mf + ((w * (D / 16) + mb) * 64 + lane) * 4);
-    }
-    if (head_ok) {
-      const int64_t pidx = ((int64_t)b * a.q_heads + h) * a.nsplit + blockIdx.x;
-      if (quad == 0) {
-        a.part_m[pidx] = M;
-        a.part_l[pidx] = L;
-      }
-      float* pa = a.part_acc + pidx * D + 4 * quad;
-#pragma unroll
-      for (int mb = 0; mb < D / 16; ++mb) *(f32x4*)(pa + 16 * mb) = o[mb];
-    }
-  }
+  merge_waves<D>(a, smem, o, m, l, wave, lane, head_ok, b, h);
 }
 
 // ------------------------------------------------------------ generic split
@@ -501,6 +656,12 @@ const void* split_kernel(bool mfma, int D) {
         case 128: return (const void*)decode_split_mfma<T, 128>;
         case 256: return (const void*)decode_split_mfma<T, 256>;
       }
+    } else {
+      switch (D) {
+        case 64: return (const void*)decode_split_f32<64, f32_tile_rows(64)>;
+        case 128: return (const void*)decode_split_f32<128, f32_tile_rows(128)>;
+        case 256: return (const void*)decode_split_f32<256, f32_tile_rows(256)>;
+      }
     }
     return nullptr;
   }
@@ -561,20 +722,21 @@ int run_decode(DecodeArgs a, int dtype, int out_dtype, void* workspace, size_t w
                           (uintptr_t)(a.ks_h * es) | (uintptr_t)(a.vs_pos * es) |
                           (uintptr_t)(a.vs_b * es) | (uintptr_t)(a.vs_h * es);
   const int D = a.key_dim;
-  const bool mfma = dtype != ALPX_F32 && D == a.value_dim && (D == 64 || D == 128 || D == 256) &&
-                    (align & 15) == 0 && getenv("ALPX_DECODE_GENERIC") == nullptr;
+  const bool mfma = D == a.value_dim && (D == 64 || D == 128 || D == 256) && (align & 15) == 0 &&
+                    getenv("ALPX_DECODE_GENERIC") == nullptr;
   const size_t need = decode_workspace(a.batch, a.q_heads, a.kv_heads, a.value_dim, a.length);
   if (workspace_bytes < need)
     return fail(ALPX_EINVAL, "decode workspace holds %zu bytes, needs %zu", workspace_bytes,
                 need);
   const void* kernel = nullptr;
   switch (dtype) {
-    case ALPX_F32: kernel = split_kernel<float>(false, D); break;
+    case ALPX_F32: kernel = split_kernel<float>(mfma, D); break;
     case ALPX_F16: kernel = split_kernel<f16_t>(mfma, D); break;
     default: kernel = split_kernel<bf16_t>(mfma, D); break;
   }
   if (kernel == nullptr) return fail(ALPX_EUNSUPPORTED, "decode: no kernel for this shape");
-  const int unit = mfma ? kTile * kWaves : kGenericTile;
+  const int unit =
+      !mfma ? kGenericTile : (dtype == ALPX_F32 ? f32_tile_rows(D) : kTile) * kWaves;
   a.head_chunks = (a.group + 15) / 16;
   const Plan p = plan_split(a.batch * a.kv_heads * a.head_chunks, a.length,
                             resident_blocks(kernel, mfma ? 256 : 64, 0), unit);

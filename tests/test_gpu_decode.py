@@ -121,6 +121,24 @@ def test_c2_decode_fp16_ragged(gpu, ops, uniform):
     assert out.dtype == torch.float16 and err <= TOL["f16"], err
 
 
+@pytest.mark.parametrize("d,hq,hkv", [(128, 16, 4), (256, 8, 2), (64, 32, 8)])
+def test_decode_fp32_ragged_long(gpu, ops, d, hq, hkv):
+    # fp32 caches (the reference's own dtype) at split-K lengths: many
+    # partials per head, ragged lengths including a 1-row sequence
+    import torch
+    rng = np.random.default_rng(d + hq)
+    B, C = 4, 3000
+    q = rng.standard_normal((B, hq, d)).astype(np.float32)
+    K = rng.standard_normal((C, B, hkv, d)).astype(np.float32)
+    V = rng.standard_normal((C, B, hkv, d)).astype(np.float32)
+    lens = np.array([3000, 1, 1777, 2048], dtype=np.int32)
+    out = ops.online_attention(_dev(torch, q, "f32", gpu), _dev(torch, K, "f32", gpu),
+                               _dev(torch, V, "f32", gpu), length=C, seq_lens=lens.tolist())
+    ref = A.online_attention(q, K, V, C, seq_lens=lens)
+    err = np.abs(out.cpu().numpy() - ref).max()
+    assert out.dtype == torch.float32 and err <= TOL["f32"], err
+
+
 def test_c2_decode_fp16_full_size(gpu, ops):
     import torch
     c = I.c2_decode_fp16()
