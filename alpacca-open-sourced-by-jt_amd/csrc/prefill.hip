@@ -22,6 +22,8 @@
 // window).
 #include <math.h>
 
+#include <type_traits>
+
 #include "alpx_common.h"
 #include "decode_internal.h"
 #include "timing.h"
@@ -73,28 +75,49 @@ __device__ __forceinline__ bool prefill_work(const PrefillArgs& a, int& kvh, int
 // multiplies (64 per tile) are skipped on almost every tile.
 constexpr float kRescale = 8.0f;
 
+// K and V tiles sit unpadded in LDS, written by direct-to-LDS buffer loads
+// (no staging registers, no LDS write instructions).  16-byte unit c of row r
+// is stored at unit c ^ swz(r): the K operand reads (eight consecutive rows,
+// one unit each) and the V transposing reads (four consecutive rows, a pair
+// of units each) then touch distinct banks.
+__device__ __forceinline__ int swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+template <int V>
+using Par = std::integral_constant<int, V>;
+
+// Marks a register value as used (and possibly changed) at this point, so
+// the work producing it stays before it (the compiler would otherwise sink
+// register-only work past the block barrier into the next iteration).
+template <typename V>
+__device__ __forceinline__ void pin(V& x) {
+#if defined(__HIP_DEVICE_COMPILE__)  // the "v" constraint exists only for the GPU target
+  asm volatile("" : "+v"(x));
+#else
+  (void)x;
+#endif
+}
+
 template <typename T, typename TO, int D, int BK, int NQB>
 __global__ void __launch_bounds__(256, 2)
 prefill_mfma(PrefillArgs a) {
   typedef typename Vec8<T>::type V8;
   typedef typename Vec4<T>::type V4;
-  // LDS row strides (elements).  K rows are read 16 B per lane, 16 rows at a
-  // time: a 16-byte bank shift per row keeps 8 consecutive rows on distinct
-  // banks.  V rows are read by 4-row transposing reads of 32 B per row: a
-  // 32-byte shift keeps those 4 rows on distinct banks.
-  constexpr int kStride = D + 8;
-  constexpr int kVStride = D + 16;
-  constexpr int kTileElems = BK * kVStride;
-  constexpr int kUnits = D / 8;           // 16-byte units per row
-  constexpr int kUPT = BK * kUnits / 256; // units per thread per tensor per tile
+  constexpr int U = D / 8;                  // 16-byte units per row
+  constexpr int kRowB = D * (int)sizeof(T);
+  constexpr int kTileB = BK * kRowB;        // one K or V tile
+  constexpr int kIW = BK * U / 256;         // direct-load instructions per wave per tile
   constexpr int KB = BK / 16;
   constexpr int KK = BK / 32;
   constexpr int MB = D / 16;
   constexpr int KS = D / 32;
   constexpr int kWaveCols = 16 * NQB;
   constexpr int kCols = 4 * kWaveCols;
-  static_assert(kUPT >= 1 && BK * kUnits % 256 == 0, "tile must split evenly over 256 threads");
-  __shared__ __attribute__((aligned(16))) T smem[4 * kTileElems];
+  static_assert(kIW >= 1 && BK * U % 256 == 0, "tile must split evenly over 4 waves");
+  static_assert(U >= 8, "the row swizzle needs 8 units per row");
+  // K tile buffers at 0 and kTileB, V tile buffers at 2 and 3 kTileB.
+  __shared__ __attribute__((aligned(1024))) char smem[4 * kTileB];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -126,10 +149,14 @@ prefill_mfma(PrefillArgs a) {
   const int wt_first = min(wcol0, cols - 1) / G;
   const int wt_last = (min(wcol0 + kWaveCols, cols) - 1) / G;
 
-  // Key rows [lo, hi) that any column of the block can see.
+  // Key rows [lo, hi) that any column of the block can see, in nt tiles.
   const int hi = max(0, min(a.kv_tokens, rel0 + bt_last + 1));
   int lo = 0;
   if (a.window > 0) lo = min(hi, max(0, rel0 + bt_first - a.window + 1)) / BK * BK;
+  // Every wave walks all nt tiles of the block; keys a wave's columns cannot
+  // see (past its diagonal, before its window) are masked, which costs at
+  // most about one tile per wave and keeps the waves' pipelines in step.
+  const int nt = (hi - lo + BK - 1) / BK;
 
   // B operand of S^T = K Q^T: lane holds Q[column][32 ks + 8 quad + 0..7].
   V8 qv[NQB][KS];
@@ -143,166 +170,220 @@ prefill_mfma(PrefillArgs a) {
     }
   }
 
-  f32x4 o[NQB][MB];  // O^T[d = 16 mb + 4 quad + i][column]
-  float m[NQB], l[NQB];
+  f32x4 o[NQB][MB];   // O^T[d = 16 mb + 4 quad + i][column]
+  f32x4 lsum[NQB];    // row sums of P, accumulated by MFMA (all four entries equal)
+  float m[NQB], pend[NQB];
 #pragma unroll
   for (int qb = 0; qb < NQB; ++qb) {
     m[qb] = -INFINITY;
-    l[qb] = 0.f;
+    pend[qb] = 1.f;
+    lsum[qb] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) o[qb][mb] = (f32x4){0.f, 0.f, 0.f, 0.f};
   }
+  bool pend_any = false;
   const float c2 = a.scale_log2;
   const float thr = kRescale / c2;
+  V8 ones;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ones[j] = from_f32<T>(1.0f);
 
+  // Direct loads: wave-instruction q of a tile fills LDS bytes [1024 q,
+  // 1024 q + 1024), lane L the 16 bytes at 1024 q + 16 L, i.e. row
+  // (64 q + L) / U, stored unit (64 q + L) % U, which holds logical unit
+  // stored ^ swz(row).  Rows at or past kv_tokens read as zero.
+  uint32_t kofs[kIW], vofs[kIW];
+#pragma unroll
+  for (int t = 0; t < kIW; ++t) {
+    const int sl = (wave * kIW + t) * 64 + lane;
+    const int row = sl / U;
+    const int c = (sl % U) ^ swz(row);
+    kofs[t] = (uint32_t)(((int64_t)row * a.ks_pos + 8 * c) * (int64_t)sizeof(T));
+    vofs[t] = (uint32_t)(((int64_t)row * a.vs_pos + 8 * c) * (int64_t)sizeof(T));
+  }
   const T* kg = (const T*)a.k + (int64_t)kvh * D;
   const T* vg = (const T*)a.v + (int64_t)kvh * D;
-  // Tile loads are raw buffer loads: a per-tile scalar resource (base = row
-  // k0) plus per-thread constant byte offsets, so no per-tile vector address
-  // arithmetic.  Rows at or past kv_tokens read as zero (masked anyway).
-  int urow[kUPT];
-  uint32_t kofs[kUPT], vofs[kUPT];
+  auto load_tile = [&](const T* g, int64_t pos, const uint32_t (&ofs)[kIW], int t, int buf) {
+    const int k0 = lo + t * BK;
+    const __amdgpu_buffer_rsrc_t r = buffer_rsrc(
+        g + (int64_t)k0 * pos, (uint32_t)((int64_t)(a.kv_tokens - k0) * pos * (int64_t)sizeof(T)));
+#if defined(__HIP_DEVICE_COMPILE__)  // LDS address-space operands exist only for the GPU target
 #pragma unroll
-  for (int u = 0; u < kUPT; ++u) {
-    const int idx = u * 256 + tid;
-    urow[u] = idx / kUnits;
-    const int c = idx - urow[u] * kUnits;
-    kofs[u] = (uint32_t)((urow[u] * a.ks_pos + 8 * c) * (int64_t)sizeof(T));
-    vofs[u] = (uint32_t)((urow[u] * a.vs_pos + 8 * c) * (int64_t)sizeof(T));
-  }
-  V8 kreg[kUPT], vreg[kUPT];
-  auto gload = [&](int k0) {
-    const uint32_t rows = (uint32_t)(a.kv_tokens - k0);
-    const __amdgpu_buffer_rsrc_t kr =
-        buffer_rsrc(kg + (int64_t)k0 * a.ks_pos, (uint32_t)(rows * a.ks_pos * sizeof(T)));
-    const __amdgpu_buffer_rsrc_t vr =
-        buffer_rsrc(vg + (int64_t)k0 * a.vs_pos, (uint32_t)(rows * a.vs_pos * sizeof(T)));
-#pragma unroll
-    for (int u = 0; u < kUPT; ++u) {
-      kreg[u] = __builtin_bit_cast(V8, __builtin_amdgcn_raw_buffer_load_b128(kr, kofs[u], 0, 0));
-      vreg[u] = __builtin_bit_cast(V8, __builtin_amdgcn_raw_buffer_load_b128(vr, vofs[u], 0, 0));
-    }
-  };
-  auto lstore = [&](int buf) {
-    T* Kd = smem + 2 * buf * kTileElems;
-    T* Vd = Kd + kTileElems;
-#pragma unroll
-    for (int u = 0; u < kUPT; ++u) {
-      const int idx = u * 256 + tid;
-      const int r = urow[u];
-      const int c = idx - r * kUnits;
-      *(V8*)(Kd + r * kStride + 8 * c) = kreg[u];
-      *(V8*)(Vd + r * kVStride + 8 * c) = vreg[u];
-    }
+    for (int i = 0; i < kIW; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          r, (lds_void_t*)(smem + buf * kTileB + (wave * kIW + i) * 1024), 16, ofs[i], 0, 0, 0);
+#else
+    (void)r;
+    (void)ofs;
+#endif
   };
 
-  if (lo < hi) {
-    gload(lo);
-    lstore(0);
-  }
-  __syncthreads();
+  // LDS read offsets.  K operand: row 16 kb + hl, logical unit 4 ks + quad.
+  uint32_t kadr[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) kadr[ks] = hl * kRowB + (((4 * ks + quad) ^ swz(hl & 7)) * 16);
+  // V transposing reads: row 32 kk + 16 h + tr_row, elements 16 mb + 4 (hl & 3)
+  // + 0..3, i.e. logical unit 2 mb + ((hl & 3) >> 1); with mb = 4 x + y the
+  // stored unit is 8 x + ((2 y + cb) ^ swz(tr_row)).
   const int tr_row = 4 * quad + (hl >> 2);
-  const int tr_col = 4 * (hl & 3);
-  int buf = 0;
-  for (int k0 = lo; k0 < hi; k0 += BK) {
-    const bool next = k0 + BK < hi;
-    if (next) gload(k0 + BK);
-    const bool skip = k0 > rel0 + wt_last ||
-                      (a.window > 0 && k0 + BK - 1 <= rel0 + wt_first - a.window);
-    if (!skip) {
-      // The mask is needed only on tiles that straddle a row's diagonal or
-      // window edge, or run past the last row; the branch is wave-uniform.
-      const bool need_mask = k0 + BK - 1 > rel0 + wt_first || k0 + BK > hi ||
-                             (a.window > 0 && k0 <= rel0 + wt_last - a.window);
-      const T* Ks = smem + 2 * buf * kTileElems;
-      const T* Vs = Ks + kTileElems;
-      f32x4 sc[KB][NQB];
+  uint32_t vadr[4];
+#pragma unroll
+  for (int y = 0; y < 4; ++y)
+    vadr[y] = tr_row * kRowB + (((2 * y + ((hl & 3) >> 1)) ^ swz(tr_row & 7)) * 16) + (hl & 1) * 8;
+
+  // Scores (S^T tiles) of two tiles and P operands of two tiles, by parity.
+  f32x4 sc[2][KB][NQB];
+  V8 pv[2][KK][NQB];
+
+  auto qk = [&](auto kpar, auto spar) {
+    constexpr int KP = decltype(kpar)::value, SP = decltype(spar)::value;
+    const char* kb0 = smem + KP * kTileB;
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+      for (int qb = 0; qb < NQB; ++qb) sc[SP][kb][qb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb) {
-        const V8 ka = *(const V8*)(Ks + (16 * kb + hl) * kStride + 8 * quad);
+        const V8 ka = *(const V8*)(kb0 + kb * 16 * kRowB + kadr[ks]);
 #pragma unroll
         for (int qb = 0; qb < NQB; ++qb)
-          sc[kb][qb] = mfma16x16x32(ka, qv[qb][0], (f32x4){0.f, 0.f, 0.f, 0.f});
+          sc[SP][kb][qb] = mfma16x16x32(ka, qv[qb][ks], sc[SP][kb][qb]);
+      }
+  };
+  auto pvmul = [&](auto vpar, auto ppar) {
+    constexpr int VP = decltype(vpar)::value, PP = decltype(ppar)::value;
+    const char* vb0 = smem + (2 + VP) * kTileB;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        const V4 v0 = lds_read_tr4((const T*)(vb0 + 32 * kk * kRowB + 128 * (mb >> 2) + vadr[mb & 3]));
+        const V4 v1 =
+            lds_read_tr4((const T*)(vb0 + (32 * kk + 16) * kRowB + 128 * (mb >> 2) + vadr[mb & 3]));
+        const V8 va = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) o[qb][mb] = mfma16x16x32(va, pv[PP][kk][qb], o[qb][mb]);
       }
 #pragma unroll
-      for (int ks = 1; ks < KS; ++ks) {
+    for (int kk = 0; kk < KK; ++kk)
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb) {
-          const V8 ka = *(const V8*)(Ks + (16 * kb + hl) * kStride + 32 * ks + 8 * quad);
+      for (int qb = 0; qb < NQB; ++qb) lsum[qb] = mfma16x16x32(ones, pv[PP][kk][qb], lsum[qb]);
+  };
+  // Online softmax of tile t (base 2, lazy reference max: m moves only when a
+  // score exceeds it by more than kRescale / c2; the O / l rescale this
+  // needs is applied before the next PV step).
+  auto mask = [&](auto spar, int t) {
+    constexpr int SP = decltype(spar)::value;
+    const int k0 = lo + t * BK;
 #pragma unroll
-          for (int qb = 0; qb < NQB; ++qb) sc[kb][qb] = mfma16x16x32(ka, qv[qb][ks], sc[kb][qb]);
+    for (int qb = 0; qb < NQB; ++qb) {
+      const int qrel = rel0 + tok[qb];
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = k0 + 16 * kb + 4 * quad + i;
+          const bool ok = key < hi && key <= qrel && (a.window <= 0 || key > qrel - a.window);
+          sc[SP][kb][qb][i] = ok ? sc[SP][kb][qb][i] : -INFINITY;
         }
-      }
-      if (__builtin_expect(need_mask, 0)) {
-        __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  auto softmax = [&](auto spar) {
+    constexpr int SP = decltype(spar)::value;
 #pragma unroll
-        for (int qb = 0; qb < NQB; ++qb) {
-          const int qrel = rel0 + tok[qb];
+    for (int qb = 0; qb < NQB; ++qb) {
+      float mx = sc[SP][0][qb][0];
 #pragma unroll
-          for (int kb = 0; kb < KB; ++kb) {
+      for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const int key = k0 + 16 * kb + 4 * quad + i;
-              const bool ok = key < hi && key <= qrel && (a.window <= 0 || key > qrel - a.window);
-              sc[kb][qb][i] = ok ? sc[kb][qb][i] : -INFINITY;
-            }
-          }
-        }
-      }
-      V8 pv[KK][NQB];
+        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[SP][kb][qb][i]);
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const bool grow = mx > m[qb] + thr;
+      const float mn = grow ? mx : m[qb];
+      pend[qb] = grow ? fast_exp2((m[qb] - mn) * c2) : 1.f;
+      pend_any |= __ballot(grow) != 0;
+      m[qb] = mn;
+      const float mc = mn == -INFINITY ? 0.f : mn * c2;
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          pv[SP][kb >> 1][qb][4 * (kb & 1) + i] =
+              from_f32<T>(fast_exp2(__builtin_fmaf(sc[SP][kb][qb][i], c2, -mc)));
+    }
+  };
+  auto need_mask = [&](int t) {
+    const int k0 = lo + t * BK;
+    return k0 + BK - 1 > rel0 + wt_first || k0 + BK > hi ||
+           (a.window > 0 && k0 <= rel0 + wt_last - a.window);
+  };
+
+  // Iteration j: PV(j-1), softmax(j), QK(j+1) (tile indices), while the
+  // direct loads of K(j+2) and V(j) land in the buffers iteration j-1 read.
+  auto iteration = [&](auto par, int j) {
+    constexpr int P = decltype(par)::value;  // = j & 1
+    if (j + 2 < nt) load_tile(kg, a.ks_pos, kofs, j + 2, P);
+    if (j < nt) load_tile(vg, a.vs_pos, vofs, j, 2 + P);
+    if (__builtin_expect(pend_any, 0)) {
 #pragma unroll
       for (int qb = 0; qb < NQB; ++qb) {
-        float mx = sc[0][qb][0];
+        lsum[qb] *= pend[qb];
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[kb][qb][i]);
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const bool grow = mx > m[qb] + thr;
-        if (__ballot(grow) != 0) {  // rare: move the reference max and rescale
-          const float mn = grow ? mx : m[qb];
-          const float alpha = m[qb] == -INFINITY ? 0.f : fast_exp2((m[qb] - mn) * c2);
-          l[qb] *= alpha;
-#pragma unroll
-          for (int mb = 0; mb < MB; ++mb) o[qb][mb] *= alpha;
-          m[qb] = mn;
-        }
-        const float mc = m[qb] == -INFINITY ? 0.f : m[qb] * c2;
-        float ps = 0.f;
-#pragma unroll
-        for (int kb = 0; kb < KB; ++kb) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float p = fast_exp2(__builtin_fmaf(sc[kb][qb][i], c2, -mc));
-            ps += p;
-            pv[kb >> 1][qb][4 * (kb & 1) + i] = from_f32<T>(p);
-          }
-        }
-        l[qb] += ps;
+        for (int mb = 0; mb < MB; ++mb) o[qb][mb] *= pend[qb];
+        pend[qb] = 1.f;
       }
-      // O^T += V^T P^T; rows 32 kk + 16 h + 4 quad + 0..3 via transposing reads.
-#pragma unroll
-      for (int kk = 0; kk < KK; ++kk) {
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb) {
-          const V4 v0 = lds_read_tr4(Vs + (32 * kk + tr_row) * kVStride + 16 * mb + tr_col);
-          const V4 v1 = lds_read_tr4(Vs + (32 * kk + 16 + tr_row) * kVStride + 16 * mb + tr_col);
-          const V8 va = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
-#pragma unroll
-          for (int qb = 0; qb < NQB; ++qb) o[qb][mb] = mfma16x16x32(va, pv[kk][qb], o[qb][mb]);
-        }
-      }
+      pend_any = false;
     }
-    if (next) lstore(buf ^ 1);
+    if (__builtin_expect(need_mask(j), 0)) mask(Par<P>(), j);
+    // One basic block of independent MFMA and VALU work.  At j = 0 the PV
+    // step multiplies zeroed P by a zeroed V buffer; at j = nt the softmax
+    // sees a fully masked tile (k0 >= hi) and its P is never used.
+    __builtin_amdgcn_sched_barrier(0);
+    pvmul(Par<P ^ 1>(), Par<P ^ 1>());
+    softmax(Par<P>());
+    qk(Par<P ^ 1>(), Par<P ^ 1>());
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb) {
+      pin(m[qb]);
+      pin(pend[qb]);
+      pin(lsum[qb]);
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) pin(o[qb][mb]);
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) pin(pv[P][kk][qb]);
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) pin(sc[P ^ 1][kb][qb]);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    buf ^= 1;
+  };
+
+  // Zero V buffer 1 (read by the j = 0 PV step) and the P operands it uses.
+#pragma unroll
+  for (int i = 0; i < kTileB / (256 * 16); ++i)
+    *(u32x4*)(smem + 3 * kTileB + (i * 256 + tid) * 16) = (u32x4){0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int kk = 0; kk < KK; ++kk)
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb) pv[1][kk][qb] = (V8){};
+  if (nt > 0) load_tile(kg, a.ks_pos, kofs, 0, 0);
+  if (nt > 1) load_tile(kg, a.ks_pos, kofs, 1, 1);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  qk(Par<0>(), Par<0>());
+  __syncthreads();  // K(0) fully read before iteration 0 refills its buffer
+  for (int j = 0; j <= nt; j += 2) {
+    iteration(Par<0>(), j);
+    if (j + 1 <= nt) iteration(Par<1>(), j + 1);
   }
 
 #pragma unroll
   for (int qb = 0; qb < NQB; ++qb) {
-    float lt = l[qb] + __shfl_xor(l[qb], 16);
-    lt += __shfl_xor(lt, 32);
+    const float lt = lsum[qb][0];
     const float inv = lt > 0.f ? 1.0f / lt : 0.f;
     if (!cok[qb]) continue;
     TO* op = (TO*)a.out + ((int64_t)tok[qb] * a.q_heads + hq[qb]) * D + 4 * quad;
