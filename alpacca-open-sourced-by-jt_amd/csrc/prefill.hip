@@ -77,10 +77,23 @@ constexpr float kRescale = 8.0f;
 
 // K and V tiles sit unpadded in LDS, written by direct-to-LDS buffer loads
 // (no staging registers, no LDS write instructions).  16-byte unit c of row r
-// is stored at unit c ^ swz(r): the K operand reads (eight consecutive rows,
-// one unit each) and the V transposing reads (four consecutive rows, a pair
-// of units each) then touch distinct banks.
-__device__ __forceinline__ int swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+// is stored at unit c ^ swz(r), with a swizzle per tile chosen from
+// bank-conflict counter measurements on gfx950 of the two read patterns:
+//   K operand reads (ds_read_b128: 16 consecutive rows, one unit each):
+//     conflict-free with swz = r mod 16 (r mod 8 for 128-byte rows);
+//   V transposing reads (ds_read_b64_tr_b16: 4-row groups, a unit pair
+//     {2y, 2y+1} each): conflict-free with swz = ((r mod 8) << 1) | bit 3 of r
+//     for rows of 256 bytes or more, r mod 8 for 128-byte rows.
+// Every swizzle is below 16, so it only permutes units inside each aligned
+// group of 16 units (256 bytes).
+template <int ROW_BYTES>
+__device__ __forceinline__ int swz_k(int r) {
+  return ROW_BYTES >= 256 ? (r & 15) : (r & 7);
+}
+template <int ROW_BYTES>
+__device__ __forceinline__ int swz_v(int r) {
+  return ROW_BYTES >= 256 ? (((r & 7) << 1) | ((r >> 3) & 1)) : (r & 7);
+}
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
@@ -191,15 +204,16 @@ prefill_mfma(PrefillArgs a) {
   // Direct loads: wave-instruction q of a tile fills LDS bytes [1024 q,
   // 1024 q + 1024), lane L the 16 bytes at 1024 q + 16 L, i.e. row
   // (64 q + L) / U, stored unit (64 q + L) % U, which holds logical unit
-  // stored ^ swz(row).  Rows at or past kv_tokens read as zero.
+  // stored ^ swz_k/swz_v(row).  Rows at or past kv_tokens read as zero.
   uint32_t kofs[kIW], vofs[kIW];
 #pragma unroll
   for (int t = 0; t < kIW; ++t) {
     const int sl = (wave * kIW + t) * 64 + lane;
     const int row = sl / U;
-    const int c = (sl % U) ^ swz(row);
-    kofs[t] = (uint32_t)(((int64_t)row * a.ks_pos + 8 * c) * (int64_t)sizeof(T));
-    vofs[t] = (uint32_t)(((int64_t)row * a.vs_pos + 8 * c) * (int64_t)sizeof(T));
+    const int ck = (sl % U) ^ swz_k<kRowB>(row);
+    const int cv = (sl % U) ^ swz_v<kRowB>(row);
+    kofs[t] = (uint32_t)(((int64_t)row * a.ks_pos + 8 * ck) * (int64_t)sizeof(T));
+    vofs[t] = (uint32_t)(((int64_t)row * a.vs_pos + 8 * cv) * (int64_t)sizeof(T));
   }
   const T* kg = (const T*)a.k + (int64_t)kvh * D;
   const T* vg = (const T*)a.v + (int64_t)kvh * D;
@@ -218,18 +232,25 @@ prefill_mfma(PrefillArgs a) {
 #endif
   };
 
-  // LDS read offsets.  K operand: row 16 kb + hl, logical unit 4 ks + quad.
+  // LDS read offsets (the swizzle only depends on a row's index mod 16, and
+  // tile row bases are multiples of 16).  K operand: row 16 kb + hl,
+  // logical unit 4 ks + quad.
   uint32_t kadr[KS];
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks) kadr[ks] = hl * kRowB + (((4 * ks + quad) ^ swz(hl & 7)) * 16);
+  for (int ks = 0; ks < KS; ++ks) kadr[ks] = hl * kRowB + (((4 * ks + quad) ^ swz_k<kRowB>(hl)) * 16);
   // V transposing reads: row 32 kk + 16 h + tr_row, elements 16 mb + 4 (hl & 3)
-  // + 0..3, i.e. logical unit 2 mb + ((hl & 3) >> 1); with mb = 4 x + y the
-  // stored unit is 8 x + ((2 y + cb) ^ swz(tr_row)).
+  // + 0..3, i.e. logical unit 2 mb + cb (cb = (hl & 3) >> 1).  With mb = 4 x + y
+  // that unit is 16 (x >> 1) + (8 (x & 1) + 2 y + cb), and the swizzle (< 16)
+  // only touches the bracket, so x >> 1 becomes a constant 256-byte offset.
   const int tr_row = 4 * quad + (hl >> 2);
-  uint32_t vadr[4];
+  constexpr int VXB = MB >= 8 ? 2 : 1;
+  uint32_t vadr[VXB][4];
 #pragma unroll
-  for (int y = 0; y < 4; ++y)
-    vadr[y] = tr_row * kRowB + (((2 * y + ((hl & 3) >> 1)) ^ swz(tr_row & 7)) * 16) + (hl & 1) * 8;
+  for (int xb = 0; xb < VXB; ++xb)
+#pragma unroll
+    for (int y = 0; y < 4; ++y)
+      vadr[xb][y] = tr_row * kRowB + (((8 * xb + 2 * y + ((hl & 3) >> 1)) ^ swz_v<kRowB>(tr_row)) * 16) +
+                    (hl & 1) * 8;
 
   // Scores (S^T tiles) of two tiles and P operands of two tiles, by parity.
   f32x4 sc[2][KB][NQB];
@@ -259,9 +280,9 @@ prefill_mfma(PrefillArgs a) {
     for (int kk = 0; kk < KK; ++kk)
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
-        const V4 v0 = lds_read_tr4((const T*)(vb0 + 32 * kk * kRowB + 128 * (mb >> 2) + vadr[mb & 3]));
-        const V4 v1 =
-            lds_read_tr4((const T*)(vb0 + (32 * kk + 16) * kRowB + 128 * (mb >> 2) + vadr[mb & 3]));
+        const uint32_t va0 = vadr[(mb >> 2) & (VXB - 1)][mb & 3] + 256 * (mb >> 3);
+        const V4 v0 = lds_read_tr4((const T*)(vb0 + 32 * kk * kRowB + va0));
+        const V4 v1 = lds_read_tr4((const T*)(vb0 + (32 * kk + 16) * kRowB + va0));
         const V8 va = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
 #pragma unroll
         for (int qb = 0; qb < NQB; ++qb) o[qb][mb] = mfma16x16x32(va, pv[PP][kk][qb], o[qb][mb]);
