@@ -11,7 +11,10 @@
 // O^T += V^T P^T with P taken straight from the score registers and V^T read
 // from the row-major LDS tile with transposing reads.  K/V tiles are double
 // buffered: the next tile's global loads are in flight while the current
-// tile is multiplied.  Tiles entirely above the diagonal are never loaded;
+// tile is multiplied.  One iteration's MFMA block holds PV of tile j - 1,
+// the exp / convert work of tile j and QK of tile j + 1, at raised wave
+// priority; the softmax max bookkeeping runs ahead of it (see grow_check).
+// Tiles entirely above the diagonal are never loaded;
 // tiles entirely above one wave's diagonal are skipped by that wave.  Blocks
 // are mapped so that one kv head's blocks share one XCD (and its L2), with
 // the latest (most expensive) column tiles launched first.
@@ -96,6 +99,41 @@ __device__ __forceinline__ int swz_v(int r) {
 }
 
 typedef __attribute__((address_space(3))) void lds_void_t;
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// Buffer resource words of a raw (stride 0) buffer of `bytes` bytes at
+// `base`; loads at offsets past `bytes` return zero.
+__device__ __forceinline__ i32x4 rsrc_words(const void* base, uint32_t bytes) {
+  const uint64_t p = (uint64_t)(uintptr_t)base;
+  return (i32x4){(int)(uint32_t)p, (int)((uint32_t)(p >> 32) & 0xffffu), (int)bytes, 0x00020000};
+}
+
+// One direct-to-LDS 16-byte-per-lane buffer load: lane L's 16 bytes at
+// buffer offset `voff` land at LDS byte `lds + 16 L` (`lds` wave-uniform).
+// Written as inline assembly (the same three instructions the compiler
+// emits for __builtin_amdgcn_raw_ptr_buffer_load_lds) because the
+// compiler's wait insertion counts that builtin as an LDS store that may
+// alias every later LDS read: it put a wait for all outstanding loads in
+// front of the first LDS read of each iteration -- the reads of the other
+// buffer -- which exposed the whole latency of the tile loads just issued.
+// The kernel waits for these loads itself (s_waitcnt 0) before each
+// barrier.  m0 is written here and nowhere else in the prefill kernels (no
+// other instruction they contain reads it).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"  // m0 is reserved; the clobber is intended
+__device__ __forceinline__ void lds_dma16(i32x4 r, uint32_t lds, uint32_t voff) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(lds), "v"(voff), "s"(r)
+               : "memory", "m0");
+#else
+  (void)r;
+  (void)lds;
+  (void)voff;
+#endif
+}
+#pragma clang diagnostic pop
 
 template <int V>
 using Par = std::integral_constant<int, V>;
@@ -185,10 +223,11 @@ prefill_mfma(PrefillArgs a) {
 
   f32x4 o[NQB][MB];   // O^T[d = 16 mb + 4 quad + i][column]
   f32x4 lsum[NQB];    // row sums of P, accumulated by MFMA (all four entries equal)
-  float m[NQB], pend[NQB];
+  float m[NQB], mc[NQB], pend[NQB];  // mc = m * c2 (0 while m = -inf)
 #pragma unroll
   for (int qb = 0; qb < NQB; ++qb) {
     m[qb] = -INFINITY;
+    mc[qb] = 0.f;
     pend[qb] = 1.f;
     lsum[qb] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -219,17 +258,12 @@ prefill_mfma(PrefillArgs a) {
   const T* vg = (const T*)a.v + (int64_t)kvh * D;
   auto load_tile = [&](const T* g, int64_t pos, const uint32_t (&ofs)[kIW], int t, int buf) {
     const int k0 = lo + t * BK;
-    const __amdgpu_buffer_rsrc_t r = buffer_rsrc(
+    const i32x4 r = rsrc_words(
         g + (int64_t)k0 * pos, (uint32_t)((int64_t)(a.kv_tokens - k0) * pos * (int64_t)sizeof(T)));
-#if defined(__HIP_DEVICE_COMPILE__)  // LDS address-space operands exist only for the GPU target
+    const uint32_t lds0 =
+        (uint32_t)(uintptr_t)(lds_void_t*)(smem + buf * kTileB + wave * kIW * 1024);
 #pragma unroll
-    for (int i = 0; i < kIW; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          r, (lds_void_t*)(smem + buf * kTileB + (wave * kIW + i) * 1024), 16, ofs[i], 0, 0, 0);
-#else
-    (void)r;
-    (void)ofs;
-#endif
+    for (int i = 0; i < kIW; ++i) lds_dma16(r, lds0 + i * 1024, ofs[i]);
   };
 
   // LDS read offsets (the swizzle only depends on a row's index mod 16, and
@@ -256,7 +290,7 @@ prefill_mfma(PrefillArgs a) {
   f32x4 sc[2][KB][NQB];
   V8 pv[2][KK][NQB];
 
-  auto qk = [&](auto kpar, auto spar) {
+  auto qk = [&](auto kpar, auto spar) __attribute__((always_inline)) {
     constexpr int KP = decltype(kpar)::value, SP = decltype(spar)::value;
     const char* kb0 = smem + KP * kTileB;
 #pragma unroll
@@ -273,7 +307,7 @@ prefill_mfma(PrefillArgs a) {
           sc[SP][kb][qb] = mfma16x16x32(ka, qv[qb][ks], sc[SP][kb][qb]);
       }
   };
-  auto pvmul = [&](auto vpar, auto ppar) {
+  auto pvmul = [&](auto vpar, auto ppar) __attribute__((always_inline)) {
     constexpr int VP = decltype(vpar)::value, PP = decltype(ppar)::value;
     const char* vb0 = smem + (2 + VP) * kTileB;
 #pragma unroll
@@ -292,9 +326,6 @@ prefill_mfma(PrefillArgs a) {
 #pragma unroll
       for (int qb = 0; qb < NQB; ++qb) lsum[qb] = mfma16x16x32(ones, pv[PP][kk][qb], lsum[qb]);
   };
-  // Online softmax of tile t (base 2, lazy reference max: m moves only when a
-  // score exceeds it by more than kRescale / c2; the O / l rescale this
-  // needs is applied before the next PV step).
   auto mask = [&](auto spar, int t) {
     constexpr int SP = decltype(spar)::value;
     const int k0 = lo + t * BK;
@@ -311,7 +342,31 @@ prefill_mfma(PrefillArgs a) {
         }
     }
   };
-  auto softmax = [&](auto spar) {
+  // Online softmax, base 2, with a lazy reference max: a column's m moves
+  // only when one of its scores exceeds m by more than kRescale / c2 (so P
+  // stays <= 2^kRescale), and the O / l rescale a move needs is applied
+  // before the next PV step.  The scores of tile j are in registers when
+  // iteration j starts, so the growth check runs there, ahead of the
+  // interleaved block: each lane compares the max of its own scores with
+  // m + thr, and only when some lane of the wave grew (rare after a
+  // column's first tile) does the wave take the exact column max across the
+  // four lanes of each column (l, l ^ 16, l ^ 32, l ^ 48) and move m.  The
+  // block then forms P against the settled m.
+  auto grow_check = [&](auto spar) __attribute__((always_inline)) {
+    constexpr int SP = decltype(spar)::value;
+    bool grow = false;
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb) {
+      float mx = sc[SP][0][qb][0];
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[SP][kb][qb][i]);
+      grow |= mx > m[qb] + thr;
+    }
+    return __ballot(grow) != 0;
+  };
+  auto move_max = [&](auto spar) __attribute__((always_inline)) {
     constexpr int SP = decltype(spar)::value;
 #pragma unroll
     for (int qb = 0; qb < NQB; ++qb) {
@@ -322,19 +377,24 @@ prefill_mfma(PrefillArgs a) {
         for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[SP][kb][qb][i]);
       mx = fmaxf(mx, __shfl_xor(mx, 16));
       mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const bool grow = mx > m[qb] + thr;
-      const float mn = grow ? mx : m[qb];
-      pend[qb] = grow ? fast_exp2((m[qb] - mn) * c2) : 1.f;
-      pend_any |= __ballot(grow) != 0;
+      const bool g = mx > m[qb] + thr;
+      const float mn = g ? mx : m[qb];
+      pend[qb] = g ? fast_exp2((m[qb] - mn) * c2) : 1.f;
+      pend_any |= __ballot(g) != 0;
       m[qb] = mn;
-      const float mc = mn == -INFINITY ? 0.f : mn * c2;
+      mc[qb] = mn == -INFINITY ? 0.f : mn * c2;
+    }
+  };
+  auto softmax = [&](auto spar) __attribute__((always_inline)) {
+    constexpr int SP = decltype(spar)::value;
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb)
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
           pv[SP][kb >> 1][qb][4 * (kb & 1) + i] =
-              from_f32<T>(fast_exp2(__builtin_fmaf(sc[SP][kb][qb][i], c2, -mc)));
-    }
+              from_f32<T>(fast_exp2(__builtin_fmaf(sc[SP][kb][qb][i], c2, -mc[qb])));
   };
   auto need_mask = [&](int t) {
     const int k0 = lo + t * BK;
@@ -346,8 +406,17 @@ prefill_mfma(PrefillArgs a) {
   // direct loads of K(j+2) and V(j) land in the buffers iteration j-1 read.
   auto iteration = [&](auto par, int j) {
     constexpr int P = decltype(par)::value;  // = j & 1
+    // Nothing is outstanding here at run time (the previous iteration ended
+    // with a full wait), but the compiler's wait tracking may still carry
+    // memory operations from before the loop (a register spill store); left
+    // pending, it answers them with a full memory wait in front of this
+    // iteration's first LDS read, which would also wait for the tile loads
+    // issued below.  An explicit wait here clears its scoreboard for free.
+    __builtin_amdgcn_s_waitcnt(0);
     if (j + 2 < nt) load_tile(kg, a.ks_pos, kofs, j + 2, P);
     if (j < nt) load_tile(vg, a.vs_pos, vofs, j, 2 + P);
+    // Rescale for the m moved at tile j - 1 (O holds tiles <= j - 2 and is
+    // about to take PV(j - 1), formed against the moved m).
     if (__builtin_expect(pend_any, 0)) {
 #pragma unroll
       for (int qb = 0; qb < NQB; ++qb) {
@@ -359,17 +428,21 @@ prefill_mfma(PrefillArgs a) {
       pend_any = false;
     }
     if (__builtin_expect(need_mask(j), 0)) mask(Par<P>(), j);
+    if (__builtin_expect(grow_check(Par<P>()), 0)) move_max(Par<P>());
     // One basic block of independent MFMA and VALU work.  At j = 0 the PV
     // step multiplies zeroed P by a zeroed V buffer; at j = nt the softmax
     // sees a fully masked tile (k0 >= hi) and its P is never used.
     __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_setprio(1);
     pvmul(Par<P ^ 1>(), Par<P ^ 1>());
     softmax(Par<P>());
     qk(Par<P ^ 1>(), Par<P ^ 1>());
+    __builtin_amdgcn_s_setprio(0);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int qb = 0; qb < NQB; ++qb) {
       pin(m[qb]);
+      pin(mc[qb]);
       pin(pend[qb]);
       pin(lsum[qb]);
 #pragma unroll
