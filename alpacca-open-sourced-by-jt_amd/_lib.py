@@ -44,13 +44,37 @@ SIGNATURES = {
     "alpx_gdn_chunk_prefill": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
                                         _c_ptr, _c_size, _c_int, _c_int, _c_int, _c_int, _c_int,
                                         _c_int, _c_int, _c_int, _c_ptr]),
+    "alpx_silu": (_c_int, [_c_ptr, _c_ptr, _c_i64, _c_int, _c_int, _c_ptr]),
+    "alpx_row_norm": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_i64, _c_int, _c_i64, _c_i64,
+                               _c_float, _c_int, _c_int, _c_int, _c_ptr]),
+    "alpx_conv_step": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_int, _c_int, _c_i64,
+                                _c_i64, _c_int, _c_int, _c_ptr]),
+    "alpx_recurrent_parameters": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
+                                           _c_i64, _c_int, _c_ptr]),
+    "alpx_imrope": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_i64, _c_i64, _c_int, _c_int,
+                             ctypes.POINTER(ctypes.c_int), ctypes.c_double, ctypes.c_double,
+                             _c_int, _c_int, _c_ptr]),
+    "alpx_attention_prologue": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
+                                         _c_ptr, _c_ptr, _c_int, _c_i64, _c_int, _c_int, _c_int,
+                                         _c_int, _c_int, _c_i64, _c_ptr,
+                                         ctypes.POINTER(ctypes.c_int), ctypes.c_double,
+                                         _c_float, _c_ptr]),
+    "alpx_recurrent_step_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int]),
+    "alpx_recurrent_step": (_c_int, [_c_ptr, _c_ptr, _c_i64, _c_i64, _c_ptr, _c_int, _c_ptr,
+                                     _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
+                                     _c_ptr, _c_size, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                     _c_float, _c_int, _c_ptr]),
     "alpx_timing_enable": (_c_int, [_c_int]),
     "alpx_timing_read": (_c_int, [_c_int, ctypes.POINTER(ctypes.c_double),
                                   ctypes.POINTER(ctypes.c_int64)]),
 }
 
 # alpx_timed_kernel ids
-T_KV_APPEND, T_DECODE, T_DECODE_COMBINE, T_PREFILL, T_GDN_CHUNK, T_GDN_STEP, T_AUX = range(7)
+(T_KV_APPEND, T_DECODE, T_DECODE_COMBINE, T_PREFILL, T_GDN_CHUNK, T_GDN_STEP, T_AUX, T_LAYER,
+ T_RECURRENT_STEP) = range(9)
+
+# alpx_row_norm modes
+NORM_L2, NORM_RMS, NORM_RMS_GATE = 0, 1, 2
 
 
 def timing_enable(on: bool) -> None:

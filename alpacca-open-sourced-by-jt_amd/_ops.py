@@ -165,3 +165,164 @@ def gdn_chunk(state, q, k, v, beta, log_decay, out_dtype=None):
         _lib.stream_handle(torch, state.device))
     _lib.check(rc)
     return out
+
+
+def silu(values, out_dtype=None):
+    """Elementwise ``x * sigmoid(x)``; returns a new tensor."""
+    torch = _torch()
+    out = torch.empty(values.shape, dtype=values.dtype if out_dtype is None else out_dtype,
+                      device=values.device)
+    rc = _lib.lib().alpx_silu(values.data_ptr(), out.data_ptr(), values.numel(),
+                              _lib.dtype_code(torch, values.dtype),
+                              _lib.dtype_code(torch, out.dtype),
+                              _lib.stream_handle(torch, values.device))
+    _lib.check(rc)
+    return out
+
+
+def row_norm(x, *, mode, eps, weight=None, gate=None, n=None, rows=None, group_rows=0,
+             group_stride=0, out_dtype=None, out=None):
+    """Row-wise L2 / RMS / gated-RMS normalisation over the last axis of
+    ``x`` (contiguous unless ``rows``/``group_*`` describe a strided view of
+    its storage, with ``n`` the row width).  ``weight`` fp32 ``[n]``;
+    ``gate`` contiguous like the output.  Returns ``[rows, n]`` (shaped like
+    ``x`` for contiguous rows)."""
+    torch = _torch()
+    n = int(x.shape[-1]) if n is None else int(n)
+    if rows is None:
+        rows = x.numel() // n
+    if out is None:
+        shape = x.shape if group_rows == 0 else (rows, n)
+        out = torch.empty(shape, dtype=x.dtype if out_dtype is None else out_dtype,
+                          device=x.device)
+    rc = _lib.lib().alpx_row_norm(
+        x.data_ptr(), None if weight is None else weight.data_ptr(),
+        None if gate is None else gate.data_ptr(), out.data_ptr(), int(rows), n,
+        int(group_rows), int(group_stride), float(eps), int(mode),
+        _lib.dtype_code(torch, x.dtype), _lib.dtype_code(torch, out.dtype),
+        _lib.stream_handle(torch, x.device))
+    _lib.check(rc)
+    return out
+
+
+def conv_step(current, weight, history, *, weight_layout="kc", apply_silu=False,
+              out_dtype=None):
+    """Causal depthwise convolution step on ``current [B, C]`` with
+    ``history [B, K-1, C]`` (fp32, shifted in place) and ``weight`` ``[K, C]``
+    (``"kc"``) or ``[C, K]`` (``"ck"``).  Returns ``[B, C]``."""
+    torch = _torch()
+    bsz, channels = (int(x) for x in current.shape)
+    if weight_layout == "kc":
+        kernel = int(weight.shape[0])
+        tap_stride, ch_stride = channels, 1
+    else:
+        kernel = int(weight.shape[1])
+        tap_stride, ch_stride = 1, kernel
+    out = torch.empty((bsz, channels), dtype=torch.float32 if out_dtype is None else out_dtype,
+                      device=current.device)
+    rc = _lib.lib().alpx_conv_step(
+        current.data_ptr(), weight.data_ptr(), None if history is None else history.data_ptr(),
+        out.data_ptr(), bsz, channels, kernel, tap_stride, ch_stride, 1 if apply_silu else 0,
+        _lib.dtype_code(torch, out.dtype), _lib.stream_handle(torch, current.device))
+    _lib.check(rc)
+    return out
+
+
+def recurrent_parameters(beta_logits, alpha_logits, dt_bias, ssm_a):
+    """``(beta, log_decay)`` shaped like ``beta_logits`` (fp32)."""
+    torch = _torch()
+    beta = torch.empty_like(beta_logits)
+    g = torch.empty_like(beta_logits)
+    heads = int(dt_bias.shape[0])
+    rc = _lib.lib().alpx_recurrent_parameters(
+        beta_logits.data_ptr(), alpha_logits.data_ptr(), dt_bias.data_ptr(), ssm_a.data_ptr(),
+        beta.data_ptr(), g.data_ptr(), beta_logits.numel(), heads,
+        _lib.stream_handle(torch, beta_logits.device))
+    _lib.check(rc)
+    return beta, g
+
+
+def _sections(sections):
+    import ctypes
+    sec = (ctypes.c_int * 4)(*[int(x) for x in sections])
+    return sec
+
+
+def imrope(values, position_lanes, sections, *, frequency_base, frequency_scale=1.0,
+           out_dtype=None):
+    """IMROPE over the last axis of ``values``.  ``position_lanes`` int64
+    ``(4,)`` (one lane vector for every row) or ``[rows, 4]`` (one per row,
+    rows = values.numel() // values.shape[-1])."""
+    torch = _torch()
+    dim = int(values.shape[-1])
+    rows = values.numel() // dim
+    lanes = position_lanes.to(device=values.device, dtype=torch.int64).contiguous()
+    stride = 0 if lanes.numel() == 4 else 4
+    out = torch.empty(values.shape, dtype=values.dtype if out_dtype is None else out_dtype,
+                      device=values.device)
+    rc = _lib.lib().alpx_imrope(
+        values.data_ptr(), out.data_ptr(), lanes.data_ptr(), stride, rows, 1, dim,
+        _sections(sections), float(frequency_base), float(frequency_scale),
+        _lib.dtype_code(torch, values.dtype), _lib.dtype_code(torch, out.dtype),
+        _lib.stream_handle(torch, values.device))
+    _lib.check(rc)
+    return out
+
+
+def attention_prologue(query_gate, key, value, q_norm, k_norm, key_cache, value_cache, *,
+                       position=0, positions=None, sections, frequency_base, eps):
+    """Fused Qwen3.5 attention prologue for one token per sequence:
+    ``query_gate [B, Hq, 2D]``, ``key [B, Hkv, D]``, ``value [B, Hkv, Dv]``;
+    appends the normalised, rotated key and the value to the caches
+    ``[C, B, Hkv, D|Dv]``.  Returns ``(query [B, Hq, D], gate [B, Hq, D])``."""
+    torch = _torch()
+    capacity, bsz, kv_heads, dim = (int(x) for x in key_cache.shape)
+    value_dim = int(value_cache.shape[3])
+    q_heads = int(query_gate.shape[1])
+    query = torch.empty((bsz, q_heads, dim), dtype=key_cache.dtype, device=key_cache.device)
+    gate = torch.empty_like(query)
+    pos_ptr = None
+    if positions is not None:
+        positions = positions.to(device=key_cache.device, dtype=torch.int32).contiguous()
+        pos_ptr = positions.data_ptr()
+    rc = _lib.lib().alpx_attention_prologue(
+        query_gate.data_ptr(), key.data_ptr(), value.data_ptr(), q_norm.data_ptr(),
+        k_norm.data_ptr(), query.data_ptr(), gate.data_ptr(), key_cache.data_ptr(),
+        value_cache.data_ptr(), _lib.dtype_code(torch, key_cache.dtype), capacity, bsz,
+        q_heads, kv_heads, dim, value_dim, int(position), pos_ptr, _sections(sections),
+        float(frequency_base), float(eps), _lib.stream_handle(torch, key_cache.device))
+    _lib.check(rc)
+    return query, gate
+
+
+def recurrent_step(current, conv_weight, conv_history, gate, beta_logits, alpha_logits, dt_bias,
+                   ssm_a, norm_weight, state, *, key_heads, key_dim, eps, weight_layout="kc",
+                   out_dtype=None):
+    """Fused Qwen3.5 recurrent-layer token (all fp32 inputs); updates
+    ``conv_history [B, K-1, C]`` and ``state [B, Hv, Dv, Dk]`` in place and
+    returns ``[B, Hv * Dv]``."""
+    torch = _torch()
+    bsz, hv, dv, dk = (int(x) for x in state.shape)
+    channels = int(current.shape[1])
+    if weight_layout == "kc":
+        kernel = int(conv_weight.shape[0])
+        tap_stride, ch_stride = channels, 1
+    else:
+        kernel = int(conv_weight.shape[1])
+        tap_stride, ch_stride = 1, kernel
+    out = torch.empty((bsz, hv * dv), dtype=torch.float32 if out_dtype is None else out_dtype,
+                      device=state.device)
+    L = _lib.lib()
+    nbytes = L.alpx_recurrent_step_workspace_bytes(bsz, int(key_heads), hv, int(key_dim), dv)
+    if nbytes == 0:
+        raise ValueError("invalid recurrent step sizes")
+    ws = _lib.workspace(torch, state.device, nbytes)
+    rc = L.alpx_recurrent_step(
+        current.data_ptr(), conv_weight.data_ptr(), tap_stride, ch_stride,
+        None if conv_history is None else conv_history.data_ptr(), kernel, gate.data_ptr(),
+        beta_logits.data_ptr(), alpha_logits.data_ptr(), dt_bias.data_ptr(), ssm_a.data_ptr(),
+        norm_weight.data_ptr(), state.data_ptr(), out.data_ptr(), ws.data_ptr(), ws.numel(),
+        bsz, int(key_heads), hv, int(key_dim), dv, float(eps),
+        _lib.dtype_code(torch, out.dtype), _lib.stream_handle(torch, state.device))
+    _lib.check(rc)
+    return out

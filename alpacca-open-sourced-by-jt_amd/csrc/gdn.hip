@@ -32,6 +32,7 @@
 #include <math.h>
 
 #include "alpx_common.h"
+#include "gdn_internal.h"
 #include "timing.h"
 
 namespace alpx {
@@ -679,11 +680,12 @@ int validate(const void* state, const void* q, const void* k, const void* v, con
 }  // namespace
 }  // namespace alpx
 
-extern "C" int alpx_gdn_step(float* state, const void* q, const void* k, const void* v,
-                             const float* beta, const float* log_decay, void* out, int batch,
-                             int key_heads, int value_heads, int key_dim, int value_dim,
-                             int dtype, int out_dtype, void* stream) {
-  using namespace alpx;
+namespace alpx {
+
+int gdn_step_launch(float* state, const void* q, const void* k, const void* v, const float* beta,
+                    const float* log_decay, void* out, int batch, int key_heads,
+                    int value_heads, int key_dim, int value_dim, int dtype, int out_dtype,
+                    hipStream_t s) {
   int rc = validate(state, q, k, v, beta, log_decay, out, batch, key_heads, value_heads, key_dim,
                     value_dim, dtype, out_dtype, "alpx_gdn_step");
   if (rc != ALPX_OK) return rc;
@@ -702,13 +704,24 @@ extern "C" int alpx_gdn_step(float* state, const void* q, const void* k, const v
   a.Dk = key_dim;
   a.Dv = value_dim;
   a.scale = 1.0f / sqrtf((float)key_dim);
-  hipStream_t s = (hipStream_t)stream;
-  TimedRegion timed(ALPX_T_GDN_STEP, s);
   switch (dtype) {
     case ALPX_F32: return launch_step<float>(a, out_dtype, s);
     case ALPX_F16: return launch_step<f16_t>(a, out_dtype, s);
     default: return launch_step<bf16_t>(a, out_dtype, s);
   }
+}
+
+}  // namespace alpx
+
+extern "C" int alpx_gdn_step(float* state, const void* q, const void* k, const void* v,
+                             const float* beta, const float* log_decay, void* out, int batch,
+                             int key_heads, int value_heads, int key_dim, int value_dim,
+                             int dtype, int out_dtype, void* stream) {
+  using namespace alpx;
+  hipStream_t s = (hipStream_t)stream;
+  TimedRegion timed(ALPX_T_GDN_STEP, s);
+  return gdn_step_launch(state, q, k, v, beta, log_decay, out, batch, key_heads, value_heads,
+                         key_dim, value_dim, dtype, out_dtype, s);
 }
 
 extern "C" size_t alpx_gdn_chunk_workspace_bytes(int batch, int tokens, int value_heads,

@@ -1,0 +1,649 @@
+// Qwen3.5 layer primitives on either side of the attention / GDN kernels.
+//
+// Row norms (L2, RMS, RMS x SiLU gate), the depthwise causal convolution
+// step, the recurrent parameters (beta, log decay), IMROPE, and two fused
+// decode-step entry points built from them:
+//  * the full-attention prologue: joint query/gate split, per-head Q/K
+//    RMSNorm, IMROPE at the text position and the K/V cache append, one
+//    wave per (sequence, head) in one launch;
+//  * the recurrent-layer step: convolution + SiLU + split + Q/K L2 norm +
+//    beta / log decay in one launch (one wave per head slot), the GDN step
+//    kernel, and the gated RMSNorm.
+// All of it is bandwidth / latency work: one wave owns one row (a head of
+// 64..256 values), reductions are wave shuffles, and rotations stage the
+// normalised row in LDS so every lane can read its pair partner.
+#include <math.h>
+
+#include "alpx_common.h"
+#include "gdn_internal.h"
+#include "timing.h"
+
+namespace alpx {
+namespace {
+
+constexpr int kNormL2 = 0;        // x / max(||x||, eps)
+constexpr int kNormRms = 1;       // x / sqrt(mean(x^2) + eps) * w
+constexpr int kNormRmsGate = 2;   // rms_norm(x) * w * silu(gate)
+constexpr int kMaxDim = 512;      // widest row a prologue / prep wave stages
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+__device__ __forceinline__ float silu_f(float x) { return x * stable_sigmoid(x); }
+
+// Stable softplus log(1 + e^x) (two branches, as tensor.stable_softplus).
+__device__ __forceinline__ float softplus_f(float x) {
+  return x > 0.f ? x + log1pf(expf(-x)) : log1pf(expf(x));
+}
+
+// IMROPE position lane of rotary pair p (interleaved T/H/W/E schedule).
+__device__ __forceinline__ int imrope_lane(int p, const int (&sec)[4], int R) {
+  const int sector = p % R;
+  if (sector % 3 == 1 && sector < 3 * sec[1]) return 1;
+  if (sector % 3 == 2 && sector < 3 * sec[2]) return 2;
+  if (sector % 3 == 0 && sector < 3 * sec[0]) return 0;
+  return 3;
+}
+
+// cos / sin of pair p's angle pos * scale * base^(-2 p / (2 R)), formed in
+// double precision: the angles reach 10^4-10^5 rad at long contexts, where a
+// float angle alone would carry an error of ~10^-3 rad.
+__device__ __forceinline__ void rope_cs(double pos, int p, int R, double base, double scale,
+                                        float& c, float& s) {
+  const double theta = pos * scale * pow(base, -2.0 * (double)p / (double)(2 * R));
+  double sd, cd;
+  sincos(theta, &sd, &cd);
+  c = (float)cd;
+  s = (float)sd;
+}
+
+// ---------------------------------------------------------------- row norm
+
+struct NormArgs {
+  const void* x;
+  const float* w;
+  const void* gate;
+  void* out;
+  int64_t rows;
+  int64_t grp_rows, grp_stride;  // input row r at (r / grp_rows) * grp_stride + (r % grp_rows) * n
+  int n;
+  float eps;
+};
+
+template <typename T, typename TO, int MODE>
+__global__ void __launch_bounds__(256) row_norm_kernel(NormArgs a) {
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= a.rows) return;  // the whole wave leaves together
+  const int lane = threadIdx.x & 63;
+  const T* x = (const T*)a.x + (r / a.grp_rows) * a.grp_stride + (r % a.grp_rows) * a.n;
+  float ss = 0.f;
+  for (int i = lane; i < a.n; i += 64) {
+    const float v = to_f32(x[i]);
+    ss = fmaf(v, v, ss);
+  }
+  ss = wave_sum(ss);
+  const float den = MODE == kNormL2 ? fmaxf(sqrtf(ss), a.eps) : sqrtf(ss / (float)a.n + a.eps);
+  TO* o = (TO*)a.out + r * a.n;
+  const T* g = (const T*)a.gate + r * a.n;
+  for (int i = lane; i < a.n; i += 64) {
+    float v = to_f32(x[i]) / den;
+    if (MODE != kNormL2) v *= a.w[i];
+    if (MODE == kNormRmsGate) v *= silu_f(to_f32(g[i]));
+    o[i] = from_f32<TO>(v);
+  }
+}
+
+template <typename T, typename TO>
+int launch_norm(const NormArgs& a, int mode, hipStream_t s) {
+  const dim3 grid((unsigned)((a.rows + 3) / 4));
+  switch (mode) {
+    case kNormL2: hipLaunchKernelGGL((row_norm_kernel<T, TO, kNormL2>), grid, dim3(256), 0, s, a); break;
+    case kNormRms: hipLaunchKernelGGL((row_norm_kernel<T, TO, kNormRms>), grid, dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL((row_norm_kernel<T, TO, kNormRmsGate>), grid, dim3(256), 0, s, a); break;
+  }
+  return check_launch("alpx_row_norm");
+}
+
+template <typename T>
+int launch_norm_to(const NormArgs& a, int mode, int out_dtype, hipStream_t s) {
+  switch (out_dtype) {
+    case ALPX_F32: return launch_norm<T, float>(a, mode, s);
+    case ALPX_F16: return launch_norm<T, f16_t>(a, mode, s);
+    default: return launch_norm<T, bf16_t>(a, mode, s);
+  }
+}
+
+int run_norm(const NormArgs& a, int mode, int dtype, int out_dtype, hipStream_t s) {
+  if (a.rows == 0) return ALPX_OK;
+  switch (dtype) {
+    case ALPX_F32: return launch_norm_to<float>(a, mode, out_dtype, s);
+    case ALPX_F16: return launch_norm_to<f16_t>(a, mode, out_dtype, s);
+    default: return launch_norm_to<bf16_t>(a, mode, out_dtype, s);
+  }
+}
+
+// --------------------------------------------------------- conv step
+
+struct ConvArgs {
+  const float* cur;   // [B, C]
+  const float* w;     // tap t, channel c at t * w_tap + c * w_ch
+  float* hist;        // [B, K - 1, C], oldest first
+  void* out;          // [B, C]
+  int64_t w_tap, w_ch;
+  int B, C, K;
+  int silu;
+};
+
+template <typename TO>
+__global__ void __launch_bounds__(256) conv_step_kernel(ConvArgs a) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)a.B * a.C) return;
+  const int64_t b = i / a.C;
+  const int c = (int)(i - b * a.C);
+  float* h = a.hist + b * (int64_t)(a.K - 1) * a.C + c;
+  const float x = a.cur[i];
+  float acc = 0.f;
+  for (int t = 0; t < a.K - 1; ++t) acc = fmaf(h[(int64_t)t * a.C], a.w[t * a.w_tap + c * a.w_ch], acc);
+  acc = fmaf(x, a.w[(a.K - 1) * a.w_tap + c * a.w_ch], acc);
+  for (int t = 0; t + 1 < a.K - 1; ++t) h[(int64_t)t * a.C] = h[(int64_t)(t + 1) * a.C];
+  if (a.K > 1) h[(int64_t)(a.K - 2) * a.C] = x;
+  ((TO*)a.out)[i] = from_f32<TO>(a.silu ? silu_f(acc) : acc);
+}
+
+// ------------------------------------------------- recurrent parameters
+
+__global__ void __launch_bounds__(256)
+recurrent_params_kernel(const float* __restrict__ bl, const float* __restrict__ al,
+                        const float* __restrict__ dtb, const float* __restrict__ ssm,
+                        float* beta, float* g, int64_t n, int heads) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const int h = (int)(i % heads);
+  beta[i] = stable_sigmoid(bl[i]);
+  g[i] = softplus_f(al[i] + dtb[h]) * ssm[h];
+}
+
+// ------------------------------------------------------------- IMROPE
+
+struct RopeArgs {
+  const void* x;    // [rows, heads, dim]
+  void* out;
+  const int64_t* pos;  // lanes (T, H, W, E) of row r at pos + r * pos_stride
+  int64_t rows, pos_stride;
+  int heads, dim, R;
+  int sec[4];
+  double base, scale;
+};
+
+// One thread per (row, head, j): j < R rotates the pair (j, j + R); the
+// remaining j copy the unrotated tail coordinates 2 R .. dim - 1.
+template <typename T, typename TO>
+__global__ void __launch_bounds__(256) imrope_kernel(RopeArgs a) {
+  const int per_head = a.dim - a.R;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= a.rows * a.heads * per_head) return;
+  const int64_t rh = i / per_head;
+  const int j = (int)(i - rh * per_head);
+  const int64_t row = rh / a.heads;
+  const T* x = (const T*)a.x + rh * a.dim;
+  TO* o = (TO*)a.out + rh * a.dim;
+  if (j < a.R) {
+    const int lane = imrope_lane(j, a.sec, a.R);
+    float c, s;
+    rope_cs((double)a.pos[row * a.pos_stride + lane], j, a.R, a.base, a.scale, c, s);
+    const float x0 = to_f32(x[j]), x1 = to_f32(x[j + a.R]);
+    o[j] = from_f32<TO>(x0 * c - x1 * s);
+    o[j + a.R] = from_f32<TO>(x0 * s + x1 * c);
+  } else {
+    const int e = j + a.R;
+    o[e] = from_f32<TO>(to_f32(x[e]));
+  }
+}
+
+template <typename T>
+int launch_rope(const RopeArgs& a, int out_dtype, hipStream_t s) {
+  const int64_t n = a.rows * a.heads * (a.dim - a.R);
+  const dim3 grid((unsigned)((n + 255) / 256));
+  switch (out_dtype) {
+    case ALPX_F32: hipLaunchKernelGGL((imrope_kernel<T, float>), grid, dim3(256), 0, s, a); break;
+    case ALPX_F16: hipLaunchKernelGGL((imrope_kernel<T, f16_t>), grid, dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL((imrope_kernel<T, bf16_t>), grid, dim3(256), 0, s, a); break;
+  }
+  return check_launch("alpx_imrope");
+}
+
+// ---------------------------------------------- attention prologue (fused)
+
+struct ProArgs {
+  const void* qg;    // [B, Hq, 2 D]: per head D query then D gate values
+  const void* k;     // [B, Hkv, D]
+  const void* v;     // [B, Hkv, Dv]
+  const float* qw;   // [D]
+  const float* kw;   // [D]
+  void* q_out;       // [B, Hq, D]
+  void* g_out;       // [B, Hq, D]
+  void* kc;          // [capacity, B, Hkv, D]
+  void* vc;          // [capacity, B, Hkv, Dv]
+  const int32_t* positions;  // device [B] or null (then `position` for all)
+  int64_t position, capacity;
+  int B, Hq, Hkv, D, Dv, R;
+  int sec[4];
+  double base;
+  float eps;
+};
+
+// One wave per (sequence, slot): slots 0 .. Hq - 1 are query heads (RMSNorm
+// + IMROPE, gate copy), Hq .. Hq + Hkv - 1 key heads (RMSNorm + IMROPE, to
+// the key cache), the rest value heads (copied to the value cache).  Cache
+// rows at a position outside [0, capacity) are not written.
+template <typename T>
+__global__ void __launch_bounds__(256) attn_prologue_kernel(ProArgs a) {
+  __shared__ float stage[4][kMaxDim];
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int slots = a.Hq + 2 * a.Hkv;
+  const int64_t id = (int64_t)blockIdx.x * 4 + wave;
+  if (id >= (int64_t)a.B * slots) return;
+  const int b = (int)(id / slots);
+  const int j = (int)(id - (int64_t)b * slots);
+  const int64_t pos = a.positions ? (int64_t)a.positions[b] : a.position;
+  const bool in_cache = pos >= 0 && pos < a.capacity;
+  if (j >= a.Hq + a.Hkv) {  // value head
+    const int h = j - a.Hq - a.Hkv;
+    if (!in_cache) return;
+    const T* src = (const T*)a.v + ((int64_t)b * a.Hkv + h) * a.Dv;
+    T* dst = (T*)a.vc + ((pos * a.B + b) * a.Hkv + h) * a.Dv;
+    for (int i = lane; i < a.Dv; i += 64) dst[i] = src[i];
+    return;
+  }
+  const bool is_q = j < a.Hq;
+  const int h = is_q ? j : j - a.Hq;
+  const T* src = is_q ? (const T*)a.qg + ((int64_t)b * a.Hq + h) * 2 * a.D
+                      : (const T*)a.k + ((int64_t)b * a.Hkv + h) * a.D;
+  const float* w = is_q ? a.qw : a.kw;
+  float ss = 0.f;
+  for (int i = lane; i < a.D; i += 64) {
+    const float x = to_f32(src[i]);
+    ss = fmaf(x, x, ss);
+  }
+  ss = wave_sum(ss);
+  const float den = sqrtf(ss / (float)a.D + a.eps);
+  float* st = stage[wave];
+  for (int i = lane; i < a.D; i += 64) st[i] = to_f32(src[i]) / den * w[i];
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  T* dst;
+  if (is_q) {
+    dst = (T*)a.q_out + ((int64_t)b * a.Hq + h) * a.D;
+    T* gd = (T*)a.g_out + ((int64_t)b * a.Hq + h) * a.D;
+    for (int i = lane; i < a.D; i += 64) gd[i] = src[a.D + i];
+  } else {
+    if (!in_cache) return;
+    dst = (T*)a.kc + ((pos * a.B + b) * a.Hkv + h) * a.D;
+  }
+  const double p = (double)pos;  // text position lanes (p, p, p, 0)
+  for (int i = lane; i < a.D; i += 64) {
+    float y = st[i];
+    if (i < 2 * a.R) {
+      const int pr = i < a.R ? i : i - a.R;
+      const int ln = imrope_lane(pr, a.sec, a.R);
+      float c, s;
+      rope_cs(ln == 3 ? 0.0 : p, pr, a.R, a.base, 1.0, c, s);
+      y = i < a.R ? st[i] * c - st[i + a.R] * s : st[pr] * s + st[i] * c;
+    }
+    dst[i] = from_f32<T>(y);
+  }
+}
+
+// --------------------------------------- recurrent-layer prep (fused)
+
+struct PrepArgs {
+  const float* cur;   // [B, C], C = 2 Hk Dk + Hv Dv
+  const float* w;     // conv weights, tap t / channel c at t * w_tap + c * w_ch
+  float* hist;        // [B, K - 1, C]
+  const float* bl;    // [B, Hv]
+  const float* al;    // [B, Hv]
+  const float* dtb;   // [Hv]
+  const float* ssm;   // [Hv]
+  float* q;           // out [B, Hk, Dk]
+  float* k;           // out [B, Hk, Dk]
+  float* v;           // out [B, Hv, Dv]
+  float* beta;        // out [B, Hv]
+  float* g;           // out [B, Hv]
+  int64_t w_tap, w_ch;
+  int B, K, Hk, Hv, Dk, Dv;
+  float eps;
+};
+
+// One wave per (sequence, head slot): Hk query slots, Hk key slots, Hv
+// value slots.  Each lane convolves its channels (then SiLU) and shifts
+// their history; query / key slots L2-normalise the head; value slot h
+// also forms beta and the log decay of value head h.
+__global__ void __launch_bounds__(256) recurrent_prep_kernel(PrepArgs a) {
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int slots = 2 * a.Hk + a.Hv;
+  const int64_t id = (int64_t)blockIdx.x * 4 + wave;
+  if (id >= (int64_t)a.B * slots) return;
+  const int b = (int)(id / slots);
+  const int j = (int)(id - (int64_t)b * slots);
+  const int C = 2 * a.Hk * a.Dk + a.Hv * a.Dv;
+  int c0, n;
+  float* dst;
+  if (j < 2 * a.Hk) {
+    c0 = j * a.Dk;
+    n = a.Dk;
+    dst = (j < a.Hk ? a.q + ((int64_t)b * a.Hk + j) * a.Dk
+                    : a.k + ((int64_t)b * a.Hk + (j - a.Hk)) * a.Dk);
+  } else {
+    const int h = j - 2 * a.Hk;
+    c0 = 2 * a.Hk * a.Dk + h * a.Dv;
+    n = a.Dv;
+    dst = a.v + ((int64_t)b * a.Hv + h) * a.Dv;
+    if (lane == 0) {
+      const int64_t bh = (int64_t)b * a.Hv + h;
+      a.beta[bh] = stable_sigmoid(a.bl[bh]);
+      a.g[bh] = softplus_f(a.al[bh] + a.dtb[h]) * a.ssm[h];
+    }
+  }
+  constexpr int kPer = kMaxDim / 64;
+  float y[kPer];
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < kPer; ++e) {
+    const int i = lane + 64 * e;
+    y[e] = 0.f;
+    if (i >= n) continue;
+    const int c = c0 + i;
+    float* h = a.hist + (int64_t)b * (a.K - 1) * C + c;
+    const float x = a.cur[(int64_t)b * C + c];
+    float acc = 0.f;
+    for (int t = 0; t < a.K - 1; ++t) acc = fmaf(h[(int64_t)t * C], a.w[t * a.w_tap + c * a.w_ch], acc);
+    acc = fmaf(x, a.w[(a.K - 1) * a.w_tap + c * a.w_ch], acc);
+    for (int t = 0; t + 1 < a.K - 1; ++t) h[(int64_t)t * C] = h[(int64_t)(t + 1) * C];
+    if (a.K > 1) h[(int64_t)(a.K - 2) * C] = x;
+    y[e] = silu_f(acc);
+    ss = fmaf(y[e], y[e], ss);
+  }
+  float inv = 1.f;
+  if (j < 2 * a.Hk) inv = 1.f / fmaxf(sqrtf(wave_sum(ss)), a.eps);
+#pragma unroll
+  for (int e = 0; e < kPer; ++e) {
+    const int i = lane + 64 * e;
+    if (i < n) dst[i] = j < 2 * a.Hk ? y[e] * inv : y[e];
+  }
+}
+
+bool bad_sections(const int* sections, int& R) {
+  if (!sections) return true;
+  R = 0;
+  for (int i = 0; i < 4; ++i) {
+    if (sections[i] < 0) return true;
+    R += sections[i];
+  }
+  return R <= 0;
+}
+
+}  // namespace
+}  // namespace alpx
+
+// ------------------------------------------------------------- C-ABI
+
+extern "C" int alpx_row_norm(const void* x, const float* weight, const void* gate, void* out,
+                             int64_t rows, int n, int64_t group_rows, int64_t group_stride,
+                             float eps, int mode, int dtype, int out_dtype, void* stream) {
+  using namespace alpx;
+  if (!x || !out) return fail(ALPX_EINVAL, "alpx_row_norm: null buffer");
+  if (!dtype_ok(dtype) || !dtype_ok(out_dtype)) return fail(ALPX_EINVAL, "alpx_row_norm: unknown dtype");
+  if (mode < kNormL2 || mode > kNormRmsGate) return fail(ALPX_EINVAL, "alpx_row_norm: unknown mode");
+  if (rows < 0 || n <= 0) return fail(ALPX_EINVAL, "alpx_row_norm: rows must be >= 0 and width positive");
+  if (!(eps > 0.f) || !isfinite(eps)) return fail(ALPX_EINVAL, "epsilon must be positive and finite");
+  if (mode != kNormL2 && !weight) return fail(ALPX_EINVAL, "alpx_row_norm: RMSNorm needs a weight");
+  if (mode == kNormRmsGate && !gate) return fail(ALPX_EINVAL, "alpx_row_norm: gated RMSNorm needs a gate");
+  if (group_rows <= 0) {
+    group_rows = rows > 0 ? rows : 1;
+    group_stride = group_rows * n;
+  }
+  if (group_stride < group_rows * n) return fail(ALPX_EINVAL, "alpx_row_norm: group stride smaller than its rows");
+  NormArgs a;
+  a.x = x;
+  a.w = weight;
+  a.gate = gate;
+  a.out = out;
+  a.rows = rows;
+  a.grp_rows = group_rows;
+  a.grp_stride = group_stride;
+  a.n = n;
+  a.eps = eps;
+  hipStream_t s = (hipStream_t)stream;
+  TimedRegion timed(ALPX_T_LAYER, s);
+  return run_norm(a, mode, dtype, out_dtype, s);
+}
+
+extern "C" int alpx_conv_step(const float* current, const float* weight, float* history,
+                              void* out, int batch, int channels, int kernel,
+                              int64_t weight_tap_stride, int64_t weight_channel_stride,
+                              int apply_silu, int out_dtype, void* stream) {
+  using namespace alpx;
+  if (!current || !weight || !out || (kernel > 1 && !history))
+    return fail(ALPX_EINVAL, "alpx_conv_step: null buffer");
+  if (!dtype_ok(out_dtype)) return fail(ALPX_EINVAL, "alpx_conv_step: unknown dtype");
+  if (batch <= 0 || channels <= 0 || kernel <= 0)
+    return fail(ALPX_EINVAL, "alpx_conv_step: sizes must be positive");
+  ConvArgs a;
+  a.cur = current;
+  a.w = weight;
+  a.hist = history;
+  a.out = out;
+  a.w_tap = weight_tap_stride;
+  a.w_ch = weight_channel_stride;
+  a.B = batch;
+  a.C = channels;
+  a.K = kernel;
+  a.silu = apply_silu ? 1 : 0;
+  hipStream_t s = (hipStream_t)stream;
+  TimedRegion timed(ALPX_T_LAYER, s);
+  const dim3 grid((unsigned)(((int64_t)batch * channels + 255) / 256));
+  switch (out_dtype) {
+    case ALPX_F32: hipLaunchKernelGGL(conv_step_kernel<float>, grid, dim3(256), 0, s, a); break;
+    case ALPX_F16: hipLaunchKernelGGL(conv_step_kernel<f16_t>, grid, dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL(conv_step_kernel<bf16_t>, grid, dim3(256), 0, s, a); break;
+  }
+  return check_launch("alpx_conv_step");
+}
+
+extern "C" int alpx_recurrent_parameters(const float* beta_logits, const float* alpha_logits,
+                                         const float* dt_bias, const float* ssm_a, float* beta,
+                                         float* log_decay, int64_t count, int heads,
+                                         void* stream) {
+  using namespace alpx;
+  if (!beta_logits || !alpha_logits || !dt_bias || !ssm_a || !beta || !log_decay)
+    return fail(ALPX_EINVAL, "alpx_recurrent_parameters: null buffer");
+  if (count < 0 || heads <= 0 || count % heads != 0)
+    return fail(ALPX_EINVAL, "time-step bias and ssm_a must match value heads");
+  if (count == 0) return ALPX_OK;
+  hipStream_t s = (hipStream_t)stream;
+  TimedRegion timed(ALPX_T_LAYER, s);
+  hipLaunchKernelGGL(recurrent_params_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0,
+                     s, beta_logits, alpha_logits, dt_bias, ssm_a, beta, log_decay, count, heads);
+  return check_launch("alpx_recurrent_parameters");
+}
+
+extern "C" int alpx_imrope(const void* x, void* out, const int64_t* positions,
+                           int64_t position_stride, int64_t rows, int heads, int dim,
+                           const int* sections, double frequency_base, double frequency_scale,
+                           int dtype, int out_dtype, void* stream) {
+  using namespace alpx;
+  if (!x || !out || !positions) return fail(ALPX_EINVAL, "alpx_imrope: null buffer");
+  if (!dtype_ok(dtype) || !dtype_ok(out_dtype)) return fail(ALPX_EINVAL, "alpx_imrope: unknown dtype");
+  int R = 0;
+  if (bad_sections(sections, R)) return fail(ALPX_EINVAL, "IMRoPE requires at least one rotary pair");
+  if (rows < 0 || heads <= 0 || dim <= 0) return fail(ALPX_EINVAL, "alpx_imrope: sizes must be positive");
+  if (dim < 2 * R) return fail(ALPX_EINVAL, "IMRoPE input is shorter than twice the section sum");
+  if (!(frequency_base > 0.0) || !isfinite(frequency_base) || !(frequency_scale > 0.0) ||
+      !isfinite(frequency_scale))
+    return fail(ALPX_EINVAL, "frequency_base and frequency_scale must be positive and finite");
+  if (position_stride < 0) return fail(ALPX_EINVAL, "alpx_imrope: negative position stride");
+  if (rows == 0) return ALPX_OK;
+  RopeArgs a;
+  a.x = x;
+  a.out = out;
+  a.pos = positions;
+  a.rows = rows;
+  a.pos_stride = position_stride;
+  a.heads = heads;
+  a.dim = dim;
+  a.R = R;
+  for (int i = 0; i < 4; ++i) a.sec[i] = sections[i];
+  a.base = frequency_base;
+  a.scale = frequency_scale;
+  hipStream_t s = (hipStream_t)stream;
+  TimedRegion timed(ALPX_T_LAYER, s);
+  switch (dtype) {
+    case ALPX_F32: return launch_rope<float>(a, out_dtype, s);
+    case ALPX_F16: return launch_rope<f16_t>(a, out_dtype, s);
+    default: return launch_rope<bf16_t>(a, out_dtype, s);
+  }
+}
+
+extern "C" int alpx_attention_prologue(const void* query_gate, const void* key, const void* value,
+                                       const float* q_norm, const float* k_norm, void* query_out,
+                                       void* gate_out, void* key_cache, void* value_cache,
+                                       int dtype, int64_t capacity, int batch, int q_heads,
+                                       int kv_heads, int head_dim, int value_dim,
+                                       int64_t position, const int32_t* positions,
+                                       const int* sections, double frequency_base, float eps,
+                                       void* stream) {
+  using namespace alpx;
+  if (!query_gate || !key || !value || !q_norm || !k_norm || !query_out || !gate_out ||
+      !key_cache || !value_cache)
+    return fail(ALPX_EINVAL, "alpx_attention_prologue: null buffer");
+  if (!dtype_ok(dtype)) return fail(ALPX_EINVAL, "alpx_attention_prologue: unknown dtype");
+  if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || head_dim <= 0 || value_dim <= 0 || capacity <= 0)
+    return fail(ALPX_EINVAL, "alpx_attention_prologue: sizes must be positive");
+  if (q_heads % kv_heads != 0) return fail(ALPX_EINVAL, "attention query heads must be a multiple of KV heads");
+  if (head_dim > kMaxDim || value_dim > kMaxDim)
+    return fail(ALPX_EUNSUPPORTED, "alpx_attention_prologue: head dims above %d", kMaxDim);
+  int R = 0;
+  if (bad_sections(sections, R)) return fail(ALPX_EINVAL, "IMRoPE requires at least one rotary pair");
+  if (head_dim < 2 * R) return fail(ALPX_EINVAL, "IMRoPE input is shorter than twice the section sum");
+  if (!(frequency_base > 0.0) || !isfinite(frequency_base))
+    return fail(ALPX_EINVAL, "frequency_base must be positive and finite");
+  if (!(eps > 0.f) || !isfinite(eps)) return fail(ALPX_EINVAL, "epsilon must be positive and finite");
+  if (!positions && (position < 0 || position >= capacity))
+    return fail(ALPX_ERANGE, "attention cache position exceeds capacity");
+  ProArgs a;
+  a.qg = query_gate;
+  a.k = key;
+  a.v = value;
+  a.qw = q_norm;
+  a.kw = k_norm;
+  a.q_out = query_out;
+  a.g_out = gate_out;
+  a.kc = key_cache;
+  a.vc = value_cache;
+  a.positions = positions;
+  a.position = position;
+  a.capacity = capacity;
+  a.B = batch;
+  a.Hq = q_heads;
+  a.Hkv = kv_heads;
+  a.D = head_dim;
+  a.Dv = value_dim;
+  a.R = R;
+  for (int i = 0; i < 4; ++i) a.sec[i] = sections[i];
+  a.base = frequency_base;
+  a.eps = eps;
+  hipStream_t s = (hipStream_t)stream;
+  TimedRegion timed(ALPX_T_LAYER, s);
+  const int64_t waves = (int64_t)batch * (q_heads + 2 * kv_heads);
+  const dim3 grid((unsigned)((waves + 3) / 4));
+  switch (dtype) {
+    case ALPX_F32: hipLaunchKernelGGL(attn_prologue_kernel<float>, grid, dim3(256), 0, s, a); break;
+    case ALPX_F16: hipLaunchKernelGGL(attn_prologue_kernel<f16_t>, grid, dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL(attn_prologue_kernel<bf16_t>, grid, dim3(256), 0, s, a); break;
+  }
+  return check_launch("alpx_attention_prologue");
+}
+
+extern "C" size_t alpx_recurrent_step_workspace_bytes(int batch, int key_heads, int value_heads,
+                                                      int key_dim, int value_dim) {
+  if (batch <= 0 || key_heads <= 0 || value_heads <= 0 || key_dim <= 0 || value_dim <= 0) return 0;
+  const size_t b = (size_t)batch;
+  const size_t floats = b * (2 * (size_t)key_heads * key_dim + 2 * (size_t)value_heads * value_dim +
+                             2 * (size_t)value_heads);
+  return floats * sizeof(float) + 256;
+}
+
+extern "C" int alpx_recurrent_step(const float* current, const float* conv_weight,
+                                   int64_t weight_tap_stride, int64_t weight_channel_stride,
+                                   float* conv_history, int conv_kernel, const float* gate,
+                                   const float* beta_logits, const float* alpha_logits,
+                                   const float* dt_bias, const float* ssm_a,
+                                   const float* norm_weight, float* state, void* out,
+                                   void* workspace, size_t workspace_bytes, int batch,
+                                   int key_heads, int value_heads, int key_dim, int value_dim,
+                                   float eps, int out_dtype, void* stream) {
+  using namespace alpx;
+  if (!current || !conv_weight || (conv_kernel > 1 && !conv_history) || !gate || !beta_logits ||
+      !alpha_logits || !dt_bias || !ssm_a || !norm_weight || !state || !out || !workspace)
+    return fail(ALPX_EINVAL, "alpx_recurrent_step: null buffer");
+  if (!dtype_ok(out_dtype)) return fail(ALPX_EINVAL, "alpx_recurrent_step: unknown dtype");
+  if (batch <= 0 || key_heads <= 0 || value_heads <= 0 || key_dim <= 0 || value_dim <= 0 ||
+      conv_kernel <= 0)
+    return fail(ALPX_EINVAL, "alpx_recurrent_step: sizes must be positive");
+  if (value_heads % key_heads != 0) return fail(ALPX_EINVAL, "GDN value heads must be a multiple of key heads");
+  if (key_dim > 256 || value_dim > kMaxDim)
+    return fail(ALPX_EUNSUPPORTED, "alpx_recurrent_step: key dim above 256 or value dim above %d", kMaxDim);
+  if (!(eps > 0.f) || !isfinite(eps)) return fail(ALPX_EINVAL, "epsilon must be positive and finite");
+  const size_t need = alpx_recurrent_step_workspace_bytes(batch, key_heads, value_heads, key_dim, value_dim);
+  if (workspace_bytes < need)
+    return fail(ALPX_EINVAL, "alpx_recurrent_step: workspace of %zu bytes, %zu needed", workspace_bytes, need);
+  float* base = (float*)(((uintptr_t)workspace + 255) & ~(uintptr_t)255);
+  PrepArgs a;
+  a.cur = current;
+  a.w = conv_weight;
+  a.hist = conv_history;
+  a.bl = beta_logits;
+  a.al = alpha_logits;
+  a.dtb = dt_bias;
+  a.ssm = ssm_a;
+  a.q = base;
+  a.k = a.q + (size_t)batch * key_heads * key_dim;
+  a.v = a.k + (size_t)batch * key_heads * key_dim;
+  a.beta = a.v + (size_t)batch * value_heads * value_dim;
+  a.g = a.beta + (size_t)batch * value_heads;
+  float* o = a.g + (size_t)batch * value_heads;
+  a.w_tap = weight_tap_stride;
+  a.w_ch = weight_channel_stride;
+  a.B = batch;
+  a.K = conv_kernel;
+  a.Hk = key_heads;
+  a.Hv = value_heads;
+  a.Dk = key_dim;
+  a.Dv = value_dim;
+  a.eps = eps;
+  hipStream_t s = (hipStream_t)stream;
+  TimedRegion timed(ALPX_T_RECURRENT_STEP, s);
+  const int64_t waves = (int64_t)batch * (2 * key_heads + value_heads);
+  hipLaunchKernelGGL(recurrent_prep_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, a);
+  int rc = check_launch("alpx_recurrent_step prep");
+  if (rc != ALPX_OK) return rc;
+  rc = gdn_step_launch(state, a.q, a.k, a.v, a.beta, a.g, o, batch, key_heads, value_heads,
+                       key_dim, value_dim, ALPX_F32, ALPX_F32, s);
+  if (rc != ALPX_OK) return rc;
+  NormArgs na;
+  na.x = o;
+  na.w = norm_weight;
+  na.gate = gate;
+  na.out = out;
+  na.rows = (int64_t)batch * value_heads;
+  na.grp_rows = na.rows;
+  na.grp_stride = na.rows * value_dim;
+  na.n = value_dim;
+  na.eps = eps;
+  return run_norm(na, kNormRmsGate, ALPX_F32, out_dtype, s);
+}

@@ -10,6 +10,10 @@ Same names, argument order and layouts as the reference (qwen35_kernels.py):
 * ``qwen35_full_attention_prefill(queries [Tq, Hq, D], keys, values,
   prefix_length=0) -> [Tq, Hq, Dv]``: token t attends to cache rows
   ``0 .. prefix_length + t`` (qwen35_kernels.py:395-411)
+* the recurrent-layer helpers around the GDN step: ``qwen35_conv_step``
+  (:261-274), ``qwen35_normalize_qk`` (:277-287), ``qwen35_beta_decay``
+  (:290-307), ``qwen35_gated_rms`` (:335-352) and
+  ``qwen35_recurrent_layer`` (:349-360)
 
 NumPy in -> NumPy out (upload, compute on the device, download); torch
 device tensors in -> device tensor out.  All arithmetic runs in libalpx.so.
@@ -19,7 +23,7 @@ from __future__ import annotations
 
 import math
 
-from . import _host, _ops
+from . import _host, _lib, _ops
 
 
 def available() -> bool:
@@ -88,5 +92,93 @@ def qwen35_gdn_step(state_matrix, queries, keys, values, beta, log_decay):
     return out
 
 
-__all__ = ["available", "backend_name", "qwen35_full_attention_decode",
-           "qwen35_full_attention_prefill", "qwen35_gdn_step"]
+def _writeback(host_array, device_tensor):
+    """Copy a device result into a caller-owned NumPy array (in-place
+    contract of the reference's mutating helpers)."""
+    host_array[...] = device_tensor.cpu().numpy()
+
+
+def _check_inplace_host(array, what):
+    import numpy as np
+    if not (isinstance(array, np.ndarray) and array.dtype == np.float32
+            and array.flags.c_contiguous):
+        raise ValueError(f"{what} must be a contiguous float32 NumPy array (updated in place)")
+
+
+def qwen35_conv_step(current, weights, history):
+    """Depthwise causal convolution step + SiLU: ``current [C]``,
+    ``weights [C, K]``, ``history [K-1, C]`` (shifted in place).  Returns
+    ``(output [C], history)`` (qwen35_kernels.py:261-274)."""
+    torch = _host.torch_mod()
+    host = _host.is_host(current)
+    if host and len(history):
+        _check_inplace_host(history, "convolution history")
+    cur = _host.to_device(current, torch.float32)
+    w = _host.to_device(weights, torch.float32)
+    kernel = int(w.shape[1])
+    if int(w.shape[0]) != int(cur.shape[0]):
+        raise ValueError("convolution weights must match current channels")
+    hist = _host.to_device(history, torch.float32) if kernel > 1 else None
+    if hist is not None and tuple(hist.shape) != (kernel - 1, int(cur.shape[0])):
+        raise ValueError("convolution history must hold kernel - 1 rows of every channel")
+    out = _ops.conv_step(cur.unsqueeze(0), w, None if hist is None else hist.unsqueeze(0),
+                         weight_layout="ck", apply_silu=True)[0]
+    if host:
+        if hist is not None:
+            _writeback(history, hist)
+        return _host.to_host(out), history
+    if hist is not None and hist.data_ptr() != history.data_ptr():
+        history.copy_(hist)
+    return out, history
+
+
+def qwen35_normalize_qk(queries, keys, epsilon: float):
+    """Each head row divided by ``max(||row||, epsilon)``
+    (qwen35_kernels.py:277-287)."""
+    torch = _host.torch_mod()
+    host = _host.is_host(queries)
+    q = _host.to_device(queries, torch.float32)
+    k = _host.to_device(keys, torch.float32)
+    qn = _ops.row_norm(q, mode=_lib.NORM_L2, eps=float(epsilon))
+    kn = _ops.row_norm(k, mode=_lib.NORM_L2, eps=float(epsilon))
+    return (_host.to_host(qn), _host.to_host(kn)) if host else (qn, kn)
+
+
+def qwen35_beta_decay(beta_logits, alpha_logits, dt_bias, ssm_a):
+    """``(sigmoid(beta_logits), softplus(alpha_logits + dt_bias) * ssm_a)``
+    per value head (qwen35_kernels.py:290-307)."""
+    torch = _host.torch_mod()
+    host = _host.is_host(beta_logits)
+    b, a, d, s = (_host.to_device(x, torch.float32).reshape(-1)
+                  for x in (beta_logits, alpha_logits, dt_bias, ssm_a))
+    beta, g = _ops.recurrent_parameters(b.unsqueeze(0), a.unsqueeze(0), d, s)
+    return (_host.to_host(beta[0]), _host.to_host(g[0])) if host else (beta[0], g[0])
+
+
+def qwen35_gated_rms(values, weight, gates, epsilon: float):
+    """RMSNorm of each head row times ``silu(gates)``
+    (qwen35_kernels.py:335-352)."""
+    torch = _host.torch_mod()
+    host = _host.is_host(values)
+    v = _host.to_device(values, torch.float32)
+    w = _host.to_device(weight, torch.float32)
+    g = _host.to_device(gates, torch.float32)
+    out = _ops.row_norm(v, mode=_lib.NORM_RMS_GATE, eps=float(epsilon), weight=w, gate=g)
+    return _host.to_host(out) if host else out
+
+
+def qwen35_recurrent_layer(state_matrix, queries, keys, values, beta_logits, alpha_logits,
+                           dt_bias, ssm_a, norm_weight, gates, epsilon: float):
+    """Normalise q / k, form beta / log decay, run the GDN step on the
+    state (in place) and apply the gated RMSNorm; returns
+    ``(gated, queries, keys)`` with the normalised queries / keys
+    (qwen35_kernels.py:349-360)."""
+    queries, keys = qwen35_normalize_qk(queries, keys, epsilon)
+    beta, log_decay = qwen35_beta_decay(beta_logits, alpha_logits, dt_bias, ssm_a)
+    output = qwen35_gdn_step(state_matrix, queries, keys, values, beta, log_decay)
+    return qwen35_gated_rms(output, norm_weight, gates, epsilon), queries, keys
+
+
+__all__ = ["available", "backend_name", "qwen35_beta_decay", "qwen35_conv_step",
+           "qwen35_full_attention_decode", "qwen35_full_attention_prefill", "qwen35_gated_rms",
+           "qwen35_gdn_step", "qwen35_normalize_qk", "qwen35_recurrent_layer"]

@@ -479,6 +479,222 @@ class Qwen35RocmOps:
         self._same_dtype("sigmoid gate", values, gate)
         return _ops.sigmoid_gate(values, gate)
 
+    # ------------------------------------------------ layer primitives
+
+    def _fp32(self, value: Any, name: str, *, dimensions: int | None = None) -> Any:
+        value = self._tensor(value, name, dimensions=dimensions)
+        if value.dtype != self.torch.float32:
+            raise TypeError(f"{name} must use float32")
+        return value
+
+    def silu(self, values: Any) -> Any:
+        """``values * sigmoid(values)`` (qwen35_rocm_ops.py:276-278)."""
+        values = self._tensor(values, "SiLU input")
+        return _ops.silu(values)
+
+    def rms_norm(self, values: Any, weight: Any, epsilon: float) -> Any:
+        """Learned RMSNorm over the final axis (qwen35_rocm_ops.py:251-258)."""
+        values = self._tensor(values, "RMSNorm input")
+        weight = self._fp32(weight, "RMSNorm weight", dimensions=1)
+        epsilon = _positive_finite("epsilon", epsilon)
+        if not values.shape or int(values.shape[-1]) != int(weight.shape[0]):
+            raise ValueError("RMSNorm weight must match the input's final dimension")
+        return _ops.row_norm(values, mode=_lib.NORM_RMS, eps=epsilon, weight=weight)
+
+    def l2_normalize(self, values: Any, epsilon: float) -> Any:
+        """``values / max(||values||, epsilon)`` over the final axis
+        (qwen35_rocm_ops.py:260-268)."""
+        values = self._tensor(values, "L2 input")
+        epsilon = _positive_finite("epsilon", epsilon)
+        if not values.shape or int(values.shape[-1]) <= 0:
+            raise ValueError("L2 input final dimension must be nonempty")
+        return _ops.row_norm(values, mode=_lib.NORM_L2, eps=epsilon)
+
+    def recurrent_gate(self, values: Any, weight: Any, gate: Any, epsilon: float) -> Any:
+        """``rms_norm(values) * silu(gate)`` (qwen35_rocm_ops.py:292-296)."""
+        values = self._tensor(values, "RMSNorm input")
+        weight = self._fp32(weight, "RMSNorm weight", dimensions=1)
+        epsilon = _positive_finite("epsilon", epsilon)
+        if not values.shape or int(values.shape[-1]) != int(weight.shape[0]):
+            raise ValueError("RMSNorm weight must match the input's final dimension")
+        gate = self._tensor(gate, "recurrent SiLU gate")
+        self._same_shape(values, gate, "recurrent gate")
+        self._same_dtype("recurrent gate", values, gate)
+        return _ops.row_norm(values, mode=_lib.NORM_RMS_GATE, eps=epsilon, weight=weight,
+                             gate=gate)
+
+    def split_query_gate(self, projected: Any, *, query_heads: int,
+                         head_dimension: int) -> tuple[Any, Any]:
+        """Split the joint Q/gate projection: per head ``head_dimension``
+        query values then as many gate values (qwen35_rocm_ops.py:298-318)."""
+        projected = self._tensor(projected, "joint Q/gate projection")
+        heads = _positive_integer("query_heads", query_heads)
+        width = _positive_integer("head_dimension", head_dimension)
+        expected = heads * 2 * width
+        actual = int(projected.shape[-1]) if projected.shape else 0
+        if actual != expected:
+            raise ValueError(
+                f"joint Q/gate width is {actual}, expected "
+                f"{expected} ({heads} heads * Q/gate stride {2 * width})")
+        reshaped = projected.reshape(_shape(projected)[:-1] + (heads, 2 * width))
+        return reshaped[..., :width].contiguous(), reshaped[..., width:].contiguous()
+
+    def causal_convolution_step_(self, current: Any, weights: Any, history: Any) -> Any:
+        """Raw depthwise causal convolution of ``current [B, C]`` with
+        ``weights [K, C]``; ``history [B, K-1, C]`` shifts in place
+        (qwen35_rocm_ops.py:320-341).  SiLU is the separate ``silu``."""
+        current = self._fp32(current, "convolution current", dimensions=2)
+        weights = self._fp32(weights, "convolution weights", dimensions=2)
+        history = self._fp32(history, "convolution history", dimensions=3)
+        batch, channels = _shape(current)
+        kernel, weight_channels = _shape(weights)
+        if weight_channels != channels:
+            raise ValueError("convolution weights must match current channels")
+        if _shape(history) != (batch, kernel - 1, channels):
+            raise ValueError(
+                "convolution history must have shape "
+                f"{(batch, kernel - 1, channels)}, got {_shape(history)}")
+        return _ops.conv_step(current, weights, history if kernel > 1 else None)
+
+    def recurrent_parameters(self, beta_logits: Any, alpha_logits: Any, dt_bias: Any,
+                             ssm_a: Any) -> tuple[Any, Any]:
+        """``(sigmoid(beta_logits), softplus(alpha_logits + dt_bias) * ssm_a)``
+        (qwen35_rocm_ops.py:343-360)."""
+        beta_logits = self._fp32(beta_logits, "beta logits", dimensions=2)
+        alpha_logits = self._fp32(alpha_logits, "alpha logits", dimensions=2)
+        dt_bias = self._fp32(dt_bias, "time-step bias", dimensions=1)
+        ssm_a = self._fp32(ssm_a, "converted ssm_a", dimensions=1)
+        self._same_shape(beta_logits, alpha_logits, "recurrent parameter logits")
+        heads = int(beta_logits.shape[1])
+        if _shape(dt_bias) != (heads,) or _shape(ssm_a) != (heads,):
+            raise ValueError("time-step bias and ssm_a must match value heads")
+        return _ops.recurrent_parameters(beta_logits, alpha_logits, dt_bias, ssm_a)
+
+    def imrope(self, values: Any, position_lanes: Any, sections: Sequence[int], *,
+               frequency_base: float, frequency_scale: float = 1.0) -> Any:
+        """IMROPE with one position-lane vector ``(4,)`` (int64) for every
+        row (qwen35_rocm_ops.py:409-473); a ``[rows, 4]`` lane array gives
+        each row (all axes but the last) its own lanes (extension)."""
+        values = self._tensor(values, "IMRoPE input")
+        position_lanes = self._tensor(position_lanes, "IMRoPE position lanes",
+                                      allow_integer=True)
+        rows = values.numel() // max(1, int(values.shape[-1])) if values.shape else 0
+        if position_lanes.dtype != self.torch.int64 or (
+                _shape(position_lanes) != (4,) and _shape(position_lanes) != (rows, 4)):
+            raise ValueError("IMRoPE position lanes must be int64 shape (4,)")
+        if len(sections) != 4:
+            raise ValueError("IMRoPE requires four sections")
+        section = tuple(_nonnegative_integer("IMRoPE section", item) for item in sections)
+        rotary_pairs = sum(section)
+        if rotary_pairs <= 0:
+            raise ValueError("IMRoPE requires at least one rotary pair")
+        if not values.shape or int(values.shape[-1]) < 2 * rotary_pairs:
+            raise ValueError("IMRoPE input is shorter than twice the section sum")
+        base = _positive_finite("frequency_base", frequency_base)
+        scale = _positive_finite("frequency_scale", frequency_scale)
+        return _ops.imrope(values, position_lanes, section, frequency_base=base,
+                           frequency_scale=scale)
+
+    def attention_prologue_(self, query_gate: Any, key: Any, value: Any, query_norm: Any,
+                            key_norm: Any, key_cache: Any, value_cache: Any, *, position: int,
+                            sections: Sequence[int], frequency_base: float,
+                            epsilon: float) -> tuple[Any, Any, int]:
+        """Fused Qwen3.5 full-attention prologue for one decode token per
+        sequence (extension; the steps of qwen35_runtime.py:597-650): split
+        the joint projection ``query_gate [B, Hq * 2 D]``, RMSNorm the query
+        heads with ``query_norm`` and the key heads ``key [B, Hkv * D]`` with
+        ``key_norm``, IMROPE at the text position, and append the rotated
+        key and ``value [B, Hkv * Dv]`` at ``position``.  Returns
+        ``(query [B, Hq, D], gate [B, Hq, D], position + 1)``; pass the gate
+        to ``online_attention(..., gate=gate)``."""
+        key_cache = self._tensor(key_cache, "attention key cache", dimensions=4)
+        value_cache = self._tensor(value_cache, "attention value cache", dimensions=4)
+        capacity, batch, kv_heads, width = _shape(key_cache)
+        value_width = int(value_cache.shape[3])
+        query_gate = self._tensor(query_gate, "joint Q/gate projection", dimensions=2)
+        key = self._tensor(key, "attention key", dimensions=2)
+        value = self._tensor(value, "attention value", dimensions=2)
+        query_norm = self._fp32(query_norm, "query RMSNorm weight", dimensions=1)
+        key_norm = self._fp32(key_norm, "key RMSNorm weight", dimensions=1)
+        position = _nonnegative_integer("attention cache position", position)
+        if position >= capacity:
+            raise ValueError("attention cache position exceeds capacity")
+        if _shape(value_cache)[:3] != (capacity, batch, kv_heads):
+            raise ValueError("attention K/V cache capacity, batch, or heads differ")
+        if int(query_gate.shape[0]) != batch or int(query_gate.shape[1]) % (2 * width):
+            raise ValueError("joint Q/gate projection does not match the cache head width")
+        query_heads = int(query_gate.shape[1]) // (2 * width)
+        if query_heads % kv_heads:
+            raise ValueError("attention query heads must be a multiple of KV heads")
+        if _shape(key) != (batch, kv_heads * width) or _shape(value) != (batch,
+                                                                          kv_heads * value_width):
+            raise ValueError("attention key/value do not match cache token shape")
+        if _shape(query_norm) != (width,) or _shape(key_norm) != (width,):
+            raise ValueError("RMSNorm weight must match the head dimension")
+        self._same_dtype("attention prologue", query_gate, key, value, key_cache, value_cache)
+        if len(sections) != 4:
+            raise ValueError("IMRoPE requires four sections")
+        section = tuple(_nonnegative_integer("IMRoPE section", item) for item in sections)
+        query, gate = _ops.attention_prologue(
+            query_gate.reshape(batch, query_heads, 2 * width), key, value, query_norm, key_norm,
+            key_cache, value_cache, position=position, sections=section,
+            frequency_base=_positive_finite("frequency_base", frequency_base),
+            eps=_positive_finite("epsilon", epsilon))
+        return query, gate, position + 1
+
+    def recurrent_layer_step_(self, workspace: RocmRecurrentWorkspace, mixed: Any,
+                              convolution_weights: Any, gate: Any, beta_logits: Any,
+                              alpha_logits: Any, dt_bias: Any, ssm_a: Any, norm_weight: Any, *,
+                              key_heads: int, key_dimension: int, epsilon: float,
+                              out_dtype: Any = None) -> Any:
+        """One token of the Qwen3.5 recurrent (GDN) layer after its
+        projections, fused (extension; the chain of qwen35_numpy.py:63-131):
+        convolution + SiLU of ``mixed [B, 2 Hk Dk + Hv Dv]`` against the
+        workspace's history, split, Q/K L2 norm, recurrent parameters, the
+        GDN step on the workspace's delta state and the gated RMSNorm with
+        ``gate [B, Hv * Dv]``.  Both workspace tensors advance in place.
+        Returns ``[B, Hv * Dv]``."""
+        history = self._fp32(workspace.convolution_history, "convolution history",
+                             dimensions=3)
+        state = self._fp32(workspace.delta_state, "GDN state", dimensions=4)
+        mixed = self._fp32(mixed, "convolution current", dimensions=2)
+        weights = self._fp32(convolution_weights, "convolution weights", dimensions=2)
+        gate = self._fp32(gate, "recurrent SiLU gate", dimensions=2)
+        beta_logits = self._fp32(beta_logits, "beta logits", dimensions=2)
+        alpha_logits = self._fp32(alpha_logits, "alpha logits", dimensions=2)
+        dt_bias = self._fp32(dt_bias, "time-step bias", dimensions=1)
+        ssm_a = self._fp32(ssm_a, "converted ssm_a", dimensions=1)
+        norm_weight = self._fp32(norm_weight, "RMSNorm weight", dimensions=1)
+        batch, value_heads, value_width, key_width = _shape(state)
+        key_heads = _positive_integer("key_heads", key_heads)
+        key_dimension = _positive_integer("key_dimension", key_dimension)
+        if key_dimension != key_width:
+            raise ValueError("GDN query/key must match state batch and key dimension")
+        if value_heads % key_heads:
+            raise ValueError("GDN value heads must be a multiple of key heads")
+        channels = 2 * key_heads * key_width + value_heads * value_width
+        kernel = int(weights.shape[0])
+        if _shape(mixed) != (batch, channels) or _shape(weights) != (kernel, channels):
+            raise ValueError("convolution weights must match current channels")
+        if _shape(history) != (batch, kernel - 1, channels):
+            raise ValueError(
+                "convolution history must have shape "
+                f"{(batch, kernel - 1, channels)}, got {_shape(history)}")
+        if _shape(gate) != (batch, value_heads * value_width):
+            raise ValueError("recurrent gate must match batch, value heads and width")
+        if _shape(beta_logits) != (batch, value_heads) or _shape(alpha_logits) != (batch,
+                                                                                 value_heads):
+            raise ValueError("GDN beta must match batch and value heads")
+        if _shape(dt_bias) != (value_heads,) or _shape(ssm_a) != (value_heads,):
+            raise ValueError("time-step bias and ssm_a must match value heads")
+        if _shape(norm_weight) != (value_width,):
+            raise ValueError("RMSNorm weight must match the input's final dimension")
+        return _ops.recurrent_step(mixed, weights, history if kernel > 1 else None, gate,
+                                   beta_logits, alpha_logits, dt_bias, ssm_a, norm_weight, state,
+                                   key_heads=key_heads, key_dim=key_dimension,
+                                   eps=_positive_finite("epsilon", epsilon),
+                                   out_dtype=out_dtype)
+
 
 __all__ = [
     "Qwen35RocmOps",

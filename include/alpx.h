@@ -204,6 +204,116 @@ int alpx_sigmoid_gate(const void* values, const void* gate, void* out, int64_t n
                       int out_dtype, void* stream);
 
 /*
+ * SiLU: out[i] = values[i] * sigmoid(values[i]) (stable sigmoid), the
+ * activation between the convolution step and the split in the recurrent
+ * layer.  Replaces Qwen35RocmOps.silu (qwen35_rocm_ops.py:276-278) and
+ * qwen35_ops.silu (qwen35_ops.py:26-31).  out may alias values when the
+ * dtypes match.
+ */
+int alpx_silu(const void* values, void* out, int64_t n, int dtype, int out_dtype, void* stream);
+
+/*
+ * Qwen3.5 layer primitives around the kernels above (the decomposed ROCm
+ * operations of qwen35_rocm_ops.py and the NumPy/Numba helpers of
+ * qwen35_kernels.py / qwen35_ops.py).  Inputs and outputs are contiguous
+ * unless strides are given.
+ */
+
+/* Row-wise normalisation of `rows` rows of `n` values.  Input row r starts
+ * at element (r / group_rows) * group_stride + (r % group_rows) * n
+ * (group_rows <= 0: contiguous rows); gate and out rows are contiguous.
+ *   mode 0 (L2):       out = x / max(||x||_2, eps)
+ *     Qwen35RocmOps.l2_normalize (qwen35_rocm_ops.py:260-268),
+ *     qwen35_normalize_qk (qwen35_kernels.py:277-287),
+ *     tensor.l2_normalize (tensor.py:139-158);
+ *   mode 1 (RMS):      out = x / sqrt(mean(x^2) + eps) * weight
+ *     Qwen35RocmOps.rms_norm (qwen35_rocm_ops.py:251-258),
+ *     qwen35_ops.rms_norm (qwen35_ops.py:46-76), the per-head Q/K norms
+ *     of qwen35_runtime.py:625-630;
+ *   mode 2 (gated):    out = rms_norm(x) * silu(gate)
+ *     Qwen35RocmOps.recurrent_gate (qwen35_rocm_ops.py:292-296),
+ *     qwen35_gated_rms (qwen35_kernels.py:335-352).
+ * weight: fp32 [n] (modes 1, 2); x and gate use `dtype`, out `out_dtype`. */
+int alpx_row_norm(const void* x, const float* weight, const void* gate, void* out, int64_t rows,
+                  int n, int64_t group_rows, int64_t group_stride, float eps, int mode, int dtype,
+                  int out_dtype, void* stream);
+
+/* Depthwise causal convolution step, fp32 state:
+ *   out[b, c] = sum_{t < K-1} history[b, t, c] w(t, c) + current[b, c] w(K-1, c)
+ * then history[b] shifts by one row (oldest dropped, current appended) and,
+ * with apply_silu, out = silu(out).  w(t, c) = weight[t * weight_tap_stride
+ * + c * weight_channel_stride]: [K, C] (ROCm / GGUF order) is (C, 1), [C, K]
+ * (qwen35_kernels order) is (1, K).  Replaces
+ * Qwen35RocmOps.causal_convolution_step_ (qwen35_rocm_ops.py:320-341; no
+ * SiLU), qwen35_conv_step (qwen35_kernels.py:53-68, :261-274; with SiLU)
+ * and qwen35_ops.depthwise_causal_conv_step (qwen35_ops.py:218-258). */
+int alpx_conv_step(const float* current, const float* weight, float* history, void* out,
+                   int batch, int channels, int kernel, int64_t weight_tap_stride,
+                   int64_t weight_channel_stride, int apply_silu, int out_dtype, void* stream);
+
+/* GDN recurrent parameters for `count` = batch * heads entries (fp32):
+ * beta = sigmoid(beta_logits), log_decay = softplus(alpha_logits +
+ * dt_bias[i % heads]) * ssm_a[i % heads].  Replaces
+ * Qwen35RocmOps.recurrent_parameters (qwen35_rocm_ops.py:343-360) and
+ * qwen35_beta_decay (qwen35_kernels.py:290-307). */
+int alpx_recurrent_parameters(const float* beta_logits, const float* alpha_logits,
+                              const float* dt_bias, const float* ssm_a, float* beta,
+                              float* log_decay, int64_t count, int heads, void* stream);
+
+/* IMROPE (Qwen interleaved multi-section rotary embedding, NeoX half-split
+ * pairs) of x [rows, heads, dim]: with R = sum(sections) (host int[4]),
+ * pair p < R rotates coordinates (p, p + R) by theta = pos(lane(p)) *
+ * frequency_scale * frequency_base^(-2p / (2R)); coordinates >= 2R are
+ * copied.  positions: device int64, lanes (T, H, W, E) of row r at
+ * positions + r * position_stride (stride 0: one lane vector for all rows).
+ * Replaces Qwen35RocmOps.imrope (qwen35_rocm_ops.py:409-473) and
+ * qwen35_ops.imrope_rotate (qwen35_ops.py:138-215). */
+int alpx_imrope(const void* x, void* out, const int64_t* positions, int64_t position_stride,
+                int64_t rows, int heads, int dim, const int* sections, double frequency_base,
+                double frequency_scale, int dtype, int out_dtype, void* stream);
+
+/* Qwen3.5 full-attention decode prologue, fused, one token per sequence
+ * (qwen35_runtime.py:597-650): the joint projection query_gate [B, Hq, 2D]
+ * is split (Qwen35RocmOps.split_query_gate, qwen35_rocm_ops.py:298-318)
+ * into query_out [B, Hq, D] (RMSNorm with q_norm, then IMROPE) and
+ * gate_out [B, Hq, D]; key [B, Hkv, D] is RMSNormed with k_norm, rotated
+ * and written to key_cache[pos_b, b]; value [B, Hkv, Dv] is written to
+ * value_cache[pos_b, b] (caches [capacity, B, Hkv, D|Dv], as
+ * alpx_kv_append).  pos_b = positions[b] (device int32) or `position`;
+ * the IMROPE lanes are the text lanes (pos_b, pos_b, pos_b, 0)
+ * (qwen35_ops.imrope_text_position, qwen35_ops.py:102-108).  All tensors
+ * use `dtype`; norm weights are fp32.  Device positions outside
+ * [0, capacity) skip the cache writes. */
+int alpx_attention_prologue(const void* query_gate, const void* key, const void* value,
+                            const float* q_norm, const float* k_norm, void* query_out,
+                            void* gate_out, void* key_cache, void* value_cache, int dtype,
+                            int64_t capacity, int batch, int q_heads, int kv_heads, int head_dim,
+                            int value_dim, int64_t position, const int32_t* positions,
+                            const int* sections, double frequency_base, float eps, void* stream);
+
+/* Workspace bytes for alpx_recurrent_step. */
+size_t alpx_recurrent_step_workspace_bytes(int batch, int key_heads, int value_heads, int key_dim,
+                                           int value_dim);
+
+/* One token of the Qwen3.5 recurrent (GDN) layer after its projections,
+ * fused (qwen35_numpy.py:63-131, the recurrent half of
+ * qwen35_recurrent_layer, qwen35_kernels.py:349-360): conv step + SiLU of
+ * current [B, C] (C = 2 Hk Dk + Hv Dv) with conv_weight (strides as
+ * alpx_conv_step) and conv_history [B, K-1, C]; split into q [Hk, Dk],
+ * k [Hk, Dk], v [Hv, Dv]; L2-normalised q / k; beta / log decay from
+ * beta_logits, alpha_logits [B, Hv], dt_bias, ssm_a [Hv]; the GDN step on
+ * state [B, Hv, Dv, Dk] (alpx_gdn_step); then out [B, Hv * Dv] =
+ * gated RMSNorm with norm_weight [Dv] and gate [B, Hv * Dv].  All inputs
+ * fp32 (the reference's dtype); out in out_dtype.  Three launches. */
+int alpx_recurrent_step(const float* current, const float* conv_weight, int64_t weight_tap_stride,
+                        int64_t weight_channel_stride, float* conv_history, int conv_kernel,
+                        const float* gate, const float* beta_logits, const float* alpha_logits,
+                        const float* dt_bias, const float* ssm_a, const float* norm_weight,
+                        float* state, void* out, void* workspace, size_t workspace_bytes,
+                        int batch, int key_heads, int value_heads, int key_dim, int value_dim,
+                        float eps, int out_dtype, void* stream);
+
+/*
  * Kernel timing (measurement support, no reference counterpart: it serves
  * the roofline measurement of bench.py).  While enabled, each entry point
  * records a pair of HIP events on its launch stream around the kernel named
@@ -218,9 +328,11 @@ enum alpx_timed_kernel {
   ALPX_T_PREFILL = 3,
   ALPX_T_GDN_CHUNK = 4,
   ALPX_T_GDN_STEP = 5,
-  ALPX_T_AUX = 6
+  ALPX_T_AUX = 6,
+  ALPX_T_LAYER = 7,          /* layer primitives and the attention prologue */
+  ALPX_T_RECURRENT_STEP = 8  /* the whole fused recurrent-layer step */
 };
-#define ALPX_TIMING_KERNELS 7
+#define ALPX_TIMING_KERNELS 9
 int alpx_timing_enable(int enable);
 int alpx_timing_read(int kernel, double* total_ms, int64_t* launches);
 

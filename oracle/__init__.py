@@ -8,6 +8,10 @@ library replaces (alpaccaroo, mounted read-only as the reference tree):
   output gate.
 * ``oracle.gdn`` -- the gated delta-rule (GDN) recurrence, token-sequential,
   plus the GDN input preparation (L2 normalisation, beta/decay).
+* ``oracle.layer`` -- the Qwen3.5 layer primitives on either side of the
+  kernels: causal convolution step, SiLU, L2 / RMS / gated RMS norms, the
+  recurrent parameters, IMROPE, the query/gate split, and the composed
+  attention prologue and recurrent-layer step.
 * ``oracle.rope`` -- the llama "norm" (adjacent-pair) rotary embedding used
   to build prefill inputs.
 * ``oracle.inputs`` -- seeded synthetic inputs for the five benchmark
@@ -25,6 +29,6 @@ the mistake it would catch).  No function of this package is left
 "parity unpinned".
 """
 
-from . import attention, gdn, inputs, rope  # noqa: F401
+from . import attention, gdn, inputs, layer, rope  # noqa: F401
 
-__all__ = ["attention", "gdn", "inputs", "rope"]
+__all__ = ["attention", "gdn", "inputs", "layer", "rope"]

@@ -85,3 +85,40 @@ def test_facade_validation_mirrors_reference(pkg):
         m.Qwen35RocmOps(_capability=m.RocmCapability(False, "no device"))
     with pytest.raises(ValueError, match="positive integer"):
         ops.zeros((0, 2))
+
+
+def test_layer_entry_points_validate_without_gpu(pkg):
+    lib = pkg._lib.lib()
+    L = pkg._lib
+    fake = ctypes.c_void_p(256)  # never dereferenced: validation fails first
+    sec = (ctypes.c_int * 4)(11, 11, 10, 0)
+    bad = (ctypes.c_int * 4)(0, 0, 0, 0)
+    assert lib.alpx_row_norm(None, None, None, None, 4, 8, 0, 0, 1e-6, 0, 0, 0, None) == L.EINVAL
+    assert lib.alpx_row_norm(fake, None, None, fake, 4, 8, 0, 0, 1e-6, 1, 0, 0, None) == L.EINVAL
+    assert "weight" in L.last_error()
+    assert lib.alpx_row_norm(fake, fake, None, fake, 4, 8, 0, 0, 1e-6, 2, 0, 0, None) == L.EINVAL
+    assert "gate" in L.last_error()
+    assert lib.alpx_row_norm(fake, None, None, fake, 4, 8, 0, 0, 0.0, 0, 0, 0, None) == L.EINVAL
+    assert "epsilon" in L.last_error()
+    assert lib.alpx_conv_step(None, fake, fake, fake, 1, 4, 4, 4, 1, 0, 0, None) == L.EINVAL
+    assert lib.alpx_recurrent_parameters(fake, fake, fake, fake, fake, fake, 7, 2, None) == L.EINVAL
+    assert "value heads" in L.last_error()
+    assert lib.alpx_imrope(fake, fake, fake, 0, 4, 1, 64, bad, 1e4, 1.0, 0, 0, None) == L.EINVAL
+    assert "rotary pair" in L.last_error()
+    assert lib.alpx_imrope(fake, fake, fake, 0, 4, 1, 32, sec, 1e4, 1.0, 0, 0, None) == L.EINVAL
+    assert "shorter" in L.last_error()
+    rc = lib.alpx_attention_prologue(fake, fake, fake, fake, fake, fake, fake, fake, fake, 2, 64, 1,
+                                     16, 2, 256, 256, 64, None, sec, 1e7, 1e-6, None)
+    assert rc == L.ERANGE and "exceeds capacity" in L.last_error()
+    rc = lib.alpx_attention_prologue(fake, fake, fake, fake, fake, fake, fake, fake, fake, 2, 64, 1,
+                                     15, 2, 256, 256, 0, None, sec, 1e7, 1e-6, None)
+    assert rc == L.EINVAL and "multiple of KV heads" in L.last_error()
+    assert lib.alpx_recurrent_step_workspace_bytes(1, 16, 32, 128, 128) > 0
+    assert lib.alpx_recurrent_step_workspace_bytes(1, 0, 32, 128, 128) == 0
+    rc = lib.alpx_recurrent_step(fake, fake, 4, 1, fake, 4, fake, fake, fake, fake, fake, fake,
+                                 fake, fake, fake, 16, 1, 16, 32, 128, 128, 1e-6, 0, None)
+    assert rc == L.EINVAL and "workspace" in L.last_error()
+    rc = lib.alpx_recurrent_step(fake, fake, 4, 1, fake, 4, fake, fake, fake, fake, fake, fake,
+                                 fake, fake, fake, 1 << 30, 1, 16, 30, 128, 128, 1e-6, 0, None)
+    assert rc == L.EINVAL and "multiple of key heads" in L.last_error()
+    assert lib.alpx_silu(None, fake, 4, 0, 0, None) == L.EINVAL
