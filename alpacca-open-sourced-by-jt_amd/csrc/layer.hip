@@ -48,16 +48,18 @@ __device__ __forceinline__ int imrope_lane(int p, const int (&sec)[4], int R) {
   return 3;
 }
 
-// cos / sin of pair p's angle pos * scale * base^(-2 p / (2 R)), formed in
-// double precision: the angles reach 10^4-10^5 rad at long contexts, where a
-// float angle alone would carry an error of ~10^-3 rad.
-__device__ __forceinline__ void rope_cs(double pos, int p, int R, double base, double scale,
-                                        float& c, float& s) {
-  const double theta = pos * scale * pow(base, -2.0 * (double)p / (double)(2 * R));
-  double sd, cd;
-  sincos(theta, &sd, &cd);
-  c = (float)cd;
-  s = (float)sd;
+constexpr int kMaxPairs = kMaxDim / 2;
+
+// cos / sin of the angle pos * inv (inv = scale * base^(-2 p / (2 R)),
+// formed on the host in double precision).  The angle reaches 10^4-10^6 rad
+// at long contexts, where a float angle alone would be off by ~10^-3 rad,
+// so it is reduced modulo 2 pi in double precision first; sin / cos of the
+// reduced angle (|r| <= pi) are then taken in float.
+__device__ __forceinline__ void rope_cs(double pos, double inv, float& c, float& s) {
+  constexpr double kTwoPi = 6.283185307179586476925;
+  const double theta = pos * inv;
+  const double r = theta - kTwoPi * rint(theta * (1.0 / kTwoPi));
+  sincosf((float)r, &s, &c);
 }
 
 // ---------------------------------------------------------------- row norm
@@ -175,7 +177,7 @@ struct RopeArgs {
   int64_t rows, pos_stride;
   int heads, dim, R;
   int sec[4];
-  double base, scale;
+  double inv[kMaxPairs];  // scale * base^(-2 p / (2 R)) per pair p
 };
 
 // One thread per (row, head, j): j < R rotates the pair (j, j + R); the
@@ -193,7 +195,7 @@ __global__ void __launch_bounds__(256) imrope_kernel(RopeArgs a) {
   if (j < a.R) {
     const int lane = imrope_lane(j, a.sec, a.R);
     float c, s;
-    rope_cs((double)a.pos[row * a.pos_stride + lane], j, a.R, a.base, a.scale, c, s);
+    rope_cs((double)a.pos[row * a.pos_stride + lane], a.inv[j], c, s);
     const float x0 = to_f32(x[j]), x1 = to_f32(x[j + a.R]);
     o[j] = from_f32<TO>(x0 * c - x1 * s);
     o[j + a.R] = from_f32<TO>(x0 * s + x1 * c);
@@ -231,8 +233,8 @@ struct ProArgs {
   int64_t position, capacity;
   int B, Hq, Hkv, D, Dv, R;
   int sec[4];
-  double base;
   float eps;
+  double inv[kMaxPairs];  // base^(-2 p / (2 R)) per pair p
 };
 
 // One wave per (sequence, slot): slots 0 .. Hq - 1 are query heads (RMSNorm
@@ -264,35 +266,60 @@ __global__ void __launch_bounds__(256) attn_prologue_kernel(ProArgs a) {
   const T* src = is_q ? (const T*)a.qg + ((int64_t)b * a.Hq + h) * 2 * a.D
                       : (const T*)a.k + ((int64_t)b * a.Hkv + h) * a.D;
   const float* w = is_q ? a.qw : a.kw;
-  float ss = 0.f;
-  for (int i = lane; i < a.D; i += 64) {
-    const float x = to_f32(src[i]);
-    ss = fmaf(x, x, ss);
+  // Every load first (row, weight, gate half), then the reduction.
+  constexpr int kPer = kMaxDim / 64;
+  float x[kPer], wt[kPer];
+  T gv[kPer];
+#pragma unroll
+  for (int e = 0; e < kPer; ++e) {
+    const int i = lane + 64 * e;
+    if (i < a.D) {
+      x[e] = to_f32(src[i]);
+      wt[e] = w[i];
+      if (is_q) gv[e] = src[a.D + i];
+    }
   }
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < kPer; ++e)
+    if (lane + 64 * e < a.D) ss = fmaf(x[e], x[e], ss);
   ss = wave_sum(ss);
   const float den = sqrtf(ss / (float)a.D + a.eps);
   float* st = stage[wave];
-  for (int i = lane; i < a.D; i += 64) st[i] = to_f32(src[i]) / den * w[i];
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+#pragma unroll
+  for (int e = 0; e < kPer; ++e) {
+    const int i = lane + 64 * e;
+    if (i < a.D) {
+      x[e] = x[e] / den * wt[e];
+      st[i] = x[e];
+    }
+  }
   T* dst;
   if (is_q) {
     dst = (T*)a.q_out + ((int64_t)b * a.Hq + h) * a.D;
     T* gd = (T*)a.g_out + ((int64_t)b * a.Hq + h) * a.D;
-    for (int i = lane; i < a.D; i += 64) gd[i] = src[a.D + i];
+#pragma unroll
+    for (int e = 0; e < kPer; ++e)
+      if (lane + 64 * e < a.D) gd[lane + 64 * e] = gv[e];
   } else {
     if (!in_cache) return;
     dst = (T*)a.kc + ((pos * a.B + b) * a.Hkv + h) * a.D;
   }
+  // LDS traffic of one wave is processed in issue order, so the partner
+  // reads below see this wave's stores.
+  __builtin_amdgcn_wave_barrier();
   const double p = (double)pos;  // text position lanes (p, p, p, 0)
-  for (int i = lane; i < a.D; i += 64) {
-    float y = st[i];
+#pragma unroll
+  for (int e = 0; e < kPer; ++e) {
+    const int i = lane + 64 * e;
+    if (i >= a.D) continue;
+    float y = x[e];
     if (i < 2 * a.R) {
       const int pr = i < a.R ? i : i - a.R;
       const int ln = imrope_lane(pr, a.sec, a.R);
-      float c, s;
-      rope_cs(ln == 3 ? 0.0 : p, pr, a.R, a.base, 1.0, c, s);
-      y = i < a.R ? st[i] * c - st[i + a.R] * s : st[pr] * s + st[i] * c;
+      float c, sn;
+      rope_cs(ln == 3 ? 0.0 : p, a.inv[pr], c, sn);
+      y = i < a.R ? x[e] * c - st[i + a.R] * sn : st[pr] * sn + x[e] * c;
     }
     dst[i] = from_f32<T>(y);
   }
@@ -350,7 +377,25 @@ __global__ void __launch_bounds__(256) recurrent_prep_kernel(PrepArgs a) {
     }
   }
   constexpr int kPer = kMaxDim / 64;
-  float y[kPer];
+  constexpr int kTaps = 4;  // history rows held in registers (longer kernels loop)
+  const int64_t rowC = (int64_t)b * C;
+  float* hist = a.hist + (int64_t)b * (a.K - 1) * C;
+  // Every load of the lane's channels first: current sample, history taps
+  // and weights; then the convolutions; then the history shift and outputs.
+  float y[kPer], xc[kPer], hv[kPer][kTaps], wv[kPer][kTaps + 1];
+#pragma unroll
+  for (int e = 0; e < kPer; ++e) {
+    const int i = lane + 64 * e;
+    if (i >= n) continue;
+    const int c = c0 + i;
+    xc[e] = a.cur[rowC + c];
+#pragma unroll
+    for (int t = 0; t < kTaps; ++t)
+      if (t < a.K - 1) hv[e][t] = hist[(int64_t)t * C + c];
+#pragma unroll
+    for (int t = 0; t <= kTaps; ++t)
+      if (t < a.K) wv[e][t] = a.w[t * a.w_tap + c * a.w_ch];
+  }
   float ss = 0.f;
 #pragma unroll
   for (int e = 0; e < kPer; ++e) {
@@ -358,13 +403,18 @@ __global__ void __launch_bounds__(256) recurrent_prep_kernel(PrepArgs a) {
     y[e] = 0.f;
     if (i >= n) continue;
     const int c = c0 + i;
-    float* h = a.hist + (int64_t)b * (a.K - 1) * C + c;
-    const float x = a.cur[(int64_t)b * C + c];
     float acc = 0.f;
-    for (int t = 0; t < a.K - 1; ++t) acc = fmaf(h[(int64_t)t * C], a.w[t * a.w_tap + c * a.w_ch], acc);
-    acc = fmaf(x, a.w[(a.K - 1) * a.w_tap + c * a.w_ch], acc);
-    for (int t = 0; t + 1 < a.K - 1; ++t) h[(int64_t)t * C] = h[(int64_t)(t + 1) * C];
-    if (a.K > 1) h[(int64_t)(a.K - 2) * C] = x;
+#pragma unroll
+    for (int t = 0; t < kTaps; ++t)
+      if (t < a.K - 1) acc = fmaf(hv[e][t], wv[e][t], acc);
+    for (int t = kTaps; t < a.K - 1; ++t)  // kernels longer than kTaps + 1 taps
+      acc = fmaf(hist[(int64_t)t * C + c], a.w[t * a.w_tap + c * a.w_ch], acc);
+    float wl = 0.f;  // weight of the current sample (tap K - 1)
+#pragma unroll
+    for (int t = 0; t <= kTaps; ++t)
+      if (t == a.K - 1) wl = wv[e][t];
+    if (a.K - 1 > kTaps) wl = a.w[(a.K - 1) * a.w_tap + c * a.w_ch];
+    acc = fmaf(xc[e], wl, acc);
     y[e] = silu_f(acc);
     ss = fmaf(y[e], y[e], ss);
   }
@@ -373,8 +423,23 @@ __global__ void __launch_bounds__(256) recurrent_prep_kernel(PrepArgs a) {
 #pragma unroll
   for (int e = 0; e < kPer; ++e) {
     const int i = lane + 64 * e;
-    if (i < n) dst[i] = j < 2 * a.Hk ? y[e] * inv : y[e];
+    if (i >= n) continue;
+    const int c = c0 + i;
+    dst[i] = j < 2 * a.Hk ? y[e] * inv : y[e];
+    // shift the lane's history column: row t takes row t + 1, the last row
+    // takes the current sample
+#pragma unroll
+    for (int t = 0; t + 1 < kTaps; ++t)
+      if (t + 1 < a.K - 1) hist[(int64_t)t * C + c] = hv[e][t + 1];
+    for (int t = kTaps - 1; t + 1 < a.K - 1; ++t)
+      hist[(int64_t)t * C + c] = hist[(int64_t)(t + 1) * C + c];
+    if (a.K > 1) hist[(int64_t)(a.K - 2) * C + c] = xc[e];
   }
+}
+
+// scale * base^(-2 p / (2 R)) for p < R, in double precision.
+void inverse_frequencies(double* inv, int R, double base, double scale) {
+  for (int p = 0; p < R; ++p) inv[p] = scale * pow(base, -2.0 * (double)p / (double)(2 * R));
 }
 
 bool bad_sections(const int* sections, int& R) {
@@ -483,6 +548,7 @@ extern "C" int alpx_imrope(const void* x, void* out, const int64_t* positions,
   if (bad_sections(sections, R)) return fail(ALPX_EINVAL, "IMRoPE requires at least one rotary pair");
   if (rows < 0 || heads <= 0 || dim <= 0) return fail(ALPX_EINVAL, "alpx_imrope: sizes must be positive");
   if (dim < 2 * R) return fail(ALPX_EINVAL, "IMRoPE input is shorter than twice the section sum");
+  if (R > kMaxPairs) return fail(ALPX_EUNSUPPORTED, "alpx_imrope: more than %d rotary pairs", kMaxPairs);
   if (!(frequency_base > 0.0) || !isfinite(frequency_base) || !(frequency_scale > 0.0) ||
       !isfinite(frequency_scale))
     return fail(ALPX_EINVAL, "frequency_base and frequency_scale must be positive and finite");
@@ -498,8 +564,7 @@ extern "C" int alpx_imrope(const void* x, void* out, const int64_t* positions,
   a.dim = dim;
   a.R = R;
   for (int i = 0; i < 4; ++i) a.sec[i] = sections[i];
-  a.base = frequency_base;
-  a.scale = frequency_scale;
+  inverse_frequencies(a.inv, R, frequency_base, frequency_scale);
   hipStream_t s = (hipStream_t)stream;
   TimedRegion timed(ALPX_T_LAYER, s);
   switch (dtype) {
@@ -555,7 +620,7 @@ extern "C" int alpx_attention_prologue(const void* query_gate, const void* key, 
   a.Dv = value_dim;
   a.R = R;
   for (int i = 0; i < 4; ++i) a.sec[i] = sections[i];
-  a.base = frequency_base;
+  inverse_frequencies(a.inv, R, frequency_base, 1.0);
   a.eps = eps;
   hipStream_t s = (hipStream_t)stream;
   TimedRegion timed(ALPX_T_LAYER, s);

@@ -178,6 +178,90 @@ def bench_gdn(torch, ops, lib, *, steps, warmup, seed=5):
             "decode_kernel_gbs": step_bytes / (dk_ms * 1e-3) / 1e9}
 
 
+def bench_layers(torch, ops, lib, *, steps, warmup, seed=6):
+    """The two fused Qwen3.5 decode-step paths around the kernels.
+
+    * Attention layer at the C4 geometry (4 sequences, 16 q / 2 kv heads,
+      head_dim 256, bf16 cache of 32768 rows): fused prologue (query/gate
+      split, Q/K RMSNorm, IMROPE, append at row 32767) + split-K decode over
+      32768 rows with the fused sigmoid gate.  Bytes per step: the K/V rows
+      read (as C4) plus the prologue's projection reads and cache writes.
+    * Recurrent layer at the C5 geometry (16 k / 32 v heads, Dk = Dv = 128,
+      conv kernel 4, batch 1): conv + SiLU + split + Q/K L2 + beta/decay,
+      GDN step, gated RMSNorm.  Bytes per step: state read + write, conv
+      history read + write, conv weights, projections in, output out."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    dev = torch.device("cuda")
+    bf = torch.bfloat16
+    b, hq, hkv, d, ctx = 4, 16, 2, 256, 32768
+    K = torch.randn((ctx, b, hkv, d), generator=g, device=dev).to(bf)
+    V = torch.randn((ctx, b, hkv, d), generator=g, device=dev).to(bf)
+    qg = torch.randn((b, hq * 2 * d), generator=g, device=dev).to(bf)
+    kn = torch.randn((b, hkv * d), generator=g, device=dev).to(bf)
+    vn = torch.randn((b, hkv * d), generator=g, device=dev).to(bf)
+    qw = torch.rand((d,), generator=g, device=dev) + 0.5
+    kw = torch.rand((d,), generator=g, device=dev) + 0.5
+
+    def attn_step():
+        q, gate, _ = ops.attention_prologue_(qg, kn, vn, qw, kw, K, V, position=ctx - 1,
+                                             sections=(11, 11, 10, 0),
+                                             frequency_base=10000000.0, epsilon=1e-6)
+        return ops.online_attention(q, K, V, length=ctx, gate=gate)
+
+    a_ms = _timed_steps(torch, attn_step, steps, warmup)
+    lib.timing_enable(True)
+    for _ in range(steps):
+        attn_step()
+    torch.cuda.synchronize()
+    pro_ms = _kernel_avg_ms(lib, lib.T_LAYER)
+    lib.timing_enable(False)
+    es = 2
+    a_bytes = (2 * ctx * b * hkv * d * es + (hq * 2 * d + 2 * hkv * d) * b * es
+               + 2 * b * hkv * d * es + 2 * b * hq * d * es + b * hq * d * es)
+
+    bsz, hk, hv, dk, dv, kern = 1, 16, 32, 128, 128, 4
+    chn = 2 * hk * dk + hv * dv
+    ws = ops.initialize_recurrent_workspace(batch_size=bsz, convolution_kernel=kern,
+                                            convolution_channels=chn, value_heads=hv,
+                                            value_dimension=dv, key_dimension=dk)
+    mixed = torch.randn((bsz, chn), generator=g, device=dev)
+    cw = torch.randn((kern, chn), generator=g, device=dev) * 0.5
+    gate = torch.randn((bsz, hv * dv), generator=g, device=dev)
+    bl = torch.randn((bsz, hv), generator=g, device=dev)
+    al = torch.randn((bsz, hv), generator=g, device=dev)
+    dt = torch.randn((hv,), generator=g, device=dev)
+    ssm = -torch.exp(torch.rand((hv,), generator=g, device=dev) * 2 - 1)
+    nw = torch.rand((dv,), generator=g, device=dev) + 0.5
+
+    def rec_step():
+        return ops.recurrent_layer_step_(ws, mixed, cw, gate, bl, al, dt, ssm, nw,
+                                         key_heads=hk, key_dimension=dk, epsilon=1e-6)
+
+    r_ms = _timed_steps(torch, rec_step, steps, warmup)
+    lib.timing_enable(True)
+    for _ in range(steps):
+        rec_step()
+    torch.cuda.synchronize()
+    rk_ms = _kernel_avg_ms(lib, lib.T_RECURRENT_STEP)
+    lib.timing_enable(False)
+    r_bytes = (2 * bsz * hv * dv * dk * 4 + 2 * bsz * (kern - 1) * chn * 4 + kern * chn * 4
+               + bsz * chn * 4 + 2 * bsz * hv * dv * 4 + 2 * bsz * hv * 4 + 2 * hv * 4 + dv * 4)
+    return {
+        "attention_layer_c4": {
+            "us_per_step": round(a_ms * 1e3, 2),
+            "prologue_us": round(pro_ms * 1e3, 2),
+            "step_bytes": a_bytes,
+            "step_gbs": round(a_bytes / (a_ms * 1e-3) / 1e9, 1),
+            "frac_hbm": round(a_bytes / (a_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
+        "recurrent_layer_c5": {
+            "us_per_step": round(r_ms * 1e3, 2),
+            "three_kernel_us": round(rk_ms * 1e3, 2),
+            "step_bytes": r_bytes,
+            "kernel_gbs": round(r_bytes / (rk_ms * 1e-3) / 1e9, 1),
+            "frac_hbm": round(r_bytes / (rk_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
+    }
+
+
 def cpu_baseline_c2(q, K, V, batch, hkv, d, budget_s=12.0):
     """Time the oracle's two-pass llama decode (fp32, model.py:1246-1252) on
     the C2 workload; returns GB/s of algorithmic bytes and the sample."""
@@ -327,8 +411,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only-headline", action="store_true")
-    ap.add_argument("--workloads", default="c4,c3,c5,c1",
-                    help="comma list of secondary workloads to run (c1, c3, c4, c5)")
+    ap.add_argument("--workloads", default="c4,c3,c5,c1,layers",
+                    help="comma list of secondary workloads to run (c1, c3, c4, c5, layers)")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="run the counter-run workload (copy calibration + C2 steps)")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -394,6 +478,8 @@ def main() -> int:
             "us_per_step": round(c1["ms_per_step"] * 1e3, 2),
             "split_us": round(c1["split_ms"] * 1e3, 2),
             "combine_us": round(c1["combine_ms"] * 1e3, 2)}
+    if "layers" in wl:
+        extra.update(bench_layers(torch, ops, lib, steps=steps, warmup=warmup))
     extra["c2_combine_ms"] = round(c2["combine_ms"], 5)
 
     cpu = None

@@ -234,12 +234,14 @@ def test_attention_prologue_then_gated_decode(gpu, ops, dtype):
 
 # ------------------------------------------------ recurrent-layer step
 
-@pytest.mark.parametrize("batch,hk,hv,dk,dv", [(1, 16, 32, 128, 128), (2, 2, 4, 64, 96),
-                                               (3, 1, 2, 256, 40)])
-def test_recurrent_layer_step_matches_oracle_over_tokens(gpu, ops, batch, hk, hv, dk, dv):
+@pytest.mark.parametrize("batch,hk,hv,dk,dv,kernel", [(1, 16, 32, 128, 128, 4),
+                                                      (2, 2, 4, 64, 96, 4),
+                                                      (3, 1, 2, 256, 40, 4), (2, 2, 4, 64, 32, 6),
+                                                      (1, 2, 2, 32, 32, 2), (1, 2, 2, 32, 32, 1)])
+def test_recurrent_layer_step_matches_oracle_over_tokens(gpu, ops, batch, hk, hv, dk, dv, kernel):
     import torch
-    rng = np.random.default_rng(batch * 100 + hk)
-    kernel, eps, steps = 4, 1e-6, 6
+    rng = np.random.default_rng(batch * 100 + hk + kernel)
+    eps, steps = 1e-6, 6
     chn = 2 * hk * dk + hv * dv
     w = (rng.standard_normal((kernel, chn)) * 0.5).astype(np.float32)
     dt = rng.standard_normal(hv).astype(np.float32)
