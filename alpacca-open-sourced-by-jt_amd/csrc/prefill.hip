@@ -138,6 +138,60 @@ __device__ __forceinline__ void lds_dma16(i32x4 r, uint32_t lds, uint32_t voff) 
 template <int V>
 using Par = std::integral_constant<int, V>;
 
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(Par<B>());
+    static_for<B + 1, E>(f);
+  }
+}
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// LDS operand reads of the iteration block, issued as inline assembly so
+// that their order, and the distance between a read and the MFMA that
+// consumes it, is the kernel's and not the scheduler's (left to it, the
+// scheduler placed each read right in front of its consumer and exposed
+// the LDS latency on every MFMA pair).  The compiler does not track these
+// reads: lds_wait<N> waits until at most N LDS operations of the wave are
+// outstanding and, by taking the operand as a read-write register, keeps
+// every use of the operand behind the wait.  Nothing else in the block
+// issues LDS or scalar-memory operations, so the LDS counter holds exactly
+// these reads, in issue order.
+template <int OFS>
+__device__ __forceinline__ u32x2 lds_tr64(uint32_t addr) {
+  static_assert(OFS >= 0 && OFS < 65536, "LDS immediate offset is 16 bits");
+  u32x2 r;
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "n"(OFS));
+#else
+  (void)addr;
+  r = (u32x2){0u, 0u};
+#endif
+  return r;
+}
+template <int OFS>
+__device__ __forceinline__ u32x4 lds_b128(uint32_t addr) {
+  static_assert(OFS >= 0 && OFS < 65536, "LDS immediate offset is 16 bits");
+  u32x4 r;
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(r) : "v"(addr), "n"(OFS));
+#else
+  (void)addr;
+  r = (u32x4){0u, 0u, 0u, 0u};
+#endif
+  return r;
+}
+template <int N, typename X>
+__device__ __forceinline__ void lds_wait(X& x) {
+  static_assert(N >= 0 && N < 16, "lgkmcnt is 4 bits");
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(x) : "n"(N));
+#else
+  (void)x;
+#endif
+}
+
 // Marks a register value as used (and possibly changed) at this point, so
 // the work producing it stays before it (the compiler would otherwise sink
 // register-only work past the block barrier into the next iteration).
@@ -154,7 +208,6 @@ template <typename T, typename TO, int D, int BK, int NQB>
 __global__ void __launch_bounds__(256, 2)
 prefill_mfma(PrefillArgs a) {
   typedef typename Vec8<T>::type V8;
-  typedef typename Vec4<T>::type V4;
   constexpr int U = D / 8;                  // 16-byte units per row
   constexpr int kRowB = D * (int)sizeof(T);
   constexpr int kTileB = BK * kRowB;        // one K or V tile
@@ -222,23 +275,20 @@ prefill_mfma(PrefillArgs a) {
   }
 
   f32x4 o[NQB][MB];   // O^T[d = 16 mb + 4 quad + i][column]
-  f32x4 lsum[NQB];    // row sums of P, accumulated by MFMA (all four entries equal)
+  float lsum[NQB];    // this lane's share (its 4-key slices) of the column's sum of P
   float m[NQB], mc[NQB], pend[NQB];  // mc = m * c2 (0 while m = -inf)
 #pragma unroll
   for (int qb = 0; qb < NQB; ++qb) {
     m[qb] = -INFINITY;
     mc[qb] = 0.f;
     pend[qb] = 1.f;
-    lsum[qb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    lsum[qb] = 0.f;
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) o[qb][mb] = (f32x4){0.f, 0.f, 0.f, 0.f};
   }
   bool pend_any = false;
   const float c2 = a.scale_log2;
   const float thr = kRescale / c2;
-  V8 ones;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) ones[j] = from_f32<T>(1.0f);
 
   // Direct loads: wave-instruction q of a tile fills LDS bytes [1024 q,
   // 1024 q + 1024), lane L the 16 bytes at 1024 q + 16 L, i.e. row
@@ -286,48 +336,37 @@ prefill_mfma(PrefillArgs a) {
       vadr[xb][y] = tr_row * kRowB + (((8 * xb + 2 * y + ((hl & 3) >> 1)) ^ swz_v<kRowB>(tr_row)) * 16) +
                     (hl & 1) * 8;
 
-  // Scores (S^T tiles) of two tiles and P operands of two tiles, by parity.
-  f32x4 sc[2][KB][NQB];
+  // Scores (S^T tiles) of one tile -- the block reads tile j's scores
+  // before it writes tile j + 1's -- and P operands of two tiles, by parity.
+  f32x4 sc[KB][NQB];
   V8 pv[2][KK][NQB];
+  const uint32_t lbase = (uint32_t)(uintptr_t)(lds_void_t*)smem;
 
-  auto qk = [&](auto kpar, auto spar) __attribute__((always_inline)) {
-    constexpr int KP = decltype(kpar)::value, SP = decltype(spar)::value;
-    const char* kb0 = smem + KP * kTileB;
-#pragma unroll
-    for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-      for (int qb = 0; qb < NQB; ++qb) sc[SP][kb][qb] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  // QK of the first tile (before the loop), from K buffer 0.
+  auto qk_first = [&]() __attribute__((always_inline)) {
+    V8 ka[KS][KB];
+    static_for<0, KS>([&](auto ks_) __attribute__((always_inline)) {
+      constexpr int ks = decltype(ks_)::value;
+      static_for<0, KB>([&](auto kb_) __attribute__((always_inline)) {
+        constexpr int kb = decltype(kb_)::value;
+        ka[ks][kb] = __builtin_bit_cast(V8, lds_b128<kb * 16 * kRowB>(lbase + kadr[ks]));
+      });
+    });
+    lds_wait<0>(ka[0][0]);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
-        const V8 ka = *(const V8*)(kb0 + kb * 16 * kRowB + kadr[ks]);
+      for (int kb = 0; kb < KB; ++kb) pin(ka[ks][kb]);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int qb = 0; qb < NQB; ++qb)
-          sc[SP][kb][qb] = mfma16x16x32(ka, qv[qb][ks], sc[SP][kb][qb]);
-      }
+          sc[kb][qb] = mfma16x16x32(ka[ks][kb], qv[qb][ks],
+                                    ks == 0 ? (f32x4){0.f, 0.f, 0.f, 0.f} : sc[kb][qb]);
   };
-  auto pvmul = [&](auto vpar, auto ppar) __attribute__((always_inline)) {
-    constexpr int VP = decltype(vpar)::value, PP = decltype(ppar)::value;
-    const char* vb0 = smem + (2 + VP) * kTileB;
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk)
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
-        const uint32_t va0 = vadr[(mb >> 2) & (VXB - 1)][mb & 3] + 256 * (mb >> 3);
-        const V4 v0 = lds_read_tr4((const T*)(vb0 + 32 * kk * kRowB + va0));
-        const V4 v1 = lds_read_tr4((const T*)(vb0 + (32 * kk + 16) * kRowB + va0));
-        const V8 va = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
-#pragma unroll
-        for (int qb = 0; qb < NQB; ++qb) o[qb][mb] = mfma16x16x32(va, pv[PP][kk][qb], o[qb][mb]);
-      }
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk)
-#pragma unroll
-      for (int qb = 0; qb < NQB; ++qb) lsum[qb] = mfma16x16x32(ones, pv[PP][kk][qb], lsum[qb]);
-  };
-  auto mask = [&](auto spar, int t) {
-    constexpr int SP = decltype(spar)::value;
+  auto mask = [&](int t) __attribute__((always_inline)) {
     const int k0 = lo + t * BK;
 #pragma unroll
     for (int qb = 0; qb < NQB; ++qb) {
@@ -338,7 +377,7 @@ prefill_mfma(PrefillArgs a) {
         for (int i = 0; i < 4; ++i) {
           const int key = k0 + 16 * kb + 4 * quad + i;
           const bool ok = key < hi && key <= qrel && (a.window <= 0 || key > qrel - a.window);
-          sc[SP][kb][qb][i] = ok ? sc[SP][kb][qb][i] : -INFINITY;
+          sc[kb][qb][i] = ok ? sc[kb][qb][i] : -INFINITY;
         }
     }
   };
@@ -352,49 +391,37 @@ prefill_mfma(PrefillArgs a) {
   // column's first tile) does the wave take the exact column max across the
   // four lanes of each column (l, l ^ 16, l ^ 32, l ^ 48) and move m.  The
   // block then forms P against the settled m.
-  auto grow_check = [&](auto spar) __attribute__((always_inline)) {
-    constexpr int SP = decltype(spar)::value;
+  auto grow_check = [&]() __attribute__((always_inline)) {
     bool grow = false;
 #pragma unroll
     for (int qb = 0; qb < NQB; ++qb) {
-      float mx = sc[SP][0][qb][0];
+      float mx = sc[0][qb][0];
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[SP][kb][qb][i]);
+        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[kb][qb][i]);
       grow |= mx > m[qb] + thr;
     }
     return __ballot(grow) != 0;
   };
-  auto move_max = [&](auto spar) __attribute__((always_inline)) {
-    constexpr int SP = decltype(spar)::value;
+  auto move_max = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int qb = 0; qb < NQB; ++qb) {
-      float mx = sc[SP][0][qb][0];
+      float mx = sc[0][qb][0];
 #pragma unroll
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[SP][kb][qb][i]);
+        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[kb][qb][i]);
       mx = fmaxf(mx, __shfl_xor(mx, 16));
       mx = fmaxf(mx, __shfl_xor(mx, 32));
       const bool g = mx > m[qb] + thr;
       const float mn = g ? mx : m[qb];
       pend[qb] = g ? fast_exp2((m[qb] - mn) * c2) : 1.f;
+      lsum[qb] *= pend[qb];  // l takes tile j's P next, formed against the moved m
       pend_any |= __ballot(g) != 0;
       m[qb] = mn;
       mc[qb] = mn == -INFINITY ? 0.f : mn * c2;
     }
-  };
-  auto softmax = [&](auto spar) __attribute__((always_inline)) {
-    constexpr int SP = decltype(spar)::value;
-#pragma unroll
-    for (int qb = 0; qb < NQB; ++qb)
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          pv[SP][kb >> 1][qb][4 * (kb & 1) + i] =
-              from_f32<T>(fast_exp2(__builtin_fmaf(sc[SP][kb][qb][i], c2, -mc[qb])));
   };
   auto need_mask = [&](int t) {
     const int k0 = lo + t * BK;
@@ -402,9 +429,69 @@ prefill_mfma(PrefillArgs a) {
            (a.window > 0 && k0 <= rel0 + wt_last - a.window);
   };
 
+  // The interleaved block of iteration j (Q = parity of j - 1 and j + 1):
+  // operands 0 .. NV-1 are the V^T operands of PV(j - 1) (two transposing
+  // reads each, from V buffer 2 + Q), operands NV .. N-1 the K operands of
+  // QK(j + 1) (one read each, from K buffer Q).  Reads run L operands ahead
+  // of the MFMAs that consume them.  The softmax of tile j (scores in sc, P
+  // into pv[P], row sums into lsum) is spread over the first KB * NQB
+  // operand steps, all before the first QK MFMA overwrites sc.
+  auto block = [&](auto par) __attribute__((always_inline)) {
+    constexpr int P = decltype(par)::value;
+    constexpr int Q = P ^ 1;
+    constexpr int NV = KK * MB, NK = KS * KB, N = NV + NK;
+    constexpr int NS = KB * NQB;
+    constexpr int L = 4;
+    static_assert(NS <= NV, "the softmax must read the scores before QK overwrites them");
+    V8 opd[N];
+    auto issue = [&](auto oo) __attribute__((always_inline)) {
+      constexpr int O = decltype(oo)::value;
+      if constexpr (O < NV) {
+        constexpr int kk = O / MB, mb = O % MB;
+        constexpr int base = (2 + Q) * kTileB + 32 * kk * kRowB + 256 * (mb >> 3);
+        const uint32_t ad = lbase + vadr[(mb >> 2) & (VXB - 1)][mb & 3];
+        const u32x2 v0 = lds_tr64<base>(ad);
+        const u32x2 v1 = lds_tr64<base + 16 * kRowB>(ad);
+        opd[O] = __builtin_bit_cast(V8, (u32x4){v0.x, v0.y, v1.x, v1.y});
+      } else {
+        constexpr int ks = (O - NV) / KB, kb = (O - NV) % KB;
+        opd[O] = __builtin_bit_cast(V8, lds_b128<Q * kTileB + kb * 16 * kRowB>(lbase + kadr[ks]));
+      }
+    };
+    static_for<0, L>(issue);
+    static_for<0, N>([&](auto oo) __attribute__((always_inline)) {
+      constexpr int O = decltype(oo)::value;
+      if constexpr (O + L < N) issue(Par<O + L>());
+      // reads issued after operand O's: one per later operand, two per later V operand
+      constexpr int last = O + L < N ? O + L : N - 1;
+      constexpr int later_v = O + 1 < NV ? (last < NV ? last : NV - 1) - O : 0;
+      lds_wait<(last - O) + later_v>(opd[O]);
+      if constexpr (O < NV) {
+        constexpr int kk = O / MB, mb = O % MB;
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) o[qb][mb] = mfma16x16x32(opd[O], pv[Q][kk][qb], o[qb][mb]);
+      } else {
+        constexpr int ks = (O - NV) / KB, kb = (O - NV) % KB;
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb)
+          sc[kb][qb] = mfma16x16x32(opd[O], qv[qb][ks],
+                                    ks == 0 ? (f32x4){0.f, 0.f, 0.f, 0.f} : sc[kb][qb]);
+      }
+      if constexpr (O < NS) {
+        constexpr int kb = O / NQB, qb = O % NQB;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float p = fast_exp2(__builtin_fmaf(sc[kb][qb][i], c2, -mc[qb]));
+          lsum[qb] += p;
+          pv[P][kb >> 1][qb][4 * (kb & 1) + i] = from_f32<T>(p);
+        }
+      }
+    });
+  };
+
   // Iteration j: PV(j-1), softmax(j), QK(j+1) (tile indices), while the
   // direct loads of K(j+2) and V(j) land in the buffers iteration j-1 read.
-  auto iteration = [&](auto par, int j) {
+  auto iteration = [&](auto par, int j) __attribute__((always_inline)) {
     constexpr int P = decltype(par)::value;  // = j & 1
     // Nothing is outstanding here at run time (the previous iteration ended
     // with a full wait), but the compiler's wait tracking may still carry
@@ -416,27 +503,25 @@ prefill_mfma(PrefillArgs a) {
     if (j + 2 < nt) load_tile(kg, a.ks_pos, kofs, j + 2, P);
     if (j < nt) load_tile(vg, a.vs_pos, vofs, j, 2 + P);
     // Rescale for the m moved at tile j - 1 (O holds tiles <= j - 2 and is
-    // about to take PV(j - 1), formed against the moved m).
+    // about to take PV(j - 1), formed against the moved m; l was rescaled
+    // at the move, before it took tile j - 1's P).
     if (__builtin_expect(pend_any, 0)) {
 #pragma unroll
       for (int qb = 0; qb < NQB; ++qb) {
-        lsum[qb] *= pend[qb];
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) o[qb][mb] *= pend[qb];
         pend[qb] = 1.f;
       }
       pend_any = false;
     }
-    if (__builtin_expect(need_mask(j), 0)) mask(Par<P>(), j);
-    if (__builtin_expect(grow_check(Par<P>()), 0)) move_max(Par<P>());
+    if (__builtin_expect(need_mask(j), 0)) mask(j);
+    if (__builtin_expect(grow_check(), 0)) move_max();
     // One basic block of independent MFMA and VALU work.  At j = 0 the PV
     // step multiplies zeroed P by a zeroed V buffer; at j = nt the softmax
     // sees a fully masked tile (k0 >= hi) and its P is never used.
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_setprio(1);
-    pvmul(Par<P ^ 1>(), Par<P ^ 1>());
-    softmax(Par<P>());
-    qk(Par<P ^ 1>(), Par<P ^ 1>());
+    block(Par<P>());
     __builtin_amdgcn_s_setprio(0);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -450,7 +535,7 @@ prefill_mfma(PrefillArgs a) {
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) pin(pv[P][kk][qb]);
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb) pin(sc[P ^ 1][kb][qb]);
+      for (int kb = 0; kb < KB; ++kb) pin(sc[kb][qb]);
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -468,7 +553,7 @@ prefill_mfma(PrefillArgs a) {
   if (nt > 1) load_tile(kg, a.ks_pos, kofs, 1, 1);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  qk(Par<0>(), Par<0>());
+  qk_first();
   __syncthreads();  // K(0) fully read before iteration 0 refills its buffer
   for (int j = 0; j <= nt; j += 2) {
     iteration(Par<0>(), j);
@@ -477,7 +562,10 @@ prefill_mfma(PrefillArgs a) {
 
 #pragma unroll
   for (int qb = 0; qb < NQB; ++qb) {
-    const float lt = lsum[qb][0];
+    // the column's sum over its four lanes (l, l ^ 16, l ^ 32, l ^ 48)
+    float lt = lsum[qb];
+    lt += __shfl_xor(lt, 16);
+    lt += __shfl_xor(lt, 32);
     const float inv = lt > 0.f ? 1.0f / lt : 0.f;
     if (!cok[qb]) continue;
     TO* op = (TO*)a.out + ((int64_t)tok[qb] * a.q_heads + hq[qb]) * D + 4 * quad;
