@@ -59,6 +59,15 @@ SIGNATURES = {
                                          _c_int, _c_int, _c_i64, _c_ptr,
                                          ctypes.POINTER(ctypes.c_int), ctypes.c_double,
                                          _c_float, _c_ptr]),
+    "alpx_attention_prologue_chunk": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
+                                               _c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_int,
+                                               _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                               _c_i64, ctypes.POINTER(ctypes.c_int),
+                                               ctypes.c_double, _c_float, _c_ptr]),
+    "alpx_recurrent_prefill_prep": (_c_int, [_c_ptr, _c_ptr, _c_i64, _c_i64, _c_ptr, _c_int,
+                                             _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
+                                             _c_ptr, _c_ptr, _c_ptr, _c_int, _c_int, _c_int,
+                                             _c_int, _c_int, _c_float, _c_int, _c_ptr]),
     "alpx_recurrent_step_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int]),
     "alpx_recurrent_step": (_c_int, [_c_ptr, _c_ptr, _c_i64, _c_i64, _c_ptr, _c_int, _c_ptr,
                                      _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,

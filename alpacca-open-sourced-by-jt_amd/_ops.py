@@ -295,6 +295,61 @@ def attention_prologue(query_gate, key, value, q_norm, k_norm, key_cache, value_
     return query, gate
 
 
+def attention_prologue_chunk(query_gate, key, value, q_norm, k_norm, key_cache, value_cache, *,
+                             batch_index, position, sections, frequency_base, eps):
+    """Attention prologue for ``T`` consecutive tokens of cache sequence
+    ``batch_index`` at positions ``position ..``: ``query_gate [T, Hq, 2D]``,
+    ``key [T, Hkv, D]``, ``value [T, Hkv, Dv]``.  Returns
+    ``(query [T, Hq, D], gate [T, Hq, D])``."""
+    torch = _torch()
+    capacity, cache_batch, kv_heads, dim = (int(x) for x in key_cache.shape)
+    value_dim = int(value_cache.shape[3])
+    tokens, q_heads = int(query_gate.shape[0]), int(query_gate.shape[1])
+    query = torch.empty((tokens, q_heads, dim), dtype=key_cache.dtype, device=key_cache.device)
+    gate = torch.empty_like(query)
+    rc = _lib.lib().alpx_attention_prologue_chunk(
+        query_gate.data_ptr(), key.data_ptr(), value.data_ptr(), q_norm.data_ptr(),
+        k_norm.data_ptr(), query.data_ptr(), gate.data_ptr(), key_cache.data_ptr(),
+        value_cache.data_ptr(), _lib.dtype_code(torch, key_cache.dtype), capacity, cache_batch,
+        int(batch_index), tokens, q_heads, kv_heads, dim, value_dim, int(position),
+        _sections(sections), float(frequency_base), float(eps),
+        _lib.stream_handle(torch, key_cache.device))
+    _lib.check(rc)
+    return query, gate
+
+
+def recurrent_prefill_prep(current, conv_weight, conv_history, beta_logits, alpha_logits,
+                           dt_bias, ssm_a, *, key_heads, key_dim, value_heads, value_dim, eps,
+                           qkv_dtype, weight_layout="kc"):
+    """Recurrent-layer inputs for ``T`` consecutive tokens of one sequence
+    (all fp32 inputs): ``current [T, C]``, ``conv_history [K-1, C]`` (moved
+    on in place).  Returns ``(q [T, Hk, Dk], k, v [T, Hv, Dv]`` in
+    ``qkv_dtype``, ``beta [T, Hv], log_decay [T, Hv])``."""
+    torch = _torch()
+    tokens, channels = (int(x) for x in current.shape)
+    if weight_layout == "kc":
+        kernel = int(conv_weight.shape[0])
+        tap_stride, ch_stride = channels, 1
+    else:
+        kernel = int(conv_weight.shape[1])
+        tap_stride, ch_stride = 1, kernel
+    dev = current.device
+    q = torch.empty((tokens, int(key_heads), int(key_dim)), dtype=qkv_dtype, device=dev)
+    k = torch.empty_like(q)
+    v = torch.empty((tokens, int(value_heads), int(value_dim)), dtype=qkv_dtype, device=dev)
+    beta = torch.empty((tokens, int(value_heads)), dtype=torch.float32, device=dev)
+    g = torch.empty_like(beta)
+    rc = _lib.lib().alpx_recurrent_prefill_prep(
+        current.data_ptr(), conv_weight.data_ptr(), tap_stride, ch_stride,
+        None if conv_history is None else conv_history.data_ptr(), kernel,
+        beta_logits.data_ptr(), alpha_logits.data_ptr(), dt_bias.data_ptr(), ssm_a.data_ptr(),
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(), g.data_ptr(), tokens,
+        int(key_heads), int(value_heads), int(key_dim), int(value_dim), float(eps),
+        _lib.dtype_code(torch, qkv_dtype), _lib.stream_handle(torch, dev))
+    _lib.check(rc)
+    return q, k, v, beta, g
+
+
 def recurrent_step(current, conv_weight, conv_history, gate, beta_logits, alpha_logits, dt_bias,
                    ssm_a, norm_weight, state, *, key_heads, key_dim, eps, weight_layout="kc",
                    out_dtype=None):

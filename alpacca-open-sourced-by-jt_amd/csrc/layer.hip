@@ -229,9 +229,12 @@ struct ProArgs {
   void* g_out;       // [B, Hq, D]
   void* kc;          // [capacity, B, Hkv, D]
   void* vc;          // [capacity, B, Hkv, Dv]
-  const int32_t* positions;  // device [B] or null (then `position` for all)
+  const int32_t* positions;  // device [B] or null (then position + r pos_step for row r)
   int64_t position, capacity;
+  int64_t pos_step;  // 0: one token per sequence; 1: the rows are one sequence's chunk
   int B, Hq, Hkv, D, Dv, R;
+  int CB;            // cache batch count (cache row = pos * CB + cache sequence)
+  int bsel;          // < 0: row r is cache sequence r; else every row is cache sequence bsel
   int sec[4];
   float eps;
   double inv[kMaxPairs];  // base^(-2 p / (2 R)) per pair p
@@ -251,13 +254,14 @@ __global__ void __launch_bounds__(256) attn_prologue_kernel(ProArgs a) {
   if (id >= (int64_t)a.B * slots) return;
   const int b = (int)(id / slots);
   const int j = (int)(id - (int64_t)b * slots);
-  const int64_t pos = a.positions ? (int64_t)a.positions[b] : a.position;
+  const int64_t pos = a.positions ? (int64_t)a.positions[b] : a.position + b * a.pos_step;
   const bool in_cache = pos >= 0 && pos < a.capacity;
+  const int64_t crow = pos * a.CB + (a.bsel < 0 ? b : a.bsel);  // cache row of this token
   if (j >= a.Hq + a.Hkv) {  // value head
     const int h = j - a.Hq - a.Hkv;
     if (!in_cache) return;
     const T* src = (const T*)a.v + ((int64_t)b * a.Hkv + h) * a.Dv;
-    T* dst = (T*)a.vc + ((pos * a.B + b) * a.Hkv + h) * a.Dv;
+    T* dst = (T*)a.vc + (crow * a.Hkv + h) * a.Dv;
     for (int i = lane; i < a.Dv; i += 64) dst[i] = src[i];
     return;
   }
@@ -303,7 +307,7 @@ __global__ void __launch_bounds__(256) attn_prologue_kernel(ProArgs a) {
       if (lane + 64 * e < a.D) gd[lane + 64 * e] = gv[e];
   } else {
     if (!in_cache) return;
-    dst = (T*)a.kc + ((pos * a.B + b) * a.Hkv + h) * a.D;
+    dst = (T*)a.kc + (crow * a.Hkv + h) * a.D;
   }
   // LDS traffic of one wave is processed in issue order, so the partner
   // reads below see this wave's stores.
@@ -434,6 +438,119 @@ __global__ void __launch_bounds__(256) recurrent_prep_kernel(PrepArgs a) {
     for (int t = kTaps - 1; t + 1 < a.K - 1; ++t)
       hist[(int64_t)t * C + c] = hist[(int64_t)(t + 1) * C + c];
     if (a.K > 1) hist[(int64_t)(a.K - 2) * C + c] = xc[e];
+  }
+}
+
+// ----------------------------------- recurrent-layer prep over a chunk
+
+struct ChunkPrepArgs {
+  const float* x;     // [T, C] convolution inputs of T consecutive tokens
+  const float* w;     // conv weights, tap i / channel c at i * w_tap + c * w_ch
+  const float* hist;  // [K - 1, C] history before token 0 (row 0 oldest)
+  const float* bl;    // [T, Hv]
+  const float* al;    // [T, Hv]
+  const float* dtb;   // [Hv]
+  const float* ssm;   // [Hv]
+  void* q;            // out [T, Hk, Dk]
+  void* k;            // out [T, Hk, Dk]
+  void* v;            // out [T, Hv, Dv]
+  float* beta;        // out [T, Hv]
+  float* g;           // out [T, Hv]
+  int64_t w_tap, w_ch;
+  int T, K, Hk, Hv, Dk, Dv;
+  float eps;
+};
+
+// One wave per (token, head slot), as recurrent_prep_kernel, with token t's
+// convolution window taken from the extended sequence E = [history; x]:
+// tap i reads E row t + i (tap K - 1 is x[t]).  The history is read only;
+// conv_history_advance moves it on afterwards.
+template <typename TO>
+__global__ void __launch_bounds__(256) recurrent_chunk_prep_kernel(ChunkPrepArgs a) {
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int slots = 2 * a.Hk + a.Hv;
+  const int64_t id = (int64_t)blockIdx.x * 4 + wave;
+  if (id >= (int64_t)a.T * slots) return;
+  const int t = (int)(id / slots);
+  const int j = (int)(id - (int64_t)t * slots);
+  const int C = 2 * a.Hk * a.Dk + a.Hv * a.Dv;
+  int c0, n;
+  TO* dst;
+  if (j < 2 * a.Hk) {
+    c0 = j * a.Dk;
+    n = a.Dk;
+    dst = j < a.Hk ? (TO*)a.q + ((int64_t)t * a.Hk + j) * a.Dk
+                   : (TO*)a.k + ((int64_t)t * a.Hk + (j - a.Hk)) * a.Dk;
+  } else {
+    const int h = j - 2 * a.Hk;
+    c0 = 2 * a.Hk * a.Dk + h * a.Dv;
+    n = a.Dv;
+    dst = (TO*)a.v + ((int64_t)t * a.Hv + h) * a.Dv;
+    if (lane == 0) {
+      const int64_t th = (int64_t)t * a.Hv + h;
+      a.beta[th] = stable_sigmoid(a.bl[th]);
+      a.g[th] = softplus_f(a.al[th] + a.dtb[h]) * a.ssm[h];
+    }
+  }
+  constexpr int kPer = kMaxDim / 64;
+  constexpr int kTaps = 4;  // taps held in registers (longer kernels loop)
+  float y[kPer], xv[kPer][kTaps], wv[kPer][kTaps];
+  // every load first: the window rows and weights of the lane's channels
+#pragma unroll
+  for (int e = 0; e < kPer; ++e) {
+    const int i = lane + 64 * e;
+    if (i >= n) continue;
+    const int c = c0 + i;
+#pragma unroll
+    for (int tap = 0; tap < kTaps; ++tap) {
+      if (tap >= a.K) continue;
+      const int er = t + tap;  // E row
+      xv[e][tap] = er < a.K - 1 ? a.hist[(int64_t)er * C + c]
+                                : a.x[(int64_t)(er - (a.K - 1)) * C + c];
+      wv[e][tap] = a.w[tap * a.w_tap + c * a.w_ch];
+    }
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < kPer; ++e) {
+    const int i = lane + 64 * e;
+    y[e] = 0.f;
+    if (i >= n) continue;
+    const int c = c0 + i;
+    float acc = 0.f;
+#pragma unroll
+    for (int tap = 0; tap < kTaps; ++tap)
+      if (tap < a.K) acc = fmaf(xv[e][tap], wv[e][tap], acc);
+    for (int tap = kTaps; tap < a.K; ++tap) {  // kernels longer than kTaps taps
+      const int er = t + tap;
+      const float xe = er < a.K - 1 ? a.hist[(int64_t)er * C + c]
+                                    : a.x[(int64_t)(er - (a.K - 1)) * C + c];
+      acc = fmaf(xe, a.w[tap * a.w_tap + c * a.w_ch], acc);
+    }
+    y[e] = silu_f(acc);
+    ss = fmaf(y[e], y[e], ss);
+  }
+  float inv = 1.f;
+  if (j < 2 * a.Hk) inv = 1.f / fmaxf(sqrtf(wave_sum(ss)), a.eps);
+#pragma unroll
+  for (int e = 0; e < kPer; ++e) {
+    const int i = lane + 64 * e;
+    if (i < n) dst[i] = from_f32<TO>(j < 2 * a.Hk ? y[e] * inv : y[e]);
+  }
+}
+
+// History after the chunk: the last K - 1 rows of E = [history; x].  One
+// thread per channel walks the rows upward, so a history row it still has
+// to read (row T + r > r) is never overwritten first.
+__global__ void __launch_bounds__(256) conv_history_advance(float* hist, const float* x, int T,
+                                                            int K, int C) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= C) return;
+  for (int r = 0; r + 1 < K; ++r) {
+    const int er = T + r;
+    hist[(int64_t)r * C + c] =
+        er < K - 1 ? hist[(int64_t)er * C + c] : x[(int64_t)(er - (K - 1)) * C + c];
   }
 }
 
@@ -574,31 +691,35 @@ extern "C" int alpx_imrope(const void* x, void* out, const int64_t* positions,
   }
 }
 
-extern "C" int alpx_attention_prologue(const void* query_gate, const void* key, const void* value,
-                                       const float* q_norm, const float* k_norm, void* query_out,
-                                       void* gate_out, void* key_cache, void* value_cache,
-                                       int dtype, int64_t capacity, int batch, int q_heads,
-                                       int kv_heads, int head_dim, int value_dim,
-                                       int64_t position, const int32_t* positions,
-                                       const int* sections, double frequency_base, float eps,
-                                       void* stream) {
+namespace {
+// Shared by the decode (one token per sequence) and chunk (one sequence's
+// consecutive tokens) forms of the attention prologue.
+int attention_prologue_launch(const char* what, const void* query_gate, const void* key,
+                              const void* value, const float* q_norm, const float* k_norm,
+                              void* query_out, void* gate_out, void* key_cache,
+                              void* value_cache, int dtype, int64_t capacity, int rows,
+                              int cache_batch, int bsel, int64_t pos_step, int q_heads,
+                              int kv_heads, int head_dim, int value_dim, int64_t position,
+                              const int32_t* positions, const int* sections,
+                              double frequency_base, float eps, void* stream) {
   using namespace alpx;
   if (!query_gate || !key || !value || !q_norm || !k_norm || !query_out || !gate_out ||
       !key_cache || !value_cache)
-    return fail(ALPX_EINVAL, "alpx_attention_prologue: null buffer");
-  if (!dtype_ok(dtype)) return fail(ALPX_EINVAL, "alpx_attention_prologue: unknown dtype");
-  if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || head_dim <= 0 || value_dim <= 0 || capacity <= 0)
-    return fail(ALPX_EINVAL, "alpx_attention_prologue: sizes must be positive");
+    return fail(ALPX_EINVAL, "%s: null buffer", what);
+  if (!dtype_ok(dtype)) return fail(ALPX_EINVAL, "%s: unknown dtype", what);
+  if (rows <= 0 || cache_batch <= 0 || q_heads <= 0 || kv_heads <= 0 || head_dim <= 0 ||
+      value_dim <= 0 || capacity <= 0)
+    return fail(ALPX_EINVAL, "%s: sizes must be positive", what);
   if (q_heads % kv_heads != 0) return fail(ALPX_EINVAL, "attention query heads must be a multiple of KV heads");
   if (head_dim > kMaxDim || value_dim > kMaxDim)
-    return fail(ALPX_EUNSUPPORTED, "alpx_attention_prologue: head dims above %d", kMaxDim);
+    return fail(ALPX_EUNSUPPORTED, "%s: head dims above %d", what, kMaxDim);
   int R = 0;
   if (bad_sections(sections, R)) return fail(ALPX_EINVAL, "IMRoPE requires at least one rotary pair");
   if (head_dim < 2 * R) return fail(ALPX_EINVAL, "IMRoPE input is shorter than twice the section sum");
   if (!(frequency_base > 0.0) || !isfinite(frequency_base))
     return fail(ALPX_EINVAL, "frequency_base must be positive and finite");
   if (!(eps > 0.f) || !isfinite(eps)) return fail(ALPX_EINVAL, "epsilon must be positive and finite");
-  if (!positions && (position < 0 || position >= capacity))
+  if (!positions && (position < 0 || position + pos_step * (rows - 1) >= capacity))
     return fail(ALPX_ERANGE, "attention cache position exceeds capacity");
   ProArgs a;
   a.qg = query_gate;
@@ -613,7 +734,10 @@ extern "C" int alpx_attention_prologue(const void* query_gate, const void* key, 
   a.positions = positions;
   a.position = position;
   a.capacity = capacity;
-  a.B = batch;
+  a.pos_step = pos_step;
+  a.B = rows;
+  a.CB = cache_batch;
+  a.bsel = bsel;
   a.Hq = q_heads;
   a.Hkv = kv_heads;
   a.D = head_dim;
@@ -624,14 +748,49 @@ extern "C" int alpx_attention_prologue(const void* query_gate, const void* key, 
   a.eps = eps;
   hipStream_t s = (hipStream_t)stream;
   TimedRegion timed(ALPX_T_LAYER, s);
-  const int64_t waves = (int64_t)batch * (q_heads + 2 * kv_heads);
+  const int64_t waves = (int64_t)rows * (q_heads + 2 * kv_heads);
   const dim3 grid((unsigned)((waves + 3) / 4));
   switch (dtype) {
     case ALPX_F32: hipLaunchKernelGGL(attn_prologue_kernel<float>, grid, dim3(256), 0, s, a); break;
     case ALPX_F16: hipLaunchKernelGGL(attn_prologue_kernel<f16_t>, grid, dim3(256), 0, s, a); break;
     default: hipLaunchKernelGGL(attn_prologue_kernel<bf16_t>, grid, dim3(256), 0, s, a); break;
   }
-  return check_launch("alpx_attention_prologue");
+  return check_launch(what);
+}
+}  // namespace
+
+extern "C" int alpx_attention_prologue(const void* query_gate, const void* key, const void* value,
+                                       const float* q_norm, const float* k_norm, void* query_out,
+                                       void* gate_out, void* key_cache, void* value_cache,
+                                       int dtype, int64_t capacity, int batch, int q_heads,
+                                       int kv_heads, int head_dim, int value_dim,
+                                       int64_t position, const int32_t* positions,
+                                       const int* sections, double frequency_base, float eps,
+                                       void* stream) {
+  return attention_prologue_launch("alpx_attention_prologue", query_gate, key, value, q_norm,
+                                   k_norm, query_out, gate_out, key_cache, value_cache, dtype,
+                                   capacity, batch, batch, -1, 0, q_heads, kv_heads, head_dim,
+                                   value_dim, position, positions, sections, frequency_base, eps,
+                                   stream);
+}
+
+extern "C" int alpx_attention_prologue_chunk(const void* query_gate, const void* key,
+                                             const void* value, const float* q_norm,
+                                             const float* k_norm, void* query_out,
+                                             void* gate_out, void* key_cache, void* value_cache,
+                                             int dtype, int64_t capacity, int cache_batch,
+                                             int batch_index, int tokens, int q_heads,
+                                             int kv_heads, int head_dim, int value_dim,
+                                             int64_t position, const int* sections,
+                                             double frequency_base, float eps, void* stream) {
+  using namespace alpx;
+  if (batch_index < 0 || batch_index >= cache_batch)
+    return fail(ALPX_EINVAL, "batch_index exceeds the cache batch");
+  return attention_prologue_launch("alpx_attention_prologue_chunk", query_gate, key, value,
+                                   q_norm, k_norm, query_out, gate_out, key_cache, value_cache,
+                                   dtype, capacity, tokens, cache_batch, batch_index, 1, q_heads,
+                                   kv_heads, head_dim, value_dim, position, nullptr, sections,
+                                   frequency_base, eps, stream);
 }
 
 extern "C" size_t alpx_recurrent_step_workspace_bytes(int batch, int key_heads, int value_heads,
@@ -711,4 +870,65 @@ extern "C" int alpx_recurrent_step(const float* current, const float* conv_weigh
   na.n = value_dim;
   na.eps = eps;
   return run_norm(na, kNormRmsGate, ALPX_F32, out_dtype, s);
+}
+
+extern "C" int alpx_recurrent_prefill_prep(const float* current, const float* conv_weight,
+                                           int64_t weight_tap_stride, int64_t weight_channel_stride,
+                                           float* conv_history, int conv_kernel,
+                                           const float* beta_logits, const float* alpha_logits,
+                                           const float* dt_bias, const float* ssm_a, void* q_out,
+                                           void* k_out, void* v_out, float* beta_out,
+                                           float* log_decay_out, int tokens, int key_heads,
+                                           int value_heads, int key_dim, int value_dim, float eps,
+                                           int out_dtype, void* stream) {
+  using namespace alpx;
+  if (!current || !conv_weight || (conv_kernel > 1 && !conv_history) || !beta_logits ||
+      !alpha_logits || !dt_bias || !ssm_a || !q_out || !k_out || !v_out || !beta_out ||
+      !log_decay_out)
+    return fail(ALPX_EINVAL, "alpx_recurrent_prefill_prep: null buffer");
+  if (!dtype_ok(out_dtype)) return fail(ALPX_EINVAL, "alpx_recurrent_prefill_prep: unknown dtype");
+  if (tokens <= 0 || key_heads <= 0 || value_heads <= 0 || key_dim <= 0 || value_dim <= 0 ||
+      conv_kernel <= 0)
+    return fail(ALPX_EINVAL, "alpx_recurrent_prefill_prep: sizes must be positive");
+  if (value_heads % key_heads != 0) return fail(ALPX_EINVAL, "GDN value heads must be a multiple of key heads");
+  if (key_dim > kMaxDim || value_dim > kMaxDim)
+    return fail(ALPX_EUNSUPPORTED, "alpx_recurrent_prefill_prep: head dims above %d", kMaxDim);
+  if (!(eps > 0.f) || !isfinite(eps)) return fail(ALPX_EINVAL, "epsilon must be positive and finite");
+  ChunkPrepArgs a;
+  a.x = current;
+  a.w = conv_weight;
+  a.hist = conv_history;
+  a.bl = beta_logits;
+  a.al = alpha_logits;
+  a.dtb = dt_bias;
+  a.ssm = ssm_a;
+  a.q = q_out;
+  a.k = k_out;
+  a.v = v_out;
+  a.beta = beta_out;
+  a.g = log_decay_out;
+  a.w_tap = weight_tap_stride;
+  a.w_ch = weight_channel_stride;
+  a.T = tokens;
+  a.K = conv_kernel;
+  a.Hk = key_heads;
+  a.Hv = value_heads;
+  a.Dk = key_dim;
+  a.Dv = value_dim;
+  a.eps = eps;
+  hipStream_t s = (hipStream_t)stream;
+  TimedRegion timed(ALPX_T_LAYER, s);
+  const int64_t waves = (int64_t)tokens * (2 * key_heads + value_heads);
+  const dim3 grid((unsigned)((waves + 3) / 4));
+  switch (out_dtype) {
+    case ALPX_F32: hipLaunchKernelGGL(recurrent_chunk_prep_kernel<float>, grid, dim3(256), 0, s, a); break;
+    case ALPX_F16: hipLaunchKernelGGL(recurrent_chunk_prep_kernel<f16_t>, grid, dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL(recurrent_chunk_prep_kernel<bf16_t>, grid, dim3(256), 0, s, a); break;
+  }
+  int rc = check_launch("alpx_recurrent_prefill_prep");
+  if (rc != ALPX_OK || conv_kernel <= 1) return rc;
+  const int C = 2 * key_heads * key_dim + value_heads * value_dim;
+  hipLaunchKernelGGL(conv_history_advance, dim3((unsigned)((C + 255) / 256)), dim3(256), 0, s,
+                     conv_history, current, tokens, conv_kernel, C);
+  return check_launch("alpx_recurrent_prefill_prep (history)");
 }

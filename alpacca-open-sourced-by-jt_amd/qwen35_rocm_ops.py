@@ -695,6 +695,140 @@ class Qwen35RocmOps:
                                    eps=_positive_finite("epsilon", epsilon),
                                    out_dtype=out_dtype)
 
+    # ------------------------------------------------------ chunked prefill
+
+    def attention_layer_prefill_(self, query_gate: Any, key: Any, value: Any, query_norm: Any,
+                                 key_norm: Any, key_cache: Any, value_cache: Any, *,
+                                 position: int, sections: Sequence[int], frequency_base: float,
+                                 epsilon: float, batch_index: int = 0,
+                                 scale: float | None = None) -> tuple[Any, int]:
+        """A prefill chunk of the Qwen3.5 full-attention layer after its
+        projections (extension): the reference runs Qwen35Model._attention
+        once per token (qwen35_runtime.py:597-665, driven token by token by
+        prefill_state, qwen35_runtime.py:777-810); this runs the ``T`` tokens
+        of ``query_gate [T, Hq * 2 D]``, ``key [T, Hkv * D]`` and
+        ``value [T, Hkv * Dv]`` of cache sequence ``batch_index`` at
+        positions ``position .. position + T - 1`` as one fused prologue
+        (split, Q/K RMSNorm, IMROPE, cache append), one causal prefill
+        attention over the cache and one sigmoid gate.  Returns
+        ``(gated output [T, Hq, Dv], position + T)``."""
+        key_cache = self._tensor(key_cache, "attention key cache", dimensions=4)
+        value_cache = self._tensor(value_cache, "attention value cache", dimensions=4)
+        capacity, batch, kv_heads, width = _shape(key_cache)
+        value_width = int(value_cache.shape[3])
+        query_gate = self._tensor(query_gate, "joint Q/gate projection", dimensions=2)
+        key = self._tensor(key, "attention key", dimensions=2)
+        value = self._tensor(value, "attention value", dimensions=2)
+        query_norm = self._fp32(query_norm, "query RMSNorm weight", dimensions=1)
+        key_norm = self._fp32(key_norm, "key RMSNorm weight", dimensions=1)
+        position = _nonnegative_integer("attention cache position", position)
+        batch_index = _nonnegative_integer("batch_index", batch_index)
+        tokens = int(query_gate.shape[0])
+        if tokens <= 0:
+            raise ValueError("prefill chunk must hold at least one token")
+        if batch_index >= batch:
+            raise ValueError("batch_index exceeds the cache batch")
+        if position + tokens > capacity:
+            raise ValueError("attention cache position exceeds capacity")
+        if _shape(value_cache)[:3] != (capacity, batch, kv_heads):
+            raise ValueError("attention K/V cache capacity, batch, or heads differ")
+        if int(query_gate.shape[1]) % (2 * width):
+            raise ValueError("joint Q/gate projection does not match the cache head width")
+        query_heads = int(query_gate.shape[1]) // (2 * width)
+        if query_heads % kv_heads:
+            raise ValueError("attention query heads must be a multiple of KV heads")
+        if _shape(key) != (tokens, kv_heads * width) or _shape(value) != (tokens,
+                                                                           kv_heads * value_width):
+            raise ValueError("attention key/value do not match cache token shape")
+        if _shape(query_norm) != (width,) or _shape(key_norm) != (width,):
+            raise ValueError("RMSNorm weight must match the head dimension")
+        self._same_dtype("attention prefill", query_gate, key, value, key_cache, value_cache)
+        if len(sections) != 4:
+            raise ValueError("IMRoPE requires four sections")
+        section = tuple(_nonnegative_integer("IMRoPE section", item) for item in sections)
+        query, gate = _ops.attention_prologue_chunk(
+            query_gate.reshape(tokens, query_heads, 2 * width), key, value, query_norm,
+            key_norm, key_cache, value_cache, batch_index=batch_index, position=position,
+            sections=section, frequency_base=_positive_finite("frequency_base", frequency_base),
+            eps=_positive_finite("epsilon", epsilon))
+        attended = self.attention_prefill(query, key_cache, value_cache, position=position,
+                                          batch_index=batch_index, scale=scale)
+        return _ops.sigmoid_gate(attended, gate), position + tokens
+
+    def recurrent_layer_prefill_(self, workspace: RocmRecurrentWorkspace, mixed: Any,
+                                 convolution_weights: Any, gate: Any, beta_logits: Any,
+                                 alpha_logits: Any, dt_bias: Any, ssm_a: Any, norm_weight: Any,
+                                 *, key_heads: int, key_dimension: int, epsilon: float,
+                                 batch_index: int = 0, out_dtype: Any = None) -> Any:
+        """A prefill chunk of the Qwen3.5 recurrent (GDN) layer after its
+        projections (extension): the reference runs the per-token chain of
+        qwen35_numpy.py:63-131 / Qwen35Model._recurrent once per token
+        (qwen35_runtime.py:777-810); this runs the ``T`` tokens of
+        ``mixed [T, 2 Hk Dk + Hv Dv]``, ``gate [T, Hv * Dv]`` and the logits
+        ``[T, Hv]`` of workspace sequence ``batch_index`` as one convolution
+        prep (conv + SiLU over the chunk, split, Q/K L2 norm, beta / decay,
+        history moved on), the chunked GDN on the sequence's delta state and
+        one gated RMSNorm.  The chunked GDN takes its q / k / v in bf16 when
+        the MFMA path covers the shape (key_dimension 64 / 128 / 256, value
+        width a multiple of 16) and in fp32, token by token, otherwise.
+        Returns ``[T, Hv * Dv]``."""
+        torch = self.torch
+        history = self._fp32(workspace.convolution_history, "convolution history",
+                             dimensions=3)
+        state = self._fp32(workspace.delta_state, "GDN state", dimensions=4)
+        mixed = self._fp32(mixed, "convolution current", dimensions=2)
+        weights = self._fp32(convolution_weights, "convolution weights", dimensions=2)
+        gate = self._fp32(gate, "recurrent SiLU gate", dimensions=2)
+        beta_logits = self._fp32(beta_logits, "beta logits", dimensions=2)
+        alpha_logits = self._fp32(alpha_logits, "alpha logits", dimensions=2)
+        dt_bias = self._fp32(dt_bias, "time-step bias", dimensions=1)
+        ssm_a = self._fp32(ssm_a, "converted ssm_a", dimensions=1)
+        norm_weight = self._fp32(norm_weight, "RMSNorm weight", dimensions=1)
+        batch, value_heads, value_width, key_width = _shape(state)
+        key_heads = _positive_integer("key_heads", key_heads)
+        key_dimension = _positive_integer("key_dimension", key_dimension)
+        batch_index = _nonnegative_integer("batch_index", batch_index)
+        if batch_index >= batch:
+            raise ValueError("batch_index exceeds the workspace batch")
+        if key_dimension != key_width:
+            raise ValueError("GDN query/key must match state batch and key dimension")
+        if value_heads % key_heads:
+            raise ValueError("GDN value heads must be a multiple of key heads")
+        channels = 2 * key_heads * key_width + value_heads * value_width
+        kernel = int(weights.shape[0])
+        tokens = int(mixed.shape[0])
+        if tokens <= 0:
+            raise ValueError("prefill chunk must hold at least one token")
+        if _shape(mixed) != (tokens, channels) or _shape(weights) != (kernel, channels):
+            raise ValueError("convolution weights must match current channels")
+        if _shape(history) != (batch, kernel - 1, channels):
+            raise ValueError(
+                "convolution history must have shape "
+                f"{(batch, kernel - 1, channels)}, got {_shape(history)}")
+        if _shape(gate) != (tokens, value_heads * value_width):
+            raise ValueError("recurrent gate must match tokens, value heads and width")
+        if _shape(beta_logits) != (tokens, value_heads) or _shape(alpha_logits) != (tokens,
+                                                                                  value_heads):
+            raise ValueError("GDN beta must match tokens and value heads")
+        if _shape(dt_bias) != (value_heads,) or _shape(ssm_a) != (value_heads,):
+            raise ValueError("time-step bias and ssm_a must match value heads")
+        if _shape(norm_weight) != (value_width,):
+            raise ValueError("RMSNorm weight must match the input's final dimension")
+        eps = _positive_finite("epsilon", epsilon)
+        mfma = key_width in (64, 128, 256) and value_width % 16 == 0
+        qkv_dtype = torch.bfloat16 if mfma else torch.float32
+        q, k, v, beta, g = _ops.recurrent_prefill_prep(
+            mixed, weights, history[batch_index] if kernel > 1 else None, beta_logits,
+            alpha_logits, dt_bias, ssm_a, key_heads=key_heads, key_dim=key_width,
+            value_heads=value_heads, value_dim=value_width, eps=eps, qkv_dtype=qkv_dtype)
+        seq_state = state[batch_index:batch_index + 1]
+        attended = _ops.gdn_chunk(seq_state, q.unsqueeze(0), k.unsqueeze(0), v.unsqueeze(0),
+                                  beta.unsqueeze(0), g.unsqueeze(0), out_dtype=torch.float32)
+        return _ops.row_norm(attended.reshape(tokens * value_heads, value_width),
+                             mode=_lib.NORM_RMS_GATE, eps=eps, weight=norm_weight,
+                             gate=gate, out_dtype=torch.float32 if out_dtype is None
+                             else out_dtype).reshape(tokens, value_heads * value_width)
+
 
 __all__ = [
     "Qwen35RocmOps",

@@ -313,6 +313,45 @@ int alpx_recurrent_step(const float* current, const float* conv_weight, int64_t 
                         int batch, int key_heads, int value_heads, int key_dim, int value_dim,
                         float eps, int out_dtype, void* stream);
 
+/* Qwen3.5 full-attention prologue for a prefill chunk of one sequence:
+ * `tokens` consecutive tokens at positions position .. position + tokens - 1
+ * of cache sequence batch_index (caches [capacity, cache_batch, Hkv, D|Dv]).
+ * Row t of query_gate [T, Hq, 2D], key [T, Hkv, D], value [T, Hkv, Dv] is
+ * processed as alpx_attention_prologue processes one sequence's token at
+ * position + t, and its key / value rows land at cache row position + t.
+ * Replaces the prologue half of the reference's token-sequential prefill,
+ * one Qwen35Model._attention call per token (qwen35_runtime.py:597-650,
+ * driven by prefill_state, qwen35_runtime.py:777-810); the chunk then runs
+ * alpx_prefill_causal over the cache and alpx_sigmoid_gate. */
+int alpx_attention_prologue_chunk(const void* query_gate, const void* key, const void* value,
+                                  const float* q_norm, const float* k_norm, void* query_out,
+                                  void* gate_out, void* key_cache, void* value_cache, int dtype,
+                                  int64_t capacity, int cache_batch, int batch_index, int tokens,
+                                  int q_heads, int kv_heads, int head_dim, int value_dim,
+                                  int64_t position, const int* sections, double frequency_base,
+                                  float eps, void* stream);
+
+/* Qwen3.5 recurrent-layer inputs for a prefill chunk of one sequence: the
+ * depthwise causal convolution + SiLU of current [T, C] (C = 2 Hk Dk +
+ * Hv Dv; weights strided as alpx_conv_step) continuing conv_history
+ * [K-1, C], split into q_out / k_out [T, Hk, Dk] (L2-normalised) and
+ * v_out [T, Hv, Dv] in out_dtype, and beta_out / log_decay_out [T, Hv]
+ * from beta_logits / alpha_logits [T, Hv], dt_bias and ssm_a [Hv]; the
+ * history then advances to the chunk's last K-1 rows.  Token t's values
+ * equal those alpx_recurrent_step forms for it after tokens 0 .. t-1 (the
+ * per-token chain of qwen35_numpy.py:63-131 that the reference's
+ * token-sequential prefill runs, qwen35_runtime.py:777-810); the chunk
+ * then runs alpx_gdn_chunk_prefill and the gated alpx_row_norm.  All
+ * inputs fp32.  Two launches. */
+int alpx_recurrent_prefill_prep(const float* current, const float* conv_weight,
+                                int64_t weight_tap_stride, int64_t weight_channel_stride,
+                                float* conv_history, int conv_kernel, const float* beta_logits,
+                                const float* alpha_logits, const float* dt_bias,
+                                const float* ssm_a, void* q_out, void* k_out, void* v_out,
+                                float* beta_out, float* log_decay_out, int tokens, int key_heads,
+                                int value_heads, int key_dim, int value_dim, float eps,
+                                int out_dtype, void* stream);
+
 /*
  * Kernel timing (measurement support, no reference counterpart: it serves
  * the roofline measurement of bench.py).  While enabled, each entry point

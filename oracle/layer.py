@@ -203,3 +203,78 @@ def recurrent_layer_step(mixed, conv_w, history, gate, beta_logits, alpha_logits
         gt = np.asarray(gate[b], dtype=np.float64).reshape(value_heads, value_dim)
         out[b] = gated_rms_norm(o, norm_weight, gt, eps).reshape(-1)
     return out, new_hist
+
+
+def attention_layer_prefill(query_gate, key, value, q_norm, k_norm, eps, position, sections,
+                            base, key_cache, value_cache, *, round_rows=None):
+    """The reference's token-sequential prefill of one Qwen3.5 full-attention
+    layer after its projections (Qwen35Model.prefill_state ->
+    forward_token -> _attention per token, qwen35_runtime.py:597-665,
+    777-810) for one sequence: token t of ``query_gate [T, Hq * 2 D]``,
+    ``key [T, Hkv * D]``, ``value [T, Hkv * Dv]`` runs the decode prologue at
+    position ``position + t``, appends its rotated key / value at that cache
+    row (``key_cache [cap, Hkv, D]``, ``value_cache [cap, Hkv, Dv]``, updated
+    in place), attends over rows ``0 .. position + t`` and applies the
+    sigmoid gate.  ``round_rows`` (e.g. a bf16 rounding function) is applied
+    to each appended key / value row, as a cache of that dtype stores it.
+    Returns ``[T, Hq, Dv]``."""
+    from . import attention as A
+    query_gate = np.asarray(query_gate, dtype=np.float64)
+    tokens = query_gate.shape[0]
+    d = np.asarray(q_norm).shape[0]
+    hkv = np.asarray(key).shape[1] // d
+    out = []
+    for t in range(tokens):
+        pos = position + t
+        q, g, kr, v = attention_prologue(query_gate[t:t + 1], np.asarray(key)[t:t + 1],
+                                         np.asarray(value)[t:t + 1], q_norm, k_norm, eps,
+                                         [pos], sections, base)
+        krow, vrow = kr[0], v[0]
+        if round_rows is not None:
+            krow, vrow = round_rows(krow), round_rows(vrow)
+        key_cache[pos] = krow
+        value_cache[pos] = vrow
+        hq = q.shape[1]
+        att = A.attention_decode_twopass(q[0].reshape(-1), key_cache[:pos + 1],
+                                         value_cache[:pos + 1], hq // hkv, 1.0 / np.sqrt(d))
+        out.append(A.sigmoid_gate(att, g[0]))
+    return np.stack(out)
+
+
+def recurrent_layer_prefill(mixed, conv_w, history, gate, beta_logits, alpha_logits, dt_bias,
+                            ssm_a, norm_weight, state, *, key_heads, key_dim, value_heads,
+                            value_dim, eps, round_qkv=None):
+    """The reference's token-sequential prefill of one Qwen3.5 recurrent
+    layer after its projections (the per-token chain of
+    qwen35_numpy.py:63-131 run once per token by prefill_state,
+    qwen35_runtime.py:777-810) for one sequence: ``recurrent_layer_step``
+    on token t of ``mixed [T, C]``, ``gate [T, Hv * Dv]`` and the logits
+    ``[T, Hv]``, carrying ``history [K-1, C]`` and ``state [Hv, Dv, Dk]``
+    (updated in place).  ``round_qkv`` (e.g. bf16 rounding) is applied to
+    the normalised q / k and to v before the GDN step, as a path that feeds
+    the recurrence in that dtype does.  Returns ``(out [T, Hv * Dv],
+    new_history)``."""
+    mixed = np.asarray(mixed, dtype=np.float64)
+    hist = np.asarray(history, dtype=np.float64)[None].copy()
+    st = state[None]
+    outs = []
+    for t in range(mixed.shape[0]):
+        if round_qkv is None:
+            o, hist = recurrent_layer_step(
+                mixed[t:t + 1], conv_w, hist, np.asarray(gate)[t:t + 1],
+                np.asarray(beta_logits)[t:t + 1], np.asarray(alpha_logits)[t:t + 1], dt_bias,
+                ssm_a, norm_weight, st, key_heads=key_heads, key_dim=key_dim,
+                value_heads=value_heads, value_dim=value_dim, eps=eps)
+        else:
+            act, hist = conv_step(mixed[t:t + 1], conv_w, hist, apply_silu=True)
+            w = key_heads * key_dim
+            q = round_qkv(l2_normalize(act[0, :w].reshape(key_heads, key_dim), eps))
+            k = round_qkv(l2_normalize(act[0, w:2 * w].reshape(key_heads, key_dim), eps))
+            v = round_qkv(act[0, 2 * w:].reshape(value_heads, value_dim))
+            beta, g = recurrent_parameters(np.asarray(beta_logits)[t:t + 1],
+                                           np.asarray(alpha_logits)[t:t + 1], dt_bias, ssm_a)
+            og = gdn.gdn_step(st[0], q, k, v, beta[0], g[0])
+            gt = np.asarray(gate, dtype=np.float64)[t].reshape(value_heads, value_dim)
+            o = gated_rms_norm(og, norm_weight, gt, eps).reshape(1, -1)
+        outs.append(o[0])
+    return np.stack(outs), hist[0]

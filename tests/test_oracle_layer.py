@@ -264,3 +264,86 @@ def test_recurrent_layer_step_matches_composed_reference_chain():
 def test_conv_history_length_is_checked():
     with pytest.raises(ValueError):
         L.conv_step(np.zeros(3), np.zeros((4, 3)), np.zeros((2, 3)))
+
+
+# ------------------------------------------------------- chunked prefill
+
+def _attn_layer_inputs(rng, tokens, hq, hkv, d, dv):
+    qg = rng.standard_normal((tokens, hq * 2 * d))
+    k = rng.standard_normal((tokens, hkv * d))
+    v = rng.standard_normal((tokens, hkv * dv))
+    qn = 1.0 + 0.1 * rng.standard_normal(d)
+    kn = 1.0 + 0.1 * rng.standard_normal(d)
+    return qg, k, v, qn, kn
+
+
+def test_attention_layer_prefill_equals_the_batched_causal_form():
+    # The token-sequential chain (one decode per token) equals one causal
+    # prefill over the cache of the rotated queries: token t sees exactly
+    # the rows 0 .. position + t.  Catches an off-by-one in the visible
+    # range or a query rotated at the wrong position.
+    from oracle import attention as A
+    rng = _rng(11)
+    tokens, hq, hkv, d, dv, position = 9, 4, 2, 16, 16, 5
+    sections, base, eps = (3, 3, 2, 0), 10000.0, 1e-6
+    qg, k, v, qn, kn = _attn_layer_inputs(rng, tokens, hq, hkv, d, dv)
+    kc = np.zeros((position + tokens + 3, hkv, d))
+    vc = np.zeros((position + tokens + 3, hkv, dv))
+    kc[:position] = rng.standard_normal((position, hkv, d))
+    vc[:position] = rng.standard_normal((position, hkv, dv))
+    out = L.attention_layer_prefill(qg, k, v, qn, kn, eps, position, sections, base, kc, vc)
+    q, g = L.split_query_gate(qg, hq, d)
+    lanes = L.text_lanes(np.arange(position, position + tokens))[:, None, :]
+    qr = L.imrope(L.rms_norm(q, qn, eps), lanes, sections, base)
+    att = A.full_attention_prefill(qr, kc[:position + tokens], vc[:position + tokens],
+                                   prefix_length=position)
+    np.testing.assert_allclose(out, A.sigmoid_gate(att, g), rtol=1e-12, atol=1e-12)
+    # the appended rows are the rotated keys and raw values at their positions
+    kr = L.imrope(L.rms_norm(k.reshape(tokens, hkv, d), kn, eps), lanes, sections, base)
+    np.testing.assert_allclose(kc[position:position + tokens], kr, rtol=1e-12, atol=1e-12)
+    np.testing.assert_array_equal(vc[position:position + tokens], v.reshape(tokens, hkv, dv))
+    assert not kc[position + tokens:].any()
+
+
+def _extended_conv(mixed, conv_w, history):
+    # the chunk-form convolution: token t convolves rows t .. t + K - 1 of
+    # E = [history; mixed]; the new history is E's last K - 1 rows
+    e = np.concatenate((history, mixed), axis=0)
+    kernel = conv_w.shape[0]
+    out = np.stack([np.sum(e[t:t + kernel] * conv_w, axis=0) for t in range(mixed.shape[0])])
+    return L.silu(out), e[e.shape[0] - (kernel - 1):]
+
+
+def test_recurrent_layer_prefill_equals_chunk_form():
+    # The token-sequential chain equals the chunk form the device runs:
+    # convolution over E = [history; x], one GDN scan, one gated norm.
+    # Catches a window shifted by one row, a stale history row, or taps in
+    # reverse order -- and, with T < K - 1, a history that keeps old rows.
+    rng = _rng(12)
+    hk, hv, dk, dv, kernel, eps = 2, 4, 8, 8, 4, 1e-6
+    c = 2 * hk * dk + hv * dv
+    for tokens in (7, 2):
+        mixed = rng.standard_normal((tokens, c))
+        conv_w = rng.standard_normal((kernel, c))
+        hist = rng.standard_normal((kernel - 1, c))
+        gate = rng.standard_normal((tokens, hv * dv))
+        bl, al = rng.standard_normal((tokens, hv)), rng.standard_normal((tokens, hv))
+        dtb, ssm = rng.standard_normal(hv), -np.exp(rng.uniform(-1, 1, hv))
+        nw = 1.0 + 0.1 * rng.standard_normal(dv)
+        s0 = 0.1 * rng.standard_normal((hv, dv, dk))
+        st = s0.copy()
+        out, new_hist = L.recurrent_layer_prefill(
+            mixed, conv_w, hist, gate, bl, al, dtb, ssm, nw, st, key_heads=hk, key_dim=dk,
+            value_heads=hv, value_dim=dv, eps=eps)
+        act, want_hist = _extended_conv(mixed, conv_w, hist)
+        np.testing.assert_array_equal(new_hist, want_hist)
+        w = hk * dk
+        q = L.l2_normalize(act[:, :w].reshape(tokens, hk, dk), eps)
+        k = L.l2_normalize(act[:, w:2 * w].reshape(tokens, hk, dk), eps)
+        v = act[:, 2 * w:].reshape(tokens, hv, dv)
+        beta, g = L.recurrent_parameters(bl, al, dtb, ssm)
+        s2 = s0.copy()
+        o = G.gdn_scan(s2, q, k, v, beta, g)
+        want = L.gated_rms_norm(np.asarray(o), nw, gate.reshape(tokens, hv, dv), eps)
+        np.testing.assert_allclose(out, want.reshape(tokens, -1), rtol=1e-11, atol=1e-12)
+        np.testing.assert_allclose(st, s2, rtol=1e-11, atol=1e-13)
