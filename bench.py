@@ -262,6 +262,81 @@ def bench_layers(torch, ops, lib, *, steps, warmup, seed=6):
     }
 
 
+def bench_layer_prefill(torch, ops, lib, *, steps, warmup, seed=7):
+    """The chunked Qwen3.5 layer prefill against the device's own
+    token-by-token path (the reference's prefill is token-sequential).
+
+    * Attention layer, Qwen3.5 head geometry (16 q / 2 kv heads, head_dim
+      256, bf16), one sequence: a 2048-token chunk at position 2048 of a
+      4096-row cache -- chunk prologue + causal prefill + sigmoid gate.
+      FLOPs count causal-valid pairs (4 D Hq per pair).  Token path: 2048 x
+      (decode prologue + gated split-K decode).
+    * Recurrent layer, C5 geometry (16 k / 32 v heads, Dk = Dv = 128, conv
+      kernel 4): a 1024-token chunk -- chunk prep + chunked GDN + gated
+      RMSNorm.  Token path: 1024 fused recurrent-layer steps."""
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    dev = torch.device("cuda")
+    bf = torch.bfloat16
+    hq, hkv, d, prefix, T = 16, 2, 256, 2048, 2048
+    sec, base, eps = (11, 11, 10, 0), 10000000.0, 1e-6
+    K = torch.randn((prefix + T, 1, hkv, d), generator=g, device=dev).to(bf)
+    V = torch.randn((prefix + T, 1, hkv, d), generator=g, device=dev).to(bf)
+    qg = torch.randn((T, hq * 2 * d), generator=g, device=dev).to(bf)
+    kn = torch.randn((T, hkv * d), generator=g, device=dev).to(bf)
+    vn = torch.randn((T, hkv * d), generator=g, device=dev).to(bf)
+    qw = torch.rand((d,), generator=g, device=dev) + 0.5
+    kw = torch.rand((d,), generator=g, device=dev) + 0.5
+    chunk = lambda: ops.attention_layer_prefill_(  # noqa: E731
+        qg, kn, vn, qw, kw, K, V, position=prefix, sections=sec, frequency_base=base,
+        epsilon=eps)
+    a_ms = _timed_steps(torch, chunk, max(3, steps // 5), 2)
+
+    def tokens_attn():
+        for t in range(T):
+            q, gate, _ = ops.attention_prologue_(qg[t:t + 1], kn[t:t + 1], vn[t:t + 1], qw, kw,
+                                                 K, V, position=prefix + t, sections=sec,
+                                                 frequency_base=base, epsilon=eps)
+            ops.online_attention(q, K, V, length=prefix + t + 1, gate=gate)
+
+    at_ms = _timed_steps(torch, tokens_attn, 2, 1)
+    pairs = sum(prefix + i + 1 for i in range(T))
+    a_flops = 4 * d * hq * pairs
+
+    hk, hv, dk, dv, kern, R = 16, 32, 128, 128, 4, 1024
+    chn = 2 * hk * dk + hv * dv
+    ws = ops.initialize_recurrent_workspace(batch_size=1, convolution_kernel=kern,
+                                            convolution_channels=chn, value_heads=hv,
+                                            value_dimension=dv, key_dimension=dk)
+    mixed = torch.randn((R, chn), generator=g, device=dev)
+    cw = torch.randn((kern, chn), generator=g, device=dev) * 0.5
+    gate = torch.randn((R, hv * dv), generator=g, device=dev)
+    bl = torch.randn((R, hv), generator=g, device=dev)
+    al = torch.randn((R, hv), generator=g, device=dev)
+    dt = torch.randn((hv,), generator=g, device=dev)
+    ssm = -torch.exp(torch.rand((hv,), generator=g, device=dev) * 2 - 1)
+    nw = torch.rand((dv,), generator=g, device=dev) + 0.5
+    rchunk = lambda: ops.recurrent_layer_prefill_(  # noqa: E731
+        ws, mixed, cw, gate, bl, al, dt, ssm, nw, key_heads=hk, key_dimension=dk, epsilon=eps)
+    r_ms = _timed_steps(torch, rchunk, max(3, steps // 5), 2)
+
+    def tokens_rec():
+        for t in range(R):
+            ops.recurrent_layer_step_(ws, mixed[t:t + 1], cw, gate[t:t + 1], bl[t:t + 1],
+                                      al[t:t + 1], dt, ssm, nw, key_heads=hk, key_dimension=dk,
+                                      epsilon=eps)
+
+    rt_ms = _timed_steps(torch, tokens_rec, 2, 1)
+    return {
+        "attention_layer_prefill_qwen35_2k_on_2k": {
+            "chunk_ms": round(a_ms, 4), "token_path_ms": round(at_ms, 3),
+            "speedup": round(at_ms / a_ms, 1), "flops": a_flops,
+            "chunk_tflops": round(a_flops / (a_ms * 1e-3) / 1e12, 1)},
+        "recurrent_layer_prefill_c5_1024": {
+            "chunk_ms": round(r_ms, 4), "token_path_ms": round(rt_ms, 3),
+            "speedup": round(rt_ms / r_ms, 1)},
+    }
+
+
 def cpu_baseline_c2(q, K, V, batch, hkv, d, budget_s=12.0):
     """Time the oracle's two-pass llama decode (fp32, model.py:1246-1252) on
     the C2 workload; returns GB/s of algorithmic bytes and the sample."""
@@ -411,8 +486,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only-headline", action="store_true")
-    ap.add_argument("--workloads", default="c4,c3,c5,c1,layers",
-                    help="comma list of secondary workloads to run (c1, c3, c4, c5, layers)")
+    ap.add_argument("--workloads", default="c4,c3,c5,c1,layers,lprefill",
+                    help="comma list of secondary workloads to run "
+                         "(c1, c3, c4, c5, layers, lprefill)")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="run the counter-run workload (copy calibration + C2 steps)")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -480,6 +556,8 @@ def main() -> int:
             "combine_us": round(c1["combine_ms"] * 1e3, 2)}
     if "layers" in wl:
         extra.update(bench_layers(torch, ops, lib, steps=steps, warmup=warmup))
+    if "lprefill" in wl:
+        extra.update(bench_layer_prefill(torch, ops, lib, steps=steps, warmup=warmup))
     extra["c2_combine_ms"] = round(c2["combine_ms"], 5)
 
     cpu = None
