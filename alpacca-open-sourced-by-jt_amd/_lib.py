@@ -28,6 +28,10 @@ SIGNATURES = {
     "alpx_device_arch": (_c_int, [_c_int, ctypes.c_char_p, _c_int]),
     "alpx_kv_append": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_int, _c_int,
                                 _c_int, _c_int, _c_int, _c_i64, _c_ptr, _c_ptr]),
+    "alpx_kv_export": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_int, _c_int,
+                                _c_int, _c_int, _c_int, _c_i64, _c_i64, _c_ptr]),
+    "alpx_kv_import": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_int, _c_int,
+                                _c_int, _c_int, _c_int, _c_i64, _c_i64, _c_ptr]),
     "alpx_decode_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int]),
     "alpx_decode_gqa": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr,
                                  _c_ptr, _c_size, _c_int, _c_int, _c_int, _c_int, _c_int,

@@ -37,6 +37,37 @@ def kv_append(key_cache, value_cache, key, value, *, position=None, positions=No
     _lib.check(rc)
 
 
+def kv_export(key_cache, value_cache, *, batch_index, row0, rows):
+    """Rows ``[row0, row0 + rows)`` of cache sequence ``batch_index`` as
+    contiguous fp32 ``(key [rows, Hkv, D], value [rows, Hkv, Dv])``."""
+    torch = _torch()
+    capacity, batch, kv_heads, dim = (int(x) for x in key_cache.shape)
+    value_dim = int(value_cache.shape[3])
+    dev = key_cache.device
+    k = torch.empty((rows, kv_heads, dim), dtype=torch.float32, device=dev)
+    v = torch.empty((rows, kv_heads, value_dim), dtype=torch.float32, device=dev)
+    rc = _lib.lib().alpx_kv_export(
+        key_cache.data_ptr(), value_cache.data_ptr(), k.data_ptr(), v.data_ptr(),
+        _lib.dtype_code(torch, key_cache.dtype), capacity, batch, kv_heads, dim, value_dim,
+        int(batch_index), int(row0), int(rows), _lib.stream_handle(torch, dev))
+    _lib.check(rc)
+    return k, v
+
+
+def kv_import(key_rows, value_rows, key_cache, value_cache, *, batch_index, row0):
+    """Writes fp32 rows ``[rows, Hkv, D|Dv]`` into cache sequence
+    ``batch_index`` from row ``row0`` (rounded to the cache dtype)."""
+    torch = _torch()
+    capacity, batch, kv_heads, dim = (int(x) for x in key_cache.shape)
+    value_dim = int(value_cache.shape[3])
+    rc = _lib.lib().alpx_kv_import(
+        key_rows.data_ptr(), value_rows.data_ptr(), key_cache.data_ptr(),
+        value_cache.data_ptr(), _lib.dtype_code(torch, key_cache.dtype), capacity, batch,
+        kv_heads, dim, value_dim, int(batch_index), int(row0), int(key_rows.shape[0]),
+        _lib.stream_handle(torch, key_cache.device))
+    _lib.check(rc)
+
+
 def decode(q, key_cache, value_cache, *, length, k_strides, v_strides, batch, kv_heads,
            seq_lens=None, gate=None, scale=None, out_dtype=None, out=None):
     """Split-K GQA decode.  ``q [B, Hq, D]`` contiguous; K/V addressed by

@@ -76,6 +76,28 @@ int alpx_kv_append(void* key_cache, void* value_cache, const void* key, const vo
                    int value_dim, int tokens, int64_t position, const int32_t* positions,
                    void* stream);
 
+/* K/V state transfer for one sequence of a cache [capacity, batch, kv_heads,
+ * key_dim|value_dim] (fp32 / fp16 / bf16, `dtype`): alpx_kv_export widens
+ * cache rows [row0, row0 + rows) of sequence batch_index into contiguous
+ * fp32 key_rows [rows, kv_heads, key_dim] and value_rows [rows, kv_heads,
+ * value_dim]; alpx_kv_import writes such fp32 rows into the cache, rounding
+ * to nearest even for fp16 / bf16 caches (bit-exact copies for fp32).  The
+ * fp32 rows are the reference's attention state layout and snapshot record
+ * (FullAttentionState.key / value and FullAttentionSnapshot, memory.py:
+ * 223-241, 385-475, "f32-le"), so export + a device-to-host copy gives the
+ * bytes of FullAttentionState.snapshot and a host-to-device copy + import
+ * restores one; an fp16 cache stores rows as the reference's half-precision
+ * device mirror does (ALPACCAROO_KV_F16, cuda.py:1729-1738; _sync_mirror,
+ * cuda.py:1875-1900).  Rows outside [0, capacity) fail with ALPX_ERANGE. */
+int alpx_kv_export(const void* key_cache, const void* value_cache, float* key_rows,
+                   float* value_rows, int dtype, int64_t capacity, int batch, int kv_heads,
+                   int key_dim, int value_dim, int batch_index, int64_t row0, int64_t rows,
+                   void* stream);
+int alpx_kv_import(const float* key_rows, const float* value_rows, void* key_cache,
+                   void* value_cache, int dtype, int64_t capacity, int batch, int kv_heads,
+                   int key_dim, int value_dim, int batch_index, int64_t row0, int64_t rows,
+                   void* stream);
+
 /*
  * Workspace size in bytes needed by alpx_decode_gqa for these sizes
  * (split-K partials: running max, running sum and the unnormalised

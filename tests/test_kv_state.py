@@ -1,0 +1,175 @@
+"""Device K/V state transfer (alpacca memory drop-in): snapshot records in
+the reference's "f32-le" format, restore, truncate.  The format oracle is
+the reference's own encoding (memory._f32_to_bytes, memory.py:71-78):
+row-major float32 little-endian bytes of the rows [length, kv_heads, dim];
+a cache of a narrower dtype stores round-to-nearest-even values
+(oracle.inputs.round_to).  Everything is bit-exact.  The validation tests
+run on CPU tensors (no device operation happens before a record is
+rejected); the transfer tests need the GPU."""
+
+import importlib
+
+import numpy as np
+import pytest
+
+from oracle import inputs as I
+
+
+def _mem():
+    return importlib.import_module("alpacca-open-sourced-by-jt_amd.memory")
+
+
+def _td(torch, name):
+    return {"f32": torch.float32, "f16": torch.float16, "bf16": torch.bfloat16}[name]
+
+
+def _bits(t):
+    import torch
+    return (t.view(torch.int16) if t.element_size() == 2 else t.view(torch.int32)).cpu().numpy()
+
+
+# --------------------------------------------------------------- CPU: records
+
+def test_restore_rejects_mismatched_records_before_touching_the_device():
+    import torch
+    M = _mem()
+    kc = torch.zeros((8, 2, 2, 4))
+    st = M.DeviceFullAttentionState(kc, torch.zeros((8, 2, 2, 3)), layer_index=3, batch_index=1)
+    good = dict(layer_index=3, logical_length=2, kv_heads=2, key_dim=4, value_dim=3,
+                key=bytes(2 * 2 * 4 * 4), value=bytes(2 * 2 * 3 * 4))
+    for change, err in [({"layer_index": 2}, "layer index"), ({"dtype": "f16-le"}, "dtype"),
+                        ({"key_dim": 8}, "shape"), ({"logical_length": 9}, "capacity"),
+                        ({"key": bytes(7)}, "bytes")]:
+        rec = M.FullAttentionSnapshot(**{**good, **change})
+        with pytest.raises(M.SnapshotMismatchError, match=err):
+            st.restore(rec)
+    assert st.logical_length == 0
+    with pytest.raises(M.StateError, match="cannot extend"):
+        st.truncate(1)
+    with pytest.raises(M.StateError, match="batch_index"):
+        M.DeviceFullAttentionState(kc, torch.zeros((8, 2, 2, 3)), batch_index=2)
+
+
+def test_recurrent_truncate_needs_replay_and_records_are_checked():
+    import torch
+    M = _mem()
+
+    class WS:
+        convolution_history = torch.zeros((2, 3, 10))
+        delta_state = torch.zeros((2, 4, 5, 6))
+    st = M.DeviceRecurrentState(WS(), key_heads=2, layer_index=1, logical_position=7)
+    st.truncate(7)  # the live position is allowed
+    with pytest.raises(M.ReplayRequiredError):
+        st.truncate(6)
+    snap = st.snapshot()
+    assert (snap.conv_kernel, snap.conv_channels, snap.recurrent_value_heads,
+            snap.recurrent_value_dim, snap.recurrent_key_dim) == (4, 10, 4, 5, 6)
+    assert len(snap.conv_history) == 3 * 10 * 4 and len(snap.delta_matrix) == 4 * 5 * 6 * 4
+    with pytest.raises(M.SnapshotMismatchError, match="shape"):
+        st.restore(M.RecurrentSnapshot(**{**{f: getattr(snap, f) for f in snap.__slots__},
+                                          "recurrent_key_heads": 3}))
+
+
+# --------------------------------------------------------------- GPU: transfer
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
+def test_attention_snapshot_bytes_restore_and_truncate(gpu, dtype):
+    import torch
+    M = _mem()
+    rng = np.random.default_rng(len(dtype))
+    cap, batch, hkv, d, dv, bi, n = 40, 3, 2, 32, 24, 1, 11
+    td = _td(torch, dtype)
+    kc = torch.zeros((cap, batch, hkv, d), dtype=td, device=gpu)
+    vc = torch.zeros((cap, batch, hkv, dv), dtype=td, device=gpu)
+    other = torch.from_numpy(rng.standard_normal((cap, hkv, d)).astype(np.float32)).to(td)
+    kc[:, 0] = other.to(gpu)
+    st = M.DeviceFullAttentionState(kc, vc, layer_index=5, batch_index=bi)
+    rows_k = I.round_to(rng.standard_normal((n, hkv * d)), dtype)
+    rows_v = I.round_to(rng.standard_normal((n, hkv * dv)), dtype)
+    for t in range(n):
+        st.append(torch.from_numpy(rows_k[t].astype(np.float32)).to(gpu).to(td),
+                  torch.from_numpy(rows_v[t].astype(np.float32)).to(gpu).to(td))
+    snap = st.snapshot()
+    assert (snap.layer_index, snap.logical_length, snap.kv_heads, snap.key_dim,
+            snap.value_dim, snap.dtype, snap.kind) == (5, n, hkv, d, dv, "f32-le", "attention")
+    # the reference's encoding of the same rows, byte for byte
+    assert snap.key == np.asarray(rows_k, dtype="<f4").tobytes()
+    assert snap.value == np.asarray(rows_v, dtype="<f4").tobytes()
+    # the other sequences were never written
+    assert torch.equal(kc[:, 0].cpu(), other) and not kc[:, 2].any() and not kc[n:, bi].any()
+    # restore into another sequence of a fresh cache: identical bits
+    kc2 = torch.zeros_like(kc)
+    vc2 = torch.zeros_like(vc)
+    st2 = M.DeviceFullAttentionState(kc2, vc2, layer_index=5, batch_index=2)
+    st2.restore(snap)
+    assert st2.logical_length == n
+    assert np.array_equal(_bits(kc2[:n, 2]), _bits(kc[:n, bi]))
+    assert np.array_equal(_bits(vc2[:n, 2]), _bits(vc[:n, bi]))
+    assert not kc2[:, :2].any() and not kc2[n:].any()
+    # truncate drops rows; the next append lands at the new length
+    st.truncate(4)
+    st.append(torch.zeros(hkv * d, dtype=td, device=gpu), torch.ones(hkv * dv, dtype=td, device=gpu))
+    snap4 = st.snapshot()
+    assert snap4.logical_length == 5
+    want_v = np.concatenate([rows_v[:4], np.ones((1, hkv * dv))]).astype("<f4").tobytes()
+    assert snap4.value == want_v
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_restore_of_fp32_rows_rounds_to_nearest_even(gpu, dtype):
+    # a reference (fp32 host) snapshot restored into a narrow device cache
+    # stores each value rounded to nearest even, as the half-precision
+    # device mirror does -- ties included
+    import torch
+    M = _mem()
+    rng = np.random.default_rng(9)
+    n, hkv, d = 7, 2, 16
+    k = rng.standard_normal((n, hkv, d)).astype(np.float32) * 3
+    v = rng.standard_normal((n, hkv, d)).astype(np.float32)
+    # exact ties of the target format in the first row
+    if dtype == "bf16":
+        k[0, 0, :4] = np.array([1 + 2 ** -8, 1 + 3 * 2 ** -8, -(1 + 2 ** -8), 2 ** -130],
+                               dtype=np.float32)
+    else:
+        k[0, 0, :4] = np.array([1 + 2 ** -11, 1 + 3 * 2 ** -11, 70000.0, 2 ** -30],
+                               dtype=np.float32)
+    rec = M.FullAttentionSnapshot(layer_index=0, logical_length=n, kv_heads=hkv, key_dim=d,
+                                  value_dim=d, key=k.astype("<f4").tobytes(),
+                                  value=v.astype("<f4").tobytes())
+    td = _td(torch, dtype)
+    kc = torch.zeros((16, 1, hkv, d), dtype=td, device=gpu)
+    vc = torch.zeros_like(kc)
+    M.DeviceFullAttentionState(kc, vc).restore(rec)
+    if dtype == "bf16":
+        want = I.f32_to_bf16_bits(k).view(np.int16)
+    else:
+        want = k.astype(np.float16).view(np.int16)
+    assert np.array_equal(_bits(kc[:n, 0]), want)
+
+
+@pytest.mark.gpu
+def test_recurrent_snapshot_restore_round_trip(gpu):
+    import torch
+    M = _mem()
+    ops = importlib.import_module("alpacca-open-sourced-by-jt_amd.qwen35_rocm_ops").Qwen35RocmOps()
+    ws = ops.initialize_recurrent_workspace(batch_size=2, convolution_kernel=4,
+                                            convolution_channels=96, value_heads=4,
+                                            value_dimension=8, key_dimension=16)
+    rng = np.random.default_rng(3)
+    h = rng.standard_normal((3, 96)).astype(np.float32)
+    s = rng.standard_normal((4, 8, 16)).astype(np.float32)
+    ws.convolution_history[1].copy_(torch.from_numpy(h))
+    ws.delta_state[1].copy_(torch.from_numpy(s))
+    st = M.DeviceRecurrentState(ws, key_heads=2, layer_index=4, batch_index=1,
+                                logical_position=12)
+    snap = st.snapshot()
+    assert snap.conv_history == h.astype("<f4").tobytes()
+    assert snap.delta_matrix == s.astype("<f4").tobytes()
+    assert (snap.logical_position, snap.conv_kernel, snap.recurrent_key_heads) == (12, 4, 2)
+    st0 = M.DeviceRecurrentState(ws, key_heads=2, layer_index=4, batch_index=0)
+    st0.restore(snap)
+    assert st0.logical_position == 12
+    assert torch.equal(ws.convolution_history[0], ws.convolution_history[1])
+    assert torch.equal(ws.delta_state[0], ws.delta_state[1])
