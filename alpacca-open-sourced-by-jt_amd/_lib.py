@@ -28,6 +28,13 @@ SIGNATURES = {
     "alpx_device_arch": (_c_int, [_c_int, ctypes.c_char_p, _c_int]),
     "alpx_kv_append": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_int, _c_int,
                                 _c_int, _c_int, _c_int, _c_i64, _c_ptr, _c_ptr]),
+    "alpx_kv_append_paged": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_int,
+                                      _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                      _c_i64, _c_ptr, _c_ptr]),
+    "alpx_decode_gqa_paged": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_int, _c_int,
+                                       _c_ptr, _c_int, _c_ptr, _c_ptr, _c_ptr, _c_size, _c_int,
+                                       _c_int, _c_int, _c_int, _c_int, _c_float, _c_int, _c_int,
+                                       _c_ptr]),
     "alpx_kv_export": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_int, _c_int,
                                 _c_int, _c_int, _c_int, _c_i64, _c_i64, _c_ptr]),
     "alpx_kv_import": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_int, _c_int,

@@ -37,6 +37,56 @@ def kv_append(key_cache, value_cache, key, value, *, position=None, positions=No
     _lib.check(rc)
 
 
+def kv_append_paged(key_pages, value_pages, block_table, key, value, *, position=None,
+                    positions=None):
+    """Appends ``key/value [T, B, Hkv, D|Dv]`` through ``block_table
+    [B, max_pages]`` (int32) into pages ``[P, page_size, Hkv, D|Dv]``."""
+    torch = _torch()
+    num_pages, page_size, kv_heads, dim = (int(x) for x in key_pages.shape)
+    value_dim = int(value_pages.shape[3])
+    tokens, batch = int(key.shape[0]), int(key.shape[1])
+    max_pages = int(block_table.shape[1])
+    pos_ptr = None
+    if positions is not None:
+        positions = positions.to(device=key_pages.device, dtype=torch.int32).contiguous()
+        pos_ptr = positions.data_ptr()
+    rc = _lib.lib().alpx_kv_append_paged(
+        key_pages.data_ptr(), value_pages.data_ptr(), key.data_ptr(), value.data_ptr(),
+        block_table.data_ptr(), max_pages, page_size, num_pages,
+        _lib.dtype_code(torch, key_pages.dtype), batch, kv_heads, dim, value_dim, tokens,
+        0 if position is None else int(position), pos_ptr,
+        _lib.stream_handle(torch, key_pages.device))
+    _lib.check(rc)
+
+
+def decode_paged(q, key_pages, value_pages, block_table, *, length, seq_lens=None, gate=None,
+                 scale, out_dtype=None):
+    """Split-K decode of ``q [B, Hq, D]`` over paged caches; returns
+    ``[B, Hq, Dv]``."""
+    torch = _torch()
+    num_pages, page_size, kv_heads, dim = (int(x) for x in key_pages.shape)
+    value_dim = int(value_pages.shape[3])
+    batch, q_heads = int(q.shape[0]), int(q.shape[1])
+    out = torch.empty((batch, q_heads, value_dim),
+                      dtype=q.dtype if out_dtype is None else out_dtype, device=q.device)
+    L = _lib.lib()
+    nbytes = L.alpx_decode_workspace_bytes(batch, q_heads, kv_heads, value_dim, int(length))
+    ws = _lib.workspace(torch, q.device, nbytes)
+    lens_ptr = None
+    if seq_lens is not None:
+        seq_lens = seq_lens.to(device=q.device, dtype=torch.int32).contiguous()
+        lens_ptr = seq_lens.data_ptr()
+    rc = L.alpx_decode_gqa_paged(
+        q.data_ptr(), key_pages.data_ptr(), value_pages.data_ptr(), block_table.data_ptr(),
+        int(block_table.shape[1]), page_size, num_pages, lens_ptr, int(length),
+        None if gate is None else gate.data_ptr(), out.data_ptr(), ws.data_ptr(), ws.numel(),
+        batch, q_heads, kv_heads, dim, value_dim, float(scale),
+        _lib.dtype_code(torch, q.dtype), _lib.dtype_code(torch, out.dtype),
+        _lib.stream_handle(torch, q.device))
+    _lib.check(rc)
+    return out
+
+
 def kv_export(key_cache, value_cache, *, batch_index, row0, rows):
     """Rows ``[row0, row0 + rows)`` of cache sequence ``batch_index`` as
     contiguous fp32 ``(key [rows, Hkv, D], value [rows, Hkv, Dv])``."""

@@ -65,6 +65,19 @@ __device__ __forceinline__ int seq_lo(const DecodeArgs& a, int b, int hi) {
   return (int)(n > hi ? hi : n);
 }
 
+// Element offset of cache row `row` of sequence b, kv head kvh (page lookup
+// for paged caches; a table entry outside [0, num_pages) is clamped, so a
+// bad table reads a wrong page but never leaves the page pool).
+__device__ __forceinline__ int64_t row_offset(const DecodeArgs& a, int b, int kvh, int row,
+                                              int64_t s_pos, int64_t s_b, int64_t s_h,
+                                              int64_t s_page) {
+  if (a.pages == nullptr) return (int64_t)b * s_b + (int64_t)kvh * s_h + (int64_t)row * s_pos;
+  int pg = a.pages[(int64_t)b * a.max_pages + (row >> a.page_shift)];
+  pg = min(max(pg, 0), a.num_pages - 1);
+  return (int64_t)pg * s_page + (int64_t)kvh * s_h +
+         (int64_t)(row & ((1 << a.page_shift) - 1)) * s_pos;
+}
+
 __device__ __forceinline__ void wave_sync_lds() {
   // LDS operations of one wavefront complete in issue order; this only
   // stops the compiler from moving LDS accesses across the point.
@@ -149,7 +162,7 @@ constexpr int merge_lds_bytes() {
 // The next tile's loads are issued as soon as the current tile is staged,
 // so every wave keeps a tile in flight.  At the end the four waves' online
 // softmax states are merged through LDS into one partial per block.
-template <typename T, int D>
+template <typename T, int D, bool PAGED>
 __global__ void __launch_bounds__(256)
 decode_split_mfma(DecodeArgs a) {
   typedef typename Vec8<T>::type V8;
@@ -202,14 +215,24 @@ decode_split_mfma(DecodeArgs a) {
   V8 kr[kIters];  // K rows, 16 bytes per lane, row-major
   V8 vr[kIters];  // V rows, same layout
   auto load_tile = [&](int p) {
+    // Paged: a wave tile starts at a multiple of kTile and never crosses a
+    // page (page size a multiple of kTile), so its page is looked up once.
+    const T* kt = kbase;
+    const T* vt = vbase;
+    if constexpr (PAGED) {
+      kt = (const T*)a.k + row_offset(a, b, kvh, p, a.ks_pos, 0, a.ks_h, a.ks_page) -
+           (int64_t)p * a.ks_pos;
+      vt = (const T*)a.v + row_offset(a, b, kvh, p, a.vs_pos, 0, a.vs_h, a.vs_page) -
+           (int64_t)p * a.vs_pos;
+    }
 #pragma unroll
     for (int it = 0; it < kIters; ++it) {
       const int u = it * 64 + lane;
       const int r = u / kUnits;
       const int c = u - r * kUnits;
       const int row = min(p + r, last);
-      kr[it] = *(const V8*)(kbase + (int64_t)row * a.ks_pos + 8 * c);
-      vr[it] = __builtin_nontemporal_load((const V8*)(vbase + (int64_t)row * a.vs_pos + 8 * c));
+      kr[it] = *(const V8*)(kt + (int64_t)row * a.ks_pos + 8 * c);
+      vr[it] = __builtin_nontemporal_load((const V8*)(vt + (int64_t)row * a.vs_pos + 8 * c));
     }
   };
 
@@ -292,7 +315,7 @@ decode_split_mfma(DecodeArgs a) {
 //     4 quad + j] (one 16-byte LDS read per g) and Q[head hl][same d];
 //   O^T = V^T P^T, k-step (blk, i): lane supplies P[16 blk + 4 quad + i]
 //     [head hl] (its own score slot) and V[that row][16 mb + hl].
-template <int D, int R>
+template <int D, int R, bool PAGED>
 __global__ void __launch_bounds__(256)
 decode_split_f32(DecodeArgs a) {
   constexpr int kStride = D + 4;  // floats: rows 4 apart sit 16 banks apart
@@ -342,14 +365,22 @@ decode_split_f32(DecodeArgs a) {
 
   f32x4 kr[kIters], vr[kIters];
   auto load_tile = [&](int p) {
+    const float* kt = kbase;  // paged: one page per tile, as in decode_split_mfma
+    const float* vt = vbase;
+    if constexpr (PAGED) {
+      kt = (const float*)a.k + row_offset(a, b, kvh, p, a.ks_pos, 0, a.ks_h, a.ks_page) -
+           (int64_t)p * a.ks_pos;
+      vt = (const float*)a.v + row_offset(a, b, kvh, p, a.vs_pos, 0, a.vs_h, a.vs_page) -
+           (int64_t)p * a.vs_pos;
+    }
 #pragma unroll
     for (int it = 0; it < kIters; ++it) {
       const int u = it * 64 + lane;
       const int r = u / kUnits;
       const int c = u - r * kUnits;
       const int row = min(p + r, last);
-      kr[it] = *(const f32x4*)(kbase + (int64_t)row * a.ks_pos + 4 * c);
-      vr[it] = __builtin_nontemporal_load((const f32x4*)(vbase + (int64_t)row * a.vs_pos + 4 * c));
+      kr[it] = *(const f32x4*)(kt + (int64_t)row * a.ks_pos + 4 * c);
+      vr[it] = __builtin_nontemporal_load((const f32x4*)(vt + (int64_t)row * a.vs_pos + 4 * c));
     }
   };
 
@@ -456,9 +487,6 @@ decode_split_generic(DecodeArgs a) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) acc[hh][e] = 0.f;
   }
-  const T* kbase = (const T*)a.k + (int64_t)b * a.ks_b + (int64_t)kvh * a.ks_h;
-  const T* vbase = (const T*)a.v + (int64_t)b * a.vs_b + (int64_t)kvh * a.vs_h;
-
   for (int p0 = start; p0 < end; p0 += kGenericTile) {
     const int pos = p0 + lane;
     const bool live = pos < end;
@@ -466,7 +494,7 @@ decode_split_generic(DecodeArgs a) {
 #pragma unroll
     for (int hh = 0; hh < 16; ++hh) s[hh] = 0.f;
     if (live) {
-      const T* row = kbase + (int64_t)pos * a.ks_pos;
+      const T* row = (const T*)a.k + row_offset(a, b, kvh, pos, a.ks_pos, a.ks_b, a.ks_h, a.ks_page);
       for (int d = 0; d < D; ++d) {
         const float kv = to_f32(row[d]);
 #pragma unroll
@@ -493,7 +521,8 @@ decode_split_generic(DecodeArgs a) {
     __syncthreads();
     const int n = min(kGenericTile, end - p0);
     for (int j = 0; j < n; ++j) {
-      const T* vrow = vbase + (int64_t)(p0 + j) * a.vs_pos;
+      const T* vrow =
+          (const T*)a.v + row_offset(a, b, kvh, p0 + j, a.vs_pos, a.vs_b, a.vs_h, a.vs_page);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int d = lane + 64 * e;
@@ -648,19 +677,25 @@ size_t workspace_for(int batch, int q_heads, int value_dim, int nsplit) {
 }
 
 template <typename T>
-const void* split_kernel(bool mfma, int D) {
+const void* split_kernel(bool mfma, bool paged, int D) {
   if (mfma) {
     if constexpr (sizeof(T) == 2) {
       switch (D) {
-        case 64: return (const void*)decode_split_mfma<T, 64>;
-        case 128: return (const void*)decode_split_mfma<T, 128>;
-        case 256: return (const void*)decode_split_mfma<T, 256>;
+        case 64: return paged ? (const void*)decode_split_mfma<T, 64, true>
+                              : (const void*)decode_split_mfma<T, 64, false>;
+        case 128: return paged ? (const void*)decode_split_mfma<T, 128, true>
+                               : (const void*)decode_split_mfma<T, 128, false>;
+        case 256: return paged ? (const void*)decode_split_mfma<T, 256, true>
+                               : (const void*)decode_split_mfma<T, 256, false>;
       }
     } else {
       switch (D) {
-        case 64: return (const void*)decode_split_f32<64, f32_tile_rows(64)>;
-        case 128: return (const void*)decode_split_f32<128, f32_tile_rows(128)>;
-        case 256: return (const void*)decode_split_f32<256, f32_tile_rows(256)>;
+        case 64: return paged ? (const void*)decode_split_f32<64, f32_tile_rows(64), true>
+                              : (const void*)decode_split_f32<64, f32_tile_rows(64), false>;
+        case 128: return paged ? (const void*)decode_split_f32<128, f32_tile_rows(128), true>
+                               : (const void*)decode_split_f32<128, f32_tile_rows(128), false>;
+        case 256: return paged ? (const void*)decode_split_f32<256, f32_tile_rows(256), true>
+                               : (const void*)decode_split_f32<256, f32_tile_rows(256), false>;
       }
     }
     return nullptr;
@@ -720,7 +755,8 @@ int run_decode(DecodeArgs a, int dtype, int out_dtype, void* workspace, size_t w
   const uintptr_t align = (uintptr_t)a.q | (uintptr_t)a.k | (uintptr_t)a.v |
                           (uintptr_t)(a.ks_pos * es) | (uintptr_t)(a.ks_b * es) |
                           (uintptr_t)(a.ks_h * es) | (uintptr_t)(a.vs_pos * es) |
-                          (uintptr_t)(a.vs_b * es) | (uintptr_t)(a.vs_h * es);
+                          (uintptr_t)(a.vs_b * es) | (uintptr_t)(a.vs_h * es) |
+                          (uintptr_t)(a.ks_page * es) | (uintptr_t)(a.vs_page * es);
   const int D = a.key_dim;
   const bool mfma = D == a.value_dim && (D == 64 || D == 128 || D == 256) && (align & 15) == 0 &&
                     getenv("ALPX_DECODE_GENERIC") == nullptr;
@@ -729,10 +765,11 @@ int run_decode(DecodeArgs a, int dtype, int out_dtype, void* workspace, size_t w
     return fail(ALPX_EINVAL, "decode workspace holds %zu bytes, needs %zu", workspace_bytes,
                 need);
   const void* kernel = nullptr;
+  const bool paged = a.pages != nullptr;
   switch (dtype) {
-    case ALPX_F32: kernel = split_kernel<float>(mfma, D); break;
-    case ALPX_F16: kernel = split_kernel<f16_t>(mfma, D); break;
-    default: kernel = split_kernel<bf16_t>(mfma, D); break;
+    case ALPX_F32: kernel = split_kernel<float>(mfma, paged, D); break;
+    case ALPX_F16: kernel = split_kernel<f16_t>(mfma, paged, D); break;
+    default: kernel = split_kernel<bf16_t>(mfma, paged, D); break;
   }
   if (kernel == nullptr) return fail(ALPX_EUNSUPPORTED, "decode: no kernel for this shape");
   const int unit =
@@ -802,6 +839,64 @@ extern "C" int alpx_decode_gqa(const void* q, const void* key_cache, const void*
   a.causal_pos0 = -1;
   a.kv_start = 0;
   a.window = 0;
+  a.length = length;
+  a.batch = batch;
+  a.q_heads = q_heads;
+  a.kv_heads = kv_heads;
+  a.group = q_heads / kv_heads;
+  a.key_dim = key_dim;
+  a.value_dim = value_dim;
+  a.scale_log2 = scale * kLog2e;
+  return run_decode(a, dtype, out_dtype, workspace, workspace_bytes, (hipStream_t)stream,
+                    ALPX_T_DECODE, ALPX_T_DECODE_COMBINE);
+}
+
+extern "C" int alpx_decode_gqa_paged(const void* q, const void* key_pages,
+                                     const void* value_pages, const int32_t* block_table,
+                                     int max_pages, int page_size, int num_pages,
+                                     const int32_t* seq_lens, int length, const void* gate,
+                                     void* out, void* workspace, size_t workspace_bytes,
+                                     int batch, int q_heads, int kv_heads, int key_dim,
+                                     int value_dim, float scale, int dtype, int out_dtype,
+                                     void* stream) {
+  using namespace alpx;
+  if (!q || !key_pages || !value_pages || !block_table || !out || !workspace)
+    return fail(ALPX_EINVAL, "alpx_decode_gqa_paged: null buffer");
+  if (!dtype_ok(dtype) || !dtype_ok(out_dtype))
+    return fail(ALPX_EINVAL, "alpx_decode_gqa_paged: unknown dtype");
+  if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || key_dim <= 0 || value_dim <= 0 ||
+      max_pages <= 0 || num_pages <= 0)
+    return fail(ALPX_EINVAL, "alpx_decode_gqa_paged: sizes must be positive");
+  if (page_size < kTile || (page_size & (page_size - 1)) != 0)
+    return fail(ALPX_EINVAL, "page size must be a power of two of at least %d rows", kTile);
+  if (length <= 0) return fail(ALPX_EINVAL, "attention cache length must be a positive integer");
+  if ((int64_t)max_pages * page_size < length)
+    return fail(ALPX_ERANGE, "the block table covers %lld rows, fewer than length %d",
+                (long long)max_pages * page_size, length);
+  if (q_heads % kv_heads != 0)
+    return fail(ALPX_EINVAL, "attention query heads must be a multiple of KV heads");
+  if (!(scale > 0.0f) || !isfinite(scale))
+    return fail(ALPX_EINVAL, "attention scale must be positive and finite");
+  if (key_dim > 256 || value_dim > 256)
+    return fail(ALPX_EUNSUPPORTED, "alpx_decode_gqa_paged: head dims above 256 are not supported");
+  DecodeArgs a = {};
+  a.q = q;
+  a.k = key_pages;
+  a.v = value_pages;
+  a.seq_lens = seq_lens;
+  a.gate = gate;
+  a.out = out;
+  a.ks_pos = (int64_t)kv_heads * key_dim;
+  a.ks_h = key_dim;
+  a.vs_pos = (int64_t)kv_heads * value_dim;
+  a.vs_h = value_dim;
+  a.ks_page = (int64_t)page_size * a.ks_pos;
+  a.vs_page = (int64_t)page_size * a.vs_pos;
+  a.pages = block_table;
+  a.page_shift = __builtin_ctz((unsigned)page_size);
+  a.max_pages = max_pages;
+  a.num_pages = num_pages;
+  a.causal_pos0 = -1;
   a.length = length;
   a.batch = batch;
   a.q_heads = q_heads;

@@ -26,6 +26,15 @@ struct DecodeArgs {
   int nsplit;       // partial slots per (b, h)
   int chunk;        // rows per slot
   float scale_log2; // softmax scale * log2(e)
+  // Paged caches (pages != null): cache row j of sequence b lives in page
+  // pages[b * max_pages + (j >> page_shift)] (clamped to [0, num_pages)),
+  // at row (j & (page size - 1)) of that page; ks_page / vs_page are the
+  // page strides in elements, ks_b / vs_b are unused.
+  const int32_t* pages;
+  int page_shift;
+  int max_pages;
+  int num_pages;
+  int64_t ks_page, vs_page;
 };
 
 // Bytes of split partials for `batch` rows of `q_heads` heads over `length`

@@ -147,6 +147,26 @@ class RocmAttentionWorkspace:
         }
 
 
+@dataclass(frozen=True)
+class RocmPagedAttentionWorkspace:
+    """A paged K/V pool (extension): pages ``[num_pages, page_size,
+    kv_heads, dim]``; a caller-owned int32 block table ``[batch, max_pages]``
+    maps each sequence's logical pages to pool pages."""
+
+    key_pages: Any
+    value_pages: Any
+    page_size: int
+
+    def descriptor(self) -> dict[str, Any]:
+        return {
+            "key_pages": _tensor_descriptor(self.key_pages),
+            "value_pages": _tensor_descriptor(self.value_pages),
+            "layout": "page,row_in_page,kv_head,head_dimension",
+            "page_size": self.page_size,
+            "initialization": "deterministic-zero",
+        }
+
+
 class Qwen35RocmOps:
     """gfx950 implementation of the Qwen35 attention/recurrence boundaries."""
 
@@ -695,6 +715,98 @@ class Qwen35RocmOps:
                                    eps=_positive_finite("epsilon", epsilon),
                                    out_dtype=out_dtype)
 
+    # ------------------------------------------------------------ paged K/V
+
+    def initialize_paged_attention_workspace(self, *, num_pages: int, page_size: int,
+                                             kv_heads: int, key_dimension: int,
+                                             value_dimension: int,
+                                             dtype: Any = None) -> RocmPagedAttentionWorkspace:
+        """A zeroed page pool (extension; the contiguous counterpart is
+        ``initialize_attention_workspace``, qwen35_rocm_ops.py:73-86)."""
+        pages = _positive_integer("num_pages", num_pages)
+        size = _positive_integer("page_size", page_size)
+        if size < 32 or size & (size - 1):
+            raise ValueError("page_size must be a power of two of at least 32")
+        heads = _positive_integer("kv_heads", kv_heads)
+        key_width = _positive_integer("key_dimension", key_dimension)
+        value_width = _positive_integer("value_dimension", value_dimension)
+        dtype = self.torch.float32 if dtype is None else dtype
+        keys = self.torch.zeros((pages, size, heads, key_width), dtype=dtype, device=self.device)
+        values = self.torch.zeros((pages, size, heads, value_width), dtype=dtype,
+                                  device=self.device)
+        return RocmPagedAttentionWorkspace(keys, values, size)
+
+    def _paged(self, key_pages, value_pages, block_table):
+        key_pages = self._tensor(key_pages, "attention key pages", dimensions=4)
+        value_pages = self._tensor(value_pages, "attention value pages", dimensions=4)
+        if _shape(key_pages)[:3] != _shape(value_pages)[:3]:
+            raise ValueError("attention K/V pages differ in count, size or heads")
+        if block_table.dim() != 2 or block_table.dtype != self.torch.int32:
+            raise TypeError("block table must be a [batch, max_pages] int32 tensor")
+        if block_table.device != key_pages.device or not block_table.is_contiguous():
+            raise ValueError("block table must be a contiguous tensor on the cache device")
+        self._same_dtype("paged attention", key_pages, value_pages)
+        return key_pages, value_pages
+
+    def paged_attention_append_(self, key_pages: Any, value_pages: Any, block_table: Any,
+                                position: Any, key: Any, value: Any) -> Any:
+        """``attention_append_`` (qwen35_rocm_ops.py:475-500) through a block
+        table: ``key [B, Hkv, D]`` / ``value [B, Hkv, Dv]`` of each sequence
+        land at logical row ``position`` (an int, or a device int32 ``[B]``
+        tensor of per-sequence positions).  Returns ``position + 1``."""
+        key_pages, value_pages = self._paged(key_pages, value_pages, block_table)
+        key = self._tensor(key, "attention key", dimensions=3)
+        value = self._tensor(value, "attention value", dimensions=3)
+        batch = int(block_table.shape[0])
+        _, size, heads, width = _shape(key_pages)
+        if _shape(key) != (batch, heads, width) or _shape(value) != (batch, heads,
+                                                                     int(value_pages.shape[3])):
+            raise ValueError("attention key/value do not match the page token shape")
+        self._same_dtype("paged append", key, value, key_pages)
+        if isinstance(position, int):
+            position = _nonnegative_integer("attention cache position", position)
+            if position >= int(block_table.shape[1]) * size:
+                raise ValueError("attention cache position exceeds capacity")
+            _ops.kv_append_paged(key_pages, value_pages, block_table, key.unsqueeze(0),
+                                 value.unsqueeze(0), position=position)
+            return position + 1
+        _ops.kv_append_paged(key_pages, value_pages, block_table, key.unsqueeze(0),
+                             value.unsqueeze(0), positions=position)
+        return position + 1
+
+    def paged_online_attention(self, query: Any, key_pages: Any, value_pages: Any,
+                               block_table: Any, *, length: int, seq_lens: Any = None,
+                               scale: float | None = None, gate: Any = None,
+                               out_dtype: Any = None) -> Any:
+        """``online_attention`` (qwen35_rocm_ops.py:502-564) over paged
+        caches: query ``[B, Hq, D]`` attends to logical rows
+        ``0 .. length - 1`` (or ``seq_lens[b]``) of its sequence's pages.
+        Same plan and arithmetic as the contiguous call, so the same rows
+        give the same bits.  Returns ``[B, Hq, Dv]``."""
+        key_pages, value_pages = self._paged(key_pages, value_pages, block_table)
+        query = self._tensor(query, "attention query", dimensions=3)
+        length = _positive_integer("attention cache length", length)
+        batch, query_heads, width = _shape(query)
+        _, size, heads, key_width = _shape(key_pages)
+        if int(block_table.shape[0]) != batch:
+            raise ValueError("block table batch does not match the query batch")
+        if length > int(block_table.shape[1]) * size:
+            raise ValueError("attention cache length exceeds capacity")
+        if width != key_width:
+            raise ValueError("attention query does not match K cache head width")
+        if query_heads % heads:
+            raise ValueError("attention query heads must be a multiple of KV heads")
+        self._same_dtype("paged attention", query, key_pages)
+        if gate is not None:
+            gate = self._tensor(gate, "attention gate", dimensions=3)
+            if _shape(gate) != (batch, query_heads, int(value_pages.shape[3])):
+                raise ValueError("attention gate must match the output shape")
+        scale_value = (1.0 / math.sqrt(key_width) if scale is None
+                       else _positive_finite("attention scale", scale))
+        return _ops.decode_paged(query, key_pages, value_pages, block_table, length=length,
+                                 seq_lens=seq_lens, gate=gate, scale=scale_value,
+                                 out_dtype=out_dtype)
+
     # ------------------------------------------------------ chunked prefill
 
     def attention_layer_prefill_(self, query_gate: Any, key: Any, value: Any, query_norm: Any,
@@ -832,6 +944,7 @@ class Qwen35RocmOps:
 
 __all__ = [
     "Qwen35RocmOps",
+    "RocmPagedAttentionWorkspace",
     "Qwen35RocmUnavailable",
     "RocmAttentionWorkspace",
     "RocmCapability",

@@ -262,6 +262,35 @@ def bench_layers(torch, ops, lib, *, steps, warmup, seed=6):
     }
 
 
+def bench_paged(torch, ops, lib, c2, *, steps, warmup, seed=8):
+    """C2 through a paged pool: the same 16 x 8192 fp16 rows in 256-row pages
+    assigned in shuffled order; the step is the paged split + combine."""
+    q, K, V = c2["tensors"]
+    batch, hkv, d, ctx, page = 16, 8, 128, 8192, 256
+    max_pages = ctx // page
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    perm = torch.randperm(batch * max_pages, generator=g).to(torch.int32)
+    table = perm.reshape(batch, max_pages).to(q.device)
+    pw = ops.initialize_paged_attention_workspace(num_pages=batch * max_pages, page_size=page,
+                                                  kv_heads=hkv, key_dimension=d,
+                                                  value_dimension=d, dtype=q.dtype)
+    _mod("_ops").kv_append_paged(pw.key_pages, pw.value_pages, table, K, V, position=0)
+    fn = lambda: ops.paged_online_attention(q, pw.key_pages, pw.value_pages, table,  # noqa: E731
+                                            length=ctx)
+    ms = _timed_steps(torch, fn, steps, warmup)
+    lib.timing_enable(True)
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    split_ms = _kernel_avg_ms(lib, lib.T_DECODE)
+    lib.timing_enable(False)
+    return {"c2_paged_256_rows": {
+        "ms_per_step": round(ms, 5), "gbs": round(c2["step_bytes"] / (ms * 1e-3) / 1e9, 1),
+        "split_ms": round(split_ms, 5),
+        "split_gbs": round(c2["split_alg_bytes"] / (split_ms * 1e-3) / 1e9, 1),
+        "vs_contiguous_step": round(c2["ms_per_step"] / ms, 3)}}
+
+
 def bench_layer_prefill(torch, ops, lib, *, steps, warmup, seed=7):
     """The chunked Qwen3.5 layer prefill against the device's own
     token-by-token path (the reference's prefill is token-sequential).
@@ -486,9 +515,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only-headline", action="store_true")
-    ap.add_argument("--workloads", default="c4,c3,c5,c1,layers,lprefill",
+    ap.add_argument("--workloads", default="c4,c3,c5,c1,layers,lprefill,paged",
                     help="comma list of secondary workloads to run "
-                         "(c1, c3, c4, c5, layers, lprefill)")
+                         "(c1, c3, c4, c5, layers, lprefill, paged)")
     ap.add_argument("--pmc-probe", action="store_true",
                     help="run the counter-run workload (copy calibration + C2 steps)")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -556,6 +585,8 @@ def main() -> int:
             "combine_us": round(c1["combine_ms"] * 1e3, 2)}
     if "layers" in wl:
         extra.update(bench_layers(torch, ops, lib, steps=steps, warmup=warmup))
+    if "paged" in wl:
+        extra.update(bench_paged(torch, ops, lib, c2, steps=steps, warmup=warmup))
     if "lprefill" in wl:
         extra.update(bench_layer_prefill(torch, ops, lib, steps=steps, warmup=warmup))
     extra["c2_combine_ms"] = round(c2["combine_ms"], 5)

@@ -76,6 +76,30 @@ int alpx_kv_append(void* key_cache, void* value_cache, const void* key, const vo
                    int value_dim, int tokens, int64_t position, const int32_t* positions,
                    void* stream);
 
+/* Paged K/V cache (an extension: the reference keeps one contiguous
+ * [n_ctx, Hkv, D] array per layer, model.py:866-870, or growing host rows,
+ * memory.py:385-475).  Pages are [num_pages, page_size, kv_heads,
+ * key_dim|value_dim]; block_table [batch, max_pages] (device int32) maps
+ * logical row j of sequence b to row (j % page_size) of page
+ * block_table[b * max_pages + j / page_size].  page_size is a power of two
+ * (at least 32 for decode).  alpx_kv_append_paged is alpx_kv_append
+ * through the table (bit-exact; rows past the table or naming a page
+ * outside [0, num_pages) are skipped); alpx_decode_gqa_paged is
+ * alpx_decode_gqa over the table (same split plan and arithmetic, so its
+ * result equals the contiguous cache's bit for bit; a page index outside
+ * [0, num_pages) is clamped into the pool).  Workspace as
+ * alpx_decode_workspace_bytes. */
+int alpx_kv_append_paged(void* key_pages, void* value_pages, const void* key, const void* value,
+                         const int32_t* block_table, int max_pages, int page_size, int num_pages,
+                         int dtype, int batch, int kv_heads, int key_dim, int value_dim,
+                         int tokens, int64_t position, const int32_t* positions, void* stream);
+int alpx_decode_gqa_paged(const void* q, const void* key_pages, const void* value_pages,
+                          const int32_t* block_table, int max_pages, int page_size,
+                          int num_pages, const int32_t* seq_lens, int length, const void* gate,
+                          void* out, void* workspace, size_t workspace_bytes, int batch,
+                          int q_heads, int kv_heads, int key_dim, int value_dim, float scale,
+                          int dtype, int out_dtype, void* stream);
+
 /* K/V state transfer for one sequence of a cache [capacity, batch, kv_heads,
  * key_dim|value_dim] (fp32 / fp16 / bf16, `dtype`): alpx_kv_export widens
  * cache rows [row0, row0 + rows) of sequence batch_index into contiguous

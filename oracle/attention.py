@@ -262,3 +262,14 @@ def causal_gqa_step_scalar(query_heads, key_cache, value_cache, scale=None):
             for c in range(dv)
         ])
     return result
+
+
+def paged_rows(pages, block_table, batch_index, length):
+    """Logical rows ``0 .. length - 1`` of sequence ``batch_index`` of a paged
+    cache ``pages [P, page_size, Hkv, D]`` under ``block_table [B, max_pages]``
+    (row j = row j % page_size of page block_table[b, j // page_size]):
+    the contiguous ``[length, Hkv, D]`` rows the same attention reads."""
+    pages = np.asarray(pages)
+    size = pages.shape[1]
+    rows = [pages[block_table[batch_index][j // size], j % size] for j in range(length)]
+    return np.stack(rows) if rows else pages[:0, 0]

@@ -348,3 +348,20 @@ def test_config_generators_small():
     c5 = I.c5_gdn_bf16(tokens=4)
     np.testing.assert_allclose(np.linalg.norm(c5["q"], axis=-1), 1.0, atol=1e-2)
     assert np.all(c5["g"] <= 0) and np.all((c5["beta"] > 0) & (c5["beta"] < 1))
+
+
+def test_paged_rows_gather_through_the_block_table():
+    # identity table = contiguous slicing; a shuffled table reorders pages;
+    # rows cross a page boundary at multiples of the page size
+    rng = np.random.default_rng(4)
+    size, hkv, d = 4, 2, 3
+    pages = rng.standard_normal((6, size, hkv, d))
+    ident = np.array([[0, 1, 2], [3, 4, 5]])
+    np.testing.assert_array_equal(A.paged_rows(pages, ident, 0, 10),
+                                  pages[:3].reshape(12, hkv, d)[:10])
+    table = np.array([[5, 0, 3], [1, 2, 4]])
+    got = A.paged_rows(pages, table, 0, 9)
+    np.testing.assert_array_equal(got[:4], pages[5])
+    np.testing.assert_array_equal(got[4:8], pages[0])
+    np.testing.assert_array_equal(got[8], pages[3, 0])
+    assert A.paged_rows(pages, table, 1, 0).shape == (0, hkv, d)
