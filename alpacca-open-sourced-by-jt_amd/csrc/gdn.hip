@@ -188,10 +188,12 @@ __device__ __forceinline__ int tr_slot(int quad, int j) { return 16 * (j >> 2) +
 __host__ __device__ inline int64_t ws_per_chunk(int Dk) { return kC + 2 * kC * kC + (int64_t)kC * Dk; }
 
 // Per-chunk workspace, in order: Gc * log2(e) [kC] fp32, then hi and lo bf16
-// planes of Ub [kC x kC], M [kC x kC] and W [kC x Dk].  Ub's columns are
-// stored in operand order: position 32 ks + 8 quad + j of a row holds
-// column 32 ks + tr_slot(quad, j), so one 16-byte load gives a lane its
-// A operand for the transposing read of V.
+// planes of Ub [kC x kC], M [kC x kC] and W [kC x Dk].  Each plane is stored
+// fragment-major (frag_idx): the 16 bytes a lane feeds to one MFMA as its A
+// operand are contiguous and the 64 lanes of a wave follow each other, so a
+// wave's operand load is one contiguous 1 KiB access.  Ub's columns are
+// additionally stored in operand order: position 32 ks + 8 quad + j of a row
+// holds column 32 ks + tr_slot(quad, j), matching the transposing read of V.
 struct ChunkWs {
   float* g;
   bf16_t *u_hi, *u_lo, *m_hi, *m_lo, *w_hi, *w_lo;
@@ -207,6 +209,13 @@ __device__ __forceinline__ ChunkWs chunk_ws(float* base, int dk) {
   w.w_hi = w.m_lo + kC * kC;
   w.w_lo = w.w_hi + kC * dk;
   return w;
+}
+
+// Element (row t, position p) of a kC-row plane whose rows hold `cols`
+// positions -> its fragment-major index: (row tile t/16, k step p/32,
+// lane 16 * ((p/8) % 4) + t % 16, element p % 8).
+__device__ __forceinline__ int frag_idx(int t, int p, int cols) {
+  return ((((t >> 4) * (cols >> 5) + (p >> 5)) * 4 + ((p >> 3) & 3)) * 16 + (t & 15)) * 8 + (p & 7);
 }
 
 // Column i of Ub -> its position in the operand-ordered row.
@@ -299,7 +308,7 @@ gdn_prep(GdnArgs a) {
         const int i = 16 * ib + hl;
         const float dec = i <= t ? expf(Gs[t] - Gs[i]) : 0.f;
         Bm[t * kF + i] = i < t ? Bs[t] * dec * kk[ib][r] : 0.f;
-        store_split(out.m_hi, out.m_lo, t * kC + i, dec * qk[ib][r]);
+        store_split(out.m_hi, out.m_lo, frag_idx(t, i, kC), dec * qk[ib][r]);
       }
     }
   }
@@ -362,7 +371,7 @@ gdn_prep(GdnArgs a) {
   // Ub = T diag(beta)
   for (int idx = tid; idx < kC * kC; idx += 256) {
     const int t = idx / kC, i = idx - (idx / kC) * kC;
-    store_split(out.u_hi, out.u_lo, t * kC + u_pos(i), Tm[t * kF + i] * Bs[i]);
+    store_split(out.u_hi, out.u_lo, frag_idx(t, u_pos(i), kC), Tm[t * kF + i] * Bs[i]);
   }
   // W = T diag(beta exp(Gc)) K: wave w computes rows 16w..16w+15.
   {
@@ -392,7 +401,7 @@ gdn_prep(GdnArgs a) {
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r)
-        store_split(out.w_hi, out.w_lo, (16 * wave + 4 * quad + r) * DK + 16 * nb + hl, acc[r]);
+        store_split(out.w_hi, out.w_lo, frag_idx(16 * wave + 4 * quad + r, 16 * nb + hl, DK), acc[r]);
     }
   }
 }
@@ -491,15 +500,16 @@ gdn_apply(GdnArgs a) {
     in.g = w.g[tid & (kC - 1)];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      in.w_hi[ks] = *(const bf16x8*)(w.w_hi + trow * DK + 32 * ks + 8 * quad);
-      in.w_lo[ks] = *(const bf16x8*)(w.w_lo + trow * DK + 32 * ks + 8 * quad);
+      in.w_hi[ks] = *(const bf16x8*)(w.w_hi + ((wave * KS + ks) * 64 + lane) * 8);
+      in.w_lo[ks] = *(const bf16x8*)(w.w_lo + ((wave * KS + ks) * 64 + lane) * 8);
     }
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      in.u_hi[ks] = *(const bf16x8*)(w.u_hi + trow * kC + 32 * ks + 8 * quad);
-      in.u_lo[ks] = *(const bf16x8*)(w.u_lo + trow * kC + 32 * ks + 8 * quad);
-      in.m_hi[ks] = *(const bf16x8*)(w.m_hi + trow * kC + 32 * ks + 8 * quad);
-      in.m_lo[ks] = *(const bf16x8*)(w.m_lo + trow * kC + 32 * ks + 8 * quad);
+      const int f = ((wave * 2 + ks) * 64 + lane) * 8;
+      in.u_hi[ks] = *(const bf16x8*)(w.u_hi + f);
+      in.u_lo[ks] = *(const bf16x8*)(w.u_lo + f);
+      in.m_hi[ks] = *(const bf16x8*)(w.m_hi + f);
+      in.m_lo[ks] = *(const bf16x8*)(w.m_lo + f);
     }
   };
 
