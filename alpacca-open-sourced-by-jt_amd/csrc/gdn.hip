@@ -423,17 +423,23 @@ __device__ __forceinline__ void apply_block(const GdnArgs& a, int& slice, int& h
   b = rest / a.Hv;
 }
 
-// Global inputs of one chunk for one thread: its share of the K/Q/V rows
-// and decays (staged in LDS) and the rows of W, Ub and M its lane feeds to
-// the MFMAs as A operands.
+// Global inputs of one chunk for one thread, in three groups fetched at
+// different points of the chunk loop: the K/Q/V rows and decays that are
+// staged in LDS, the rows of W and Ub its lane feeds to the Delta MFMAs as A
+// operands, and the rows of M for the output MFMAs.
 template <int DK>
-struct ApplyIn {
+struct StageIn {
   static constexpr int kUnitsPerThread = kC * (DK / 8) / 256;
   bf16x8 k[kUnitsPerThread], q[kUnitsPerThread];
   bf16x8 v;
   float g;
+};
+template <int DK>
+struct DeltaIn {
   bf16x8 w_hi[DK / 32], w_lo[DK / 32];
   bf16x8 u_hi[2], u_lo[2];
+};
+struct OutIn {
   bf16x8 m_hi[2], m_lo[2];
 };
 
@@ -444,12 +450,8 @@ gdn_apply(GdnArgs a) {
   constexpr int kSF = DK + 4;
   constexpr int kDF = kC + 4;
   constexpr int KS = DK / 32;
-  // DK <= 128: the next chunk's inputs are fetched while this chunk computes.
-  // DK = 256 has no registers for a second set; its fetch is issued at the
-  // end of the previous chunk (one exposed latency per chunk).
-  constexpr bool kAhead = DK <= 128;
   constexpr int kUnits = DK / 8;
-  constexpr int kUPT = ApplyIn<DK>::kUnitsPerThread;
+  constexpr int kUPT = StageIn<DK>::kUnitsPerThread;
   __shared__ __attribute__((aligned(16))) bf16_t Ks[kC * kS];
   __shared__ __attribute__((aligned(16))) bf16_t Qs[kC * kS];
   __shared__ __attribute__((aligned(16))) bf16_t Vs[kC * 24];  // [t][16 rows] + pad
@@ -473,31 +475,28 @@ gdn_apply(GdnArgs a) {
   const int tr_col = 4 * (hl & 3);
   const int trow = 16 * wave + hl;  // A-operand row of this lane
 
-  // Every load is unconditional (rows past the end read a clamped row and
-  // are zeroed), so one fetch puts all of a chunk's inputs in flight.
-  auto fetch = [&](ApplyIn<DK>& in, int c) {
+  // Every load reads a clamped row and is issued unconditionally; rows past
+  // the end of the sequence are zeroed when staged, so a fetch puts its whole
+  // group in flight without branches.
+  auto fetch_stage = [&](StageIn<DK>& in, int c) __attribute__((always_inline)) {
     const int t0 = c * kC;
 #pragma unroll
     for (int u = 0; u < kUPT; ++u) {
       const int idx = u * 256 + tid;
       const int r = idx / kUnits, cc = idx - (idx / kUnits) * kUnits;
-      const int t = t0 + r;
       const int64_t off =
-          (((int64_t)b * a.T + min(t, a.T - 1)) * a.Hk + kh) * DK + 8 * cc;
-      const bf16x8 kv = *(const bf16x8*)((const bf16_t*)a.k + off);
-      const bf16x8 qv = *(const bf16x8*)((const bf16_t*)a.q + off);
-      in.k[u] = t < a.T ? kv : (bf16x8){};
-      in.q[u] = t < a.T ? qv : (bf16x8){};
+          (((int64_t)b * a.T + min(t0 + r, a.T - 1)) * a.Hk + kh) * DK + 8 * cc;
+      in.k[u] = *(const bf16x8*)((const bf16_t*)a.k + off);
+      in.q[u] = *(const bf16x8*)((const bf16_t*)a.q + off);
     }
-    {
-      const int t = (tid & 127) >> 1, half = tid & 1;
-      const bf16x8 vv = *(const bf16x8*)((const bf16_t*)a.v +
-                                         (((int64_t)b * a.T + min(t0 + t, a.T - 1)) * a.Hv + h) *
-                                             a.Dv + r0 + 8 * half);
-      in.v = t0 + t < a.T ? vv : (bf16x8){};
-    }
+    const int t = (tid & 127) >> 1, half = tid & 1;
+    in.v = *(const bf16x8*)((const bf16_t*)a.v +
+                            (((int64_t)b * a.T + min(t0 + t, a.T - 1)) * a.Hv + h) * a.Dv + r0 +
+                            8 * half);
+    in.g = a.ws[(bh * a.nchunks + c) * ws_per_chunk(DK) + (tid & (kC - 1))];
+  };
+  auto fetch_delta = [&](DeltaIn<DK>& in, int c) __attribute__((always_inline)) {
     const ChunkWs w = chunk_ws(a.ws + (bh * a.nchunks + c) * ws_per_chunk(DK), DK);
-    in.g = w.g[tid & (kC - 1)];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       in.w_hi[ks] = *(const bf16x8*)(w.w_hi + ((wave * KS + ks) * 64 + lane) * 8);
@@ -508,27 +507,51 @@ gdn_apply(GdnArgs a) {
       const int f = ((wave * 2 + ks) * 64 + lane) * 8;
       in.u_hi[ks] = *(const bf16x8*)(w.u_hi + f);
       in.u_lo[ks] = *(const bf16x8*)(w.u_lo + f);
+    }
+  };
+  auto fetch_out = [&](OutIn& in, int c) __attribute__((always_inline)) {
+    const ChunkWs w = chunk_ws(a.ws + (bh * a.nchunks + c) * ws_per_chunk(DK), DK);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int f = ((wave * 2 + ks) * 64 + lane) * 8;
       in.m_hi[ks] = *(const bf16x8*)(w.m_hi + f);
       in.m_lo[ks] = *(const bf16x8*)(w.m_lo + f);
     }
   };
 
-  ApplyIn<DK> nxt;
-  fetch(nxt, 0);
+  // Each group is re-fetched for chunk c + 1 right after its last use in
+  // chunk c, into the same registers, so the loads overlap the rest of the
+  // chunk without a second register set.  The last chunk re-reads itself
+  // (unused) rather than branching, which would make the compiler wait for
+  // every outstanding load at the top of the loop.
+  StageIn<DK> st;
+  DeltaIn<DK> dl;
+  OutIn oi;
+  // Issue order st, dl, oi as in the loop (the loads complete in order, so the
+  // loop's first wait for st must not also cover dl and oi).
+  fetch_stage(st, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  fetch_delta(dl, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  fetch_out(oi, 0);
+  __builtin_amdgcn_sched_barrier(0);
   for (int c = 0; c < a.nchunks; ++c) {
     const int t0 = c * kC;
-    const ApplyIn<DK> cur = nxt;
+    const int cn = min(c + 1, a.nchunks - 1);
+    const bf16x8 zero = {};
 #pragma unroll
     for (int u = 0; u < kUPT; ++u) {
       const int idx = u * 256 + tid;
       const int r = idx / kUnits, cc = idx - (idx / kUnits) * kUnits;
-      *(bf16x8*)(Ks + r * kS + 8 * cc) = cur.k[u];
-      *(bf16x8*)(Qs + r * kS + 8 * cc) = cur.q[u];
+      const bool ok = t0 + r < a.T;
+      *(bf16x8*)(Ks + r * kS + 8 * cc) = ok ? st.k[u] : zero;
+      *(bf16x8*)(Qs + r * kS + 8 * cc) = ok ? st.q[u] : zero;
     }
-    if (tid < kC * 2) *(bf16x8*)(Vs + (tid >> 1) * 24 + 8 * (tid & 1)) = cur.v;
-    if (tid < kC) Gs[tid] = cur.g;
+    if (tid < kC * 2)
+      *(bf16x8*)(Vs + (tid >> 1) * 24 + 8 * (tid & 1)) = t0 + (tid >> 1) < a.T ? st.v : zero;
+    if (tid < kC) Gs[tid] = st.g;
     __syncthreads();
-    if (kAhead && c + 1 < a.nchunks) fetch(nxt, c + 1);
+    fetch_stage(st, cn);
 
     // S^T operand (B: k = d, n = state row): lane holds S[hl][32 ks + 8 quad + 0..7].
     bf16x8 shi[KS], slo[KS];
@@ -539,9 +562,9 @@ gdn_apply(GdnArgs a) {
     f32x4 ws_acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      ws_acc = mfma16x16x32(cur.w_hi[ks], shi[ks], ws_acc);
-      ws_acc = mfma16x16x32(cur.w_hi[ks], slo[ks], ws_acc);
-      ws_acc = mfma16x16x32(cur.w_lo[ks], shi[ks], ws_acc);
+      ws_acc = mfma16x16x32(dl.w_hi[ks], shi[ks], ws_acc);
+      ws_acc = mfma16x16x32(dl.w_hi[ks], slo[ks], ws_acc);
+      ws_acc = mfma16x16x32(dl.w_lo[ks], shi[ks], ws_acc);
     }
     f32x4 uv = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -549,12 +572,13 @@ gdn_apply(GdnArgs a) {
       const bf16x4 v0 = lds_read_tr4(Vs + (32 * ks + tr_row) * 24 + tr_col);
       const bf16x4 v1 = lds_read_tr4(Vs + (32 * ks + 16 + tr_row) * 24 + tr_col);
       const bf16x8 vb = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
-      uv = mfma16x16x32(cur.u_hi[ks], vb, uv);
-      uv = mfma16x16x32(cur.u_lo[ks], vb, uv);
+      uv = mfma16x16x32(dl.u_hi[ks], vb, uv);
+      uv = mfma16x16x32(dl.u_lo[ks], vb, uv);
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r)
       Dt[hl * kDF + 16 * wave + 4 * quad + r] = uv[r] - ws_acc[r];  // Delta^T[state row][t]
+    fetch_delta(dl, cn);
     // (2a) Q S^T for the output rows of this wave
     f32x4 qs = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -571,10 +595,11 @@ gdn_apply(GdnArgs a) {
     for (int ks = 0; ks < 2; ++ks) {
       bf16x8 dhi, dlo;
       split8(Dt + hl * kDF + 32 * ks + 8 * quad, dhi, dlo);
-      md = mfma16x16x32(cur.m_hi[ks], dhi, md);
-      md = mfma16x16x32(cur.m_hi[ks], dlo, md);
-      md = mfma16x16x32(cur.m_lo[ks], dhi, md);
+      md = mfma16x16x32(oi.m_hi[ks], dhi, md);
+      md = mfma16x16x32(oi.m_hi[ks], dlo, md);
+      md = mfma16x16x32(oi.m_lo[ks], dhi, md);
     }
+    fetch_out(oi, cn);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int t = 16 * wave + 4 * quad + r;
@@ -616,7 +641,6 @@ gdn_apply(GdnArgs a) {
         *sp = gl * *sp + acc[r];
       }
     }
-    if (!kAhead && c + 1 < a.nchunks) fetch(nxt, c + 1);
     __syncthreads();
   }
   for (int idx = tid; idx < 16 * DK; idx += 256) {
