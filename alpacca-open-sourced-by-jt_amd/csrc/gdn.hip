@@ -15,16 +15,18 @@
 //  phase A, gdn_prep, one block per (sequence, head, chunk), state-free:
 //    Gc = cumsum(g); A = exp(Gc_t - Gc_i) k_t.k_i (i < t);
 //    M = exp(Gc_t - Gc_i) q_t.k_i (i <= t); T = (I + diag(beta) A)^-1 by
-//    16x16 forward substitution plus block recursion; Ub = T diag(beta);
-//    W = T diag(beta exp(Gc)) K.  K K^T and Q K^T run on bf16 MFMA (exact
-//    products of bf16 inputs, fp32 sums); W on bf16 MFMA with T split into
-//    hi + lo bf16 parts.  Ub, M and W are stored already split into hi and
-//    lo bf16 planes (the same bytes as fp32), Gc in base 2, so phase B
-//    loads MFMA operands directly.
+//    16x16 forward substitution plus block recursion.  K K^T and Q K^T run
+//    on bf16 MFMA (exact products of bf16 inputs, fp32 sums).  T and M are
+//    stored split into hi and lo bf16 planes (the same bytes as fp32), with
+//    Gc in base 2 and beta, so phase B loads its MFMA operands directly.
 //  phase B, gdn_apply, one block per (sequence, head, 16 state rows),
 //    sequential over chunks with the 16 x Dk state slice resident in LDS:
-//    Delta = Ub V - W S^T;  O = (diag(exp Gc) Q S^T + M Delta) / sqrt(Dk);
+//    X = diag(beta) (V - diag(exp Gc) K S^T);  Delta = T X;
+//    O = (diag(exp Gc) Q S^T + M Delta) / sqrt(Dk);
 //    S <- exp(Gc_last) S + (diag(exp(Gc_last - Gc)) Delta)^T K.
+//    (Delta = T X is Ub V - W S^T with Ub = T diag(beta) and
+//    W = T diag(beta exp Gc) K folded together, so phase B reads T, 16 KiB
+//    per head and chunk, instead of Ub and W, 48 KiB at Dk = 128.)
 //    fp32 x fp32 products use three bf16 MFMAs (hi.hi + hi.lo + lo.hi),
 //    fp32 x bf16 products two, so the state keeps ~fp32 accuracy.
 // Tokens past the end of the last chunk are padded as k = q = v = 0,
@@ -185,43 +187,44 @@ __device__ __forceinline__ void split8(const float* x, bf16x8& hi, bf16x8& lo) {
 // k-slot j of lane group `quad` is row 16 (j / 4) + 4 quad + j % 4.
 __device__ __forceinline__ int tr_slot(int quad, int j) { return 16 * (j >> 2) + 4 * quad + (j & 3); }
 
-__host__ __device__ inline int64_t ws_per_chunk(int Dk) { return kC + 2 * kC * kC + (int64_t)kC * Dk; }
+__host__ __device__ inline int64_t ws_per_chunk() { return 2 * kC + 2 * kC * kC; }
 
-// Per-chunk workspace, in order: Gc * log2(e) [kC] fp32, then hi and lo bf16
-// planes of Ub [kC x kC], M [kC x kC] and W [kC x Dk].  Each plane is stored
-// fragment-major (frag_idx): the 16 bytes a lane feeds to one MFMA as its A
-// operand are contiguous and the 64 lanes of a wave follow each other, so a
-// wave's operand load is one contiguous 1 KiB access.  Ub's columns are
-// additionally stored in operand order: position 32 ks + 8 quad + j of a row
-// holds column 32 ks + tr_slot(quad, j), matching the transposing read of V.
+// Per-chunk workspace, in order: Gc * log2(e) [kC] fp32, beta [kC] fp32,
+// then the hi and lo bf16 planes of T [kC x kC] and of M [kC x kC].  Each
+// plane is stored fragment-major (frag_idx): the 16 bytes a lane feeds to one
+// MFMA as its A operand are contiguous and the 64 lanes of a wave follow each
+// other, so a wave's operand load is one contiguous 1 KiB access.  M's
+// columns are additionally stored in k-slot order (slot_pos), matching the
+// order in which phase B holds Delta.
 struct ChunkWs {
   float* g;
-  bf16_t *u_hi, *u_lo, *m_hi, *m_lo, *w_hi, *w_lo;
+  float* beta;
+  bf16_t *t_hi, *t_lo, *m_hi, *m_lo;
 };
 
-__device__ __forceinline__ ChunkWs chunk_ws(float* base, int dk) {
+__device__ __forceinline__ ChunkWs chunk_ws(float* base) {
   ChunkWs w;
   w.g = base;
-  w.u_hi = (bf16_t*)(base + kC);
-  w.u_lo = w.u_hi + kC * kC;
-  w.m_hi = w.u_lo + kC * kC;
+  w.beta = base + kC;
+  w.t_hi = (bf16_t*)(base + 2 * kC);
+  w.t_lo = w.t_hi + kC * kC;
+  w.m_hi = w.t_lo + kC * kC;
   w.m_lo = w.m_hi + kC * kC;
-  w.w_hi = w.m_lo + kC * kC;
-  w.w_lo = w.w_hi + kC * dk;
   return w;
 }
 
-// Element (row t, position p) of a kC-row plane whose rows hold `cols`
-// positions -> its fragment-major index: (row tile t/16, k step p/32,
-// lane 16 * ((p/8) % 4) + t % 16, element p % 8).
-__device__ __forceinline__ int frag_idx(int t, int p, int cols) {
-  return ((((t >> 4) * (cols >> 5) + (p >> 5)) * 4 + ((p >> 3) & 3)) * 16 + (t & 15)) * 8 + (p & 7);
-}
-
-// Column i of Ub -> its position in the operand-ordered row.
-__device__ __forceinline__ int u_pos(int i) {
+// Column i of a kC-column operand -> its position when the columns are in
+// k-slot order (position 32 ks + 8 quad + j holds column 32 ks + tr_slot(quad, j)).
+__device__ __forceinline__ int slot_pos(int i) {
   const int ks = i >> 5, r = i & 31;
   return 32 * ks + 8 * ((r & 15) >> 2) + 4 * (r >> 4) + (r & 3);
+}
+
+// Element (row t, column p) of a kC-row plane with `cols` columns -> its
+// fragment-major index: (row tile t/16, k step p/32, lane
+// 16 * ((p/8) % 4) + t % 16, element p % 8).
+__device__ __forceinline__ int frag_idx(int t, int p, int cols) {
+  return ((((t >> 4) * (cols >> 5) + (p >> 5)) * 4 + ((p >> 3) & 3)) * 16 + (t & 15)) * 8 + (p & 7);
 }
 
 __device__ __forceinline__ void store_split(bf16_t* hi, bf16_t* lo, int idx, float v) {
@@ -281,10 +284,14 @@ gdn_prep(GdnArgs a) {
   }
   __syncthreads();
 
-  const ChunkWs out = chunk_ws(a.ws + (((int64_t)b * a.Hv + h) * a.nchunks + c) * ws_per_chunk(DK), DK);
-  if (tid < kC) out.g[tid] = Gs[tid] * 1.4426950408889634f;
+  const ChunkWs out = chunk_ws(a.ws + (((int64_t)b * a.Hv + h) * a.nchunks + c) * ws_per_chunk());
+  if (tid < kC) {
+    out.g[tid] = Gs[tid] * 1.4426950408889634f;
+    out.beta[tid] = Bs[tid];
+  }
 
-  // K K^T and Q K^T: wave w computes rows 16w..16w+15.
+  // Bm = diag(beta) (exp(Gc_t - Gc_i) k_t.k_i)_{i<t} and
+  // M = (exp(Gc_t - Gc_i) q_t.k_i)_{i<=t}: wave w computes rows 16w..16w+15.
   {
     f32x4 kk[4], qk[4];
 #pragma unroll
@@ -308,7 +315,7 @@ gdn_prep(GdnArgs a) {
         const int i = 16 * ib + hl;
         const float dec = i <= t ? expf(Gs[t] - Gs[i]) : 0.f;
         Bm[t * kF + i] = i < t ? Bs[t] * dec * kk[ib][r] : 0.f;
-        store_split(out.m_hi, out.m_lo, frag_idx(t, i, kC), dec * qk[ib][r]);
+        store_split(out.m_hi, out.m_lo, frag_idx(t, slot_pos(i), kC), dec * qk[ib][r]);
       }
     }
   }
@@ -368,41 +375,9 @@ gdn_prep(GdnArgs a) {
     __syncthreads();
   }
 
-  // Ub = T diag(beta)
   for (int idx = tid; idx < kC * kC; idx += 256) {
     const int t = idx / kC, i = idx - (idx / kC) * kC;
-    store_split(out.u_hi, out.u_lo, frag_idx(t, u_pos(i), kC), Tm[t * kF + i] * Bs[i]);
-  }
-  // W = T diag(beta exp(Gc)) K: wave w computes rows 16w..16w+15.
-  {
-    bf16x8 ahi[2], alo[2];
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      float x[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int i = 32 * ks + tr_slot(quad, j);
-        x[j] = Tm[(16 * wave + hl) * kF + i] * Bs[i] * expf(Gs[i]);
-      }
-      split8(x, ahi[ks], alo[ks]);
-    }
-    const int tr_row = 4 * quad + (hl >> 2);
-    const int tr_col = 4 * (hl & 3);
-#pragma unroll
-    for (int nb = 0; nb < DK / 16; ++nb) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const bf16x4 k0 = lds_read_tr4(Ks + (32 * ks + tr_row) * kS + 16 * nb + tr_col);
-        const bf16x4 k1 = lds_read_tr4(Ks + (32 * ks + 16 + tr_row) * kS + 16 * nb + tr_col);
-        const bf16x8 kb = __builtin_shufflevector(k0, k1, 0, 1, 2, 3, 4, 5, 6, 7);
-        acc = mfma16x16x32(ahi[ks], kb, acc);
-        acc = mfma16x16x32(alo[ks], kb, acc);
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        store_split(out.w_hi, out.w_lo, frag_idx(16 * wave + 4 * quad + r, 16 * nb + hl, DK), acc[r]);
-    }
+    store_split(out.t_hi, out.t_lo, frag_idx(t, i, kC), Tm[t * kF + i]);
   }
 }
 
@@ -411,7 +386,7 @@ gdn_prep(GdnArgs a) {
 // Block -> (16-row state slice, value head, batch).  Consecutive block ids
 // run on consecutive XCDs, so the ids are permuted to give the slices of one
 // head neighbouring positions on one XCD: they read the same per-chunk
-// workspace (Ub, M, W) and share that XCD's L2.
+// K/Q rows and T and share that XCD's L2.
 __device__ __forceinline__ void apply_block(const GdnArgs& a, int& slice, int& h, int& b) {
   const int slices = a.Dv / 16;
   const int n = slices * a.Hv * a.B;
@@ -424,22 +399,20 @@ __device__ __forceinline__ void apply_block(const GdnArgs& a, int& slice, int& h
 }
 
 // Global inputs of one chunk for one thread, in three groups fetched at
-// different points of the chunk loop: the K/Q/V rows and decays that are
-// staged in LDS, the rows of W and Ub its lane feeds to the Delta MFMAs as A
-// operands, and the rows of M for the output MFMAs.
+// different points of the chunk loop: the K/Q/V rows, decays and betas that
+// are staged in LDS, and the rows of T and of M its lane feeds to the Delta
+// and output MFMAs as A operands.
 template <int DK>
 struct StageIn {
   static constexpr int kUnitsPerThread = kC * (DK / 8) / 256;
   bf16x8 k[kUnitsPerThread], q[kUnitsPerThread];
   bf16x8 v;
-  float g;
+  float g, beta;
 };
-template <int DK>
-struct DeltaIn {
-  bf16x8 w_hi[DK / 32], w_lo[DK / 32];
-  bf16x8 u_hi[2], u_lo[2];
+struct TIn {
+  bf16x8 t_hi[2], t_lo[2];
 };
-struct OutIn {
+struct MIn {
   bf16x8 m_hi[2], m_lo[2];
 };
 
@@ -456,8 +429,10 @@ gdn_apply(GdnArgs a) {
   __shared__ __attribute__((aligned(16))) bf16_t Qs[kC * kS];
   __shared__ __attribute__((aligned(16))) bf16_t Vs[kC * 24];  // [t][16 rows] + pad
   __shared__ __attribute__((aligned(16))) float Ss[16 * kSF];  // state slice [r][d]
+  __shared__ __attribute__((aligned(16))) float Xt[16 * kDF];  // X^T [r][t]
   __shared__ __attribute__((aligned(16))) float Dt[16 * kDF];  // Delta^T [r][t]
-  __shared__ float Gs[kC];
+  __shared__ __attribute__((aligned(16))) float Gs[kC];
+  __shared__ __attribute__((aligned(16))) float Bs[kC];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hl = lane & 15, quad = lane >> 4;
@@ -473,7 +448,7 @@ gdn_apply(GdnArgs a) {
   }
   const int tr_row = 4 * quad + (hl >> 2);
   const int tr_col = 4 * (hl & 3);
-  const int trow = 16 * wave + hl;  // A-operand row of this lane
+  const int tw = 16 * wave;  // first token of this wave's 16-token tile
 
   // Every load reads a clamped row and is issued unconditionally; rows past
   // the end of the sequence are zeroed when staged, so a fetch puts its whole
@@ -493,24 +468,21 @@ gdn_apply(GdnArgs a) {
     in.v = *(const bf16x8*)((const bf16_t*)a.v +
                             (((int64_t)b * a.T + min(t0 + t, a.T - 1)) * a.Hv + h) * a.Dv + r0 +
                             8 * half);
-    in.g = a.ws[(bh * a.nchunks + c) * ws_per_chunk(DK) + (tid & (kC - 1))];
+    const ChunkWs w = chunk_ws(a.ws + (bh * a.nchunks + c) * ws_per_chunk());
+    in.g = w.g[tid & (kC - 1)];
+    in.beta = w.beta[tid & (kC - 1)];
   };
-  auto fetch_delta = [&](DeltaIn<DK>& in, int c) __attribute__((always_inline)) {
-    const ChunkWs w = chunk_ws(a.ws + (bh * a.nchunks + c) * ws_per_chunk(DK), DK);
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      in.w_hi[ks] = *(const bf16x8*)(w.w_hi + ((wave * KS + ks) * 64 + lane) * 8);
-      in.w_lo[ks] = *(const bf16x8*)(w.w_lo + ((wave * KS + ks) * 64 + lane) * 8);
-    }
+  auto fetch_t = [&](TIn& in, int c) __attribute__((always_inline)) {
+    const ChunkWs w = chunk_ws(a.ws + (bh * a.nchunks + c) * ws_per_chunk());
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       const int f = ((wave * 2 + ks) * 64 + lane) * 8;
-      in.u_hi[ks] = *(const bf16x8*)(w.u_hi + f);
-      in.u_lo[ks] = *(const bf16x8*)(w.u_lo + f);
+      in.t_hi[ks] = *(const bf16x8*)(w.t_hi + f);
+      in.t_lo[ks] = *(const bf16x8*)(w.t_lo + f);
     }
   };
-  auto fetch_out = [&](OutIn& in, int c) __attribute__((always_inline)) {
-    const ChunkWs w = chunk_ws(a.ws + (bh * a.nchunks + c) * ws_per_chunk(DK), DK);
+  auto fetch_m = [&](MIn& in, int c) __attribute__((always_inline)) {
+    const ChunkWs w = chunk_ws(a.ws + (bh * a.nchunks + c) * ws_per_chunk());
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       const int f = ((wave * 2 + ks) * 64 + lane) * 8;
@@ -523,17 +495,17 @@ gdn_apply(GdnArgs a) {
   // chunk c, into the same registers, so the loads overlap the rest of the
   // chunk without a second register set.  The last chunk re-reads itself
   // (unused) rather than branching, which would make the compiler wait for
-  // every outstanding load at the top of the loop.
+  // every outstanding load at the top of the loop.  Issue order st, ti, mi
+  // as in the loop (the loads complete in order, so the loop's first wait
+  // for st must not also cover ti and mi).
   StageIn<DK> st;
-  DeltaIn<DK> dl;
-  OutIn oi;
-  // Issue order st, dl, oi as in the loop (the loads complete in order, so the
-  // loop's first wait for st must not also cover dl and oi).
+  TIn ti;
+  MIn mi;
   fetch_stage(st, 0);
   __builtin_amdgcn_sched_barrier(0);
-  fetch_delta(dl, 0);
+  fetch_t(ti, 0);
   __builtin_amdgcn_sched_barrier(0);
-  fetch_out(oi, 0);
+  fetch_m(mi, 0);
   __builtin_amdgcn_sched_barrier(0);
   for (int c = 0; c < a.nchunks; ++c) {
     const int t0 = c * kC;
@@ -549,7 +521,10 @@ gdn_apply(GdnArgs a) {
     }
     if (tid < kC * 2)
       *(bf16x8*)(Vs + (tid >> 1) * 24 + 8 * (tid & 1)) = t0 + (tid >> 1) < a.T ? st.v : zero;
-    if (tid < kC) Gs[tid] = st.g;
+    if (tid < kC) {
+      Gs[tid] = st.g;
+      Bs[tid] = st.beta;
+    }
     __syncthreads();
     fetch_stage(st, cn);
 
@@ -557,52 +532,87 @@ gdn_apply(GdnArgs a) {
     bf16x8 shi[KS], slo[KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) split8(Ss + hl * kSF + 32 * ks + 8 * quad, shi[ks], slo[ks]);
-
-    // (1) Delta rows 16w.. = Ub V - W S^T
-    f32x4 ws_acc = {0.f, 0.f, 0.f, 0.f};
+    // Q and K rows of this wave's tokens (A operands).
+    bf16x8 qa[KS], ka[KS];
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      ws_acc = mfma16x16x32(dl.w_hi[ks], shi[ks], ws_acc);
-      ws_acc = mfma16x16x32(dl.w_hi[ks], slo[ks], ws_acc);
-      ws_acc = mfma16x16x32(dl.w_lo[ks], shi[ks], ws_acc);
+      qa[ks] = *(const bf16x8*)(Qs + (tw + hl) * kS + 32 * ks + 8 * quad);
+      ka[ks] = *(const bf16x8*)(Ks + (tw + hl) * kS + 32 * ks + 8 * quad);
     }
-    f32x4 uv = {0.f, 0.f, 0.f, 0.f};
+
+    // (1a) X = diag(beta) (V - diag(exp Gc) K S^T), rows tw.. (lane: t = tw + 4 quad + r, row hl)
+    f32x4 kst = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const bf16x4 v0 = lds_read_tr4(Vs + (32 * ks + tr_row) * 24 + tr_col);
-      const bf16x4 v1 = lds_read_tr4(Vs + (32 * ks + 16 + tr_row) * 24 + tr_col);
-      const bf16x8 vb = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
-      uv = mfma16x16x32(dl.u_hi[ks], vb, uv);
-      uv = mfma16x16x32(dl.u_lo[ks], vb, uv);
+    for (int ks = 0; ks < KS; ++ks) {
+      kst = mfma16x16x32(ka[ks], shi[ks], kst);
+      kst = mfma16x16x32(ka[ks], slo[ks], kst);
     }
+    {
+      const bf16x4 v4 = lds_read_tr4(Vs + (tw + tr_row) * 24 + tr_col);
+      const f32x4 g4 = *(const f32x4*)(Gs + tw + 4 * quad);
+      const f32x4 b4 = *(const f32x4*)(Bs + tw + 4 * quad);
+      f32x4 x;
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      Dt[hl * kDF + 16 * wave + 4 * quad + r] = uv[r] - ws_acc[r];  // Delta^T[state row][t]
-    fetch_delta(dl, cn);
+      for (int r = 0; r < 4; ++r) x[r] = b4[r] * (static_cast<float>(v4[r]) - fast_exp2(g4[r]) * kst[r]);
+      *(f32x4*)(Xt + hl * kDF + tw + 4 * quad) = x;
+    }
     // (2a) Q S^T for the output rows of this wave
     f32x4 qs = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      const bf16x8 qa = *(const bf16x8*)(Qs + trow * kS + 32 * ks + 8 * quad);
-      qs = mfma16x16x32(qa, shi[ks], qs);
-      qs = mfma16x16x32(qa, slo[ks], qs);
+      qs = mfma16x16x32(qa[ks], shi[ks], qs);
+      qs = mfma16x16x32(qa[ks], slo[ks], qs);
     }
-    __syncthreads();  // Dt complete; every wave has read Ss
+    __syncthreads();  // X complete; every wave has read Ss
 
-    // (2b) O = exp(Gc) Q S^T + M Delta
+    // (1b) Delta rows tw.. = T X.  T is lower triangular, so waves 0 and 1
+    // (tokens < 32) skip the k step over tokens 32..63.
+    f32x4 dacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      if (ks == 0 || wave >= 2) {
+        bf16x8 xhi, xlo;
+        split8(Xt + hl * kDF + 32 * ks + 8 * quad, xhi, xlo);
+        dacc = mfma16x16x32(ti.t_hi[ks], xhi, dacc);
+        dacc = mfma16x16x32(ti.t_hi[ks], xlo, dacc);
+        dacc = mfma16x16x32(ti.t_lo[ks], xhi, dacc);
+      }
+    }
+    *(f32x4*)(Dt + hl * kDF + tw + 4 * quad) = dacc;  // Delta^T[state row][t]
+    fetch_t(ti, cn);
+    __syncthreads();  // Dt complete; every wave has read Xt
+
+    // Delta in the k-slot order of the transposing reads:
+    // dv[ks][j] = Delta[32 ks + tr_slot(quad, j)][hl].
+    float dv[2][8];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const f32x4 d0 = *(const f32x4*)(Dt + hl * kDF + 32 * ks + 4 * quad);
+      const f32x4 d1 = *(const f32x4*)(Dt + hl * kDF + 32 * ks + 16 + 4 * quad);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        dv[ks][r] = d0[r];
+        dv[ks][4 + r] = d1[r];
+      }
+    }
+
+    // (2b) O = exp(Gc) Q S^T + M Delta (M's columns are stored in the same
+    // k-slot order as dv; M is causal, so waves 0 and 1 skip tokens 32..63).
     f32x4 md = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      bf16x8 dhi, dlo;
-      split8(Dt + hl * kDF + 32 * ks + 8 * quad, dhi, dlo);
-      md = mfma16x16x32(oi.m_hi[ks], dhi, md);
-      md = mfma16x16x32(oi.m_hi[ks], dlo, md);
-      md = mfma16x16x32(oi.m_lo[ks], dhi, md);
+      if (ks == 0 || wave >= 2) {
+        bf16x8 dhi, dlo;
+        split8(dv[ks], dhi, dlo);
+        md = mfma16x16x32(mi.m_hi[ks], dhi, md);
+        md = mfma16x16x32(mi.m_hi[ks], dlo, md);
+        md = mfma16x16x32(mi.m_lo[ks], dhi, md);
+      }
     }
-    fetch_out(oi, cn);
+    fetch_m(mi, cn);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int t = 16 * wave + 4 * quad + r;
+      const int t = tw + 4 * quad + r;
       if (t0 + t < a.T) {
         const float o = (fast_exp2(Gs[t]) * qs[r] + md[r]) * a.scale;
         ((TO*)a.out)[(((int64_t)b * a.T + t0 + t) * a.Hv + h) * a.Dv + r0 + hl] = from_f32<TO>(o);
@@ -616,10 +626,7 @@ gdn_apply(GdnArgs a) {
     for (int ks = 0; ks < 2; ++ks) {
       float x[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int t = 32 * ks + tr_slot(quad, j);
-        x[j] = Dt[hl * kDF + t] * fast_exp2(glast - Gs[t]);
-      }
+      for (int j = 0; j < 8; ++j) x[j] = dv[ks][j] * fast_exp2(glast - Gs[32 * ks + tr_slot(quad, j)]);
       split8(x, dthi[ks], dtlo[ks]);
     }
     const float gl = fast_exp2(glast);
@@ -763,7 +770,7 @@ extern "C" size_t alpx_gdn_chunk_workspace_bytes(int batch, int tokens, int valu
   using namespace alpx;
   if (batch <= 0 || tokens <= 0 || value_heads <= 0 || key_dim <= 0) return 0;
   const int64_t chunks = (tokens + kC - 1) / kC;
-  return (size_t)batch * value_heads * chunks * ws_per_chunk(key_dim) * sizeof(float);
+  return (size_t)batch * value_heads * chunks * ws_per_chunk() * sizeof(float);
 }
 
 extern "C" int alpx_gdn_chunk_prefill(float* state, const void* q, const void* k, const void* v,

@@ -10,17 +10,18 @@ cumulative log decay Gc[t] = g_0 + ... + g_t (within the chunk) and
 gamma = exp(Gc):
 
   A[t, i]  = exp(Gc[t] - Gc[i]) * (k_t . k_i)      for i < t   (else 0)
-  M[t, i]  = exp(Gc[t] - Gc[i]) * (q_t . k_i)      for i <= t  (else 0)
   T        = (I + diag(beta) A)^-1                 (unit lower triangular)
-  Ub       = T diag(beta)                          (C x C)
-  W        = T diag(beta * gamma) K                (C x Dk)
-  Delta    = Ub V - W S^T                          (C x Dv; row t = delta_t)
+  X        = diag(beta) (V - diag(gamma) K S^T)    (C x Dv)
+  Delta    = T X                                   (C x Dv; row t = delta_t)
+  M[t, i]  = exp(Gc[t] - Gc[i]) * (q_t . k_i)      for i <= t  (else 0)
   O        = (diag(gamma) Q S^T + M Delta) / sqrt(Dk)
   S_next   = gamma[C-1] S + (diag(exp(Gc[C-1] - Gc)) Delta)^T K
 
-The state-independent part (A, M, T, Ub, W) is computed per (head, chunk)
-in parallel; only the last three lines carry the chunk-to-chunk dependency,
-and they are independent across the Dv rows of S.
+The state-independent part (Gc, T, M) is computed per (head, chunk) in
+parallel (phase A); the rest carries the chunk-to-chunk dependency (phase B)
+and is independent across the Dv rows of S.  Delta = T X is the familiar
+Ub V - W S^T with Ub = T diag(beta) and W = T diag(beta gamma) K
+(``delta_ub_w``), folded so that phase B reads T instead of Ub and W.
 """
 
 from __future__ import annotations
@@ -57,24 +58,32 @@ def invert_unit_lower(B, block=16):
     return T
 
 
-def chunk_prep(q, k, beta, g):
-    """State-independent per-chunk quantities.  q, k [C, Dk]; beta, g [C]."""
+def chunk_prep(k, beta, g):
+    """State-independent per-chunk quantities (phase A).  k [C, Dk]; beta, g [C]."""
     Gc = np.cumsum(g)
     decay = np.exp(Gc[:, None] - Gc[None, :])
-    C = q.shape[0]
+    C = k.shape[0]
     lower = np.tril(np.ones((C, C), dtype=bool), -1)
     A = np.where(lower, decay * (k @ k.T), 0.0)
-    M = np.where(lower | np.eye(C, dtype=bool), decay * (q @ k.T), 0.0)
     T = invert_unit_lower(beta[:, None] * A)
+    return Gc, T
+
+
+def delta_ub_w(S, k, v, beta, Gc, T):
+    """Delta in the unfolded form Ub V - W S^T (cross-check of T X)."""
     Ub = T * beta[None, :]
     W = Ub @ (np.exp(Gc)[:, None] * k)
-    return Gc, M, Ub, W
+    return Ub @ v - W @ S.T
 
 
-def chunk_apply(S, q, k, v, Gc, M, Ub, W):
-    """Carry the state through one chunk; returns (outputs [C, Dv], S_next)."""
+def chunk_apply(S, q, k, v, beta, Gc, T):
+    """Carry the state through one chunk (phase B); returns (outputs [C, Dv], S_next)."""
     dk = q.shape[1]
-    Delta = Ub @ v - W @ S.T
+    C = q.shape[0]
+    X = beta[:, None] * (v - np.exp(Gc)[:, None] * (k @ S.T))
+    Delta = T @ X
+    causal = np.tril(np.ones((C, C), dtype=bool))
+    M = np.where(causal, np.exp(Gc[:, None] - Gc[None, :]) * (q @ k.T), 0.0)
     O = (np.exp(Gc)[:, None] * (q @ S.T) + M @ Delta) / math.sqrt(dk)
     tail = np.exp(Gc[-1] - Gc)
     S_next = math.exp(Gc[-1]) * S + (tail[:, None] * Delta).T @ k
@@ -95,9 +104,9 @@ def gdn_chunked(state, q, k, v, beta, g, chunk=64):
         for c0 in range(0, t_count, chunk):
             s = slice(c0, c0 + chunk)
             qc, kc = q[s, kh].astype(np.float64), k[s, kh].astype(np.float64)
-            Gc, M, Ub, W = chunk_prep(qc, kc, beta[s, h].astype(np.float64),
-                                      g[s, h].astype(np.float64))
-            O, S = chunk_apply(S, qc, kc, v[s, h].astype(np.float64), Gc, M, Ub, W)
+            bc = beta[s, h].astype(np.float64)
+            Gc, T = chunk_prep(kc, bc, g[s, h].astype(np.float64))
+            O, S = chunk_apply(S, qc, kc, v[s, h].astype(np.float64), bc, Gc, T)
             out[s, h] = O
         state[h] = S
     return out

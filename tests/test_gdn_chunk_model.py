@@ -40,3 +40,17 @@ def test_chunked_c5_shape_slice():
     out = CM.gdn_chunked(s_chk, c["q"], c["k"], v, c["beta"][:, :4], c["g"][:, :4])
     np.testing.assert_allclose(out, ref, atol=1e-9)
     np.testing.assert_allclose(s_chk, s_seq, atol=1e-9)
+
+
+def test_folded_delta_equals_ub_w_form():
+    # Delta = T X (what phase B computes) against Ub V - W S^T formed
+    # separately, on one chunk with a nonzero state
+    c = I.c5_gdn_bf16(tokens=64, hk=1, hv=1, dk=32, dv=24)
+    rng = np.random.default_rng(2)
+    S = rng.standard_normal((24, 32)) * 0.3
+    k = c["k"][:, 0].astype(np.float64)
+    v = c["v"][:, 0].astype(np.float64)
+    beta = c["beta"][:, 0].astype(np.float64)
+    Gc, T = CM.chunk_prep(k, beta, c["g"][:, 0].astype(np.float64))
+    X = beta[:, None] * (v - np.exp(Gc)[:, None] * (k @ S.T))
+    np.testing.assert_allclose(T @ X, CM.delta_ub_w(S, k, v, beta, Gc, T), atol=1e-12)
