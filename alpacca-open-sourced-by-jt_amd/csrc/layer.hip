@@ -540,6 +540,114 @@ __global__ void __launch_bounds__(256) recurrent_chunk_prep_kernel(ChunkPrepArgs
   }
 }
 
+// Tiled form of the chunk prep for conv kernels of up to kTileTaps taps and
+// head dims that are multiples of 4 (at most 256): one block per (64-token
+// tile, head slot).  Thread (cg, tg) owns channels 4 cg .. 4 cg + 3 of the
+// slot for P = 64 / TG consecutive tokens and holds the P + K - 1 window
+// rows they need as 16-byte vectors, so each input element is loaded about
+// once instead of K times by K different waves.  The L2 norm of a q / k row
+// is a shuffle sum over the CG lanes that share the token (CG = channel
+// groups rounded up to 16, 32 or 64; idle lanes add zero).  Per element the
+// convolution, SiLU and scaling are the same operations, in the same order,
+// as recurrent_chunk_prep_kernel.
+constexpr int kTileTokens = 64;
+constexpr int kTileTaps = 4;
+
+inline bool aligned(const void* p, size_t bytes) { return (uintptr_t)p % bytes == 0; }
+
+template <typename TO>
+__device__ __forceinline__ void store4(TO* p, const float (&v)[4]) {
+  if constexpr (sizeof(TO) == 4) {
+    *(f32x4*)p = (f32x4){v[0], v[1], v[2], v[3]};
+  } else {
+    typedef TO T4 __attribute__((ext_vector_type(4)));
+    *(T4*)p = (T4){from_f32<TO>(v[0]), from_f32<TO>(v[1]), from_f32<TO>(v[2]), from_f32<TO>(v[3])};
+  }
+}
+
+template <typename TO>
+__global__ void __launch_bounds__(256) recurrent_chunk_prep_tile(ChunkPrepArgs a) {
+  constexpr int kMaxP = 16;
+  const int tid = threadIdx.x;
+  const int j = blockIdx.y;
+  const int t0 = blockIdx.x * kTileTokens;
+  const int C = 2 * a.Hk * a.Dk + a.Hv * a.Dv;
+  const bool is_qk = j < 2 * a.Hk;
+  int c0, n;
+  TO* dst;
+  int64_t dstride;
+  if (is_qk) {
+    c0 = j * a.Dk;
+    n = a.Dk;
+    dst = j < a.Hk ? (TO*)a.q + (int64_t)j * a.Dk : (TO*)a.k + (int64_t)(j - a.Hk) * a.Dk;
+    dstride = (int64_t)a.Hk * a.Dk;
+  } else {
+    const int h = j - 2 * a.Hk;
+    c0 = 2 * a.Hk * a.Dk + h * a.Dv;
+    n = a.Dv;
+    dst = (TO*)a.v + (int64_t)h * a.Dv;
+    dstride = (int64_t)a.Hv * a.Dv;
+    if (tid < kTileTokens && t0 + tid < a.T) {
+      const int64_t th = (int64_t)(t0 + tid) * a.Hv + h;
+      a.beta[th] = stable_sigmoid(a.bl[th]);
+      a.g[th] = softplus_f(a.al[th] + a.dtb[h]) * a.ssm[h];
+    }
+  }
+  const int ng = n >> 2;
+  const int CG = ng <= 16 ? 16 : ng <= 32 ? 32 : 64;
+  const int P = kTileTokens * CG / 256;  // 4, 8 or 16
+  const int cg = tid & (CG - 1), tg = tid / CG;
+  const bool act = cg < ng;
+  const int c = c0 + 4 * (act ? cg : 0);
+  const int tb = t0 + tg * P;
+  const int K = a.K;
+
+  float w[kTileTaps][4];
+#pragma unroll
+  for (int tap = 0; tap < kTileTaps; ++tap)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) w[tap][e] = tap < K ? a.w[tap * a.w_tap + (c + e) * a.w_ch] : 0.f;
+  // Window rows tb .. tb + P + K - 2 of E = [history; x]; rows past the
+  // end of x read its last row (their tokens are not stored).
+  f32x4 win[kMaxP + kTileTaps - 1];
+#pragma unroll
+  for (int r = 0; r < kMaxP + kTileTaps - 1; ++r) {
+    win[r] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    if (r < P + K - 1) {
+      const int er = tb + r;
+      const int xr = er - (K - 1);
+      const float* src = xr < 0 ? a.hist + (int64_t)er * C + c
+                                : a.x + (int64_t)min(xr, a.T - 1) * C + c;
+      win[r] = *(const f32x4*)src;
+    }
+  }
+#pragma unroll
+  for (int p = 0; p < kMaxP; ++p) {
+    if (p < P) {
+      float y[4];
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float acc = 0.f;
+#pragma unroll
+        for (int tap = 0; tap < kTileTaps; ++tap)
+          if (tap < K && p + tap < kMaxP + kTileTaps - 1) acc = fmaf(win[p + tap][e], w[tap][e], acc);
+        y[e] = silu_f(acc);
+        ss = fmaf(y[e], y[e], ss);
+      }
+      if (is_qk) {
+        ss = act ? ss : 0.f;
+        for (int off = CG >> 1; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+        const float inv = 1.f / fmaxf(sqrtf(ss), a.eps);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] *= inv;
+      }
+      const int t = tb + p;
+      if (act && t < a.T) store4(dst + (int64_t)t * dstride + 4 * cg, y);
+    }
+  }
+}
+
 // History after the chunk: the last K - 1 rows of E = [history; x].  One
 // thread per channel walks the rows upward, so a history row it still has
 // to read (row T + r > r) is never overwritten first.
@@ -918,12 +1026,27 @@ extern "C" int alpx_recurrent_prefill_prep(const float* current, const float* co
   a.eps = eps;
   hipStream_t s = (hipStream_t)stream;
   TimedRegion timed(ALPX_T_LAYER, s);
-  const int64_t waves = (int64_t)tokens * (2 * key_heads + value_heads);
-  const dim3 grid((unsigned)((waves + 3) / 4));
-  switch (out_dtype) {
-    case ALPX_F32: hipLaunchKernelGGL(recurrent_chunk_prep_kernel<float>, grid, dim3(256), 0, s, a); break;
-    case ALPX_F16: hipLaunchKernelGGL(recurrent_chunk_prep_kernel<f16_t>, grid, dim3(256), 0, s, a); break;
-    default: hipLaunchKernelGGL(recurrent_chunk_prep_kernel<bf16_t>, grid, dim3(256), 0, s, a); break;
+  const int slots = 2 * key_heads + value_heads;
+  const size_t osz = dtype_size(out_dtype);
+  const bool tiled = conv_kernel <= kTileTaps && key_dim % 4 == 0 && value_dim % 4 == 0 &&
+                     key_dim <= 256 && value_dim <= 256 && aligned(current, 16) &&
+                     (conv_kernel == 1 || aligned(conv_history, 16)) &&
+                     aligned(q_out, 4 * osz) && aligned(k_out, 4 * osz) && aligned(v_out, 4 * osz);
+  if (tiled) {
+    const dim3 grid((unsigned)((tokens + kTileTokens - 1) / kTileTokens), (unsigned)slots);
+    switch (out_dtype) {
+      case ALPX_F32: hipLaunchKernelGGL(recurrent_chunk_prep_tile<float>, grid, dim3(256), 0, s, a); break;
+      case ALPX_F16: hipLaunchKernelGGL(recurrent_chunk_prep_tile<f16_t>, grid, dim3(256), 0, s, a); break;
+      default: hipLaunchKernelGGL(recurrent_chunk_prep_tile<bf16_t>, grid, dim3(256), 0, s, a); break;
+    }
+  } else {
+    const int64_t waves = (int64_t)tokens * slots;
+    const dim3 grid((unsigned)((waves + 3) / 4));
+    switch (out_dtype) {
+      case ALPX_F32: hipLaunchKernelGGL(recurrent_chunk_prep_kernel<float>, grid, dim3(256), 0, s, a); break;
+      case ALPX_F16: hipLaunchKernelGGL(recurrent_chunk_prep_kernel<f16_t>, grid, dim3(256), 0, s, a); break;
+      default: hipLaunchKernelGGL(recurrent_chunk_prep_kernel<bf16_t>, grid, dim3(256), 0, s, a); break;
+    }
   }
   int rc = check_launch("alpx_recurrent_prefill_prep");
   if (rc != ALPX_OK || conv_kernel <= 1) return rc;

@@ -135,14 +135,20 @@ def _rec_inputs(rng, tokens, hk, hv, dk, dv, kernel):
                 s0=(f(hv, dv, dk) * 0.1))
 
 
-@pytest.mark.parametrize("tokens,kernel", [(37, 4), (2, 4), (5, 1), (9, 6)])
-def test_recurrent_prefill_prep_matches_oracle(gpu, tokens, kernel):
+@pytest.mark.parametrize("tokens,kernel,hk,hv,dk,dv", [
+    (37, 4, 2, 4, 64, 32), (2, 4, 2, 4, 64, 32), (5, 1, 2, 4, 64, 32), (9, 6, 2, 4, 64, 32),
+    (150, 4, 1, 2, 256, 128), (70, 3, 2, 4, 128, 40), (65, 2, 1, 3, 20, 36),
+    (21, 4, 1, 2, 30, 16)])
+def test_recurrent_prefill_prep_matches_oracle(gpu, tokens, kernel, hk, hv, dk, dv):
     # conv + SiLU over the chunk continuing the history, split, L2 norm,
-    # beta / decay (fp32 outputs), and the history moved on
+    # beta / decay (fp32 outputs), and the history moved on; kernels of up
+    # to 4 taps with head dims that are multiples of 4 take the tiled
+    # kernel (token tiles of 64, partial last tile), the rest (6 taps,
+    # dk = 30) the per-wave kernel
     import torch
     P = _mod("_ops")
     rng = np.random.default_rng(tokens * 10 + kernel)
-    hk, hv, dk, dv, eps = 2, 4, 64, 32, 1e-6
+    eps = 1e-6
     x = _rec_inputs(rng, tokens, hk, hv, dk, dv, kernel)
     H = _f32(torch, x["hist"], gpu) if kernel > 1 else None
     q, k, v, beta, g = P.recurrent_prefill_prep(
