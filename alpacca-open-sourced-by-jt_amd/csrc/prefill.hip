@@ -262,33 +262,40 @@ prefill_mfma(PrefillArgs a) {
   // most about one tile per wave and keeps the waves' pipelines in step.
   const int nt = (hi - lo + BK - 1) / BK;
 
-  // B operand of S^T = K Q^T: lane holds Q[column][32 ks + 8 quad + 0..7].
+  // B operand of S^T = K Q^T: lane holds Q[column][32 ks + 8 quad + 0..7],
+  // pre-multiplied by scale * log2(e) (and rounded once to T), so that the
+  // product lands in the base-2 softmax domain.
+  const float c2 = a.scale_log2;
   V8 qv[NQB][KS];
 #pragma unroll
   for (int qb = 0; qb < NQB; ++qb) {
     const T* qp = (const T*)a.q + ((int64_t)tok[qb] * a.q_heads + hq[qb]) * D + 8 * quad;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      const V8 x = *(const V8*)(qp + 32 * ks);
+      V8 x = *(const V8*)(qp + 32 * ks);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = from_f32<T>(to_f32(x[e]) * c2);
       qv[qb][ks] = cok[qb] ? x : (V8){};
     }
   }
 
   f32x4 o[NQB][MB];   // O^T[d = 16 mb + 4 quad + i][column]
   float lsum[NQB];    // this lane's share (its 4-key slices) of the column's sum of P
-  float m[NQB], mc[NQB], pend[NQB];  // mc = m * c2 (0 while m = -inf)
+  // m: the column's reference max (base-2 domain); mc: the offset the QK
+  // product subtracts through its accumulator input (m, or 0 while m is
+  // -inf); lim: how far above mc a score may reach before m must move.
+  float m[NQB], mc[NQB], lim[NQB], pend[NQB];
 #pragma unroll
   for (int qb = 0; qb < NQB; ++qb) {
     m[qb] = -INFINITY;
     mc[qb] = 0.f;
+    lim[qb] = -INFINITY;
     pend[qb] = 1.f;
     lsum[qb] = 0.f;
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) o[qb][mb] = (f32x4){0.f, 0.f, 0.f, 0.f};
   }
   bool pend_any = false;
-  const float c2 = a.scale_log2;
-  const float thr = kRescale / c2;
 
   // Direct loads: wave-instruction q of a tile fills LDS bytes [1024 q,
   // 1024 q + 1024), lane L the 16 bytes at 1024 q + 16 L, i.e. row
@@ -382,12 +389,13 @@ prefill_mfma(PrefillArgs a) {
     }
   };
   // Online softmax, base 2, with a lazy reference max: a column's m moves
-  // only when one of its scores exceeds m by more than kRescale / c2 (so P
-  // stays <= 2^kRescale), and the O / l rescale a move needs is applied
-  // before the next PV step.  The scores of tile j are in registers when
-  // iteration j starts, so the growth check runs there, ahead of the
-  // interleaved block: each lane compares the max of its own scores with
-  // m + thr, and only when some lane of the wave grew (rare after a
+  // only when one of its scores exceeds m by more than kRescale (so P stays
+  // <= 2^kRescale), and the O / l rescale a move needs is applied before
+  // the next PV step.  The QK product takes -mc as its accumulator input,
+  // so scores arrive as s * scale * log2(e) - mc and P is exp2 of the score
+  // as it stands.  The scores of tile j are in registers when iteration j
+  // starts, so the growth check runs there, ahead of the interleaved block:
+  // each lane compares the max of its own scores with lim, and only when some lane of the wave grew (rare after a
   // column's first tile) does the wave take the exact column max across the
   // four lanes of each column (l, l ^ 16, l ^ 32, l ^ 48) and move m.  The
   // block then forms P against the settled m.
@@ -400,7 +408,7 @@ prefill_mfma(PrefillArgs a) {
       for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
         for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[kb][qb][i]);
-      grow |= mx > m[qb] + thr;
+      grow |= mx > lim[qb];
     }
     return __ballot(grow) != 0;
   };
@@ -414,13 +422,20 @@ prefill_mfma(PrefillArgs a) {
         for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[kb][qb][i]);
       mx = fmaxf(mx, __shfl_xor(mx, 16));
       mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const bool g = mx > m[qb] + thr;
-      const float mn = g ? mx : m[qb];
-      pend[qb] = g ? fast_exp2((m[qb] - mn) * c2) : 1.f;
+      const bool g = mx > lim[qb];
+      const float mn = g ? mx + mc[qb] : m[qb];
+      pend[qb] = g ? fast_exp2(m[qb] - mn) : 1.f;
       lsum[qb] *= pend[qb];  // l takes tile j's P next, formed against the moved m
       pend_any |= __ballot(g) != 0;
+      // this tile's scores hold s - mc(old); shift them onto the new offset
+      const float sh = g ? mx : 0.f;
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sc[kb][qb][i] -= sh;
       m[qb] = mn;
-      mc[qb] = mn == -INFINITY ? 0.f : mn * c2;
+      mc[qb] = g ? mn : mc[qb];
+      lim[qb] = m[qb] - mc[qb] + kRescale;
     }
   };
   auto need_mask = [&](int t) {
@@ -475,13 +490,13 @@ prefill_mfma(PrefillArgs a) {
 #pragma unroll
         for (int qb = 0; qb < NQB; ++qb)
           sc[kb][qb] = mfma16x16x32(opd[O], qv[qb][ks],
-                                    ks == 0 ? (f32x4){0.f, 0.f, 0.f, 0.f} : sc[kb][qb]);
+                                    ks == 0 ? (f32x4){-mc[qb], -mc[qb], -mc[qb], -mc[qb]} : sc[kb][qb]);
       }
       if constexpr (O < NS) {
         constexpr int kb = O / NQB, qb = O % NQB;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float p = fast_exp2(__builtin_fmaf(sc[kb][qb][i], c2, -mc[qb]));
+          const float p = fast_exp2(sc[kb][qb][i]);
           lsum[qb] += p;
           pv[P][kb >> 1][qb][4 * (kb & 1) + i] = from_f32<T>(p);
         }
@@ -528,6 +543,7 @@ prefill_mfma(PrefillArgs a) {
     for (int qb = 0; qb < NQB; ++qb) {
       pin(m[qb]);
       pin(mc[qb]);
+      pin(lim[qb]);
       pin(pend[qb]);
       pin(lsum[qb]);
 #pragma unroll
