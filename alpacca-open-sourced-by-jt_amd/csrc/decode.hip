@@ -36,6 +36,10 @@ namespace alpx {
 namespace {
 
 constexpr int kTile = 32;   // rows per wavefront step (MFMA path)
+// Lazy softmax reference of the MFMA split kernel: P stays <= 2^8.
+constexpr float kDecodeRescale = 8.0f;
+// Buffer-load cache policy: nontemporal (V is streamed once per step).
+constexpr int kAuxNontemporal = 2;
 constexpr int kWaves = 4;   // wavefronts (= slots) per block (MFMA path)
 constexpr int kGenericTile = 64;
 constexpr int kMaxSlots = 2048;
@@ -183,7 +187,6 @@ decode_split_mfma(DecodeArgs a) {
   const int len = seq_len(a, b);
   const int start = max(blockIdx.x * a.chunk, seq_lo(a, b, len));
   const int end = min(blockIdx.x * a.chunk + a.chunk, len);
-  const int last = end - 1;
   const int hl = lane & 15;  // query-head column (N index) of this lane
   const int quad = lane >> 4;
   const int g_in = hc * 16 + hl;
@@ -214,25 +217,33 @@ decode_split_mfma(DecodeArgs a) {
 
   V8 kr[kIters];  // K rows, 16 bytes per lane, row-major
   V8 vr[kIters];  // V rows, same layout
+  // Tile loads are raw buffer loads from the tile's first row: load `it`
+  // covers rows kRowsPerLoad * it + lane / kUnits, 16-byte unit lane %
+  // kUnits, so a lane's byte offset is its base plus it * (row step), one
+  // add per load.  The buffer ends at row `end`: rows past it read as zero
+  // (their scores are masked, their P is zero).
+  constexpr int kRowsPerLoad = 64 / kUnits;
+  const uint32_t koff = (uint32_t)(((lane / kUnits) * a.ks_pos + 8 * (lane % kUnits)) * (int64_t)sizeof(T));
+  const uint32_t voff = (uint32_t)(((lane / kUnits) * a.vs_pos + 8 * (lane % kUnits)) * (int64_t)sizeof(T));
+  const uint32_t kstep = (uint32_t)(kRowsPerLoad * a.ks_pos * (int64_t)sizeof(T));
+  const uint32_t vstep = (uint32_t)(kRowsPerLoad * a.vs_pos * (int64_t)sizeof(T));
   auto load_tile = [&](int p) {
     // Paged: a wave tile starts at a multiple of kTile and never crosses a
     // page (page size a multiple of kTile), so its page is looked up once.
-    const T* kt = kbase;
-    const T* vt = vbase;
+    const T* kt = kbase + (int64_t)p * a.ks_pos;
+    const T* vt = vbase + (int64_t)p * a.vs_pos;
     if constexpr (PAGED) {
-      kt = (const T*)a.k + row_offset(a, b, kvh, p, a.ks_pos, 0, a.ks_h, a.ks_page) -
-           (int64_t)p * a.ks_pos;
-      vt = (const T*)a.v + row_offset(a, b, kvh, p, a.vs_pos, 0, a.vs_h, a.vs_page) -
-           (int64_t)p * a.vs_pos;
+      kt = (const T*)a.k + row_offset(a, b, kvh, p, a.ks_pos, 0, a.ks_h, a.ks_page);
+      vt = (const T*)a.v + row_offset(a, b, kvh, p, a.vs_pos, 0, a.vs_h, a.vs_page);
     }
+    const int rows = min(end - p, kTile);
+    const __amdgpu_buffer_rsrc_t kres = buffer_rsrc(kt, (uint32_t)(rows * a.ks_pos * (int64_t)sizeof(T)));
+    const __amdgpu_buffer_rsrc_t vres = buffer_rsrc(vt, (uint32_t)(rows * a.vs_pos * (int64_t)sizeof(T)));
 #pragma unroll
     for (int it = 0; it < kIters; ++it) {
-      const int u = it * 64 + lane;
-      const int r = u / kUnits;
-      const int c = u - r * kUnits;
-      const int row = min(p + r, last);
-      kr[it] = *(const V8*)(kt + (int64_t)row * a.ks_pos + 8 * c);
-      vr[it] = __builtin_nontemporal_load((const V8*)(vt + (int64_t)row * a.vs_pos + 8 * c));
+      kr[it] = __builtin_bit_cast(V8, __builtin_amdgcn_raw_buffer_load_b128(kres, koff + it * kstep, 0, 0));
+      vr[it] = __builtin_bit_cast(
+          V8, __builtin_amdgcn_raw_buffer_load_b128(vres, voff + it * vstep, 0, kAuxNontemporal));
     }
   };
 
@@ -274,8 +285,13 @@ decode_split_mfma(DecodeArgs a) {
     }
     mx = fmaxf(mx, __shfl_xor(mx, 16));
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float mn = fmaxf(m, mx);  // finite: every tile holds at least one live row
-    const float alpha = fast_exp2(m - mn);
+    // Lazy reference max: m moves only when the tile's max exceeds it by
+    // more than kDecodeRescale (so P <= 2^kDecodeRescale), and O is rescaled
+    // only on a step where some head of the wave moved.  Every tile holds at
+    // least one live row, so the first tile always moves m off -inf.
+    const bool grow = mx > m + kDecodeRescale;
+    const float mn = grow ? mx : m;
+    const float alpha = grow ? fast_exp2(m - mn) : 1.f;
     V8 pv;
     float ps = 0.f;
 #pragma unroll
@@ -286,8 +302,10 @@ decode_split_mfma(DecodeArgs a) {
     }
     l = l * alpha + ps;
     m = mn;
+    if (__builtin_expect(__ballot(grow) != 0, 0)) {
 #pragma unroll
-    for (int mb = 0; mb < D / 16; ++mb) o[mb] *= alpha;
+      for (int mb = 0; mb < D / 16; ++mb) o[mb] *= alpha;
+    }
     // O^T += V^T P^T.  A operand: lane holds V[row(quad, j)][16 mb + hl], j = 0..7,
     // gathered with two transposing reads of 4 rows (16 h + 4 quad + 0..3) each.
     const int tr_row = 4 * quad + (hl >> 2);
@@ -758,7 +776,10 @@ int run_decode(DecodeArgs a, int dtype, int out_dtype, void* workspace, size_t w
                           (uintptr_t)(a.vs_b * es) | (uintptr_t)(a.vs_h * es) |
                           (uintptr_t)(a.ks_page * es) | (uintptr_t)(a.vs_page * es);
   const int D = a.key_dim;
+  // the MFMA kernels address a wave tile's rows with 32-bit byte offsets
+  const int64_t max_pos = a.ks_pos > a.vs_pos ? a.ks_pos : a.vs_pos;
   const bool mfma = D == a.value_dim && (D == 64 || D == 128 || D == 256) && (align & 15) == 0 &&
+                    (int64_t)kTile * max_pos * (int64_t)es < ((int64_t)1 << 31) &&
                     getenv("ALPX_DECODE_GENERIC") == nullptr;
   const size_t need = decode_workspace(a.batch, a.q_heads, a.kv_heads, a.value_dim, a.length);
   if (workspace_bytes < need)
