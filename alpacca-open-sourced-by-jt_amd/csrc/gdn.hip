@@ -744,7 +744,7 @@ int gdn_step_launch(float* state, const void* q, const void* k, const void* v, c
   a.Hv = value_heads;
   a.Dk = key_dim;
   a.Dv = value_dim;
-  a.scale = 1.0f / sqrtf((float)key_dim);
+  a.scale = gdn_output_scale(key_dim);
   switch (dtype) {
     case ALPX_F32: return launch_step<float>(a, out_dtype, s);
     case ALPX_F16: return launch_step<f16_t>(a, out_dtype, s);
@@ -799,7 +799,7 @@ extern "C" int alpx_gdn_chunk_prefill(float* state, const void* q, const void* k
   a.Dk = key_dim;
   a.Dv = value_dim;
   a.nchunks = (tokens + kC - 1) / kC;
-  a.scale = 1.0f / sqrtf((float)key_dim);
+  a.scale = gdn_output_scale(key_dim);
   const uintptr_t align = (uintptr_t)q | (uintptr_t)k | (uintptr_t)v;
   const bool chunked = dtype == ALPX_BF16 && (key_dim == 64 || key_dim == 128 || key_dim == 256) &&
                        value_dim % 16 == 0 && (align & 15) == 0 &&

@@ -75,11 +75,9 @@ struct NormArgs {
   float eps;
 };
 
+// Row r of a row norm, by one wave.
 template <typename T, typename TO, int MODE>
-__global__ void __launch_bounds__(256) row_norm_kernel(NormArgs a) {
-  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (r >= a.rows) return;  // the whole wave leaves together
-  const int lane = threadIdx.x & 63;
+__device__ __forceinline__ void norm_row(const NormArgs& a, int64_t r, int lane) {
   const T* x = (const T*)a.x + (r / a.grp_rows) * a.grp_stride + (r % a.grp_rows) * a.n;
   float ss = 0.f;
   for (int i = lane; i < a.n; i += 64) {
@@ -96,6 +94,13 @@ __global__ void __launch_bounds__(256) row_norm_kernel(NormArgs a) {
     if (MODE == kNormRmsGate) v *= silu_f(to_f32(g[i]));
     o[i] = from_f32<TO>(v);
   }
+}
+
+template <typename T, typename TO, int MODE>
+__global__ void __launch_bounds__(256) row_norm_kernel(NormArgs a) {
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= a.rows) return;  // the whole wave leaves together
+  norm_row<T, TO, MODE>(a, r, threadIdx.x & 63);
 }
 
 template <typename T, typename TO>
@@ -349,38 +354,17 @@ struct PrepArgs {
   float eps;
 };
 
-// One wave per (sequence, head slot): Hk query slots, Hk key slots, Hv
-// value slots.  Each lane convolves its channels (then SiLU) and shifts
-// their history; query / key slots L2-normalise the head; value slot h
-// also forms beta and the log decay of value head h.
-__global__ void __launch_bounds__(256) recurrent_prep_kernel(PrepArgs a) {
-  const int wave = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
-  const int slots = 2 * a.Hk + a.Hv;
-  const int64_t id = (int64_t)blockIdx.x * 4 + wave;
-  if (id >= (int64_t)a.B * slots) return;
-  const int b = (int)(id / slots);
-  const int j = (int)(id - (int64_t)b * slots);
+// Convolution step of one head slot of sequence b (one wave): channels
+// [c0, c0 + n) of the C = 2 Hk Dk + Hv Dv mixed channels.  Each lane
+// convolves its channels (then SiLU) and shifts their history; `l2` slots
+// (query / key) are L2-normalised over the head.  Results go to dst[0, n).
+// `mid` runs between the slot's loads and its arithmetic (a caller issues
+// further loads there, so that the slot's waits do not cover them).  Rows
+// of up to 64 kPer channels.
+template <int kPer, typename Mid>
+__device__ __forceinline__ void prep_slot(const PrepArgs& a, int b, int c0, int n, bool l2,
+                                          float* dst, int lane, Mid&& mid) {
   const int C = 2 * a.Hk * a.Dk + a.Hv * a.Dv;
-  int c0, n;
-  float* dst;
-  if (j < 2 * a.Hk) {
-    c0 = j * a.Dk;
-    n = a.Dk;
-    dst = (j < a.Hk ? a.q + ((int64_t)b * a.Hk + j) * a.Dk
-                    : a.k + ((int64_t)b * a.Hk + (j - a.Hk)) * a.Dk);
-  } else {
-    const int h = j - 2 * a.Hk;
-    c0 = 2 * a.Hk * a.Dk + h * a.Dv;
-    n = a.Dv;
-    dst = a.v + ((int64_t)b * a.Hv + h) * a.Dv;
-    if (lane == 0) {
-      const int64_t bh = (int64_t)b * a.Hv + h;
-      a.beta[bh] = stable_sigmoid(a.bl[bh]);
-      a.g[bh] = softplus_f(a.al[bh] + a.dtb[h]) * a.ssm[h];
-    }
-  }
-  constexpr int kPer = kMaxDim / 64;
   constexpr int kTaps = 4;  // history rows held in registers (longer kernels loop)
   const int64_t rowC = (int64_t)b * C;
   float* hist = a.hist + (int64_t)b * (a.K - 1) * C;
@@ -400,6 +384,7 @@ __global__ void __launch_bounds__(256) recurrent_prep_kernel(PrepArgs a) {
     for (int t = 0; t <= kTaps; ++t)
       if (t < a.K) wv[e][t] = a.w[t * a.w_tap + c * a.w_ch];
   }
+  mid();
   float ss = 0.f;
 #pragma unroll
   for (int e = 0; e < kPer; ++e) {
@@ -423,13 +408,13 @@ __global__ void __launch_bounds__(256) recurrent_prep_kernel(PrepArgs a) {
     ss = fmaf(y[e], y[e], ss);
   }
   float inv = 1.f;
-  if (j < 2 * a.Hk) inv = 1.f / fmaxf(sqrtf(wave_sum(ss)), a.eps);
+  if (l2) inv = 1.f / fmaxf(sqrtf(wave_sum(ss)), a.eps);
 #pragma unroll
   for (int e = 0; e < kPer; ++e) {
     const int i = lane + 64 * e;
     if (i >= n) continue;
     const int c = c0 + i;
-    dst[i] = j < 2 * a.Hk ? y[e] * inv : y[e];
+    dst[i] = l2 ? y[e] * inv : y[e];
     // shift the lane's history column: row t takes row t + 1, the last row
     // takes the current sample
 #pragma unroll
@@ -439,6 +424,243 @@ __global__ void __launch_bounds__(256) recurrent_prep_kernel(PrepArgs a) {
       hist[(int64_t)t * C + c] = hist[(int64_t)(t + 1) * C + c];
     if (a.K > 1) hist[(int64_t)(a.K - 2) * C + c] = xc[e];
   }
+}
+
+// beta = sigmoid(b), log decay = softplus(a + dt_bias) * ssm_a of value head h.
+__device__ __forceinline__ void recurrent_params(const PrepArgs& a, int b, int h, float& beta,
+                                                 float& g) {
+  const int64_t bh = (int64_t)b * a.Hv + h;
+  beta = stable_sigmoid(a.bl[bh]);
+  g = softplus_f(a.al[bh] + a.dtb[h]) * a.ssm[h];
+}
+
+// One wave per (sequence, head slot): Hk query slots, Hk key slots, Hv
+// value slots; value slot h also forms beta and the log decay of value
+// head h.
+__global__ void __launch_bounds__(256) recurrent_prep_kernel(PrepArgs a) {
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int slots = 2 * a.Hk + a.Hv;
+  const int64_t id = (int64_t)blockIdx.x * 4 + wave;
+  if (id >= (int64_t)a.B * slots) return;
+  const int b = (int)(id / slots);
+  const int j = (int)(id - (int64_t)b * slots);
+  if (j < 2 * a.Hk) {
+    float* dst = j < a.Hk ? a.q + ((int64_t)b * a.Hk + j) * a.Dk
+                          : a.k + ((int64_t)b * a.Hk + (j - a.Hk)) * a.Dk;
+    prep_slot<kMaxDim / 64>(a, b, j * a.Dk, a.Dk, true, dst, lane, [] {});
+  } else {
+    const int h = j - 2 * a.Hk;
+    if (lane == 0) {
+      const int64_t bh = (int64_t)b * a.Hv + h;
+      recurrent_params(a, b, h, a.beta[bh], a.g[bh]);
+    }
+    prep_slot<kMaxDim / 64>(a, b, 2 * a.Hk * a.Dk + h * a.Dv, a.Dv, false,
+              a.v + ((int64_t)b * a.Hv + h) * a.Dv, lane, [] {});
+  }
+}
+
+// ------------------------------- recurrent-layer step in two launches
+//
+// Launch A, one block per (sequence, value head h, 16 state rows), the GDN
+// step's geometry (recurrent_rows_kernel): the block recomputes the
+// convolution + SiLU + L2 norm of h's query and key heads (key head
+// h % Hk) from the history without writing it, forms the convolution of
+// its own 16 value channels (and shifts their history: no other block
+// touches them), beta and the log decay, then runs the GDN step on its
+// rows and writes o.  Launch B (recurrent_finish_kernel): the gated
+// RMSNorm of every o row and the history shift of the query / key
+// channels, which every A block of the key head read.  Each value is
+// formed with the arithmetic, in the order, of recurrent_prep_kernel,
+// gdn_step_kernel and row_norm_kernel.
+
+constexpr int kRowsThreads = 256;
+constexpr int kRowsPerBlock = 16;  // 8 half-waves x kRowsPerHalf rows
+constexpr int kRowsPerHalf = 2;
+constexpr int kRowsDim = 256;      // widest key / value head of launch A
+
+struct RowsArgs {
+  PrepArgs p;   // q / k / v outputs unused; hist: value channels written
+  float* state;  // [B, Hv, Dv, Dk]
+  float* o;      // [B, Hv, Dv] fp32, scaled by 1 / sqrt(Dk)
+  float scale;
+};
+
+// Convolution + SiLU of channel c of sequence b (taps from the history,
+// the current sample last), as prep_slot: up to kTaps history rows and
+// their weights are loaded together before any arithmetic (a loop over a
+// run-time tap count would wait for each load in turn).
+__device__ __forceinline__ float conv_silu(const PrepArgs& a, int64_t rowC, const float* hist,
+                                           int C, int c) {
+  constexpr int kTaps = 4;
+  float hv[kTaps], wv[kTaps + 1];
+  const float xc = a.cur[rowC + c];
+#pragma unroll
+  for (int t = 0; t < kTaps; ++t)
+    if (t < a.K - 1) hv[t] = hist[(int64_t)t * C + c];
+#pragma unroll
+  for (int t = 0; t <= kTaps; ++t)
+    if (t < a.K) wv[t] = a.w[t * a.w_tap + c * a.w_ch];
+  float acc = 0.f;
+#pragma unroll
+  for (int t = 0; t < kTaps; ++t)
+    if (t < a.K - 1) acc = fmaf(hv[t], wv[t], acc);
+  for (int t = kTaps; t < a.K - 1; ++t)  // kernels longer than kTaps + 1 taps
+    acc = fmaf(hist[(int64_t)t * C + c], a.w[t * a.w_tap + c * a.w_ch], acc);
+  float wl = 0.f;  // weight of the current sample (tap K - 1)
+#pragma unroll
+  for (int t = 0; t <= kTaps; ++t)
+    if (t == a.K - 1) wl = wv[t];
+  if (a.K - 1 > kTaps) wl = a.w[(a.K - 1) * a.w_tap + c * a.w_ch];
+  acc = fmaf(xc, wl, acc);
+  return silu_f(acc);
+}
+
+template <int NV>
+__global__ void __launch_bounds__(kRowsThreads) recurrent_rows_kernel(RowsArgs f) {
+  const PrepArgs& a = f.p;
+  __shared__ float qk[2][kRowsDim];  // SiLU(conv) of the query and key heads, then normalised
+  __shared__ float inv[2];
+  __shared__ float vs[kRowsPerBlock];
+  __shared__ float bg[2];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = blockIdx.y, b = blockIdx.z, kh = h % a.Hk;
+  const int Dk = a.Dk, Dv = a.Dv;
+  const int C = 2 * a.Hk * Dk + a.Hv * Dv;
+  const int64_t rowC = (int64_t)b * C;
+  float* hist = a.hist + (int64_t)b * (a.K - 1) * C;
+  const int rb = blockIdx.x * kRowsPerBlock;
+  const int l32 = tid & 31, hw = tid >> 5;
+  const int r0 = rb + hw * kRowsPerHalf;
+  const int64_t bh = (int64_t)b * a.Hv + h;
+
+  // The state rows first (rows rb + 2 hw + j, lane columns 4 l32 + 128 e +
+  // 0..3, as gdn_step_kernel): they depend on nothing, so they are in
+  // flight with the convolution loads and the block waits one round trip.
+  float s[kRowsPerHalf][NV][4];
+#pragma unroll
+  for (int j = 0; j < kRowsPerHalf; ++j) {
+    const float* row = f.state + (bh * Dv + min(r0 + j, Dv - 1)) * Dk;
+#pragma unroll
+    for (int e = 0; e < NV; ++e) {
+      const int c0 = 4 * l32 + 128 * e;
+      const f32x4 x = *(const f32x4*)(row + min(c0, Dk - 4));
+#pragma unroll
+      for (int c = 0; c < 4; ++c) s[j][e][c] = c0 < Dk ? x[c] : 0.f;
+    }
+  }
+
+  // convolutions: query / key channel pairs, then the block's value rows
+  for (int i = tid; i < 2 * Dk; i += kRowsThreads) {
+    const int slot = i / Dk, d = i - slot * Dk;
+    qk[slot][d] = conv_silu(a, rowC, hist, C, slot * a.Hk * Dk + kh * Dk + d);
+  }
+  if (tid < kRowsPerBlock && rb + tid < Dv) {
+    const int c = 2 * a.Hk * Dk + h * Dv + rb + tid;
+    const float xc = a.cur[rowC + c];
+    vs[tid] = conv_silu(a, rowC, hist, C, c);
+    // shift this value channel's history (only this block reads it)
+    for (int t = 0; t + 1 < a.K - 1; ++t) hist[(int64_t)t * C + c] = hist[(int64_t)(t + 1) * C + c];
+    if (a.K > 1) hist[(int64_t)(a.K - 2) * C + c] = xc;
+  }
+  if (tid == kRowsThreads - 1) recurrent_params(a, b, h, bg[0], bg[1]);
+  __syncthreads();
+  // L2 norms of the query (wave 0) and key (wave 1) heads, summed as
+  // prep_slot sums them (lane-strided channels, then the wave sum)
+  if (wave < 2) {
+    float ss = 0.f;
+    for (int d = lane; d < Dk; d += 64) ss = fmaf(qk[wave][d], qk[wave][d], ss);
+    ss = wave_sum(ss);
+    if (lane == 0) inv[wave] = 1.f / fmaxf(sqrtf(ss), a.eps);
+  }
+  __syncthreads();
+
+  // GDN step on the block's rows, as gdn_step_kernel
+  float kk[NV][4], qq[NV][4];
+#pragma unroll
+  for (int e = 0; e < NV; ++e)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int col = 4 * l32 + 128 * e + c;
+      kk[e][c] = col < Dk ? qk[1][col] * inv[1] : 0.f;
+      qq[e][c] = col < Dk ? qk[0][col] * inv[0] : 0.f;
+    }
+  const float decay = __expf(bg[1]);
+  const float beta = bg[0];
+  float p[kRowsPerHalf];
+#pragma unroll
+  for (int j = 0; j < kRowsPerHalf; ++j) {
+    p[j] = 0.f;
+#pragma unroll
+    for (int e = 0; e < NV; ++e)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        s[j][e][c] *= decay;
+        p[j] += s[j][e][c] * kk[e][c];
+      }
+  }
+#pragma unroll
+  for (int off = 16; off >= 1; off >>= 1)
+#pragma unroll
+    for (int j = 0; j < kRowsPerHalf; ++j) p[j] += __shfl_xor(p[j], off, 32);
+  float o[kRowsPerHalf];
+#pragma unroll
+  for (int j = 0; j < kRowsPerHalf; ++j) {
+    const float vv = vs[min(r0 + j, Dv - 1) - rb];
+    const float delta = beta * (vv - p[j]);
+    o[j] = 0.f;
+#pragma unroll
+    for (int e = 0; e < NV; ++e)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        s[j][e][c] += delta * kk[e][c];
+        o[j] += s[j][e][c] * qq[e][c];
+      }
+  }
+#pragma unroll
+  for (int j = 0; j < kRowsPerHalf; ++j) {
+    const int r = r0 + j;
+    if (r >= Dv) break;
+    float* row = f.state + (bh * Dv + r) * Dk;
+#pragma unroll
+    for (int e = 0; e < NV; ++e) {
+      const int c0 = 4 * l32 + 128 * e;
+      if (c0 < Dk) *(f32x4*)(row + c0) = (f32x4){s[j][e][0], s[j][e][1], s[j][e][2], s[j][e][3]};
+    }
+  }
+#pragma unroll
+  for (int off = 16; off >= 1; off >>= 1)
+#pragma unroll
+    for (int j = 0; j < kRowsPerHalf; ++j) o[j] += __shfl_xor(o[j], off, 32);
+  if (l32 < kRowsPerHalf && r0 + l32 < Dv) {
+    const float oj = l32 == 0 ? o[0] : o[1];
+    f.o[bh * Dv + r0 + l32] = oj * f.scale;
+  }
+}
+
+// Launch B: waves [0, norm_rows) take one gated-norm row each; the rest
+// shift the history of the 2 Hk Dk query / key channels (one lane each).
+struct FinishArgs {
+  NormArgs norm;
+  const float* cur;  // [B, C]
+  float* hist;       // [B, K - 1, C]
+  int B, C, K, qk_channels;
+};
+
+template <typename TO>
+__global__ void __launch_bounds__(256) recurrent_finish_kernel(FinishArgs f) {
+  const int64_t w = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (w < f.norm.rows) {
+    norm_row<float, TO, kNormRmsGate>(f.norm, w, lane);
+    return;
+  }
+  const int64_t i = (w - f.norm.rows) * 64 + lane;
+  if (i >= (int64_t)f.B * f.qk_channels) return;
+  const int b = (int)(i / f.qk_channels), c = (int)(i - (int64_t)b * f.qk_channels);
+  float* hist = f.hist + (int64_t)b * (f.K - 1) * f.C;
+  for (int t = 0; t + 1 < f.K - 1; ++t) hist[(int64_t)t * f.C + c] = hist[(int64_t)(t + 1) * f.C + c];
+  if (f.K > 1) hist[(int64_t)(f.K - 2) * f.C + c] = f.cur[(int64_t)b * f.C + c];
 }
 
 // ----------------------------------- recurrent-layer prep over a chunk
@@ -960,6 +1182,49 @@ extern "C" int alpx_recurrent_step(const float* current, const float* conv_weigh
   a.eps = eps;
   hipStream_t s = (hipStream_t)stream;
   TimedRegion timed(ALPX_T_RECURRENT_STEP, s);
+  // Two launches (recurrent_rows_kernel, recurrent_finish_kernel) when the
+  // heads fit launch A; otherwise prep, GDN step and norm separately.
+  const bool rows_path = key_dim % 4 == 0 && key_dim <= kRowsDim && ((uintptr_t)state & 15) == 0 &&
+                         getenv("ALPX_RECURRENT_UNFUSED") == nullptr;
+  if (rows_path) {
+    RowsArgs ra;
+    ra.p = a;
+    ra.state = state;
+    ra.o = o;
+    ra.scale = gdn_output_scale(key_dim);
+    const dim3 grid((unsigned)((value_dim + kRowsPerBlock - 1) / kRowsPerBlock), value_heads, batch);
+    if (key_dim <= 128)
+      hipLaunchKernelGGL((recurrent_rows_kernel<1>), grid, dim3(kRowsThreads), 0, s, ra);
+    else
+      hipLaunchKernelGGL((recurrent_rows_kernel<2>), grid, dim3(kRowsThreads), 0, s, ra);
+    int rc = check_launch("alpx_recurrent_step rows");
+    if (rc != ALPX_OK) return rc;
+    FinishArgs fa;
+    fa.norm.x = o;
+    fa.norm.w = norm_weight;
+    fa.norm.gate = gate;
+    fa.norm.out = out;
+    fa.norm.rows = (int64_t)batch * value_heads;
+    fa.norm.grp_rows = fa.norm.rows;
+    fa.norm.grp_stride = fa.norm.rows * value_dim;
+    fa.norm.n = value_dim;
+    fa.norm.eps = eps;
+    fa.cur = current;
+    fa.hist = conv_history;
+    fa.B = batch;
+    fa.C = 2 * key_heads * key_dim + value_heads * value_dim;
+    fa.K = conv_kernel;
+    fa.qk_channels = 2 * key_heads * key_dim;
+    const int64_t shift_waves = conv_kernel > 1 ? ((int64_t)batch * fa.qk_channels + 63) / 64 : 0;
+    const int64_t fwaves = fa.norm.rows + shift_waves;
+    const dim3 fgrid((unsigned)((fwaves + 3) / 4));
+    switch (out_dtype) {
+      case ALPX_F32: hipLaunchKernelGGL((recurrent_finish_kernel<float>), fgrid, dim3(256), 0, s, fa); break;
+      case ALPX_F16: hipLaunchKernelGGL((recurrent_finish_kernel<f16_t>), fgrid, dim3(256), 0, s, fa); break;
+      default: hipLaunchKernelGGL((recurrent_finish_kernel<bf16_t>), fgrid, dim3(256), 0, s, fa); break;
+    }
+    return check_launch("alpx_recurrent_step finish");
+  }
   const int64_t waves = (int64_t)batch * (2 * key_heads + value_heads);
   hipLaunchKernelGGL(recurrent_prep_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, a);
   int rc = check_launch("alpx_recurrent_step prep");

@@ -234,10 +234,13 @@ def test_attention_prologue_then_gated_decode(gpu, ops, dtype):
 
 # ------------------------------------------------ recurrent-layer step
 
+# (1, 1, 2, 64, 300, 3): value rows wider than the one-launch step takes,
+# so the prep / GDN step / norm launches run.
 @pytest.mark.parametrize("batch,hk,hv,dk,dv,kernel", [(1, 16, 32, 128, 128, 4),
                                                       (2, 2, 4, 64, 96, 4),
                                                       (3, 1, 2, 256, 40, 4), (2, 2, 4, 64, 32, 6),
-                                                      (1, 2, 2, 32, 32, 2), (1, 2, 2, 32, 32, 1)])
+                                                      (1, 2, 2, 32, 32, 2), (1, 2, 2, 32, 32, 1),
+                                                      (1, 1, 2, 64, 300, 3)])
 def test_recurrent_layer_step_matches_oracle_over_tokens(gpu, ops, batch, hk, hv, dk, dv, kernel):
     import torch
     rng = np.random.default_rng(batch * 100 + hk + kernel)
@@ -266,6 +269,54 @@ def test_recurrent_layer_step_matches_oracle_over_tokens(gpu, ops, batch, hk, hv
         assert np.abs(out.cpu().numpy() - ref).max() <= 1e-4
     assert np.abs(ws.delta_state.cpu().numpy() - state).max() <= 1e-4
     assert np.array_equal(ws.convolution_history.cpu().numpy(), hist.astype(np.float32))
+
+
+def _recurrent_run(ops, torch, gpu, rng_seed, batch, hk, hv, dk, dv, kernel, out_dtype, steps):
+    """Runs `steps` recurrent-layer steps on a fresh workspace; returns the
+    outputs and the final state and convolution history (host copies)."""
+    rng = np.random.default_rng(rng_seed)
+    chn = 2 * hk * dk + hv * dv
+    w = (rng.standard_normal((kernel, chn)) * 0.5).astype(np.float32)
+    dt = rng.standard_normal(hv).astype(np.float32)
+    ssm = (-np.exp(rng.uniform(-1, 1, hv))).astype(np.float32)
+    nw = rng.uniform(0.5, 1.5, dv).astype(np.float32)
+    ws = ops.initialize_recurrent_workspace(batch_size=batch, convolution_kernel=kernel,
+                                            convolution_channels=chn, value_heads=hv,
+                                            value_dimension=dv, key_dimension=dk)
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(gpu)  # noqa: E731
+    outs = []
+    for _ in range(steps):
+        mixed = rng.standard_normal((batch, chn)).astype(np.float32)
+        gate = rng.standard_normal((batch, hv * dv)).astype(np.float32)
+        bl = rng.standard_normal((batch, hv)).astype(np.float32)
+        al = rng.standard_normal((batch, hv)).astype(np.float32)
+        out = ops.recurrent_layer_step_(ws, T(mixed), T(w), T(gate), T(bl), T(al), T(dt), T(ssm),
+                                        T(nw), key_heads=hk, key_dimension=dk, epsilon=1e-6,
+                                        out_dtype=out_dtype)
+        outs.append(out.float().cpu().numpy())
+    return outs, ws.delta_state.cpu().numpy(), ws.convolution_history.cpu().numpy()
+
+
+@pytest.mark.parametrize("out_name", ["f32", "bf16"])
+@pytest.mark.parametrize("batch,hk,hv,dk,dv,kernel", [(1, 16, 32, 128, 128, 4),
+                                                      (2, 2, 4, 64, 96, 4),
+                                                      (3, 1, 2, 256, 40, 4),
+                                                      (1, 2, 6, 32, 48, 1)])
+def test_recurrent_layer_step_one_launch_matches_three_launches(gpu, ops, monkeypatch, out_name,
+                                                                batch, hk, hv, dk, dv, kernel):
+    """The one-launch step (one block per key head) performs the prep / GDN
+    step / gated-norm arithmetic of the three-launch path in the same order,
+    so the two agree bit for bit (outputs, state and history)."""
+    import torch
+    args = (ops, torch, gpu, 7 + hk * 3 + kernel, batch, hk, hv, dk, dv, kernel,
+            _td(torch, out_name), 4)
+    fused = _recurrent_run(*args)
+    monkeypatch.setenv("ALPX_RECURRENT_UNFUSED", "1")
+    split = _recurrent_run(*args)
+    for a, b in zip(fused[0], split[0]):
+        assert np.array_equal(a, b)
+    assert np.array_equal(fused[1], split[1])
+    assert np.array_equal(fused[2], split[2])
 
 
 def test_qwen35_recurrent_layer_numpy(gpu):
