@@ -350,7 +350,10 @@ size_t alpx_recurrent_step_workspace_bytes(int batch, int key_heads, int value_h
  * beta_logits, alpha_logits [B, Hv], dt_bias, ssm_a [Hv]; the GDN step on
  * state [B, Hv, Dv, Dk] (alpx_gdn_step); then out [B, Hv * Dv] =
  * gated RMSNorm with norm_weight [Dv] and gate [B, Hv * Dv].  All inputs
- * fp32 (the reference's dtype); out in out_dtype.  Three launches. */
+ * fp32 (the reference's dtype); out in out_dtype.  Two launches (state
+ * rows, then norm + query/key history shift) when key_dim is a multiple of
+ * 4 up to 256 and the state is 16-byte aligned, three otherwise; both give
+ * bit-identical results. */
 int alpx_recurrent_step(const float* current, const float* conv_weight, int64_t weight_tap_stride,
                         int64_t weight_channel_stride, float* conv_history, int conv_kernel,
                         const float* gate, const float* beta_logits, const float* alpha_logits,
