@@ -163,11 +163,12 @@ def sigmoid_gate(values, gate, out_dtype=None):
 
 
 def prefill(q, key, value, *, pos0, scale=None, window=0, kv_start=0, kv_tokens=None,
-            k_pos_stride=None, v_pos_stride=None, out_dtype=None, out=None):
+            k_pos_stride=None, v_pos_stride=None, out_dtype=None, out=None, gate=None):
     """Causal GQA prefill.  ``q [T, Hq, D]`` contiguous; ``key``/``value``
     cache rows ``j < kv_tokens`` of ``kv_heads`` heads, row stride given in
-    elements (default: contiguous ``[T_kv, Hkv, D]``).  Returns
-    ``[T, Hq, Dv]``."""
+    elements (default: contiguous ``[T_kv, Hkv, D]``).  With ``gate``
+    (contiguous ``[T, Hq, Dv]``, q's dtype) the output is multiplied by
+    sigmoid(gate) before it is rounded.  Returns ``[T, Hq, Dv]``."""
     torch = _torch()
     q_tokens, q_heads, key_dim = (int(x) for x in q.shape)
     kv_heads = int(key.shape[-2])
@@ -190,21 +191,23 @@ def prefill(q, key, value, *, pos0, scale=None, window=0, kv_start=0, kv_tokens=
     # only the split-K fallback (fp32, odd shapes) touches the workspace
     fast = (q.dtype != torch.float32 and key_dim == value_dim and key_dim in (64, 128, 256))
     ws = None if fast else _lib.workspace(torch, q.device, nbytes)
-    rc = L.alpx_prefill_causal(
-        q.data_ptr(), key.data_ptr(), value.data_ptr(), out.data_ptr(),
-        None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(),
-        q_tokens, int(kv_tokens), q_heads, kv_heads, key_dim, value_dim, int(k_pos_stride),
-        int(v_pos_stride), int(pos0), int(window), int(kv_start), float(scale),
-        _lib.dtype_code(torch, q.dtype), _lib.dtype_code(torch, out.dtype),
-        _lib.stream_handle(torch, q.device))
+
+    def call(workspace):
+        args = (None if workspace is None else workspace.data_ptr(),
+                0 if workspace is None else workspace.numel(), q_tokens, int(kv_tokens), q_heads,
+                kv_heads, key_dim, value_dim, int(k_pos_stride), int(v_pos_stride), int(pos0),
+                int(window), int(kv_start), float(scale), _lib.dtype_code(torch, q.dtype),
+                _lib.dtype_code(torch, out.dtype), _lib.stream_handle(torch, q.device))
+        if gate is None:
+            return L.alpx_prefill_causal(q.data_ptr(), key.data_ptr(), value.data_ptr(),
+                                         out.data_ptr(), *args)
+        return L.alpx_prefill_causal_gated(q.data_ptr(), key.data_ptr(), value.data_ptr(),
+                                           gate.data_ptr(), out.data_ptr(), *args)
+
+    rc = call(ws)
     if rc == _lib.EINVAL and ws is None:  # unaligned rows fell back: retry with workspace
         ws = _lib.workspace(torch, q.device, nbytes)
-        rc = L.alpx_prefill_causal(
-            q.data_ptr(), key.data_ptr(), value.data_ptr(), out.data_ptr(), ws.data_ptr(),
-            ws.numel(), q_tokens, int(kv_tokens), q_heads, kv_heads, key_dim, value_dim,
-            int(k_pos_stride), int(v_pos_stride), int(pos0), int(window), int(kv_start),
-            float(scale), _lib.dtype_code(torch, q.dtype), _lib.dtype_code(torch, out.dtype),
-            _lib.stream_handle(torch, q.device))
+        rc = call(ws)
     _lib.check(rc)
     return out
 

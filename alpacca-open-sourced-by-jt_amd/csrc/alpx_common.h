@@ -45,6 +45,13 @@ __device__ __forceinline__ float stable_sigmoid(float x) {
   return z / (1.0f + z);
 }
 
+// Logistic function as 1 / (1 + 2^(-x log2 e)) on the hardware exp2 and
+// reciprocal (about 2 ulp): saturates to exactly 0 and 1 without overflow
+// trouble (2^(+large) = inf gives 1 / inf = 0), so it needs no branch.
+__device__ __forceinline__ float fast_sigmoid(float x) {
+  return __builtin_amdgcn_rcpf(1.0f + fast_exp2(-x * kLog2e));
+}
+
 // Vector of 8 16-bit elements of type T, the MFMA k=32 operand of one lane.
 template <typename T> struct Vec8;
 template <> struct Vec8<f16_t> { typedef f16x8 type; };

@@ -38,6 +38,7 @@ struct PrefillArgs {
   const void* q;
   const void* k;
   const void* v;
+  const void* gate;  // null, or [q_tokens, q_heads, D] in T: out *= sigmoid(gate)
   void* out;
   int64_t ks_pos, vs_pos;  // elements between cache rows (head stride = head_dim)
   int64_t pos0;            // absolute position of query token 0
@@ -584,7 +585,22 @@ prefill_mfma(PrefillArgs a) {
     lt += __shfl_xor(lt, 32);
     const float inv = lt > 0.f ? 1.0f / lt : 0.f;
     if (!cok[qb]) continue;
-    TO* op = (TO*)a.out + ((int64_t)tok[qb] * a.q_heads + hq[qb]) * D + 4 * quad;
+    const int64_t ofs = ((int64_t)tok[qb] * a.q_heads + hq[qb]) * D + 4 * quad;
+    TO* op = (TO*)a.out + ofs;
+    if (a.gate != nullptr) {  // the sigmoid output gate, before the single rounding
+      typedef typename Vec4<T>::type V4;
+      const T* gp = (const T*)a.gate + ofs;
+      V4 gv[MB];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) gv[mb] = *(const V4*)(gp + 16 * mb);
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          op[16 * mb + i] = from_f32<TO>(o[qb][mb][i] * inv * fast_sigmoid(to_f32(gv[mb][i])));
+      }
+      continue;
+    }
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
@@ -624,12 +640,13 @@ extern "C" size_t alpx_prefill_workspace_bytes(int q_tokens, int q_heads, int kv
   return decode_workspace(q_tokens, q_heads, kv_heads, value_dim, kv_tokens);
 }
 
-extern "C" int alpx_prefill_causal(const void* q, const void* key, const void* value, void* out,
-                                   void* workspace, size_t workspace_bytes, int q_tokens,
-                                   int kv_tokens, int q_heads, int kv_heads, int key_dim,
-                                   int value_dim, int64_t k_pos_stride, int64_t v_pos_stride,
-                                   int64_t q_pos0, int window, int64_t kv_start, float scale,
-                                   int dtype, int out_dtype, void* stream) {
+namespace {
+
+int prefill_impl(const void* q, const void* key, const void* value, const void* gate, void* out,
+                 void* workspace, size_t workspace_bytes, int q_tokens, int kv_tokens,
+                 int q_heads, int kv_heads, int key_dim, int value_dim, int64_t k_pos_stride,
+                 int64_t v_pos_stride, int64_t q_pos0, int window, int64_t kv_start, float scale,
+                 int dtype, int out_dtype, void* stream) {
   using namespace alpx;
   if (!q || !key || !value || !out) return fail(ALPX_EINVAL, "alpx_prefill_causal: null buffer");
   if (!dtype_ok(dtype) || !dtype_ok(out_dtype))
@@ -651,7 +668,7 @@ extern "C" int alpx_prefill_causal(const void* q, const void* key, const void* v
   hipStream_t s = (hipStream_t)stream;
   const int group = q_heads / kv_heads;
   const size_t es = dtype_size(dtype);
-  const uintptr_t align = (uintptr_t)q | (uintptr_t)key | (uintptr_t)value |
+  const uintptr_t align = (uintptr_t)q | (uintptr_t)key | (uintptr_t)value | (uintptr_t)gate |
                           (uintptr_t)(k_pos_stride * es) | (uintptr_t)(v_pos_stride * es);
   const bool mfma = dtype != ALPX_F32 && key_dim == value_dim &&
                     (key_dim == 64 || key_dim == 128 || key_dim == 256) && (align & 15) == 0 &&
@@ -670,6 +687,7 @@ extern "C" int alpx_prefill_causal(const void* q, const void* key, const void* v
     a.q = q;
     a.k = key;
     a.v = value;
+    a.gate = gate;
     a.out = out;
     a.ks_pos = k_pos_stride;
     a.vs_pos = v_pos_stride;
@@ -701,7 +719,7 @@ extern "C" int alpx_prefill_causal(const void* q, const void* key, const void* v
   a.k = key;
   a.v = value;
   a.seq_lens = nullptr;
-  a.gate = nullptr;
+  a.gate = gate;  // the combine pass applies it ([token][head][d] = [b][h][d])
   a.out = out;
   a.ks_pos = k_pos_stride;
   a.ks_b = 0;
@@ -722,4 +740,30 @@ extern "C" int alpx_prefill_causal(const void* q, const void* key, const void* v
   a.scale_log2 = scale * kLog2e;
   return run_decode(a, dtype, out_dtype, workspace, workspace_bytes, s, ALPX_T_PREFILL,
                     ALPX_T_AUX);
+}
+
+}  // namespace
+
+extern "C" int alpx_prefill_causal(const void* q, const void* key, const void* value, void* out,
+                                   void* workspace, size_t workspace_bytes, int q_tokens,
+                                   int kv_tokens, int q_heads, int kv_heads, int key_dim,
+                                   int value_dim, int64_t k_pos_stride, int64_t v_pos_stride,
+                                   int64_t q_pos0, int window, int64_t kv_start, float scale,
+                                   int dtype, int out_dtype, void* stream) {
+  return prefill_impl(q, key, value, nullptr, out, workspace, workspace_bytes, q_tokens, kv_tokens,
+                      q_heads, kv_heads, key_dim, value_dim, k_pos_stride, v_pos_stride, q_pos0,
+                      window, kv_start, scale, dtype, out_dtype, stream);
+}
+
+extern "C" int alpx_prefill_causal_gated(const void* q, const void* key, const void* value,
+                                         const void* gate, void* out, void* workspace,
+                                         size_t workspace_bytes, int q_tokens, int kv_tokens,
+                                         int q_heads, int kv_heads, int key_dim, int value_dim,
+                                         int64_t k_pos_stride, int64_t v_pos_stride,
+                                         int64_t q_pos0, int window, int64_t kv_start,
+                                         float scale, int dtype, int out_dtype, void* stream) {
+  if (!gate) return alpx::fail(ALPX_EINVAL, "alpx_prefill_causal_gated: null gate");
+  return prefill_impl(q, key, value, gate, out, workspace, workspace_bytes, q_tokens, kv_tokens,
+                      q_heads, kv_heads, key_dim, value_dim, k_pos_stride, v_pos_stride, q_pos0,
+                      window, kv_start, scale, dtype, out_dtype, stream);
 }

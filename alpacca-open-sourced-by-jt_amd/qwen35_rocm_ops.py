@@ -390,12 +390,15 @@ class Qwen35RocmOps:
 
     def attention_prefill(self, query: Any, key_cache: Any, value_cache: Any, *,
                           position: int, batch_index: int = 0, scale: float | None = None,
-                          window: int = 0, out_dtype: Any = None) -> Any:
+                          window: int = 0, out_dtype: Any = None, gate: Any = None) -> Any:
         """Causal prefill over the ROCm cache layout (extension): query
         ``[T, Hq, D]`` of sequence ``batch_index`` at positions
         ``position .. position + T - 1`` attends to its cache rows
         ``0 .. position + t`` (``qwen35_full_attention_prefill`` semantics,
-        qwen35_kernels.py:395-411, with prefix_length = position)."""
+        qwen35_kernels.py:395-411, with prefix_length = position).  With
+        ``gate [T, Hq, Dv]`` the output is ``attention * sigmoid(gate)``
+        (the gate placement of qwen35_runtime.py:653-660), formed before
+        the output is rounded."""
         query = self._tensor(query, "prefill query", dimensions=3)
         key_cache = self._tensor(key_cache, "attention key cache", dimensions=4)
         value_cache = self._tensor(value_cache, "attention value cache", dimensions=4)
@@ -416,6 +419,11 @@ class Qwen35RocmOps:
         if query_heads % kv_heads:
             raise ValueError("attention query heads must be a multiple of KV heads")
         self._same_dtype("prefill", query, key_cache, value_cache)
+        if gate is not None:
+            gate = self._tensor(gate, "attention output gate", dimensions=3)
+            if _shape(gate) != (tokens, query_heads, value_shape[3]):
+                raise ValueError("sigmoid gate must match values")
+            self._same_dtype("prefill gate", query, gate)
         scale_value = (1.0 / math.sqrt(key_width) if scale is None
                        else _positive_finite("attention scale", scale))
         return _ops.prefill(query, key_cache[0, batch_index], value_cache[0, batch_index],
@@ -423,7 +431,7 @@ class Qwen35RocmOps:
                             kv_tokens=position + tokens,
                             k_pos_stride=batch * kv_heads * key_width,
                             v_pos_stride=batch * kv_heads * value_shape[3],
-                            out_dtype=out_dtype)
+                            out_dtype=out_dtype, gate=gate)
 
     def append_prefill_attention_(self, query: Any, key: Any, value: Any, key_cache: Any,
                                   value_cache: Any, *, position: int,
@@ -821,8 +829,8 @@ class Qwen35RocmOps:
         of ``query_gate [T, Hq * 2 D]``, ``key [T, Hkv * D]`` and
         ``value [T, Hkv * Dv]`` of cache sequence ``batch_index`` at
         positions ``position .. position + T - 1`` as one fused prologue
-        (split, Q/K RMSNorm, IMROPE, cache append), one causal prefill
-        attention over the cache and one sigmoid gate.  Returns
+        (split, Q/K RMSNorm, IMROPE, cache append) and one causal prefill
+        attention over the cache with the sigmoid gate in its epilogue.  Returns
         ``(gated output [T, Hq, Dv], position + T)``."""
         key_cache = self._tensor(key_cache, "attention key cache", dimensions=4)
         value_cache = self._tensor(value_cache, "attention value cache", dimensions=4)
@@ -863,9 +871,9 @@ class Qwen35RocmOps:
             key_norm, key_cache, value_cache, batch_index=batch_index, position=position,
             sections=section, frequency_base=_positive_finite("frequency_base", frequency_base),
             eps=_positive_finite("epsilon", epsilon))
-        attended = self.attention_prefill(query, key_cache, value_cache, position=position,
-                                          batch_index=batch_index, scale=scale)
-        return _ops.sigmoid_gate(attended, gate), position + tokens
+        gated = self.attention_prefill(query, key_cache, value_cache, position=position,
+                                       batch_index=batch_index, scale=scale, gate=gate)
+        return gated, position + tokens
 
     def recurrent_layer_prefill_(self, workspace: RocmRecurrentWorkspace, mixed: Any,
                                  convolution_weights: Any, gate: Any, beta_logits: Any,

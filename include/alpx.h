@@ -200,6 +200,21 @@ int alpx_prefill_causal(const void* q, const void* key, const void* value, void*
                         int64_t kv_start, float scale, int dtype, int out_dtype, void* stream);
 
 /*
+ * alpx_prefill_causal with the Qwen3.5 sigmoid output gate applied before
+ * the output is rounded: out = attention * sigmoid(gate), gate
+ * [q_tokens, q_heads, value_dim] in `dtype`.  Replaces the pair
+ * causal prefill + Qwen35RocmOps.sigmoid_gate (qwen35_rocm_ops.py:286-290;
+ * gate placement qwen35_runtime.py:653-660) in a prefill chunk of the
+ * full-attention layer.  The stable sigmoid is tensor.py:123-129's.
+ */
+int alpx_prefill_causal_gated(const void* q, const void* key, const void* value, const void* gate,
+                              void* out, void* workspace, size_t workspace_bytes, int q_tokens,
+                              int kv_tokens, int q_heads, int kv_heads, int key_dim,
+                              int value_dim, int64_t k_pos_stride, int64_t v_pos_stride,
+                              int64_t q_pos0, int window, int64_t kv_start, float scale, int dtype,
+                              int out_dtype, void* stream);
+
+/*
  * Gated delta-rule (GDN) decode step, in place on the state.
  * Replaces Qwen35RocmOps.gated_delta_net_step_ (qwen35_rocm_ops.py:362-407),
  * qwen35_kernels.qwen35_gdn_step (qwen35_kernels.py:310-332) and

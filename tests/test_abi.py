@@ -44,6 +44,14 @@ def test_null_buffers_rejected_without_gpu(pkg):
         pkg._lib.check(rc)
 
 
+def test_gated_prefill_rejects_null_gate_without_gpu(pkg):
+    lib = pkg._lib.lib()
+    fake = ctypes.c_void_p(256)  # never dereferenced: validation fails first
+    rc = lib.alpx_prefill_causal_gated(fake, fake, fake, None, fake, None, 0, 4, 8, 4, 2, 64, 64,
+                                       128, 128, 4, 0, 0, 0.125, 2, 2, None)
+    assert rc == pkg._lib.EINVAL and "null gate" in pkg._lib.last_error()
+
+
 def test_range_and_shape_errors_without_gpu(pkg):
     lib = pkg._lib.lib()
     fake = ctypes.c_void_p(256)  # never dereferenced: validation fails first

@@ -101,6 +101,37 @@ def test_prefill_window_and_kv_start(gpu, dtype):
     assert err <= TOL[dtype], err
 
 
+@pytest.mark.parametrize("dtype,d", [("bf16", 128), ("f16", 256), ("bf16", 64), ("f32", 128)])
+def test_prefill_gated_is_gate_times_prefill(gpu, dtype, d):
+    """The gated prefill (sigmoid gate in the MFMA epilogue, or in the
+    combine pass of the fp32 fallback) equals the ungated prefill times
+    sigmoid(gate) with the product taken in fp32 before rounding; and it
+    matches the oracle's attention * sigmoid(gate) (tensor.py:123-129)."""
+    import torch
+    rng = np.random.default_rng(d + len(dtype))
+    tq, prefix, hq, hkv = 70, 90, 8, 2
+    total = prefix + tq
+    q = I.round_to(rng.standard_normal((tq, hq, d)), dtype)
+    K = I.round_to(rng.standard_normal((total, hkv, d)), dtype)
+    V = I.round_to(rng.standard_normal((total, hkv, d)), dtype)
+    g = I.round_to(rng.standard_normal((tq, hq, d)) * 3, dtype)
+    ops_mod = _mod("_ops")
+    args = (_dev(torch, q, dtype, gpu), _dev(torch, K, dtype, gpu), _dev(torch, V, dtype, gpu))
+    plain = ops_mod.prefill(*args, pos0=prefix, out_dtype=torch.float32)
+    gated = ops_mod.prefill(*args, pos0=prefix, out_dtype=torch.float32,
+                            gate=_dev(torch, g, dtype, gpu))
+    gt = torch.from_numpy(g.astype(np.float32)).to(gpu)
+    expect = plain * torch.sigmoid(gt)
+    assert torch.allclose(gated, expect, rtol=1e-5, atol=1e-6)
+    ref = A.full_attention_prefill(q, K, V, prefix_length=prefix) * (1.0 / (1.0 + np.exp(-g)))
+    assert np.abs(gated.cpu().numpy() - ref).max() <= TOL[dtype]
+    # bf16 / fp16 output: one rounding of the gated value
+    if dtype != "f32":
+        gated_t = ops_mod.prefill(*args, pos0=prefix, gate=_dev(torch, g, dtype, gpu))
+        assert gated_t.dtype == _tdtype(torch, dtype)
+        assert np.abs(gated_t.float().cpu().numpy() - ref).max() <= TOL[dtype]
+
+
 def test_prefill_rows_without_keys_are_zero(gpu):
     import torch
     rng = np.random.default_rng(6)
