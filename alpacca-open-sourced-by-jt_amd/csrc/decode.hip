@@ -9,14 +9,15 @@
 // the occupancy API so that all blocks are resident in a single round.
 //
 //  * fp16/bf16, head_dim 64/128/256 (decode_split_mfma): 4 wavefronts per
-//    block, 32 rows per wave step.  K rows are loaded with 128-bit loads
-//    straight into the A operand of v_mfma_f32_16x16x32_{f16,bf16}
-//    (S^T = K Q^T: 16 rows x 16 query heads per instruction), so scores need
-//    no cross-lane dot-product reduction.  V rows are loaded with 128-bit
-//    loads, staged in a per-wave LDS tile and read back with transposing LDS
-//    reads as the A operand of O^T = V^T P^T, so the probabilities never
-//    leave the registers the score MFMA wrote them to.  The softmax max is a
-//    2-step cross-lane (xor 16, xor 32) reduction.
+//    block, 32 rows per wave step.  K and V rows are fetched row-major with
+//    128-bit buffer loads (whole lines per load) and staged in a per-wave
+//    LDS tile.  K is read back as the A operand of
+//    v_mfma_f32_16x16x32_{f16,bf16} (S^T = K Q^T: 16 rows x 16 query heads
+//    per instruction), so scores need no cross-lane dot-product reduction;
+//    V is read back with transposing LDS reads as the A operand of
+//    O^T = V^T P^T, so the probabilities never leave the registers the
+//    score MFMA wrote them to.  The softmax max is a 2-step cross-lane
+//    (xor 16, xor 32) reduction.
 //  * everything else (fp32, odd head dims, unaligned caches):
 //    decode_split_generic, one wavefront per block, VALU dot products.
 //
