@@ -379,6 +379,38 @@ def attention_prologue(query_gate, key, value, q_norm, k_norm, key_cache, value_
     return query, gate
 
 
+def attention_layer_step(query_gate, key, value, q_norm, k_norm, key_cache, value_cache, *,
+                         position, sections, frequency_base, eps, scale=None, out_dtype=None):
+    """One decode token of the Qwen3.5 attention layer in two launches: the
+    prologue (Q/K RMSNorm + IMROPE, cache append at ``position``) inside the
+    split-K decode launch, then the combine with the sigmoid gate taken from
+    the second half of ``query_gate [B, Hq, 2D]``.  ``key`` / ``value``
+    ``[B, Hkv, D]``; caches ``[C, B, Hkv, D]`` (fp16 / bf16, D in 64, 128,
+    256).  Returns the gated output ``[B, Hq, D]`` over ``position + 1``
+    cache rows."""
+    torch = _torch()
+    capacity, bsz, kv_heads, dim = (int(x) for x in key_cache.shape)
+    q_heads = int(query_gate.shape[1])
+    if scale is None:
+        scale = 1.0 / math.sqrt(dim)
+    out_dtype = key_cache.dtype if out_dtype is None else out_dtype
+    out = torch.empty((bsz, q_heads, dim), dtype=out_dtype, device=key_cache.device)
+    L = _lib.lib()
+    nbytes = L.alpx_decode_workspace_bytes(bsz, q_heads, kv_heads, dim, int(position) + 1)
+    if nbytes == 0:
+        raise ValueError("invalid attention step sizes")
+    ws = _lib.workspace(torch, key_cache.device, nbytes)
+    rc = L.alpx_attention_layer_step(
+        query_gate.data_ptr(), key.data_ptr(), value.data_ptr(), q_norm.data_ptr(),
+        k_norm.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(), out.data_ptr(),
+        ws.data_ptr(), ws.numel(), _lib.dtype_code(torch, key_cache.dtype),
+        _lib.dtype_code(torch, out.dtype), capacity, bsz, q_heads, kv_heads, dim, int(position),
+        _sections(sections), float(frequency_base), float(eps), float(scale),
+        _lib.stream_handle(torch, key_cache.device))
+    _lib.check(rc)
+    return out
+
+
 def attention_prologue_chunk(query_gate, key, value, q_norm, k_norm, key_cache, value_cache, *,
                              batch_index, position, sections, frequency_base, eps):
     """Attention prologue for ``T`` consecutive tokens of cache sequence

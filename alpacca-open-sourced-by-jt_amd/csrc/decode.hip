@@ -31,6 +31,7 @@
 
 #include "alpx_common.h"
 #include "decode_internal.h"
+#include "rope_internal.h"
 #include "timing.h"
 
 namespace alpx {
@@ -167,9 +168,16 @@ constexpr int merge_lds_bytes() {
 // The next tile's loads are issued as soon as the current tile is staged,
 // so every wave keeps a tile in flight.  At the end the four waves' online
 // softmax states are merged through LDS into one partial per block.
-template <typename T, int D, bool PAGED>
-__global__ void __launch_bounds__(256)
-decode_split_mfma(DecodeArgs a) {
+//
+// PRO: the Qwen3.5 attention prologue runs in the same launch.  Every block
+// forms its query heads from the joint projection (RMSNorm x weight, IMROPE
+// at the new token's position, by norm_rope as in the prologue kernel) into
+// LDS.  The blocks whose chunk holds the new row form that key row the same
+// way and put it and the value row into their staged tile in LDS, over
+// whatever their own loads fetched of that row; the one with head chunk 0
+// also writes both rows to the cache.
+template <typename T, int D, bool PAGED, bool PRO>
+__device__ __forceinline__ void split_body(const DecodeArgs& a, const SplitPrologue* pp) {
   typedef typename Vec8<T>::type V8;
   typedef typename Vec4<T>::type V4;
   constexpr int kStride = D + 8;          // LDS row stride (elements), 16-byte aligned rows
@@ -178,7 +186,10 @@ decode_split_mfma(DecodeArgs a) {
   constexpr int kTileElems = kTile * kStride;
   constexpr int kTileBytes = 2 * kWaves * kTileElems * (int)sizeof(T);
   constexpr int kLdsBytes = kTileBytes > merge_lds_bytes<D>() ? kTileBytes : merge_lds_bytes<D>();
-  __shared__ __attribute__((aligned(16))) char smem[kLdsBytes];
+  // PRO: 16 query rows and the new key and value rows (T), then one float
+  // row per wave for the rotation partners.
+  constexpr int kProBytes = PRO ? (16 + 2) * D * (int)sizeof(T) + kWaves * D * 4 : 0;
+  __shared__ __attribute__((aligned(16))) char smem[kLdsBytes + kProBytes];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -196,7 +207,63 @@ decode_split_mfma(DecodeArgs a) {
 
   // B operand of S^T = K Q^T: lane holds Q[h][32 ks + 8 quad + 0..7].
   V8 qv[D / 32];
-  {
+  [[maybe_unused]] bool owns_new = false;  // PRO: the new row is in this block's chunk
+  [[maybe_unused]] const T* new_kv = nullptr;  // PRO: new key row, then value row (LDS)
+  if constexpr (PRO) {
+    constexpr int kPer = D / 64;
+    T* qrows = (T*)(smem + kLdsBytes);
+    T* nkv = qrows + 16 * D;
+    float* stage = (float*)(nkv + 2 * D) + wave * D;
+    const int64_t pos = pp->position;
+    owns_new = pos >= start && pos < end;
+    new_kv = nkv;
+    if (owns_new && wave < 2) {
+      const int64_t src_row = ((int64_t)b * a.kv_heads + kvh) * D;  // [B, Hkv, D]
+      if (wave == 0) {
+        const T* src = (const T*)pp->key + src_row;
+        float x[kPer], wt[kPer];
+#pragma unroll
+        for (int e = 0; e < kPer; ++e) {
+          x[e] = to_f32(src[lane + 64 * e]);
+          wt[e] = pp->kw[lane + 64 * e];
+        }
+        norm_rope<T, kPer>(x, wt, D, pp->eps, pp->sec, pp->R, pp->inv, (double)pos, stage, nkv,
+                           lane);
+      } else {
+        const T* src = (const T*)pp->value + src_row;
+#pragma unroll
+        for (int e = 0; e < kPer; ++e) nkv[D + lane + 64 * e] = src[lane + 64 * e];
+      }
+      if (hc == 0) {
+        // this wave's own LDS stores above are done before these reads
+        __builtin_amdgcn_wave_barrier();
+        T* dst = wave == 0 ? (T*)a.k + pos * a.ks_pos + (int64_t)b * a.ks_b + (int64_t)kvh * a.ks_h
+                           : (T*)a.v + pos * a.vs_pos + (int64_t)b * a.vs_b + (int64_t)kvh * a.vs_h;
+#pragma unroll
+        for (int e = 0; e < kPer; ++e) dst[lane + 64 * e] = nkv[wave * D + lane + 64 * e];
+      }
+    }
+    // query heads hc * 16 + j of this kv group, one wave per head
+    for (int j = wave; j < 16; j += kWaves) {
+      const int g = hc * 16 + j;
+      if (g >= a.group) break;
+      const T* src = (const T*)pp->qg + ((int64_t)b * a.q_heads + kvh * a.group + g) * (2 * D);
+      float x[kPer], wt[kPer];
+#pragma unroll
+      for (int e = 0; e < kPer; ++e) {
+        x[e] = to_f32(src[lane + 64 * e]);
+        wt[e] = pp->qw[lane + 64 * e];
+      }
+      norm_rope<T, kPer>(x, wt, D, pp->eps, pp->sec, pp->R, pp->inv, (double)pos, stage,
+                         qrows + j * D, lane);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < D / 32; ++ks) {
+      const V8 x = *(const V8*)(qrows + hl * D + 32 * ks + 8 * quad);
+      qv[ks] = head_ok ? x : (V8){};
+    }
+  } else {
     const T* qp = (const T*)a.q + ((int64_t)b * a.q_heads + h) * D + 8 * quad;
 #pragma unroll
     for (int ks = 0; ks < D / 32; ++ks) {
@@ -261,6 +328,15 @@ decode_split_mfma(DecodeArgs a) {
       *(V8*)(ldsk + r * kStride + 8 * c) = kr[it];
       *(V8*)(ldsv + r * kStride + 8 * c) = vr[it];
     }
+    if constexpr (PRO) {
+      const int64_t r = pp->position - p0;
+      if (owns_new && r >= 0 && r < kTile) {
+        for (int i = lane; i < D; i += 64) {
+          ldsk[r * kStride + i] = new_kv[i];
+          ldsv[r * kStride + i] = new_kv[D + i];
+        }
+      }
+    }
     if (pn < end) load_tile(pn);
     wave_sync_lds();
     // Scores for 32 rows x 16 heads: lane holds S[pos = p0 + 16 blk + 4 quad + i][hl].
@@ -323,6 +399,18 @@ decode_split_mfma(DecodeArgs a) {
   }
 
   merge_waves<D>(a, smem, o, m, l, wave, lane, head_ok, b, h);
+}
+
+template <typename T, int D, bool PAGED>
+__global__ void __launch_bounds__(256)
+decode_split_mfma(DecodeArgs a) {
+  split_body<T, D, PAGED, false>(a, nullptr);
+}
+
+template <typename T, int D>
+__global__ void __launch_bounds__(256)
+decode_split_mfma_pro(DecodeArgs a, SplitPrologue pp) {
+  split_body<T, D, false, true>(a, &pp);
 }
 
 // fp32 caches: the same split structure on v_mfma_f32_16x16x4_f32 (fp32
@@ -643,7 +731,7 @@ decode_combine(DecodeArgs a) {
     }
   }
   float r = L > 0.f ? A / L : 0.f;
-  if (a.gate != nullptr) r *= stable_sigmoid(to_f32(((const T*)a.gate)[bh * DV + d]));
+  if (a.gate != nullptr) r *= stable_sigmoid(to_f32(((const T*)a.gate)[bh * a.gate_stride + d]));
   ((TO*)a.out)[bh * DV + d] = from_f32<TO>(r);
 }
 
@@ -696,6 +784,18 @@ size_t workspace_for(int batch, int q_heads, int value_dim, int nsplit) {
 }
 
 template <typename T>
+const void* split_kernel_pro(int D) {
+  if constexpr (sizeof(T) == 2) {
+    switch (D) {
+      case 64: return (const void*)decode_split_mfma_pro<T, 64>;
+      case 128: return (const void*)decode_split_mfma_pro<T, 128>;
+      case 256: return (const void*)decode_split_mfma_pro<T, 256>;
+    }
+  }
+  return nullptr;
+}
+
+template <typename T>
 const void* split_kernel(bool mfma, bool paged, int D) {
   if (mfma) {
     if constexpr (sizeof(T) == 2) {
@@ -739,9 +839,9 @@ int launch_combine(int out_dtype, const DecodeArgs& a, hipStream_t s) {
   return check_launch("decode_combine");
 }
 
-template <typename T>
-int launch_split(const void* kernel, bool mfma, const DecodeArgs& a, dim3 grid, hipStream_t s) {
-  void* args[] = {(void*)&a};
+int launch_split(const void* kernel, bool mfma, const DecodeArgs& a, const SplitPrologue* pro,
+                 dim3 grid, hipStream_t s) {
+  void* args[] = {(void*)&a, (void*)pro};
   hipError_t err = hipLaunchKernel(kernel, grid, dim3(mfma ? 256 : 64), args, 0, s);
   if (err != hipSuccess)
     return fail(ALPX_EHIP, "decode split launch failed: %s", hipGetErrorString(err));
@@ -769,7 +869,7 @@ size_t decode_workspace(int batch, int q_heads, int kv_heads, int value_dim, int
 }
 
 int run_decode(DecodeArgs a, int dtype, int out_dtype, void* workspace, size_t workspace_bytes,
-               hipStream_t s, int split_timer, int combine_timer) {
+               hipStream_t s, int split_timer, int combine_timer, const SplitPrologue* pro) {
   const size_t es = dtype_size(dtype);
   const uintptr_t align = (uintptr_t)a.q | (uintptr_t)a.k | (uintptr_t)a.v |
                           (uintptr_t)(a.ks_pos * es) | (uintptr_t)(a.ks_b * es) |
@@ -788,12 +888,25 @@ int run_decode(DecodeArgs a, int dtype, int out_dtype, void* workspace, size_t w
                 need);
   const void* kernel = nullptr;
   const bool paged = a.pages != nullptr;
-  switch (dtype) {
-    case ALPX_F32: kernel = split_kernel<float>(mfma, paged, D); break;
-    case ALPX_F16: kernel = split_kernel<f16_t>(mfma, paged, D); break;
-    default: kernel = split_kernel<bf16_t>(mfma, paged, D); break;
+  if (pro != nullptr) {
+    // fused prologue: 16-bit MFMA split over a contiguous cache only
+    if (mfma && !paged && a.seq_lens == nullptr && a.causal_pos0 < 0) {
+      if (dtype == ALPX_F16) kernel = split_kernel_pro<f16_t>(D);
+      if (dtype == ALPX_BF16) kernel = split_kernel_pro<bf16_t>(D);
+    }
+    if (kernel == nullptr)
+      return fail(ALPX_EUNSUPPORTED,
+                  "fused attention step: needs fp16/bf16 caches, key_dim == value_dim in "
+                  "{64, 128, 256} and 16-byte aligned rows");
+  } else {
+    switch (dtype) {
+      case ALPX_F32: kernel = split_kernel<float>(mfma, paged, D); break;
+      case ALPX_F16: kernel = split_kernel<f16_t>(mfma, paged, D); break;
+      default: kernel = split_kernel<bf16_t>(mfma, paged, D); break;
+    }
   }
   if (kernel == nullptr) return fail(ALPX_EUNSUPPORTED, "decode: no kernel for this shape");
+  if (a.gate_stride == 0) a.gate_stride = a.value_dim;
   const int unit =
       !mfma ? kGenericTile : (dtype == ALPX_F32 ? f32_tile_rows(D) : kTile) * kWaves;
   a.head_chunks = (a.group + 15) / 16;
@@ -810,7 +923,7 @@ int run_decode(DecodeArgs a, int dtype, int out_dtype, void* workspace, size_t w
   int rc;
   {
     TimedRegion timed(split_timer, s);
-    rc = launch_split<float>(kernel, mfma, a, grid, s);
+    rc = launch_split(kernel, mfma, a, pro, grid, s);
   }
   if (rc != ALPX_OK) return rc;
   TimedRegion timed(combine_timer, s);

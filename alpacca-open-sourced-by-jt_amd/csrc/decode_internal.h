@@ -4,6 +4,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "rope_internal.h"
+
 namespace alpx {
 
 struct DecodeArgs {
@@ -35,6 +37,22 @@ struct DecodeArgs {
   int max_pages;
   int num_pages;
   int64_t ks_page, vs_page;
+  int64_t gate_stride;  // elements between the gate rows of (b, h); 0 = value_dim
+};
+
+// The Qwen3.5 attention prologue fused into the split launch: one new token
+// per sequence, every sequence at cache row `position`.
+struct SplitPrologue {
+  const void* qg;      // [B, Hq, 2 D]: per head D query then D gate values
+  const void* key;     // [B, Hkv, D] new key rows, before norm and rotation
+  const void* value;   // [B, Hkv, D] new value rows
+  const float* qw;     // [D] query RMSNorm weight
+  const float* kw;     // [D] key RMSNorm weight
+  int64_t position;
+  int R;               // rotary pairs
+  int sec[4];
+  float eps;
+  double inv[kMaxPairs];  // base^(-2 p / (2 R)) per pair p
 };
 
 // Bytes of split partials for `batch` rows of `q_heads` heads over `length`
@@ -45,6 +63,7 @@ size_t decode_workspace(int batch, int q_heads, int kv_heads, int value_dim, int
 // strides, sizes, causal fields, scale_log2); fills the partial pointers,
 // nsplit and chunk.  Validation is the caller's job.
 int run_decode(DecodeArgs a, int dtype, int out_dtype, void* workspace, size_t workspace_bytes,
-               hipStream_t stream, int split_timer, int combine_timer);
+               hipStream_t stream, int split_timer, int combine_timer,
+               const SplitPrologue* pro = nullptr);
 
 }  // namespace alpx

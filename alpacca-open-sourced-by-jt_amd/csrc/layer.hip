@@ -15,7 +15,9 @@
 #include <math.h>
 
 #include "alpx_common.h"
+#include "decode_internal.h"
 #include "gdn_internal.h"
+#include "rope_internal.h"
 #include "timing.h"
 
 namespace alpx {
@@ -39,28 +41,7 @@ __device__ __forceinline__ float softplus_f(float x) {
   return x > 0.f ? x + log1pf(expf(-x)) : log1pf(expf(x));
 }
 
-// IMROPE position lane of rotary pair p (interleaved T/H/W/E schedule).
-__device__ __forceinline__ int imrope_lane(int p, const int (&sec)[4], int R) {
-  const int sector = p % R;
-  if (sector % 3 == 1 && sector < 3 * sec[1]) return 1;
-  if (sector % 3 == 2 && sector < 3 * sec[2]) return 2;
-  if (sector % 3 == 0 && sector < 3 * sec[0]) return 0;
-  return 3;
-}
-
-constexpr int kMaxPairs = kMaxDim / 2;
-
-// cos / sin of the angle pos * inv (inv = scale * base^(-2 p / (2 R)),
-// formed on the host in double precision).  The angle reaches 10^4-10^6 rad
-// at long contexts, where a float angle alone would be off by ~10^-3 rad,
-// so it is reduced modulo 2 pi in double precision first; sin / cos of the
-// reduced angle (|r| <= pi) are then taken in float.
-__device__ __forceinline__ void rope_cs(double pos, double inv, float& c, float& s) {
-  constexpr double kTwoPi = 6.283185307179586476925;
-  const double theta = pos * inv;
-  const double r = theta - kTwoPi * rint(theta * (1.0 / kTwoPi));
-  sincosf((float)r, &s, &c);
-}
+static_assert(kMaxDim == kRopeMaxDim, "prologue rows and rope rows share one width");
 
 // ---------------------------------------------------------------- row norm
 
@@ -288,21 +269,6 @@ __global__ void __launch_bounds__(256) attn_prologue_kernel(ProArgs a) {
       if (is_q) gv[e] = src[a.D + i];
     }
   }
-  float ss = 0.f;
-#pragma unroll
-  for (int e = 0; e < kPer; ++e)
-    if (lane + 64 * e < a.D) ss = fmaf(x[e], x[e], ss);
-  ss = wave_sum(ss);
-  const float den = sqrtf(ss / (float)a.D + a.eps);
-  float* st = stage[wave];
-#pragma unroll
-  for (int e = 0; e < kPer; ++e) {
-    const int i = lane + 64 * e;
-    if (i < a.D) {
-      x[e] = x[e] / den * wt[e];
-      st[i] = x[e];
-    }
-  }
   T* dst;
   if (is_q) {
     dst = (T*)a.q_out + ((int64_t)b * a.Hq + h) * a.D;
@@ -314,24 +280,8 @@ __global__ void __launch_bounds__(256) attn_prologue_kernel(ProArgs a) {
     if (!in_cache) return;
     dst = (T*)a.kc + (crow * a.Hkv + h) * a.D;
   }
-  // LDS traffic of one wave is processed in issue order, so the partner
-  // reads below see this wave's stores.
-  __builtin_amdgcn_wave_barrier();
-  const double p = (double)pos;  // text position lanes (p, p, p, 0)
-#pragma unroll
-  for (int e = 0; e < kPer; ++e) {
-    const int i = lane + 64 * e;
-    if (i >= a.D) continue;
-    float y = x[e];
-    if (i < 2 * a.R) {
-      const int pr = i < a.R ? i : i - a.R;
-      const int ln = imrope_lane(pr, a.sec, a.R);
-      float c, sn;
-      rope_cs(ln == 3 ? 0.0 : p, a.inv[pr], c, sn);
-      y = i < a.R ? x[e] * c - st[i + a.R] * sn : st[pr] * sn + x[e] * c;
-    }
-    dst[i] = from_f32<T>(y);
-  }
+  // text position lanes (p, p, p, 0)
+  norm_rope<T, kPer>(x, wt, a.D, a.eps, a.sec, a.R, a.inv, (double)pos, stage[wave], dst, lane);
 }
 
 // --------------------------------------- recurrent-layer prep (fused)
@@ -884,7 +834,8 @@ __global__ void __launch_bounds__(256) conv_history_advance(float* hist, const f
   }
 }
 
-// scale * base^(-2 p / (2 R)) for p < R, in double precision.
+}  // namespace
+
 void inverse_frequencies(double* inv, int R, double base, double scale) {
   for (int p = 0; p < R; ++p) inv[p] = scale * pow(base, -2.0 * (double)p / (double)(2 * R));
 }
@@ -899,7 +850,6 @@ bool bad_sections(const int* sections, int& R) {
   return R <= 0;
 }
 
-}  // namespace
 }  // namespace alpx
 
 // ------------------------------------------------------------- C-ABI
@@ -1121,6 +1071,72 @@ extern "C" int alpx_attention_prologue_chunk(const void* query_gate, const void*
                                    dtype, capacity, tokens, cache_batch, batch_index, 1, q_heads,
                                    kv_heads, head_dim, value_dim, position, nullptr, sections,
                                    frequency_base, eps, stream);
+}
+
+extern "C" int alpx_attention_layer_step(const void* query_gate, const void* key,
+                                         const void* value, const float* q_norm,
+                                         const float* k_norm, void* key_cache, void* value_cache,
+                                         void* out, void* workspace, size_t workspace_bytes,
+                                         int dtype, int out_dtype, int64_t capacity, int batch,
+                                         int q_heads, int kv_heads, int head_dim,
+                                         int64_t position, const int* sections,
+                                         double frequency_base, float eps, float scale,
+                                         void* stream) {
+  using namespace alpx;
+  if (!query_gate || !key || !value || !q_norm || !k_norm || !key_cache || !value_cache ||
+      !out || !workspace)
+    return fail(ALPX_EINVAL, "alpx_attention_layer_step: null buffer");
+  if (!dtype_ok(dtype) || !dtype_ok(out_dtype))
+    return fail(ALPX_EINVAL, "alpx_attention_layer_step: unknown dtype");
+  if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || head_dim <= 0 || capacity <= 0)
+    return fail(ALPX_EINVAL, "alpx_attention_layer_step: sizes must be positive");
+  if (q_heads % kv_heads != 0)
+    return fail(ALPX_EINVAL, "attention query heads must be a multiple of KV heads");
+  if (position < 0 || position >= capacity)
+    return fail(ALPX_ERANGE, "attention cache position exceeds capacity");
+  if (position + 1 > INT32_MAX)
+    return fail(ALPX_EUNSUPPORTED, "alpx_attention_layer_step: cache length above 2^31 - 1");
+  if (!(scale > 0.0f) || !isfinite(scale))
+    return fail(ALPX_EINVAL, "attention scale must be positive and finite");
+  int R = 0;
+  if (bad_sections(sections, R)) return fail(ALPX_EINVAL, "IMRoPE requires at least one rotary pair");
+  if (head_dim < 2 * R) return fail(ALPX_EINVAL, "IMRoPE input is shorter than twice the section sum");
+  if (!(frequency_base > 0.0) || !isfinite(frequency_base))
+    return fail(ALPX_EINVAL, "frequency_base must be positive and finite");
+  if (!(eps > 0.f) || !isfinite(eps)) return fail(ALPX_EINVAL, "epsilon must be positive and finite");
+  SplitPrologue pp = {};
+  pp.qg = query_gate;
+  pp.key = key;
+  pp.value = value;
+  pp.qw = q_norm;
+  pp.kw = k_norm;
+  pp.position = position;
+  pp.R = R;
+  for (int i = 0; i < 4; ++i) pp.sec[i] = sections[i];
+  pp.eps = eps;
+  inverse_frequencies(pp.inv, R, frequency_base, 1.0);
+  const int64_t D = head_dim;
+  DecodeArgs a = {};
+  a.q = query_gate;  // not read by the fused split; its alignment is checked with the rest
+  a.k = key_cache;
+  a.v = value_cache;
+  a.gate = (const char*)query_gate + D * dtype_size(dtype);
+  a.gate_stride = 2 * D;
+  a.out = out;
+  a.ks_pos = a.vs_pos = (int64_t)batch * kv_heads * D;
+  a.ks_b = a.vs_b = (int64_t)kv_heads * D;
+  a.ks_h = a.vs_h = D;
+  a.causal_pos0 = -1;
+  a.length = (int)(position + 1);
+  a.batch = batch;
+  a.q_heads = q_heads;
+  a.kv_heads = kv_heads;
+  a.group = q_heads / kv_heads;
+  a.key_dim = head_dim;
+  a.value_dim = head_dim;
+  a.scale_log2 = scale * kLog2e;
+  return run_decode(a, dtype, out_dtype, workspace, workspace_bytes, (hipStream_t)stream,
+                    ALPX_T_DECODE, ALPX_T_DECODE_COMBINE, &pp);
 }
 
 extern "C" size_t alpx_recurrent_step_workspace_bytes(int batch, int key_heads, int value_heads,

@@ -670,6 +670,68 @@ class Qwen35RocmOps:
             eps=_positive_finite("epsilon", epsilon))
         return query, gate, position + 1
 
+    def attention_layer_step_(self, query_gate: Any, key: Any, value: Any, query_norm: Any,
+                              key_norm: Any, key_cache: Any, value_cache: Any, *, position: int,
+                              sections: Sequence[int], frequency_base: float, epsilon: float,
+                              scale: float | None = None,
+                              out_dtype: Any = None) -> tuple[Any, int]:
+        """One decode token of the Qwen3.5 full-attention layer after its
+        projections (extension; qwen35_runtime.py:597-665 for one token per
+        sequence): the prologue of ``attention_prologue_`` and the gated
+        ``online_attention`` over ``position + 1`` cache rows.  fp16 / bf16
+        caches with equal key and value widths of 64, 128 or 256 run it as
+        two launches (prologue fused into the split-K launch, gate in the
+        combine); other shapes run the prologue and the gated decode as
+        separate launches.  Returns ``(gated output [B, Hq, Dv],
+        position + 1)``."""
+        key_cache = self._tensor(key_cache, "attention key cache", dimensions=4)
+        value_cache = self._tensor(value_cache, "attention value cache", dimensions=4)
+        width = int(key_cache.shape[3])
+        value_width = int(value_cache.shape[3])
+        fused = (key_cache.dtype in (self.torch.float16, self.torch.bfloat16)
+                 and width == value_width and width in (64, 128, 256))
+        if not fused:
+            query, gate, length = self.attention_prologue_(
+                query_gate, key, value, query_norm, key_norm, key_cache, value_cache,
+                position=position, sections=sections, frequency_base=frequency_base,
+                epsilon=epsilon)
+            out = self.online_attention(query, key_cache, value_cache, length=length,
+                                        scale=scale, gate=gate, out_dtype=out_dtype)
+            return out, length
+        capacity, batch, kv_heads, _ = _shape(key_cache)
+        query_gate = self._tensor(query_gate, "joint Q/gate projection", dimensions=2)
+        key = self._tensor(key, "attention key", dimensions=2)
+        value = self._tensor(value, "attention value", dimensions=2)
+        query_norm = self._fp32(query_norm, "query RMSNorm weight", dimensions=1)
+        key_norm = self._fp32(key_norm, "key RMSNorm weight", dimensions=1)
+        position = _nonnegative_integer("attention cache position", position)
+        if position >= capacity:
+            raise ValueError("attention cache position exceeds capacity")
+        if _shape(value_cache)[:3] != (capacity, batch, kv_heads):
+            raise ValueError("attention K/V cache capacity, batch, or heads differ")
+        if int(query_gate.shape[0]) != batch or int(query_gate.shape[1]) % (2 * width):
+            raise ValueError("joint Q/gate projection does not match the cache head width")
+        query_heads = int(query_gate.shape[1]) // (2 * width)
+        if query_heads % kv_heads:
+            raise ValueError("attention query heads must be a multiple of KV heads")
+        if _shape(key) != (batch, kv_heads * width) or _shape(value) != (batch,
+                                                                          kv_heads * width):
+            raise ValueError("attention key/value do not match cache token shape")
+        if _shape(query_norm) != (width,) or _shape(key_norm) != (width,):
+            raise ValueError("RMSNorm weight must match the head dimension")
+        self._same_dtype("attention step", query_gate, key, value, key_cache, value_cache)
+        if len(sections) != 4:
+            raise ValueError("IMRoPE requires four sections")
+        section = tuple(_nonnegative_integer("IMRoPE section", item) for item in sections)
+        scale_value = (1.0 / math.sqrt(width) if scale is None
+                       else _positive_finite("attention scale", scale))
+        out = _ops.attention_layer_step(
+            query_gate.reshape(batch, query_heads, 2 * width), key, value, query_norm, key_norm,
+            key_cache, value_cache, position=position, sections=section,
+            frequency_base=_positive_finite("frequency_base", frequency_base),
+            eps=_positive_finite("epsilon", epsilon), scale=scale_value, out_dtype=out_dtype)
+        return out, position + 1
+
     def recurrent_layer_step_(self, workspace: RocmRecurrentWorkspace, mixed: Any,
                               convolution_weights: Any, gate: Any, beta_logits: Any,
                               alpha_logits: Any, dt_bias: Any, ssm_a: Any, norm_weight: Any, *,

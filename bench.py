@@ -182,10 +182,13 @@ def bench_layers(torch, ops, lib, *, steps, warmup, seed=6):
     """The two fused Qwen3.5 decode-step paths around the kernels.
 
     * Attention layer at the C4 geometry (4 sequences, 16 q / 2 kv heads,
-      head_dim 256, bf16 cache of 32768 rows): fused prologue (query/gate
-      split, Q/K RMSNorm, IMROPE, append at row 32767) + split-K decode over
-      32768 rows with the fused sigmoid gate.  Bytes per step: the K/V rows
-      read (as C4) plus the prologue's projection reads and cache writes.
+      head_dim 256, bf16 cache of 32768 rows): prologue (query/gate split,
+      Q/K RMSNorm, IMROPE, append at row 32767) inside the split-K launch
+      over 32768 rows, then the combine with the sigmoid gate (two
+      launches; ``kernel_us`` is their HIP-event sum).  The three-launch
+      path (prologue kernel, split, combine) is timed beside it.  Bytes per
+      step: the K/V rows read (as C4) plus the prologue's projection reads
+      and cache writes.
     * Recurrent layer at the C5 geometry (16 k / 32 v heads, Dk = Dv = 128,
       conv kernel 4, batch 1): conv + SiLU + split + Q/K L2 + beta/decay,
       GDN step, gated RMSNorm (two launches; ``kernel_us`` is their
@@ -203,18 +206,22 @@ def bench_layers(torch, ops, lib, *, steps, warmup, seed=6):
     qw = torch.rand((d,), generator=g, device=dev) + 0.5
     kw = torch.rand((d,), generator=g, device=dev) + 0.5
 
+    rope = dict(sections=(11, 11, 10, 0), frequency_base=10000000.0, epsilon=1e-6)
+
     def attn_step():
-        q, gate, _ = ops.attention_prologue_(qg, kn, vn, qw, kw, K, V, position=ctx - 1,
-                                             sections=(11, 11, 10, 0),
-                                             frequency_base=10000000.0, epsilon=1e-6)
+        return ops.attention_layer_step_(qg, kn, vn, qw, kw, K, V, position=ctx - 1, **rope)
+
+    def attn_three_launches():
+        q, gate, _ = ops.attention_prologue_(qg, kn, vn, qw, kw, K, V, position=ctx - 1, **rope)
         return ops.online_attention(q, K, V, length=ctx, gate=gate)
 
     a_ms = _timed_steps(torch, attn_step, steps, warmup)
+    a3_ms = _timed_steps(torch, attn_three_launches, steps, warmup)
     lib.timing_enable(True)
     for _ in range(steps):
         attn_step()
     torch.cuda.synchronize()
-    pro_ms = _kernel_avg_ms(lib, lib.T_LAYER)
+    ak_ms = _kernel_avg_ms(lib, lib.T_DECODE) + _kernel_avg_ms(lib, lib.T_DECODE_COMBINE)
     lib.timing_enable(False)
     es = 2
     a_bytes = (2 * ctx * b * hkv * d * es + (hq * 2 * d + 2 * hkv * d) * b * es
@@ -250,7 +257,8 @@ def bench_layers(torch, ops, lib, *, steps, warmup, seed=6):
     return {
         "attention_layer_c4": {
             "us_per_step": round(a_ms * 1e3, 2),
-            "prologue_us": round(pro_ms * 1e3, 2),
+            "kernel_us": round(ak_ms * 1e3, 2),
+            "three_launch_us_per_step": round(a3_ms * 1e3, 2),
             "step_bytes": a_bytes,
             "step_gbs": round(a_bytes / (a_ms * 1e-3) / 1e9, 1),
             "frac_hbm": round(a_bytes / (a_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
@@ -299,8 +307,9 @@ def bench_layer_prefill(torch, ops, lib, *, steps, warmup, seed=7):
     * Attention layer, Qwen3.5 head geometry (16 q / 2 kv heads, head_dim
       256, bf16), one sequence: a 2048-token chunk at position 2048 of a
       4096-row cache -- chunk prologue + causal prefill + sigmoid gate.
-      FLOPs count causal-valid pairs (4 D Hq per pair).  Token path: 2048 x
-      (decode prologue + gated split-K decode).
+      FLOPs count causal-valid pairs (4 D Hq per pair).  Token path: 2048
+      attention-layer decode steps (prologue in the split-K launch, gated
+      combine).
     * Recurrent layer, C5 geometry (16 k / 32 v heads, Dk = Dv = 128, conv
       kernel 4): a 1024-token chunk -- chunk prep + chunked GDN + gated
       RMSNorm.  Token path: 1024 fused recurrent-layer steps."""
@@ -323,10 +332,9 @@ def bench_layer_prefill(torch, ops, lib, *, steps, warmup, seed=7):
 
     def tokens_attn():
         for t in range(T):
-            q, gate, _ = ops.attention_prologue_(qg[t:t + 1], kn[t:t + 1], vn[t:t + 1], qw, kw,
-                                                 K, V, position=prefix + t, sections=sec,
-                                                 frequency_base=base, epsilon=eps)
-            ops.online_attention(q, K, V, length=prefix + t + 1, gate=gate)
+            ops.attention_layer_step_(qg[t:t + 1], kn[t:t + 1], vn[t:t + 1], qw, kw, K, V,
+                                      position=prefix + t, sections=sec, frequency_base=base,
+                                      epsilon=eps)
 
     at_ms = _timed_steps(torch, tokens_attn, 2, 1)
     pairs = sum(prefix + i + 1 for i in range(T))

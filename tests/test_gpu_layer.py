@@ -232,6 +232,96 @@ def test_attention_prologue_then_gated_decode(gpu, ops, dtype):
         assert np.abs(_np(out[bb]) - ref).max() <= tol
 
 
+# (b, hq, hkv, d, cap, pos): the Qwen3.5 C4 geometry; head_dim 128 at group
+# 8; group 40 at head_dim 64 (three 16-head column blocks, so three blocks
+# hold the new row and only the first writes it); position 0 (one cache
+# row); a position on a split-chunk edge.
+_STEP_SHAPES = [(4, 16, 2, 256, 640, 600), (2, 16, 2, 128, 300, 257),
+                (1, 40, 1, 64, 200, 130), (3, 8, 2, 128, 64, 0), (1, 16, 2, 256, 4096, 3071)]
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("b,hq,hkv,d,cap,pos", _STEP_SHAPES)
+def test_attention_layer_step_fused_equals_two_calls(gpu, ops, dtype, b, hq, hkv, d, cap, pos):
+    """The fused step (prologue inside the split-K launch, gate read from
+    the joint projection in the combine) returns the bytes of
+    attention_prologue_ + online_attention(gate=) and leaves the caches in
+    the same state; both match the oracle."""
+    import torch
+    rng = np.random.default_rng(b * 1000 + hq * 10 + d + pos)
+    sections, base, eps = (11, 11, 10, 0), 10000000.0, 1e-6
+    if 2 * sum(sections) > d:
+        sections = (4, 4, 2, 0)
+    kc = I.round_to(rng.standard_normal((cap, b, hkv, d)), dtype)
+    vc = I.round_to(rng.standard_normal((cap, b, hkv, d)), dtype)
+    qg = I.round_to(rng.standard_normal((b, hq * 2 * d)) * 3, dtype)
+    k = I.round_to(rng.standard_normal((b, hkv * d)) * 3, dtype)
+    v = I.round_to(rng.standard_normal((b, hkv * d)), dtype)
+    qw = torch.from_numpy(rng.uniform(0.5, 1.5, d).astype(np.float32)).to(gpu)
+    kw = torch.from_numpy(rng.uniform(0.5, 1.5, d).astype(np.float32)).to(gpu)
+    args = (_dev(torch, qg, dtype, gpu), _dev(torch, k, dtype, gpu), _dev(torch, v, dtype, gpu),
+            qw, kw)
+    kw_args = dict(position=pos, sections=sections, frequency_base=base, epsilon=eps)
+    KC1, VC1 = _dev(torch, kc, dtype, gpu), _dev(torch, vc, dtype, gpu)
+    q_dev, gate_dev, nxt = ops.attention_prologue_(*args, KC1, VC1, **kw_args)
+    two = ops.online_attention(q_dev, KC1, VC1, length=nxt, gate=gate_dev)
+    two32 = ops.online_attention(q_dev, KC1, VC1, length=nxt, gate=gate_dev,
+                                 out_dtype=torch.float32)
+    KC2, VC2 = _dev(torch, kc, dtype, gpu), _dev(torch, vc, dtype, gpu)
+    fused, n2 = ops.attention_layer_step_(*args, KC2, VC2, **kw_args)
+    fused32, _ = ops.attention_layer_step_(*args, KC2, VC2, out_dtype=torch.float32, **kw_args)
+    torch.cuda.synchronize()
+    assert n2 == nxt == pos + 1
+    assert fused.dtype == _td(torch, dtype) and fused.shape == (b, hq, d)
+    assert torch.equal(fused.view(torch.int16), two.view(torch.int16))
+    assert torch.equal(fused32, two32)
+    assert torch.equal(KC2.view(torch.int16), KC1.view(torch.int16))
+    assert torch.equal(VC2.view(torch.int16), VC1.view(torch.int16))
+    # against the oracle: prologue on the host inputs, decode on the cache
+    # the device wrote
+    rq, rg, rk, rv = L.attention_prologue(qg, k, v, _np(qw), _np(kw), eps, np.full(b, pos),
+                                          sections, base)
+    tol = _tol(dtype)
+    got_k = _np(KC2)
+    assert np.abs(got_k[pos] - rk).max() <= tol
+    assert np.array_equal(_np(VC2)[pos], rv)
+    vc_dev = _np(VC2)
+    for bb in range(b):
+        ref = A.attention_decode_twopass(rq[bb], got_k[:pos + 1, bb], vc_dev[:pos + 1, bb],
+                                         hq // hkv, 1.0 / np.sqrt(d))
+        ref = ref * (1.0 / (1.0 + np.exp(-rg[bb])))
+        assert np.abs(_np(fused32[bb]) - ref).max() <= tol
+
+
+def test_attention_layer_step_fp32_runs_two_calls(gpu, ops):
+    """fp32 caches take the separate prologue + gated decode launches."""
+    import torch
+    rng = np.random.default_rng(3)
+    b, hq, hkv, d, cap, pos = 2, 8, 2, 64, 100, 70
+    sections, base, eps = (4, 4, 2, 0), 10000.0, 1e-6
+    kc = rng.standard_normal((cap, b, hkv, d)).astype(np.float32)
+    vc = rng.standard_normal((cap, b, hkv, d)).astype(np.float32)
+    qg = rng.standard_normal((b, hq * 2 * d)).astype(np.float32)
+    k = rng.standard_normal((b, hkv * d)).astype(np.float32)
+    v = rng.standard_normal((b, hkv * d)).astype(np.float32)
+    qw = rng.uniform(0.5, 1.5, d).astype(np.float32)
+    kw = rng.uniform(0.5, 1.5, d).astype(np.float32)
+    KC, VC = _dev(torch, kc, "f32", gpu), _dev(torch, vc, "f32", gpu)
+    out, n = ops.attention_layer_step_(
+        _dev(torch, qg, "f32", gpu), _dev(torch, k, "f32", gpu), _dev(torch, v, "f32", gpu),
+        torch.from_numpy(qw).to(gpu), torch.from_numpy(kw).to(gpu), KC, VC, position=pos,
+        sections=sections, frequency_base=base, epsilon=eps)
+    assert n == pos + 1
+    rq, rg, rk, rv = L.attention_prologue(qg, k, v, qw, kw, eps, np.full(b, pos), sections, base)
+    got_k, got_v = _np(KC), _np(VC)
+    assert np.abs(got_k[pos] - rk).max() <= 1e-4
+    for bb in range(b):
+        ref = A.attention_decode_twopass(rq[bb], got_k[:pos + 1, bb], got_v[:pos + 1, bb],
+                                         hq // hkv, 1.0 / 8.0)
+        ref = ref * (1.0 / (1.0 + np.exp(-rg[bb])))
+        assert np.abs(_np(out[bb]) - ref).max() <= 1e-4
+
+
 # ------------------------------------------------ recurrent-layer step
 
 # (1, 1, 2, 64, 300, 3): value rows wider than the one-launch step takes,
