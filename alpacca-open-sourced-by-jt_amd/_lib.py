@@ -77,8 +77,8 @@ SIGNATURES = {
     "alpx_attention_layer_step": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
                                            _c_ptr, _c_ptr, _c_ptr, _c_size, _c_int, _c_int,
                                            _c_i64, _c_int, _c_int, _c_int, _c_int, _c_i64,
-                                           ctypes.POINTER(ctypes.c_int), ctypes.c_double,
-                                           _c_float, _c_float, _c_ptr]),
+                                           _c_ptr, ctypes.POINTER(ctypes.c_int),
+                                           ctypes.c_double, _c_float, _c_float, _c_ptr]),
     "alpx_attention_prologue_chunk": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
                                                _c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_int,
                                                _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,

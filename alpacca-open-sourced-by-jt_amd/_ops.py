@@ -380,14 +380,17 @@ def attention_prologue(query_gate, key, value, q_norm, k_norm, key_cache, value_
 
 
 def attention_layer_step(query_gate, key, value, q_norm, k_norm, key_cache, value_cache, *,
-                         position, sections, frequency_base, eps, scale=None, out_dtype=None):
+                         position, sections, frequency_base, eps, positions=None, scale=None,
+                         out_dtype=None):
     """One decode token of the Qwen3.5 attention layer in two launches: the
     prologue (Q/K RMSNorm + IMROPE, cache append at ``position``) inside the
     split-K decode launch, then the combine with the sigmoid gate taken from
     the second half of ``query_gate [B, Hq, 2D]``.  ``key`` / ``value``
     ``[B, Hkv, D]``; caches ``[C, B, Hkv, D]`` (fp16 / bf16, D in 64, 128,
-    256).  Returns the gated output ``[B, Hq, D]`` over ``position + 1``
-    cache rows."""
+    256).  With ``positions`` (device int32 ``[B]``, each at most
+    ``position``) sequence b's token sits at row ``positions[b]`` and
+    attends rows ``0 .. positions[b]``.  Returns the gated output
+    ``[B, Hq, D]``."""
     torch = _torch()
     capacity, bsz, kv_heads, dim = (int(x) for x in key_cache.shape)
     q_heads = int(query_gate.shape[1])
@@ -400,12 +403,16 @@ def attention_layer_step(query_gate, key, value, q_norm, k_norm, key_cache, valu
     if nbytes == 0:
         raise ValueError("invalid attention step sizes")
     ws = _lib.workspace(torch, key_cache.device, nbytes)
+    pos_ptr = None
+    if positions is not None:
+        positions = positions.to(device=key_cache.device, dtype=torch.int32).contiguous()
+        pos_ptr = positions.data_ptr()
     rc = L.alpx_attention_layer_step(
         query_gate.data_ptr(), key.data_ptr(), value.data_ptr(), q_norm.data_ptr(),
         k_norm.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(), out.data_ptr(),
         ws.data_ptr(), ws.numel(), _lib.dtype_code(torch, key_cache.dtype),
         _lib.dtype_code(torch, out.dtype), capacity, bsz, q_heads, kv_heads, dim, int(position),
-        _sections(sections), float(frequency_base), float(eps), float(scale),
+        pos_ptr, _sections(sections), float(frequency_base), float(eps), float(scale),
         _lib.stream_handle(torch, key_cache.device))
     _lib.check(rc)
     return out

@@ -59,7 +59,7 @@ __device__ __forceinline__ int seq_len(const DecodeArgs& a, int b) {
   if (a.causal_pos0 >= 0)
     n = a.causal_pos0 + b + 1 - a.kv_start;
   else
-    n = a.seq_lens == nullptr ? a.length : a.seq_lens[b];
+    n = a.seq_lens == nullptr ? a.length : (int64_t)a.seq_lens[b] + a.len_bias;
   n = n < 0 ? 0 : n;
   return (int)(n > a.length ? a.length : n);
 }
@@ -214,7 +214,7 @@ __device__ __forceinline__ void split_body(const DecodeArgs& a, const SplitProlo
     T* qrows = (T*)(smem + kLdsBytes);
     T* nkv = qrows + 16 * D;
     float* stage = (float*)(nkv + 2 * D) + wave * D;
-    const int64_t pos = pp->position;
+    const int64_t pos = pp->positions ? (int64_t)pp->positions[b] : pp->position;
     owns_new = pos >= start && pos < end;
     new_kv = nkv;
     if (owns_new && wave < 2) {
@@ -329,7 +329,7 @@ __device__ __forceinline__ void split_body(const DecodeArgs& a, const SplitProlo
       *(V8*)(ldsv + r * kStride + 8 * c) = vr[it];
     }
     if constexpr (PRO) {
-      const int64_t r = pp->position - p0;
+      const int64_t r = (pp->positions ? (int64_t)pp->positions[b] : pp->position) - p0;
       if (owns_new && r >= 0 && r < kTile) {
         for (int i = lane; i < D; i += 64) {
           ldsk[r * kStride + i] = new_kv[i];
@@ -890,7 +890,7 @@ int run_decode(DecodeArgs a, int dtype, int out_dtype, void* workspace, size_t w
   const bool paged = a.pages != nullptr;
   if (pro != nullptr) {
     // fused prologue: 16-bit MFMA split over a contiguous cache only
-    if (mfma && !paged && a.seq_lens == nullptr && a.causal_pos0 < 0) {
+    if (mfma && !paged && a.causal_pos0 < 0) {
       if (dtype == ALPX_F16) kernel = split_kernel_pro<f16_t>(D);
       if (dtype == ALPX_BF16) kernel = split_kernel_pro<bf16_t>(D);
     }

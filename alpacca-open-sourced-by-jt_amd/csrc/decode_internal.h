@@ -38,16 +38,19 @@ struct DecodeArgs {
   int num_pages;
   int64_t ks_page, vs_page;
   int64_t gate_stride;  // elements between the gate rows of (b, h); 0 = value_dim
+  int len_bias;         // added to seq_lens[b] (decode mode)
 };
 
 // The Qwen3.5 attention prologue fused into the split launch: one new token
-// per sequence, every sequence at cache row `position`.
+// per sequence, at cache row positions[b] (device) or, without positions,
+// at `position` for every sequence.
 struct SplitPrologue {
   const void* qg;      // [B, Hq, 2 D]: per head D query then D gate values
   const void* key;     // [B, Hkv, D] new key rows, before norm and rotation
   const void* value;   // [B, Hkv, D] new value rows
   const float* qw;     // [D] query RMSNorm weight
   const float* kw;     // [D] key RMSNorm weight
+  const int32_t* positions;
   int64_t position;
   int R;               // rotary pairs
   int sec[4];

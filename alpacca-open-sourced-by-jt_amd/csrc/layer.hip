@@ -1079,7 +1079,8 @@ extern "C" int alpx_attention_layer_step(const void* query_gate, const void* key
                                          void* out, void* workspace, size_t workspace_bytes,
                                          int dtype, int out_dtype, int64_t capacity, int batch,
                                          int q_heads, int kv_heads, int head_dim,
-                                         int64_t position, const int* sections,
+                                         int64_t position, const int32_t* positions,
+                                         const int* sections,
                                          double frequency_base, float eps, float scale,
                                          void* stream) {
   using namespace alpx;
@@ -1110,6 +1111,7 @@ extern "C" int alpx_attention_layer_step(const void* query_gate, const void* key
   pp.value = value;
   pp.qw = q_norm;
   pp.kw = k_norm;
+  pp.positions = positions;
   pp.position = position;
   pp.R = R;
   for (int i = 0; i < 4; ++i) pp.sec[i] = sections[i];
@@ -1128,6 +1130,10 @@ extern "C" int alpx_attention_layer_step(const void* query_gate, const void* key
   a.ks_h = a.vs_h = D;
   a.causal_pos0 = -1;
   a.length = (int)(position + 1);
+  if (positions != nullptr) {  // sequence b attends rows 0 .. positions[b]
+    a.seq_lens = positions;
+    a.len_bias = 1;
+  }
   a.batch = batch;
   a.q_heads = q_heads;
   a.kv_heads = kv_heads;

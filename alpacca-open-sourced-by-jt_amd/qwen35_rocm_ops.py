@@ -673,7 +673,7 @@ class Qwen35RocmOps:
     def attention_layer_step_(self, query_gate: Any, key: Any, value: Any, query_norm: Any,
                               key_norm: Any, key_cache: Any, value_cache: Any, *, position: int,
                               sections: Sequence[int], frequency_base: float, epsilon: float,
-                              scale: float | None = None,
+                              positions: Any = None, scale: float | None = None,
                               out_dtype: Any = None) -> tuple[Any, int]:
         """One decode token of the Qwen3.5 full-attention layer after its
         projections (extension; qwen35_runtime.py:597-665 for one token per
@@ -682,23 +682,15 @@ class Qwen35RocmOps:
         caches with equal key and value widths of 64, 128 or 256 run it as
         two launches (prologue fused into the split-K launch, gate in the
         combine); other shapes run the prologue and the gated decode as
-        separate launches.  Returns ``(gated output [B, Hq, Dv],
+        separate launches.  ``positions`` (extension; host ints or a device
+        int32 tensor ``[B]``) puts sequence b's token at row ``positions[b]``
+        (ragged batch); ``position`` then bounds them, and host values above
+        it or below 0 are rejected.  Returns ``(gated output [B, Hq, Dv],
         position + 1)``."""
         key_cache = self._tensor(key_cache, "attention key cache", dimensions=4)
         value_cache = self._tensor(value_cache, "attention value cache", dimensions=4)
-        width = int(key_cache.shape[3])
+        capacity, batch, kv_heads, width = _shape(key_cache)
         value_width = int(value_cache.shape[3])
-        fused = (key_cache.dtype in (self.torch.float16, self.torch.bfloat16)
-                 and width == value_width and width in (64, 128, 256))
-        if not fused:
-            query, gate, length = self.attention_prologue_(
-                query_gate, key, value, query_norm, key_norm, key_cache, value_cache,
-                position=position, sections=sections, frequency_base=frequency_base,
-                epsilon=epsilon)
-            out = self.online_attention(query, key_cache, value_cache, length=length,
-                                        scale=scale, gate=gate, out_dtype=out_dtype)
-            return out, length
-        capacity, batch, kv_heads, _ = _shape(key_cache)
         query_gate = self._tensor(query_gate, "joint Q/gate projection", dimensions=2)
         key = self._tensor(key, "attention key", dimensions=2)
         value = self._tensor(value, "attention value", dimensions=2)
@@ -715,7 +707,7 @@ class Qwen35RocmOps:
         if query_heads % kv_heads:
             raise ValueError("attention query heads must be a multiple of KV heads")
         if _shape(key) != (batch, kv_heads * width) or _shape(value) != (batch,
-                                                                          kv_heads * width):
+                                                                          kv_heads * value_width):
             raise ValueError("attention key/value do not match cache token shape")
         if _shape(query_norm) != (width,) or _shape(key_norm) != (width,):
             raise ValueError("RMSNorm weight must match the head dimension")
@@ -723,13 +715,35 @@ class Qwen35RocmOps:
         if len(sections) != 4:
             raise ValueError("IMRoPE requires four sections")
         section = tuple(_nonnegative_integer("IMRoPE section", item) for item in sections)
+        base = _positive_finite("frequency_base", frequency_base)
+        eps = _positive_finite("epsilon", epsilon)
+        if positions is not None:
+            if not self.torch.is_tensor(positions) or positions.device.type != "cuda":
+                host = [int(p) for p in positions]
+                if len(host) != batch or any(p < 0 or p > position for p in host):
+                    raise ValueError("positions must hold one row in [0, position] per sequence")
+                positions = self.torch.tensor(host, dtype=self.torch.int32, device=self.device)
+            elif _shape(positions) != (batch,):
+                raise ValueError("positions must hold one row per sequence")
+            positions = positions.to(self.torch.int32).contiguous()
+        query_gate = query_gate.reshape(batch, query_heads, 2 * width)
+        fused = (key_cache.dtype in (self.torch.float16, self.torch.bfloat16)
+                 and width == value_width and width in (64, 128, 256))
+        if not fused:
+            query, gate = _ops.attention_prologue(
+                query_gate, key, value, query_norm, key_norm, key_cache, value_cache,
+                position=position, positions=positions, sections=section, frequency_base=base,
+                eps=eps)
+            out = self.online_attention(query, key_cache, value_cache, length=position + 1,
+                                        scale=scale, seq_lens=None if positions is None
+                                        else positions + 1, gate=gate, out_dtype=out_dtype)
+            return out, position + 1
         scale_value = (1.0 / math.sqrt(width) if scale is None
                        else _positive_finite("attention scale", scale))
         out = _ops.attention_layer_step(
-            query_gate.reshape(batch, query_heads, 2 * width), key, value, query_norm, key_norm,
-            key_cache, value_cache, position=position, sections=section,
-            frequency_base=_positive_finite("frequency_base", frequency_base),
-            eps=_positive_finite("epsilon", epsilon), scale=scale_value, out_dtype=out_dtype)
+            query_gate, key, value, query_norm, key_norm, key_cache, value_cache,
+            position=position, sections=section, frequency_base=base, eps=eps,
+            positions=positions, scale=scale_value, out_dtype=out_dtype)
         return out, position + 1
 
     def recurrent_layer_step_(self, workspace: RocmRecurrentWorkspace, mixed: Any,

@@ -355,15 +355,19 @@ int alpx_attention_prologue(const void* query_gate, const void* key, const void*
 /* One decode token of the Qwen3.5 full-attention layer after its
  * projections (qwen35_runtime.py:597-665 for one token per sequence:
  * alpx_attention_prologue followed by alpx_decode_gqa with the sigmoid
- * gate), in two launches.  The split-K launch forms each block's query
- * heads from query_gate [B, Hq, 2D] (RMSNorm with q_norm, IMROPE at the
- * text lanes (position, position, position, 0)) and, in the blocks whose
- * chunk holds cache row `position`, the key row from key [B, Hkv, D]; the
- * rotated key and value [B, Hkv, D] are written to row `position` of the
- * caches [capacity, B, Hkv, D].  Attention runs over rows 0 .. position
- * with `scale`; the combine multiplies by sigmoid of the gate half of
- * query_gate and writes out [B, Hq, D] in out_dtype.  The values equal
- * those of the two-call path bit for bit.  fp16 / bf16 only, key width =
+ * gate), in two launches.  Sequence b's token sits at cache row pos_b =
+ * positions[b] (device int32) or, with positions null, `position`; with
+ * positions, `position` bounds them (a pos_b outside [0, position] writes
+ * no cache row and attends rows 0 .. min(pos_b, position)).  The split-K
+ * launch forms each block's query heads from query_gate [B, Hq, 2D]
+ * (RMSNorm with q_norm, IMROPE at the text lanes (pos_b, pos_b, pos_b, 0))
+ * and, in the blocks whose chunk holds row pos_b, the key row from key
+ * [B, Hkv, D]; the rotated key and value [B, Hkv, D] are written to row
+ * pos_b of the caches [capacity, B, Hkv, D].  Attention runs over rows
+ * 0 .. pos_b with `scale`; the combine multiplies by sigmoid of the gate
+ * half of query_gate and writes out [B, Hq, D] in out_dtype.  The values
+ * equal those of alpx_attention_prologue + alpx_decode_gqa (seq_lens =
+ * pos_b + 1, length position + 1) bit for bit.  fp16 / bf16 only, key width =
  * value width in {64, 128, 256}, 16-byte aligned buffers (others:
  * ALPX_EUNSUPPORTED).  workspace: alpx_decode_workspace_bytes(batch,
  * q_heads, kv_heads, head_dim, position + 1) bytes. */
@@ -372,8 +376,8 @@ int alpx_attention_layer_step(const void* query_gate, const void* key, const voi
                               void* value_cache, void* out, void* workspace,
                               size_t workspace_bytes, int dtype, int out_dtype, int64_t capacity,
                               int batch, int q_heads, int kv_heads, int head_dim,
-                              int64_t position, const int* sections, double frequency_base,
-                              float eps, float scale, void* stream);
+                              int64_t position, const int32_t* positions, const int* sections,
+                              double frequency_base, float eps, float scale, void* stream);
 
 /* Workspace bytes for alpx_recurrent_step. */
 size_t alpx_recurrent_step_workspace_bytes(int batch, int key_heads, int value_heads, int key_dim,

@@ -122,23 +122,23 @@ def test_layer_entry_points_validate_without_gpu(pkg):
                                      15, 2, 256, 256, 0, None, sec, 1e7, 1e-6, None)
     assert rc == L.EINVAL and "multiple of KV heads" in L.last_error()
     f9 = (fake,) * 9
-    rc = lib.alpx_attention_layer_step(*f9, 1 << 20, 2, 2, 64, 1, 16, 2, 256, 64, sec, 1e7,
+    rc = lib.alpx_attention_layer_step(*f9, 1 << 20, 2, 2, 64, 1, 16, 2, 256, 64, None, sec, 1e7,
                                        1e-6, 0.0625, None)
     assert rc == L.ERANGE and "exceeds capacity" in L.last_error()
-    rc = lib.alpx_attention_layer_step(*f9[:8], None, 1 << 20, 2, 2, 64, 1, 16, 2, 256, 10, sec,
-                                       1e7, 1e-6, 0.0625, None)
+    rc = lib.alpx_attention_layer_step(*f9[:8], None, 1 << 20, 2, 2, 64, 1, 16, 2, 256, 10,
+                                       None, sec, 1e7, 1e-6, 0.0625, None)
     assert rc == L.EINVAL and "null" in L.last_error()
-    rc = lib.alpx_attention_layer_step(*f9, 1 << 20, 2, 2, 64, 1, 16, 2, 256, 10, bad, 1e7,
+    rc = lib.alpx_attention_layer_step(*f9, 1 << 20, 2, 2, 64, 1, 16, 2, 256, 10, None, bad, 1e7,
                                        1e-6, 0.0625, None)
     assert rc == L.EINVAL and "rotary pair" in L.last_error()
-    rc = lib.alpx_attention_layer_step(*f9, 16, 2, 2, 64, 1, 16, 2, 256, 10, sec, 1e7, 1e-6,
+    rc = lib.alpx_attention_layer_step(*f9, 16, 2, 2, 64, 1, 16, 2, 256, 10, None, sec, 1e7, 1e-6,
                                        0.0625, None)
     assert rc == L.EINVAL and "workspace" in L.last_error()
     # fp32 caches and widths outside {64, 128, 256} have no fused kernel
-    rc = lib.alpx_attention_layer_step(*f9, 1 << 20, 0, 0, 64, 1, 16, 2, 256, 10, sec, 1e7,
+    rc = lib.alpx_attention_layer_step(*f9, 1 << 20, 0, 0, 64, 1, 16, 2, 256, 10, None, sec, 1e7,
                                        1e-6, 0.0625, None)
     assert rc == L.EUNSUPPORTED and "fused attention step" in L.last_error()
-    rc = lib.alpx_attention_layer_step(*f9, 1 << 20, 2, 2, 64, 1, 16, 2, 96, 10, sec, 1e7,
+    rc = lib.alpx_attention_layer_step(*f9, 1 << 20, 2, 2, 64, 1, 16, 2, 96, 10, None, sec, 1e7,
                                        1e-6, 0.0625, None)
     assert rc == L.EUNSUPPORTED and "fused attention step" in L.last_error()
     assert lib.alpx_recurrent_step_workspace_bytes(1, 16, 32, 128, 128) > 0

@@ -293,6 +293,69 @@ def test_attention_layer_step_fused_equals_two_calls(gpu, ops, dtype, b, hq, hkv
         assert np.abs(_np(fused32[bb]) - ref).max() <= tol
 
 
+@pytest.mark.parametrize("dtype,d,rows,bound", [("bf16", 256, (600, 17, 0, 333), 600),
+                                                ("f16", 128, (5, 290, 64), 299),
+                                                ("f32", 64, (40, 3), 70)])
+def test_attention_layer_step_ragged_positions(gpu, ops, dtype, d, rows, bound):
+    """Per-sequence rows (a ragged batch): the fused step equals the
+    prologue with positions + the gated decode with seq_lens = row + 1 bit
+    for bit (fp32 takes those two calls itself), and both match the
+    oracle per sequence."""
+    import torch
+    rng = np.random.default_rng(d + len(rows))
+    b, hq, hkv, cap = len(rows), 16, 2, bound + 40
+    sections, base, eps = (11, 11, 10, 0), 10000000.0, 1e-6
+    if 2 * sum(sections) > d:
+        sections = (4, 4, 2, 0)
+    kc = I.round_to(rng.standard_normal((cap, b, hkv, d)), dtype)
+    vc = I.round_to(rng.standard_normal((cap, b, hkv, d)), dtype)
+    qg = I.round_to(rng.standard_normal((b, hq * 2 * d)) * 3, dtype)
+    k = I.round_to(rng.standard_normal((b, hkv * d)) * 3, dtype)
+    v = I.round_to(rng.standard_normal((b, hkv * d)), dtype)
+    qw_h = rng.uniform(0.5, 1.5, d).astype(np.float32)
+    kw_h = rng.uniform(0.5, 1.5, d).astype(np.float32)
+    qw, kw = torch.from_numpy(qw_h).to(gpu), torch.from_numpy(kw_h).to(gpu)
+    args = (_dev(torch, qg, dtype, gpu), _dev(torch, k, dtype, gpu), _dev(torch, v, dtype, gpu),
+            qw, kw)
+    pos_dev = torch.tensor(rows, dtype=torch.int32, device=gpu)
+    KC2, VC2 = _dev(torch, kc, dtype, gpu), _dev(torch, vc, dtype, gpu)
+    fused, n = ops.attention_layer_step_(*args, KC2, VC2, position=bound, positions=list(rows),
+                                         sections=sections, frequency_base=base, epsilon=eps,
+                                         out_dtype=torch.float32)
+    assert n == bound + 1
+    if dtype != "f32":
+        KC1, VC1 = _dev(torch, kc, dtype, gpu), _dev(torch, vc, dtype, gpu)
+        q_dev, gate_dev = _mod("_ops").attention_prologue(
+            args[0].reshape(b, hq, 2 * d), args[1], args[2], qw, kw, KC1, VC1, position=bound,
+            positions=pos_dev, sections=sections, frequency_base=base, eps=eps)
+        two = ops.online_attention(q_dev, KC1, VC1, length=bound + 1, seq_lens=pos_dev + 1,
+                                   gate=gate_dev, out_dtype=torch.float32)
+        fused_dev, _ = ops.attention_layer_step_(*args, _dev(torch, kc, dtype, gpu),
+                                                 _dev(torch, vc, dtype, gpu), position=bound,
+                                                 positions=pos_dev, sections=sections,
+                                                 frequency_base=base, epsilon=eps,
+                                                 out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        assert torch.equal(fused, two) and torch.equal(fused_dev, two)
+        assert torch.equal(KC2.view(torch.int16), KC1.view(torch.int16))
+        assert torch.equal(VC2.view(torch.int16), VC1.view(torch.int16))
+    rq, rg, rk, rv = L.attention_prologue(qg, k, v, qw_h, kw_h, eps, np.array(rows), sections,
+                                          base)
+    tol = _tol(dtype)
+    got_k, got_v = _np(KC2), _np(VC2)
+    for bb, p in enumerate(rows):
+        assert np.abs(got_k[p, bb] - rk[bb]).max() <= tol
+        assert np.array_equal(got_v[p, bb], rv[bb])
+        ref = A.attention_decode_twopass(rq[bb], got_k[:p + 1, bb], got_v[:p + 1, bb],
+                                         hq // hkv, 1.0 / np.sqrt(d))
+        ref = ref * (1.0 / (1.0 + np.exp(-rg[bb])))
+        assert np.abs(_np(fused[bb]) - ref).max() <= tol
+    # the rows other sequences' tokens went to are untouched
+    mask = np.ones((cap, b), bool)
+    mask[list(rows), np.arange(b)] = False
+    assert np.array_equal(got_k[mask], kc[mask])
+
+
 def test_attention_layer_step_fp32_runs_two_calls(gpu, ops):
     """fp32 caches take the separate prologue + gated decode launches."""
     import torch
