@@ -356,6 +356,54 @@ def test_attention_layer_step_ragged_positions(gpu, ops, dtype, d, rows, bound):
     assert np.array_equal(got_k[mask], kc[mask])
 
 
+def test_attention_layer_step_decode_loop_in_a_graph(gpu, ops):
+    """A decode loop as one captured graph replayed per token: the step
+    reads device positions and inputs that the host refreshes between
+    replays (the split plan is sized for the whole cache).  Every replay
+    equals the eager step bit for bit, with eager work and synchronisation
+    between replays, and the caches end identical."""
+    import torch
+    g = torch.Generator(device=gpu).manual_seed(21)
+    bf = torch.bfloat16
+    b, hq, hkv, d, cap = 2, 16, 2, 256, 192
+    rope = dict(sections=(11, 11, 10, 0), frequency_base=10000000.0, epsilon=1e-6)
+    KG = torch.randn((cap, b, hkv, d), generator=g, device=gpu).to(bf)
+    VG = torch.randn((cap, b, hkv, d), generator=g, device=gpu).to(bf)
+    qg = torch.zeros((b, hq * 2 * d), dtype=bf, device=gpu)
+    kn = torch.zeros((b, hkv * d), dtype=bf, device=gpu)
+    vn = torch.zeros((b, hkv * d), dtype=bf, device=gpu)
+    qw = torch.rand((d,), generator=g, device=gpu) + 0.5
+    kw = torch.rand((d,), generator=g, device=gpu) + 0.5
+    pos = torch.tensor([5, 9], dtype=torch.int32, device=gpu)
+
+    def step(K, V):
+        return ops.attention_layer_step_(qg, kn, vn, qw, kw, K, V, position=cap - 1,
+                                         positions=pos, **rope)[0]
+
+    side = torch.cuda.Stream(device=gpu)
+    side.wait_stream(torch.cuda.current_stream(gpu))
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step(KG, VG)
+    torch.cuda.current_stream(gpu).wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out_g = step(KG, VG)
+    KE, VE = KG.clone(), VG.clone()
+    for i in range(6):
+        pos.copy_(torch.tensor([10 + 17 * i, 40 + 3 * i], dtype=torch.int32))
+        qg.copy_(torch.randn(qg.shape, generator=g, device=gpu) * 3)
+        kn.copy_(torch.randn(kn.shape, generator=g, device=gpu) * 3)
+        vn.copy_(torch.randn(vn.shape, generator=g, device=gpu))
+        graph.replay()
+        torch.cuda.synchronize()
+        out_e = step(KE, VE)
+        torch.cuda.synchronize()
+        assert torch.equal(out_g.view(torch.int16), out_e.view(torch.int16)), i
+    assert torch.equal(KG.view(torch.int16), KE.view(torch.int16))
+    assert torch.equal(VG.view(torch.int16), VE.view(torch.int16))
+
+
 def test_attention_layer_step_fp32_runs_two_calls(gpu, ops):
     """fp32 caches take the separate prologue + gated decode launches."""
     import torch
