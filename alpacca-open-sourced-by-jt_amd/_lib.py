@@ -74,6 +74,10 @@ SIGNATURES = {
                                          _c_int, _c_int, _c_i64, _c_ptr,
                                          ctypes.POINTER(ctypes.c_int), ctypes.c_double,
                                          _c_float, _c_ptr]),
+    "alpx_prefill_causal_paged": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_int,
+                                           _c_int, _c_int, _c_ptr, _c_ptr, _c_int, _c_int,
+                                           _c_int, _c_int, _c_int, _c_i64, _c_int, _c_i64,
+                                           _c_float, _c_int, _c_ptr]),
     "alpx_attention_layer_step": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
                                            _c_ptr, _c_ptr, _c_ptr, _c_size, _c_int, _c_int,
                                            _c_i64, _c_int, _c_int, _c_int, _c_int, _c_i64,

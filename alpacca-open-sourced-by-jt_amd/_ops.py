@@ -87,6 +87,28 @@ def decode_paged(q, key_pages, value_pages, block_table, *, length, seq_lens=Non
     return out
 
 
+def prefill_paged(q, key_pages, value_pages, block_table, *, batch_index, pos0, kv_tokens,
+                  scale=None, window=0, kv_start=0, gate=None):
+    """Causal prefill of ``q [T, Hq, D]`` at positions ``pos0 ..`` over the
+    first ``kv_tokens`` logical rows of sequence ``batch_index`` of paged
+    caches ``[num_pages, page_size, Hkv, D]``; output ``[T, Hq, D]`` in q's
+    dtype, times sigmoid(gate) when ``gate`` is given."""
+    torch = _torch()
+    num_pages, page_size, kv_heads, dim = (int(x) for x in key_pages.shape)
+    tokens, q_heads = int(q.shape[0]), int(q.shape[1])
+    if scale is None:
+        scale = 1.0 / math.sqrt(dim)
+    out = torch.empty((tokens, q_heads, dim), dtype=q.dtype, device=q.device)
+    rc = _lib.lib().alpx_prefill_causal_paged(
+        q.data_ptr(), key_pages.data_ptr(), value_pages.data_ptr(), block_table.data_ptr(),
+        int(block_table.shape[1]), page_size, num_pages, int(batch_index),
+        None if gate is None else gate.data_ptr(), out.data_ptr(), tokens, int(kv_tokens),
+        q_heads, kv_heads, dim, int(pos0), int(window), int(kv_start), float(scale),
+        _lib.dtype_code(torch, q.dtype), _lib.stream_handle(torch, q.device))
+    _lib.check(rc)
+    return out
+
+
 def kv_export(key_cache, value_cache, *, batch_index, row0, rows):
     """Rows ``[row0, row0 + rows)`` of cache sequence ``batch_index`` as
     contiguous fp32 ``(key [rows, Hkv, D], value [rows, Hkv, Dv])``."""

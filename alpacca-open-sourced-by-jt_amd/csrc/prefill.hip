@@ -48,6 +48,13 @@ struct PrefillArgs {
   int col_tiles;           // column tiles per kv head
   int per_xcd;             // work items per XCD slice of the grid
   float scale_log2;
+  // Paged caches (the PAGED kernels): cache row j lives in page
+  // pages[j >> page_shift] (clamped to [0, num_pages)), at row
+  // j & (page size - 1); ks_page / vs_page are the page strides in elements.
+  const int32_t* pages;
+  int page_shift;
+  int num_pages;
+  int64_t ks_page, vs_page;
 };
 
 constexpr int kXcds = 8;  // MI355X: workgroup b is dispatched to XCD b % 8
@@ -205,7 +212,7 @@ __device__ __forceinline__ void pin(V& x) {
 #endif
 }
 
-template <typename T, typename TO, int D, int BK, int NQB>
+template <typename T, typename TO, int D, int BK, int NQB, bool PAGED = false>
 __global__ void __launch_bounds__(256, 2)
 prefill_mfma(PrefillArgs a) {
   typedef typename Vec8<T>::type V8;
@@ -314,10 +321,45 @@ prefill_mfma(PrefillArgs a) {
   }
   const T* kg = (const T*)a.k + (int64_t)kvh * D;
   const T* vg = (const T*)a.v + (int64_t)kvh * D;
-  auto load_tile = [&](const T* g, int64_t pos, const uint32_t (&ofs)[kIW], int t, int buf) {
+  // Paged: the block's page numbers (clamped) are staged in LDS once, so a
+  // tile's page lookup is an LDS read rather than a global load on the
+  // path to its tile loads; ranges of more than kPageSlots pages look up
+  // the table directly.
+  constexpr int kPageSlots = PAGED ? 1024 : 1;
+  __shared__ int page_lds[kPageSlots];
+  [[maybe_unused]] int page0 = 0;
+  [[maybe_unused]] bool pages_in_lds = false;
+  if constexpr (PAGED) {
+    page0 = lo >> a.page_shift;
+    const int np = nt > 0 ? ((hi - 1) >> a.page_shift) - page0 + 1 : 0;
+    pages_in_lds = np <= kPageSlots;
+    if (pages_in_lds) {
+      for (int i = threadIdx.x; i < np; i += 256) {
+        const int pg = a.pages[page0 + i];
+        page_lds[i] = pg < 0 ? 0 : (pg >= a.num_pages ? a.num_pages - 1 : pg);
+      }
+    }
+    __syncthreads();
+  }
+  // A tile starts at a multiple of BK and a page holds a multiple of BK
+  // rows, so a paged tile lies in one page, looked up once per tile.
+  auto load_tile = [&](const T* g, int64_t pos, int64_t page_stride, const uint32_t (&ofs)[kIW],
+                       int t, int buf) {
     const int k0 = lo + t * BK;
+    const T* base = g + (int64_t)k0 * pos;
+    if constexpr (PAGED) {
+      const int pi = k0 >> a.page_shift;
+      int pg;
+      if (pages_in_lds) {
+        pg = __builtin_amdgcn_readfirstlane(page_lds[pi - page0]);
+      } else {
+        pg = a.pages[pi];
+        pg = pg < 0 ? 0 : (pg >= a.num_pages ? a.num_pages - 1 : pg);
+      }
+      base = g + (int64_t)pg * page_stride + (int64_t)(k0 & ((1 << a.page_shift) - 1)) * pos;
+    }
     const i32x4 r = rsrc_words(
-        g + (int64_t)k0 * pos, (uint32_t)((int64_t)(a.kv_tokens - k0) * pos * (int64_t)sizeof(T)));
+        base, (uint32_t)((int64_t)(a.kv_tokens - k0) * pos * (int64_t)sizeof(T)));
     const uint32_t lds0 =
         (uint32_t)(uintptr_t)(lds_void_t*)(smem + buf * kTileB + wave * kIW * 1024);
 #pragma unroll
@@ -516,8 +558,8 @@ prefill_mfma(PrefillArgs a) {
     // iteration's first LDS read, which would also wait for the tile loads
     // issued below.  An explicit wait here clears its scoreboard for free.
     __builtin_amdgcn_s_waitcnt(0);
-    if (j + 2 < nt) load_tile(kg, a.ks_pos, kofs, j + 2, P);
-    if (j < nt) load_tile(vg, a.vs_pos, vofs, j, 2 + P);
+    if (j + 2 < nt) load_tile(kg, a.ks_pos, a.ks_page, kofs, j + 2, P);
+    if (j < nt) load_tile(vg, a.vs_pos, a.vs_page, vofs, j, 2 + P);
     // Rescale for the m moved at tile j - 1 (O holds tiles <= j - 2 and is
     // about to take PV(j - 1), formed against the moved m; l was rescaled
     // at the move, before it took tile j - 1's P).
@@ -566,8 +608,8 @@ prefill_mfma(PrefillArgs a) {
   for (int kk = 0; kk < KK; ++kk)
 #pragma unroll
     for (int qb = 0; qb < NQB; ++qb) pv[1][kk][qb] = (V8){};
-  if (nt > 0) load_tile(kg, a.ks_pos, kofs, 0, 0);
-  if (nt > 1) load_tile(kg, a.ks_pos, kofs, 1, 1);
+  if (nt > 0) load_tile(kg, a.ks_pos, a.ks_page, kofs, 0, 0);
+  if (nt > 1) load_tile(kg, a.ks_pos, a.ks_page, kofs, 1, 1);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   qk_first();
@@ -619,6 +661,17 @@ const void* pick_kernel(int D) {
   return nullptr;
 }
 
+// Paged caches: output in the cache dtype only.
+template <typename T>
+const void* pick_kernel_paged(int D) {
+  switch (D) {
+    case 64: return (const void*)prefill_mfma<T, T, 64, 64, 2, true>;
+    case 128: return (const void*)prefill_mfma<T, T, 128, 64, 2, true>;
+    case 256: return (const void*)prefill_mfma<T, T, 256, 32, 1, true>;
+  }
+  return nullptr;
+}
+
 template <typename T>
 const void* pick_kernel_out(int D, int out_dtype) {
   switch (out_dtype) {
@@ -646,7 +699,8 @@ int prefill_impl(const void* q, const void* key, const void* value, const void* 
                  void* workspace, size_t workspace_bytes, int q_tokens, int kv_tokens,
                  int q_heads, int kv_heads, int key_dim, int value_dim, int64_t k_pos_stride,
                  int64_t v_pos_stride, int64_t q_pos0, int window, int64_t kv_start, float scale,
-                 int dtype, int out_dtype, void* stream) {
+                 int dtype, int out_dtype, void* stream, const int32_t* pages = nullptr,
+                 int page_shift = 0, int num_pages = 0) {
   using namespace alpx;
   if (!q || !key || !value || !out) return fail(ALPX_EINVAL, "alpx_prefill_causal: null buffer");
   if (!dtype_ok(dtype) || !dtype_ok(out_dtype))
@@ -677,13 +731,25 @@ int prefill_impl(const void* q, const void* key, const void* value, const void* 
   const bool offsets_fit = (int64_t)kv_tokens * k_pos_stride * (int64_t)es < ((int64_t)1 << 31) &&
                            (int64_t)kv_tokens * v_pos_stride * (int64_t)es < ((int64_t)1 << 31) &&
                            q_pos0 - kv_start < ((int64_t)1 << 30) && q_pos0 - kv_start > -((int64_t)1 << 30);
+  if (pages != nullptr && !(mfma && offsets_fit && out_dtype == dtype))
+    return fail(ALPX_EUNSUPPORTED,
+                "alpx_prefill_causal_paged: needs fp16/bf16 pages, head_dim in {64, 128, 256}, "
+                "16-byte aligned rows and out_dtype == dtype");
   if (mfma && offsets_fit) {
     const void* kernel = nullptr;
-    if (dtype == ALPX_F16)
+    if (pages != nullptr)
+      kernel = dtype == ALPX_F16 ? pick_kernel_paged<f16_t>(key_dim)
+                                 : pick_kernel_paged<bf16_t>(key_dim);
+    else if (dtype == ALPX_F16)
       kernel = pick_kernel_out<f16_t>(key_dim, out_dtype);
     else
       kernel = pick_kernel_out<bf16_t>(key_dim, out_dtype);
-    PrefillArgs a;
+    PrefillArgs a = {};
+    a.pages = pages;
+    a.page_shift = page_shift;
+    a.num_pages = num_pages;
+    a.ks_page = ((int64_t)1 << page_shift) * k_pos_stride;
+    a.vs_page = ((int64_t)1 << page_shift) * v_pos_stride;
     a.q = q;
     a.k = key;
     a.v = value;
@@ -766,4 +832,26 @@ extern "C" int alpx_prefill_causal_gated(const void* q, const void* key, const v
   return prefill_impl(q, key, value, gate, out, workspace, workspace_bytes, q_tokens, kv_tokens,
                       q_heads, kv_heads, key_dim, value_dim, k_pos_stride, v_pos_stride, q_pos0,
                       window, kv_start, scale, dtype, out_dtype, stream);
+}
+
+extern "C" int alpx_prefill_causal_paged(const void* q, const void* key_pages,
+                                         const void* value_pages, const int32_t* block_table,
+                                         int max_pages, int page_size, int num_pages,
+                                         int batch_index, const void* gate, void* out,
+                                         int q_tokens, int kv_tokens, int q_heads, int kv_heads,
+                                         int head_dim, int64_t q_pos0, int window,
+                                         int64_t kv_start, float scale, int dtype, void* stream) {
+  using namespace alpx;
+  if (!block_table) return fail(ALPX_EINVAL, "alpx_prefill_causal_paged: null block table");
+  if (max_pages <= 0 || num_pages <= 0 || batch_index < 0)
+    return fail(ALPX_EINVAL, "alpx_prefill_causal_paged: sizes must be positive");
+  if (page_size < 64 || (page_size & (page_size - 1)) != 0)
+    return fail(ALPX_EINVAL, "alpx_prefill_causal_paged: page_size must be a power of two >= 64");
+  if ((int64_t)kv_tokens > (int64_t)max_pages * page_size)
+    return fail(ALPX_ERANGE, "attention cache length exceeds capacity");
+  const int64_t row = (int64_t)kv_heads * head_dim;
+  return prefill_impl(q, key_pages, value_pages, gate, out, nullptr, 0, q_tokens, kv_tokens,
+                      q_heads, kv_heads, head_dim, head_dim, row, row, q_pos0, window, kv_start,
+                      scale, dtype, dtype, stream, block_table + (int64_t)batch_index * max_pages,
+                      __builtin_ctz((unsigned)page_size), num_pages);
 }

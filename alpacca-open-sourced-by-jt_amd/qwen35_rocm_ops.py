@@ -891,6 +891,45 @@ class Qwen35RocmOps:
                                  seq_lens=seq_lens, gate=gate, scale=scale_value,
                                  out_dtype=out_dtype)
 
+    def paged_attention_prefill(self, query: Any, key_pages: Any, value_pages: Any,
+                                block_table: Any, *, position: int, batch_index: int = 0,
+                                scale: float | None = None, gate: Any = None) -> Any:
+        """``attention_prefill`` over paged caches (extension): the ``T``
+        query tokens ``[T, Hq, D]`` of sequence ``batch_index`` sit at
+        logical rows ``position .. position + T - 1`` (already appended) and
+        attend causally to rows ``0 ..`` of that sequence's pages.  Same
+        kernel and arithmetic as the contiguous call, so the same rows give
+        the same bits; output ``[T, Hq, D]`` in the query dtype (times
+        sigmoid(gate) with ``gate [T, Hq, D]``).  fp16 / bf16, head width
+        64, 128 or 256, page size a power of two >= 64."""
+        key_pages, value_pages = self._paged(key_pages, value_pages, block_table)
+        query = self._tensor(query, "attention query", dimensions=3)
+        position = _nonnegative_integer("attention cache position", position)
+        batch_index = _nonnegative_integer("batch_index", batch_index)
+        tokens, query_heads, width = _shape(query)
+        _, size, heads, key_width = _shape(key_pages)
+        if batch_index >= int(block_table.shape[0]):
+            raise ValueError("batch_index exceeds the block table batch")
+        if tokens <= 0:
+            raise ValueError("prefill chunk must hold at least one token")
+        if position + tokens > int(block_table.shape[1]) * size:
+            raise ValueError("attention cache position exceeds capacity")
+        if width != key_width or int(value_pages.shape[3]) != width:
+            raise ValueError("attention query does not match the K/V page head width")
+        if query_heads % heads:
+            raise ValueError("attention query heads must be a multiple of KV heads")
+        self._same_dtype("paged attention prefill", query, key_pages)
+        if gate is not None:
+            gate = self._tensor(gate, "sigmoid-gate logits", dimensions=3)
+            if _shape(gate) != (tokens, query_heads, width):
+                raise ValueError("sigmoid-gate logits must match the attention output")
+            self._same_dtype("attention gate", query, gate)
+        scale_value = (1.0 / math.sqrt(key_width) if scale is None
+                       else _positive_finite("attention scale", scale))
+        return _ops.prefill_paged(query, key_pages, value_pages, block_table,
+                                  batch_index=batch_index, pos0=position,
+                                  kv_tokens=position + tokens, scale=scale_value, gate=gate)
+
     # ------------------------------------------------------ chunked prefill
 
     def attention_layer_prefill_(self, query_gate: Any, key: Any, value: Any, query_norm: Any,

@@ -125,10 +125,27 @@ def bench_prefill(torch, ops, lib, *, steps, warmup, seed=3):
     torch.cuda.synchronize()
     k_ms = _kernel_avg_ms(lib, lib.T_PREFILL)
     lib.timing_enable(False)
+    # the same rows in a paged pool: 256-row pages in shuffled order
+    page, n_pages = 256, (prefix + tq) // 256
+    perm = torch.randperm(n_pages, generator=torch.Generator().manual_seed(seed))
+    kp = torch.empty((n_pages, page, hkv, d), dtype=K.dtype, device=dev)
+    vp = torch.empty_like(kp)
+    kp[perm.to(dev)] = K.view(n_pages, page, hkv, d)
+    vp[perm.to(dev)] = V.view(n_pages, page, hkv, d)
+    table = perm.to(torch.int32).view(1, n_pages).to(dev)
+    fp = lambda: ops.paged_attention_prefill(q, kp, vp, table, position=prefix)  # noqa: E731
+    _timed_steps(torch, fp, 3, 2)
+    lib.timing_enable(True)
+    for _ in range(steps):
+        fp()
+    torch.cuda.synchronize()
+    pk_ms = _kernel_avg_ms(lib, lib.T_PREFILL)
+    lib.timing_enable(False)
     pairs = sum(prefix + i + 1 for i in range(tq))  # 6,292,480
     flops = 4 * d * hq * pairs                      # QK^T and PV, 2 FLOP per MAC
     return {"ms_per_step": ms, "kernel_ms": k_ms, "flops": flops,
-            "tflops": flops / (ms * 1e-3) / 1e12, "kernel_tflops": flops / (k_ms * 1e-3) / 1e12}
+            "tflops": flops / (ms * 1e-3) / 1e12, "kernel_tflops": flops / (k_ms * 1e-3) / 1e12,
+            "paged_kernel_ms": pk_ms}
 
 
 def bench_gdn(torch, ops, lib, *, steps, warmup, seed=5):
@@ -571,7 +588,9 @@ def main() -> int:
             "ms_per_step": round(c3["ms_per_step"], 4),
             "kernel_ms": round(c3["kernel_ms"], 4),
             "kernel_tflops": round(c3["kernel_tflops"], 1),
-            "flops_per_step": c3["flops"]}
+            "flops_per_step": c3["flops"],
+            "paged_256_rows_kernel_ms": round(c3["paged_kernel_ms"], 4),
+            "paged_vs_contiguous_kernel": round(c3["kernel_ms"] / c3["paged_kernel_ms"], 3)}
     if "c5" in wl:
         c5 = bench_gdn(torch, ops, lib, steps=steps, warmup=warmup)
         extra["c5_gdn_bf16"] = {

@@ -93,6 +93,20 @@ int alpx_kv_append_paged(void* key_pages, void* value_pages, const void* key, co
                          const int32_t* block_table, int max_pages, int page_size, int num_pages,
                          int dtype, int batch, int kv_heads, int key_dim, int value_dim,
                          int tokens, int64_t position, const int32_t* positions, void* stream);
+/* Causal prefill (as alpx_prefill_causal / _gated, with gate optional:
+ * null = no gate) of q [q_tokens, Hq, D] at positions q_pos0 .. over the
+ * first kv_tokens logical rows of sequence batch_index of a paged cache
+ * (pages and block_table as above; page_size a power of two >= 64, so a
+ * key tile never crosses a page).  Same kernel, tiling and arithmetic as
+ * the contiguous call, so the same rows give the same bits.  fp16 / bf16
+ * pages, head_dim = value width in {64, 128, 256}, output in `dtype`
+ * (others: ALPX_EUNSUPPORTED).  No workspace. */
+int alpx_prefill_causal_paged(const void* q, const void* key_pages, const void* value_pages,
+                              const int32_t* block_table, int max_pages, int page_size,
+                              int num_pages, int batch_index, const void* gate, void* out,
+                              int q_tokens, int kv_tokens, int q_heads, int kv_heads,
+                              int head_dim, int64_t q_pos0, int window, int64_t kv_start,
+                              float scale, int dtype, void* stream);
 int alpx_decode_gqa_paged(const void* q, const void* key_pages, const void* value_pages,
                           const int32_t* block_table, int max_pages, int page_size,
                           int num_pages, const int32_t* seq_lens, int length, const void* gate,

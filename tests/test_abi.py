@@ -122,6 +122,18 @@ def test_layer_entry_points_validate_without_gpu(pkg):
                                      15, 2, 256, 256, 0, None, sec, 1e7, 1e-6, None)
     assert rc == L.EINVAL and "multiple of KV heads" in L.last_error()
     f9 = (fake,) * 9
+    rc = lib.alpx_prefill_causal_paged(fake, fake, fake, fake, 4, 32, 8, 0, None, fake, 8, 64,
+                                       8, 2, 128, 56, 0, 0, 0.0884, 2, None)
+    assert rc == L.EINVAL and "power of two" in L.last_error()
+    rc = lib.alpx_prefill_causal_paged(fake, fake, fake, fake, 4, 64, 8, 0, None, fake, 8, 264,
+                                       8, 2, 128, 256, 0, 0, 0.0884, 2, None)
+    assert rc == L.ERANGE and "exceeds capacity" in L.last_error()
+    rc = lib.alpx_prefill_causal_paged(fake, fake, fake, None, 4, 64, 8, 0, None, fake, 8, 64,
+                                       8, 2, 128, 56, 0, 0, 0.0884, 2, None)
+    assert rc == L.EINVAL and "null block table" in L.last_error()
+    rc = lib.alpx_prefill_causal_paged(fake, fake, fake, fake, 4, 64, 8, 0, None, fake, 8, 64,
+                                       8, 2, 128, 56, 0, 0, 0.0884, 0, None)
+    assert rc == L.EUNSUPPORTED and "paged" in L.last_error()
     rc = lib.alpx_attention_layer_step(*f9, 1 << 20, 2, 2, 64, 1, 16, 2, 256, 64, None, sec, 1e7,
                                        1e-6, 0.0625, None)
     assert rc == L.ERANGE and "exceeds capacity" in L.last_error()

@@ -356,12 +356,13 @@ def test_attention_layer_step_ragged_positions(gpu, ops, dtype, d, rows, bound):
     assert np.array_equal(got_k[mask], kc[mask])
 
 
-def test_attention_layer_step_decode_loop_in_a_graph(gpu, ops):
-    """A decode loop as one captured graph replayed per token: the step
-    reads device positions and inputs that the host refreshes between
-    replays (the split plan is sized for the whole cache).  Every replay
-    equals the eager step bit for bit, with eager work and synchronisation
-    between replays, and the caches end identical."""
+def test_layer_steps_decode_loop_in_a_graph(gpu, ops):
+    """A decode loop as one captured graph replayed per token: an attention
+    layer step (reading device positions) and a recurrent layer step, whose
+    inputs the host refreshes between replays (the attention split plan is
+    sized for the whole cache).  Every replay equals the eager steps bit for
+    bit, with eager work and synchronisation between replays, and the
+    caches and recurrent state end identical."""
     import torch
     g = torch.Generator(device=gpu).manual_seed(21)
     bf = torch.bfloat16
@@ -375,33 +376,62 @@ def test_attention_layer_step_decode_loop_in_a_graph(gpu, ops):
     qw = torch.rand((d,), generator=g, device=gpu) + 0.5
     kw = torch.rand((d,), generator=g, device=gpu) + 0.5
     pos = torch.tensor([5, 9], dtype=torch.int32, device=gpu)
+    hk, hv, dk, dv, kern = 4, 8, 64, 64, 4
+    chn = 2 * hk * dk + hv * dv
 
-    def step(K, V):
-        return ops.attention_layer_step_(qg, kn, vn, qw, kw, K, V, position=cap - 1,
-                                         positions=pos, **rope)[0]
+    def rec_ws():
+        return ops.initialize_recurrent_workspace(batch_size=b, convolution_kernel=kern,
+                                                  convolution_channels=chn, value_heads=hv,
+                                                  value_dimension=dv, key_dimension=dk)
+
+    wg = rec_ws()
+    wg.delta_state.copy_(torch.randn(wg.delta_state.shape, generator=g, device=gpu) * 0.1)
+    mixed = torch.zeros((b, chn), device=gpu)
+    cw = torch.randn((kern, chn), generator=g, device=gpu) * 0.5
+    rgate = torch.zeros((b, hv * dv), device=gpu)
+    bl = torch.zeros((b, hv), device=gpu)
+    al = torch.zeros((b, hv), device=gpu)
+    dt = torch.randn((hv,), generator=g, device=gpu)
+    ssm = -torch.exp(torch.rand((hv,), generator=g, device=gpu) * 2 - 1)
+    nw = torch.rand((dv,), generator=g, device=gpu) + 0.5
+
+    def step(K, V, w):
+        out = ops.attention_layer_step_(qg, kn, vn, qw, kw, K, V, position=cap - 1,
+                                        positions=pos, **rope)[0]
+        rec = ops.recurrent_layer_step_(w, mixed, cw, rgate, bl, al, dt, ssm, nw, key_heads=hk,
+                                        key_dimension=dk, epsilon=1e-6)
+        return out, rec
 
     side = torch.cuda.Stream(device=gpu)
     side.wait_stream(torch.cuda.current_stream(gpu))
     with torch.cuda.stream(side):
         for _ in range(2):
-            step(KG, VG)
+            step(KG, VG, wg)
     torch.cuda.current_stream(gpu).wait_stream(side)
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        out_g = step(KG, VG)
+        out_g, rec_g = step(KG, VG, wg)
     KE, VE = KG.clone(), VG.clone()
+    we = rec_ws()
+    we.delta_state.copy_(wg.delta_state)
+    we.convolution_history.copy_(wg.convolution_history)
     for i in range(6):
         pos.copy_(torch.tensor([10 + 17 * i, 40 + 3 * i], dtype=torch.int32))
         qg.copy_(torch.randn(qg.shape, generator=g, device=gpu) * 3)
         kn.copy_(torch.randn(kn.shape, generator=g, device=gpu) * 3)
         vn.copy_(torch.randn(vn.shape, generator=g, device=gpu))
+        for t in (mixed, rgate, bl, al):
+            t.copy_(torch.randn(t.shape, generator=g, device=gpu))
         graph.replay()
         torch.cuda.synchronize()
-        out_e = step(KE, VE)
+        out_e, rec_e = step(KE, VE, we)
         torch.cuda.synchronize()
         assert torch.equal(out_g.view(torch.int16), out_e.view(torch.int16)), i
+        assert torch.equal(rec_g, rec_e), i
     assert torch.equal(KG.view(torch.int16), KE.view(torch.int16))
     assert torch.equal(VG.view(torch.int16), VE.view(torch.int16))
+    assert torch.equal(wg.delta_state, we.delta_state)
+    assert torch.equal(wg.convolution_history, we.convolution_history)
 
 
 def test_attention_layer_step_fp32_runs_two_calls(gpu, ops):

@@ -134,3 +134,51 @@ def test_paged_append_one_token_per_sequence_and_bad_arguments(gpu, ops):
     q = torch.randn((batch, 4, d), device=gpu).to(torch.bfloat16)
     with pytest.raises(ValueError, match="capacity"):
         ops.paged_online_attention(q, pw.key_pages, pw.value_pages, table, length=129)
+
+
+@pytest.mark.parametrize("dtype,d,page,hq,hkv,tq,prefix,gated", [
+    ("bf16", 128, 64, 32, 8, 200, 300, False), ("f16", 256, 128, 16, 2, 130, 190, True),
+    ("bf16", 64, 256, 8, 2, 70, 0, False), ("bf16", 256, 64, 16, 2, 64, 448, True)])
+def test_paged_prefill_equals_contiguous_bit_for_bit(gpu, ops, dtype, d, page, hq, hkv, tq,
+                                                     prefix, gated):
+    """Causal prefill of one sequence's chunk over its pages (shuffled pool,
+    two sequences sharing it) returns the contiguous prefill's bytes, with
+    and without the sigmoid gate, and matches the oracle."""
+    import torch
+    rng = np.random.default_rng(d + tq + page)
+    batch = 2
+    cap = ((prefix + tq + page - 1) // page) * page
+    ws, pw, table, _ = _fill(torch, ops, gpu, rng, dtype, batch, cap, hkv, d, page, False)
+    td = _td(torch, dtype)
+    q = torch.from_numpy(I.round_to(rng.standard_normal((tq, hq, d)), dtype)
+                         .astype(np.float32)).to(gpu).to(td)
+    gate = None
+    if gated:
+        gate = torch.from_numpy(I.round_to(rng.standard_normal((tq, hq, d)) * 2, dtype)
+                                .astype(np.float32)).to(gpu).to(td)
+    for bi in range(batch):
+        ref = ops.attention_prefill(q, ws.key_cache, ws.value_cache, position=prefix,
+                                    batch_index=bi, gate=gate)
+        got = ops.paged_attention_prefill(q, pw.key_pages, pw.value_pages, table,
+                                          position=prefix, batch_index=bi, gate=gate)
+        torch.cuda.synchronize()
+        assert got.dtype == td and got.shape == (tq, hq, d)
+        assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), bi
+        K = ws.key_cache[:prefix + tq, bi].float().cpu().numpy()
+        V = ws.value_cache[:prefix + tq, bi].float().cpu().numpy()
+        expect = A.full_attention_prefill(q.float().cpu().numpy(), K, V, prefix_length=prefix)
+        if gated:
+            expect = expect / (1.0 + np.exp(-gate.float().cpu().numpy()))
+        assert np.abs(got.float().cpu().numpy() - expect).max() <= 2e-2
+
+
+def test_paged_prefill_rejects_unsupported(gpu, ops):
+    import torch
+    rng = np.random.default_rng(4)
+    ws, pw, table, _ = _fill(torch, ops, gpu, rng, "f32", 1, 128, 2, 64, 64, False)
+    q = torch.zeros((8, 4, 64), device=gpu)
+    L = importlib.import_module("alpacca-open-sourced-by-jt_amd._lib")
+    with pytest.raises(L.AlpxUnsupported):
+        ops.paged_attention_prefill(q, pw.key_pages, pw.value_pages, table, position=8)
+    with pytest.raises(ValueError):
+        ops.paged_attention_prefill(q, pw.key_pages, pw.value_pages, table, position=125)
