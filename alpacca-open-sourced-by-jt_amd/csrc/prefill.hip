@@ -342,22 +342,23 @@ prefill_mfma(PrefillArgs a) {
     __syncthreads();
   }
   // A tile starts at a multiple of BK and a page holds a multiple of BK
-  // rows, so a paged tile lies in one page, looked up once per tile.
+  // rows, so a paged tile lies in one page, looked up once per tile (when
+  // its K rows are loaded; its V rows reuse the number).
+  [[maybe_unused]] auto tile_page = [&](int t) -> int {
+    if constexpr (PAGED) {
+      const int pi = (lo + t * BK) >> a.page_shift;
+      if (pages_in_lds) return __builtin_amdgcn_readfirstlane(page_lds[pi - page0]);
+      const int pg = a.pages[pi];
+      return pg < 0 ? 0 : (pg >= a.num_pages ? a.num_pages - 1 : pg);
+    }
+    return 0;
+  };
   auto load_tile = [&](const T* g, int64_t pos, int64_t page_stride, const uint32_t (&ofs)[kIW],
-                       int t, int buf) {
+                       int t, int buf, int pg) {
     const int k0 = lo + t * BK;
     const T* base = g + (int64_t)k0 * pos;
-    if constexpr (PAGED) {
-      const int pi = k0 >> a.page_shift;
-      int pg;
-      if (pages_in_lds) {
-        pg = __builtin_amdgcn_readfirstlane(page_lds[pi - page0]);
-      } else {
-        pg = a.pages[pi];
-        pg = pg < 0 ? 0 : (pg >= a.num_pages ? a.num_pages - 1 : pg);
-      }
+    if constexpr (PAGED)
       base = g + (int64_t)pg * page_stride + (int64_t)(k0 & ((1 << a.page_shift) - 1)) * pos;
-    }
     const i32x4 r = rsrc_words(
         base, (uint32_t)((int64_t)(a.kv_tokens - k0) * pos * (int64_t)sizeof(T)));
     const uint32_t lds0 =
@@ -547,6 +548,10 @@ prefill_mfma(PrefillArgs a) {
     });
   };
 
+  // Paged: page of the K tile last loaded into buffer P (tile j + 2 - P's
+  // parity partner), reused for that tile's V load two iterations later.
+  int kpage[2] = {0, 0};
+
   // Iteration j: PV(j-1), softmax(j), QK(j+1) (tile indices), while the
   // direct loads of K(j+2) and V(j) land in the buffers iteration j-1 read.
   auto iteration = [&](auto par, int j) __attribute__((always_inline)) {
@@ -558,8 +563,12 @@ prefill_mfma(PrefillArgs a) {
     // iteration's first LDS read, which would also wait for the tile loads
     // issued below.  An explicit wait here clears its scoreboard for free.
     __builtin_amdgcn_s_waitcnt(0);
-    if (j + 2 < nt) load_tile(kg, a.ks_pos, a.ks_page, kofs, j + 2, P);
-    if (j < nt) load_tile(vg, a.vs_pos, a.vs_page, vofs, j, 2 + P);
+    const int v_page = kpage[P];  // page of tile j, looked up with K(j)
+    if (j + 2 < nt) {
+      if constexpr (PAGED) kpage[P] = tile_page(j + 2);
+      load_tile(kg, a.ks_pos, a.ks_page, kofs, j + 2, P, kpage[P]);
+    }
+    if (j < nt) load_tile(vg, a.vs_pos, a.vs_page, vofs, j, 2 + P, v_page);
     // Rescale for the m moved at tile j - 1 (O holds tiles <= j - 2 and is
     // about to take PV(j - 1), formed against the moved m; l was rescaled
     // at the move, before it took tile j - 1's P).
@@ -608,8 +617,14 @@ prefill_mfma(PrefillArgs a) {
   for (int kk = 0; kk < KK; ++kk)
 #pragma unroll
     for (int qb = 0; qb < NQB; ++qb) pv[1][kk][qb] = (V8){};
-  if (nt > 0) load_tile(kg, a.ks_pos, a.ks_page, kofs, 0, 0);
-  if (nt > 1) load_tile(kg, a.ks_pos, a.ks_page, kofs, 1, 1);
+  if (nt > 0) {
+    if constexpr (PAGED) kpage[0] = tile_page(0);
+    load_tile(kg, a.ks_pos, a.ks_page, kofs, 0, 0, kpage[0]);
+  }
+  if (nt > 1) {
+    if constexpr (PAGED) kpage[1] = tile_page(1);
+    load_tile(kg, a.ks_pos, a.ks_page, kofs, 1, 1, kpage[1]);
+  }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   qk_first();
