@@ -356,6 +356,25 @@ def test_attention_layer_step_ragged_positions(gpu, ops, dtype, d, rows, bound):
     assert np.array_equal(got_k[mask], kc[mask])
 
 
+def test_attention_layer_step_rejects_bad_positions(gpu, ops):
+    import torch
+    b, hq, hkv, d, cap = 2, 8, 2, 128, 64
+    z = lambda *shape: torch.zeros(shape, dtype=torch.bfloat16, device=gpu)  # noqa: E731
+    w = torch.ones(d, device=gpu)
+    args = (z(b, hq * 2 * d), z(b, hkv * d), z(b, hkv * d), w, w, z(cap, b, hkv, d),
+            z(cap, b, hkv, d))
+    rope = dict(sections=(11, 11, 10, 0), frequency_base=1e7, epsilon=1e-6)
+    with pytest.raises(ValueError, match="one row in"):
+        ops.attention_layer_step_(*args, position=20, positions=[3, 21], **rope)
+    with pytest.raises(ValueError, match="one row in"):
+        ops.attention_layer_step_(*args, position=20, positions=[3], **rope)
+    with pytest.raises(ValueError, match="one row per sequence"):
+        ops.attention_layer_step_(*args, position=20,
+                                  positions=torch.zeros(3, dtype=torch.int32, device=gpu), **rope)
+    with pytest.raises(ValueError, match="exceeds capacity"):
+        ops.attention_layer_step_(*args, position=cap, **rope)
+
+
 def test_layer_steps_decode_loop_in_a_graph(gpu, ops):
     """A decode loop as one captured graph replayed per token: an attention
     layer step (reading device positions) and a recurrent layer step, whose
