@@ -669,13 +669,14 @@ decode_split_generic(DecodeArgs a) {
 // query head for 64 output columns.  Wave w folds slots w, w+4, ... into an
 // online (m, l, acc) state; each group of four slots has its max, sum and
 // partial loads issued together (none depends on the running max), so the
-// kernel pays about one memory round trip.  The four wave states are then
-// merged through LDS by wave 0.
-template <typename T, typename TO>
+// kernel pays about one memory round trip.  The NW wave states are then
+// merged through LDS by wave 0.  With at most four slots (NW = 1) one wave
+// folds them all from a single group of loads, with no LDS merge.
+template <typename T, typename TO, int NW>
 __global__ void __launch_bounds__(256)
 decode_combine(DecodeArgs a) {
   constexpr int kGroup = 4;
-  __shared__ float red[3][kWaves - 1][64];
+  __shared__ float red[3][NW > 1 ? NW - 1 : 1][64];
   const int64_t bh = blockIdx.x;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -687,11 +688,11 @@ decode_combine(DecodeArgs a) {
   const float* pl = a.part_l + bh * ns;
   const float* pa = a.part_acc + bh * ns * DV + dc;
   float m = -INFINITY, l = 0.f, acc = 0.f;
-  for (int s0 = wave; s0 < ns; s0 += kGroup * kWaves) {
+  for (int s0 = wave; s0 < ns; s0 += kGroup * NW) {
     float xm[kGroup], xl[kGroup], xa[kGroup];
 #pragma unroll
     for (int u = 0; u < kGroup; ++u) {
-      const int s = s0 + u * kWaves;
+      const int s = s0 + u * NW;
       const bool ok = s < ns;
       xm[u] = ok ? pm[s] : -INFINITY;
       xl[u] = ok ? pl[s] : 0.f;
@@ -708,23 +709,25 @@ decode_combine(DecodeArgs a) {
       m = mn;
     }
   }
-  if (wave > 0) {
-    red[0][wave - 1][lane] = m;
-    red[1][wave - 1][lane] = l;
-    red[2][wave - 1][lane] = acc;
+  if constexpr (NW > 1) {
+    if (wave > 0) {
+      red[0][wave - 1][lane] = m;
+      red[1][wave - 1][lane] = l;
+      red[2][wave - 1][lane] = acc;
+    }
+    __syncthreads();
   }
-  __syncthreads();
   if (wave != 0 || d >= DV) return;
   float M = m;
 #pragma unroll
-  for (int w = 0; w < kWaves - 1; ++w) M = fmaxf(M, red[0][w][lane]);
+  for (int w = 0; w < NW - 1; ++w) M = fmaxf(M, red[0][w][lane]);
   float L = 0.f, A = 0.f;
   if (M != -INFINITY) {
     const float c0 = fast_exp2(m - M);
     L = l * c0;
     A = acc * c0;
 #pragma unroll
-    for (int w = 0; w < kWaves - 1; ++w) {
+    for (int w = 0; w < NW - 1; ++w) {
       const float cw = fast_exp2(red[0][w][lane] - M);
       L += red[1][w][lane] * cw;
       A += red[2][w][lane] * cw;
@@ -822,20 +825,22 @@ const void* split_kernel(bool mfma, bool paged, int D) {
   return (const void*)decode_split_generic<T>;
 }
 
+template <typename T, int NW>
+void launch_combine_nw(int out_dtype, const DecodeArgs& a, hipStream_t s) {
+  const dim3 grid(a.batch * a.q_heads, (a.value_dim + 63) / 64), block(64 * NW);
+  switch (out_dtype) {
+    case ALPX_F32: hipLaunchKernelGGL((decode_combine<T, float, NW>), grid, block, 0, s, a); break;
+    case ALPX_F16: hipLaunchKernelGGL((decode_combine<T, f16_t, NW>), grid, block, 0, s, a); break;
+    default: hipLaunchKernelGGL((decode_combine<T, bf16_t, NW>), grid, block, 0, s, a); break;
+  }
+}
+
 template <typename T>
 int launch_combine(int out_dtype, const DecodeArgs& a, hipStream_t s) {
-  dim3 grid(a.batch * a.q_heads, (a.value_dim + 63) / 64);
-  switch (out_dtype) {
-    case ALPX_F32:
-      hipLaunchKernelGGL((decode_combine<T, float>), grid, dim3(256), 0, s, a);
-      break;
-    case ALPX_F16:
-      hipLaunchKernelGGL((decode_combine<T, f16_t>), grid, dim3(256), 0, s, a);
-      break;
-    default:
-      hipLaunchKernelGGL((decode_combine<T, bf16_t>), grid, dim3(256), 0, s, a);
-      break;
-  }
+  if (a.nsplit <= 4)
+    launch_combine_nw<T, 1>(out_dtype, a, s);
+  else
+    launch_combine_nw<T, kWaves>(out_dtype, a, s);
   return check_launch("decode_combine");
 }
 
