@@ -44,6 +44,10 @@ SIGNATURES = {
                                  _c_ptr, _c_size, _c_int, _c_int, _c_int, _c_int, _c_int,
                                  _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_float,
                                  _c_int, _c_int, _c_ptr]),
+    "alpx_decode_gqa_noalloc": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr,
+                                         _c_int, _c_int, _c_int, _c_int, _c_int, _c_i64, _c_i64,
+                                         _c_i64, _c_i64, _c_i64, _c_i64, _c_float, _c_int,
+                                         _c_int, _c_ptr]),
     "alpx_sigmoid_gate": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_i64, _c_int, _c_int, _c_ptr]),
     "alpx_prefill_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int]),
     "alpx_prefill_causal": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_size, _c_int,
@@ -207,15 +211,29 @@ def stream_handle(torch, device) -> int:
 
 
 _workspaces: dict = {}
+# Workspaces replaced by a larger one stay allocated until the process ends:
+# a HIP graph captured while one of them was current keeps its address in
+# its kernel arguments, and replays of that graph still write there.  Were
+# the buffer returned to torch's caching allocator, those replays would
+# overwrite whatever tensor torch handed the memory to next.  Each retired
+# buffer is smaller than its successor, so at most about as much again as
+# the largest workspace is held.
+_retired: dict = {}
 
 
 def workspace(torch, device, nbytes: int):
     """A grow-only scratch workspace per device, owned by this module.
     Calls that share it are ordered on one stream (the reference's
-    one-caller-at-a-time contract, serve.py:326)."""
+    one-caller-at-a-time contract, serve.py:326).  A graph that captures a
+    call keeps using the workspace that was current at capture time, so
+    graphs should be captured after the largest workspace a process needs
+    has been sized (one eager call of each shape), though a later growth
+    never frees the buffer a graph holds."""
     key = str(device)
     buf = _workspaces.get(key)
     if buf is None or buf.numel() < nbytes:
+        if buf is not None:
+            _retired.setdefault(key, []).append(buf)
         buf = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device)
         _workspaces[key] = buf
     return buf

@@ -29,6 +29,8 @@
 // and invalidate the XCD L2 in every block.)
 #include <math.h>
 
+#include <mutex>
+
 #include "alpx_common.h"
 #include "decode_internal.h"
 #include "rope_internal.h"
@@ -874,7 +876,8 @@ size_t decode_workspace(int batch, int q_heads, int kv_heads, int value_dim, int
 }
 
 int run_decode(DecodeArgs a, int dtype, int out_dtype, void* workspace, size_t workspace_bytes,
-               hipStream_t s, int split_timer, int combine_timer, const SplitPrologue* pro) {
+               hipStream_t s, int split_timer, int combine_timer, const SplitPrologue* pro,
+               const char* fixed_scratch) {
   const size_t es = dtype_size(dtype);
   const uintptr_t align = (uintptr_t)a.q | (uintptr_t)a.k | (uintptr_t)a.v |
                           (uintptr_t)(a.ks_pos * es) | (uintptr_t)(a.ks_b * es) |
@@ -888,7 +891,7 @@ int run_decode(DecodeArgs a, int dtype, int out_dtype, void* workspace, size_t w
                     (int64_t)kTile * max_pos * (int64_t)es < ((int64_t)1 << 31) &&
                     getenv("ALPX_DECODE_GENERIC") == nullptr;
   const size_t need = decode_workspace(a.batch, a.q_heads, a.kv_heads, a.value_dim, a.length);
-  if (workspace_bytes < need)
+  if (fixed_scratch == nullptr && workspace_bytes < need)
     return fail(ALPX_EINVAL, "decode workspace holds %zu bytes, needs %zu", workspace_bytes,
                 need);
   const void* kernel = nullptr;
@@ -918,6 +921,13 @@ int run_decode(DecodeArgs a, int dtype, int out_dtype, void* workspace, size_t w
   const Plan p = plan_split(a.batch * a.kv_heads * a.head_chunks, a.length,
                             resident_blocks(kernel, mfma ? 256 : 64, 0), unit);
   const size_t n = (size_t)a.batch * a.q_heads * p.nsplit;
+  if (fixed_scratch != nullptr && workspace_for(a.batch, a.q_heads, a.value_dim, p.nsplit) >
+                                      workspace_bytes)
+    return fail(ALPX_ERANGE,
+                "%s: this call needs %zu bytes of split partials, more than the %zu-byte static "
+                "scratch (call the entry point that takes a workspace)",
+                fixed_scratch, workspace_for(a.batch, a.q_heads, a.value_dim, p.nsplit),
+                workspace_bytes);
   char* ws = (char*)workspace;
   a.part_m = (float*)ws;
   a.part_l = (float*)(ws + align256(n * sizeof(float)));
@@ -941,28 +951,80 @@ int run_decode(DecodeArgs a, int dtype, int out_dtype, void* workspace, size_t w
 
 }  // namespace alpx
 
-extern "C" int alpx_decode_gqa(const void* q, const void* key_cache, const void* value_cache,
-                               const int32_t* seq_lens, int length, const void* gate, void* out,
-                               void* workspace, size_t workspace_bytes, int batch, int q_heads,
-                               int kv_heads, int key_dim, int value_dim, int64_t k_pos_stride,
-                               int64_t k_batch_stride, int64_t k_head_stride,
-                               int64_t v_pos_stride, int64_t v_batch_stride,
-                               int64_t v_head_stride, float scale, int dtype, int out_dtype,
-                               void* stream) {
-  using namespace alpx;
-  if (!q || !key_cache || !value_cache || !out || !workspace)
-    return fail(ALPX_EINVAL, "alpx_decode_gqa: null buffer");
-  if (!dtype_ok(dtype) || !dtype_ok(out_dtype))
-    return fail(ALPX_EINVAL, "alpx_decode_gqa: unknown dtype");
+namespace alpx {
+namespace {
+
+// ------------------------------------------------------------ static scratch
+
+// Split partials of alpx_decode_gqa_noalloc.  Each GPU the library runs on
+// holds its own copy of this array from the module's load until the process
+// ends.  In host code `scratch` only names the symbol: its device address
+// (one per GPU) comes from hipGetSymbolAddress, looked up once per device
+// and kept in g_scratch_ptr.  Every split block writes its partial slot
+// (an empty chunk writes m = -inf, l = 0, acc = 0) before the combine reads
+// it, so nothing in the array has to start at zero and the previous call's
+// contents never leak into a result.  Calls on one GPU share the array:
+// calls that overlap in time on one GPU (different streams, no ordering)
+// race on it.
+static __device__ __align__(256) unsigned char scratch[ALPX_DECODE_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+
+// Device address of `scratch` on the device that runs `stream` (the current
+// device for the null stream).
+int scratch_address(hipStream_t stream, void** out) {
+  int current = 0;
+  hipError_t err = hipGetDevice(&current);
+  if (err != hipSuccess) return fail(ALPX_EHIP, "hipGetDevice: %s", hipGetErrorString(err));
+  int device = current;
+  if (stream != nullptr) {
+    err = hipStreamGetDevice(stream, &device);
+    if (err != hipSuccess)
+      return fail(ALPX_EHIP, "hipStreamGetDevice: %s", hipGetErrorString(err));
+  }
+  if (device < 0 || device >= kMaxDevices)
+    return fail(ALPX_EUNSUPPORTED, "device %d is beyond the %d this library tracks", device,
+                kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[device] == nullptr) {
+    // the symbol lookup resolves on the current device: make it `device`
+    if (device != current && (err = hipSetDevice(device)) != hipSuccess)
+      return fail(ALPX_EHIP, "hipSetDevice(%d): %s", device, hipGetErrorString(err));
+    void* ptr = nullptr;
+    err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (device != current) (void)hipSetDevice(current);
+    if (err != hipSuccess || ptr == nullptr)
+      return fail(ALPX_EHIP, "hipGetSymbolAddress(scratch) on device %d: %s", device,
+                  hipGetErrorString(err));
+    g_scratch_ptr[device] = ptr;
+  }
+  *out = g_scratch_ptr[device];
+  return ALPX_OK;
+}
+
+// Validates and runs one contiguous-cache decode on `workspace`
+// (fixed_scratch: see run_decode).
+int decode_gqa(const char* who, const void* q, const void* key_cache, const void* value_cache,
+               const int32_t* seq_lens, int length, const void* gate, void* out, void* workspace,
+               size_t workspace_bytes, int batch, int q_heads, int kv_heads, int key_dim,
+               int value_dim, int64_t k_pos_stride, int64_t k_batch_stride,
+               int64_t k_head_stride, int64_t v_pos_stride, int64_t v_batch_stride,
+               int64_t v_head_stride, float scale, int dtype, int out_dtype, hipStream_t stream,
+               const char* fixed_scratch) {
+  if (!q || !key_cache || !value_cache || !out || (!workspace && !fixed_scratch))
+    return fail(ALPX_EINVAL, "%s: null buffer", who);
+  if (!dtype_ok(dtype) || !dtype_ok(out_dtype)) return fail(ALPX_EINVAL, "%s: unknown dtype", who);
   if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || key_dim <= 0 || value_dim <= 0)
-    return fail(ALPX_EINVAL, "alpx_decode_gqa: sizes must be positive");
+    return fail(ALPX_EINVAL, "%s: sizes must be positive", who);
   if (length <= 0) return fail(ALPX_EINVAL, "attention cache length must be a positive integer");
   if (q_heads % kv_heads != 0)
     return fail(ALPX_EINVAL, "attention query heads must be a multiple of KV heads");
   if (!(scale > 0.0f) || !isfinite(scale))
     return fail(ALPX_EINVAL, "attention scale must be positive and finite");
   if (key_dim > 256 || value_dim > 256)
-    return fail(ALPX_EUNSUPPORTED, "alpx_decode_gqa: head dims above 256 are not supported");
+    return fail(ALPX_EUNSUPPORTED, "%s: head dims above 256 are not supported", who);
   DecodeArgs a = {};
   a.q = q;
   a.k = key_cache;
@@ -987,8 +1049,47 @@ extern "C" int alpx_decode_gqa(const void* q, const void* key_cache, const void*
   a.key_dim = key_dim;
   a.value_dim = value_dim;
   a.scale_log2 = scale * kLog2e;
-  return run_decode(a, dtype, out_dtype, workspace, workspace_bytes, (hipStream_t)stream,
-                    ALPX_T_DECODE, ALPX_T_DECODE_COMBINE);
+  if (fixed_scratch != nullptr) {
+    const int rc = scratch_address(stream, &workspace);
+    if (rc != ALPX_OK) return rc;
+    workspace_bytes = ALPX_DECODE_SCRATCH_BYTES;
+  }
+  return run_decode(a, dtype, out_dtype, workspace, workspace_bytes, stream, ALPX_T_DECODE,
+                    ALPX_T_DECODE_COMBINE, nullptr, fixed_scratch);
+}
+
+}  // namespace
+}  // namespace alpx
+
+extern "C" int alpx_decode_gqa(const void* q, const void* key_cache, const void* value_cache,
+                               const int32_t* seq_lens, int length, const void* gate, void* out,
+                               void* workspace, size_t workspace_bytes, int batch, int q_heads,
+                               int kv_heads, int key_dim, int value_dim, int64_t k_pos_stride,
+                               int64_t k_batch_stride, int64_t k_head_stride,
+                               int64_t v_pos_stride, int64_t v_batch_stride,
+                               int64_t v_head_stride, float scale, int dtype, int out_dtype,
+                               void* stream) {
+  return alpx::decode_gqa("alpx_decode_gqa", q, key_cache, value_cache, seq_lens, length, gate,
+                          out, workspace, workspace_bytes, batch, q_heads, kv_heads, key_dim,
+                          value_dim, k_pos_stride, k_batch_stride, k_head_stride, v_pos_stride,
+                          v_batch_stride, v_head_stride, scale, dtype, out_dtype,
+                          (hipStream_t)stream, nullptr);
+}
+
+extern "C" int alpx_decode_gqa_noalloc(const void* q, const void* key_cache,
+                                       const void* value_cache, const int32_t* seq_lens,
+                                       int length, const void* gate, void* out, int batch,
+                                       int q_heads, int kv_heads, int key_dim, int value_dim,
+                                       int64_t k_pos_stride, int64_t k_batch_stride,
+                                       int64_t k_head_stride, int64_t v_pos_stride,
+                                       int64_t v_batch_stride, int64_t v_head_stride,
+                                       float scale, int dtype, int out_dtype, void* stream) {
+  using namespace alpx;
+  return decode_gqa("alpx_decode_gqa_noalloc", q, key_cache, value_cache, seq_lens, length, gate,
+                    out, nullptr, 0, batch, q_heads, kv_heads, key_dim,
+                    value_dim, k_pos_stride, k_batch_stride, k_head_stride, v_pos_stride,
+                    v_batch_stride, v_head_stride, scale, dtype, out_dtype, (hipStream_t)stream,
+                    "alpx_decode_gqa_noalloc");
 }
 
 extern "C" int alpx_decode_gqa_paged(const void* q, const void* key_pages,

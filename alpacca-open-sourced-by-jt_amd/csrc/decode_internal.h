@@ -64,9 +64,13 @@ size_t decode_workspace(int batch, int q_heads, int kv_heads, int value_dim, int
 
 // Plans and launches split + combine for fully described args (pointers,
 // strides, sizes, causal fields, scale_log2); fills the partial pointers,
-// nsplit and chunk.  Validation is the caller's job.
+// nsplit and chunk.  Validation is the caller's job.  A caller-owned
+// workspace must hold decode_workspace() bytes (the device-independent
+// bound); with `fixed_scratch` (the entry point's name) the workspace is a
+// fixed-size static array and only the bytes of the plan actually chosen
+// must fit.
 int run_decode(DecodeArgs a, int dtype, int out_dtype, void* workspace, size_t workspace_bytes,
                hipStream_t stream, int split_timer, int combine_timer,
-               const SplitPrologue* pro = nullptr);
+               const SplitPrologue* pro = nullptr, const char* fixed_scratch = nullptr);
 
 }  // namespace alpx

@@ -180,6 +180,33 @@ int alpx_decode_gqa(const void* q, const void* key_cache, const void* value_cach
                     int64_t v_batch_stride, int64_t v_head_stride, float scale, int dtype,
                     int out_dtype, void* stream);
 
+/* Bytes of the static scratch array alpx_decode_gqa_noalloc keeps on each
+ * GPU (16 MiB). */
+#define ALPX_DECODE_SCRATCH_BYTES ((size_t)16 << 20)
+
+/*
+ * alpx_decode_gqa without a workspace argument and without any allocation.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments (minus workspace),
+ * kernels, split plan and result (bit for bit) as alpx_decode_gqa.  The
+ * split partials live in a static device array of
+ * ALPX_DECODE_SCRATCH_BYTES per GPU, held from the library's load until
+ * the process ends; its address on each device is looked up on the first
+ * call there.  A call whose split plan needs more partial bytes than that
+ * (many sequences x query heads x splits) fails with ALPX_ERANGE before
+ * anything is enqueued; use alpx_decode_gqa then.  Every call on one GPU
+ * shares the array, so calls that overlap on one GPU (unordered streams)
+ * race; calls ordered on one stream are safe.  Nothing in the array needs
+ * initial contents.
+ */
+int alpx_decode_gqa_noalloc(const void* q, const void* key_cache, const void* value_cache,
+                            const int32_t* seq_lens, int length, const void* gate, void* out,
+                            int batch, int q_heads, int kv_heads, int key_dim, int value_dim,
+                            int64_t k_pos_stride, int64_t k_batch_stride, int64_t k_head_stride,
+                            int64_t v_pos_stride, int64_t v_batch_stride, int64_t v_head_stride,
+                            float scale, int dtype, int out_dtype, void* stream);
+
 /*
  * Workspace bytes alpx_prefill_causal may need (only its fallback path, for
  * fp32 or unsupported shapes, uses it).

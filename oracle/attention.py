@@ -41,13 +41,6 @@ def attention_append(key_cache, value_cache, position, key, value):
     return position + 1
 
 
-def cache_write_rows(cache, pos0, rows):
-    """Llama-class prefill cache write ``cache[pos0:pos0+n] = rows``
-    (model.py:1335-1337; decode form model.py:1431-1432 with n = 1)."""
-    cache[pos0:pos0 + len(rows)] = rows
-    return cache
-
-
 def ragged_append(key_cache, value_cache, positions, key, value):
     """Per-sequence append for a ragged batch: sequence ``b`` writes its
     ``key[t, b]`` rows at ``positions[b] + t`` of cache ``[C, B, Hkv, D]``.

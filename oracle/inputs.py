@@ -51,19 +51,6 @@ def round_to(x, dtype):
     raise ValueError(f"unknown dtype {dtype!r}")
 
 
-def storage(x, dtype):
-    """The array as it is stored in memory for ``dtype``: float32, float16,
-    or uint16 bf16 bit patterns."""
-    x = np.asarray(x, dtype=np.float32)
-    if dtype == "f32":
-        return np.ascontiguousarray(x)
-    if dtype == "f16":
-        return np.ascontiguousarray(x.astype(np.float16))
-    if dtype == "bf16":
-        return np.ascontiguousarray(f32_to_bf16_bits(x))
-    raise ValueError(f"unknown dtype {dtype!r}")
-
-
 def _normal(rng, shape):
     return rng.standard_normal(size=shape, dtype=np.float32)
 

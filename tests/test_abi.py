@@ -42,6 +42,14 @@ def test_null_buffers_rejected_without_gpu(pkg):
     assert rc == pkg._lib.EINVAL
     with pytest.raises(ValueError):
         pkg._lib.check(rc)
+    # the allocation-free variant validates before it looks up its scratch
+    rc = lib.alpx_decode_gqa_noalloc(None, None, None, None, 4, None, None, 1, 4, 2, 64, 64,
+                                     128, 0, 64, 128, 0, 64, 0.125, 0, 0, None)
+    assert rc == pkg._lib.EINVAL and "null" in pkg._lib.last_error()
+    fake = ctypes.c_void_p(256)  # never dereferenced: validation fails first
+    rc = lib.alpx_decode_gqa_noalloc(fake, fake, fake, None, 4, None, fake, 1, 6, 4, 64, 64,
+                                     256, 0, 64, 256, 0, 64, 0.125, 1, 1, None)
+    assert rc == pkg._lib.EINVAL and "multiple of KV heads" in pkg._lib.last_error()
 
 
 def test_gated_prefill_rejects_null_gate_without_gpu(pkg):

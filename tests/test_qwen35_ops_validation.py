@@ -1,0 +1,69 @@
+"""CPU checks of the ``qwen35_ops`` drop-in's contract validation: the same
+exception types and messages as the reference (qwen35_ops.py:318-345,
+381-390, 436-460), raised before any device work (no GPU needed)."""
+
+import importlib
+
+import pytest
+
+
+@pytest.fixture(scope="module")
+def q35():
+    return importlib.import_module("alpacca-open-sourced-by-jt_amd.qwen35_ops")
+
+
+S = [[0.0, 0.0], [0.0, 0.0], [0.0, 0.0]]  # [value 3][key 2]
+
+
+@pytest.mark.parametrize("beta", [-0.1, 1.5, float("nan"), float("inf")])
+def test_gdn_step_rejects_beta_outside_unit_interval(q35, beta):
+    with pytest.raises(ValueError, match=r"beta must be finite and in \[0, 1\]"):
+        q35.gated_delta_net_step(S, [1, 0], [1, 0], [1, 2, 3], beta=beta, log_decay=0.0)
+
+
+@pytest.mark.parametrize("g", [0.01, float("nan"), float("-inf")])
+def test_gdn_step_rejects_positive_or_nonfinite_log_decay(q35, g):
+    with pytest.raises(ValueError, match="log_decay must be finite and non-positive"):
+        q35.gated_delta_net_step(S, [1, 0], [1, 0], [1, 2, 3], beta=0.5, log_decay=g)
+
+
+def test_gdn_step_shape_errors(q35):
+    with pytest.raises(ValueError, match="nonzero value and key dimensions"):
+        q35.gated_delta_net_step([], [1], [1], [1], beta=0.5, log_decay=0.0)
+    with pytest.raises(ValueError, match="same key dimension"):
+        q35.gated_delta_net_step([[0, 0], [0]], [1, 0], [1, 0], [1, 2], beta=0.5, log_decay=0.0)
+    with pytest.raises(ValueError, match="query/key lengths"):
+        q35.gated_delta_net_step(S, [1, 0, 0], [1, 0], [1, 2, 3], beta=0.5, log_decay=0.0)
+    with pytest.raises(ValueError, match="value length"):
+        q35.gated_delta_net_step(S, [1, 0], [1, 0], [1, 2], beta=0.5, log_decay=0.0)
+
+
+def test_gdn_scan_checks_token_axis_and_every_token(q35):
+    with pytest.raises(ValueError, match="token-axis lengths must agree"):
+        q35.gated_delta_net_scan(S, [[1, 0]], [[1, 0]], [[1, 2, 3]], [0.5, 0.5], [0.0])
+    # a bad beta on the last token raises the step's error
+    with pytest.raises(ValueError, match=r"beta must be finite and in \[0, 1\]"):
+        q35.gated_delta_net_scan(S, [[1, 0]] * 2, [[1, 0]] * 2, [[1, 2, 3]] * 2, [0.5, 2.0],
+                                 [0.0, 0.0])
+
+
+def test_causal_gqa_step_validation(q35):
+    q = [[1.0, 0.0]] * 4
+    K = [[[1.0, 0.0]] * 2] * 3
+    V = [[[1.0]] * 2] * 3
+    with pytest.raises(ValueError, match="equal nonempty K/V caches"):
+        q35.causal_gqa_step(q, K, V[:2])
+    with pytest.raises(ValueError, match="equal nonempty K/V caches"):
+        q35.causal_gqa_step([], K, V)
+    with pytest.raises(ValueError, match="multiple of KV heads"):
+        q35.causal_gqa_step(q[:3], K, V)
+    with pytest.raises(ValueError, match="same KV head count"):
+        q35.causal_gqa_step(q, K[:2] + [[[1.0, 0.0]]], V)
+    with pytest.raises(ValueError, match="query heads must be nonempty and equally sized"):
+        q35.causal_gqa_step([[1.0, 0.0]] * 3 + [[1.0]], K, V)
+    with pytest.raises(ValueError, match="key heads must match"):
+        q35.causal_gqa_step(q, [[[1.0, 0.0, 0.0]] * 2] * 3, V)
+    with pytest.raises(ValueError, match="value heads must be nonempty"):
+        q35.causal_gqa_step(q, K, [[[1.0]] * 2] * 2 + [[[1.0, 2.0]] * 2])
+    with pytest.raises(ValueError, match="scale must be positive and finite"):
+        q35.causal_gqa_step(q, K, V, scale=0.0)
