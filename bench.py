@@ -1,16 +1,29 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X attention path; prints ONE JSON line.
 
-Headline (``value``): GQA decode attention at 8K context -- BASELINE config
-C2, uniform-8192 variant: 16 sequences x 8192 cached rows, 32 query / 8 KV
-heads, head_dim 128, fp16 cache in the ROCm layout [8192, 16, 8, 128] --
-reported as algorithmic HBM GB/s (K + V bytes of every valid row, plus q and
-o) per decode step, whole step (split + combine) timed.  ``roofline`` covers
-the dominant kernel (the split-K pass), timed with HIP events recorded by
-the library on its launch stream over the timed region.  ``extra`` carries
-the other configs (C1 fp32 decode, C4 gated bf16 decode, ...).
-``cpu_baseline`` times the NumPy oracle (the reference's two-pass llama
-algorithm, fp32) on the same C2 workload on this host.
+Headline (``value``): GQA decode attention at 8K context -- config C2,
+uniform-8192 variant: 16 sequences x 8192 cached rows, 32 query / 8 KV heads,
+head_dim 128, fp16 cache in the ROCm layout [8192, 16, 8, 128] -- reported as
+algorithmic HBM GB/s (K + V bytes of every valid row, plus q and o) per
+decode step, whole step (split + combine) timed.  ``roofline`` covers the
+dominant kernel (the split-K pass), timed with HIP events recorded by the
+library on its launch stream over the timed region.  ``cpu_baseline`` times
+the NumPy oracle (the reference's two-pass llama algorithm, fp32) on the
+same workload on this host.
+
+``extra`` carries every other config, each with its own ``roofline`` block
+(dominant kernel, algorithmic work per launch / HIP-event average) and its
+own ``cpu_baseline`` (the reference algorithm the config names, restated in
+NumPy, timed on a bounded sample on this host):
+
+* C2 ragged: lengths ``rng(2).integers(1024, 8193, 16)``, GB/s of valid rows;
+* C1: fp32 decode, 32/8 heads, head_dim 64, 512 rows;
+* C3: the 2048 new rows appended to a 2048-row bf16 cache, then causal
+  prefill over 4096 positions (append + prefill is the timed step);
+* C4: Qwen3.5 gated decode, 4 x 32768 bf16 rows, 16/2 heads, head_dim 256;
+* C5: gated delta rule, 1024-token chunked prefill + 256 decode steps;
+* the Qwen3.5 layer steps around the kernels, eager and replayed from a
+  captured HIP graph (the way a decode loop runs them).
 
 ``roofline.traffic`` (HBM bytes per split launch) comes from two rocprofv3
 counter runs of ``bench.py --pmc-probe`` (FETCH_SIZE, then WRITE_SIZE), each
@@ -51,6 +64,8 @@ def _mod(name):
     return importlib.import_module(f"{PACKAGE}.{name}")
 
 
+# ------------------------------------------------------------ timing helpers
+
 def _timed_steps(torch, fn, steps, warmup):
     for _ in range(warmup):
         fn()
@@ -62,36 +77,162 @@ def _timed_steps(torch, fn, steps, warmup):
     return (time.perf_counter() - t0) / steps * 1e3
 
 
-def _kernel_avg_ms(lib, kernel):
-    total, count = lib.timing_read(kernel)
-    return (total / count) if count else float("nan")
+GRAPH_CALLS = 32  # calls captured per graph: one graph launch per 32 decode steps
 
+
+def _graph_replay_ms(torch, fn, steps, warmup):
+    """Host-timed ms per call when ``GRAPH_CALLS`` consecutive calls of
+    ``fn`` are captured in one graph and the graph is replayed, as a decode
+    loop does (inputs in fixed device buffers; one graph launch per
+    ``GRAPH_CALLS`` steps, since one HIP graph launch costs more than one
+    kernel launch)."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(GRAPH_CALLS):
+            fn()
+    replays = max(1, steps // GRAPH_CALLS)
+    for _ in range(max(1, warmup // GRAPH_CALLS)):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(replays):
+        graph.replay()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) / (replays * GRAPH_CALLS) * 1e3
+    del graph
+    return ms
+
+
+def _event_kernel_ms(torch, lib, fn, steps, kernels):
+    """Average HIP-event duration (ms) of each library kernel id in
+    ``kernels`` over ``steps`` calls of ``fn`` (events recorded by the
+    library on the launch stream)."""
+    lib.timing_enable(True)
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    out = []
+    for k in kernels:
+        total, count = lib.timing_read(k)
+        out.append(total / count if count else float("nan"))
+    lib.timing_enable(False)
+    return out
+
+
+def _roofline(kernel, bound, work, ms, *, peak=None, traffic=None, work_name="bytes"):
+    """Roofline block: ``work`` algorithmic bytes (hbm) or FLOPs (mfma) per
+    launch over the kernel's average launch duration ``ms``."""
+    if bound == "hbm":
+        achieved, unit, peak = work / (ms * 1e-3) / 1e9, "GB/s", peak or HBM_PEAK_GBS
+    else:
+        achieved, unit, peak = work / (ms * 1e-3) / 1e12, "TFLOP/s", peak or BF16_PEAK_TFLOPS
+    return {"kernel": kernel, "bound": bound, "achieved": round(achieved, 1), "peak": peak,
+            "unit": unit, "frac": round(achieved / peak, 4), "traffic": traffic,
+            "avg_launch_ms": round(ms, 5), f"alg_{work_name}_per_launch": work}
+
+
+# ------------------------------------------------------------ CPU baselines
+
+def _host_info():
+    cores = len(os.sched_getaffinity(0))
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    blas = None
+    try:
+        from threadpoolctl import threadpool_info
+        info = [i for i in threadpool_info() if i.get("user_api") == "blas"]
+        if info:
+            blas = {"library": info[0].get("internal_api"),
+                    "threads": max(int(i.get("num_threads", 1)) for i in info)}
+    except Exception:  # pragma: no cover - depends on the image
+        pass
+    return {"cpu_model": model, "affinity_cores": cores, "blas": blas}
+
+
+def _blas_threads(host):
+    return host["blas"]["threads"] if host.get("blas") else 1
+
+
+def _median_runs(fn, budget_s, min_runs=3, max_runs=50):
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < min_runs or (time.perf_counter() - t_start < budget_s
+                                    and len(times) < max_runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+def cpu_decode_twopass(q, K, V, hkv, d, storage_bytes, label, host, budget_s):
+    """The reference's two-pass llama decode (model.py:1246-1252) in fp32
+    over per-sequence contiguous ``(t, n_kv, hd)`` caches (the llama
+    layout).  GB/s counts the workload's K/V bytes at its storage size."""
+    import numpy as np
+    from oracle import attention as A
+    qh = q.float().cpu().numpy()
+    lens = [int(k.shape[0]) for k in K]
+    Kh = [np.ascontiguousarray(k.float().cpu().numpy()) for k in K]
+    Vh = [np.ascontiguousarray(v.float().cpu().numpy()) for v in V]
+    group = qh.shape[1] // hkv
+    scale = 1.0 / math.sqrt(d)
+
+    def step():
+        for b in range(len(Kh)):
+            A.attention_decode_twopass(qh[b], Kh[b], Vh[b], group, scale, acc=np.float32)
+
+    step_s, runs = _median_runs(step, budget_s)
+    step_bytes = 2 * sum(lens) * hkv * d * storage_bytes + 2 * qh.size * storage_bytes
+    return {"value": round(step_bytes / step_s / 1e9, 3), "unit": "GB/s",
+            "cores": _blas_threads(host), "kind": "port",
+            "ms_per_step": round(step_s * 1e3, 3),
+            "sample": f"{label}, NumPy two-pass fp32 oracle (model.py:1246-1252), "
+                      f"median of {runs} runs"}
+
+
+# ------------------------------------------------------------ GPU workloads
 
 def bench_decode(torch, ops, lib, *, batch, ctx, hq, hkv, d, dtype, gate, steps, warmup,
-                 seed):
+                 seed, seq_lens=None, graph=False):
+    """One decode config: eager step time, HIP-event split / combine
+    durations, and (``graph``) the per-replay time of a captured step.
+    Algorithmic bytes count K + V of every valid row (``seq_lens`` or
+    ``ctx`` per sequence) plus q (and gate) in and o out."""
     g = torch.Generator(device="cuda").manual_seed(seed)
     dev = torch.device("cuda")
     q = torch.randn((batch, hq, d), generator=g, device=dev).to(dtype)
     K = torch.randn((ctx, batch, hkv, d), generator=g, device=dev).to(dtype)
     V = torch.randn((ctx, batch, hkv, d), generator=g, device=dev).to(dtype)
     gt = torch.randn((batch, hq, d), generator=g, device=dev).to(dtype) if gate else None
-    fn = lambda: ops.online_attention(q, K, V, length=ctx, gate=gt)  # noqa: E731
+    lens_dev = None
+    if seq_lens is not None:
+        lens_dev = torch.tensor(seq_lens, dtype=torch.int32, device=dev)
+    fn = lambda: ops.online_attention(q, K, V, length=ctx, gate=gt,  # noqa: E731
+                                      seq_lens=lens_dev)
     # Timed region 1: the K steps as a caller runs them (value, ms_per_step).
     ms = _timed_steps(torch, fn, steps, warmup)
     # Timed region 2: the same K steps with the library's HIP-event brackets
     # on the launch stream, for per-kernel durations (roofline).  Event
     # records cost a few microseconds each, so region 1 excludes them.
-    lib.timing_enable(True)
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        fn()
-    torch.cuda.synchronize()
-    ev_ms = (time.perf_counter() - t0) / steps * 1e3
-    split_ms = _kernel_avg_ms(lib, lib.T_DECODE)
-    comb_ms = _kernel_avg_ms(lib, lib.T_DECODE_COMBINE)
-    lib.timing_enable(False)
+    split_ms, comb_ms = _event_kernel_ms(torch, lib, fn, steps, (lib.T_DECODE,
+                                                                 lib.T_DECODE_COMBINE))
+    graph_ms = _graph_replay_ms(torch, fn, steps, warmup) if graph else None
     es = q.element_size()
-    kv_bytes = 2 * ctx * batch * hkv * d * es
+    rows = batch * ctx if seq_lens is None else int(sum(seq_lens))
+    kv_bytes = 2 * rows * hkv * d * es
     q_bytes = batch * hq * d * es
     step_bytes = kv_bytes + q_bytes * (3 if gate else 2)  # + gate + o
     return {
@@ -99,7 +240,7 @@ def bench_decode(torch, ops, lib, *, batch, ctx, hq, hkv, d, dtype, gate, steps,
         "gbs": step_bytes / (ms * 1e-3) / 1e9,
         "split_ms": split_ms,
         "combine_ms": comb_ms,
-        "ms_per_step_with_events": ev_ms,
+        "graph_ms": graph_ms,
         "split_alg_bytes": kv_bytes + q_bytes,
         "split_gbs": (kv_bytes + q_bytes) / (split_ms * 1e-3) / 1e9,
         "step_bytes": step_bytes,
@@ -108,23 +249,26 @@ def bench_decode(torch, ops, lib, *, batch, ctx, hq, hkv, d, dtype, gate, steps,
 
 
 def bench_prefill(torch, ops, lib, *, steps, warmup, seed=3):
-    """C3: causal prefill of a 2048-token bf16 chunk whose K/V were appended
-    at rows 2048..4095 of a [4096, 1, 8, 128] cache; 32 query heads.  The
-    step is the prefill attention call; FLOPs count causal-valid pairs only."""
+    """C3: the 2048 new K/V rows of a bf16 chunk appended at rows 2048..4095
+    of a [4096, 1, 8, 128] cache, then causal prefill of the chunk's 2048
+    queries (32 heads) over 4096 positions.  The timed step is append +
+    prefill (append_prefill_attention_); the attention kernel alone is timed
+    with HIP events.  FLOPs count causal-valid pairs only."""
     g = torch.Generator(device="cuda").manual_seed(seed)
     dev = torch.device("cuda")
+    bf = torch.bfloat16
     tq, prefix, hq, hkv, d = 2048, 2048, 32, 8, 128
-    K = torch.randn((prefix + tq, 1, hkv, d), generator=g, device=dev).to(torch.bfloat16)
-    V = torch.randn((prefix + tq, 1, hkv, d), generator=g, device=dev).to(torch.bfloat16)
-    q = torch.randn((tq, hq, d), generator=g, device=dev).to(torch.bfloat16)
-    fn = lambda: ops.attention_prefill(q, K, V, position=prefix)  # noqa: E731
-    ms = _timed_steps(torch, fn, steps, warmup)
-    lib.timing_enable(True)
-    for _ in range(steps):
-        fn()
-    torch.cuda.synchronize()
-    k_ms = _kernel_avg_ms(lib, lib.T_PREFILL)
-    lib.timing_enable(False)
+    K = torch.randn((prefix + tq, 1, hkv, d), generator=g, device=dev).to(bf)
+    V = torch.randn((prefix + tq, 1, hkv, d), generator=g, device=dev).to(bf)
+    q = torch.randn((tq, hq, d), generator=g, device=dev).to(bf)
+    k_new = torch.randn((tq, hkv, d), generator=g, device=dev).to(bf)
+    v_new = torch.randn((tq, hkv, d), generator=g, device=dev).to(bf)
+    step = lambda: ops.append_prefill_attention_(q, k_new, v_new, K, V,  # noqa: E731
+                                                 position=prefix)
+    ms = _timed_steps(torch, step, steps, warmup)
+    app_ms, k_ms = _event_kernel_ms(torch, lib, step, steps, (lib.T_KV_APPEND, lib.T_PREFILL))
+    attn = lambda: ops.attention_prefill(q, K, V, position=prefix)  # noqa: E731
+    attn_ms = _timed_steps(torch, attn, steps, warmup)
     # the same rows in a paged pool: 256-row pages in shuffled order
     page, n_pages = 256, (prefix + tq) // 256
     perm = torch.randperm(n_pages, generator=torch.Generator().manual_seed(seed))
@@ -135,17 +279,15 @@ def bench_prefill(torch, ops, lib, *, steps, warmup, seed=3):
     table = perm.to(torch.int32).view(1, n_pages).to(dev)
     fp = lambda: ops.paged_attention_prefill(q, kp, vp, table, position=prefix)  # noqa: E731
     _timed_steps(torch, fp, 3, 2)
-    lib.timing_enable(True)
-    for _ in range(steps):
-        fp()
-    torch.cuda.synchronize()
-    pk_ms = _kernel_avg_ms(lib, lib.T_PREFILL)
-    lib.timing_enable(False)
+    (pk_ms,) = _event_kernel_ms(torch, lib, fp, steps, (lib.T_PREFILL,))
     pairs = sum(prefix + i + 1 for i in range(tq))  # 6,292,480
     flops = 4 * d * hq * pairs                      # QK^T and PV, 2 FLOP per MAC
-    return {"ms_per_step": ms, "kernel_ms": k_ms, "flops": flops,
-            "tflops": flops / (ms * 1e-3) / 1e12, "kernel_tflops": flops / (k_ms * 1e-3) / 1e12,
-            "paged_kernel_ms": pk_ms}
+    append_bytes = 2 * 2 * tq * hkv * d * 2         # K and V rows read + written
+    return {"ms_per_step": ms, "attention_ms_per_call": attn_ms, "kernel_ms": k_ms,
+            "append_kernel_ms": app_ms, "flops": flops, "append_bytes": append_bytes,
+            "tflops": flops / (ms * 1e-3) / 1e12,
+            "kernel_tflops": flops / (k_ms * 1e-3) / 1e12, "paged_kernel_ms": pk_ms,
+            "tensors": (q, K, V)}
 
 
 def bench_gdn(torch, ops, lib, *, steps, warmup, seed=5):
@@ -167,12 +309,7 @@ def bench_gdn(torch, ops, lib, *, steps, warmup, seed=5):
     S = torch.zeros((1, hv, dv, dk), dtype=torch.float32, device=dev)
     fn = lambda: ops.gated_delta_net_chunk_(S, q, k, v, beta, gl)  # noqa: E731
     ms = _timed_steps(torch, fn, steps, warmup)
-    lib.timing_enable(True)
-    for _ in range(steps):
-        fn()
-    torch.cuda.synchronize()
-    k_ms = _kernel_avg_ms(lib, lib.T_GDN_CHUNK)
-    lib.timing_enable(False)
+    (k_ms,) = _event_kernel_ms(torch, lib, fn, steps, (lib.T_GDN_CHUNK,))
     head_chunks = hv * (T // C)
     flops = head_chunks * (2 * C * C * (3 * dk + 2 * dv) + 6 * C * dk * dv)
     # decode: 256 steps on the carried state
@@ -181,22 +318,20 @@ def bench_gdn(torch, ops, lib, *, steps, warmup, seed=5):
     step = lambda: ops.gated_delta_net_step_(S, q1, k1, v1, b1, g1)  # noqa: E731
     n_dec = 256
     dec_ms = _timed_steps(torch, step, n_dec, 16)
-    lib.timing_enable(True)
-    for _ in range(n_dec):
-        step()
-    torch.cuda.synchronize()
-    dk_ms = _kernel_avg_ms(lib, lib.T_GDN_STEP)
-    lib.timing_enable(False)
+    (dk_ms,) = _event_kernel_ms(torch, lib, step, n_dec, (lib.T_GDN_STEP,))
+    dec_graph_ms = _graph_replay_ms(torch, step, n_dec, 16)
     step_bytes = 2 * hv * dv * dk * 4 + (2 * hk * dk + 2 * hv * dv) * 2
     return {"prefill_ms": ms, "prefill_kernel_ms": k_ms, "prefill_flops": flops,
             "prefill_tflops": flops / (k_ms * 1e-3) / 1e12,
             "decode_us_per_step": dec_ms * 1e3, "decode_kernel_us": dk_ms * 1e3,
+            "decode_graph_us_per_step": dec_graph_ms * 1e3,
             "decode_step_bytes": step_bytes,
             "decode_kernel_gbs": step_bytes / (dk_ms * 1e-3) / 1e9}
 
 
 def bench_layers(torch, ops, lib, *, steps, warmup, seed=6):
-    """The two fused Qwen3.5 decode-step paths around the kernels.
+    """The two fused Qwen3.5 decode-step paths around the kernels, eager and
+    replayed from a captured graph.
 
     * Attention layer at the C4 geometry (4 sequences, 16 q / 2 kv heads,
       head_dim 256, bf16 cache of 32768 rows): prologue (query/gate split,
@@ -234,12 +369,10 @@ def bench_layers(torch, ops, lib, *, steps, warmup, seed=6):
 
     a_ms = _timed_steps(torch, attn_step, steps, warmup)
     a3_ms = _timed_steps(torch, attn_three_launches, steps, warmup)
-    lib.timing_enable(True)
-    for _ in range(steps):
-        attn_step()
-    torch.cuda.synchronize()
-    ak_ms = _kernel_avg_ms(lib, lib.T_DECODE) + _kernel_avg_ms(lib, lib.T_DECODE_COMBINE)
-    lib.timing_enable(False)
+    split_ms, comb_ms = _event_kernel_ms(torch, lib, attn_step, steps,
+                                         (lib.T_DECODE, lib.T_DECODE_COMBINE))
+    ak_ms = split_ms + comb_ms
+    ag_ms = _graph_replay_ms(torch, attn_step, steps, warmup)
     es = 2
     a_bytes = (2 * ctx * b * hkv * d * es + (hq * 2 * d + 2 * hkv * d) * b * es
                + 2 * b * hkv * d * es + 2 * b * hq * d * es + b * hq * d * es)
@@ -263,28 +396,30 @@ def bench_layers(torch, ops, lib, *, steps, warmup, seed=6):
                                          key_heads=hk, key_dimension=dk, epsilon=1e-6)
 
     r_ms = _timed_steps(torch, rec_step, steps, warmup)
-    lib.timing_enable(True)
-    for _ in range(steps):
-        rec_step()
-    torch.cuda.synchronize()
-    rk_ms = _kernel_avg_ms(lib, lib.T_RECURRENT_STEP)
-    lib.timing_enable(False)
+    (rk_ms,) = _event_kernel_ms(torch, lib, rec_step, steps, (lib.T_RECURRENT_STEP,))
+    rg_ms = _graph_replay_ms(torch, rec_step, steps, warmup)
     r_bytes = (2 * bsz * hv * dv * dk * 4 + 2 * bsz * (kern - 1) * chn * 4 + kern * chn * 4
                + bsz * chn * 4 + 2 * bsz * hv * dv * 4 + 2 * bsz * hv * 4 + 2 * hv * 4 + dv * 4)
     return {
         "attention_layer_c4": {
             "us_per_step": round(a_ms * 1e3, 2),
+            "graph_us_per_step": round(ag_ms * 1e3, 2),
             "kernel_us": round(ak_ms * 1e3, 2),
             "three_launch_us_per_step": round(a3_ms * 1e3, 2),
             "step_bytes": a_bytes,
             "step_gbs": round(a_bytes / (a_ms * 1e-3) / 1e9, 1),
-            "frac_hbm": round(a_bytes / (a_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
+            "frac_hbm": round(a_bytes / (a_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "roofline": _roofline("decode_split_mfma_pro<bf16,256> + decode_combine", "hbm",
+                                  a_bytes, ak_ms)},
         "recurrent_layer_c5": {
             "us_per_step": round(r_ms * 1e3, 2),
+            "graph_us_per_step": round(rg_ms * 1e3, 2),
             "kernel_us": round(rk_ms * 1e3, 2),
             "step_bytes": r_bytes,
             "kernel_gbs": round(r_bytes / (rk_ms * 1e-3) / 1e9, 1),
-            "frac_hbm": round(r_bytes / (rk_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
+            "frac_hbm": round(r_bytes / (rk_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "roofline": _roofline("recurrent_rows_kernel + recurrent_finish_kernel", "hbm",
+                                  r_bytes, rk_ms)},
     }
 
 
@@ -304,12 +439,7 @@ def bench_paged(torch, ops, lib, c2, *, steps, warmup, seed=8):
     fn = lambda: ops.paged_online_attention(q, pw.key_pages, pw.value_pages, table,  # noqa: E731
                                             length=ctx)
     ms = _timed_steps(torch, fn, steps, warmup)
-    lib.timing_enable(True)
-    for _ in range(steps):
-        fn()
-    torch.cuda.synchronize()
-    split_ms = _kernel_avg_ms(lib, lib.T_DECODE)
-    lib.timing_enable(False)
+    (split_ms,) = _event_kernel_ms(torch, lib, fn, steps, (lib.T_DECODE,))
     return {"c2_paged_256_rows": {
         "ms_per_step": round(ms, 5), "gbs": round(c2["step_bytes"] / (ms * 1e-3) / 1e9, 1),
         "split_ms": round(split_ms, 5),
@@ -392,43 +522,102 @@ def bench_layer_prefill(torch, ops, lib, *, steps, warmup, seed=7):
     }
 
 
-def cpu_baseline_c2(q, K, V, batch, hkv, d, budget_s=12.0):
-    """Time the oracle's two-pass llama decode (fp32, model.py:1246-1252) on
-    the C2 workload; returns GB/s of algorithmic bytes and the sample."""
+# ------------------------------------------------------------ CPU legs per config
+
+def cpu_c3(tensors, host, budget_s=12.0):
+    """The reference's batched causal llama prefill (model.py:1254-1272:
+    materialised masked scores, max-subtracted softmax, fp32) over the C3
+    chunk after its append."""
     import numpy as np
     from oracle import attention as A
-    try:
-        from threadpoolctl import threadpool_info
-        blas = [i for i in threadpool_info() if i.get("user_api") == "blas"]
-        cores = max(int(i.get("num_threads", 1)) for i in blas) if blas else 1
-    except Exception:  # pragma: no cover
-        cores = 1
+    q, K, V = tensors
     qh = q.float().cpu().numpy()
-    # llama layout: one contiguous (t, n_kv, hd) fp32 cache per sequence
-    Kh = [np.ascontiguousarray(K[:, b].float().cpu().numpy()) for b in range(batch)]
-    Vh = [np.ascontiguousarray(V[:, b].float().cpu().numpy()) for b in range(batch)]
-    group = qh.shape[1] // hkv
-    scale = 1.0 / math.sqrt(d)
-    times = []
-    t_start = time.perf_counter()
-    while len(times) < 3 or (time.perf_counter() - t_start < budget_s and len(times) < 50):
-        t0 = time.perf_counter()
-        for b in range(batch):
-            A.attention_decode_twopass(qh[b], Kh[b], Vh[b], group, scale, acc=np.float32)
-        times.append(time.perf_counter() - t0)
-    step_s = statistics.median(times)
-    es = 2  # algorithmic bytes are counted at the workload's fp16 storage size
-    ctx = Kh[0].shape[0]
-    step_bytes = 2 * ctx * batch * hkv * d * es + 2 * qh.size * es
-    return {
-        "value": step_bytes / step_s / 1e9,
-        "unit": "GB/s",
-        "cores": cores,
-        "kind": "port",
-        "sample": (f"full C2 uniform-8192 step (16 sequences, NumPy two-pass fp32 "
-                   f"oracle), median of {len(times)} runs, {step_s * 1e3:.1f} ms/step"),
-    }
+    Kh = np.ascontiguousarray(K[:, 0].float().cpu().numpy())
+    Vh = np.ascontiguousarray(V[:, 0].float().cpu().numpy())
+    prefix = Kh.shape[0] - qh.shape[0]
+    positions = prefix + np.arange(qh.shape[0])
+    group = qh.shape[1] // Kh.shape[1]
+    scale = 1.0 / math.sqrt(qh.shape[2])
+    step_s, runs = _median_runs(
+        lambda: A.attention_batch(qh, Kh, Vh, positions, group, scale, acc=np.float32),
+        budget_s, min_runs=2, max_runs=10)
+    pairs = sum(prefix + i + 1 for i in range(qh.shape[0]))
+    flops = 4 * qh.shape[2] * qh.shape[1] * pairs
+    return {"value": round(flops / step_s / 1e12, 4), "unit": "TFLOP/s",
+            "cores": _blas_threads(host), "kind": "port", "ms_per_step": round(step_s * 1e3, 1),
+            "sample": f"full C3 prefill attention (2048 queries x 4096 positions, 32/8 heads), "
+                      f"NumPy batched two-pass fp32 oracle (model.py:1254-1272), causal-valid "
+                      f"FLOPs, median of {runs} runs"}
 
+
+def cpu_c4(tensors, host, budget_s=10.0):
+    """C4 on the CPU: the online per-position loop of
+    qwen35_full_attention_decode (qwen35_kernels.py:376-391) on a bounded
+    sample (one sequence, its first ``rows`` cache rows, all 16 heads),
+    scaled to GB/s of the rows it reads; plus the vectorised two-pass over
+    the full step as a second figure."""
+    import numpy as np
+    from oracle import attention as A
+    q, K, V = tensors
+    qh = q.float().cpu().numpy()
+    rows = 2048
+    k0 = np.ascontiguousarray(K[:rows, 0].float().cpu().numpy())
+    v0 = np.ascontiguousarray(V[:rows, 0].float().cpu().numpy())
+    t0 = time.perf_counter()
+    A.full_attention_decode_online(qh[0], k0, v0, acc=np.float32)
+    online_s = time.perf_counter() - t0
+    hkv, d = k0.shape[1], k0.shape[2]
+    online_bytes = 2 * rows * hkv * d * 2
+    two = cpu_decode_twopass(q, [K[:, b] for b in range(K.shape[1])],
+                             [V[:, b] for b in range(V.shape[1])], hkv, d, 2,
+                             "full C4 step (4 sequences x 32768 rows)", host, budget_s)
+    return {"value": round(online_bytes / online_s / 1e9, 4), "unit": "GB/s", "cores": 1,
+            "kind": "port", "online_rows_per_s": round(rows / online_s, 1),
+            "sample": f"online per-position loop (qwen35_kernels.py:376-391), one sequence, "
+                      f"first {rows} of 32768 rows, 16 heads, fp32; bf16 storage bytes",
+            "two_pass": two}
+
+
+def cpu_c5(host):
+    """C5 on the CPU: the reference's token-sequential qwen35_gdn_step
+    (qwen35_kernels.py:322-331), one call per token, fp32: the 1024-token
+    prefill (first 256 tokens timed, scaled) and 256 decode steps (first 64
+    timed)."""
+    import numpy as np
+    from oracle import gdn as G
+    rng = np.random.default_rng(5)
+    hk, hv, dk, dv = 16, 32, 128, 128
+    n = 256
+    q = rng.standard_normal((n, hk, dk)).astype(np.float32)
+    k = rng.standard_normal((n, hk, dk)).astype(np.float32)
+    q /= np.linalg.norm(q, axis=-1, keepdims=True)
+    k /= np.linalg.norm(k, axis=-1, keepdims=True)
+    v = rng.standard_normal((n, hv, dv)).astype(np.float32)
+    beta = (1 / (1 + np.exp(-rng.standard_normal((n, hv))))).astype(np.float32)
+    g = (-np.exp(rng.uniform(-1, 1, hv)) * np.log1p(np.exp(rng.standard_normal((n, hv))))
+         ).astype(np.float32)
+    S = np.zeros((hv, dv, dk), dtype=np.float32)
+    t0 = time.perf_counter()
+    for t in range(n):
+        G.gdn_step(S, q[t], k[t], v[t], beta[t], g[t], acc=np.float32)
+    per_token = (time.perf_counter() - t0) / n
+    flops = 32 * 16 * (2 * 64 * 64 * (3 * dk + 2 * dv) + 6 * 64 * dk * dv)
+    prefill_s = per_token * 1024
+    return {"value": round(flops / prefill_s / 1e12, 6), "unit": "TFLOP/s",
+            "cores": 1, "kind": "port", "prefill_ms": round(prefill_s * 1e3, 2),
+            "decode_us_per_step": round(per_token * 1e6, 1),
+            "sample": f"token-sequential qwen35_gdn_step (qwen35_kernels.py:322-331), fp32, "
+                      f"{n} tokens timed, 1024-token prefill time scaled from them; TFLOP/s "
+                      f"on the chunked-form FLOP count the GPU line uses"}
+
+
+def cpu_c1(tensors, host, budget_s=3.0):
+    q, K, V = tensors
+    return cpu_decode_twopass(q, [K[:, 0]], [V[:, 0]], 8, 64, 4,
+                              "full C1 step (32/8 heads, 512 rows)", host, budget_s)
+
+
+# ------------------------------------------------------------ counter runs
 
 def _c2_tensors(torch, seed=2):
     g = torch.Generator(device="cuda").manual_seed(seed)
@@ -439,18 +628,29 @@ def _c2_tensors(torch, seed=2):
     return q, K, V
 
 
-def pmc_probe(torch, ops, steps) -> int:
+def pmc_probe(torch, ops, lib, steps, workload="c2") -> int:
     """Workload for the counter runs: 3 plain copies of known size (the
     library's append kernel writing a whole C2-sized K and V cache: it reads
-    and writes 2 x 268,435,456 bytes per launch), then ``steps`` C2 decode
-    steps.  Prints the copy's byte count for the summary step."""
+    and writes 2 x 268,435,456 bytes per launch), then ``steps`` steps of
+    ``workload``: C2 decode (c2), C3 append + prefill (c3) or the C5
+    chunked GDN prefill (c5).  Prints the copy's byte count for the summary
+    step."""
     q, K, V = _c2_tensors(torch)
     Kc, Vc = torch.empty_like(K), torch.empty_like(V)
     ops_mod = _mod("_ops")
     for _ in range(3):
         ops_mod.kv_append(Kc, Vc, K, V, position=0)
-    for _ in range(steps):
-        ops.online_attention(q, K, V, length=C2_SHAPE["ctx"])
+    if workload == "c2":
+        for _ in range(steps):
+            ops.online_attention(q, K, V, length=C2_SHAPE["ctx"])
+    elif workload == "c3":
+        del Kc, Vc
+        bench_prefill(torch, ops, lib, steps=steps, warmup=1)
+    elif workload == "c5":
+        del Kc, Vc
+        bench_gdn(torch, ops, lib, steps=steps, warmup=1)
+    else:
+        raise SystemExit(f"unknown probe workload {workload!r}")
     torch.cuda.synchronize()
     copy_bytes = 2 * K.numel() * K.element_size()
     print(json.dumps({"copy_kernel": COPY_KERNEL, "copy_read_bytes": copy_bytes,
@@ -539,13 +739,15 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--only-headline", action="store_true")
-    ap.add_argument("--workloads", default="c4,c3,c5,c1,layers,lprefill,paged",
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--only-headline", action="store_true",
+                    help="C2 uniform only (no other workloads)")
+    ap.add_argument("--workloads", default="ragged,c4,c3,c5,c1,layers,lprefill,paged",
                     help="comma list of secondary workloads to run "
-                         "(c1, c3, c4, c5, layers, lprefill, paged)")
-    ap.add_argument("--pmc-probe", action="store_true",
-                    help="run the counter-run workload (copy calibration + C2 steps)")
+                         "(ragged, c1, c3, c4, c5, layers, lprefill, paged)")
+    ap.add_argument("--pmc-probe", nargs="?", const="c2", default=None, metavar="WORKLOAD",
+                    help="run the counter-run workload: copy calibration + c2 (default), c3 "
+                         "or c5 steps")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="summarise two rocprofv3 counter runs of --pmc-probe")
     args = ap.parse_args()
@@ -553,7 +755,8 @@ def main() -> int:
         return traffic_summary(*args.traffic_summary)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
-              "(the path has no multi-GPU component in this build)", file=sys.stderr)
+              "(every GPU box of this build has one GPU; the sharding design is "
+              "described, not run)", file=sys.stderr)
         return 2
 
     import torch
@@ -564,53 +767,100 @@ def main() -> int:
     ops = _mod("qwen35_rocm_ops").Qwen35RocmOps()
     steps, warmup = args.steps, args.warmup
     if args.pmc_probe:
-        return pmc_probe(torch, ops, 5)
+        return pmc_probe(torch, ops, lib, 5, args.pmc_probe)
+    host = None if args.no_cpu else _host_info()
 
     # headline: C2 uniform-8192 fp16
     c2 = bench_decode(torch, ops, lib, batch=16, ctx=8192, hq=32, hkv=8, d=128,
                       dtype=torch.float16, gate=False, steps=steps, warmup=warmup, seed=2)
     extra = {}
-    wl = set(args.workloads.split(",")) if not args.only_headline or "--workloads" in " ".join(sys.argv) else set()
+    wl = set() if args.only_headline else set(args.workloads.split(","))
+    if "ragged" in wl:
+        # C2 ragged: the survey's draw rule, rng(seed 2).integers(1024, 8193, 16)
+        import numpy as np
+        lens = np.random.default_rng(2).integers(1024, 8192 + 1, 16).astype(np.int32).tolist()
+        cr = bench_decode(torch, ops, lib, batch=16, ctx=8192, hq=32, hkv=8, d=128,
+                          dtype=torch.float16, gate=False, steps=steps, warmup=warmup, seed=2,
+                          seq_lens=lens)
+        entry = {
+            "gbs": round(cr["gbs"], 1), "frac_hbm": round(cr["gbs"] / HBM_PEAK_GBS, 4),
+            "ms_per_step": round(cr["ms_per_step"], 5), "seq_lens": lens,
+            "valid_rows": int(sum(lens)), "step_bytes": cr["step_bytes"],
+            "combine_ms": round(cr["combine_ms"], 5),
+            "roofline": _roofline("decode_split_mfma<f16,128>", "hbm", cr["split_alg_bytes"],
+                                  cr["split_ms"])}
+        if host:
+            q, K, V = cr["tensors"]
+            entry["cpu_baseline"] = cpu_decode_twopass(
+                q, [K[:n, b] for b, n in enumerate(lens)], [V[:n, b] for b, n in enumerate(lens)],
+                8, 128, 2, "full C2 ragged step (16 sequences, lengths above)", host, 8.0)
+        cr.pop("tensors")
+        extra["c2_ragged_decode_fp16"] = entry
     if "c4" in wl:
         c4 = bench_decode(torch, ops, lib, batch=4, ctx=32768, hq=16, hkv=2, d=256,
                           dtype=torch.bfloat16, gate=True, steps=steps, warmup=warmup, seed=4)
-        c4.pop("tensors")
-        extra["c4_gated_decode_bf16_32k"] = {
+        entry = {
             "gbs": round(c4["gbs"], 1), "frac_hbm": round(c4["gbs"] / HBM_PEAK_GBS, 4),
-            "ms_per_step": round(c4["ms_per_step"], 4),
-            "split_kernel_gbs": round(c4["split_gbs"], 1),
-            "split_ms": round(c4["split_ms"], 4), "combine_ms": round(c4["combine_ms"], 4)}
+            "ms_per_step": round(c4["ms_per_step"], 4), "step_bytes": c4["step_bytes"],
+            "combine_ms": round(c4["combine_ms"], 4),
+            "roofline": _roofline("decode_split_mfma<bf16,256>", "hbm", c4["split_alg_bytes"],
+                                  c4["split_ms"])}
+        if host:
+            entry["cpu_baseline"] = cpu_c4(c4["tensors"], host)
+        c4.pop("tensors")
+        extra["c4_gated_decode_bf16_32k"] = entry
     if "c3" in wl:
         c3 = bench_prefill(torch, ops, lib, steps=steps, warmup=warmup)
-        extra["c3_prefill_bf16_2k_on_2k"] = {
+        entry = {
             "tflops": round(c3["tflops"], 1),
             "frac_mfma_bf16": round(c3["tflops"] / BF16_PEAK_TFLOPS, 4),
             "ms_per_step": round(c3["ms_per_step"], 4),
-            "kernel_ms": round(c3["kernel_ms"], 4),
-            "kernel_tflops": round(c3["kernel_tflops"], 1),
+            "step": "append 2048 K/V rows + causal prefill over 4096 positions",
+            "attention_only_ms_per_call": round(c3["attention_ms_per_call"], 4),
+            "append_kernel_ms": round(c3["append_kernel_ms"], 4),
+            "append_gbs": round(c3["append_bytes"] / (c3["append_kernel_ms"] * 1e-3) / 1e9, 1),
             "flops_per_step": c3["flops"],
             "paged_256_rows_kernel_ms": round(c3["paged_kernel_ms"], 4),
-            "paged_vs_contiguous_kernel": round(c3["kernel_ms"] / c3["paged_kernel_ms"], 3)}
+            "paged_vs_contiguous_kernel": round(c3["kernel_ms"] / c3["paged_kernel_ms"], 3),
+            "roofline": _roofline("prefill_mfma<bf16,bf16,128>", "mfma", c3["flops"],
+                                  c3["kernel_ms"], work_name="flops")}
+        if host:
+            entry["cpu_baseline"] = cpu_c3(c3["tensors"], host)
+        c3.pop("tensors")
+        extra["c3_prefill_bf16_2k_on_2k"] = entry
     if "c5" in wl:
         c5 = bench_gdn(torch, ops, lib, steps=steps, warmup=warmup)
-        extra["c5_gdn_bf16"] = {
+        entry = {
             "prefill_1024_ms": round(c5["prefill_ms"], 4),
             "prefill_kernel_ms": round(c5["prefill_kernel_ms"], 4),
-            "prefill_kernel_tflops": round(c5["prefill_tflops"], 1),
-            "prefill_frac_mfma_bf16": round(c5["prefill_tflops"] / BF16_PEAK_TFLOPS, 4),
             "prefill_flops_chunked": c5["prefill_flops"],
+            "prefill_flops_sequential": 1024 * 32 * 7 * 128 * 128,
             "decode_us_per_step": round(c5["decode_us_per_step"], 2),
+            "decode_graph_us_per_step": round(c5["decode_graph_us_per_step"], 2),
             "decode_kernel_us": round(c5["decode_kernel_us"], 2),
-            "decode_kernel_gbs": round(c5["decode_kernel_gbs"], 1),
-            "decode_frac_hbm": round(c5["decode_kernel_gbs"] / HBM_PEAK_GBS, 4)}
+            "roofline": _roofline("gdn_prep<128> + gdn_apply<bf16,128>", "mfma",
+                                  c5["prefill_flops"], c5["prefill_kernel_ms"],
+                                  work_name="flops"),
+            "decode_roofline": _roofline("gdn_step_kernel<bf16>", "hbm",
+                                         c5["decode_step_bytes"], c5["decode_kernel_us"] * 1e-3)}
+        if host:
+            entry["cpu_baseline"] = cpu_c5(host)
+        extra["c5_gdn_bf16"] = entry
     if "c1" in wl:
         c1 = bench_decode(torch, ops, lib, batch=1, ctx=512, hq=32, hkv=8, d=64,
-                          dtype=torch.float32, gate=False, steps=steps, warmup=warmup, seed=1)
-        c1.pop("tensors")
-        extra["c1_decode_fp32_512"] = {
+                          dtype=torch.float32, gate=False, steps=steps, warmup=warmup, seed=1,
+                          graph=True)
+        entry = {
             "us_per_step": round(c1["ms_per_step"] * 1e3, 2),
+            "graph_us_per_step": round(c1["graph_ms"] * 1e3, 2),
             "split_us": round(c1["split_ms"] * 1e3, 2),
-            "combine_us": round(c1["combine_ms"] * 1e3, 2)}
+            "combine_us": round(c1["combine_ms"] * 1e3, 2),
+            "roofline": _roofline("decode_split_f32<64>", "hbm", c1["split_alg_bytes"],
+                                  c1["split_ms"])}
+        if host:
+            entry["cpu_baseline"] = cpu_c1(c1["tensors"], host)
+        c1.pop("tensors")
+        extra["c1_decode_fp32_512"] = entry
     if "layers" in wl:
         extra.update(bench_layers(torch, ops, lib, steps=steps, warmup=warmup))
     if "paged" in wl:
@@ -620,9 +870,11 @@ def main() -> int:
     extra["c2_combine_ms"] = round(c2["combine_ms"], 5)
 
     cpu = None
-    if not args.no_cpu:
+    if host:
         q, K, V = c2["tensors"]
-        cpu = cpu_baseline_c2(q, K, V, 16, 8, 128)
+        cpu = cpu_decode_twopass(q, [K[:, b] for b in range(16)], [V[:, b] for b in range(16)],
+                                 8, 128, 2, "full C2 uniform-8192 step (16 sequences)", host, 12.0)
+        extra["cpu_host"] = host
     c2.pop("tensors")
 
     traffic = _measured_traffic()
@@ -650,17 +902,9 @@ def main() -> int:
             "batch": 16, "ctx": 8192, "q_heads": 32, "kv_heads": 8, "head_dim": 128,
             "frac_of_hbm_peak": round(c2["gbs"] / HBM_PEAK_GBS, 4),
         },
-        "roofline": {
-            "kernel": "decode_split_mfma<f16,128>",
-            "bound": "hbm",
-            "achieved": round(c2["split_gbs"], 1),
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(c2["split_gbs"] / HBM_PEAK_GBS, 4),
-            "traffic": traffic["traffic_bytes_per_launch"] if traffic else None,
-            "avg_launch_ms": round(c2["split_ms"], 5),
-            "alg_bytes_per_launch": c2["split_alg_bytes"],
-        },
+        "roofline": _roofline("decode_split_mfma<f16,128>", "hbm", c2["split_alg_bytes"],
+                              c2["split_ms"],
+                              traffic=traffic["traffic_bytes_per_launch"] if traffic else None),
         "cpu_baseline": cpu,
         "extra": extra,
     }
