@@ -73,6 +73,116 @@ __device__ __forceinline__ int seq_lo(const DecodeArgs& a, int b, int hi) {
   return (int)(n > hi ? hi : n);
 }
 
+// ------------------------------------------------------------ balanced plan
+//
+// Ragged decode (device seq_lens) plans its split from the device lengths:
+// the valid rows of all sequences are cut into chunks of one size C (the
+// total over items_target, rounded up to a whole block step) and block x of
+// a grid row takes the x-th (sequence, chunk) item, items listed in
+// sequence order.  Every block streams at most C rows whatever the spread
+// of the lengths, so the step time follows the total row count, not the
+// longest sequence.  Since sum_b ceil(len_b / C) <= total / C + batch <=
+// items_target + batch, the grid (items_max = items_target + batch) holds
+// every item; blocks past the last item exit.  The functions below are
+// wave-collective (every lane of the calling wave active) and every wave
+// that calls them gets the same result.
+
+__device__ __forceinline__ int64_t wave_sum(int64_t x) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off);
+  return x;
+}
+
+__device__ __forceinline__ int wave_inclusive_scan(int x, int lane) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(x, off);
+    if (lane >= off) x += y;
+  }
+  return x;
+}
+
+// Common chunk size C of the balanced plan; n0 is the length of sequence
+// `lane` (the first 64 sequences: most batches need no second load).
+__device__ __forceinline__ int balanced_chunk(const DecodeArgs& a, int lane, int& n0) {
+  n0 = lane < a.batch ? seq_len(a, lane) : 0;
+  int64_t total = n0;
+  for (int b0 = 64; b0 < a.batch; b0 += 64) {
+    const int b = b0 + lane;
+    if (b < a.batch) total += seq_len(a, b);
+  }
+  total = wave_sum(total);
+  int64_t c = (total + a.items_target - 1) / a.items_target;
+  c = (c + a.unit - 1) / a.unit * a.unit;
+  return c < a.unit ? a.unit : (int)c;
+}
+
+// Item `item` of the balanced plan: its sequence (-1 past the last item)
+// and cache rows [start, end) (chunk start / C of its sequence).
+__device__ __forceinline__ void balanced_item(const DecodeArgs& a, int item, int& b_out,
+                                              int& start, int& end, int& chunk_out) {
+  const int lane = threadIdx.x & 63;
+  int n0;
+  const int chunk = balanced_chunk(a, lane, n0);
+  chunk_out = chunk;
+  b_out = -1;
+  start = end = 0;
+  int base = 0;
+  for (int b0 = 0; b0 < a.batch; b0 += 64) {
+    const int b = b0 + lane;
+    const int n = b0 == 0 ? n0 : (b < a.batch ? seq_len(a, b) : 0);
+    const int cnt = (n + chunk - 1) / chunk;
+    const int incl = wave_inclusive_scan(cnt, lane);
+    const int excl = incl - cnt;
+    const bool mine = cnt > 0 && item >= base + excl && item < base + incl;
+    const unsigned long long hit = __ballot(mine);
+    if (hit != 0) {
+      const int src = __ffsll((long long)hit) - 1;
+      b_out = __shfl(b, src);
+      start = (item - base - __shfl(excl, src)) * chunk;
+      end = min(start + chunk, __shfl(n, src));
+      return;
+    }
+    base += __shfl(incl, 63);
+  }
+}
+
+// Item count of sequence b in the balanced plan.
+__device__ __forceinline__ int balanced_count(const DecodeArgs& a, int want_b) {
+  const int lane = threadIdx.x & 63;
+  int n0;
+  const int chunk = balanced_chunk(a, lane, n0);
+  const int n = want_b < 64 ? __shfl(n0, want_b) : seq_len(a, want_b);
+  return (n + chunk - 1) / chunk;
+}
+
+// The block's sequence, cache rows [start, end) (b < 0: nothing to do)
+// and split slot: partial (b, h, slot) is written at (b * Hq + h) * nsplit
+// + slot.  Uniform plan: slot = blockIdx.x.  Balanced plan: the chunk's
+// index within its sequence (nsplit bounds the items of one sequence).
+__device__ __forceinline__ void block_rows(const DecodeArgs& a, int& b, int& start, int& end,
+                                           int& slot) {
+  if (a.balanced) {
+    int chunk;
+    balanced_item(a, blockIdx.x, b, start, end, chunk);
+    slot = b < 0 ? 0 : start / chunk;
+  } else {
+    b = blockIdx.z;
+    const int len = seq_len(a, b);
+    start = max((int)blockIdx.x * a.chunk, seq_lo(a, b, len));
+    end = min((int)blockIdx.x * a.chunk + a.chunk, len);
+    slot = blockIdx.x;
+  }
+  b = __builtin_amdgcn_readfirstlane(b);
+  start = __builtin_amdgcn_readfirstlane(start);
+  end = __builtin_amdgcn_readfirstlane(end);
+  slot = __builtin_amdgcn_readfirstlane(slot);
+}
+
+__device__ __forceinline__ int64_t partial_slot(const DecodeArgs& a, int b, int h, int slot) {
+  return ((int64_t)b * a.q_heads + h) * a.nsplit + slot;
+}
+
 // Element offset of cache row `row` of sequence b, kv head kvh (page lookup
 // for paged caches; a table entry outside [0, num_pages) is clamped, so a
 // bad table reads a wrong page but never leaves the page pool).
@@ -100,7 +210,7 @@ __device__ __forceinline__ void wave_sync_lds() {
 template <int D>
 __device__ __forceinline__ void merge_waves(const DecodeArgs& a, char* smem, f32x4 (&o)[D / 16],
                                             float m, float l, int wave, int lane, bool head_ok,
-                                            int b, int h) {
+                                            int b, int h, int slot) {
   constexpr int kMergeO = (kWaves - 1) * (D / 16) * 64 * 4;   // floats
   const int quad = lane >> 4;
   l += __shfl_xor(l, 16);
@@ -139,7 +249,7 @@ __device__ __forceinline__ void merge_waves(const DecodeArgs& a, char* smem, f32
         o[mb] += cw * *(const f32x4*)(mf + ((w * (D / 16) + mb) * 64 + lane) * 4);
     }
     if (head_ok) {
-      const int64_t pidx = ((int64_t)b * a.q_heads + h) * a.nsplit + blockIdx.x;
+      const int64_t pidx = partial_slot(a, b, h, slot);
       if (quad == 0) {
         a.part_m[pidx] = M;
         a.part_l[pidx] = L;
@@ -195,12 +305,11 @@ __device__ __forceinline__ void split_body(const DecodeArgs& a, const SplitProlo
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int b = blockIdx.z;
+  int b, start, end, slot;
+  block_rows(a, b, start, end, slot);
+  if (b < 0) return;  // past the last item of a balanced plan (whole block)
   const int hc = blockIdx.y % a.head_chunks;
   const int kvh = blockIdx.y / a.head_chunks;
-  const int len = seq_len(a, b);
-  const int start = max(blockIdx.x * a.chunk, seq_lo(a, b, len));
-  const int end = min(blockIdx.x * a.chunk + a.chunk, len);
   const int hl = lane & 15;  // query-head column (N index) of this lane
   const int quad = lane >> 4;
   const int g_in = hc * 16 + hl;
@@ -400,7 +509,7 @@ __device__ __forceinline__ void split_body(const DecodeArgs& a, const SplitProlo
     p0 = pn;
   }
 
-  merge_waves<D>(a, smem, o, m, l, wave, lane, head_ok, b, h);
+  merge_waves<D>(a, smem, o, m, l, wave, lane, head_ok, b, h, slot);
 }
 
 template <typename T, int D, bool PAGED>
@@ -439,12 +548,11 @@ decode_split_f32(DecodeArgs a) {
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int b = blockIdx.z;
+  int b, start, end, slot;
+  block_rows(a, b, start, end, slot);
+  if (b < 0) return;  // past the last item of a balanced plan (whole block)
   const int hc = blockIdx.y % a.head_chunks;
   const int kvh = blockIdx.y / a.head_chunks;
-  const int len = seq_len(a, b);
-  const int start = max(blockIdx.x * a.chunk, seq_lo(a, b, len));
-  const int end = min(blockIdx.x * a.chunk + a.chunk, len);
   const int last = end - 1;
   const int hl = lane & 15;
   const int quad = lane >> 4;
@@ -558,7 +666,7 @@ decode_split_f32(DecodeArgs a) {
     wave_sync_lds();
     p0 = pn;
   }
-  merge_waves<D>(a, smem, o, m, l, wave, lane, head_ok, b, h);
+  merge_waves<D>(a, smem, o, m, l, wave, lane, head_ok, b, h, slot);
 }
 
 // ------------------------------------------------------------ generic split
@@ -569,13 +677,11 @@ decode_split_generic(DecodeArgs a) {
   __shared__ float qs[16][256];
   __shared__ float ps[kGenericTile][17];
   const int lane = threadIdx.x;
-  const int b = blockIdx.z;
+  int b, start, end, slot;
+  block_rows(a, b, start, end, slot);
+  if (b < 0) return;  // past the last item of a balanced plan (whole block)
   const int hc = blockIdx.y % a.head_chunks;
   const int kvh = blockIdx.y / a.head_chunks;
-  const int slot = blockIdx.x;
-  const int len = seq_len(a, b);
-  const int start = max(slot * a.chunk, seq_lo(a, b, len));
-  const int end = min(slot * a.chunk + a.chunk, len);
   const int D = a.key_dim, DV = a.value_dim;
   int gcount = a.group - hc * 16;
   gcount = gcount > 16 ? 16 : gcount;
@@ -652,7 +758,7 @@ decode_split_generic(DecodeArgs a) {
     float lt = l[hh];
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) lt += __shfl_xor(lt, off);
-    const int64_t pidx = ((int64_t)b * a.q_heads + h0 + hh) * a.nsplit + slot;
+    const int64_t pidx = partial_slot(a, b, h0 + hh, slot);
     if (lane == 0) {
       a.part_m[pidx] = m[hh];
       a.part_l[pidx] = lt;
@@ -668,16 +774,18 @@ decode_split_generic(DecodeArgs a) {
 // ------------------------------------------------------------ combine
 
 // Pass 2: block (b*Hq + h, 64-column slice) merges the split partials of one
-// query head for 64 output columns.  Wave w folds slots w, w+4, ... into an
-// online (m, l, acc) state; each group of four slots has its max, sum and
+// query head for 64 output columns.  Wave w folds slots w, w+NW, ... into an
+// online (m, l, acc) state; each group of slots has its max, sum and
 // partial loads issued together (none depends on the running max), so the
-// kernel pays about one memory round trip.  The NW wave states are then
-// merged through LDS by wave 0.  With at most four slots (NW = 1) one wave
-// folds them all from a single group of loads, with no LDS merge.
+// kernel pays about one memory round trip per group.  The NW wave states
+// are then merged through LDS by wave 0.  NW = 1 (uniform plans of at most
+// four splits, and every balanced plan, whose sequences hold a handful of
+// items) folds groups of 16 in one wave with no LDS merge.
 template <typename T, typename TO, int NW>
 __global__ void __launch_bounds__(256)
 decode_combine(DecodeArgs a) {
-  constexpr int kGroup = 4;
+  // partials whose loads are issued together (one memory round trip)
+  constexpr int kGroup = NW == 1 ? 16 : 4;
   __shared__ float red[3][NW > 1 ? NW - 1 : 1][64];
   const int64_t bh = blockIdx.x;
   const int lane = threadIdx.x & 63;
@@ -685,10 +793,15 @@ decode_combine(DecodeArgs a) {
   const int DV = a.value_dim;
   const int d = blockIdx.y * 64 + lane;
   const int dc = d < DV ? d : DV - 1;
-  const int ns = a.nsplit;
-  const float* pm = a.part_m + bh * ns;
-  const float* pl = a.part_l + bh * ns;
-  const float* pa = a.part_acc + bh * ns * DV + dc;
+  // Partials of (b, h): slots s < ns of row bh.  A balanced plan's count
+  // of slots for b is formed from the device lengths; the first group's
+  // loads are issued over every slot the row can hold before the count is
+  // known (one memory round trip for both), and slots past it are dropped.
+  const int cap = a.nsplit;
+  const float* pm = a.part_m + bh * cap;
+  const float* pl = a.part_l + bh * cap;
+  const float* pa = a.part_acc + bh * cap * DV + dc;
+  int ns = cap;
   float m = -INFINITY, l = 0.f, acc = 0.f;
   for (int s0 = wave; s0 < ns; s0 += kGroup * NW) {
     float xm[kGroup], xl[kGroup], xa[kGroup];
@@ -699,6 +812,17 @@ decode_combine(DecodeArgs a) {
       xm[u] = ok ? pm[s] : -INFINITY;
       xl[u] = ok ? pl[s] : 0.f;
       xa[u] = ok ? pa[(int64_t)s * DV] : 0.f;
+    }
+    if (a.balanced && s0 == wave) {
+      ns = balanced_count(a, (int)(bh / a.q_heads));
+#pragma unroll
+      for (int u = 0; u < kGroup; ++u) {
+        if (s0 + u * NW >= ns) {
+          xm[u] = -INFINITY;
+          xl[u] = 0.f;
+          xa[u] = 0.f;
+        }
+      }
     }
 #pragma unroll
     for (int u = 0; u < kGroup; ++u) {
@@ -783,9 +907,43 @@ int slot_bound(int pairs, int length) {
   return by_device < by_len ? by_device : by_len;
 }
 
-size_t workspace_for(int batch, int q_heads, int value_dim, int nsplit) {
-  const size_t n = (size_t)batch * q_heads * nsplit;
+size_t partial_bytes(size_t n, int value_dim) {
   return 2 * align256(n * sizeof(float)) + align256(n * value_dim * sizeof(float));
+}
+
+size_t workspace_for(int batch, int q_heads, int value_dim, int nsplit) {
+  return partial_bytes((size_t)batch * q_heads * nsplit, value_dim);
+}
+
+// Balanced plan: items_target blocks per grid row the chunk size is cut for
+// (the resident blocks of one row, at most kMaxItemsPerRow), plus up to
+// `batch` more for the sequences' last partial chunks.
+constexpr int kMaxItemsPerRow = 256;
+// items_target = resident blocks per grid row x NUM / DEN - batch x SUB / 2
+// Two rounds of blocks (measured on C2 ragged: split kernel 75.8% of HBM
+// against 69.6% with one round, the dispatcher filling the slots of blocks
+// that finish early).
+#ifndef ALPX_BALANCED_NUM
+#define ALPX_BALANCED_NUM 2
+#define ALPX_BALANCED_DEN 1
+#define ALPX_BALANCED_SUB 0
+#endif
+
+// Grid x of the balanced plan: the item count is at most items_target +
+// batch (see balanced_chunk) and at most batch * ceil(length / unit) (no
+// chunk is shorter than unit rows unless it ends its sequence).
+int balanced_items_max(int batch, int length, int unit, int items_target) {
+  const int64_t by_len = (int64_t)batch * ((length + unit - 1) / unit);
+  const int64_t by_target = (int64_t)items_target + batch;
+  return (int)(by_len < by_target ? by_len : by_target);
+}
+
+// Partial slots per (b, h) of the balanced plan: the items one sequence can
+// hold (C >= total / target gives ceil(len_b / C) <= target + 1, and C >=
+// unit gives at most ceil(length / unit)).
+int balanced_slots(int length, int unit, int items_target) {
+  const int by_len = (length + unit - 1) / unit;
+  return by_len < items_target + 1 ? by_len : items_target + 1;
 }
 
 template <typename T>
@@ -839,7 +997,10 @@ void launch_combine_nw(int out_dtype, const DecodeArgs& a, hipStream_t s) {
 
 template <typename T>
 int launch_combine(int out_dtype, const DecodeArgs& a, hipStream_t s) {
-  if (a.nsplit <= 4)
+  // One wave folds up to four partials from one group of loads; with more
+  // (uniform plans of many splits) four waves share them.  A balanced plan
+  // gives most sequences a handful of items: one wave.
+  if (a.nsplit <= 4 || a.balanced)
     launch_combine_nw<T, 1>(out_dtype, a, s);
   else
     launch_combine_nw<T, kWaves>(out_dtype, a, s);
@@ -864,15 +1025,21 @@ extern "C" size_t alpx_decode_workspace_bytes(int batch, int q_heads, int kv_hea
   if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || value_dim <= 0 || max_len <= 0 ||
       q_heads % kv_heads != 0)
     return 0;
-  const int hc = (q_heads / kv_heads + 15) / 16;
-  return workspace_for(batch, q_heads, value_dim, slot_bound(batch * kv_heads * hc, max_len));
+  return decode_workspace(batch, q_heads, kv_heads, value_dim, max_len);
 }
 
 namespace alpx {
 
+// Device-independent bound over both plans (split slots per (b, h) for a
+// uniform length; item slots for device lengths).
 size_t decode_workspace(int batch, int q_heads, int kv_heads, int value_dim, int length) {
   const int hc = (q_heads / kv_heads + 15) / 16;
-  return workspace_for(batch, q_heads, value_dim, slot_bound(batch * kv_heads * hc, length));
+  const size_t uniform =
+      workspace_for(batch, q_heads, value_dim, slot_bound(batch * kv_heads * hc, length));
+  // every split kernel steps at least kGenericTile rows per block step
+  const size_t items = workspace_for(batch, q_heads, value_dim,
+                                     balanced_slots(length, kGenericTile, kMaxItemsPerRow));
+  return uniform > items ? uniform : items;
 }
 
 int run_decode(DecodeArgs a, int dtype, int out_dtype, void* workspace, size_t workspace_bytes,
@@ -918,23 +1085,41 @@ int run_decode(DecodeArgs a, int dtype, int out_dtype, void* workspace, size_t w
   const int unit =
       !mfma ? kGenericTile : (dtype == ALPX_F32 ? f32_tile_rows(D) : kTile) * kWaves;
   a.head_chunks = (a.group + 15) / 16;
-  const Plan p = plan_split(a.batch * a.kv_heads * a.head_chunks, a.length,
-                            resident_blocks(kernel, mfma ? 256 : 64, 0), unit);
-  const size_t n = (size_t)a.batch * a.q_heads * p.nsplit;
-  if (fixed_scratch != nullptr && workspace_for(a.batch, a.q_heads, a.value_dim, p.nsplit) >
-                                      workspace_bytes)
+  int resident = resident_blocks(kernel, mfma ? 256 : 64, 0);
+  if (resident > kMaxResident) resident = kMaxResident;
+  const int rows_y = a.kv_heads * a.head_chunks;
+  size_t n;  // partial slots
+  dim3 grid;
+  if (a.seq_lens != nullptr && a.causal_pos0 < 0) {
+    // device lengths: balanced plan (the chunk size is formed on the device)
+    int target = resident * ALPX_BALANCED_NUM / (ALPX_BALANCED_DEN * rows_y) -
+                 a.batch * ALPX_BALANCED_SUB / 2;
+    target = target < 1 ? 1 : (target > kMaxItemsPerRow ? kMaxItemsPerRow : target);
+    a.balanced = 1;
+    a.items_target = target;
+    a.items_max = balanced_items_max(a.batch, a.length, unit, target);
+    a.unit = unit;
+    a.nsplit = balanced_slots(a.length, unit, target);
+    a.chunk = 0;
+    n = (size_t)a.batch * a.q_heads * a.nsplit;
+    grid = dim3(a.items_max, rows_y, 1);
+  } else {
+    const Plan p = plan_split(a.batch * rows_y, a.length, resident, unit);
+    a.balanced = 0;
+    a.nsplit = p.nsplit;
+    a.chunk = p.chunk;
+    n = (size_t)a.batch * a.q_heads * p.nsplit;
+    grid = dim3(p.nsplit, rows_y, a.batch);
+  }
+  if (fixed_scratch != nullptr && partial_bytes(n, a.value_dim) > workspace_bytes)
     return fail(ALPX_ERANGE,
                 "%s: this call needs %zu bytes of split partials, more than the %zu-byte static "
                 "scratch (call the entry point that takes a workspace)",
-                fixed_scratch, workspace_for(a.batch, a.q_heads, a.value_dim, p.nsplit),
-                workspace_bytes);
+                fixed_scratch, partial_bytes(n, a.value_dim), workspace_bytes);
   char* ws = (char*)workspace;
   a.part_m = (float*)ws;
   a.part_l = (float*)(ws + align256(n * sizeof(float)));
   a.part_acc = (float*)(ws + 2 * align256(n * sizeof(float)));
-  a.nsplit = p.nsplit;
-  a.chunk = p.chunk;
-  dim3 grid(p.nsplit, a.kv_heads * a.head_chunks, a.batch);
   int rc;
   {
     TimedRegion timed(split_timer, s);

@@ -39,6 +39,17 @@ struct DecodeArgs {
   int64_t ks_page, vs_page;
   int64_t gate_stride;  // elements between the gate rows of (b, h); 0 = value_dim
   int len_bias;         // added to seq_lens[b] (decode mode)
+  // Balanced plan (decode with device seq_lens): the split grid is
+  // (items_max, kv_heads * head_chunks, 1); every block of one grid row
+  // cuts the sequences' valid rows into chunks of a common size (the
+  // total of the device lengths over items_target, rounded up to `unit`)
+  // and takes the blockIdx.x-th (sequence, chunk) item of the list in
+  // sequence order.  Chunk c of sequence b writes partial slot c of (b, h);
+  // nsplit bounds the chunks of one sequence.
+  int balanced;
+  int items_target;  // blocks per grid row the chunk size is cut for
+  int items_max;     // grid x: at least the item count
+  int unit;          // rows per block step of the split kernel
 };
 
 // The Qwen3.5 attention prologue fused into the split launch: one new token

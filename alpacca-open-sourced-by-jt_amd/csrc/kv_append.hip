@@ -1,11 +1,19 @@
 // KV-cache append: a bit-exact, vectorised row copy into [C, B, Hkv, D].
 //
-// Every (token, sequence) pair owns one contiguous source row of
-// Hkv*D elements and one contiguous destination row at cache row
+// Every (token, sequence) pair owns one contiguous source row of Hkv*D
+// elements and one contiguous destination row at cache row
 // (position_b + t).  Rows are moved in the widest unit that divides the row
 // and both base pointers (16, 8, 4 or 2 bytes), so an fp16/bf16 cache of
 // head_dim 128 moves 16 bytes per lane with fully coalesced reads and
 // writes.  K and V travel in one launch (blockIdx.y selects the tensor).
+//
+// With one host position for every sequence and a contiguous cache, row
+// (t, b) lands at cache row (position + t) * batch + b: the destination of
+// the whole append is one contiguous range, the source is another, and the
+// append is a plain copy (kv_copy_kernel: no per-unit index arithmetic,
+// four independent 16-byte loads in flight per lane).  Device positions and
+// paged destinations take kv_append_rows: one block per (token, sequence)
+// row, which works out its destination once and streams the row's units.
 #include "alpx_common.h"
 #include "timing.h"
 
@@ -20,34 +28,64 @@ struct Paging {
   int max_pages, shift, num_pages;
 };
 
+constexpr int kCopyUnroll = 4;
+
+// dst[i] = src[i] for i < n (K: blockIdx.y 0, V: 1).  Lane i of a block
+// copies units base + i + j * blockDim.x, j < kCopyUnroll: the four loads
+// are issued before the four stores.  The grid covers n in one pass.
 template <typename U>
 __global__ void __launch_bounds__(256)
-kv_append_kernel(U* __restrict__ kc, U* __restrict__ vc, const U* __restrict__ k,
-                 const U* __restrict__ v, int64_t capacity, int batch, int64_t k_units,
-                 int64_t v_units, int tokens, int64_t position,
-                 const int32_t* __restrict__ positions, Paging pg) {
+kv_copy_kernel(U* __restrict__ kd, U* __restrict__ vd, const U* __restrict__ ks,
+               const U* __restrict__ vs, int64_t kn, int64_t vn) {
+  const bool is_v = blockIdx.y != 0;
+  U* __restrict__ dst = is_v ? vd : kd;
+  const U* __restrict__ src = is_v ? vs : ks;
+  const int64_t n = is_v ? vn : kn;
+  const int64_t base = (int64_t)blockIdx.x * blockDim.x * kCopyUnroll + threadIdx.x;
+  if (base >= n) return;
+  U x[kCopyUnroll];
+  if (base + (int64_t)(kCopyUnroll - 1) * blockDim.x < n) {
+#pragma unroll
+    for (int j = 0; j < kCopyUnroll; ++j) x[j] = src[base + (int64_t)j * blockDim.x];
+#pragma unroll
+    for (int j = 0; j < kCopyUnroll; ++j) dst[base + (int64_t)j * blockDim.x] = x[j];
+  } else {
+#pragma unroll
+    for (int j = 0; j < kCopyUnroll; ++j) {
+      const int64_t i = base + (int64_t)j * blockDim.x;
+      if (i < n) dst[i] = src[i];
+    }
+  }
+}
+
+// One block per source row (blockIdx.x = t * batch + b; blockIdx.y = K/V):
+// the destination row is found once per block, then the block's lanes copy
+// the row's units.
+template <typename U>
+__global__ void __launch_bounds__(256)
+kv_append_rows(U* __restrict__ kc, U* __restrict__ vc, const U* __restrict__ k,
+               const U* __restrict__ v, int64_t capacity, int batch, int k_units, int v_units,
+               int64_t position, const int32_t* __restrict__ positions, Paging pg) {
   const bool is_v = blockIdx.y != 0;
   U* __restrict__ dst = is_v ? vc : kc;
   const U* __restrict__ src = is_v ? v : k;
-  const int64_t units = is_v ? v_units : k_units;  // units per (t, b) row
-  const int64_t total = units * (int64_t)tokens * batch;
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
-    const int64_t row = i / units;
-    const int64_t u = i - row * units;
-    const int64_t t = row / batch;
-    const int b = (int)(row - t * batch);
-    const int64_t p = (positions != nullptr ? (int64_t)positions[b] : position) + t;
-    if (p < 0 || p >= capacity) continue;  // device positions: never write out of bounds
-    if (pg.table != nullptr) {
-      const int page = pg.table[(int64_t)b * pg.max_pages + (p >> pg.shift)];
-      if (page < 0 || page >= pg.num_pages) continue;
-      const int64_t drow = ((int64_t)page << pg.shift) | (p & ((1 << pg.shift) - 1));
-      dst[drow * units + u] = src[row * units + u];
-    } else {
-      dst[(p * batch + b) * units + u] = src[row * units + u];
-    }
+  const int units = is_v ? v_units : k_units;
+  const int64_t row = blockIdx.x;
+  const int64_t t = row / batch;
+  const int b = (int)(row - t * batch);
+  const int64_t p = (positions != nullptr ? (int64_t)positions[b] : position) + t;
+  if (p < 0 || p >= capacity) return;  // device positions: never write out of bounds
+  int64_t drow;
+  if (pg.table != nullptr) {
+    const int page = pg.table[(int64_t)b * pg.max_pages + (p >> pg.shift)];
+    if (page < 0 || page >= pg.num_pages) return;
+    drow = ((int64_t)page << pg.shift) | (p & ((1 << pg.shift) - 1));
+  } else {
+    drow = p * batch + b;
   }
+  U* __restrict__ d = dst + drow * units;
+  const U* __restrict__ sr = src + row * units;
+  for (int u = threadIdx.x; u < units; u += blockDim.x) d[u] = sr[u];
 }
 
 template <typename U>
@@ -56,12 +94,25 @@ int launch(void* kc, void* vc, const void* k, const void* v, int64_t capacity, i
            const int32_t* positions, Paging pg, hipStream_t stream) {
   const int64_t ku = k_bytes_row / (int64_t)sizeof(U);
   const int64_t vu = v_bytes_row / (int64_t)sizeof(U);
-  const int64_t work = (ku > vu ? ku : vu) * (int64_t)tokens * batch;
-  int64_t blocks = (work + 255) / 256;
-  if (blocks > 4096) blocks = 4096;
-  if (blocks < 1) blocks = 1;
-  hipLaunchKernelGGL(kv_append_kernel<U>, dim3((unsigned)blocks, 2), dim3(256), 0, stream,
-                     (U*)kc, (U*)vc, (const U*)k, (const U*)v, capacity, batch, ku, vu, tokens,
+  const int64_t rows = (int64_t)tokens * batch;
+  if (positions == nullptr && pg.table == nullptr) {
+    const int64_t kn = ku * rows, vn = vu * rows;
+    const int64_t per_block = 256 * kCopyUnroll;
+    const int64_t blocks = ((kn > vn ? kn : vn) + per_block - 1) / per_block;
+    // a launch dimension holds fewer than 2^32 work-items
+    if (blocks * 256 > 0xffffffffLL)
+      return fail(ALPX_EUNSUPPORTED, "alpx_kv_append: append too large");
+    const int64_t off = position * batch;  // first destination row
+    hipLaunchKernelGGL(kv_copy_kernel<U>, dim3((unsigned)blocks, 2), dim3(256), 0, stream,
+                       (U*)kc + off * ku, (U*)vc + off * vu, (const U*)k, (const U*)v, kn, vn);
+    return check_launch("alpx_kv_append");
+  }
+  const int64_t widest = ku > vu ? ku : vu;
+  const int threads = widest >= 256 ? 256 : (int)((widest + 63) / 64) * 64;
+  if (rows * threads > 0xffffffffLL || widest > 0x7fffffff)
+    return fail(ALPX_EUNSUPPORTED, "alpx_kv_append: append too large");
+  hipLaunchKernelGGL(kv_append_rows<U>, dim3((unsigned)rows, 2), dim3(threads), 0, stream,
+                     (U*)kc, (U*)vc, (const U*)k, (const U*)v, capacity, batch, (int)ku, (int)vu,
                      position, positions, pg);
   return check_launch("alpx_kv_append");
 }

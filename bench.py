@@ -447,6 +447,33 @@ def bench_paged(torch, ops, lib, c2, *, steps, warmup, seed=8):
         "vs_contiguous_step": round(c2["ms_per_step"] / ms, 3)}}
 
 
+def bench_append(torch, lib, c2, *, steps, warmup):
+    """KV append of a whole C2-sized cache (16 x 8192 rows of 8 x 128 fp16
+    K and V: 268,435,456 bytes each read and written per launch) through
+    the contiguous-copy form (one host position) and the per-row form
+    (device positions), plus the decode step's append (one row per
+    sequence).  Bytes: K and V read + written."""
+    _, K, V = c2["tensors"]
+    ops_c = _mod("_ops")
+    Kc, Vc = torch.empty_like(K), torch.empty_like(V)
+    zeros = torch.zeros(K.shape[1], dtype=torch.int32, device=K.device)
+    copy = lambda: ops_c.kv_append(Kc, Vc, K, V, position=0)  # noqa: E731
+    rows = lambda: ops_c.kv_append(Kc, Vc, K, V, positions=zeros)  # noqa: E731
+    k1, v1 = K[:1].contiguous(), V[:1].contiguous()
+    one = lambda: ops_c.kv_append(Kc, Vc, k1, v1, position=4096)  # noqa: E731
+    out = {}
+    for name, fn, nbytes in (("copy", copy, 4 * K.numel() * 2), ("rows", rows, 4 * K.numel() * 2),
+                             ("decode_row", one, 4 * k1.numel() * 2)):
+        _timed_steps(torch, fn, 3, warmup)
+        (ms,) = _event_kernel_ms(torch, lib, fn, steps, (lib.T_KV_APPEND,))
+        out[name] = {"kernel_ms": round(ms, 5), "bytes": nbytes,
+                     "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+    out["roofline"] = _roofline("kv_copy_kernel<uint4>", "hbm", out["copy"]["bytes"],
+                                out["copy"]["kernel_ms"])
+    del Kc, Vc
+    return {"kv_append_c2_cache": out}
+
+
 def bench_layer_prefill(torch, ops, lib, *, steps, warmup, seed=7):
     """The chunked Qwen3.5 layer prefill against the device's own
     token-by-token path (the reference's prefill is token-sequential).
@@ -742,9 +769,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--only-headline", action="store_true",
                     help="C2 uniform only (no other workloads)")
-    ap.add_argument("--workloads", default="ragged,c4,c3,c5,c1,layers,lprefill,paged",
+    ap.add_argument("--workloads", default="ragged,c4,c3,c5,c1,layers,lprefill,paged,append",
                     help="comma list of secondary workloads to run "
-                         "(ragged, c1, c3, c4, c5, layers, lprefill, paged)")
+                         "(ragged, c1, c3, c4, c5, layers, lprefill, paged, append)")
     ap.add_argument("--pmc-probe", nargs="?", const="c2", default=None, metavar="WORKLOAD",
                     help="run the counter-run workload: copy calibration + c2 (default), c3 "
                          "or c5 steps")
@@ -865,6 +892,8 @@ def main() -> int:
         extra.update(bench_layers(torch, ops, lib, steps=steps, warmup=warmup))
     if "paged" in wl:
         extra.update(bench_paged(torch, ops, lib, c2, steps=steps, warmup=warmup))
+    if "append" in wl:
+        extra.update(bench_append(torch, lib, c2, steps=steps, warmup=warmup))
     if "lprefill" in wl:
         extra.update(bench_layer_prefill(torch, ops, lib, steps=steps, warmup=warmup))
     extra["c2_combine_ms"] = round(c2["combine_ms"], 5)

@@ -181,8 +181,8 @@ int alpx_decode_gqa(const void* q, const void* key_cache, const void* value_cach
                     int out_dtype, void* stream);
 
 /* Bytes of the static scratch array alpx_decode_gqa_noalloc keeps on each
- * GPU (16 MiB). */
-#define ALPX_DECODE_SCRATCH_BYTES ((size_t)16 << 20)
+ * GPU (32 MiB: the C2 ragged step needs 17 MB of partials). */
+#define ALPX_DECODE_SCRATCH_BYTES ((size_t)32 << 20)
 
 /*
  * alpx_decode_gqa without a workspace argument and without any allocation.

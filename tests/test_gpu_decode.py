@@ -139,6 +139,31 @@ def test_decode_fp32_ragged_long(gpu, ops, d, hq, hkv):
     assert out.dtype == torch.float32 and err <= TOL["f32"], err
 
 
+@pytest.mark.parametrize("dtype", ["f16", "bf16", "f32"])
+def test_decode_device_lengths_skewed(gpu, ops, dtype):
+    """Device seq_lens plan the split from the lengths themselves (every
+    block streams about the same number of rows).  70 sequences -- two
+    groups of 64 in the device-side scan -- with lengths 0, 1, a few rows
+    and two long ones; a length-0 sequence returns zeros."""
+    import torch
+    rng = np.random.default_rng(70 + len(dtype))
+    B, C, hq, hkv, d = 70, 3000, 8, 2, 128
+    lens = rng.integers(0, 40, B).astype(np.int32)
+    lens[0], lens[5], lens[64], lens[69] = 0, 3000, 2999, 1
+    q = I.round_to(rng.standard_normal((B, hq, d)), dtype)
+    K = I.round_to(rng.standard_normal((C, B, hkv, d)), dtype)
+    V = I.round_to(rng.standard_normal((C, B, hkv, d)), dtype)
+    out = ops.online_attention(_dev(torch, q, dtype, gpu), _dev(torch, K, dtype, gpu),
+                               _dev(torch, V, dtype, gpu), length=C,
+                               seq_lens=torch.from_numpy(lens).to(gpu),
+                               out_dtype=torch.float32).cpu().numpy()
+    assert np.all(out[lens == 0] == 0.0)
+    live = lens > 0
+    ref = A.online_attention(q[live], K[:, live], V[:, live], C, seq_lens=lens[live])
+    err = np.abs(out[live] - ref).max()
+    assert err <= TOL[dtype], err
+
+
 def test_c2_decode_fp16_full_size(gpu, ops):
     import torch
     c = I.c2_decode_fp16()

@@ -72,11 +72,11 @@ def test_noalloc_decode_equals_workspace_decode(gpu):
 
 
 def test_noalloc_decode_rejects_plans_beyond_the_scratch(gpu):
-    """256 sequences x 64 heads at head_dim 256 need one split each, i.e.
-    16384 partials of 1032 bytes: more than the 16 MiB array."""
+    """512 sequences x 64 heads at head_dim 256 need one split each, i.e.
+    32768 partials of 1032 bytes: more than the 32 MiB array."""
     import torch
     L = _lib()
-    b, hq, hkv, d, cap = 256, 64, 64, 256, 32
+    b, hq, hkv, d, cap = 512, 64, 64, 256, 32
     print(f"no-alloc oversize: B={b} Hq={hq} Hkv={hkv} D={d} cap={cap}", flush=True)
     K = torch.zeros((cap, b, hkv, d), dtype=torch.bfloat16, device=gpu)
     q = torch.zeros((b, hq, d), dtype=torch.bfloat16, device=gpu)
