@@ -57,7 +57,7 @@ BF16_PEAK_TFLOPS = 2500.0
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "pmc_traffic_decode_split_c2_f16.md")
 C2_SHAPE = dict(batch=16, ctx=8192, hq=32, hkv=8, d=128)
 SPLIT_KERNEL = "decode_split_mfma"
-COPY_KERNEL = "kv_append_kernel"
+COPY_KERNEL = "kv_copy_kernel"
 
 
 def _mod(name):
@@ -468,7 +468,7 @@ def bench_append(torch, lib, c2, *, steps, warmup):
         (ms,) = _event_kernel_ms(torch, lib, fn, steps, (lib.T_KV_APPEND,))
         out[name] = {"kernel_ms": round(ms, 5), "bytes": nbytes,
                      "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1)}
-    out["roofline"] = _roofline("kv_copy_kernel<uint4>", "hbm", out["copy"]["bytes"],
+    out["roofline"] = _roofline("kv_copy_kernel<u32x4>", "hbm", out["copy"]["bytes"],
                                 out["copy"]["kernel_ms"])
     del Kc, Vc
     return {"kv_append_c2_cache": out}
