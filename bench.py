@@ -734,7 +734,7 @@ def traffic_summary(fetch_dir, write_dir) -> int:
     print("```")
     for ctr, dname in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
         print(f"rocprofv3 --pmc {ctr} --output-format csv -d {dname} -o run -- "
-              "python3 bench.py --pmc-probe")
+              "python3 bench.py --pmc-probe c2")
     print(f"python3 bench.py --traffic-summary {fetch_dir} {write_dir}")
     print("```\n")
     print("| kernel | counter | mean KiB / dispatch | dispatches |")
@@ -746,6 +746,105 @@ def traffic_summary(fetch_dir, write_dir) -> int:
           f"scale = known bytes / (counter KiB x 1024): fetch {f_scale:.4f}, "
           f"write {w_scale:.4f}.\n")
     print("traffic_json: " + json.dumps(rec))
+    return 0
+
+
+def _kernel_label(name):
+    """Kernel name without its parameter list (demangled names keep their
+    template arguments; `(anonymous namespace)` is shortened first)."""
+    name = name.replace("(anonymous namespace)", "anon")
+    return name.split("(")[0].strip()
+
+
+def _dispatch_counters(run_dir):
+    """{kernel name: {counter: [per-dispatch values]}} from one rocprofv3 CSV
+    counter run (rows of one dispatch are summed)."""
+    import csv
+    import glob
+    out = {}
+    for f in glob.glob(os.path.join(run_dir, "**", "*counter_collection.csv"), recursive=True):
+        per, names = {}, {}
+        with open(f, newline="") as fh:
+            for r in csv.DictReader(fh):
+                key = (r["Dispatch_Id"], r["Counter_Name"])
+                per[key] = per.get(key, 0.0) + float(r["Counter_Value"])
+                names[r["Dispatch_Id"]] = _kernel_label(r["Kernel_Name"])
+        for (d, c), v in per.items():
+            out.setdefault(names[d], {}).setdefault(c, []).append(v)
+    return out
+
+
+def counter_summary(pattern, dirs) -> int:
+    """Markdown table of the SQ counter passes in ``dirs`` (one rocprofv3
+    --pmc run each) for every kernel whose name contains ``pattern``, with
+    the ratios the counters support directly: MFMA pipe busy per busy CU
+    cycle (four SIMDs per CU), VALU instructions per MFMA, LDS waits and
+    instruction issue per wave cycle."""
+    merged = {}
+    for d in dirs:
+        for kn, cs in _dispatch_counters(d).items():
+            if pattern in kn:
+                merged.setdefault(kn, {}).update(cs)
+    if not merged:
+        raise SystemExit(f"no kernel matching {pattern!r} in {dirs}")
+    for kn, cs in sorted(merged.items()):
+        mean = {c: statistics.mean(v) for c, v in cs.items()}
+        print(f"### `{kn}`\n")
+        print("| counter | mean per dispatch | dispatches |")
+        print("|---|---:|---:|")
+        for c in sorted(mean):
+            print(f"| {c} | {mean[c]:.0f} | {len(cs[c])} |")
+        ratios = []
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in mean and mean.get("SQ_BUSY_CU_CYCLES"):
+            ratios.append(("MFMA pipe busy per busy-CU cycle (x4 SIMDs)",
+                           mean["SQ_VALU_MFMA_BUSY_CYCLES"] / (4 * mean["SQ_BUSY_CU_CYCLES"])))
+        if mean.get("SQ_INSTS_MFMA") and "SQ_INSTS_VALU" in mean:
+            ratios.append(("non-MFMA VALU instructions per MFMA",
+                           (mean["SQ_INSTS_VALU"] - mean["SQ_INSTS_MFMA"]) / mean["SQ_INSTS_MFMA"]))
+        if mean.get("SQ_INSTS_MFMA") and "SQ_INSTS_VALU_MFMA_MOPS_BF16" in mean:
+            ratios.append(("bf16 MFMA FLOP per launch (MOPS x 512)",
+                           mean["SQ_INSTS_VALU_MFMA_MOPS_BF16"] * 512))
+        if mean.get("SQ_INSTS_LDS") and "SQ_LDS_BANK_CONFLICT" in mean:
+            ratios.append(("LDS bank-conflict cycles per LDS instruction",
+                           mean["SQ_LDS_BANK_CONFLICT"] / mean["SQ_INSTS_LDS"]))
+        for num in ("SQ_WAIT_INST_LDS", "SQ_WAIT_INST_ANY", "SQ_WAIT_ANY", "SQ_ACTIVE_INST_ANY"):
+            if mean.get("SQ_WAVE_CYCLES") and num in mean:
+                ratios.append((f"{num} per wave cycle", mean[num] / mean["SQ_WAVE_CYCLES"]))
+        if ratios:
+            print("\n| derived | value |")
+            print("|---|---:|")
+            for name, v in ratios:
+                print(f"| {name} | {v:.4g} |")
+        print()
+    return 0
+
+
+def trace_summary(trace_dir) -> int:
+    """Markdown table of the library kernels in a rocprofv3 --kernel-trace
+    run: calls, average / min / max duration per (kernel, grid), by total
+    time (one kernel launched on different grids -- e.g. the uniform and
+    the length-balanced decode plans -- gets one row per grid)."""
+    import csv
+    import glob
+    files = glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no kernel_trace.csv under {trace_dir}")
+    groups = {}
+    with open(files[0], newline="") as fh:
+        for r in csv.DictReader(fh):
+            name = r["Kernel_Name"]
+            if "alpx" not in name:
+                continue
+            wg = int(r["Workgroup_Size_X"]) * int(r["Workgroup_Size_Y"]) * int(r["Workgroup_Size_Z"])
+            grid = tuple(int(r[f"Grid_Size_{d}"]) // max(1, int(r[f"Workgroup_Size_{d}"]))
+                         for d in "XYZ")
+            dur = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+            groups.setdefault((_kernel_label(name), grid, wg), []).append(dur)
+    print("| Kernel | Blocks (x, y, z) | Calls | Avg (us) | Min (us) | Max (us) |")
+    print("|---|---|---:|---:|---:|---:|")
+    for (name, grid, wg), ds in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+        print(f"| `{name}` | {grid[0]}, {grid[1]}, {grid[2]} | {len(ds)} | "
+              f"{statistics.mean(ds):.2f} | {min(ds):.2f} | {max(ds):.2f} |")
     return 0
 
 
@@ -777,9 +876,17 @@ def main() -> int:
                          "or c5 steps")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="summarise two rocprofv3 counter runs of --pmc-probe")
+    ap.add_argument("--counter-summary", nargs="+", metavar=("KERNEL", "RUN_DIR"),
+                    help="summarise rocprofv3 --pmc runs for kernels whose name contains KERNEL")
+    ap.add_argument("--trace-summary", metavar="TRACE_DIR",
+                    help="summarise a rocprofv3 --kernel-trace run")
     args = ap.parse_args()
     if args.traffic_summary:
         return traffic_summary(*args.traffic_summary)
+    if args.counter_summary:
+        return counter_summary(args.counter_summary[0], args.counter_summary[1:])
+    if args.trace_summary:
+        return trace_summary(args.trace_summary)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {args.gpus} is not supported "
               "(every GPU box of this build has one GPU; the sharding design is "
