@@ -730,13 +730,16 @@ class Qwen35RocmOps:
         fused = (key_cache.dtype in (self.torch.float16, self.torch.bfloat16)
                  and width == value_width and width in (64, 128, 256))
         if not fused:
+            # Views of the first position + 1 rows: the prologue writes no
+            # row past them, so a device position beyond `position` leaves
+            # the cache untouched, as in the fused step.
+            kc, vc = key_cache[:position + 1], value_cache[:position + 1]
             query, gate = _ops.attention_prologue(
-                query_gate, key, value, query_norm, key_norm, key_cache, value_cache,
-                position=position, positions=positions, sections=section, frequency_base=base,
-                eps=eps)
-            out = self.online_attention(query, key_cache, value_cache, length=position + 1,
-                                        scale=scale, seq_lens=None if positions is None
-                                        else positions + 1, gate=gate, out_dtype=out_dtype)
+                query_gate, key, value, query_norm, key_norm, kc, vc, position=position,
+                positions=positions, sections=section, frequency_base=base, eps=eps)
+            out = self.online_attention(query, kc, vc, length=position + 1, scale=scale,
+                                        seq_lens=None if positions is None else positions + 1,
+                                        gate=gate, out_dtype=out_dtype)
             return out, position + 1
         scale_value = (1.0 / math.sqrt(width) if scale is None
                        else _positive_finite("attention scale", scale))

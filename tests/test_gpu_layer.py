@@ -356,6 +356,49 @@ def test_attention_layer_step_ragged_positions(gpu, ops, dtype, d, rows, bound):
     assert np.array_equal(got_k[mask], kc[mask])
 
 
+@pytest.mark.parametrize("dtype,d", [("bf16", 128), ("f32", 128), ("f32", 96)])
+def test_attention_layer_step_device_position_past_the_step(gpu, ops, dtype, d):
+    """A device position beyond the step's `position` (but inside the
+    cache) writes no cache row on either form of the step -- the fused
+    kernel (fp16 / bf16, widths 64 / 128 / 256) and the prologue + gated
+    decode pair (fp32 and other widths) -- and that sequence attends to the
+    step's position + 1 rows, as the device lengths are clamped there."""
+    import torch
+    rng = np.random.default_rng(500 + d + len(dtype))
+    b, hq, hkv, cap, position = 3, 8, 2, 96, 40
+    rows = [12, 70, 40]  # sequence 1's device row lies past `position`
+    sections, base, eps = (4, 4, 2, 0), 10000.0, 1e-6
+    kc = I.round_to(rng.standard_normal((cap, b, hkv, d)), dtype)
+    vc = I.round_to(rng.standard_normal((cap, b, hkv, d)), dtype)
+    qg = I.round_to(rng.standard_normal((b, hq * 2 * d)) * 3, dtype)
+    k = I.round_to(rng.standard_normal((b, hkv * d)) * 3, dtype)
+    v = I.round_to(rng.standard_normal((b, hkv * d)), dtype)
+    qw_h = rng.uniform(0.5, 1.5, d).astype(np.float32)
+    kw_h = rng.uniform(0.5, 1.5, d).astype(np.float32)
+    KC, VC = _dev(torch, kc, dtype, gpu), _dev(torch, vc, dtype, gpu)
+    out, n = ops.attention_layer_step_(
+        _dev(torch, qg, dtype, gpu), _dev(torch, k, dtype, gpu), _dev(torch, v, dtype, gpu),
+        torch.from_numpy(qw_h).to(gpu), torch.from_numpy(kw_h).to(gpu), KC, VC,
+        position=position, positions=torch.tensor(rows, dtype=torch.int32, device=gpu),
+        sections=sections, frequency_base=base, epsilon=eps, out_dtype=torch.float32)
+    assert n == position + 1
+    got_k, got_v = _np(KC), _np(VC)
+    # sequence 1 wrote nothing; every row but the two written ones is untouched
+    mask = np.ones((cap, b), bool)
+    mask[[12, 40], [0, 2]] = False
+    assert np.array_equal(got_k[mask], kc[mask])
+    assert np.array_equal(got_v[mask], vc[mask])
+    rq, rg, rk, rv = L.attention_prologue(qg, k, v, qw_h, kw_h, eps, np.array(rows), sections,
+                                          base)
+    tol = _tol(dtype)
+    for bb, p in enumerate(rows):
+        n_rows = min(p, position) + 1
+        ref = A.attention_decode_twopass(rq[bb], got_k[:n_rows, bb], got_v[:n_rows, bb],
+                                         hq // hkv, 1.0 / np.sqrt(d))
+        ref = ref * (1.0 / (1.0 + np.exp(-rg[bb])))
+        assert np.abs(_np(out[bb]) - ref).max() <= tol, bb
+
+
 def test_attention_layer_step_rejects_bad_positions(gpu, ops):
     import torch
     b, hq, hkv, d, cap = 2, 8, 2, 128, 64
