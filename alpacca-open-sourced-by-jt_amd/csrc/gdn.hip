@@ -11,22 +11,25 @@
 // second reduction and writes the row back: the state crosses HBM exactly
 // once in each direction.
 //
-// Chunked prefill (bf16 inputs, chunks of 64 tokens, Dk 64/128/256):
+// Chunked prefill (bf16 inputs, chunks of 64 tokens, Dk 64/128/256).  With
+// gamma_t = exp(Gc_t), Gc = cumsum(g) within the chunk, S the state entering
+// the chunk, A = (gamma_t / gamma_i k_t.k_i)_{i<t},
+// M = (gamma_t / gamma_i q_t.k_i)_{i<=t} and T = (I + diag(beta) A)^-1, the
+// delta rule over the chunk is
+//    X^T = V - diag(gamma) K S^T                       (L x Dv)
+//    O   = scale diag(gamma) Q S^T + P X^T,            P = scale M T diag(beta)
+//    S^T <- gamma_L S^T + Qm^T X^T,                    Qm^T = K^T diag(gamma_L / gamma) T diag(beta)
 //  phase A, gdn_prep, one block per (sequence, head, chunk), state-free:
-//    Gc = cumsum(g); A = exp(Gc_t - Gc_i) k_t.k_i (i < t);
-//    M = exp(Gc_t - Gc_i) q_t.k_i (i <= t); T = (I + diag(beta) A)^-1 by
-//    16x16 forward substitution plus block recursion.  K K^T and Q K^T run
-//    on bf16 MFMA (exact products of bf16 inputs, fp32 sums).  T and M are
-//    stored split into hi and lo bf16 planes (the same bytes as fp32), with
-//    Gc in base 2 and beta, so phase B loads its MFMA operands directly.
+//    Gc, K K^T and Q K^T on bf16 MFMA (exact products of bf16 inputs, fp32
+//    sums), T by 16x16 forward substitution plus a block recursion, then P
+//    and Qm^T; P and Qm^T are stored split into hi and lo bf16 planes (the
+//    same bytes as fp32) as ready-made MFMA operands.
 //  phase B, gdn_apply, one block per (sequence, head, 16 state rows),
-//    sequential over chunks with the 16 x Dk state slice resident in LDS:
-//    X = diag(beta) (V - diag(exp Gc) K S^T);  Delta = T X;
-//    O = (diag(exp Gc) Q S^T + M Delta) / sqrt(Dk);
-//    S <- exp(Gc_last) S + (diag(exp(Gc_last - Gc)) Delta)^T K.
-//    (Delta = T X is Ub V - W S^T with Ub = T diag(beta) and
-//    W = T diag(beta exp Gc) K folded together, so phase B reads T, 16 KiB
-//    per head and chunk, instead of Ub and W, 48 KiB at Dk = 128.)
+//    sequential over chunks: only X^T and the state update are on the
+//    chunk-to-chunk chain (two products and two block barriers per chunk);
+//    Q S^T and P X^T for the output ride alongside.  The state slice stays
+//    in fp32 registers of the wave that updates it and is published to the
+//    other waves as hi / lo planes in LDS.
 //    fp32 x fp32 products use three bf16 MFMAs (hi.hi + hi.lo + lo.hi),
 //    fp32 x bf16 products two, so the state keeps ~fp32 accuracy.
 // Tokens past the end of the last chunk are padded as k = q = v = 0,
@@ -183,54 +186,58 @@ __device__ __forceinline__ void split8(const float* x, bf16x8& hi, bf16x8& lo) {
   }
 }
 
-// A/B operand rows in the order the transposing LDS read delivers them:
-// k-slot j of lane group `quad` is row 16 (j / 4) + 4 quad + j % 4.
+__device__ __forceinline__ void split4(f32x4 x, bf16x4& hi, bf16x4& lo) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const bf16_t h = static_cast<bf16_t>(x[j]);
+    hi[j] = h;
+    lo[j] = static_cast<bf16_t>(x[j] - static_cast<float>(h));
+  }
+}
+
+// Rows in the order the transposing LDS read delivers them: k-slot j of
+// lane group `quad` is row 16 (j / 4) + 4 quad + j % 4.
 __device__ __forceinline__ int tr_slot(int quad, int j) { return 16 * (j >> 2) + 4 * quad + (j & 3); }
 
-__host__ __device__ inline int64_t ws_per_chunk() { return 2 * kC + 2 * kC * kC; }
+__device__ __forceinline__ void wave_sync_lds() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 
-// Per-chunk workspace, in order: Gc * log2(e) [kC] fp32, beta [kC] fp32,
-// then the hi and lo bf16 planes of T [kC x kC] and of M [kC x kC].  Each
-// plane is stored fragment-major (frag_idx): the 16 bytes a lane feeds to one
-// MFMA as its A operand are contiguous and the 64 lanes of a wave follow each
-// other, so a wave's operand load is one contiguous 1 KiB access.  M's
-// columns are additionally stored in k-slot order (slot_pos), matching the
-// order in which phase B holds Delta.
+// Per-chunk workspace (fp32 words), in order: Gc * log2(e) [kC], then the hi
+// and lo bf16 planes of P and of W [kC x kC each].  Both are causal (row t
+// is zero past column t), so of the eight 16 x 32 A-operand tiles (m tile
+// mt, k step ks) only the six with 32 ks <= 16 mt + 15 are stored, in the
+// order (0,0) (1,0) (2,0) (2,1) (3,0) (3,1).  Each tile is stored
+// fragment-major: lane 16 quad + i holds row 16 mt + i, columns
+// 32 ks + 8 quad + 0..7, as 16 contiguous bytes, and the 64 lanes follow
+// each other, so a wave's operand load is one contiguous 1 KiB access.
+constexpr int kTiles = 6;
+constexpr int kTileElems = 64 * 8;
+__host__ __device__ inline int64_t ws_per_chunk() { return kC + 4 * kTiles * kTileElems / 2; }
+__device__ __forceinline__ int tile_slot(int mt, int ks) { return mt < 2 ? mt : 2 * mt - 2 + ks; }
+// Whether A-operand tile (mt, ks) of a causal kC x kC matrix is stored.
+__device__ __forceinline__ bool tile_live(int mt, int ks) { return ks == 0 || mt >= 2; }
+
 struct ChunkWs {
   float* g;
-  float* beta;
-  bf16_t *t_hi, *t_lo, *m_hi, *m_lo;
+  bf16_t *p_hi, *p_lo, *w_hi, *w_lo;
 };
 
 __device__ __forceinline__ ChunkWs chunk_ws(float* base) {
   ChunkWs w;
   w.g = base;
-  w.beta = base + kC;
-  w.t_hi = (bf16_t*)(base + 2 * kC);
-  w.t_lo = w.t_hi + kC * kC;
-  w.m_hi = w.t_lo + kC * kC;
-  w.m_lo = w.m_hi + kC * kC;
+  w.p_hi = (bf16_t*)(base + kC);
+  w.p_lo = w.p_hi + kTiles * kTileElems;
+  w.w_hi = w.p_lo + kTiles * kTileElems;
+  w.w_lo = w.w_hi + kTiles * kTileElems;
   return w;
 }
 
-// Column i of a kC-column operand -> its position when the columns are in
-// k-slot order (position 32 ks + 8 quad + j holds column 32 ks + tr_slot(quad, j)).
-__device__ __forceinline__ int slot_pos(int i) {
-  const int ks = i >> 5, r = i & 31;
-  return 32 * ks + 8 * ((r & 15) >> 2) + 4 * (r >> 4) + (r & 3);
-}
-
-// Element (row t, column p) of a kC-row plane with `cols` columns -> its
-// fragment-major index: (row tile t/16, k step p/32, lane
-// 16 * ((p/8) % 4) + t % 16, element p % 8).
-__device__ __forceinline__ int frag_idx(int t, int p, int cols) {
-  return ((((t >> 4) * (cols >> 5) + (p >> 5)) * 4 + ((p >> 3) & 3)) * 16 + (t & 15)) * 8 + (p & 7);
-}
-
-__device__ __forceinline__ void store_split(bf16_t* hi, bf16_t* lo, int idx, float v) {
-  const bf16_t h = static_cast<bf16_t>(v);
-  hi[idx] = h;
-  lo[idx] = static_cast<bf16_t>(v - static_cast<float>(h));
+// Element offset of `lane`'s 16 bytes in stored tile (mt, ks).
+__device__ __forceinline__ int tile_off(int mt, int ks, int lane) {
+  return (tile_slot(mt, ks) * 64 + lane) * 8;
 }
 
 // ------------------------------------------------------------ phase A
@@ -241,12 +248,16 @@ gdn_prep(GdnArgs a) {
   constexpr int kS = DK + 8;   // bf16 LDS row stride
   constexpr int kF = kC + 4;   // fp32 LDS row stride
   constexpr int KS = DK / 32;
+  constexpr int kUnits = DK / 8;
+  constexpr int kUPT = kC * kUnits / 256;
   __shared__ __attribute__((aligned(16))) bf16_t Ks[kC * kS];
   __shared__ __attribute__((aligned(16))) bf16_t Qs[kC * kS];
+  // diag(beta) A, then (per wave, its own 16 rows) M, P and a staging tile
   __shared__ __attribute__((aligned(16))) float Bm[kC * kF];
   __shared__ __attribute__((aligned(16))) float Tm[kC * kF];
   __shared__ __attribute__((aligned(16))) float Xs[4][16 * 17];
-  __shared__ float Gs[kC], Bs[kC];
+  __shared__ __attribute__((aligned(16))) float Gs[kC];
+  __shared__ __attribute__((aligned(16))) float Bs[kC];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hl = lane & 15, quad = lane >> 4;
@@ -254,48 +265,53 @@ gdn_prep(GdnArgs a) {
   const int kh = h % a.Hk;
   const int t0 = c * kC;
 
-  // K, Q rows of the chunk (zero past the end)
-  constexpr int kUnits = DK / 8;
+  // K, Q rows of the chunk, g and beta: every load reads a clamped row and
+  // is issued before any is used, so they are all in flight together; rows
+  // past the end are zeroed when stored.
+  bf16x8 kv[kUPT], qv[kUPT];
 #pragma unroll
-  for (int u = 0; u < kC * kUnits / 256; ++u) {
+  for (int u = 0; u < kUPT; ++u) {
     const int idx = u * 256 + tid;
     const int r = idx / kUnits, cc = idx - (idx / kUnits) * kUnits;
-    const int t = t0 + r;
-    bf16x8 kv = {}, qv = {};
-    if (t < a.T) {
-      const int64_t off = (((int64_t)b * a.T + t) * a.Hk + kh) * DK + 8 * cc;
-      kv = *(const bf16x8*)((const bf16_t*)a.k + off);
-      qv = *(const bf16x8*)((const bf16_t*)a.q + off);
-    }
-    *(bf16x8*)(Ks + r * kS + 8 * cc) = kv;
-    *(bf16x8*)(Qs + r * kS + 8 * cc) = qv;
+    const int64_t off = (((int64_t)b * a.T + min(t0 + r, a.T - 1)) * a.Hk + kh) * DK + 8 * cc;
+    kv[u] = *(const bf16x8*)((const bf16_t*)a.k + off);
+    qv[u] = *(const bf16x8*)((const bf16_t*)a.q + off);
+  }
+  const bool tok_ok = t0 + lane < a.T;
+  const int64_t goff = ((int64_t)b * a.T + min(t0 + lane, a.T - 1)) * a.Hv + h;
+  const float graw = a.g[goff], braw = a.beta[goff];
+  const bf16x8 zero8 = {};
+#pragma unroll
+  for (int u = 0; u < kUPT; ++u) {
+    const int idx = u * 256 + tid;
+    const int r = idx / kUnits, cc = idx - (idx / kUnits) * kUnits;
+    const bool ok = t0 + r < a.T;
+    *(bf16x8*)(Ks + r * kS + 8 * cc) = ok ? kv[u] : zero8;
+    *(bf16x8*)(Qs + r * kS + 8 * cc) = ok ? qv[u] : zero8;
   }
   if (wave == 0) {
-    const int t = t0 + lane;
-    const int64_t off = ((int64_t)b * a.T + t) * a.Hv + h;
-    float gv = t < a.T ? a.g[off] : 0.f;
+    float gv = tok_ok ? graw : 0.f;
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1) {
       const float y = __shfl_up(gv, d);
       if (lane >= d) gv += y;
     }
     Gs[lane] = gv;
-    Bs[lane] = t < a.T ? a.beta[off] : 0.f;
+    Bs[lane] = tok_ok ? braw : 0.f;
   }
   __syncthreads();
 
   const ChunkWs out = chunk_ws(a.ws + (((int64_t)b * a.Hv + h) * a.nchunks + c) * ws_per_chunk());
-  if (tid < kC) {
-    out.g[tid] = Gs[tid] * 1.4426950408889634f;
-    out.beta[tid] = Bs[tid];
-  }
+  if (tid < kC) out.g[tid] = Gs[tid] * kLog2e;
 
   // Bm = diag(beta) (exp(Gc_t - Gc_i) k_t.k_i)_{i<t} and
   // M = (exp(Gc_t - Gc_i) q_t.k_i)_{i<=t}: wave w computes rows 16w..16w+15.
+  // M stays in registers until T is done and Bm's space is free.
+  f32x4 mq[4];
   {
-    f32x4 kk[4], qk[4];
+    f32x4 kk[4];
 #pragma unroll
-    for (int ib = 0; ib < 4; ++ib) kk[ib] = qk[ib] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int ib = 0; ib < 4; ++ib) kk[ib] = mq[ib] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const bf16x8 ka = *(const bf16x8*)(Ks + (16 * wave + hl) * kS + 32 * ks + 8 * quad);
@@ -304,18 +320,27 @@ gdn_prep(GdnArgs a) {
       for (int ib = 0; ib < 4; ++ib) {
         const bf16x8 kb = *(const bf16x8*)(Ks + (16 * ib + hl) * kS + 32 * ks + 8 * quad);
         kk[ib] = mfma16x16x32(ka, kb, kk[ib]);
-        qk[ib] = mfma16x16x32(qa, kb, qk[ib]);
+        mq[ib] = mfma16x16x32(qa, kb, mq[ib]);
       }
     }
+    // Decays and masks as selects over values already in registers (Gc is
+    // non-increasing, so Gc_t - Gc_i <= 0 wherever i <= t).
+    const f32x4 gt = *(const f32x4*)(Gs + 16 * wave + 4 * quad);
+    const f32x4 bt = *(const f32x4*)(Bs + 16 * wave + 4 * quad);
+    float gi[4];
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib) gi[ib] = Gs[16 * ib + hl];
 #pragma unroll
     for (int ib = 0; ib < 4; ++ib) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int t = 16 * wave + 4 * quad + r;
         const int i = 16 * ib + hl;
-        const float dec = i <= t ? expf(Gs[t] - Gs[i]) : 0.f;
-        Bm[t * kF + i] = i < t ? Bs[t] * dec * kk[ib][r] : 0.f;
-        store_split(out.m_hi, out.m_lo, frag_idx(t, slot_pos(i), kC), dec * qk[ib][r]);
+        const float e = fast_exp2(fminf(gt[r] - gi[ib], 0.f) * kLog2e);
+        const float dec = i <= t ? e : 0.f;
+        const float bm = bt[r] * dec * kk[ib][r];
+        Bm[t * kF + i] = i < t ? bm : 0.f;
+        mq[ib][r] *= dec;
       }
     }
   }
@@ -337,47 +362,143 @@ gdn_prep(GdnArgs a) {
     for (int t = 0; t < 16; ++t) Tm[(base + t) * kF + base + lane] = col[t];
   }
   // Zero the strictly-upper blocks so the full 64 x 64 T can be read as is.
-  for (int idx = tid; idx < kC * kC; idx += 256) {
+#pragma unroll
+  for (int j = 0; j < kC * kC / 256; ++j) {
+    const int idx = tid + 256 * j;
     const int t = idx / kC, i = idx - (idx / kC) * kC;
     if ((i >> 4) > (t >> 4)) Tm[t * kF + i] = 0.f;
   }
   __syncthreads();
 
-  // Off-diagonal blocks: T_ij = -T_ii sum_{j<=k<i} Bm_ik T_kj, block row by
-  // block row; wave j computes block (i, j).
+  // Off-diagonal blocks: T_ij = -T_ii sum_{k<i} Bm_ik T_kj (T_kj = 0 for
+  // k < j), block row by block row; wave j computes block (i, j) on fp32
+  // MFMAs (16x16x4: lane (hl, quad) feeds A[hl][quad] and B[quad][hl] of each
+  // 4-wide k step and receives D[4 quad + e][hl]).
+#pragma unroll
   for (int bi = 1; bi < 4; ++bi) {
     if (wave < bi) {
       const int bj = wave;
       float* X = Xs[wave];
-      const int col = hl;
+      f32x4 x = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int row = 4 * quad + e;
-        float acc = 0.f;
-        for (int k = bj; k < bi; ++k)
+      for (int k = 0; k < bi; ++k) {
 #pragma unroll
-          for (int m = 0; m < 16; ++m)
-            acc += Bm[(16 * bi + row) * kF + 16 * k + m] * Tm[(16 * k + m) * kF + 16 * bj + col];
-        X[row * 17 + col] = acc;
+        for (int s4 = 0; s4 < 4; ++s4) {
+          const float av = Bm[(16 * bi + hl) * kF + 16 * k + 4 * s4 + quad];
+          const float bv = Tm[(16 * k + 4 * s4 + quad) * kF + 16 * bj + hl];
+          x = mfma16x16x4(av, bv, x);
+        }
       }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int row = 4 * quad + e;
-        float acc = 0.f;
+      for (int e = 0; e < 4; ++e) X[(4 * quad + e) * 17 + hl] = x[e];
+      wave_sync_lds();
+      f32x4 y = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int m = 0; m < 16; ++m) acc += Tm[(16 * bi + row) * kF + 16 * bi + m] * X[m * 17 + col];
-        Tm[(16 * bi + row) * kF + 16 * bj + col] = -acc;
+      for (int s4 = 0; s4 < 4; ++s4) {
+        const float av = Tm[(16 * bi + hl) * kF + 16 * bi + 4 * s4 + quad];
+        const float bv = X[(4 * s4 + quad) * 17 + hl];
+        y = mfma16x16x4(av, bv, y);
       }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) Tm[(16 * bi + 4 * quad + e) * kF + 16 * bj + hl] = -y[e];
     }
     __syncthreads();
   }
 
-  for (int idx = tid; idx < kC * kC; idx += 256) {
-    const int t = idx / kC, i = idx - (idx / kC) * kC;
-    store_split(out.t_hi, out.t_lo, frag_idx(t, i, kC), Tm[t * kF + i]);
+  // From here each wave works on its own 16 rows of Bm's space (M, then P,
+  // then a staging tile), so only wave-level ordering is needed.
+  float* const Mw = Bm + 16 * wave * kF;
+#pragma unroll
+  for (int ib = 0; ib < 4; ++ib)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) Mw[(4 * quad + r) * kF + 16 * ib + hl] = mq[ib][r];
+  wave_sync_lds();
+
+  // T's columns in the transposing read's token order (k-slot j of lane
+  // group quad is token 32 ks + tr_slot(quad, j)), shared by P and Qm^T.
+  float tc[4][2][8];
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) tc[nt][ks][j] = Tm[(32 * ks + tr_slot(quad, j)) * kF + 16 * nt + hl];
+
+  // P = scale M T diag(beta) for rows 16w..16w+15.  M (i <= t) and T
+  // (lower triangular) are causal: waves 0 and 1 skip tokens 32..63 and
+  // token tiles nt >= 2 get nothing from tokens < 32.
+  {
+    f32x4 pacc[4];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) pacc[nt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const f32x4 m0 = *(const f32x4*)(Mw + hl * kF + 32 * ks + 4 * quad);
+      const f32x4 m1 = *(const f32x4*)(Mw + hl * kF + 32 * ks + 16 + 4 * quad);
+      const float mrow[8] = {m0[0], m0[1], m0[2], m0[3], m1[0], m1[1], m1[2], m1[3]};
+      bf16x8 mh, ml;
+      split8(mrow, mh, ml);
+      if (ks == 0 || wave >= 2) {
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) {
+          if (ks == 1 || nt < 2) {
+            bf16x8 th, tl;
+            split8(tc[nt][ks], th, tl);
+            pacc[nt] = mfma16x16x32(mh, th, pacc[nt]);
+            pacc[nt] = mfma16x16x32(mh, tl, pacc[nt]);
+            pacc[nt] = mfma16x16x32(ml, th, pacc[nt]);
+          }
+        }
+      }
+    }
+    wave_sync_lds();  // M read before P overwrites it
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      const float f = a.scale * Bs[16 * nt + hl];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) Mw[(4 * quad + e) * kF + 16 * nt + hl] = f * pacc[nt][e];
+    }
+    wave_sync_lds();
+    // P as hi / lo fragments: the wave's live tiles, one unit per lane each.
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      if (tile_live(wave, ks)) {
+        const f32x4 x0 = *(const f32x4*)(Mw + hl * kF + 32 * ks + 8 * quad);
+        const f32x4 x1 = *(const f32x4*)(Mw + hl * kF + 32 * ks + 8 * quad + 4);
+        const float x[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+        bf16x8 hi, lo;
+        split8(x, hi, lo);
+        const int o = tile_off(wave, ks, lane);
+        *(bf16x8*)(out.p_hi + o) = hi;
+        *(bf16x8*)(out.p_lo + o) = lo;
+      }
+    }
+  }
+
+  // W = diag(exp(Gc_last - Gc)) T diag(beta), rows 16w..16w+15, straight
+  // from T: lane (hl, quad) forms row 16w + hl, columns 32 ks + 8 quad + 0..7.
+  {
+    const float rowf = fast_exp2((Gs[kC - 1] - Gs[16 * wave + hl]) * kLog2e);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      if (tile_live(wave, ks)) {
+        const float* tr = Tm + (16 * wave + hl) * kF + 32 * ks + 8 * quad;
+        const f32x4 x0 = *(const f32x4*)tr, x1 = *(const f32x4*)(tr + 4);
+        const f32x4 b0 = *(const f32x4*)(Bs + 32 * ks + 8 * quad);
+        const f32x4 b1 = *(const f32x4*)(Bs + 32 * ks + 8 * quad + 4);
+        float x[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          x[j] = rowf * x0[j] * b0[j];
+          x[4 + j] = rowf * x1[j] * b1[j];
+        }
+        bf16x8 hi, lo;
+        split8(x, hi, lo);
+        const int o = tile_off(wave, ks, lane);
+        *(bf16x8*)(out.w_hi + o) = hi;
+        *(bf16x8*)(out.w_lo + o) = lo;
+      }
+    }
   }
 }
 
@@ -386,7 +507,7 @@ gdn_prep(GdnArgs a) {
 // Block -> (16-row state slice, value head, batch).  Consecutive block ids
 // run on consecutive XCDs, so the ids are permuted to give the slices of one
 // head neighbouring positions on one XCD: they read the same per-chunk
-// K/Q rows and T and share that XCD's L2.
+// K/Q rows, P and Qm^T and share that XCD's L2.
 __device__ __forceinline__ void apply_block(const GdnArgs& a, int& slice, int& h, int& b) {
   const int slices = a.Dv / 16;
   const int n = slices * a.Hv * a.B;
@@ -398,41 +519,42 @@ __device__ __forceinline__ void apply_block(const GdnArgs& a, int& slice, int& h
   b = rest / a.Hv;
 }
 
-// Global inputs of one chunk for one thread, in three groups fetched at
-// different points of the chunk loop: the K/Q/V rows, decays and betas that
-// are staged in LDS, and the rows of T and of M its lane feeds to the Delta
-// and output MFMAs as A operands.
+// Global inputs of one chunk, in three groups: what the K S^T / Q S^T step
+// reads as A operands (K and Q rows of the lane's token), the P and W
+// fragments of the wave's token rows, and the V rows and decays that waves
+// 0..2 stage in LDS for everyone.
 template <int DK>
-struct StageIn {
-  static constexpr int kUnitsPerThread = kC * (DK / 8) / 256;
-  bf16x8 k[kUnitsPerThread], q[kUnitsPerThread];
-  bf16x8 v;
-  float g, beta;
+struct KqIn {
+  bf16x8 k[DK / 32], q[DK / 32];
 };
-struct TIn {
-  bf16x8 t_hi[2], t_lo[2];
+struct PwIn {
+  bf16x8 p_hi[2], p_lo[2], w_hi[2], w_lo[2];
 };
-struct MIn {
-  bf16x8 m_hi[2], m_lo[2];
+struct VgIn {
+  bf16x8 v;  // waves 0, 1: V[token tid / 2][16-column slice half tid % 2]
+  f32x4 g;   // wave 2, lanes 0..15: Gc * log2(e) of tokens 4 lane .. 4 lane + 3
 };
 
 template <typename TO, int DK>
 __global__ void __launch_bounds__(256)
 gdn_apply(GdnArgs a) {
-  constexpr int kS = DK + 8;
-  constexpr int kSF = DK + 4;
-  constexpr int kDF = kC + 4;
   constexpr int KS = DK / 32;
-  constexpr int kUnits = DK / 8;
-  constexpr int kUPT = StageIn<DK>::kUnitsPerThread;
-  __shared__ __attribute__((aligned(16))) bf16_t Ks[kC * kS];
-  __shared__ __attribute__((aligned(16))) bf16_t Qs[kC * kS];
-  __shared__ __attribute__((aligned(16))) bf16_t Vs[kC * 24];  // [t][16 rows] + pad
-  __shared__ __attribute__((aligned(16))) float Ss[16 * kSF];  // state slice [r][d]
-  __shared__ __attribute__((aligned(16))) float Xt[16 * kDF];  // X^T [r][t]
-  __shared__ __attribute__((aligned(16))) float Dt[16 * kDF];  // Delta^T [r][t]
+  constexpr int MT = DK / 64;     // state d tiles per wave
+  constexpr int PF = DK <= 128 ? 2 : 1;  // chunks of operands in flight
+  constexpr int kSB = DK + 8;     // bf16 row stride of the state planes and K tile
+  constexpr int kXB = kC + 8;     // bf16 row stride of the X^T and Y^T planes
+  constexpr int kVB = 24;         // bf16 row stride of the V tile
+  constexpr int kOB = 16 + 16 / (int)sizeof(TO);  // TO row stride of the output tile
+  __shared__ __attribute__((aligned(16))) bf16_t Sh[16 * kSB];  // S [r][d], hi
+  __shared__ __attribute__((aligned(16))) bf16_t Sl[16 * kSB];  // S [r][d], lo
+  __shared__ __attribute__((aligned(16))) bf16_t Ks[kC * kSB];  // K [t][d]
+  __shared__ __attribute__((aligned(16))) bf16_t Xh[16 * kXB];  // X^T [r][t], hi
+  __shared__ __attribute__((aligned(16))) bf16_t Xl[16 * kXB];  // X^T [r][t], lo
+  __shared__ __attribute__((aligned(16))) bf16_t Yh[16 * kXB];  // Y^T [r][t], hi
+  __shared__ __attribute__((aligned(16))) bf16_t Yl[16 * kXB];  // Y^T [r][t], lo
+  __shared__ __attribute__((aligned(16))) bf16_t Vs[kC * kVB];  // V [t][r]
+  __shared__ __attribute__((aligned(16))) TO Os[kC * kOB];      // O [t][r]
   __shared__ __attribute__((aligned(16))) float Gs[kC];
-  __shared__ __attribute__((aligned(16))) float Bs[kC];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int hl = lane & 15, quad = lane >> 4;
@@ -441,219 +563,227 @@ gdn_apply(GdnArgs a) {
   const int r0 = slice * 16;
   const int kh = h % a.Hk;
   const int64_t bh = (int64_t)b * a.Hv + h;
-  float* sg = a.state + (bh * a.Dv + r0) * DK;
-  for (int idx = tid; idx < 16 * DK; idx += 256) {
-    const int r = idx / DK, d = idx - (idx / DK) * DK;
-    Ss[r * kSF + d] = sg[(int64_t)r * DK + d];
-  }
+  const int tw = 16 * wave;  // first token of this wave's 16-token tile
   const int tr_row = 4 * quad + (hl >> 2);
   const int tr_col = 4 * (hl & 3);
-  const int tw = 16 * wave;  // first token of this wave's 16-token tile
 
-  // Every load reads a clamped row and is issued unconditionally; rows past
-  // the end of the sequence are zeroed when staged, so a fetch puts its whole
-  // group in flight without branches.
-  auto fetch_stage = [&](StageIn<DK>& in, int c) __attribute__((always_inline)) {
-    const int t0 = c * kC;
+  // The wave keeps d tiles mt = wave + 4 i of S^T in fp32 (lane: state row
+  // r0 + hl, d = 16 mt + 4 quad + e) and publishes them to every wave as
+  // hi / lo bf16 planes.
+  float* const srow = a.state + (bh * a.Dv + r0 + hl) * DK;
+  f32x4 sown[MT];
 #pragma unroll
-    for (int u = 0; u < kUPT; ++u) {
-      const int idx = u * 256 + tid;
-      const int r = idx / kUnits, cc = idx - (idx / kUnits) * kUnits;
-      const int64_t off =
-          (((int64_t)b * a.T + min(t0 + r, a.T - 1)) * a.Hk + kh) * DK + 8 * cc;
-      in.k[u] = *(const bf16x8*)((const bf16_t*)a.k + off);
-      in.q[u] = *(const bf16x8*)((const bf16_t*)a.q + off);
-    }
-    const int t = (tid & 127) >> 1, half = tid & 1;
-    in.v = *(const bf16x8*)((const bf16_t*)a.v +
-                            (((int64_t)b * a.T + min(t0 + t, a.T - 1)) * a.Hv + h) * a.Dv + r0 +
-                            8 * half);
-    const ChunkWs w = chunk_ws(a.ws + (bh * a.nchunks + c) * ws_per_chunk());
-    in.g = w.g[tid & (kC - 1)];
-    in.beta = w.beta[tid & (kC - 1)];
-  };
-  auto fetch_t = [&](TIn& in, int c) __attribute__((always_inline)) {
-    const ChunkWs w = chunk_ws(a.ws + (bh * a.nchunks + c) * ws_per_chunk());
+  for (int i = 0; i < MT; ++i) sown[i] = *(const f32x4*)(srow + 16 * (wave + 4 * i) + 4 * quad);
+  auto put_state = [&]() __attribute__((always_inline)) {
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const int f = ((wave * 2 + ks) * 64 + lane) * 8;
-      in.t_hi[ks] = *(const bf16x8*)(w.t_hi + f);
-      in.t_lo[ks] = *(const bf16x8*)(w.t_lo + f);
+    for (int i = 0; i < MT; ++i) {
+      bf16x4 hi, lo;
+      split4(sown[i], hi, lo);
+      *(bf16x4*)(Sh + hl * kSB + 16 * (wave + 4 * i) + 4 * quad) = hi;
+      *(bf16x4*)(Sl + hl * kSB + 16 * (wave + 4 * i) + 4 * quad) = lo;
     }
   };
-  auto fetch_m = [&](MIn& in, int c) __attribute__((always_inline)) {
+
+  // Every load reads a clamped row and is issued unconditionally (per
+  // wave); the rows of tokens past the end are zeroed where X^T is formed
+  // and never stored, and their rows of W are zero.
+  auto fetch_kq = [&](KqIn<DK>& in, int c) __attribute__((always_inline)) {
+    const int t = min(c * kC + tw + hl, a.T - 1);
+    const int64_t off = (((int64_t)b * a.T + t) * a.Hk + kh) * DK + 8 * quad;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      in.k[ks] = *(const bf16x8*)((const bf16_t*)a.k + off + 32 * ks);
+      in.q[ks] = *(const bf16x8*)((const bf16_t*)a.q + off + 32 * ks);
+    }
+  };
+  auto fetch_pw = [&](PwIn& in, int c) __attribute__((always_inline)) {
     const ChunkWs w = chunk_ws(a.ws + (bh * a.nchunks + c) * ws_per_chunk());
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      const int f = ((wave * 2 + ks) * 64 + lane) * 8;
-      in.m_hi[ks] = *(const bf16x8*)(w.m_hi + f);
-      in.m_lo[ks] = *(const bf16x8*)(w.m_lo + f);
+      if (tile_live(wave, ks)) {
+        const int o = tile_off(wave, ks, lane);
+        in.p_hi[ks] = *(const bf16x8*)(w.p_hi + o);
+        in.p_lo[ks] = *(const bf16x8*)(w.p_lo + o);
+        in.w_hi[ks] = *(const bf16x8*)(w.w_hi + o);
+        in.w_lo[ks] = *(const bf16x8*)(w.w_lo + o);
+      }
+    }
+  };
+  auto fetch_vg = [&](VgIn& in, int c) __attribute__((always_inline)) {
+    if (wave < 2) {
+      const int t = min(c * kC + (tid >> 1), a.T - 1);
+      in.v = *(const bf16x8*)((const bf16_t*)a.v + (((int64_t)b * a.T + t) * a.Hv + h) * a.Dv +
+                              r0 + 8 * (tid & 1));
+    } else if (wave == 2 && lane < 16) {
+      in.g = *(const f32x4*)(a.ws + (bh * a.nchunks + c) * ws_per_chunk() + 4 * lane);
+    }
+  };
+  auto stage_vg = [&](const VgIn& in, int c) __attribute__((always_inline)) {
+    if (wave < 2) {
+      const bf16x8 zero = {};
+      *(bf16x8*)(Vs + (tid >> 1) * kVB + 8 * (tid & 1)) = c * kC + (tid >> 1) < a.T ? in.v : zero;
+    } else if (wave == 2 && lane < 16) {
+      *(f32x4*)(Gs + 4 * lane) = in.g;
+    }
+  };
+  // Output tile of chunk c (staged in LDS) -> global, 16 bytes per lane.
+  auto flush_out = [&](int c) __attribute__((always_inline)) {
+    constexpr int kPer = 16 / (int)sizeof(TO);  // elements per 16 bytes
+    constexpr int kUnitsRow = 16 / kPer;
+#pragma unroll
+    for (int u0 = 0; u0 < kC * kUnitsRow; u0 += 256) {
+      const int u = u0 + tid;
+      const int t = u / kUnitsRow, part = u % kUnitsRow;
+      if (u < kC * kUnitsRow && c * kC + t < a.T)
+        *(u32x4*)((TO*)a.out + (((int64_t)b * a.T + c * kC + t) * a.Hv + h) * a.Dv + r0 +
+                  kPer * part) = *(const u32x4*)(Os + t * kOB + kPer * part);
     }
   };
 
-  // Each group is re-fetched for chunk c + 1 right after its last use in
-  // chunk c, into the same registers, so the loads overlap the rest of the
-  // chunk without a second register set.  The last chunk re-reads itself
-  // (unused) rather than branching, which would make the compiler wait for
-  // every outstanding load at the top of the loop.  Issue order st, ti, mi
-  // as in the loop (the loads complete in order, so the loop's first wait
-  // for st must not also cover ti and mi).
-  StageIn<DK> st;
-  TIn ti;
-  MIn mi;
-  fetch_stage(st, 0);
-  __builtin_amdgcn_sched_barrier(0);
-  fetch_t(ti, 0);
-  __builtin_amdgcn_sched_barrier(0);
-  fetch_m(mi, 0);
-  __builtin_amdgcn_sched_barrier(0);
-  for (int c = 0; c < a.nchunks; ++c) {
-    const int t0 = c * kC;
-    const int cn = min(c + 1, a.nchunks - 1);
-    const bf16x8 zero = {};
+  // Operands run PF chunks ahead: each set is re-fetched right after its
+  // last use, into the same registers, so the loads overlap the following
+  // chunks.  Chunks past the end re-read the last chunk (unused) rather
+  // than branching.
+  KqIn<DK> kq[PF];
+  PwIn pw[PF];
+  VgIn vg[PF];
 #pragma unroll
-    for (int u = 0; u < kUPT; ++u) {
-      const int idx = u * 256 + tid;
-      const int r = idx / kUnits, cc = idx - (idx / kUnits) * kUnits;
-      const bool ok = t0 + r < a.T;
-      *(bf16x8*)(Ks + r * kS + 8 * cc) = ok ? st.k[u] : zero;
-      *(bf16x8*)(Qs + r * kS + 8 * cc) = ok ? st.q[u] : zero;
-    }
-    if (tid < kC * 2)
-      *(bf16x8*)(Vs + (tid >> 1) * 24 + 8 * (tid & 1)) = t0 + (tid >> 1) < a.T ? st.v : zero;
-    if (tid < kC) {
-      Gs[tid] = st.g;
-      Bs[tid] = st.beta;
-    }
-    __syncthreads();
-    fetch_stage(st, cn);
+  for (int p = 0; p < PF; ++p) {
+    const int c = min(p, a.nchunks - 1);
+    fetch_vg(vg[p], c);
+    fetch_kq(kq[p], c);
+    fetch_pw(pw[p], c);
+  }
+  put_state();
+  stage_vg(vg[0], 0);
+  fetch_vg(vg[0], min(PF, a.nchunks - 1));
+  __syncthreads();
 
-    // S^T operand (B: k = d, n = state row): lane holds S[hl][32 ks + 8 quad + 0..7].
+  auto chunk = [&](int c, KqIn<DK>& kqc, PwIn& pwc, VgIn& vgn) __attribute__((always_inline)) {
+    const int t0 = c * kC;
+    const int cf = min(c + PF, a.nchunks - 1);
+    if (c > 0) flush_out(c - 1);
+
+    // (1) K S^T and Q S^T for this wave's tokens (B = S^T: lane holds
+    // S[r0 + hl][32 ks + 8 quad + 0..7]); X^T = V - diag(exp Gc) K S^T.  The
+    // wave's K rows also go to the K tile for step (3).
     bf16x8 shi[KS], slo[KS];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) split8(Ss + hl * kSF + 32 * ks + 8 * quad, shi[ks], slo[ks]);
-    // Q and K rows of this wave's tokens (A operands).
-    bf16x8 qa[KS], ka[KS];
-#pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      qa[ks] = *(const bf16x8*)(Qs + (tw + hl) * kS + 32 * ks + 8 * quad);
-      ka[ks] = *(const bf16x8*)(Ks + (tw + hl) * kS + 32 * ks + 8 * quad);
+      shi[ks] = *(const bf16x8*)(Sh + hl * kSB + 32 * ks + 8 * quad);
+      slo[ks] = *(const bf16x8*)(Sl + hl * kSB + 32 * ks + 8 * quad);
     }
-
-    // (1a) X = diag(beta) (V - diag(exp Gc) K S^T), rows tw.. (lane: t = tw + 4 quad + r, row hl)
-    f32x4 kst = {0.f, 0.f, 0.f, 0.f};
+    f32x4 kst = {0.f, 0.f, 0.f, 0.f}, qst = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      kst = mfma16x16x32(ka[ks], shi[ks], kst);
-      kst = mfma16x16x32(ka[ks], slo[ks], kst);
+      kst = mfma16x16x32(kqc.k[ks], shi[ks], kst);
+      kst = mfma16x16x32(kqc.k[ks], slo[ks], kst);
+    }
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      qst = mfma16x16x32(kqc.q[ks], shi[ks], qst);
+      qst = mfma16x16x32(kqc.q[ks], slo[ks], qst);
+    }
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) *(bf16x8*)(Ks + (tw + hl) * kSB + 32 * ks + 8 * quad) = kqc.k[ks];
+    fetch_kq(kqc, cf);
+    const bf16x4 v4 = lds_read_tr4(Vs + (tw + tr_row) * kVB + tr_col);
+    const f32x4 g4 = *(const f32x4*)(Gs + tw + 4 * quad);
+    const float glin = fast_exp2(Gs[kC - 1]);
+    f32x4 gam, xt;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      gam[e] = fast_exp2(g4[e]);
+      const bool ok = t0 + tw + 4 * quad + e < a.T;
+      xt[e] = ok ? static_cast<float>(v4[e]) - gam[e] * kst[e] : 0.f;
     }
     {
-      const bf16x4 v4 = lds_read_tr4(Vs + (tw + tr_row) * 24 + tr_col);
-      const f32x4 g4 = *(const f32x4*)(Gs + tw + 4 * quad);
-      const f32x4 b4 = *(const f32x4*)(Bs + tw + 4 * quad);
-      f32x4 x;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) x[r] = b4[r] * (static_cast<float>(v4[r]) - fast_exp2(g4[r]) * kst[r]);
-      *(f32x4*)(Xt + hl * kDF + tw + 4 * quad) = x;
+      bf16x4 hi, lo;
+      split4(xt, hi, lo);
+      *(bf16x4*)(Xh + hl * kXB + tw + 4 * quad) = hi;
+      *(bf16x4*)(Xl + hl * kXB + tw + 4 * quad) = lo;
     }
-    // (2a) Q S^T for the output rows of this wave
-    f32x4 qs = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      qs = mfma16x16x32(qa[ks], shi[ks], qs);
-      qs = mfma16x16x32(qa[ks], slo[ks], qs);
-    }
-    __syncthreads();  // X complete; every wave has read Ss
+    __syncthreads();  // X^T and the K tile complete; every wave has read S, V and Gc
 
-    // (1b) Delta rows tw.. = T X.  T is lower triangular, so waves 0 and 1
-    // (tokens < 32) skip the k step over tokens 32..63.
-    f32x4 dacc = {0.f, 0.f, 0.f, 0.f};
+    // (2) Y^T = W X^T and O = scale exp(Gc) Q S^T + P X^T for this wave's
+    // tokens (W and P are causal: waves 0 and 1, tokens < 32, skip tokens
+    // 32..63).
+    bf16x8 xhi[2], xlo[2];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      if (ks == 0 || wave >= 2) {
-        bf16x8 xhi, xlo;
-        split8(Xt + hl * kDF + 32 * ks + 8 * quad, xhi, xlo);
-        dacc = mfma16x16x32(ti.t_hi[ks], xhi, dacc);
-        dacc = mfma16x16x32(ti.t_hi[ks], xlo, dacc);
-        dacc = mfma16x16x32(ti.t_lo[ks], xhi, dacc);
-      }
+      xhi[ks] = *(const bf16x8*)(Xh + hl * kXB + 32 * ks + 8 * quad);
+      xlo[ks] = *(const bf16x8*)(Xl + hl * kXB + 32 * ks + 8 * quad);
     }
-    *(f32x4*)(Dt + hl * kDF + tw + 4 * quad) = dacc;  // Delta^T[state row][t]
-    fetch_t(ti, cn);
-    __syncthreads();  // Dt complete; every wave has read Xt
-
-    // Delta in the k-slot order of the transposing reads:
-    // dv[ks][j] = Delta[32 ks + tr_slot(quad, j)][hl].
-    float dv[2][8];
+    f32x4 yt = {0.f, 0.f, 0.f, 0.f}, po = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      const f32x4 d0 = *(const f32x4*)(Dt + hl * kDF + 32 * ks + 4 * quad);
-      const f32x4 d1 = *(const f32x4*)(Dt + hl * kDF + 32 * ks + 16 + 4 * quad);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        dv[ks][r] = d0[r];
-        dv[ks][4 + r] = d1[r];
+      if (tile_live(wave, ks)) {
+        yt = mfma16x16x32(pwc.w_hi[ks], xhi[ks], yt);
+        yt = mfma16x16x32(pwc.w_hi[ks], xlo[ks], yt);
+        yt = mfma16x16x32(pwc.w_lo[ks], xhi[ks], yt);
       }
     }
-
-    // (2b) O = exp(Gc) Q S^T + M Delta (M's columns are stored in the same
-    // k-slot order as dv; M is causal, so waves 0 and 1 skip tokens 32..63).
-    f32x4 md = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      if (ks == 0 || wave >= 2) {
-        bf16x8 dhi, dlo;
-        split8(dv[ks], dhi, dlo);
-        md = mfma16x16x32(mi.m_hi[ks], dhi, md);
-        md = mfma16x16x32(mi.m_hi[ks], dlo, md);
-        md = mfma16x16x32(mi.m_lo[ks], dhi, md);
+      if (tile_live(wave, ks)) {
+        po = mfma16x16x32(pwc.p_hi[ks], xhi[ks], po);
+        po = mfma16x16x32(pwc.p_hi[ks], xlo[ks], po);
+        po = mfma16x16x32(pwc.p_lo[ks], xhi[ks], po);
       }
     }
-    fetch_m(mi, cn);
+    {
+      bf16x4 hi, lo;
+      split4(yt, hi, lo);
+      *(bf16x4*)(Yh + hl * kXB + tw + 4 * quad) = hi;
+      *(bf16x4*)(Yl + hl * kXB + tw + 4 * quad) = lo;
+    }
+    fetch_pw(pwc, cf);
+    stage_vg(vgn, c + 1);
+    fetch_vg(vgn, min(c + 1 + PF, a.nchunks - 1));
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int t = tw + 4 * quad + r;
-      if (t0 + t < a.T) {
-        const float o = (fast_exp2(Gs[t]) * qs[r] + md[r]) * a.scale;
-        ((TO*)a.out)[(((int64_t)b * a.T + t0 + t) * a.Hv + h) * a.Dv + r0 + hl] = from_f32<TO>(o);
-      }
-    }
+    for (int e = 0; e < 4; ++e)
+      Os[(tw + 4 * quad + e) * kOB + hl] = from_f32<TO>(a.scale * gam[e] * qst[e] + po[e]);
+    __syncthreads();  // Y^T, the output tile, V and Gc of the next chunk complete
 
-    // (3) S <- exp(Gc_last) S + (diag(exp(Gc_last - Gc)) Delta)^T K  (Gs is in base 2)
-    const float glast = Gs[kC - 1];
-    bf16x8 dthi[2], dtlo[2];
+    // (3) S^T <- exp(Gc_last) S^T + K^T Y^T: A = K^T through the transposing
+    // read (k-slot j of lane group quad is token 32 ks + tr_slot(quad, j)),
+    // B = Y^T in the same token order; then publish the new state.
+    bf16x8 yhi[2], ylo[2];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      float x[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) x[j] = dv[ks][j] * fast_exp2(glast - Gs[32 * ks + tr_slot(quad, j)]);
-      split8(x, dthi[ks], dtlo[ks]);
+      const bf16x4 h0 = *(const bf16x4*)(Yh + hl * kXB + 32 * ks + 4 * quad);
+      const bf16x4 h1 = *(const bf16x4*)(Yh + hl * kXB + 32 * ks + 16 + 4 * quad);
+      const bf16x4 l0 = *(const bf16x4*)(Yl + hl * kXB + 32 * ks + 4 * quad);
+      const bf16x4 l1 = *(const bf16x4*)(Yl + hl * kXB + 32 * ks + 16 + 4 * quad);
+      yhi[ks] = __builtin_shufflevector(h0, h1, 0, 1, 2, 3, 4, 5, 6, 7);
+      ylo[ks] = __builtin_shufflevector(l0, l1, 0, 1, 2, 3, 4, 5, 6, 7);
     }
-    const float gl = fast_exp2(glast);
 #pragma unroll
-    for (int nq = 0; nq < DK / 64; ++nq) {
-      const int nb = wave + 4 * nq;
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < MT; ++i) {
+      const int mt = wave + 4 * i;
+      f32x4 acc = glin * sown[i];
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        const bf16x4 k0 = lds_read_tr4(Ks + (32 * ks + tr_row) * kS + 16 * nb + tr_col);
-        const bf16x4 k1 = lds_read_tr4(Ks + (32 * ks + 16 + tr_row) * kS + 16 * nb + tr_col);
-        const bf16x8 kb = __builtin_shufflevector(k0, k1, 0, 1, 2, 3, 4, 5, 6, 7);
-        acc = mfma16x16x32(dthi[ks], kb, acc);
-        acc = mfma16x16x32(dtlo[ks], kb, acc);
+        const bf16x4 k0 = lds_read_tr4(Ks + (32 * ks + tr_row) * kSB + 16 * mt + tr_col);
+        const bf16x4 k1 = lds_read_tr4(Ks + (32 * ks + 16 + tr_row) * kSB + 16 * mt + tr_col);
+        const bf16x8 ka = __builtin_shufflevector(k0, k1, 0, 1, 2, 3, 4, 5, 6, 7);
+        acc = mfma16x16x32(ka, yhi[ks], acc);
+        acc = mfma16x16x32(ka, ylo[ks], acc);
       }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float* sp = Ss + (4 * quad + r) * kSF + 16 * nb + hl;
-        *sp = gl * *sp + acc[r];
-      }
+      sown[i] = acc;
     }
-    __syncthreads();
+    put_state();
+    __syncthreads();  // new state published; every wave has read Y^T and the K tile
+  };
+
+  for (int c0 = 0; c0 < a.nchunks; c0 += PF) {
+#pragma unroll
+    for (int p = 0; p < PF; ++p)
+      if (c0 + p < a.nchunks) chunk(c0 + p, kq[p], pw[p], vg[(p + 1) % PF]);
   }
-  for (int idx = tid; idx < 16 * DK; idx += 256) {
-    const int r = idx / DK, d = idx - (idx / DK) * DK;
-    sg[(int64_t)r * DK + d] = Ss[r * kSF + d];
-  }
+  flush_out(a.nchunks - 1);
+#pragma unroll
+  for (int i = 0; i < MT; ++i) *(f32x4*)(srow + 16 * (wave + 4 * i) + 4 * quad) = sown[i];
 }
 
 template <int DK, typename TO>
@@ -800,7 +930,8 @@ extern "C" int alpx_gdn_chunk_prefill(float* state, const void* q, const void* k
   a.Dv = value_dim;
   a.nchunks = (tokens + kC - 1) / kC;
   a.scale = gdn_output_scale(key_dim);
-  const uintptr_t align = (uintptr_t)q | (uintptr_t)k | (uintptr_t)v;
+  const uintptr_t align =
+      (uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)state | (uintptr_t)out;
   const bool chunked = dtype == ALPX_BF16 && (key_dim == 64 || key_dim == 128 || key_dim == 256) &&
                        value_dim % 16 == 0 && (align & 15) == 0 &&
                        getenv("ALPX_GDN_SEQUENTIAL") == nullptr;

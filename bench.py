@@ -290,6 +290,14 @@ def bench_prefill(torch, ops, lib, *, steps, warmup, seed=3):
             "tensors": (q, K, V)}
 
 
+def _gdn_chunk_flops(hv, T, C, dk, dv):
+    """Products of the chunked GDN form, counted once each (hi / lo splits
+    not counted): per head and chunk K K^T and Q K^T (2 C^2 dk each), P = M T
+    (2 C^3), then K S^T, Q S^T and K^T Y (2 C dk dv each), Y = W X^T and
+    P X^T (2 C^2 dv each)."""
+    return hv * (T // C) * (2 * C * C * (2 * dk + 2 * dv + C) + 6 * C * dk * dv)
+
+
 def bench_gdn(torch, ops, lib, *, steps, warmup, seed=5):
     """C5: gated delta rule, 16 q/k heads, 32 v heads, Dk = Dv = 128, fp32
     state; a 1024-token chunked prefill, then 256 single-token decode steps.
@@ -310,8 +318,7 @@ def bench_gdn(torch, ops, lib, *, steps, warmup, seed=5):
     fn = lambda: ops.gated_delta_net_chunk_(S, q, k, v, beta, gl)  # noqa: E731
     ms = _timed_steps(torch, fn, steps, warmup)
     (k_ms,) = _event_kernel_ms(torch, lib, fn, steps, (lib.T_GDN_CHUNK,))
-    head_chunks = hv * (T // C)
-    flops = head_chunks * (2 * C * C * (3 * dk + 2 * dv) + 6 * C * dk * dv)
+    flops = _gdn_chunk_flops(hv, T, C, dk, dv)
     # decode: 256 steps on the carried state
     q1, k1, v1 = q[:, 0].contiguous(), k[:, 0].contiguous(), v[:, 0].contiguous()
     b1, g1 = beta[:, 0].contiguous(), gl[:, 0].contiguous()
@@ -628,7 +635,7 @@ def cpu_c5(host):
     for t in range(n):
         G.gdn_step(S, q[t], k[t], v[t], beta[t], g[t], acc=np.float32)
     per_token = (time.perf_counter() - t0) / n
-    flops = 32 * 16 * (2 * 64 * 64 * (3 * dk + 2 * dv) + 6 * 64 * dk * dv)
+    flops = _gdn_chunk_flops(32, 1024, 64, dk, dv)
     prefill_s = per_token * 1024
     return {"value": round(flops / prefill_s / 1e12, 6), "unit": "TFLOP/s",
             "cores": 1, "kind": "port", "prefill_ms": round(prefill_s * 1e3, 2),
