@@ -460,6 +460,9 @@ gdn_prep(GdnArgs a) {
     }
     wave_sync_lds();
     // P as hi / lo fragments: the wave's live tiles, one unit per lane each.
+  // Workspace stores are nontemporal: every block writes its fragments at
+  // the same late point, and streaming them out rather than leaving them
+  // dirty in L2 shortens the drain at the end of the kernel (2-3 us at C5).
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       if (tile_live(wave, ks)) {
@@ -469,8 +472,8 @@ gdn_prep(GdnArgs a) {
         bf16x8 hi, lo;
         split8(x, hi, lo);
         const int o = tile_off(wave, ks, lane);
-        *(bf16x8*)(out.p_hi + o) = hi;
-        *(bf16x8*)(out.p_lo + o) = lo;
+        __builtin_nontemporal_store(__builtin_bit_cast(u32x4, hi), (u32x4*)(out.p_hi + o));
+        __builtin_nontemporal_store(__builtin_bit_cast(u32x4, lo), (u32x4*)(out.p_lo + o));
       }
     }
   }
@@ -495,8 +498,8 @@ gdn_prep(GdnArgs a) {
         bf16x8 hi, lo;
         split8(x, hi, lo);
         const int o = tile_off(wave, ks, lane);
-        *(bf16x8*)(out.w_hi + o) = hi;
-        *(bf16x8*)(out.w_lo + o) = lo;
+        __builtin_nontemporal_store(__builtin_bit_cast(u32x4, hi), (u32x4*)(out.w_hi + o));
+        __builtin_nontemporal_store(__builtin_bit_cast(u32x4, lo), (u32x4*)(out.w_lo + o));
       }
     }
   }
