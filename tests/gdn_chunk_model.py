@@ -6,22 +6,28 @@ against the sequential oracle so the derivation is pinned before it is
 trusted on the GPU.
 
 Per value head with state S (Dv x Dk) entering a chunk of C tokens, with
-cumulative log decay Gc[t] = g_0 + ... + g_t (within the chunk) and
-gamma = exp(Gc):
+cumulative log decay Gc[t] = g_0 + ... + g_t (within the chunk),
+gamma = exp(Gc) and scale = 1 / sqrt(Dk):
 
   A[t, i]  = exp(Gc[t] - Gc[i]) * (k_t . k_i)      for i < t   (else 0)
-  T        = (I + diag(beta) A)^-1                 (unit lower triangular)
-  X        = diag(beta) (V - diag(gamma) K S^T)    (C x Dv)
-  Delta    = T X                                   (C x Dv; row t = delta_t)
   M[t, i]  = exp(Gc[t] - Gc[i]) * (q_t . k_i)      for i <= t  (else 0)
-  O        = (diag(gamma) Q S^T + M Delta) / sqrt(Dk)
-  S_next   = gamma[C-1] S + (diag(exp(Gc[C-1] - Gc)) Delta)^T K
+  T        = (I + diag(beta) A)^-1                 (unit lower triangular)
+  P        = scale M T diag(beta)                  (C x C, causal)
+  W        = diag(gamma[C-1] / gamma) T diag(beta) (C x C, causal)
 
-The state-independent part (Gc, T, M) is computed per (head, chunk) in
-parallel (phase A); the rest carries the chunk-to-chunk dependency (phase B)
-and is independent across the Dv rows of S.  Delta = T X is the familiar
-Ub V - W S^T with Ub = T diag(beta) and W = T diag(beta gamma) K
-(``delta_ub_w``), folded so that phase B reads T instead of Ub and W.
+are state-independent (phase A, per head and chunk in parallel); phase B
+carries the chunk-to-chunk dependency:
+
+  X^T      = V - diag(gamma) K S^T                 (C x Dv)
+  O        = scale diag(gamma) Q S^T + P X^T
+  Y^T      = W X^T
+  S_next^T = gamma[C-1] S^T + K^T Y^T
+
+This is the textbook chunked delta rule (``chunk_apply_delta``: Delta =
+T diag(beta) X^T, O = scale (diag(gamma) Q S^T + M Delta), S_next =
+gamma[C-1] S + (diag(gamma[C-1] / gamma) Delta)^T K) with T folded into P
+and W, so phase B holds no C x C inverse and its chain is X^T, Y^T and the
+state update.
 """
 
 from __future__ import annotations
@@ -58,26 +64,35 @@ def invert_unit_lower(B, block=16):
     return T
 
 
-def chunk_prep(k, beta, g):
-    """State-independent per-chunk quantities (phase A).  k [C, Dk]; beta, g [C]."""
+def chunk_prep(q, k, beta, g):
+    """State-independent per-chunk quantities (phase A).  q, k [C, Dk];
+    beta, g [C].  Returns Gc, T, P, W."""
     Gc = np.cumsum(g)
     decay = np.exp(Gc[:, None] - Gc[None, :])
-    C = k.shape[0]
+    C, dk = k.shape
     lower = np.tril(np.ones((C, C), dtype=bool), -1)
+    causal = np.tril(np.ones((C, C), dtype=bool))
     A = np.where(lower, decay * (k @ k.T), 0.0)
+    M = np.where(causal, decay * (q @ k.T), 0.0)
     T = invert_unit_lower(beta[:, None] * A)
-    return Gc, T
+    P = (M @ T) * beta[None, :] / math.sqrt(dk)
+    W = np.exp(Gc[-1] - Gc)[:, None] * T * beta[None, :]
+    return Gc, T, P, W
 
 
-def delta_ub_w(S, k, v, beta, Gc, T):
-    """Delta in the unfolded form Ub V - W S^T (cross-check of T X)."""
-    Ub = T * beta[None, :]
-    W = Ub @ (np.exp(Gc)[:, None] * k)
-    return Ub @ v - W @ S.T
-
-
-def chunk_apply(S, q, k, v, beta, Gc, T):
+def chunk_apply(S, q, k, v, Gc, P, W):
     """Carry the state through one chunk (phase B); returns (outputs [C, Dv], S_next)."""
+    dk = q.shape[1]
+    XT = v - np.exp(Gc)[:, None] * (k @ S.T)
+    O = np.exp(Gc)[:, None] * (q @ S.T) / math.sqrt(dk) + P @ XT
+    YT = W @ XT
+    S_next = (math.exp(Gc[-1]) * S.T + k.T @ YT).T
+    return O, S_next
+
+
+def chunk_apply_delta(S, q, k, v, beta, Gc, T):
+    """The textbook chunk step with Delta = T diag(beta) X^T (cross-check of
+    the folded P / W form)."""
     dk = q.shape[1]
     C = q.shape[0]
     X = beta[:, None] * (v - np.exp(Gc)[:, None] * (k @ S.T))
@@ -88,6 +103,12 @@ def chunk_apply(S, q, k, v, beta, Gc, T):
     tail = np.exp(Gc[-1] - Gc)
     S_next = math.exp(Gc[-1]) * S + (tail[:, None] * Delta).T @ k
     return O, S_next
+
+
+def live_tiles(C=64):
+    """(m tile, k step) pairs of the 16 x 32 A-operand tiles of a causal C x C
+    matrix that can hold a nonzero (the ones phase A stores)."""
+    return [(mt, ks) for mt in range(C // 16) for ks in range(C // 32) if 32 * ks <= 16 * mt + 15]
 
 
 def gdn_chunked(state, q, k, v, beta, g, chunk=64):
@@ -105,8 +126,8 @@ def gdn_chunked(state, q, k, v, beta, g, chunk=64):
             s = slice(c0, c0 + chunk)
             qc, kc = q[s, kh].astype(np.float64), k[s, kh].astype(np.float64)
             bc = beta[s, h].astype(np.float64)
-            Gc, T = chunk_prep(kc, bc, g[s, h].astype(np.float64))
-            O, S = chunk_apply(S, qc, kc, v[s, h].astype(np.float64), bc, Gc, T)
+            Gc, _, P, W = chunk_prep(qc, kc, bc, g[s, h].astype(np.float64))
+            O, S = chunk_apply(S, qc, kc, v[s, h].astype(np.float64), Gc, P, W)
             out[s, h] = O
         state[h] = S
     return out

@@ -42,15 +42,37 @@ def test_chunked_c5_shape_slice():
     np.testing.assert_allclose(s_chk, s_seq, atol=1e-9)
 
 
-def test_folded_delta_equals_ub_w_form():
-    # Delta = T X (what phase B computes) against Ub V - W S^T formed
-    # separately, on one chunk with a nonzero state
+def test_folded_form_equals_delta_form():
+    # The P / W form phase B computes against the textbook chunk step with
+    # Delta = T diag(beta) X^T, on one chunk with a nonzero state and decays
     c = I.c5_gdn_bf16(tokens=64, hk=1, hv=1, dk=32, dv=24)
     rng = np.random.default_rng(2)
     S = rng.standard_normal((24, 32)) * 0.3
+    q = c["q"][:, 0].astype(np.float64)
     k = c["k"][:, 0].astype(np.float64)
     v = c["v"][:, 0].astype(np.float64)
     beta = c["beta"][:, 0].astype(np.float64)
-    Gc, T = CM.chunk_prep(k, beta, c["g"][:, 0].astype(np.float64))
-    X = beta[:, None] * (v - np.exp(Gc)[:, None] * (k @ S.T))
-    np.testing.assert_allclose(T @ X, CM.delta_ub_w(S, k, v, beta, Gc, T), atol=1e-12)
+    Gc, T, P, W = CM.chunk_prep(q, k, beta, c["g"][:, 0].astype(np.float64))
+    o1, s1 = CM.chunk_apply(S, q, k, v, Gc, P, W)
+    o2, s2 = CM.chunk_apply_delta(S, q, k, v, beta, Gc, T)
+    np.testing.assert_allclose(o1, o2, atol=1e-12)
+    np.testing.assert_allclose(s1, s2, atol=1e-12)
+
+
+def test_stored_tiles_cover_p_and_w():
+    # Phase A stores only the six 16 x 32 tiles of P and W that can be
+    # nonzero; every other tile is exactly zero (P and W are causal).
+    c = I.c5_gdn_bf16(tokens=64, hk=1, hv=1, dk=32, dv=24)
+    q = c["q"][:, 0].astype(np.float64)
+    k = c["k"][:, 0].astype(np.float64)
+    beta = c["beta"][:, 0].astype(np.float64)
+    _, _, P, W = CM.chunk_prep(q, k, beta, c["g"][:, 0].astype(np.float64))
+    live = set(CM.live_tiles())
+    assert len(live) == 6
+    for mat in (P, W):
+        for mt in range(4):
+            for ks in range(2):
+                tile = mat[16 * mt:16 * mt + 16, 32 * ks:32 * ks + 32]
+                if (mt, ks) not in live:
+                    assert not tile.any()
+        assert np.abs(np.triu(mat, 1)).max() == 0.0
