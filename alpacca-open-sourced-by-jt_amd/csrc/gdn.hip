@@ -544,13 +544,17 @@ gdn_apply(GdnArgs a) {
   constexpr int KS = DK / 32;
   constexpr int MT = DK / 64;     // state d tiles per wave
   constexpr int PF = DK <= 128 ? 2 : 1;  // chunks of operands in flight
-  constexpr int kSB = DK + 8;     // bf16 row stride of the state planes and K tile
+  constexpr int kSB = DK + 8;     // bf16 row stride of the state planes
+  // bf16 row stride of the K tile: 8 dwords past a multiple of 64 banks, so
+  // the transposing reads of step (3) (four rows x four column groups per
+  // 16 lanes) hit distinct banks
+  constexpr int kSK = DK + 16;
   constexpr int kXB = kC + 8;     // bf16 row stride of the X^T and Y^T planes
   constexpr int kVB = 24;         // bf16 row stride of the V tile
   constexpr int kOB = 16 + 16 / (int)sizeof(TO);  // TO row stride of the output tile
   __shared__ __attribute__((aligned(16))) bf16_t Sh[16 * kSB];  // S [r][d], hi
   __shared__ __attribute__((aligned(16))) bf16_t Sl[16 * kSB];  // S [r][d], lo
-  __shared__ __attribute__((aligned(16))) bf16_t Ks[kC * kSB];  // K [t][d]
+  __shared__ __attribute__((aligned(16))) bf16_t Ks[kC * kSK];  // K [t][d]
   __shared__ __attribute__((aligned(16))) bf16_t Xh[16 * kXB];  // X^T [r][t], hi
   __shared__ __attribute__((aligned(16))) bf16_t Xl[16 * kXB];  // X^T [r][t], lo
   __shared__ __attribute__((aligned(16))) bf16_t Yh[16 * kXB];  // Y^T [r][t], hi
@@ -688,7 +692,7 @@ gdn_apply(GdnArgs a) {
       qst = mfma16x16x32(kqc.q[ks], slo[ks], qst);
     }
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) *(bf16x8*)(Ks + (tw + hl) * kSB + 32 * ks + 8 * quad) = kqc.k[ks];
+    for (int ks = 0; ks < KS; ++ks) *(bf16x8*)(Ks + (tw + hl) * kSK + 32 * ks + 8 * quad) = kqc.k[ks];
     fetch_kq(kqc, cf);
     const bf16x4 v4 = lds_read_tr4(Vs + (tw + tr_row) * kVB + tr_col);
     const f32x4 g4 = *(const f32x4*)(Gs + tw + 4 * quad);
@@ -767,8 +771,8 @@ gdn_apply(GdnArgs a) {
       f32x4 acc = glin * sown[i];
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        const bf16x4 k0 = lds_read_tr4(Ks + (32 * ks + tr_row) * kSB + 16 * mt + tr_col);
-        const bf16x4 k1 = lds_read_tr4(Ks + (32 * ks + 16 + tr_row) * kSB + 16 * mt + tr_col);
+        const bf16x4 k0 = lds_read_tr4(Ks + (32 * ks + tr_row) * kSK + 16 * mt + tr_col);
+        const bf16x4 k1 = lds_read_tr4(Ks + (32 * ks + 16 + tr_row) * kSK + 16 * mt + tr_col);
         const bf16x8 ka = __builtin_shufflevector(k0, k1, 0, 1, 2, 3, 4, 5, 6, 7);
         acc = mfma16x16x32(ka, yhi[ks], acc);
         acc = mfma16x16x32(ka, ylo[ks], acc);
