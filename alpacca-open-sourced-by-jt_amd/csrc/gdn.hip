@@ -594,17 +594,25 @@ gdn_apply(GdnArgs a) {
   // Every load reads a clamped row and is issued unconditionally (per
   // wave); the rows of tokens past the end are zeroed where X^T is formed
   // and never stored, and their rows of W are zero.
+  // Per-block bases; the per-token offsets are 24-bit products (token index
+  // times a row of at most 2^24 elements, checked on the host), so address
+  // arithmetic stays off the quarter-rate 32 / 64-bit multiplies.
+  const int krow = a.Hk * DK, vrow = a.Hv * a.Dv;
+  const bf16_t* const kbase = (const bf16_t*)a.k + (int64_t)b * a.T * krow + kh * DK + 8 * quad;
+  const bf16_t* const qbase = (const bf16_t*)a.q + (int64_t)b * a.T * krow + kh * DK + 8 * quad;
+  const bf16_t* const vbase = (const bf16_t*)a.v + (int64_t)b * a.T * vrow + h * a.Dv + r0;
+  TO* const obase = (TO*)a.out + (int64_t)b * a.T * vrow + h * a.Dv + r0;
+  float* const wsbase = a.ws + bh * a.nchunks * ws_per_chunk();
   auto fetch_kq = [&](KqIn<DK>& in, int c) __attribute__((always_inline)) {
-    const int t = min(c * kC + tw + hl, a.T - 1);
-    const int64_t off = (((int64_t)b * a.T + t) * a.Hk + kh) * DK + 8 * quad;
+    const unsigned off = __umul24((unsigned)min(c * kC + tw + hl, a.T - 1), (unsigned)krow);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      in.k[ks] = *(const bf16x8*)((const bf16_t*)a.k + off + 32 * ks);
-      in.q[ks] = *(const bf16x8*)((const bf16_t*)a.q + off + 32 * ks);
+      in.k[ks] = *(const bf16x8*)(kbase + off + 32 * ks);
+      in.q[ks] = *(const bf16x8*)(qbase + off + 32 * ks);
     }
   };
   auto fetch_pw = [&](PwIn& in, int c) __attribute__((always_inline)) {
-    const ChunkWs w = chunk_ws(a.ws + (bh * a.nchunks + c) * ws_per_chunk());
+    const ChunkWs w = chunk_ws(wsbase + c * (int)ws_per_chunk());
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       if (tile_live(wave, ks)) {
@@ -618,11 +626,10 @@ gdn_apply(GdnArgs a) {
   };
   auto fetch_vg = [&](VgIn& in, int c) __attribute__((always_inline)) {
     if (wave < 2) {
-      const int t = min(c * kC + (tid >> 1), a.T - 1);
-      in.v = *(const bf16x8*)((const bf16_t*)a.v + (((int64_t)b * a.T + t) * a.Hv + h) * a.Dv +
-                              r0 + 8 * (tid & 1));
+      const unsigned t = (unsigned)min(c * kC + (tid >> 1), a.T - 1);
+      in.v = *(const bf16x8*)(vbase + __umul24(t, (unsigned)vrow) + 8 * (tid & 1));
     } else if (wave == 2 && lane < 16) {
-      in.g = *(const f32x4*)(a.ws + (bh * a.nchunks + c) * ws_per_chunk() + 4 * lane);
+      in.g = *(const f32x4*)(wsbase + c * (int)ws_per_chunk() + 4 * lane);
     }
   };
   auto stage_vg = [&](const VgIn& in, int c) __attribute__((always_inline)) {
@@ -642,8 +649,8 @@ gdn_apply(GdnArgs a) {
       const int u = u0 + tid;
       const int t = u / kUnitsRow, part = u % kUnitsRow;
       if (u < kC * kUnitsRow && c * kC + t < a.T)
-        *(u32x4*)((TO*)a.out + (((int64_t)b * a.T + c * kC + t) * a.Hv + h) * a.Dv + r0 +
-                  kPer * part) = *(const u32x4*)(Os + t * kOB + kPer * part);
+        *(u32x4*)(obase + __umul24((unsigned)(c * kC + t), (unsigned)vrow) + kPer * part) =
+            *(const u32x4*)(Os + t * kOB + kPer * part);
     }
   };
 
@@ -669,7 +676,6 @@ gdn_apply(GdnArgs a) {
   auto chunk = [&](int c, KqIn<DK>& kqc, PwIn& pwc, VgIn& vgn) __attribute__((always_inline)) {
     const int t0 = c * kC;
     const int cf = min(c + PF, a.nchunks - 1);
-    if (c > 0) flush_out(c - 1);
 
     // (1) K S^T and Q S^T for this wave's tokens (B = S^T: lane holds
     // S[r0 + hl][32 ks + 8 quad + 0..7]); X^T = V - diag(exp Gc) K S^T.  The
@@ -691,6 +697,8 @@ gdn_apply(GdnArgs a) {
       qst = mfma16x16x32(kqc.q[ks], shi[ks], qst);
       qst = mfma16x16x32(kqc.q[ks], slo[ks], qst);
     }
+    // The previous chunk's output tile goes out while the products run.
+    if (c > 0) flush_out(c - 1);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) *(bf16x8*)(Ks + (tw + hl) * kSK + 32 * ks + 8 * quad) = kqc.k[ks];
     fetch_kq(kqc, cf);
@@ -941,6 +949,8 @@ extern "C" int alpx_gdn_chunk_prefill(float* state, const void* q, const void* k
       (uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)state | (uintptr_t)out;
   const bool chunked = dtype == ALPX_BF16 && (key_dim == 64 || key_dim == 128 || key_dim == 256) &&
                        value_dim % 16 == 0 && (align & 15) == 0 &&
+                       tokens < (1 << 24) && key_heads * key_dim < (1 << 24) &&
+                       (int64_t)value_heads * value_dim < (1 << 24) &&
                        getenv("ALPX_GDN_SEQUENTIAL") == nullptr;
   TimedRegion timed(ALPX_T_GDN_CHUNK, s);
   if (chunked) {
