@@ -405,6 +405,33 @@ gdn_prep(GdnArgs a) {
     __syncthreads();
   }
 
+  // W = diag(exp(Gc_last - Gc)) T diag(beta), rows 16w..16w+15, straight
+  // from T as soon as T is complete, so its stores drain while P is formed:
+  // lane (hl, quad) forms row 16w + hl, columns 32 ks + 8 quad + 0..7.
+  {
+    const float rowf = fast_exp2((Gs[kC - 1] - Gs[16 * wave + hl]) * kLog2e);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      if (tile_live(wave, ks)) {
+        const float* tr = Tm + (16 * wave + hl) * kF + 32 * ks + 8 * quad;
+        const f32x4 x0 = *(const f32x4*)tr, x1 = *(const f32x4*)(tr + 4);
+        const f32x4 b0 = *(const f32x4*)(Bs + 32 * ks + 8 * quad);
+        const f32x4 b1 = *(const f32x4*)(Bs + 32 * ks + 8 * quad + 4);
+        float x[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          x[j] = rowf * x0[j] * b0[j];
+          x[4 + j] = rowf * x1[j] * b1[j];
+        }
+        bf16x8 hi, lo;
+        split8(x, hi, lo);
+        const int o = tile_off(wave, ks, lane);
+        __builtin_nontemporal_store(__builtin_bit_cast(u32x4, hi), (u32x4*)(out.w_hi + o));
+        __builtin_nontemporal_store(__builtin_bit_cast(u32x4, lo), (u32x4*)(out.w_lo + o));
+      }
+    }
+  }
+
   // From here each wave works on its own 16 rows of Bm's space (M, then P,
   // then a staging tile), so only wave-level ordering is needed.
   float* const Mw = Bm + 16 * wave * kF;
@@ -460,9 +487,9 @@ gdn_prep(GdnArgs a) {
     }
     wave_sync_lds();
     // P as hi / lo fragments: the wave's live tiles, one unit per lane each.
-  // Workspace stores are nontemporal: every block writes its fragments at
-  // the same late point, and streaming them out rather than leaving them
-  // dirty in L2 shortens the drain at the end of the kernel (2-3 us at C5).
+    // Workspace stores are nontemporal: every block writes its fragments at
+    // about the same late point, and streaming them out rather than leaving
+    // them dirty in L2 shortens the drain at the end of the kernel.
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       if (tile_live(wave, ks)) {
@@ -474,32 +501,6 @@ gdn_prep(GdnArgs a) {
         const int o = tile_off(wave, ks, lane);
         __builtin_nontemporal_store(__builtin_bit_cast(u32x4, hi), (u32x4*)(out.p_hi + o));
         __builtin_nontemporal_store(__builtin_bit_cast(u32x4, lo), (u32x4*)(out.p_lo + o));
-      }
-    }
-  }
-
-  // W = diag(exp(Gc_last - Gc)) T diag(beta), rows 16w..16w+15, straight
-  // from T: lane (hl, quad) forms row 16w + hl, columns 32 ks + 8 quad + 0..7.
-  {
-    const float rowf = fast_exp2((Gs[kC - 1] - Gs[16 * wave + hl]) * kLog2e);
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      if (tile_live(wave, ks)) {
-        const float* tr = Tm + (16 * wave + hl) * kF + 32 * ks + 8 * quad;
-        const f32x4 x0 = *(const f32x4*)tr, x1 = *(const f32x4*)(tr + 4);
-        const f32x4 b0 = *(const f32x4*)(Bs + 32 * ks + 8 * quad);
-        const f32x4 b1 = *(const f32x4*)(Bs + 32 * ks + 8 * quad + 4);
-        float x[8];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          x[j] = rowf * x0[j] * b0[j];
-          x[4 + j] = rowf * x1[j] * b1[j];
-        }
-        bf16x8 hi, lo;
-        split8(x, hi, lo);
-        const int o = tile_off(wave, ks, lane);
-        __builtin_nontemporal_store(__builtin_bit_cast(u32x4, hi), (u32x4*)(out.w_hi + o));
-        __builtin_nontemporal_store(__builtin_bit_cast(u32x4, lo), (u32x4*)(out.w_lo + o));
       }
     }
   }
