@@ -280,6 +280,14 @@ gdn_prep(GdnArgs a) {
   const bool tok_ok = t0 + lane < a.T;
   const int64_t goff = ((int64_t)b * a.T + min(t0 + lane, a.T - 1)) * a.Hv + h;
   const float graw = a.g[goff], braw = a.beta[goff];
+  // The strictly-upper blocks of T are zero (the full 64 x 64 T is read as
+  // is below); they are cleared here, where the waves wait for their loads.
+#pragma unroll
+  for (int j = 0; j < kC * kC / 256; ++j) {
+    const int idx = tid + 256 * j;
+    const int t = idx / kC, i = idx - (idx / kC) * kC;
+    if ((i >> 4) > (t >> 4)) Tm[t * kF + i] = 0.f;
+  }
   const bf16x8 zero8 = {};
 #pragma unroll
   for (int u = 0; u < kUPT; ++u) {
@@ -347,26 +355,22 @@ gdn_prep(GdnArgs a) {
   __syncthreads();
 
   // Diagonal 16x16 blocks of T = (I + Bm)^-1 by forward substitution:
-  // wave w, lane j < 16 owns column j of block w.
+  // wave w, lane j < 16 owns column j of block w.  Column-oriented: once
+  // entry i of the column is final it is subtracted from every later entry,
+  // so each step's updates are independent of each other and the dependent
+  // chain is 16 steps long instead of 120.
   if (lane < 16) {
     const int base = 16 * wave;
     float col[16];
 #pragma unroll
-    for (int t = 0; t < 16; ++t) {
-      float acc = t == lane ? 1.f : 0.f;
+    for (int t = 0; t < 16; ++t) col[t] = t == lane ? 1.f : 0.f;
 #pragma unroll
-      for (int i = 0; i < t; ++i) acc -= Bm[(base + t) * kF + base + i] * col[i];
-      col[t] = acc;
+    for (int i = 0; i < 15; ++i) {
+#pragma unroll
+      for (int t = i + 1; t < 16; ++t) col[t] -= Bm[(base + t) * kF + base + i] * col[i];
     }
 #pragma unroll
     for (int t = 0; t < 16; ++t) Tm[(base + t) * kF + base + lane] = col[t];
-  }
-  // Zero the strictly-upper blocks so the full 64 x 64 T can be read as is.
-#pragma unroll
-  for (int j = 0; j < kC * kC / 256; ++j) {
-    const int idx = tid + 256 * j;
-    const int t = idx / kC, i = idx - (idx / kC) * kC;
-    if ((i >> 4) > (t >> 4)) Tm[t * kF + i] = 0.f;
   }
   __syncthreads();
 
