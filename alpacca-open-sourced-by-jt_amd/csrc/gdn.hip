@@ -242,28 +242,41 @@ __device__ __forceinline__ int tile_off(int mt, int ks, int lane) {
 
 // ------------------------------------------------------------ phase A
 
-template <int DK>
-__global__ void __launch_bounds__(256)
+// NG value heads of one key head per block (the value heads h with
+// h % Hk = kh share K and Q): four waves per value head, one load of the
+// chunk's K and Q rows for all of them.
+template <int DK, int NG>
+__global__ void __launch_bounds__(256 * NG)
 gdn_prep(GdnArgs a) {
   constexpr int kS = DK + 8;   // bf16 LDS row stride
   constexpr int kF = kC + 4;   // fp32 LDS row stride
   constexpr int KS = DK / 32;
   constexpr int kUnits = DK / 8;
-  constexpr int kUPT = kC * kUnits / 256;
+  constexpr int kUPT = kC * kUnits / (256 * NG);
+  static_assert(kUPT * 256 * NG == kC * kUnits, "K / Q rows must split evenly over the block");
   __shared__ __attribute__((aligned(16))) bf16_t Ks[kC * kS];
   __shared__ __attribute__((aligned(16))) bf16_t Qs[kC * kS];
-  // diag(beta) A, then (per wave, its own 16 rows) M, P and a staging tile
-  __shared__ __attribute__((aligned(16))) float Bm[kC * kF];
-  __shared__ __attribute__((aligned(16))) float Tm[kC * kF];
-  __shared__ __attribute__((aligned(16))) float Xs[4][16 * 17];
-  __shared__ __attribute__((aligned(16))) float Gs[kC];
-  __shared__ __attribute__((aligned(16))) float Bs[kC];
+  // Per value head: diag(beta) A, then (per wave, its own 16 rows) M, P and
+  // a staging tile; T; the block-recursion exchange; Gc; beta.
+  __shared__ __attribute__((aligned(16))) float Bm_[NG][kC * kF];
+  __shared__ __attribute__((aligned(16))) float Tm_[NG][kC * kF];
+  __shared__ __attribute__((aligned(16))) float Xs_[NG][4][16 * 17];
+  __shared__ __attribute__((aligned(16))) float Gs_[NG][kC];
+  __shared__ __attribute__((aligned(16))) float Bs_[NG][kC];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int gtid = threadIdx.x;
+  const int grp = __builtin_amdgcn_readfirstlane(gtid >> 8);  // value head of the block
+  const int tid = gtid & 255, lane = tid & 63, wave = tid >> 6;
   const int hl = lane & 15, quad = lane >> 4;
-  const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int kh = h % a.Hk;
+  const int c = blockIdx.x, b = blockIdx.z;
+  const int kh = (int)blockIdx.y % a.Hk;
+  const int h = kh + a.Hk * (NG * ((int)blockIdx.y / a.Hk) + grp);
   const int t0 = c * kC;
+  float* const Bm = Bm_[grp];
+  float* const Tm = Tm_[grp];
+  float (*const Xs)[16 * 17] = Xs_[grp];
+  float* const Gs = Gs_[grp];
+  float* const Bs = Bs_[grp];
 
   // K, Q rows of the chunk, g and beta: every load reads a clamped row and
   // is issued before any is used, so they are all in flight together; rows
@@ -271,7 +284,7 @@ gdn_prep(GdnArgs a) {
   bf16x8 kv[kUPT], qv[kUPT];
 #pragma unroll
   for (int u = 0; u < kUPT; ++u) {
-    const int idx = u * 256 + tid;
+    const int idx = u * 256 * NG + gtid;
     const int r = idx / kUnits, cc = idx - (idx / kUnits) * kUnits;
     const int64_t off = (((int64_t)b * a.T + min(t0 + r, a.T - 1)) * a.Hk + kh) * DK + 8 * cc;
     kv[u] = *(const bf16x8*)((const bf16_t*)a.k + off);
@@ -291,7 +304,7 @@ gdn_prep(GdnArgs a) {
   const bf16x8 zero8 = {};
 #pragma unroll
   for (int u = 0; u < kUPT; ++u) {
-    const int idx = u * 256 + tid;
+    const int idx = u * 256 * NG + gtid;
     const int r = idx / kUnits, cc = idx - (idx / kUnits) * kUnits;
     const bool ok = t0 + r < a.T;
     *(bf16x8*)(Ks + r * kS + 8 * cc) = ok ? kv[u] : zero8;
@@ -808,7 +821,10 @@ gdn_apply(GdnArgs a) {
 
 template <int DK, typename TO>
 int launch_chunk(const GdnArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL((gdn_prep<DK>), dim3(a.nchunks, a.Hv, a.B), dim3(256), 0, s, a);
+  if ((a.Hv / a.Hk) % 2 == 0)
+    hipLaunchKernelGGL((gdn_prep<DK, 2>), dim3(a.nchunks, a.Hv / 2, a.B), dim3(512), 0, s, a);
+  else
+    hipLaunchKernelGGL((gdn_prep<DK, 1>), dim3(a.nchunks, a.Hv, a.B), dim3(256), 0, s, a);
   int rc = check_launch("gdn_prep");
   if (rc != ALPX_OK) return rc;
   hipLaunchKernelGGL((gdn_apply<TO, DK>), dim3(a.Dv / 16 * a.Hv * a.B), dim3(256), 0, s, a);

@@ -103,7 +103,8 @@ def test_c5_chunked_prefill_then_decode_full(gpu, ops):
 
 
 @pytest.mark.parametrize("tokens,dk,dv,hk,hv", [(100, 128, 128, 2, 4), (64, 64, 32, 1, 2),
-                                                (150, 256, 64, 2, 2), (37, 128, 16, 1, 1)])
+                                                (150, 256, 64, 2, 2), (37, 128, 16, 1, 1),
+                                                (70, 128, 32, 1, 4), (40, 64, 16, 2, 6)])
 def test_chunked_shapes_and_partial_chunks(gpu, ops, tokens, dk, dv, hk, hv):
     out, S, ref, ref_state = _c5_run(ops, gpu, tokens=tokens, prefill=tokens, hk=hk, hv=hv,
                                      dk=dk, dv=dv, seed=tokens)
