@@ -770,7 +770,6 @@ gdn_apply(GdnArgs a) {
       *(bf16x4*)(Yh + hl * kXB + tw + 4 * quad) = hi;
       *(bf16x4*)(Yl + hl * kXB + tw + 4 * quad) = lo;
     }
-    fetch_pw(pwc, cf);
     stage_vg(vgn, c + 1);
     fetch_vg(vgn, min(c + 1 + PF, a.nchunks - 1));
 #pragma unroll
@@ -805,6 +804,9 @@ gdn_apply(GdnArgs a) {
       }
       sown[i] = acc;
     }
+    // P and W of chunk c + PF: issued here rather than with step (2)'s
+    // other loads, so each step issues about a third of the chunk's loads.
+    fetch_pw(pwc, cf);
     put_state();
     __syncthreads();  // new state published; every wave has read Y^T and the K tile
   };
