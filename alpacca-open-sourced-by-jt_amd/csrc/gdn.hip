@@ -13,23 +13,24 @@
 //
 // Chunked prefill (bf16 inputs, chunks of 64 tokens, Dk 64/128/256).  With
 // gamma_t = exp(Gc_t), Gc = cumsum(g) within the chunk, S the state entering
-// the chunk, A = (gamma_t / gamma_i k_t.k_i)_{i<t},
+// the chunk, scale = 1 / sqrt(Dk), A = (gamma_t / gamma_i k_t.k_i)_{i<t},
 // M = (gamma_t / gamma_i q_t.k_i)_{i<=t} and T = (I + diag(beta) A)^-1, the
 // delta rule over the chunk is
 //    X^T = V - diag(gamma) K S^T                       (L x Dv)
 //    O   = scale diag(gamma) Q S^T + P X^T,            P = scale M T diag(beta)
-//    S^T <- gamma_L S^T + Qm^T X^T,                    Qm^T = K^T diag(gamma_L / gamma) T diag(beta)
-//  phase A, gdn_prep, one block per (sequence, head, chunk), state-free:
-//    Gc, K K^T and Q K^T on bf16 MFMA (exact products of bf16 inputs, fp32
-//    sums), T by 16x16 forward substitution plus a block recursion, then P
-//    and Qm^T; P and Qm^T are stored split into hi and lo bf16 planes (the
-//    same bytes as fp32) as ready-made MFMA operands.
+//    S^T <- gamma_L S^T + K^T (W X^T),                 W = diag(gamma_L / gamma) T diag(beta)
+//  phase A, gdn_prep, one block per (sequence, chunk, pair of value heads
+//    sharing a key head), state-free: Gc, K K^T and Q K^T on bf16 MFMA
+//    (exact products of bf16 inputs, fp32 sums), T by 16x16 forward
+//    substitution plus a block recursion, then W and P; both are causal, and
+//    their live 16 x 32 tiles are stored split into hi and lo bf16 planes
+//    (the same bytes as fp32) as ready-made MFMA operands.
 //  phase B, gdn_apply, one block per (sequence, head, 16 state rows),
-//    sequential over chunks: only X^T and the state update are on the
-//    chunk-to-chunk chain (two products and two block barriers per chunk);
-//    Q S^T and P X^T for the output ride alongside.  The state slice stays
-//    in fp32 registers of the wave that updates it and is published to the
-//    other waves as hi / lo planes in LDS.
+//    sequential over chunks in three steps with a block barrier after each:
+//    K S^T and X^T, then Y^T = W X^T, then the state update; Q S^T and
+//    P X^T for the output ride alongside.  The state slice stays in fp32
+//    registers of the wave that updates it and is published to the other
+//    waves as hi / lo planes in LDS.
 //    fp32 x fp32 products use three bf16 MFMAs (hi.hi + hi.lo + lo.hi),
 //    fp32 x bf16 products two, so the state keeps ~fp32 accuracy.
 // Tokens past the end of the last chunk are padded as k = q = v = 0,
