@@ -920,12 +920,16 @@ size_t workspace_for(int batch, int q_heads, int value_dim, int nsplit) {
 // `batch` more for the sequences' last partial chunks.
 constexpr int kMaxItemsPerRow = 256;
 // items_target = resident blocks per grid row x NUM / DEN - batch x SUB / 2
-// Two rounds of blocks (measured on C2 ragged: split kernel 75.8% of HBM
-// against 69.6% with one round, the dispatcher filling the slots of blocks
-// that finish early).
+// Two and a half rounds of blocks (measured on C2 ragged, same box: step
+// 70.1-70.4% of HBM against 69.2-69.5% with two rounds and 66.8-67.0% with
+// three, whose extra partials cost more in the combine than the finer
+// balance gains; one round 64%).  Laying the padded sequences end to end and
+// giving every block the same row count (blocks crossing a sequence boundary
+// processing two segments) measured 64.7-66.1%: a segment's pipeline start
+// and merge cost more than the tail imbalance it removes.
 #ifndef ALPX_BALANCED_NUM
-#define ALPX_BALANCED_NUM 2
-#define ALPX_BALANCED_DEN 1
+#define ALPX_BALANCED_NUM 5
+#define ALPX_BALANCED_DEN 2
 #define ALPX_BALANCED_SUB 0
 #endif
 
