@@ -57,6 +57,9 @@ SIGNATURES = {
                                            _c_size, _c_int, _c_int, _c_int, _c_int, _c_int,
                                            _c_int, _c_i64, _c_i64, _c_i64, _c_int, _c_i64,
                                            _c_float, _c_int, _c_int, _c_ptr]),
+    "alpx_prefill_append": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
+                                     _c_ptr, _c_size, _c_int, _c_i64, _c_int, _c_int, _c_int,
+                                     _c_int, _c_i64, _c_int, _c_float, _c_int, _c_int, _c_ptr]),
     "alpx_gdn_step": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int,
                                _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_ptr]),
     "alpx_gdn_chunk_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int]),

@@ -87,6 +87,40 @@ def decode_paged(q, key_pages, value_pages, block_table, *, length, seq_lens=Non
     return out
 
 
+def prefill_append(q, key, value, key_cache, value_cache, *, position, scale=None, window=0,
+                   out_dtype=None, gate=None):
+    """Writes the chunk's rows ``key/value [T, Hkv, D]`` to rows ``position ..``
+    of the batch-1 caches ``[C, 1, Hkv, D]`` and returns the causal prefill
+    of ``q [T, Hq, D]`` over cache rows ``0 .. position + t`` (one launch on
+    the MFMA path)."""
+    torch = _torch()
+    q_tokens, q_heads, key_dim = (int(x) for x in q.shape)
+    capacity, _, kv_heads, _ = (int(x) for x in key_cache.shape)
+    value_dim = int(value_cache.shape[3])
+    if scale is None:
+        scale = 1.0 / math.sqrt(key_dim)
+    out_dtype = q.dtype if out_dtype is None else out_dtype
+    out = torch.empty((q_tokens, q_heads, value_dim), dtype=out_dtype, device=q.device)
+    L = _lib.lib()
+    fast = (q.dtype != torch.float32 and key_dim == value_dim and key_dim in (64, 128, 256))
+    ws = None
+    if not fast:
+        nbytes = L.alpx_prefill_workspace_bytes(q_tokens, q_heads, kv_heads, value_dim,
+                                                int(position) + q_tokens)
+        if nbytes == 0:
+            raise ValueError("invalid prefill sizes")
+        ws = _lib.workspace(torch, q.device, nbytes)
+    rc = L.alpx_prefill_append(
+        q.data_ptr(), key.data_ptr(), value.data_ptr(), key_cache.data_ptr(),
+        value_cache.data_ptr(), None if gate is None else gate.data_ptr(), out.data_ptr(),
+        None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), q_tokens,
+        capacity, q_heads, kv_heads, key_dim, value_dim, int(position), int(window),
+        float(scale), _lib.dtype_code(torch, q.dtype), _lib.dtype_code(torch, out.dtype),
+        _lib.stream_handle(torch, q.device))
+    _lib.check(rc)
+    return out
+
+
 def prefill_paged(q, key_pages, value_pages, block_table, *, batch_index, pos0, kv_tokens,
                   scale=None, window=0, kv_start=0, gate=None):
     """Causal prefill of ``q [T, Hq, D]`` at positions ``pos0 ..`` over the

@@ -55,6 +55,13 @@ struct PrefillArgs {
   int page_shift;
   int num_pages;
   int64_t ks_page, vs_page;
+  // Append mode (contiguous kernels): kn / vn hold the chunk's own K / V
+  // rows, row i being cache row new0 + i (same row strides as the cache).
+  // Tiles take rows >= new0 from them, and each block writes its tokens'
+  // rows into the cache (k / v), so no launch has to append them first.
+  const void* kn;
+  const void* vn;
+  int new0;
 };
 
 constexpr int kXcds = 8;  // MI355X: workgroup b is dispatched to XCD b % 8
@@ -111,8 +118,7 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 // Buffer resource words of a raw (stride 0) buffer of `bytes` bytes at
 // `base`; loads at offsets past `bytes` return zero.
-__device__ __forceinline__ i32x4 rsrc_words(const void* base, uint32_t bytes) {
-  const uint64_t p = (uint64_t)(uintptr_t)base;
+__device__ __forceinline__ i32x4 rsrc_words(uint64_t p, uint32_t bytes) {
   return (i32x4){(int)(uint32_t)p, (int)((uint32_t)(p >> 32) & 0xffffu), (int)bytes, 0x00020000};
 }
 
@@ -243,6 +249,44 @@ prefill_mfma(PrefillArgs a) {
   const int col0 = ctile * kCols;
   const int wcol0 = col0 + kWaveCols * wave;
 
+  // Append mode: the K and V rows (head kvh) of the tokens whose first
+  // column lies in column tile ct are copied into the cache, 16 bytes per
+  // lane, four loads in flight (clamped, so unconditional) before the
+  // stores.  No block of this launch reads those cache rows: tiles take
+  // them from kn / vn.
+  auto copy_rows = [&](int ct) {
+    const int t0 = (ct * kCols + G - 1) / G;
+    const int t1 = min(a.q_tokens, ((ct + 1) * kCols + G - 1) / G);
+    const int units = max(0, t1 - t0) * 2 * U;
+    for (int u0 = 0; u0 < units; u0 += 4 * 256) {
+      u32x4 x[4];
+      T* dst[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int u = min(u0 + 256 * k + tid, units - 1);
+        const int r = t0 + u / (2 * U), part = u % (2 * U);
+        const bool val = part >= U;
+        const int64_t pos = val ? a.vs_pos : a.ks_pos;
+        const int64_t col = (int64_t)kvh * D + 8 * (part - (val ? U : 0));
+        x[k] = *(const u32x4*)((const T*)(val ? a.vn : a.kn) + (int64_t)r * pos + col);
+        // the caches are written here and nowhere else in the kernel
+        dst[k] = (T*)const_cast<void*>(val ? a.v : a.k) + (int64_t)(a.new0 + r) * pos + col;
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        if (u0 + 256 * k + tid < units) *(u32x4*)dst[k] = x[k];
+    }
+  };
+
+  // The heavy column tiles (late tokens, many key tiles) set the kernel's
+  // end time, so of each tile and its mirror col_tiles - 1 - ctile the
+  // lighter one copies both tiles' rows (each tile's rows exactly once).
+  if (!PAGED && a.kn != nullptr) {
+    const int mirror = a.col_tiles - 1 - ctile;
+    if (ctile <= mirror) copy_rows(ctile);
+    if (ctile < mirror) copy_rows(mirror);
+  }
+
   int tok[NQB], hq[NQB];
   bool cok[NQB];
 #pragma unroll
@@ -321,6 +365,8 @@ prefill_mfma(PrefillArgs a) {
   }
   const T* kg = (const T*)a.k + (int64_t)kvh * D;
   const T* vg = (const T*)a.v + (int64_t)kvh * D;
+  const T* kgn = a.kn != nullptr ? (const T*)a.kn + (int64_t)kvh * D : nullptr;
+  const T* vgn = a.vn != nullptr ? (const T*)a.vn + (int64_t)kvh * D : nullptr;
   // Paged: the block's page numbers (clamped) are staged in LDS once, so a
   // tile's page lookup is an LDS read rather than a global load on the
   // path to its tile loads; ranges of more than kPageSlots pages look up
@@ -353,16 +399,40 @@ prefill_mfma(PrefillArgs a) {
     }
     return 0;
   };
-  auto load_tile = [&](const T* g, int64_t pos, int64_t page_stride, const uint32_t (&ofs)[kIW],
-                       int t, int buf, int pg) {
+  // gn: the chunk's own rows of this head (append mode), else null.
+  auto load_tile = [&](const T* g, const T* gn, int64_t pos, int64_t page_stride,
+                       const uint32_t (&ofs)[kIW], int t, int buf, int pg) {
     const int k0 = lo + t * BK;
     const T* base = g + (int64_t)k0 * pos;
     if constexpr (PAGED)
       base = g + (int64_t)pg * page_stride + (int64_t)(k0 & ((1 << a.page_shift) - 1)) * pos;
-    const i32x4 r = rsrc_words(
-        base, (uint32_t)((int64_t)(a.kv_tokens - k0) * pos * (int64_t)sizeof(T)));
+    const uint32_t bytes = (uint32_t)((int64_t)(a.kv_tokens - k0) * pos * (int64_t)sizeof(T));
     const uint32_t lds0 =
         (uint32_t)(uintptr_t)(lds_void_t*)(smem + buf * kTileB + wave * kIW * 1024);
+    if (!PAGED && gn != nullptr && k0 + BK > a.new0) {
+      // Rows >= new0 come from the chunk's rows: a resource whose offset of
+      // tile row i is the one of row k0 + i, based new0 - k0 rows before gn.
+      const i32x4 rn = rsrc_words(
+          (uint64_t)(uintptr_t)gn + (uint64_t)((int64_t)(k0 - a.new0) * pos * (int64_t)sizeof(T)),
+          bytes);
+      if (k0 >= a.new0) {
+#pragma unroll
+        for (int i = 0; i < kIW; ++i) lds_dma16(rn, lds0 + i * 1024, ofs[i]);
+        return;
+      }
+      // A tile across new0: each lane loads from the side its row is on.
+      const i32x4 rc = rsrc_words((uint64_t)(uintptr_t)base,
+                                  (uint32_t)((int64_t)(a.new0 - k0) * pos * (int64_t)sizeof(T)));
+#pragma unroll
+      for (int i = 0; i < kIW; ++i) {
+        if (((wave * kIW + i) * 64 + lane) / U < a.new0 - k0)
+          lds_dma16(rc, lds0 + i * 1024, ofs[i]);
+        else
+          lds_dma16(rn, lds0 + i * 1024, ofs[i]);
+      }
+      return;
+    }
+    const i32x4 r = rsrc_words((uint64_t)(uintptr_t)base, bytes);
 #pragma unroll
     for (int i = 0; i < kIW; ++i) lds_dma16(r, lds0 + i * 1024, ofs[i]);
   };
@@ -566,9 +636,9 @@ prefill_mfma(PrefillArgs a) {
     const int v_page = kpage[P];  // page of tile j, looked up with K(j)
     if (j + 2 < nt) {
       if constexpr (PAGED) kpage[P] = tile_page(j + 2);
-      load_tile(kg, a.ks_pos, a.ks_page, kofs, j + 2, P, kpage[P]);
+      load_tile(kg, kgn, a.ks_pos, a.ks_page, kofs, j + 2, P, kpage[P]);
     }
-    if (j < nt) load_tile(vg, a.vs_pos, a.vs_page, vofs, j, 2 + P, v_page);
+    if (j < nt) load_tile(vg, vgn, a.vs_pos, a.vs_page, vofs, j, 2 + P, v_page);
     // Rescale for the m moved at tile j - 1 (O holds tiles <= j - 2 and is
     // about to take PV(j - 1), formed against the moved m; l was rescaled
     // at the move, before it took tile j - 1's P).
@@ -619,11 +689,11 @@ prefill_mfma(PrefillArgs a) {
     for (int qb = 0; qb < NQB; ++qb) pv[1][kk][qb] = (V8){};
   if (nt > 0) {
     if constexpr (PAGED) kpage[0] = tile_page(0);
-    load_tile(kg, a.ks_pos, a.ks_page, kofs, 0, 0, kpage[0]);
+    load_tile(kg, kgn, a.ks_pos, a.ks_page, kofs, 0, 0, kpage[0]);
   }
   if (nt > 1) {
     if constexpr (PAGED) kpage[1] = tile_page(1);
-    load_tile(kg, a.ks_pos, a.ks_page, kofs, 1, 1, kpage[1]);
+    load_tile(kg, kgn, a.ks_pos, a.ks_page, kofs, 1, 1, kpage[1]);
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
@@ -715,7 +785,8 @@ int prefill_impl(const void* q, const void* key, const void* value, const void* 
                  int q_heads, int kv_heads, int key_dim, int value_dim, int64_t k_pos_stride,
                  int64_t v_pos_stride, int64_t q_pos0, int window, int64_t kv_start, float scale,
                  int dtype, int out_dtype, void* stream, const int32_t* pages = nullptr,
-                 int page_shift = 0, int num_pages = 0) {
+                 int page_shift = 0, int num_pages = 0, const void* kn = nullptr,
+                 const void* vn = nullptr) {
   using namespace alpx;
   if (!q || !key || !value || !out) return fail(ALPX_EINVAL, "alpx_prefill_causal: null buffer");
   if (!dtype_ok(dtype) || !dtype_ok(out_dtype))
@@ -737,8 +808,13 @@ int prefill_impl(const void* q, const void* key, const void* value, const void* 
   hipStream_t s = (hipStream_t)stream;
   const int group = q_heads / kv_heads;
   const size_t es = dtype_size(dtype);
+  // Append mode reads the chunk's rows through the cache's row strides.
+  if (kn != nullptr && (k_pos_stride != (int64_t)kv_heads * key_dim ||
+                        v_pos_stride != (int64_t)kv_heads * value_dim))
+    return fail(ALPX_EINVAL, "alpx_prefill_append: cache rows must be contiguous");
   const uintptr_t align = (uintptr_t)q | (uintptr_t)key | (uintptr_t)value | (uintptr_t)gate |
-                          (uintptr_t)(k_pos_stride * es) | (uintptr_t)(v_pos_stride * es);
+                          (uintptr_t)kn | (uintptr_t)vn | (uintptr_t)(k_pos_stride * es) |
+                          (uintptr_t)(v_pos_stride * es);
   const bool mfma = dtype != ALPX_F32 && key_dim == value_dim &&
                     (key_dim == 64 || key_dim == 128 || key_dim == 256) && (align & 15) == 0 &&
                     getenv("ALPX_PREFILL_GENERIC") == nullptr;
@@ -760,6 +836,9 @@ int prefill_impl(const void* q, const void* key, const void* value, const void* 
     else
       kernel = pick_kernel_out<bf16_t>(key_dim, out_dtype);
     PrefillArgs a = {};
+    a.kn = kn;
+    a.vn = vn;
+    a.new0 = (int)(q_pos0 - kv_start);
     a.pages = pages;
     a.page_shift = page_shift;
     a.num_pages = num_pages;
@@ -795,6 +874,12 @@ int prefill_impl(const void* q, const void* key, const void* value, const void* 
   }
 
   if (!workspace) return fail(ALPX_EINVAL, "alpx_prefill_causal: null workspace");
+  if (kn != nullptr) {  // append mode off the MFMA path: the append kernel first
+    const int rc = alpx_kv_append(const_cast<void*>(key), const_cast<void*>(value), kn, vn, dtype,
+                                  kv_tokens, 1, kv_heads, key_dim, value_dim, q_tokens,
+                                  q_pos0 - kv_start, nullptr, stream);
+    if (rc != ALPX_OK) return rc;
+  }
   DecodeArgs a = {};
   a.q = q;
   a.k = key;
@@ -847,6 +932,27 @@ extern "C" int alpx_prefill_causal_gated(const void* q, const void* key, const v
   return prefill_impl(q, key, value, gate, out, workspace, workspace_bytes, q_tokens, kv_tokens,
                       q_heads, kv_heads, key_dim, value_dim, k_pos_stride, v_pos_stride, q_pos0,
                       window, kv_start, scale, dtype, out_dtype, stream);
+}
+
+extern "C" int alpx_prefill_append(const void* q, const void* key, const void* value,
+                                   void* key_cache, void* value_cache, const void* gate, void* out,
+                                   void* workspace, size_t workspace_bytes, int q_tokens,
+                                   int64_t capacity, int q_heads, int kv_heads, int key_dim,
+                                   int value_dim, int64_t position, int window, float scale,
+                                   int dtype, int out_dtype, void* stream) {
+  using namespace alpx;
+  if (!key || !value || !key_cache || !value_cache)
+    return fail(ALPX_EINVAL, "alpx_prefill_append: null buffer");
+  if (q_tokens <= 0 || capacity <= 0 || kv_heads <= 0 || key_dim <= 0 || value_dim <= 0)
+    return fail(ALPX_EINVAL, "alpx_prefill_append: sizes must be positive");
+  if (position < 0 || position > capacity - q_tokens)
+    return fail(ALPX_ERANGE, "attention cache position exceeds capacity");
+  if (position + q_tokens > INT32_MAX)
+    return fail(ALPX_EUNSUPPORTED, "alpx_prefill_append: more than 2^31 - 1 cache rows");
+  return prefill_impl(q, key_cache, value_cache, gate, out, workspace, workspace_bytes, q_tokens,
+                      (int)(position + q_tokens), q_heads, kv_heads, key_dim, value_dim,
+                      (int64_t)kv_heads * key_dim, (int64_t)kv_heads * value_dim, position, window,
+                      0, scale, dtype, out_dtype, stream, nullptr, 0, 0, key, value);
 }
 
 extern "C" int alpx_prefill_causal_paged(const void* q, const void* key_pages,

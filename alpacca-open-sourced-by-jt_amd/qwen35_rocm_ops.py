@@ -438,18 +438,41 @@ class Qwen35RocmOps:
                                   scale: float | None = None) -> tuple[Any, int]:
         """Prefill-chunk form of ``append_online_attention_`` for a batch-1
         cache (extension): append ``key/value [T, Hkv, D]`` at ``position``
-        (bit-exact), then causal prefill attention of ``query [T, Hq, D]``.
-        Returns ``(output [T, Hq, Dv], position + T)``."""
+        (bit-exact), then causal prefill attention of ``query [T, Hq, D]``
+        over cache rows ``0 .. position + t``.  One kernel does both on the
+        MFMA path (it reads the chunk's rows from ``key/value`` and writes
+        them to the caches).  Returns ``(output [T, Hq, Dv], position + T)``."""
+        query = self._tensor(query, "prefill query", dimensions=3)
         key_cache = self._tensor(key_cache, "attention key cache", dimensions=4)
-        if int(key_cache.shape[1]) != 1:
-            raise ValueError("append_prefill_attention_ needs a batch-1 cache")
+        value_cache = self._tensor(value_cache, "attention value cache", dimensions=4)
         key = self._tensor(key, "attention key rows", dimensions=3)
         value = self._tensor(value, "attention value rows", dimensions=3)
-        self.attention_append_rows_(key_cache, value_cache, key.unsqueeze(1),
-                                    value.unsqueeze(1), position=position)
-        out = self.attention_prefill(query, key_cache, value_cache, position=position,
-                                     scale=scale)
-        return out, position + int(key.shape[0])
+        capacity, batch, kv_heads, key_width = _shape(key_cache)
+        if batch != 1:
+            raise ValueError("append_prefill_attention_ needs a batch-1 cache")
+        value_shape = _shape(value_cache)
+        if value_shape[:3] != (capacity, batch, kv_heads):
+            raise ValueError("attention K/V cache capacity, batch, or heads differ")
+        if _shape(key)[1:] != (kv_heads, key_width) or _shape(value)[1:] != value_shape[2:]:
+            raise ValueError("attention rows do not match cache token shape")
+        tokens, query_heads, query_width = _shape(query)
+        if int(key.shape[0]) != int(value.shape[0]):
+            raise ValueError("attention K/V row counts differ")
+        if int(key.shape[0]) != tokens:
+            raise ValueError("prefill query and K/V row counts differ")
+        position = _nonnegative_integer("attention cache position", position)
+        if position + tokens > capacity:
+            raise ValueError("attention cache position exceeds capacity")
+        if query_width != key_width:
+            raise ValueError("prefill query does not match K cache head width")
+        if query_heads % kv_heads:
+            raise ValueError("attention query heads must be a multiple of KV heads")
+        self._same_dtype("prefill", query, key_cache, value_cache, key, value)
+        scale_value = (1.0 / math.sqrt(key_width) if scale is None
+                       else _positive_finite("attention scale", scale))
+        out = _ops.prefill_append(query, key, value, key_cache, value_cache, position=position,
+                                  scale=scale_value)
+        return out, position + tokens
 
     # ------------------------------------------------------------ recurrence
 

@@ -77,6 +77,19 @@ def _timed_steps(torch, fn, steps, warmup):
     return (time.perf_counter() - t0) / steps * 1e3
 
 
+def _warm(torch, fn, seconds):
+    """Calls ``fn`` for about ``seconds`` (at least once): the device clock
+    takes tens of milliseconds of steady work to settle, and a ~0.1 ms
+    kernel measured after a handful of warmup calls reads a few percent
+    slow."""
+    t0 = time.perf_counter()
+    while True:
+        fn()
+        torch.cuda.synchronize()
+        if time.perf_counter() - t0 >= seconds:
+            return
+
+
 GRAPH_CALLS = 32  # calls captured per graph: one graph launch per 32 decode steps
 
 
@@ -252,8 +265,12 @@ def bench_prefill(torch, ops, lib, *, steps, warmup, seed=3):
     """C3: the 2048 new K/V rows of a bf16 chunk appended at rows 2048..4095
     of a [4096, 1, 8, 128] cache, then causal prefill of the chunk's 2048
     queries (32 heads) over 4096 positions.  The timed step is append +
-    prefill (append_prefill_attention_); the attention kernel alone is timed
-    with HIP events.  FLOPs count causal-valid pairs only."""
+    prefill (append_prefill_attention_: one prefill_mfma launch in append
+    mode, which reads the chunk's rows from k_new / v_new and writes them to
+    the cache); that kernel is timed with HIP events.  Beside it: the
+    attention kernel alone (rows already in the cache) and the two-launch
+    form (kv_append, then the prefill), host-timed per step and per kernel.
+    FLOPs count causal-valid pairs only."""
     g = torch.Generator(device="cuda").manual_seed(seed)
     dev = torch.device("cuda")
     bf = torch.bfloat16
@@ -265,10 +282,17 @@ def bench_prefill(torch, ops, lib, *, steps, warmup, seed=3):
     v_new = torch.randn((tq, hkv, d), generator=g, device=dev).to(bf)
     step = lambda: ops.append_prefill_attention_(q, k_new, v_new, K, V,  # noqa: E731
                                                  position=prefix)
+    _warm(torch, step, 0.1)
     ms = _timed_steps(torch, step, steps, warmup)
-    app_ms, k_ms = _event_kernel_ms(torch, lib, step, steps, (lib.T_KV_APPEND, lib.T_PREFILL))
+    (k_ms,) = _event_kernel_ms(torch, lib, step, steps, (lib.T_PREFILL,))
+    def two_launch():
+        ops.attention_append_rows_(K, V, k_new[:, None], v_new[:, None], position=prefix)
+        ops.attention_prefill(q, K, V, position=prefix)
+    two_ms = _timed_steps(torch, two_launch, steps, warmup)
+    (app_ms,) = _event_kernel_ms(torch, lib, two_launch, steps, (lib.T_KV_APPEND,))
     attn = lambda: ops.attention_prefill(q, K, V, position=prefix)  # noqa: E731
     attn_ms = _timed_steps(torch, attn, steps, warmup)
+    (attn_k_ms,) = _event_kernel_ms(torch, lib, attn, steps, (lib.T_PREFILL,))
     # the same rows in a paged pool: 256-row pages in shuffled order
     page, n_pages = 256, (prefix + tq) // 256
     perm = torch.randperm(n_pages, generator=torch.Generator().manual_seed(seed))
@@ -284,7 +308,8 @@ def bench_prefill(torch, ops, lib, *, steps, warmup, seed=3):
     flops = 4 * d * hq * pairs                      # QK^T and PV, 2 FLOP per MAC
     append_bytes = 2 * 2 * tq * hkv * d * 2         # K and V rows read + written
     return {"ms_per_step": ms, "attention_ms_per_call": attn_ms, "kernel_ms": k_ms,
-            "append_kernel_ms": app_ms, "flops": flops, "append_bytes": append_bytes,
+            "attention_kernel_ms": attn_k_ms, "append_kernel_ms": app_ms,
+            "two_launch_ms": two_ms, "flops": flops, "append_bytes": append_bytes,
             "tflops": flops / (ms * 1e-3) / 1e12,
             "kernel_tflops": flops / (k_ms * 1e-3) / 1e12, "paged_kernel_ms": pk_ms,
             "tensors": (q, K, V)}
@@ -956,14 +981,17 @@ def main() -> int:
             "tflops": round(c3["tflops"], 1),
             "frac_mfma_bf16": round(c3["tflops"] / BF16_PEAK_TFLOPS, 4),
             "ms_per_step": round(c3["ms_per_step"], 4),
-            "step": "append 2048 K/V rows + causal prefill over 4096 positions",
+            "step": "append 2048 K/V rows + causal prefill over 4096 positions (one launch)",
+            "step_kernel_ms": round(c3["kernel_ms"], 4),
             "attention_only_ms_per_call": round(c3["attention_ms_per_call"], 4),
-            "append_kernel_ms": round(c3["append_kernel_ms"], 4),
-            "append_gbs": round(c3["append_bytes"] / (c3["append_kernel_ms"] * 1e-3) / 1e9, 1),
+            "attention_only_kernel_ms": round(c3["attention_kernel_ms"], 4),
+            "two_launch_ms_per_step": round(c3["two_launch_ms"], 4),
+            "two_launch_append_kernel_ms": round(c3["append_kernel_ms"], 4),
             "flops_per_step": c3["flops"],
             "paged_256_rows_kernel_ms": round(c3["paged_kernel_ms"], 4),
-            "paged_vs_contiguous_kernel": round(c3["kernel_ms"] / c3["paged_kernel_ms"], 3),
-            "roofline": _roofline("prefill_mfma<bf16,bf16,128>", "mfma", c3["flops"],
+            "paged_vs_contiguous_kernel": round(c3["attention_kernel_ms"] / c3["paged_kernel_ms"],
+                                                3),
+            "roofline": _roofline("prefill_mfma<bf16,bf16,128> (append mode)", "mfma", c3["flops"],
                                   c3["kernel_ms"], work_name="flops")}
         if host:
             entry["cpu_baseline"] = cpu_c3(c3["tensors"], host)

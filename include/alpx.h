@@ -256,6 +256,28 @@ int alpx_prefill_causal_gated(const void* q, const void* key, const void* value,
                               int out_dtype, void* stream);
 
 /*
+ * A prefill chunk's cache append and causal prefill in one call: key /
+ * value [q_tokens, kv_heads, key_dim|value_dim] (contiguous) are written to
+ * rows position .. position + q_tokens - 1 of a batch-1 cache [capacity, 1,
+ * kv_heads, key_dim|value_dim] (bit-exact, as alpx_kv_append), and q
+ * attends to cache rows 0 .. position + t as in alpx_prefill_causal with
+ * q_pos0 = position, kv_start = 0 and kv_tokens = position + q_tokens
+ * (gate optional, as alpx_prefill_causal_gated).  Replaces the sequence
+ * "write the chunk's rows, then attend" of Model's batched prefill
+ * (model.py:1335-1340: cache_k / cache_v rows, then _attention_batch_np,
+ * model.py:1254-1272).  On the MFMA path this is one launch: the kernel
+ * reads the chunk's rows from key / value and each block writes its own
+ * tokens' rows into the cache; other shapes run alpx_kv_append and then
+ * alpx_prefill_causal's fallback (workspace as alpx_prefill_causal).
+ * position outside [0, capacity - q_tokens]: ALPX_ERANGE, nothing written.
+ */
+int alpx_prefill_append(const void* q, const void* key, const void* value, void* key_cache,
+                        void* value_cache, const void* gate, void* out, void* workspace,
+                        size_t workspace_bytes, int q_tokens, int64_t capacity, int q_heads,
+                        int kv_heads, int key_dim, int value_dim, int64_t position, int window,
+                        float scale, int dtype, int out_dtype, void* stream);
+
+/*
  * Gated delta-rule (GDN) decode step, in place on the state.
  * Replaces Qwen35RocmOps.gated_delta_net_step_ (qwen35_rocm_ops.py:362-407),
  * qwen35_kernels.qwen35_gdn_step (qwen35_kernels.py:310-332) and

@@ -63,6 +63,12 @@ def test_gated_prefill_rejects_null_gate_without_gpu(pkg):
 def test_range_and_shape_errors_without_gpu(pkg):
     lib = pkg._lib.lib()
     fake = ctypes.c_void_p(256)  # never dereferenced: validation fails first
+    rc = lib.alpx_prefill_append(fake, None, fake, fake, fake, None, fake, None, 0, 4, 16, 8, 2,
+                                 64, 64, 0, 0, 0.125, 2, 2, None)
+    assert rc == pkg._lib.EINVAL and "null" in pkg._lib.last_error()
+    rc = lib.alpx_prefill_append(fake, fake, fake, fake, fake, None, fake, None, 0, 4, 16, 8, 2,
+                                 64, 64, 13, 0, 0.125, 2, 2, None)
+    assert rc == pkg._lib.ERANGE and "exceeds capacity" in pkg._lib.last_error()
     rc = lib.alpx_kv_append(fake, fake, fake, fake, 1, 8, 1, 1, 4, 4, 2, 7, None, None)
     assert rc == pkg._lib.ERANGE and "exceeds capacity" in pkg._lib.last_error()
     rc = lib.alpx_decode_gqa(fake, fake, fake, None, 4, None, fake, fake, 1 << 20, 1, 6, 4, 64,

@@ -64,6 +64,60 @@ def test_c3_append_then_prefill_bf16_full_size(gpu, ops):
     assert np.abs(dec.cpu().numpy()[0] - out[-1].float().cpu().numpy()).max() <= TOL["bf16"]
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("tq,prefix,hq,hkv,d,window", [
+    (100, 0, 8, 2, 128, 0), (70, 33, 12, 4, 64, 0), (130, 200, 16, 2, 256, 0),
+    (1, 5, 4, 4, 64, 0), (96, 250, 8, 2, 128, 70), (64, 64, 32, 8, 128, 0),
+    (300, 17, 3, 1, 128, 0), (45, 100, 24, 2, 256, 40)])
+def test_prefill_append_equals_append_then_prefill(gpu, dtype, tq, prefix, hq, hkv, d, window):
+    """alpx_prefill_append (one launch on the MFMA path: the chunk's rows
+    read from key / value, each block writing its own tokens' rows) gives
+    the bits of alpx_kv_append followed by alpx_prefill_causal -- output
+    and both whole caches -- and the oracle's attention within tolerance.
+    Covers tiles across the first new row (prefix not a multiple of the key
+    tile), no prefix, a group size that does not divide a block's columns
+    (tokens whose columns span two blocks), head_dim 256 and windows."""
+    import torch
+    P = _mod("_ops")
+    rng = np.random.default_rng(tq * 13 + prefix + d + window)
+    cap = prefix + tq + 9
+    q = I.round_to(rng.standard_normal((tq, hq, d)), dtype)
+    K = I.round_to(rng.standard_normal((prefix + tq, hkv, d)), dtype)
+    V = I.round_to(rng.standard_normal((prefix + tq, hkv, d)), dtype)
+    old_k = I.round_to(rng.standard_normal((cap, 1, hkv, d)), dtype)
+    old_v = I.round_to(rng.standard_normal((cap, 1, hkv, d)), dtype)
+    old_k[:prefix, 0], old_v[:prefix, 0] = K[:prefix], V[:prefix]
+    kc_a, vc_a = _dev(torch, old_k, dtype, gpu), _dev(torch, old_v, dtype, gpu)
+    kc_b, vc_b = kc_a.clone(), vc_a.clone()
+    qd = _dev(torch, q, dtype, gpu)
+    kn, vn = _dev(torch, K[prefix:], dtype, gpu), _dev(torch, V[prefix:], dtype, gpu)
+    out_a = P.prefill_append(qd, kn, vn, kc_a, vc_a, position=prefix, window=window,
+                             out_dtype=torch.float32)
+    P.kv_append(kc_b, vc_b, kn[:, None], vn[:, None], position=prefix)
+    out_b = P.prefill(qd, kc_b[:, 0], vc_b[:, 0], pos0=prefix, kv_tokens=prefix + tq,
+                      window=window, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(kc_a, kc_b) and torch.equal(vc_a, vc_b)
+    assert torch.equal(out_a, out_b)
+    ref = A.attention_batch(q, K, V, prefix + np.arange(tq), hq // hkv, 1.0 / np.sqrt(d),
+                            window=window)
+    err = np.abs(out_a.cpu().numpy() - ref).max()
+    assert err <= TOL[dtype], err
+
+
+def test_prefill_append_range_error_leaves_cache(gpu):
+    import torch
+    P = _mod("_ops")
+    kc = torch.ones((10, 1, 2, 64), dtype=torch.bfloat16, device=gpu)
+    vc = kc.clone()
+    rows = torch.zeros((4, 2, 64), dtype=torch.bfloat16, device=gpu)
+    q = torch.zeros((4, 4, 64), dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(ValueError, match="exceeds capacity"):
+        P.prefill_append(q, rows, rows, kc, vc, position=7)
+    torch.cuda.synchronize()
+    assert bool((kc == 1).all()) and bool((vc == 1).all())
+
+
 @pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
 @pytest.mark.parametrize("tq,prefix,hq,hkv,d", [
     (1, 0, 4, 4, 64), (37, 0, 8, 2, 128), (70, 33, 32, 8, 128), (130, 200, 16, 2, 256),
