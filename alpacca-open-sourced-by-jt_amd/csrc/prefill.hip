@@ -24,7 +24,9 @@
 // visible rows are those at absolute positions <= pos0 + t (inside the
 // window).
 #include <math.h>
+#include <string.h>
 
+#include <algorithm>
 #include <type_traits>
 
 #include "alpx_common.h"
@@ -218,9 +220,72 @@ __device__ __forceinline__ void pin(V& x) {
 #endif
 }
 
-template <typename T, typename TO, int D, int BK, int NQB, bool PAGED = false>
-__global__ void __launch_bounds__(256, 2)
-prefill_mfma(PrefillArgs a) {
+// Append mode: copies the K and V rows (head kvh) of the tokens whose first
+// column lies in column tile ct into the cache, 16 bytes per lane over 256
+// threads, four loads in flight (clamped, so unconditional) before the
+// stores.  No block of the launch reads those cache rows: tiles take them
+// from kn / vn.
+template <typename T, int D, int kCols>
+__device__ __forceinline__ void copy_tile_rows(const PrefillArgs& a, int kvh, int ct, int tid) {
+  constexpr int U = D / 8;
+  const int G = a.group;
+  const int t0 = (ct * kCols + G - 1) / G;
+  const int t1 = min(a.q_tokens, ((ct + 1) * kCols + G - 1) / G);
+  const int units = max(0, t1 - t0) * 2 * U;
+  for (int u0 = 0; u0 < units; u0 += 4 * 256) {
+    u32x4 x[4];
+    T* dst[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int u = min(u0 + 256 * k + tid, units - 1);
+      const int r = t0 + u / (2 * U), part = u % (2 * U);
+      const bool val = part >= U;
+      const int64_t pos = val ? a.vs_pos : a.ks_pos;
+      const int64_t col = (int64_t)kvh * D + 8 * (part - (val ? U : 0));
+      x[k] = *(const u32x4*)((const T*)(val ? a.vn : a.kn) + (int64_t)r * pos + col);
+      // the caches are written here and nowhere else in the kernels
+      dst[k] = (T*)const_cast<void*>(val ? a.v : a.k) + (int64_t)(a.new0 + r) * pos + col;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (u0 + 256 * k + tid < units) *(u32x4*)dst[k] = x[k];
+  }
+}
+
+// Key tiles of a column tile: rows [lo, hi) that any of its columns can
+// see, in nt tiles of BK rows starting at lo.
+template <int BK, int kCols>
+__device__ __forceinline__ void tile_keys(const PrefillArgs& a, int ctile, int& lo, int& hi,
+                                          int& nt) {
+  const int G = a.group;
+  const int cols = a.q_tokens * G;
+  const int col0 = ctile * kCols;
+  const int rel0 = (int)(a.pos0 - a.kv_start);
+  const int bt_first = col0 / G;
+  const int bt_last = (min(col0 + kCols, cols) - 1) / G;
+  hi = max(0, min(a.kv_tokens, rel0 + bt_last + 1));
+  lo = 0;
+  if (a.window > 0) lo = min(hi, max(0, rel0 + bt_first - a.window + 1)) / BK * BK;
+  nt = (hi - lo + BK - 1) / BK;
+}
+
+// What a run does with its result: write the output; leave its partial
+// state (O and this lane's share of l, with the column's m and offset mc)
+// in LDS for the other group of the block; or merge that partial into its
+// own and write the output.
+constexpr int kRunWrite = 0, kRunPartial = 1, kRunMerge = 2;
+
+// One run of a group of four waves (wave 0..3, tid 0..255 within the
+// group): column tile ctile of kv head kvh over its key tiles [tb, te)
+// (counted from the tile's first visible tile; te < 0: to its last), with
+// the four K / V tile buffers at `smem` and `bar` as the group's barrier.
+// prefill_mfma runs one per block; prefill_pair runs two groups per block.
+// part_o / part_st: the partial's LDS home (written by kRunPartial, read by
+// kRunMerge).
+template <typename T, typename TO, int D, int BK, int NQB, bool PAGED, int MODE, typename Bar>
+__device__ __forceinline__ void prefill_run(const PrefillArgs& a, int kvh, int ctile, int tb,
+                                            int te, char* smem, float* part_o, float* part_st,
+                                            int wave, int tid, Bar& bar) {
   typedef typename Vec8<T>::type V8;
   constexpr int U = D / 8;                  // 16-byte units per row
   constexpr int kRowB = D * (int)sizeof(T);
@@ -234,58 +299,15 @@ prefill_mfma(PrefillArgs a) {
   constexpr int kCols = 4 * kWaveCols;
   static_assert(kIW >= 1 && BK * U % 256 == 0, "tile must split evenly over 4 waves");
   static_assert(U >= 8, "the row swizzle needs 8 units per row");
-  // K tile buffers at 0 and kTileB, V tile buffers at 2 and 3 kTileB.
-  __shared__ __attribute__((aligned(1024))) char smem[4 * kTileB];
+  // K tile buffers at smem and smem + kTileB, V tile buffers at 2 and 3 kTileB.
 
-  const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hl = lane & 15;
   const int quad = lane >> 4;
-  int kvh, ctile;
-  if (!prefill_work(a, kvh, ctile)) return;
   const int G = a.group;
   const int cols = a.q_tokens * G;
   const int col0 = ctile * kCols;
   const int wcol0 = col0 + kWaveCols * wave;
-
-  // Append mode: the K and V rows (head kvh) of the tokens whose first
-  // column lies in column tile ct are copied into the cache, 16 bytes per
-  // lane, four loads in flight (clamped, so unconditional) before the
-  // stores.  No block of this launch reads those cache rows: tiles take
-  // them from kn / vn.
-  auto copy_rows = [&](int ct) {
-    const int t0 = (ct * kCols + G - 1) / G;
-    const int t1 = min(a.q_tokens, ((ct + 1) * kCols + G - 1) / G);
-    const int units = max(0, t1 - t0) * 2 * U;
-    for (int u0 = 0; u0 < units; u0 += 4 * 256) {
-      u32x4 x[4];
-      T* dst[4];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int u = min(u0 + 256 * k + tid, units - 1);
-        const int r = t0 + u / (2 * U), part = u % (2 * U);
-        const bool val = part >= U;
-        const int64_t pos = val ? a.vs_pos : a.ks_pos;
-        const int64_t col = (int64_t)kvh * D + 8 * (part - (val ? U : 0));
-        x[k] = *(const u32x4*)((const T*)(val ? a.vn : a.kn) + (int64_t)r * pos + col);
-        // the caches are written here and nowhere else in the kernel
-        dst[k] = (T*)const_cast<void*>(val ? a.v : a.k) + (int64_t)(a.new0 + r) * pos + col;
-      }
-#pragma unroll
-      for (int k = 0; k < 4; ++k)
-        if (u0 + 256 * k + tid < units) *(u32x4*)dst[k] = x[k];
-    }
-  };
-
-  // The heavy column tiles (late tokens, many key tiles) set the kernel's
-  // end time, so of each tile and its mirror col_tiles - 1 - ctile the
-  // lighter one copies both tiles' rows (each tile's rows exactly once).
-  if (!PAGED && a.kn != nullptr) {
-    const int mirror = a.col_tiles - 1 - ctile;
-    if (ctile <= mirror) copy_rows(ctile);
-    if (ctile < mirror) copy_rows(mirror);
-  }
 
   int tok[NQB], hq[NQB];
   bool cok[NQB];
@@ -312,7 +334,12 @@ prefill_mfma(PrefillArgs a) {
   // Every wave walks all nt tiles of the block; keys a wave's columns cannot
   // see (past its diagonal, before its window) are masked, which costs at
   // most about one tile per wave and keeps the waves' pipelines in step.
-  const int nt = (hi - lo + BK - 1) / BK;
+  const int nt_all = (hi - lo + BK - 1) / BK;
+  // This run's tiles are [tb, t_end) of them, its keys end at hi_r; inside
+  // the run tiles are counted from tb.
+  const int t_end = te < 0 ? nt_all : min(te, nt_all);
+  const int nt = max(0, t_end - tb);
+  const int hi_r = min(hi, lo + t_end * BK);
 
   // B operand of S^T = K Q^T: lane holds Q[column][32 ks + 8 quad + 0..7],
   // pre-multiplied by scale * log2(e) (and rounded once to T), so that the
@@ -380,19 +407,19 @@ prefill_mfma(PrefillArgs a) {
     const int np = nt > 0 ? ((hi - 1) >> a.page_shift) - page0 + 1 : 0;
     pages_in_lds = np <= kPageSlots;
     if (pages_in_lds) {
-      for (int i = threadIdx.x; i < np; i += 256) {
+      for (int i = tid; i < np; i += 256) {
         const int pg = a.pages[page0 + i];
         page_lds[i] = pg < 0 ? 0 : (pg >= a.num_pages ? a.num_pages - 1 : pg);
       }
     }
-    __syncthreads();
+    bar();
   }
   // A tile starts at a multiple of BK and a page holds a multiple of BK
   // rows, so a paged tile lies in one page, looked up once per tile (when
   // its K rows are loaded; its V rows reuse the number).
   [[maybe_unused]] auto tile_page = [&](int t) -> int {
     if constexpr (PAGED) {
-      const int pi = (lo + t * BK) >> a.page_shift;
+      const int pi = (lo + (tb + t) * BK) >> a.page_shift;
       if (pages_in_lds) return __builtin_amdgcn_readfirstlane(page_lds[pi - page0]);
       const int pg = a.pages[pi];
       return pg < 0 ? 0 : (pg >= a.num_pages ? a.num_pages - 1 : pg);
@@ -402,7 +429,7 @@ prefill_mfma(PrefillArgs a) {
   // gn: the chunk's own rows of this head (append mode), else null.
   auto load_tile = [&](const T* g, const T* gn, int64_t pos, int64_t page_stride,
                        const uint32_t (&ofs)[kIW], int t, int buf, int pg) {
-    const int k0 = lo + t * BK;
+    const int k0 = lo + (tb + t) * BK;
     const T* base = g + (int64_t)k0 * pos;
     if constexpr (PAGED)
       base = g + (int64_t)pg * page_stride + (int64_t)(k0 & ((1 << a.page_shift) - 1)) * pos;
@@ -488,7 +515,7 @@ prefill_mfma(PrefillArgs a) {
                                     ks == 0 ? (f32x4){0.f, 0.f, 0.f, 0.f} : sc[kb][qb]);
   };
   auto mask = [&](int t) __attribute__((always_inline)) {
-    const int k0 = lo + t * BK;
+    const int k0 = lo + (tb + t) * BK;
 #pragma unroll
     for (int qb = 0; qb < NQB; ++qb) {
       const int qrel = rel0 + tok[qb];
@@ -497,7 +524,7 @@ prefill_mfma(PrefillArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int key = k0 + 16 * kb + 4 * quad + i;
-          const bool ok = key < hi && key <= qrel && (a.window <= 0 || key > qrel - a.window);
+          const bool ok = key < hi_r && key <= qrel && (a.window <= 0 || key > qrel - a.window);
           sc[kb][qb][i] = ok ? sc[kb][qb][i] : -INFINITY;
         }
     }
@@ -553,8 +580,8 @@ prefill_mfma(PrefillArgs a) {
     }
   };
   auto need_mask = [&](int t) {
-    const int k0 = lo + t * BK;
-    return k0 + BK - 1 > rel0 + wt_first || k0 + BK > hi ||
+    const int k0 = lo + (tb + t) * BK;
+    return k0 + BK - 1 > rel0 + wt_first || k0 + BK > hi_r ||
            (a.window > 0 && k0 <= rel0 + wt_last - a.window);
   };
 
@@ -655,7 +682,7 @@ prefill_mfma(PrefillArgs a) {
     if (__builtin_expect(grow_check(), 0)) move_max();
     // One basic block of independent MFMA and VALU work.  At j = 0 the PV
     // step multiplies zeroed P by a zeroed V buffer; at j = nt the softmax
-    // sees a fully masked tile (k0 >= hi) and its P is never used.
+    // sees a fully masked tile (k0 >= hi_r) and its P is never used.
     __builtin_amdgcn_sched_barrier(0);
     __builtin_amdgcn_s_setprio(1);
     block(Par<P>());
@@ -676,7 +703,7 @@ prefill_mfma(PrefillArgs a) {
       for (int kb = 0; kb < KB; ++kb) pin(sc[kb][qb]);
     }
     __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+    bar();
   };
 
   // Zero V buffer 1 (read by the j = 0 PV step) and the P operands it uses.
@@ -696,12 +723,51 @@ prefill_mfma(PrefillArgs a) {
     load_tile(kg, kgn, a.ks_pos, a.ks_page, kofs, 1, 1, kpage[1]);
   }
   __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
+  bar();
   qk_first();
-  __syncthreads();  // K(0) fully read before iteration 0 refills its buffer
+  bar();  // K(0) fully read before iteration 0 refills its buffer
   for (int j = 0; j <= nt; j += 2) {
     iteration(Par<0>(), j);
     if (j + 1 <= nt) iteration(Par<1>(), j + 1);
+  }
+
+  // Partial layout: O as [wave][qb][mb][lane] f32x4 in part_o, then
+  // [wave][qb][lane] l share, mc and m in part_st.
+  constexpr int kPartO = NQB * MB * 64;  // f32x4 per wave
+  if constexpr (MODE == kRunPartial) {
+    // The loop ended with the group's barrier: no wave reads the tile
+    // buffers any more, so part_o may overlay them.
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb) {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+        ((f32x4*)part_o)[wave * kPartO + (qb * MB + mb) * 64 + lane] = o[qb][mb];
+      float* st = part_st + ((wave * NQB + qb) * 3) * 64 + lane;
+      st[0] = lsum[qb];
+      st[64] = mc[qb];
+      st[128] = m[qb];
+    }
+    __syncthreads();  // the block's one barrier: the merging group reads after it
+    return;
+  }
+  if constexpr (MODE == kRunMerge) {
+    __syncthreads();  // the block's one barrier: the partner's partial is in LDS
+    // Both parts hold O and l relative to their own offset mc; a part whose
+    // m is still -inf saw no visible key and weighs nothing.
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb) {
+      const float* st = part_st + ((wave * NQB + qb) * 3) * 64 + lane;
+      const float l1 = st[0], mc1 = st[64], m1 = st[128];
+      const bool v0 = m[qb] != -INFINITY, v1 = m1 != -INFINITY;
+      const float M = fmaxf(v0 ? mc[qb] : -INFINITY, v1 ? mc1 : -INFINITY);
+      const float w0 = v0 ? fast_exp2(mc[qb] - M) : 0.f;
+      const float w1 = v1 ? fast_exp2(mc1 - M) : 0.f;
+      lsum[qb] = lsum[qb] * w0 + l1 * w1;
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+        o[qb][mb] = o[qb][mb] * w0 +
+                    ((const f32x4*)part_o)[wave * kPartO + (qb * MB + mb) * 64 + lane] * w1;
+    }
   }
 
 #pragma unroll
@@ -736,6 +802,121 @@ prefill_mfma(PrefillArgs a) {
   }
 }
 
+template <typename T, typename TO, int D, int BK, int NQB, bool PAGED = false>
+__global__ void __launch_bounds__(256, 2)
+prefill_mfma(PrefillArgs a) {
+  constexpr int kTileB = BK * D * (int)sizeof(T);
+  constexpr int kCols = 64 * NQB;
+  __shared__ __attribute__((aligned(1024))) char smem[4 * kTileB];
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  int kvh, ctile;
+  if (!prefill_work(a, kvh, ctile)) return;
+  // The heavy column tiles (late tokens, many key tiles) set the kernel's
+  // end time, so of each tile and its mirror col_tiles - 1 - ctile the
+  // lighter one copies both tiles' rows (each tile's rows exactly once).
+  if (!PAGED && a.kn != nullptr) {
+    const int mirror = a.col_tiles - 1 - ctile;
+    if (ctile <= mirror) copy_tile_rows<T, D, kCols>(a, kvh, ctile, tid);
+    if (ctile < mirror) copy_tile_rows<T, D, kCols>(a, kvh, mirror, tid);
+  }
+  auto bar = []() __attribute__((always_inline)) { __syncthreads(); };
+  prefill_run<T, TO, D, BK, NQB, PAGED, kRunWrite>(a, kvh, ctile, 0, -1, smem, nullptr, nullptr,
+                                                   wave, tid, bar);
+}
+
+// Work of a prefill_pair block: kv head kvh and the column tiles ta (light:
+// earlier tokens) and tb = col_tiles - 1 - ta (heavy; equal to ta for the
+// middle tile of an odd count).  Pairs are ordered kv-head-major and cut
+// into 8 contiguous slices, slice x on XCD x, so one kv head's blocks share
+// one XCD's L2.
+__device__ __forceinline__ bool pair_work(const PrefillArgs& a, int& kvh, int& ta, int& tb) {
+  const int b = blockIdx.x;
+  const int item = (b % kXcds) * a.per_xcd + b / kXcds;
+  const int pairs = (a.col_tiles + 1) / 2;
+  if (item >= a.kv_heads * pairs) return false;
+  kvh = item / pairs;
+  ta = item - kvh * pairs;
+  tb = a.col_tiles - 1 - ta;
+  return true;
+}
+
+// Barrier of one four-wave group of a prefill_pair block: a counter in LDS
+// that each wave raises once per barrier; the k-th barrier waits until it
+// reads 4 k.  A polling wave spends its time waiting on its LDS read, so
+// the other group's wave on the same SIMD keeps the issue slots (a sleep
+// between polls measured slower: it delays the wake-up).  The wait gives
+// up after 2^22 polls, a guard against a mismatched barrier count (never
+// reached in a correct run: the waves of a workgroup are resident
+// together, so all four arrive).
+struct GroupBarrier {
+  uint32_t* ctr;
+  uint32_t target;
+  __device__ __forceinline__ void operator()() {
+    target += 4;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    if ((threadIdx.x & 63) == 0)
+      __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    for (int i = 0; i < (1 << 22); ++i) {
+      const uint32_t v = __builtin_amdgcn_readfirstlane(
+          __hip_atomic_load(ctr, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+      if (v >= target) break;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  }
+};
+
+// Causal imbalance removed: one block of eight waves per CU takes a light
+// and a heavy column tile of one kv head.  Waves 0-3 (group 0) run the
+// light tile over all its key tiles, then the heavy tile over its key
+// tiles [s, nt_b); waves 4-7 (group 1) run the heavy tile over [0, s),
+// with s chosen so that both groups walk about the same number of tiles.
+// Each group has its own four tile buffers and its own barrier, so the two
+// groups' pipelines run independently (as two co-resident blocks would);
+// at the end group 0 leaves its heavy-tile partial in its LDS and group 1
+// merges it into its own (one block barrier) and writes the heavy tile.
+template <typename T, typename TO, int D, int BK, int NQB>
+__global__ void __launch_bounds__(512, 1)
+prefill_pair(PrefillArgs a) {
+  constexpr int kTileB = BK * D * (int)sizeof(T);
+  constexpr int kCols = 64 * NQB;
+  constexpr int MB = D / 16;
+  static_assert(NQB * MB * 64 * 16 * 4 <= 4 * kTileB, "the partial O must fit a group's buffers");
+  __shared__ __attribute__((aligned(1024))) char smem[8 * kTileB];
+  __shared__ float part_st[4 * NQB * 3 * 64];
+  __shared__ uint32_t gctr[2];
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wave >> 2;
+  int kvh, ta, tbt;
+  if (!pair_work(a, kvh, ta, tbt)) return;
+  if (tid < 2) gctr[tid] = 0;
+  __syncthreads();  // the group counters are zero before any group barrier
+  int lo, hi, nta = 0, ntb;
+  if (ta != tbt) tile_keys<BK, kCols>(a, ta, lo, hi, nta);
+  tile_keys<BK, kCols>(a, tbt, lo, hi, ntb);
+  // Group 0 also pays a second pipeline start: one tile's worth.
+  const int split = min(ntb, (nta + ntb + (ta != tbt ? 1 : 0) + 1) / 2);
+  GroupBarrier bar{gctr + grp, 0u};
+  char* gsmem = smem + grp * 4 * kTileB;
+  const int gw = wave & 3, gtid = tid & 255;
+  if (grp == 0) {
+    // the light tile, then the heavy tile's key tiles [split, nt_b)
+    if (ta != tbt) {
+      if (a.kn != nullptr) copy_tile_rows<T, D, kCols>(a, kvh, ta, gtid);
+      prefill_run<T, TO, D, BK, NQB, false, kRunWrite>(a, kvh, ta, 0, -1, gsmem, nullptr, nullptr,
+                                                       gw, gtid, bar);
+    }
+    prefill_run<T, TO, D, BK, NQB, false, kRunPartial>(a, kvh, tbt, split, -1, gsmem,
+                                                       (float*)smem, part_st, gw, gtid, bar);
+  } else {
+    // the heavy tile's key tiles [0, split), merged with group 0's part
+    if (a.kn != nullptr) copy_tile_rows<T, D, kCols>(a, kvh, tbt, gtid);
+    prefill_run<T, TO, D, BK, NQB, false, kRunMerge>(a, kvh, tbt, 0, split, gsmem, (float*)smem,
+                                                     part_st, gw, gtid, bar);
+  }
+}
+
 template <typename T, typename TO>
 const void* pick_kernel(int D) {
   switch (D) {
@@ -766,6 +947,25 @@ const void* pick_kernel_out(int D, int out_dtype) {
   }
 }
 
+template <typename T, typename TO>
+const void* pick_pair(int D) {
+  switch (D) {
+    case 64: return (const void*)prefill_pair<T, TO, 64, 64, 2>;
+    case 128: return (const void*)prefill_pair<T, TO, 128, 64, 2>;
+    case 256: return (const void*)prefill_pair<T, TO, 256, 32, 1>;
+  }
+  return nullptr;
+}
+
+template <typename T>
+const void* pick_pair_out(int D, int out_dtype) {
+  switch (out_dtype) {
+    case ALPX_F32: return pick_pair<T, float>(D);
+    case ALPX_F16: return pick_pair<T, f16_t>(D);
+    default: return pick_pair<T, bf16_t>(D);
+  }
+}
+
 }  // namespace
 }  // namespace alpx
 
@@ -779,6 +979,43 @@ extern "C" size_t alpx_prefill_workspace_bytes(int q_tokens, int q_heads, int kv
 }
 
 namespace {
+
+// Key tiles (of `rows` rows) that column tile ct walks: tile_keys on the host.
+int host_tile_keys(int q_tokens, int kv_tokens, int group, int rel0, int window, int cols_per_block,
+                   int rows, int ct) {
+  const int cols = q_tokens * group;
+  const int col0 = ct * cols_per_block;
+  const int hi = std::max(0, std::min(kv_tokens, rel0 + (std::min(col0 + cols_per_block, cols) - 1) / group + 1));
+  int lo = 0;
+  if (window > 0) lo = std::min(hi, std::max(0, rel0 + col0 / group - window + 1)) / rows * rows;
+  return (hi - lo + rows - 1) / rows;
+}
+
+// Kernel choice for contiguous caches.  The paired kernel gains the tail a
+// heavy column tile runs alone and pays a second pipeline start (group 0)
+// and the final merge.  Same-box sweep (2048 query tokens, 32/8 or 16/2
+// heads, pair / single time): head_dim 128 at prefix 0, 512, 1024, 2048,
+// 4096 -- 0.94, 0.98, 1.00, 1.04, 1.03; head_dim 256 at prefix 0, 2048,
+// 8192 -- 0.75, 0.91, 1.04; head_dim 64 at prefix 0, 2048 -- 0.92, 0.98;
+// 512 query tokens (64 pairs) 1.37; 8192 tokens at prefix 0 (four rounds
+// of pairs) 1.02.  So: pairs must form one round that fills the device,
+// and the heaviest column tile must walk at least R times the key tiles of
+// the lightest, R = 3 at head_dim 128 and 1.8 at 64 and 256.
+// ALPX_PREFILL_KERNEL=pair or =single overrides the choice.
+bool use_pair(int q_tokens, int kv_tokens, int kv_heads, int group, int rel0, int window,
+              int cols_per_block, int rows, int col_tiles, int key_dim, const void* pair_kernel) {
+  const char* force = getenv("ALPX_PREFILL_KERNEL");
+  if (force != nullptr && strcmp(force, "pair") == 0) return true;
+  if (force != nullptr && strcmp(force, "single") == 0) return false;
+  const int64_t pairs = (int64_t)kv_heads * ((col_tiles + 1) / 2);
+  const int resident = alpx::resident_blocks(pair_kernel, 512, 0);
+  if (pairs > resident || pairs * 10 < (int64_t)resident * 9) return false;
+  const int first = host_tile_keys(q_tokens, kv_tokens, group, rel0, window, cols_per_block, rows, 0);
+  const int last =
+      host_tile_keys(q_tokens, kv_tokens, group, rel0, window, cols_per_block, rows, col_tiles - 1);
+  const int r10 = key_dim == 128 ? 30 : 18;  // R x 10
+  return (int64_t)last * 10 >= (int64_t)r10 * std::max(1, first);
+}
 
 int prefill_impl(const void* q, const void* key, const void* value, const void* gate, void* out,
                  void* workspace, size_t workspace_bytes, int q_tokens, int kv_tokens,
@@ -827,10 +1064,21 @@ int prefill_impl(const void* q, const void* key, const void* value, const void* 
                 "alpx_prefill_causal_paged: needs fp16/bf16 pages, head_dim in {64, 128, 256}, "
                 "16-byte aligned rows and out_dtype == dtype");
   if (mfma && offsets_fit) {
+    const int cols_per_block = key_dim == 256 ? 64 : 128;
+    const int tile_rows = key_dim == 256 ? 32 : 64;
+    const int col_tiles = (int)(((int64_t)q_tokens * group + cols_per_block - 1) / cols_per_block);
+    const bool pair = pages == nullptr &&
+                      use_pair(q_tokens, kv_tokens, kv_heads, group, (int)(q_pos0 - kv_start), window,
+                               cols_per_block, tile_rows, col_tiles, key_dim,
+                               dtype == ALPX_F16 ? pick_pair_out<f16_t>(key_dim, out_dtype)
+                                                 : pick_pair_out<bf16_t>(key_dim, out_dtype));
     const void* kernel = nullptr;
     if (pages != nullptr)
       kernel = dtype == ALPX_F16 ? pick_kernel_paged<f16_t>(key_dim)
                                  : pick_kernel_paged<bf16_t>(key_dim);
+    else if (pair)
+      kernel = dtype == ALPX_F16 ? pick_pair_out<f16_t>(key_dim, out_dtype)
+                                 : pick_pair_out<bf16_t>(key_dim, out_dtype);
     else if (dtype == ALPX_F16)
       kernel = pick_kernel_out<f16_t>(key_dim, out_dtype);
     else
@@ -859,15 +1107,14 @@ int prefill_impl(const void* q, const void* key, const void* value, const void* 
     a.q_heads = q_heads;
     a.kv_heads = kv_heads;
     a.group = group;
-    const int cols_per_block = key_dim == 256 ? 64 : 128;
-    const int64_t cols = (int64_t)q_tokens * group;
-    a.col_tiles = (int)((cols + cols_per_block - 1) / cols_per_block);
-    const int64_t items = (int64_t)a.col_tiles * kv_heads;
+    a.col_tiles = col_tiles;
+    const int64_t items = (int64_t)(pair ? (a.col_tiles + 1) / 2 : a.col_tiles) * kv_heads;
     a.per_xcd = (int)((items + kXcds - 1) / kXcds);
     a.scale_log2 = scale * kLog2e;
     TimedRegion timed(ALPX_T_PREFILL, s);
     void* args[] = {(void*)&a};
-    hipError_t err = hipLaunchKernel(kernel, dim3(a.per_xcd * kXcds), dim3(256), args, 0, s);
+    hipError_t err = hipLaunchKernel(kernel, dim3(a.per_xcd * kXcds), dim3(pair ? 512 : 256), args,
+                                     0, s);
     if (err != hipSuccess)
       return fail(ALPX_EHIP, "prefill launch failed: %s", hipGetErrorString(err));
     return check_launch("prefill_mfma");

@@ -534,7 +534,8 @@ def bench_layer_prefill(torch, ops, lib, *, steps, warmup, seed=7):
     chunk = lambda: ops.attention_layer_prefill_(  # noqa: E731
         qg, kn, vn, qw, kw, K, V, position=prefix, sections=sec, frequency_base=base,
         epsilon=eps)
-    a_ms = _timed_steps(torch, chunk, max(3, steps // 5), 2)
+    _warm(torch, chunk, 0.1)
+    a_ms = _timed_steps(torch, chunk, max(10, steps // 2), 2)
 
     def tokens_attn():
         for t in range(T):
@@ -561,7 +562,8 @@ def bench_layer_prefill(torch, ops, lib, *, steps, warmup, seed=7):
     nw = torch.rand((dv,), generator=g, device=dev) + 0.5
     rchunk = lambda: ops.recurrent_layer_prefill_(  # noqa: E731
         ws, mixed, cw, gate, bl, al, dt, ssm, nw, key_heads=hk, key_dimension=dk, epsilon=eps)
-    r_ms = _timed_steps(torch, rchunk, max(3, steps // 5), 2)
+    _warm(torch, rchunk, 0.1)
+    r_ms = _timed_steps(torch, rchunk, max(10, steps // 2), 2)
 
     def tokens_rec():
         for t in range(R):

@@ -69,8 +69,10 @@ def test_c3_append_then_prefill_bf16_full_size(gpu, ops):
     (100, 0, 8, 2, 128, 0), (70, 33, 12, 4, 64, 0), (130, 200, 16, 2, 256, 0),
     (1, 5, 4, 4, 64, 0), (96, 250, 8, 2, 128, 70), (64, 64, 32, 8, 128, 0),
     (300, 17, 3, 1, 128, 0), (45, 100, 24, 2, 256, 40)])
-def test_prefill_append_equals_append_then_prefill(gpu, dtype, tq, prefix, hq, hkv, d, window):
-    """alpx_prefill_append (one launch on the MFMA path: the chunk's rows
+@pytest.mark.parametrize("kernel", ["pair", "single"])
+def test_prefill_append_equals_append_then_prefill(gpu, monkeypatch, kernel, dtype, tq, prefix, hq,
+                                                   hkv, d, window):
+    """alpx_prefill_append (one launch on the MFMA path, either contiguous kernel: the chunk's rows
     read from key / value, each block writing its own tokens' rows) gives
     the bits of alpx_kv_append followed by alpx_prefill_causal -- output
     and both whole caches -- and the oracle's attention within tolerance.
@@ -78,6 +80,7 @@ def test_prefill_append_equals_append_then_prefill(gpu, dtype, tq, prefix, hq, h
     tile), no prefix, a group size that does not divide a block's columns
     (tokens whose columns span two blocks), head_dim 256 and windows."""
     import torch
+    monkeypatch.setenv("ALPX_PREFILL_KERNEL", kernel)  # fp32 takes the split-K path either way
     P = _mod("_ops")
     rng = np.random.default_rng(tq * 13 + prefix + d + window)
     cap = prefix + tq + 9
@@ -135,6 +138,41 @@ def test_prefill_shapes(gpu, ops, dtype, tq, prefix, hq, hkv, d):
     ref = A.full_attention_prefill(q, K, V, prefix_length=prefix)
     err = np.abs(out.cpu().numpy() - ref).max()
     assert err <= TOL[dtype], err
+
+
+@pytest.mark.parametrize("kernel", ["pair", "single"])
+@pytest.mark.parametrize("tq,prefix,hq,hkv,d,window,gated", [
+    (2048, 0, 4, 1, 128, 0, False), (300, 100, 12, 4, 64, 0, False),
+    (161, 7, 8, 2, 256, 0, True), (40, 500, 8, 8, 128, 0, False),
+    (700, 300, 16, 4, 128, 200, False), (513, 0, 2, 1, 64, 0, True),
+    (96, 33, 48, 2, 256, 50, False)])
+def test_prefill_kernels_match_oracle(gpu, monkeypatch, kernel, tq, prefix, hq, hkv, d, window,
+                                      gated):
+    """Both contiguous MFMA kernels -- the paired one (a light and a heavy
+    column tile per block, the heavy tile's key tiles split between the two
+    wave groups and merged in LDS) and the one-tile-per-block one
+    (ALPX_PREFILL_KERNEL selects each) -- against the oracle: an even and an odd number
+    of column tiles (the middle tile split with itself), a single column
+    tile, group sizes that do not divide a block's columns, windows (the
+    light tile's key range not a prefix of the heavy one's), head_dim
+    64/128/256, gated and not."""
+    import torch
+    monkeypatch.setenv("ALPX_PREFILL_KERNEL", kernel)
+    rng = np.random.default_rng(tq + prefix + d + window)
+    q = I.round_to(rng.standard_normal((tq, hq, d)), "bf16")
+    K = I.round_to(rng.standard_normal((prefix + tq, hkv, d)), "bf16")
+    V = I.round_to(rng.standard_normal((prefix + tq, hkv, d)), "bf16")
+    gate = I.round_to(rng.standard_normal((tq, hq, d)) * 2, "bf16") if gated else None
+    out = _mod("_ops").prefill(_dev(torch, q, "bf16", gpu), _dev(torch, K, "bf16", gpu),
+                               _dev(torch, V, "bf16", gpu), pos0=prefix, window=window,
+                               out_dtype=torch.float32,
+                               gate=None if gate is None else _dev(torch, gate, "bf16", gpu))
+    ref = A.attention_batch(q, K, V, prefix + np.arange(tq), hq // hkv, 1.0 / np.sqrt(d),
+                            window=window)
+    if gated:
+        ref = ref / (1.0 + np.exp(-gate))
+    err = np.abs(out.cpu().numpy() - ref).max()
+    assert err <= TOL["bf16"], err
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
