@@ -212,7 +212,7 @@ struct ProArgs {
   const float* qw;   // [D]
   const float* kw;   // [D]
   void* q_out;       // [B, Hq, D]
-  void* g_out;       // [B, Hq, D]
+  void* g_out;       // [B, Hq, D], or null: the gate half is not copied
   void* kc;          // [capacity, B, Hkv, D]
   void* vc;          // [capacity, B, Hkv, Dv]
   const int32_t* positions;  // device [B] or null (then position + r pos_step for row r)
@@ -266,16 +266,18 @@ __global__ void __launch_bounds__(256) attn_prologue_kernel(ProArgs a) {
     if (i < a.D) {
       x[e] = to_f32(src[i]);
       wt[e] = w[i];
-      if (is_q) gv[e] = src[a.D + i];
+      if (is_q && a.g_out != nullptr) gv[e] = src[a.D + i];
     }
   }
   T* dst;
   if (is_q) {
     dst = (T*)a.q_out + ((int64_t)b * a.Hq + h) * a.D;
-    T* gd = (T*)a.g_out + ((int64_t)b * a.Hq + h) * a.D;
+    if (a.g_out != nullptr) {
+      T* gd = (T*)a.g_out + ((int64_t)b * a.Hq + h) * a.D;
 #pragma unroll
-    for (int e = 0; e < kPer; ++e)
-      if (lane + 64 * e < a.D) gd[lane + 64 * e] = gv[e];
+      for (int e = 0; e < kPer; ++e)
+        if (lane + 64 * e < a.D) gd[lane + 64 * e] = gv[e];
+    }
   } else {
     if (!in_cache) return;
     dst = (T*)a.kc + (crow * a.Hkv + h) * a.D;
@@ -983,8 +985,8 @@ int attention_prologue_launch(const char* what, const void* query_gate, const vo
                               const int32_t* positions, const int* sections,
                               double frequency_base, float eps, void* stream) {
   using namespace alpx;
-  if (!query_gate || !key || !value || !q_norm || !k_norm || !query_out || !gate_out ||
-      !key_cache || !value_cache)
+  if (!query_gate || !key || !value || !q_norm || !k_norm || !query_out ||
+      (!gate_out && pos_step == 0) || !key_cache || !value_cache)
     return fail(ALPX_EINVAL, "%s: null buffer", what);
   if (!dtype_ok(dtype)) return fail(ALPX_EINVAL, "%s: unknown dtype", what);
   if (rows <= 0 || cache_batch <= 0 || q_heads <= 0 || kv_heads <= 0 || head_dim <= 0 ||

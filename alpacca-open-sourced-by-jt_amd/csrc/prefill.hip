@@ -40,7 +40,8 @@ struct PrefillArgs {
   const void* q;
   const void* k;
   const void* v;
-  const void* gate;  // null, or [q_tokens, q_heads, D] in T: out *= sigmoid(gate)
+  const void* gate;  // null, or q_tokens x q_heads rows of D in T: out *= sigmoid(gate)
+  int64_t gate_stride;  // elements between the gate rows of (token, head)
   void* out;
   int64_t ks_pos, vs_pos;  // elements between cache rows (head stride = head_dim)
   int64_t pos0;            // absolute position of query token 0
@@ -782,7 +783,8 @@ __device__ __forceinline__ void prefill_run(const PrefillArgs& a, int kvh, int c
     TO* op = (TO*)a.out + ofs;
     if (a.gate != nullptr) {  // the sigmoid output gate, before the single rounding
       typedef typename Vec4<T>::type V4;
-      const T* gp = (const T*)a.gate + ofs;
+      const T* gp =
+          (const T*)a.gate + ((int64_t)tok[qb] * a.q_heads + hq[qb]) * a.gate_stride + 4 * quad;
       V4 gv[MB];
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) gv[mb] = *(const V4*)(gp + 16 * mb);
@@ -1023,7 +1025,7 @@ int prefill_impl(const void* q, const void* key, const void* value, const void* 
                  int64_t v_pos_stride, int64_t q_pos0, int window, int64_t kv_start, float scale,
                  int dtype, int out_dtype, void* stream, const int32_t* pages = nullptr,
                  int page_shift = 0, int num_pages = 0, const void* kn = nullptr,
-                 const void* vn = nullptr) {
+                 const void* vn = nullptr, int64_t gate_stride = 0) {
   using namespace alpx;
   if (!q || !key || !value || !out) return fail(ALPX_EINVAL, "alpx_prefill_causal: null buffer");
   if (!dtype_ok(dtype) || !dtype_ok(out_dtype))
@@ -1049,7 +1051,9 @@ int prefill_impl(const void* q, const void* key, const void* value, const void* 
   if (kn != nullptr && (k_pos_stride != (int64_t)kv_heads * key_dim ||
                         v_pos_stride != (int64_t)kv_heads * value_dim))
     return fail(ALPX_EINVAL, "alpx_prefill_append: cache rows must be contiguous");
+  if (gate_stride == 0) gate_stride = value_dim;
   const uintptr_t align = (uintptr_t)q | (uintptr_t)key | (uintptr_t)value | (uintptr_t)gate |
+                          (uintptr_t)(gate_stride * es) |
                           (uintptr_t)kn | (uintptr_t)vn | (uintptr_t)(k_pos_stride * es) |
                           (uintptr_t)(v_pos_stride * es);
   const bool mfma = dtype != ALPX_F32 && key_dim == value_dim &&
@@ -1096,6 +1100,7 @@ int prefill_impl(const void* q, const void* key, const void* value, const void* 
     a.k = key;
     a.v = value;
     a.gate = gate;
+    a.gate_stride = gate_stride;
     a.out = out;
     a.ks_pos = k_pos_stride;
     a.vs_pos = v_pos_stride;
@@ -1133,6 +1138,7 @@ int prefill_impl(const void* q, const void* key, const void* value, const void* 
   a.v = value;
   a.seq_lens = nullptr;
   a.gate = gate;  // the combine pass applies it ([token][head][d] = [b][h][d])
+  a.gate_stride = gate_stride;
   a.out = out;
   a.ks_pos = k_pos_stride;
   a.ks_b = 0;
@@ -1200,6 +1206,44 @@ extern "C" int alpx_prefill_append(const void* q, const void* key, const void* v
                       (int)(position + q_tokens), q_heads, kv_heads, key_dim, value_dim,
                       (int64_t)kv_heads * key_dim, (int64_t)kv_heads * value_dim, position, window,
                       0, scale, dtype, out_dtype, stream, nullptr, 0, 0, key, value);
+}
+
+extern "C" int alpx_attention_layer_prefill(
+    const void* query_gate, const void* key, const void* value, const float* q_norm,
+    const float* k_norm, void* query_out, void* key_cache, void* value_cache, void* out,
+    void* workspace, size_t workspace_bytes, int dtype, int out_dtype, int64_t capacity,
+    int cache_batch, int batch_index, int tokens, int q_heads, int kv_heads, int head_dim,
+    int64_t position, const int* sections, double frequency_base, float eps, float scale,
+    void* stream) {
+  using namespace alpx;
+  if (!out) return fail(ALPX_EINVAL, "alpx_attention_layer_prefill: null buffer");
+  if (!dtype_ok(dtype) || !dtype_ok(out_dtype))
+    return fail(ALPX_EINVAL, "alpx_attention_layer_prefill: unknown dtype");
+  if (tokens <= 0 || head_dim <= 0 || kv_heads <= 0 || cache_batch <= 0)
+    return fail(ALPX_EINVAL, "alpx_attention_layer_prefill: sizes must be positive");
+  if (head_dim > 256)
+    return fail(ALPX_EUNSUPPORTED, "alpx_prefill_causal: head dims above 256 are not supported");
+  if (position + tokens > INT32_MAX)
+    return fail(ALPX_EUNSUPPORTED, "alpx_attention_layer_prefill: more than 2^31 - 1 cache rows");
+  // The prefill's checks that need no device work, first: a failing call
+  // must not have written the caches.
+  if (!workspace && !(dtype != ALPX_F32 && (head_dim == 64 || head_dim == 128 || head_dim == 256)))
+    return fail(ALPX_EINVAL, "alpx_prefill_causal: null workspace");
+  if (!(scale > 0.0f) || !isfinite(scale))
+    return fail(ALPX_EINVAL, "attention scale must be positive and finite");
+  const int rc = alpx_attention_prologue_chunk(
+      query_gate, key, value, q_norm, k_norm, query_out, nullptr, key_cache, value_cache, dtype,
+      capacity, cache_batch, batch_index, tokens, q_heads, kv_heads, head_dim, head_dim, position,
+      sections, frequency_base, eps, stream);
+  if (rc != ALPX_OK) return rc;
+  const size_t es = dtype_size(dtype);
+  const int64_t row = (int64_t)cache_batch * kv_heads * head_dim;
+  const int64_t seq = (int64_t)batch_index * kv_heads * head_dim;
+  return prefill_impl(query_out, (const char*)key_cache + seq * es,
+                      (const char*)value_cache + seq * es, (const char*)query_gate + head_dim * es,
+                      out, workspace, workspace_bytes, tokens, (int)(position + tokens), q_heads,
+                      kv_heads, head_dim, head_dim, row, row, position, 0, 0, scale, dtype,
+                      out_dtype, stream, nullptr, 0, 0, nullptr, nullptr, 2 * (int64_t)head_dim);
 }
 
 extern "C" int alpx_prefill_causal_paged(const void* q, const void* key_pages,

@@ -971,7 +971,8 @@ class Qwen35RocmOps:
         ``value [T, Hkv * Dv]`` of cache sequence ``batch_index`` at
         positions ``position .. position + T - 1`` as one fused prologue
         (split, Q/K RMSNorm, IMROPE, cache append) and one causal prefill
-        attention over the cache with the sigmoid gate in its epilogue.  Returns
+        attention over the cache with the sigmoid gate in its epilogue, read in
+        place from ``query_gate`` (alpx_attention_layer_prefill).  Returns
         ``(gated output [T, Hq, Dv], position + T)``."""
         key_cache = self._tensor(key_cache, "attention key cache", dimensions=4)
         value_cache = self._tensor(value_cache, "attention value cache", dimensions=4)
@@ -1007,13 +1008,15 @@ class Qwen35RocmOps:
         if len(sections) != 4:
             raise ValueError("IMRoPE requires four sections")
         section = tuple(_nonnegative_integer("IMRoPE section", item) for item in sections)
-        query, gate = _ops.attention_prologue_chunk(
+        if value_width != width:
+            raise ValueError("sigmoid gate must match values")
+        scale_value = (1.0 / math.sqrt(width) if scale is None
+                       else _positive_finite("attention scale", scale))
+        gated = _ops.attention_layer_prefill(
             query_gate.reshape(tokens, query_heads, 2 * width), key, value, query_norm,
             key_norm, key_cache, value_cache, batch_index=batch_index, position=position,
             sections=section, frequency_base=_positive_finite("frequency_base", frequency_base),
-            eps=_positive_finite("epsilon", epsilon))
-        gated = self.attention_prefill(query, key_cache, value_cache, position=position,
-                                       batch_index=batch_index, scale=scale, gate=gate)
+            eps=_positive_finite("epsilon", epsilon), scale=scale_value)
         return gated, position + tokens
 
     def recurrent_layer_prefill_(self, workspace: RocmRecurrentWorkspace, mixed: Any,

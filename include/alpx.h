@@ -476,7 +476,9 @@ int alpx_recurrent_step(const float* current, const float* conv_weight, int64_t 
  * Replaces the prologue half of the reference's token-sequential prefill,
  * one Qwen35Model._attention call per token (qwen35_runtime.py:597-650,
  * driven by prefill_state, qwen35_runtime.py:777-810); the chunk then runs
- * alpx_prefill_causal over the cache and alpx_sigmoid_gate. */
+ * alpx_prefill_causal over the cache and alpx_sigmoid_gate.  gate_out may
+ * be null (the gate half is then not copied; alpx_attention_layer_prefill
+ * reads it in place). */
 int alpx_attention_prologue_chunk(const void* query_gate, const void* key, const void* value,
                                   const float* q_norm, const float* k_norm, void* query_out,
                                   void* gate_out, void* key_cache, void* value_cache, int dtype,
@@ -484,6 +486,27 @@ int alpx_attention_prologue_chunk(const void* query_gate, const void* key, const
                                   int q_heads, int kv_heads, int head_dim, int value_dim,
                                   int64_t position, const int* sections, double frequency_base,
                                   float eps, void* stream);
+
+/* A prefill chunk of the Qwen3.5 full-attention layer after its
+ * projections, in two launches: the chunk prologue (alpx_attention_prologue_
+ * chunk, without the gate copy: query rows into query_out [T, Hq, D], key /
+ * value rows into the caches) and the causal prefill over cache rows
+ * 0 .. position + t with the sigmoid gate read in place from the second
+ * half of each head's query_gate row (row stride 2 D) -- what
+ * alpx_attention_prologue_chunk + alpx_prefill_causal_gated compute, bit
+ * for bit, without the 2 x T x Hq x D gate copy.  Replaces the reference's
+ * token-sequential Qwen35Model._attention calls of a prefill
+ * (qwen35_runtime.py:597-665, prefill_state qwen35_runtime.py:777-810).
+ * value_dim must equal head_dim (the gate has head_dim values per head);
+ * workspace as alpx_prefill_causal (only its fallback path uses it). */
+int alpx_attention_layer_prefill(const void* query_gate, const void* key, const void* value,
+                                 const float* q_norm, const float* k_norm, void* query_out,
+                                 void* key_cache, void* value_cache, void* out, void* workspace,
+                                 size_t workspace_bytes, int dtype, int out_dtype,
+                                 int64_t capacity, int cache_batch, int batch_index, int tokens,
+                                 int q_heads, int kv_heads, int head_dim, int64_t position,
+                                 const int* sections, double frequency_base, float eps,
+                                 float scale, void* stream);
 
 /* Qwen3.5 recurrent-layer inputs for a prefill chunk of one sequence: the
  * depthwise causal convolution + SiLU of current [T, C] (C = 2 Hk Dk +

@@ -108,6 +108,44 @@ def test_attention_layer_prefill_matches_token_chain(gpu, ops, hq, hkv, d, secti
     assert np.abs(_np(KC)[:prefix + tokens, bi] - kco[:prefix + tokens]).max() <= 2e-2
 
 
+@pytest.mark.parametrize("hq,hkv,d,prefix,tokens,batch,bi,dtype", [
+    (16, 2, 256, 300, 130, 2, 1, "bf16"), (8, 2, 128, 0, 70, 1, 0, "f16"),
+    (4, 2, 64, 40, 33, 1, 0, "f32")])
+def test_attention_layer_prefill_equals_prologue_then_gated_prefill(gpu, hq, hkv, d, prefix,
+                                                                    tokens, batch, bi, dtype):
+    """alpx_attention_layer_prefill (prologue without the gate copy, the
+    prefill reading the gate in place from the joint projection, row stride
+    2 D) gives the bits of alpx_attention_prologue_chunk (gate copied) +
+    alpx_prefill_causal_gated: output and both caches (fp32 runs the split-K
+    fallback, whose combine applies the gate)."""
+    import torch
+    P = _mod("_ops")
+    td = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[dtype]
+    rng = np.random.default_rng(hq + d + prefix)
+    cap = prefix + tokens + 5
+    sec, base, eps = (11, 11, 10, 0), 1e6, 1e-6
+    t = lambda a: torch.from_numpy(I.round_to(a, dtype).astype(np.float32)).to(gpu).to(td)  # noqa: E731
+    kc0 = t(rng.standard_normal((cap, batch, hkv, d)))
+    vc0 = t(rng.standard_normal((cap, batch, hkv, d)))
+    qg = t(rng.standard_normal((tokens, hq, 2 * d)) * 3)
+    k = t(rng.standard_normal((tokens, hkv, d)) * 3)
+    v = t(rng.standard_normal((tokens, hkv, d)))
+    qw = torch.from_numpy(rng.uniform(0.5, 1.5, d).astype(np.float32)).to(gpu)
+    kw = torch.from_numpy(rng.uniform(0.5, 1.5, d).astype(np.float32)).to(gpu)
+    KA, VA = kc0.clone(), vc0.clone()
+    out_a = P.attention_layer_prefill(qg, k, v, qw, kw, KA, VA, batch_index=bi, position=prefix,
+                                      sections=sec, frequency_base=base, eps=eps)
+    KB, VB = kc0.clone(), vc0.clone()
+    q, g = P.attention_prologue_chunk(qg, k, v, qw, kw, KB, VB, batch_index=bi, position=prefix,
+                                      sections=sec, frequency_base=base, eps=eps)
+    out_b = P.prefill(q, KB[:, bi], VB[:, bi], pos0=prefix, kv_tokens=prefix + tokens,
+                      k_pos_stride=batch * hkv * d, v_pos_stride=batch * hkv * d, gate=g)
+    torch.cuda.synchronize()
+    assert torch.equal(KA, KB) and torch.equal(VA, VB)
+    assert torch.equal(out_a, out_b)
+    assert torch.equal(g, qg[:, :, d:])  # the copied gate is the joint row's second half
+
+
 def test_attention_layer_prefill_rejects_bad_shapes(gpu, ops):
     import torch
     KC = torch.zeros((16, 1, 2, 64), dtype=torch.bfloat16, device=gpu)
