@@ -33,8 +33,15 @@ def ops(gpu):
     return _mod("qwen35_rocm_ops").Qwen35RocmOps()
 
 
-def test_c3_append_then_prefill_bf16_full_size(gpu, ops):
+@pytest.mark.parametrize("kernel", ["auto", "pair"])
+def test_c3_append_then_prefill_bf16_full_size(gpu, ops, monkeypatch, kernel):
+    """C3 at full size through append_prefill_attention_ (one launch: the
+    chunk's rows read from k_new / v_new and written to the cache by the
+    kernel), with the kernel the host picks (one tile per block at C3) and
+    with the paired kernel forced."""
     import torch
+    if kernel != "auto":
+        monkeypatch.setenv("ALPX_PREFILL_KERNEL", kernel)
     c = I.c3_prefill_bf16()
     cap = 4096
     ws = ops.initialize_attention_workspace(capacity=cap, batch_size=1, kv_heads=8,
@@ -62,6 +69,34 @@ def test_c3_append_then_prefill_bf16_full_size(gpu, ops):
     dec = ops.online_attention(_dev(torch, c["q"][-1:], "bf16", gpu), ws.key_cache,
                                ws.value_cache, length=4096, out_dtype=torch.float32)
     assert np.abs(dec.cpu().numpy()[0] - out[-1].float().cpu().numpy()).max() <= TOL["bf16"]
+
+
+def test_qwen35_geometry_full_size_kernels_agree(gpu, monkeypatch):
+    """The Qwen3.5 attention-layer chunk at full size (2048 queries on a
+    2048-row prefix, 16/2 heads, head_dim 256, gated; the host picks the
+    paired kernel here): paired and one-tile-per-block kernels agree within
+    the bf16 tolerance, and the last row equals the gated decode of the full
+    cache (size-independent checks; the oracle covers these kernels at
+    smaller sizes)."""
+    import torch
+    g = torch.Generator(device=gpu).manual_seed(11)
+    tq, prefix, hq, hkv, d = 2048, 2048, 16, 2, 256
+    K = torch.randn((prefix + tq, 1, hkv, d), generator=g, device=gpu).to(torch.bfloat16)
+    V = torch.randn((prefix + tq, 1, hkv, d), generator=g, device=gpu).to(torch.bfloat16)
+    q = torch.randn((tq, hq, d), generator=g, device=gpu).to(torch.bfloat16)
+    gate = (torch.randn((tq, hq, d), generator=g, device=gpu) * 2).to(torch.bfloat16)
+    ops = _mod("qwen35_rocm_ops").Qwen35RocmOps()
+    outs = {}
+    for kernel in ("pair", "single"):
+        monkeypatch.setenv("ALPX_PREFILL_KERNEL", kernel)
+        outs[kernel] = ops.attention_prefill(q, K, V, position=prefix, gate=gate,
+                                             out_dtype=torch.float32)
+    monkeypatch.delenv("ALPX_PREFILL_KERNEL")
+    torch.cuda.synchronize()
+    assert (outs["pair"] - outs["single"]).abs().max().item() <= TOL["bf16"]
+    dec = ops.online_attention(q[-1:], K, V, length=prefix + tq, gate=gate[-1:],
+                               out_dtype=torch.float32)
+    assert (dec[0] - outs["pair"][-1]).abs().max().item() <= TOL["bf16"]
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "f16", "f32"])
