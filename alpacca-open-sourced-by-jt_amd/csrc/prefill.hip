@@ -283,24 +283,30 @@ constexpr int kRunWrite = 0, kRunPartial = 1, kRunMerge = 2;
 // prefill_mfma runs one per block; prefill_pair runs two groups per block.
 // part_o / part_st: the partial's LDS home (written by kRunPartial, read by
 // kRunMerge).
-template <typename T, typename TO, int D, int BK, int NQB, bool PAGED, int MODE, typename Bar>
+template <typename T, typename TO, int D, int BK, int NQB, bool PAGED, int MODE, int NW,
+          typename Bar>
 __device__ __forceinline__ void prefill_run(const PrefillArgs& a, int kvh, int ctile, int tb,
                                             int te, char* smem, float* part_o, float* part_st,
-                                            int wave, int tid, Bar& bar) {
+                                            int wave, int tid, Bar& bar, int lw, int hi_blk,
+                                            bool idle) {
   typedef typename Vec8<T>::type V8;
   constexpr int U = D / 8;                  // 16-byte units per row
   constexpr int kRowB = D * (int)sizeof(T);
   constexpr int kTileB = BK * kRowB;        // one K or V tile
-  constexpr int kIW = BK * U / 256;         // direct-load instructions per wave per tile
+  constexpr int kIW = BK * U / (64 * NW);   // direct-load instructions per wave per tile
   constexpr int KB = BK / 16;
   constexpr int KK = BK / 32;
   constexpr int MB = D / 16;
   constexpr int KS = D / 32;
   constexpr int kWaveCols = 16 * NQB;
   constexpr int kCols = 4 * kWaveCols;
-  static_assert(kIW >= 1 && BK * U % 256 == 0, "tile must split evenly over 4 waves");
+  static_assert(kIW >= 1 && BK * U % (64 * NW) == 0, "tile must split evenly over the waves");
+  static_assert(NW == 4 || (!PAGED && MODE == kRunWrite), "shared tiles: contiguous, one run");
+  static_assert(kTileB % (64 * NW * 16) == 0, "the V buffer zeroing splits evenly");
   static_assert(U >= 8, "the row swizzle needs 8 units per row");
-  // K tile buffers at smem and smem + kTileB, V tile buffers at 2 and 3 kTileB.
+  // K tile buffers at smem and smem + kTileB, V tile buffers at 2 and 3 kTileB,
+  // loaded and read by the NW waves that share them (lw = 0 .. NW - 1 among
+  // them; `wave` = 0 .. 3 places this wave's columns in its column tile).
 
   const int lane = tid & 63;
   const int hl = lane & 15;
@@ -315,7 +321,7 @@ __device__ __forceinline__ void prefill_run(const PrefillArgs& a, int kvh, int c
 #pragma unroll
   for (int qb = 0; qb < NQB; ++qb) {
     const int c = wcol0 + 16 * qb + hl;
-    cok[qb] = c < cols;
+    cok[qb] = c < cols && !idle;
     const int cc = cok[qb] ? c : cols - 1;
     tok[qb] = cc / G;
     hq[qb] = kvh * G + (cc - tok[qb] * G);
@@ -329,7 +335,11 @@ __device__ __forceinline__ void prefill_run(const PrefillArgs& a, int kvh, int c
   const int wt_last = (min(wcol0 + kWaveCols, cols) - 1) / G;
 
   // Key rows [lo, hi) that any column of the block can see, in nt tiles.
-  const int hi = max(0, min(a.kv_tokens, rel0 + bt_last + 1));
+  // Waves sharing tiles with a heavier column tile walk its key range
+  // (hi_blk) but compute only over their own tiles (nt_own), then keep
+  // loading and meeting the barrier.
+  const int hi_own = max(0, min(a.kv_tokens, rel0 + bt_last + 1));
+  const int hi = hi_blk >= 0 ? hi_blk : hi_own;
   int lo = 0;
   if (a.window > 0) lo = min(hi, max(0, rel0 + bt_first - a.window + 1)) / BK * BK;
   // Every wave walks all nt tiles of the block; keys a wave's columns cannot
@@ -341,6 +351,7 @@ __device__ __forceinline__ void prefill_run(const PrefillArgs& a, int kvh, int c
   const int t_end = te < 0 ? nt_all : min(te, nt_all);
   const int nt = max(0, t_end - tb);
   const int hi_r = min(hi, lo + t_end * BK);
+  const int nt_own = idle ? -1 : (hi_blk >= 0 ? (hi_own - lo + BK - 1) / BK : nt);
 
   // B operand of S^T = K Q^T: lane holds Q[column][32 ks + 8 quad + 0..7],
   // pre-multiplied by scale * log2(e) (and rounded once to T), so that the
@@ -384,7 +395,7 @@ __device__ __forceinline__ void prefill_run(const PrefillArgs& a, int kvh, int c
   uint32_t kofs[kIW], vofs[kIW];
 #pragma unroll
   for (int t = 0; t < kIW; ++t) {
-    const int sl = (wave * kIW + t) * 64 + lane;
+    const int sl = (lw * kIW + t) * 64 + lane;
     const int row = sl / U;
     const int ck = (sl % U) ^ swz_k<kRowB>(row);
     const int cv = (sl % U) ^ swz_v<kRowB>(row);
@@ -436,7 +447,7 @@ __device__ __forceinline__ void prefill_run(const PrefillArgs& a, int kvh, int c
       base = g + (int64_t)pg * page_stride + (int64_t)(k0 & ((1 << a.page_shift) - 1)) * pos;
     const uint32_t bytes = (uint32_t)((int64_t)(a.kv_tokens - k0) * pos * (int64_t)sizeof(T));
     const uint32_t lds0 =
-        (uint32_t)(uintptr_t)(lds_void_t*)(smem + buf * kTileB + wave * kIW * 1024);
+        (uint32_t)(uintptr_t)(lds_void_t*)(smem + buf * kTileB + lw * kIW * 1024);
     if (!PAGED && gn != nullptr && k0 + BK > a.new0) {
       // Rows >= new0 come from the chunk's rows: a resource whose offset of
       // tile row i is the one of row k0 + i, based new0 - k0 rows before gn.
@@ -453,7 +464,7 @@ __device__ __forceinline__ void prefill_run(const PrefillArgs& a, int kvh, int c
                                   (uint32_t)((int64_t)(a.new0 - k0) * pos * (int64_t)sizeof(T)));
 #pragma unroll
       for (int i = 0; i < kIW; ++i) {
-        if (((wave * kIW + i) * 64 + lane) / U < a.new0 - k0)
+        if (((lw * kIW + i) * 64 + lane) / U < a.new0 - k0)
           lds_dma16(rc, lds0 + i * 1024, ofs[i]);
         else
           lds_dma16(rn, lds0 + i * 1024, ofs[i]);
@@ -667,41 +678,45 @@ __device__ __forceinline__ void prefill_run(const PrefillArgs& a, int kvh, int c
       load_tile(kg, kgn, a.ks_pos, a.ks_page, kofs, j + 2, P, kpage[P]);
     }
     if (j < nt) load_tile(vg, vgn, a.vs_pos, a.vs_page, vofs, j, 2 + P, v_page);
-    // Rescale for the m moved at tile j - 1 (O holds tiles <= j - 2 and is
-    // about to take PV(j - 1), formed against the moved m; l was rescaled
-    // at the move, before it took tile j - 1's P).
-    if (__builtin_expect(pend_any, 0)) {
+    // Waves past their own key tiles (sharing a heavier tile's stream)
+    // only load and meet the barrier.
+    if (NW == 4 || j <= nt_own) {
+      // Rescale for the m moved at tile j - 1 (O holds tiles <= j - 2 and is
+      // about to take PV(j - 1), formed against the moved m; l was rescaled
+      // at the move, before it took tile j - 1's P).
+      if (__builtin_expect(pend_any, 0)) {
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) {
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb) o[qb][mb] *= pend[qb];
+          pend[qb] = 1.f;
+        }
+        pend_any = false;
+      }
+      if (__builtin_expect(need_mask(j), 0)) mask(j);
+      if (__builtin_expect(grow_check(), 0)) move_max();
+      // One basic block of independent MFMA and VALU work.  At j = 0 the PV
+      // step multiplies zeroed P by a zeroed V buffer; at j = nt the softmax
+      // sees a fully masked tile (k0 >= hi_r) and its P is never used.
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_setprio(1);
+      block(Par<P>());
+      __builtin_amdgcn_s_setprio(0);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int qb = 0; qb < NQB; ++qb) {
+        pin(m[qb]);
+        pin(mc[qb]);
+        pin(lim[qb]);
+        pin(pend[qb]);
+        pin(lsum[qb]);
 #pragma unroll
-        for (int mb = 0; mb < MB; ++mb) o[qb][mb] *= pend[qb];
-        pend[qb] = 1.f;
+        for (int mb = 0; mb < MB; ++mb) pin(o[qb][mb]);
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) pin(pv[P][kk][qb]);
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) pin(sc[kb][qb]);
       }
-      pend_any = false;
-    }
-    if (__builtin_expect(need_mask(j), 0)) mask(j);
-    if (__builtin_expect(grow_check(), 0)) move_max();
-    // One basic block of independent MFMA and VALU work.  At j = 0 the PV
-    // step multiplies zeroed P by a zeroed V buffer; at j = nt the softmax
-    // sees a fully masked tile (k0 >= hi_r) and its P is never used.
-    __builtin_amdgcn_sched_barrier(0);
-    __builtin_amdgcn_s_setprio(1);
-    block(Par<P>());
-    __builtin_amdgcn_s_setprio(0);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int qb = 0; qb < NQB; ++qb) {
-      pin(m[qb]);
-      pin(mc[qb]);
-      pin(lim[qb]);
-      pin(pend[qb]);
-      pin(lsum[qb]);
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) pin(o[qb][mb]);
-#pragma unroll
-      for (int kk = 0; kk < KK; ++kk) pin(pv[P][kk][qb]);
-#pragma unroll
-      for (int kb = 0; kb < KB; ++kb) pin(sc[kb][qb]);
     }
     __builtin_amdgcn_s_waitcnt(0);
     bar();
@@ -709,8 +724,8 @@ __device__ __forceinline__ void prefill_run(const PrefillArgs& a, int kvh, int c
 
   // Zero V buffer 1 (read by the j = 0 PV step) and the P operands it uses.
 #pragma unroll
-  for (int i = 0; i < kTileB / (256 * 16); ++i)
-    *(u32x4*)(smem + 3 * kTileB + (i * 256 + tid) * 16) = (u32x4){0u, 0u, 0u, 0u};
+  for (int i = 0; i < kTileB / (64 * NW * 16); ++i)
+    *(u32x4*)(smem + 3 * kTileB + ((i * NW + lw) * 64 + lane) * 16) = (u32x4){0u, 0u, 0u, 0u};
 #pragma unroll
   for (int kk = 0; kk < KK; ++kk)
 #pragma unroll
@@ -823,8 +838,8 @@ prefill_mfma(PrefillArgs a) {
     if (ctile < mirror) copy_tile_rows<T, D, kCols>(a, kvh, mirror, tid);
   }
   auto bar = []() __attribute__((always_inline)) { __syncthreads(); };
-  prefill_run<T, TO, D, BK, NQB, PAGED, kRunWrite>(a, kvh, ctile, 0, -1, smem, nullptr, nullptr,
-                                                   wave, tid, bar);
+  prefill_run<T, TO, D, BK, NQB, PAGED, kRunWrite, 4>(a, kvh, ctile, 0, -1, smem, nullptr,
+                                                      nullptr, wave, tid, bar, wave, -1, false);
 }
 
 // Work of a prefill_pair block: kv head kvh and the column tiles ta (light:
@@ -906,17 +921,52 @@ prefill_pair(PrefillArgs a) {
     // the light tile, then the heavy tile's key tiles [split, nt_b)
     if (ta != tbt) {
       if (a.kn != nullptr) copy_tile_rows<T, D, kCols>(a, kvh, ta, gtid);
-      prefill_run<T, TO, D, BK, NQB, false, kRunWrite>(a, kvh, ta, 0, -1, gsmem, nullptr, nullptr,
-                                                       gw, gtid, bar);
+      prefill_run<T, TO, D, BK, NQB, false, kRunWrite, 4>(a, kvh, ta, 0, -1, gsmem, nullptr,
+                                                          nullptr, gw, gtid, bar, gw, -1, false);
     }
-    prefill_run<T, TO, D, BK, NQB, false, kRunPartial>(a, kvh, tbt, split, -1, gsmem,
-                                                       (float*)smem, part_st, gw, gtid, bar);
+    prefill_run<T, TO, D, BK, NQB, false, kRunPartial, 4>(a, kvh, tbt, split, -1, gsmem,
+                                                          (float*)smem, part_st, gw, gtid, bar,
+                                                          gw, -1, false);
   } else {
     // the heavy tile's key tiles [0, split), merged with group 0's part
     if (a.kn != nullptr) copy_tile_rows<T, D, kCols>(a, kvh, tbt, gtid);
-    prefill_run<T, TO, D, BK, NQB, false, kRunMerge>(a, kvh, tbt, 0, split, gsmem, (float*)smem,
-                                                     part_st, gw, gtid, bar);
+    prefill_run<T, TO, D, BK, NQB, false, kRunMerge, 4>(a, kvh, tbt, 0, split, gsmem,
+                                                        (float*)smem, part_st, gw, gtid, bar, gw,
+                                                        -1, false);
   }
+}
+
+// One K/V tile stream for a light and a heavy column tile: one block of
+// eight waves per CU takes column tile ta (waves 0-3) and its mirror
+// tb = col_tiles - 1 - ta (waves 4-7) of one kv head.  Without a window
+// both walk the key tiles from row 0, so one set of tile buffers, loaded
+// by all eight waves, serves both tiles: half the direct-load bytes per
+// FLOP of two four-wave blocks, which load the same tiles separately.  The
+// loads' LDS writes and texture-path time are about a fifth of the
+// four-wave kernel's loop at head_dim 128, where LDS reads (K operands at
+// 244 B/clk per CU, transposing V reads at 131) and those writes come
+// close to the MFMA time.  The light waves stop computing after their own
+// last key tile and keep loading; the middle tile of an odd count goes to
+// waves 4-7 alone.
+template <typename T, typename TO, int D, int BK, int NQB>
+__global__ void __launch_bounds__(512, 1)
+prefill_shared(PrefillArgs a) {
+  constexpr int kTileB = BK * D * (int)sizeof(T);
+  constexpr int kCols = 64 * NQB;
+  __shared__ __attribute__((aligned(1024))) char smem[4 * kTileB];
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wave >> 2;
+  int kvh, ta, tbt;
+  if (!pair_work(a, kvh, ta, tbt)) return;
+  int lo, hi_b, ntb;
+  tile_keys<BK, kCols>(a, tbt, lo, hi_b, ntb);
+  if (a.kn != nullptr && (grp == 1 || ta != tbt))
+    copy_tile_rows<T, D, kCols>(a, kvh, grp == 0 ? ta : tbt, tid & 255);
+  auto bar = []() __attribute__((always_inline)) { __syncthreads(); };
+  prefill_run<T, TO, D, BK, NQB, false, kRunWrite, 8>(a, kvh, grp == 0 ? ta : tbt, 0, -1, smem,
+                                                      nullptr, nullptr, wave & 3, tid, bar, wave,
+                                                      hi_b, grp == 0 && ta == tbt);
 }
 
 template <typename T, typename TO>
@@ -957,6 +1007,25 @@ const void* pick_pair(int D) {
     case 256: return (const void*)prefill_pair<T, TO, 256, 32, 1>;
   }
   return nullptr;
+}
+
+template <typename T, typename TO>
+const void* pick_shared(int D) {
+  switch (D) {
+    case 64: return (const void*)prefill_shared<T, TO, 64, 64, 2>;
+    case 128: return (const void*)prefill_shared<T, TO, 128, 64, 2>;
+    case 256: return (const void*)prefill_shared<T, TO, 256, 32, 1>;
+  }
+  return nullptr;
+}
+
+template <typename T>
+const void* pick_shared_out(int D, int out_dtype) {
+  switch (out_dtype) {
+    case ALPX_F32: return pick_shared<T, float>(D);
+    case ALPX_F16: return pick_shared<T, f16_t>(D);
+    default: return pick_shared<T, bf16_t>(D);
+  }
 }
 
 template <typename T>
@@ -1002,21 +1071,44 @@ int host_tile_keys(int q_tokens, int kv_tokens, int group, int rel0, int window,
 // 512 query tokens (64 pairs) 1.37; 8192 tokens at prefix 0 (four rounds
 // of pairs) 1.02.  So: pairs must form one round that fills the device,
 // and the heaviest column tile must walk at least R times the key tiles of
-// the lightest, R = 3 at head_dim 128 and 1.8 at 64 and 256.
-// ALPX_PREFILL_KERNEL=pair or =single overrides the choice.
-bool use_pair(int q_tokens, int kv_tokens, int kv_heads, int group, int rel0, int window,
-              int cols_per_block, int rows, int col_tiles, int key_dim, const void* pair_kernel) {
+// the lightest, R = 3 at head_dim 128 and 1.8 at 64 and 256.  At head_dim
+// 256 several rounds of pairs pay as well (16/2 heads, pair / single:
+// 4096 tokens at prefix 0 -- 162 / 232 us, at prefix 1024 -- 240 / 292,
+// 8192 tokens at prefix 0 -- 656 / 859).  The shared-stream kernel (one
+// tile stream for both tiles of a pair, no window start inside the chunk)
+// pays off at head_dim 256 with long prefixes only (2048 tokens, 16/2
+// heads, shared / pair / single, us, one box: prefix 1024 -- 86.9 / 82.7 /
+// 96.6, 1536 -- 101.8 / 99.4 / 113.0, 2048 -- 118.9 / 115.8 / 127.7, 8192
+// -- 304.5 / 316.1 / 311.4; another box: 4096 -- 178.4 / 187.7 / 191.1;
+// head_dim 128 at prefix 2048: 104.7 / 105.4 / 100.8, head_dim 64: 72.1 /
+// 65.2 / 66.4), so it takes one round of pairs below a ratio of
+// kSharedBelow10 / 10.
+// ALPX_PREFILL_KERNEL=pair, =shared or =single overrides the choice
+// (=shared falls back to the single kernel where one stream cannot serve).
+enum PrefillKernelChoice { kSingleKernel, kPairKernel, kSharedKernel };
+constexpr int kSharedBelow10 = 16;
+
+PrefillKernelChoice choose_prefill(int q_tokens, int kv_tokens, int kv_heads, int group, int rel0,
+                                   int window, int cols_per_block, int rows, int col_tiles,
+                                   int key_dim, const void* pair_kernel) {
+  // both tiles of a pair walk the key rows from 0 when no window starts inside the chunk
+  const bool one_stream = window <= 0 || (int64_t)window > (int64_t)rel0 + q_tokens;
   const char* force = getenv("ALPX_PREFILL_KERNEL");
-  if (force != nullptr && strcmp(force, "pair") == 0) return true;
-  if (force != nullptr && strcmp(force, "single") == 0) return false;
+  if (force != nullptr && strcmp(force, "pair") == 0) return kPairKernel;
+  if (force != nullptr && strcmp(force, "single") == 0) return kSingleKernel;
+  if (force != nullptr && strcmp(force, "shared") == 0)
+    return one_stream ? kSharedKernel : kSingleKernel;
   const int64_t pairs = (int64_t)kv_heads * ((col_tiles + 1) / 2);
   const int resident = alpx::resident_blocks(pair_kernel, 512, 0);
-  if (pairs > resident || pairs * 10 < (int64_t)resident * 9) return false;
+  const bool one_round = pairs <= resident && pairs * 10 >= (int64_t)resident * 9;
+  if (!one_round && !(key_dim == 256 && pairs > resident)) return kSingleKernel;
   const int first = host_tile_keys(q_tokens, kv_tokens, group, rel0, window, cols_per_block, rows, 0);
   const int last =
       host_tile_keys(q_tokens, kv_tokens, group, rel0, window, cols_per_block, rows, col_tiles - 1);
+  const int64_t ratio10 = (int64_t)last * 10 / std::max(1, first);
+  if (key_dim == 256 && one_round && one_stream && ratio10 < kSharedBelow10) return kSharedKernel;
   const int r10 = key_dim == 128 ? 30 : 18;  // R x 10
-  return (int64_t)last * 10 >= (int64_t)r10 * std::max(1, first);
+  return ratio10 >= r10 ? kPairKernel : kSingleKernel;
 }
 
 int prefill_impl(const void* q, const void* key, const void* value, const void* gate, void* out,
@@ -1071,15 +1163,21 @@ int prefill_impl(const void* q, const void* key, const void* value, const void* 
     const int cols_per_block = key_dim == 256 ? 64 : 128;
     const int tile_rows = key_dim == 256 ? 32 : 64;
     const int col_tiles = (int)(((int64_t)q_tokens * group + cols_per_block - 1) / cols_per_block);
-    const bool pair = pages == nullptr &&
-                      use_pair(q_tokens, kv_tokens, kv_heads, group, (int)(q_pos0 - kv_start), window,
-                               cols_per_block, tile_rows, col_tiles, key_dim,
-                               dtype == ALPX_F16 ? pick_pair_out<f16_t>(key_dim, out_dtype)
-                                                 : pick_pair_out<bf16_t>(key_dim, out_dtype));
+    const PrefillKernelChoice choice =
+        pages != nullptr
+            ? kSingleKernel
+            : choose_prefill(q_tokens, kv_tokens, kv_heads, group, (int)(q_pos0 - kv_start), window,
+                             cols_per_block, tile_rows, col_tiles, key_dim,
+                             dtype == ALPX_F16 ? pick_pair_out<f16_t>(key_dim, out_dtype)
+                                               : pick_pair_out<bf16_t>(key_dim, out_dtype));
+    const bool pair = choice == kPairKernel, shared = choice == kSharedKernel;
     const void* kernel = nullptr;
     if (pages != nullptr)
       kernel = dtype == ALPX_F16 ? pick_kernel_paged<f16_t>(key_dim)
                                  : pick_kernel_paged<bf16_t>(key_dim);
+    else if (shared)
+      kernel = dtype == ALPX_F16 ? pick_shared_out<f16_t>(key_dim, out_dtype)
+                                 : pick_shared_out<bf16_t>(key_dim, out_dtype);
     else if (pair)
       kernel = dtype == ALPX_F16 ? pick_pair_out<f16_t>(key_dim, out_dtype)
                                  : pick_pair_out<bf16_t>(key_dim, out_dtype);
@@ -1113,13 +1211,14 @@ int prefill_impl(const void* q, const void* key, const void* value, const void* 
     a.kv_heads = kv_heads;
     a.group = group;
     a.col_tiles = col_tiles;
-    const int64_t items = (int64_t)(pair ? (a.col_tiles + 1) / 2 : a.col_tiles) * kv_heads;
+    const bool paired = pair || shared;  // a light and a heavy column tile per block
+    const int64_t items = (int64_t)(paired ? (a.col_tiles + 1) / 2 : a.col_tiles) * kv_heads;
     a.per_xcd = (int)((items + kXcds - 1) / kXcds);
     a.scale_log2 = scale * kLog2e;
     TimedRegion timed(ALPX_T_PREFILL, s);
     void* args[] = {(void*)&a};
-    hipError_t err = hipLaunchKernel(kernel, dim3(a.per_xcd * kXcds), dim3(pair ? 512 : 256), args,
-                                     0, s);
+    hipError_t err = hipLaunchKernel(kernel, dim3(a.per_xcd * kXcds), dim3(paired ? 512 : 256),
+                                     args, 0, s);
     if (err != hipSuccess)
       return fail(ALPX_EHIP, "prefill launch failed: %s", hipGetErrorString(err));
     return check_launch("prefill_mfma");

@@ -33,12 +33,12 @@ def ops(gpu):
     return _mod("qwen35_rocm_ops").Qwen35RocmOps()
 
 
-@pytest.mark.parametrize("kernel", ["auto", "pair"])
+@pytest.mark.parametrize("kernel", ["auto", "pair", "shared"])
 def test_c3_append_then_prefill_bf16_full_size(gpu, ops, monkeypatch, kernel):
     """C3 at full size through append_prefill_attention_ (one launch: the
     chunk's rows read from k_new / v_new and written to the cache by the
     kernel), with the kernel the host picks (one tile per block at C3) and
-    with the paired kernel forced."""
+    with the paired and the shared-stream kernels forced."""
     import torch
     if kernel != "auto":
         monkeypatch.setenv("ALPX_PREFILL_KERNEL", kernel)
@@ -71,29 +71,36 @@ def test_c3_append_then_prefill_bf16_full_size(gpu, ops, monkeypatch, kernel):
     assert np.abs(dec.cpu().numpy()[0] - out[-1].float().cpu().numpy()).max() <= TOL["bf16"]
 
 
-def test_qwen35_geometry_full_size_kernels_agree(gpu, monkeypatch):
+@pytest.mark.parametrize("tq,prefix", [(2048, 2048), (4096, 0)])
+def test_qwen35_geometry_full_size_kernels_agree(gpu, monkeypatch, tq, prefix):
     """The Qwen3.5 attention-layer chunk at full size (2048 queries on a
     2048-row prefix, 16/2 heads, head_dim 256, gated; the host picks the
-    paired kernel here): paired and one-tile-per-block kernels agree within
-    the bf16 tolerance, and the last row equals the gated decode of the full
-    cache (size-independent checks; the oracle covers these kernels at
-    smaller sizes)."""
+    paired kernel here) and 4096 queries at prefix 0 (two rounds of pairs,
+    also paired): the paired and one-tile-per-block kernels
+    agree within the bf16 tolerance, the shared-stream kernel gives the
+    one-tile-per-block kernel's bits (each wave runs the same tiles in the
+    same order), and the last row equals the gated decode of the full cache
+    (size-independent checks; the oracle covers these kernels at smaller
+    sizes)."""
     import torch
     g = torch.Generator(device=gpu).manual_seed(11)
-    tq, prefix, hq, hkv, d = 2048, 2048, 16, 2, 256
+    hq, hkv, d = 16, 2, 256
     K = torch.randn((prefix + tq, 1, hkv, d), generator=g, device=gpu).to(torch.bfloat16)
     V = torch.randn((prefix + tq, 1, hkv, d), generator=g, device=gpu).to(torch.bfloat16)
     q = torch.randn((tq, hq, d), generator=g, device=gpu).to(torch.bfloat16)
     gate = (torch.randn((tq, hq, d), generator=g, device=gpu) * 2).to(torch.bfloat16)
     ops = _mod("qwen35_rocm_ops").Qwen35RocmOps()
     outs = {}
-    for kernel in ("pair", "single"):
+    for kernel in ("pair", "single", "shared"):
         monkeypatch.setenv("ALPX_PREFILL_KERNEL", kernel)
         outs[kernel] = ops.attention_prefill(q, K, V, position=prefix, gate=gate,
                                              out_dtype=torch.float32)
     monkeypatch.delenv("ALPX_PREFILL_KERNEL")
+    outs["auto"] = ops.attention_prefill(q, K, V, position=prefix, gate=gate,
+                                         out_dtype=torch.float32)
     torch.cuda.synchronize()
     assert (outs["pair"] - outs["single"]).abs().max().item() <= TOL["bf16"]
+    assert torch.equal(outs["shared"], outs["single"]) and torch.equal(outs["auto"], outs["pair"])
     dec = ops.online_attention(q[-1:], K, V, length=prefix + tq, gate=gate[-1:],
                                out_dtype=torch.float32)
     assert (dec[0] - outs["pair"][-1]).abs().max().item() <= TOL["bf16"]
@@ -104,10 +111,10 @@ def test_qwen35_geometry_full_size_kernels_agree(gpu, monkeypatch):
     (100, 0, 8, 2, 128, 0), (70, 33, 12, 4, 64, 0), (130, 200, 16, 2, 256, 0),
     (1, 5, 4, 4, 64, 0), (96, 250, 8, 2, 128, 70), (64, 64, 32, 8, 128, 0),
     (300, 17, 3, 1, 128, 0), (45, 100, 24, 2, 256, 40)])
-@pytest.mark.parametrize("kernel", ["pair", "single"])
+@pytest.mark.parametrize("kernel", ["pair", "single", "shared"])
 def test_prefill_append_equals_append_then_prefill(gpu, monkeypatch, kernel, dtype, tq, prefix, hq,
                                                    hkv, d, window):
-    """alpx_prefill_append (one launch on the MFMA path, either contiguous kernel: the chunk's rows
+    """alpx_prefill_append (one launch on the MFMA path, each contiguous kernel: the chunk's rows
     read from key / value, each block writing its own tokens' rows) gives
     the bits of alpx_kv_append followed by alpx_prefill_causal -- output
     and both whole caches -- and the oracle's attention within tolerance.
@@ -175,19 +182,22 @@ def test_prefill_shapes(gpu, ops, dtype, tq, prefix, hq, hkv, d):
     assert err <= TOL[dtype], err
 
 
-@pytest.mark.parametrize("kernel", ["pair", "single"])
+@pytest.mark.parametrize("kernel", ["pair", "single", "shared"])
 @pytest.mark.parametrize("tq,prefix,hq,hkv,d,window,gated", [
     (2048, 0, 4, 1, 128, 0, False), (300, 100, 12, 4, 64, 0, False),
     (161, 7, 8, 2, 256, 0, True), (40, 500, 8, 8, 128, 0, False),
     (700, 300, 16, 4, 128, 200, False), (513, 0, 2, 1, 64, 0, True),
-    (96, 33, 48, 2, 256, 50, False)])
+    (96, 33, 48, 2, 256, 50, False), (300, 100, 8, 2, 256, 1000, True)])
 def test_prefill_kernels_match_oracle(gpu, monkeypatch, kernel, tq, prefix, hq, hkv, d, window,
                                       gated):
-    """Both contiguous MFMA kernels -- the paired one (a light and a heavy
-    column tile per block, the heavy tile's key tiles split between the two
-    wave groups and merged in LDS) and the one-tile-per-block one
-    (ALPX_PREFILL_KERNEL selects each) -- against the oracle: an even and an odd number
-    of column tiles (the middle tile split with itself), a single column
+    """The three contiguous MFMA kernels -- the paired one (a light and a
+    heavy column tile per block, the heavy tile's key tiles split between
+    the two wave groups and merged in LDS), the shared-stream one (a light
+    and a heavy column tile over one K/V tile stream; windows starting
+    inside the chunk fall back to one tile per block) and the
+    one-tile-per-block one (ALPX_PREFILL_KERNEL selects each) -- against the
+    oracle: an even and an odd number of column tiles (the middle tile
+    split with itself, or taken by one wave group alone), a single column
     tile, group sizes that do not divide a block's columns, windows (the
     light tile's key range not a prefix of the heavy one's), head_dim
     64/128/256, gated and not."""
