@@ -96,6 +96,16 @@ SIGNATURES = {
                                            _c_i64, _c_int, _c_int, _c_int, _c_int, _c_i64,
                                            _c_ptr, ctypes.POINTER(ctypes.c_int),
                                            ctypes.c_double, _c_float, _c_float, _c_ptr]),
+    # query_gate, key, value, q_norm, k_norm, key_pages, value_pages, block_table,
+    # max_pages, page_size, num_pages, out, workspace, workspace_bytes, dtype,
+    # out_dtype, batch, q_heads, kv_heads, head_dim, position, positions,
+    # sections, frequency_base, eps, scale, stream
+    "alpx_attention_layer_step_paged": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
+                                                 _c_ptr, _c_ptr, _c_int, _c_int, _c_int, _c_ptr,
+                                                 _c_ptr, _c_size, _c_int, _c_int, _c_int, _c_int,
+                                                 _c_int, _c_int, _c_i64, _c_ptr,
+                                                 ctypes.POINTER(ctypes.c_int), ctypes.c_double,
+                                                 _c_float, _c_float, _c_ptr]),
     "alpx_attention_prologue_chunk": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
                                                _c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_int,
                                                _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,

@@ -474,6 +474,42 @@ def attention_layer_step(query_gate, key, value, q_norm, k_norm, key_cache, valu
     return out
 
 
+def attention_layer_step_paged(query_gate, key, value, q_norm, k_norm, key_pages, value_pages,
+                               block_table, *, position, sections, frequency_base, eps,
+                               positions=None, scale=None, out_dtype=None):
+    """``attention_layer_step`` over a paged pool: pages ``[P, page_size,
+    Hkv, D]`` (fp16 / bf16, D in 64, 128, 256) and ``block_table [B,
+    max_pages]`` (device int32).  Sequence b's rotated key and value land at
+    its logical row ``position`` (or ``positions[b]``) through the table.
+    Returns the gated output ``[B, Hq, D]``."""
+    torch = _torch()
+    num_pages, page_size, kv_heads, dim = (int(x) for x in key_pages.shape)
+    bsz, max_pages = (int(x) for x in block_table.shape)
+    q_heads = int(query_gate.shape[1])
+    if scale is None:
+        scale = 1.0 / math.sqrt(dim)
+    out_dtype = key_pages.dtype if out_dtype is None else out_dtype
+    out = torch.empty((bsz, q_heads, dim), dtype=out_dtype, device=key_pages.device)
+    L = _lib.lib()
+    nbytes = L.alpx_decode_workspace_bytes(bsz, q_heads, kv_heads, dim, int(position) + 1)
+    if nbytes == 0:
+        raise ValueError("invalid attention step sizes")
+    ws = _lib.workspace(torch, key_pages.device, nbytes)
+    pos_ptr = None
+    if positions is not None:
+        positions = positions.to(device=key_pages.device, dtype=torch.int32).contiguous()
+        pos_ptr = positions.data_ptr()
+    rc = L.alpx_attention_layer_step_paged(
+        query_gate.data_ptr(), key.data_ptr(), value.data_ptr(), q_norm.data_ptr(),
+        k_norm.data_ptr(), key_pages.data_ptr(), value_pages.data_ptr(), block_table.data_ptr(),
+        max_pages, page_size, num_pages, out.data_ptr(), ws.data_ptr(), ws.numel(),
+        _lib.dtype_code(torch, key_pages.dtype), _lib.dtype_code(torch, out.dtype), bsz, q_heads,
+        kv_heads, dim, int(position), pos_ptr, _sections(sections), float(frequency_base),
+        float(eps), float(scale), _lib.stream_handle(torch, key_pages.device))
+    _lib.check(rc)
+    return out
+
+
 def attention_prologue_chunk(query_gate, key, value, q_norm, k_norm, key_cache, value_cache, *,
                              batch_index, position, sections, frequency_base, eps):
     """Attention prologue for ``T`` consecutive tokens of cache sequence

@@ -39,7 +39,7 @@
 namespace alpx {
 namespace {
 
-constexpr int kTile = 32;   // rows per wavefront step (MFMA path)
+constexpr int kTile = kDecodeWaveRows;  // rows per wavefront step (MFMA path)
 // Lazy softmax reference of the MFMA split kernel: P stays <= 2^8.
 constexpr float kDecodeRescale = 8.0f;
 // Buffer-load cache policy: nontemporal (V is streamed once per step).
@@ -348,10 +348,23 @@ __device__ __forceinline__ void split_body(const DecodeArgs& a, const SplitProlo
       if (hc == 0) {
         // this wave's own LDS stores above are done before these reads
         __builtin_amdgcn_wave_barrier();
-        T* dst = wave == 0 ? (T*)a.k + pos * a.ks_pos + (int64_t)b * a.ks_b + (int64_t)kvh * a.ks_h
-                           : (T*)a.v + pos * a.vs_pos + (int64_t)b * a.vs_b + (int64_t)kvh * a.vs_h;
+        T* dst = nullptr;
+        if constexpr (PAGED) {
+          // the row's page; a table entry outside the pool writes nothing
+          // (the reads clamp such entries, a write must not land elsewhere)
+          const int pg = a.pages[(int64_t)b * a.max_pages + (int)(pos >> a.page_shift)];
+          const int64_t in_page = pos & ((1 << a.page_shift) - 1);
+          if (pg >= 0 && pg < a.num_pages)
+            dst = wave == 0 ? (T*)a.k + pg * a.ks_page + in_page * a.ks_pos + (int64_t)kvh * a.ks_h
+                            : (T*)a.v + pg * a.vs_page + in_page * a.vs_pos + (int64_t)kvh * a.vs_h;
+        } else {
+          dst = wave == 0 ? (T*)a.k + pos * a.ks_pos + (int64_t)b * a.ks_b + (int64_t)kvh * a.ks_h
+                          : (T*)a.v + pos * a.vs_pos + (int64_t)b * a.vs_b + (int64_t)kvh * a.vs_h;
+        }
+        if (dst != nullptr) {
 #pragma unroll
-        for (int e = 0; e < kPer; ++e) dst[lane + 64 * e] = nkv[wave * D + lane + 64 * e];
+          for (int e = 0; e < kPer; ++e) dst[lane + 64 * e] = nkv[wave * D + lane + 64 * e];
+        }
       }
     }
     // query heads hc * 16 + j of this kv group, one wave per head
@@ -518,10 +531,10 @@ decode_split_mfma(DecodeArgs a) {
   split_body<T, D, PAGED, false>(a, nullptr);
 }
 
-template <typename T, int D>
+template <typename T, int D, bool PAGED>
 __global__ void __launch_bounds__(256)
 decode_split_mfma_pro(DecodeArgs a, SplitPrologue pp) {
-  split_body<T, D, false, true>(a, &pp);
+  split_body<T, D, PAGED, true>(a, &pp);
 }
 
 // fp32 caches: the same split structure on v_mfma_f32_16x16x4_f32 (fp32
@@ -951,12 +964,15 @@ int balanced_slots(int length, int unit, int items_target) {
 }
 
 template <typename T>
-const void* split_kernel_pro(int D) {
+const void* split_kernel_pro(int D, bool paged) {
   if constexpr (sizeof(T) == 2) {
     switch (D) {
-      case 64: return (const void*)decode_split_mfma_pro<T, 64>;
-      case 128: return (const void*)decode_split_mfma_pro<T, 128>;
-      case 256: return (const void*)decode_split_mfma_pro<T, 256>;
+      case 64: return paged ? (const void*)decode_split_mfma_pro<T, 64, true>
+                            : (const void*)decode_split_mfma_pro<T, 64, false>;
+      case 128: return paged ? (const void*)decode_split_mfma_pro<T, 128, true>
+                             : (const void*)decode_split_mfma_pro<T, 128, false>;
+      case 256: return paged ? (const void*)decode_split_mfma_pro<T, 256, true>
+                             : (const void*)decode_split_mfma_pro<T, 256, false>;
     }
   }
   return nullptr;
@@ -1068,10 +1084,10 @@ int run_decode(DecodeArgs a, int dtype, int out_dtype, void* workspace, size_t w
   const void* kernel = nullptr;
   const bool paged = a.pages != nullptr;
   if (pro != nullptr) {
-    // fused prologue: 16-bit MFMA split over a contiguous cache only
-    if (mfma && !paged && a.causal_pos0 < 0) {
-      if (dtype == ALPX_F16) kernel = split_kernel_pro<f16_t>(D);
-      if (dtype == ALPX_BF16) kernel = split_kernel_pro<bf16_t>(D);
+    // fused prologue: 16-bit MFMA split over a contiguous or paged cache
+    if (mfma && a.causal_pos0 < 0) {
+      if (dtype == ALPX_F16) kernel = split_kernel_pro<f16_t>(D, paged);
+      if (dtype == ALPX_BF16) kernel = split_kernel_pro<bf16_t>(D, paged);
     }
     if (kernel == nullptr)
       return fail(ALPX_EUNSUPPORTED,

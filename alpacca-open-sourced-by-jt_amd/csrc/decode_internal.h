@@ -8,6 +8,11 @@
 
 namespace alpx {
 
+// Rows of one wavefront step of the 16-bit MFMA split kernel: a paged cache
+// needs pages of a power-of-two size of at least this many rows, so a wave
+// tile never crosses a page.
+constexpr int kDecodeWaveRows = 32;
+
 struct DecodeArgs {
   const void* q;
   const void* k;

@@ -1075,30 +1075,41 @@ extern "C" int alpx_attention_prologue_chunk(const void* query_gate, const void*
                                    frequency_base, eps, stream);
 }
 
-extern "C" int alpx_attention_layer_step(const void* query_gate, const void* key,
-                                         const void* value, const float* q_norm,
-                                         const float* k_norm, void* key_cache, void* value_cache,
-                                         void* out, void* workspace, size_t workspace_bytes,
-                                         int dtype, int out_dtype, int64_t capacity, int batch,
-                                         int q_heads, int kv_heads, int head_dim,
-                                         int64_t position, const int32_t* positions,
-                                         const int* sections,
-                                         double frequency_base, float eps, float scale,
-                                         void* stream) {
+namespace {
+
+// Paged K/V pool of the layer step: pages [num_pages, page_size, Hkv, D],
+// block_table [batch, max_pages].
+struct LayerPages {
+  const int32_t* table;
+  int max_pages, page_size, num_pages;
+};
+
+// alpx_attention_layer_step over a contiguous cache (pages null) or a paged
+// pool: same validation, prologue and split plan.
+int layer_step_impl(const char* name, const void* query_gate, const void* key, const void* value,
+                    const float* q_norm, const float* k_norm, void* key_cache, void* value_cache,
+                    void* out, void* workspace, size_t workspace_bytes, int dtype, int out_dtype,
+                    int64_t capacity, int batch, int q_heads, int kv_heads, int head_dim,
+                    int64_t position, const int32_t* positions, const int* sections,
+                    double frequency_base, float eps, float scale, void* stream,
+                    const LayerPages* pages) {
   using namespace alpx;
   if (!query_gate || !key || !value || !q_norm || !k_norm || !key_cache || !value_cache ||
-      !out || !workspace)
-    return fail(ALPX_EINVAL, "alpx_attention_layer_step: null buffer");
-  if (!dtype_ok(dtype) || !dtype_ok(out_dtype))
-    return fail(ALPX_EINVAL, "alpx_attention_layer_step: unknown dtype");
+      !out || !workspace || (pages != nullptr && pages->table == nullptr))
+    return fail(ALPX_EINVAL, "%s: null buffer", name);
+  if (!dtype_ok(dtype) || !dtype_ok(out_dtype)) return fail(ALPX_EINVAL, "%s: unknown dtype", name);
   if (batch <= 0 || q_heads <= 0 || kv_heads <= 0 || head_dim <= 0 || capacity <= 0)
-    return fail(ALPX_EINVAL, "alpx_attention_layer_step: sizes must be positive");
+    return fail(ALPX_EINVAL, "%s: sizes must be positive", name);
+  if (pages != nullptr && (pages->page_size < kDecodeWaveRows ||
+                           (pages->page_size & (pages->page_size - 1)) != 0))
+    return fail(ALPX_EINVAL, "page size must be a power of two of at least %d rows",
+                kDecodeWaveRows);
   if (q_heads % kv_heads != 0)
     return fail(ALPX_EINVAL, "attention query heads must be a multiple of KV heads");
   if (position < 0 || position >= capacity)
     return fail(ALPX_ERANGE, "attention cache position exceeds capacity");
   if (position + 1 > INT32_MAX)
-    return fail(ALPX_EUNSUPPORTED, "alpx_attention_layer_step: cache length above 2^31 - 1");
+    return fail(ALPX_EUNSUPPORTED, "%s: cache length above 2^31 - 1", name);
   if (!(scale > 0.0f) || !isfinite(scale))
     return fail(ALPX_EINVAL, "attention scale must be positive and finite");
   int R = 0;
@@ -1127,9 +1138,19 @@ extern "C" int alpx_attention_layer_step(const void* query_gate, const void* key
   a.gate = (const char*)query_gate + D * dtype_size(dtype);
   a.gate_stride = 2 * D;
   a.out = out;
-  a.ks_pos = a.vs_pos = (int64_t)batch * kv_heads * D;
-  a.ks_b = a.vs_b = (int64_t)kv_heads * D;
-  a.ks_h = a.vs_h = D;
+  if (pages != nullptr) {  // rows of a page are [Hkv, D]
+    a.ks_pos = a.vs_pos = (int64_t)kv_heads * D;
+    a.ks_h = a.vs_h = D;
+    a.ks_page = a.vs_page = (int64_t)pages->page_size * a.ks_pos;
+    a.pages = pages->table;
+    a.page_shift = __builtin_ctz((unsigned)pages->page_size);
+    a.max_pages = pages->max_pages;
+    a.num_pages = pages->num_pages;
+  } else {
+    a.ks_pos = a.vs_pos = (int64_t)batch * kv_heads * D;
+    a.ks_b = a.vs_b = (int64_t)kv_heads * D;
+    a.ks_h = a.vs_h = D;
+  }
   a.causal_pos0 = -1;
   a.length = (int)(position + 1);
   if (positions != nullptr) {  // sequence b attends rows 0 .. positions[b]
@@ -1145,6 +1166,42 @@ extern "C" int alpx_attention_layer_step(const void* query_gate, const void* key
   a.scale_log2 = scale * kLog2e;
   return run_decode(a, dtype, out_dtype, workspace, workspace_bytes, (hipStream_t)stream,
                     ALPX_T_DECODE, ALPX_T_DECODE_COMBINE, &pp);
+}
+
+}  // namespace
+
+extern "C" int alpx_attention_layer_step(const void* query_gate, const void* key,
+                                         const void* value, const float* q_norm,
+                                         const float* k_norm, void* key_cache, void* value_cache,
+                                         void* out, void* workspace, size_t workspace_bytes,
+                                         int dtype, int out_dtype, int64_t capacity, int batch,
+                                         int q_heads, int kv_heads, int head_dim,
+                                         int64_t position, const int32_t* positions,
+                                         const int* sections,
+                                         double frequency_base, float eps, float scale,
+                                         void* stream) {
+  return layer_step_impl("alpx_attention_layer_step", query_gate, key, value, q_norm, k_norm,
+                         key_cache, value_cache, out, workspace, workspace_bytes, dtype,
+                         out_dtype, capacity, batch, q_heads, kv_heads, head_dim, position,
+                         positions, sections, frequency_base, eps, scale, stream, nullptr);
+}
+
+extern "C" int alpx_attention_layer_step_paged(
+    const void* query_gate, const void* key, const void* value, const float* q_norm,
+    const float* k_norm, void* key_pages, void* value_pages, const int32_t* block_table,
+    int max_pages, int page_size, int num_pages, void* out, void* workspace,
+    size_t workspace_bytes, int dtype, int out_dtype, int batch, int q_heads, int kv_heads,
+    int head_dim, int64_t position, const int32_t* positions, const int* sections,
+    double frequency_base, float eps, float scale, void* stream) {
+  using namespace alpx;
+  if (max_pages <= 0 || num_pages <= 0 || page_size <= 0)
+    return fail(ALPX_EINVAL, "alpx_attention_layer_step_paged: sizes must be positive");
+  const LayerPages pages = {block_table, max_pages, page_size, num_pages};
+  return layer_step_impl("alpx_attention_layer_step_paged", query_gate, key, value, q_norm,
+                         k_norm, key_pages, value_pages, out, workspace, workspace_bytes, dtype,
+                         out_dtype, (int64_t)max_pages * page_size, batch, q_heads, kv_heads,
+                         head_dim, position, positions, sections, frequency_base, eps, scale,
+                         stream, &pages);
 }
 
 extern "C" size_t alpx_recurrent_step_workspace_bytes(int batch, int key_heads, int value_heads,

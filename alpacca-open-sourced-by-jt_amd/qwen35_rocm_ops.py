@@ -917,6 +917,69 @@ class Qwen35RocmOps:
                                  seq_lens=seq_lens, gate=gate, scale=scale_value,
                                  out_dtype=out_dtype)
 
+    def paged_attention_layer_step_(self, query_gate: Any, key: Any, value: Any,
+                                    query_norm: Any, key_norm: Any, key_pages: Any,
+                                    value_pages: Any, block_table: Any, *, position: int,
+                                    sections: Sequence[int], frequency_base: float,
+                                    epsilon: float, positions: Any = None,
+                                    scale: float | None = None,
+                                    out_dtype: Any = None) -> tuple[Any, int]:
+        """``attention_layer_step_`` over a paged pool (extension): the same
+        prologue, two launches and arithmetic, with sequence b's rotated key
+        and value written to its logical row ``position`` (or
+        ``positions[b]``) through ``block_table`` and attention over its
+        rows ``0 .. position``; the same rows give the contiguous step's
+        bits.  A table entry outside the pool writes no row.  fp16 / bf16
+        pages with equal key and value widths of 64, 128 or 256.  Returns
+        ``(gated output [B, Hq, D], position + 1)``."""
+        key_pages, value_pages = self._paged(key_pages, value_pages, block_table)
+        num_pages, size, kv_heads, width = _shape(key_pages)
+        batch, max_pages = (int(x) for x in block_table.shape)
+        if (key_pages.dtype not in (self.torch.float16, self.torch.bfloat16)
+                or int(value_pages.shape[3]) != width or width not in (64, 128, 256)):
+            raise ValueError("paged attention layer step needs fp16/bf16 pages with equal key "
+                             "and value widths of 64, 128 or 256")
+        query_gate = self._tensor(query_gate, "joint Q/gate projection", dimensions=2)
+        key = self._tensor(key, "attention key", dimensions=2)
+        value = self._tensor(value, "attention value", dimensions=2)
+        query_norm = self._fp32(query_norm, "query RMSNorm weight", dimensions=1)
+        key_norm = self._fp32(key_norm, "key RMSNorm weight", dimensions=1)
+        position = _nonnegative_integer("attention cache position", position)
+        if position >= max_pages * size:
+            raise ValueError("attention cache position exceeds capacity")
+        if int(query_gate.shape[0]) != batch or int(query_gate.shape[1]) % (2 * width):
+            raise ValueError("joint Q/gate projection does not match the page head width")
+        query_heads = int(query_gate.shape[1]) // (2 * width)
+        if query_heads % kv_heads:
+            raise ValueError("attention query heads must be a multiple of KV heads")
+        if _shape(key) != (batch, kv_heads * width) or _shape(value) != (batch, kv_heads * width):
+            raise ValueError("attention key/value do not match the page token shape")
+        if _shape(query_norm) != (width,) or _shape(key_norm) != (width,):
+            raise ValueError("RMSNorm weight must match the head dimension")
+        self._same_dtype("paged attention step", query_gate, key, value, key_pages)
+        if len(sections) != 4:
+            raise ValueError("IMRoPE requires four sections")
+        section = tuple(_nonnegative_integer("IMRoPE section", item) for item in sections)
+        base = _positive_finite("frequency_base", frequency_base)
+        eps = _positive_finite("epsilon", epsilon)
+        if positions is not None:
+            if not self.torch.is_tensor(positions) or positions.device.type != "cuda":
+                host = [int(p) for p in positions]
+                if len(host) != batch or any(p < 0 or p > position for p in host):
+                    raise ValueError("positions must hold one row in [0, position] per sequence")
+                positions = self.torch.tensor(host, dtype=self.torch.int32, device=self.device)
+            elif _shape(positions) != (batch,):
+                raise ValueError("positions must hold one row per sequence")
+            positions = positions.to(self.torch.int32).contiguous()
+        scale_value = (1.0 / math.sqrt(width) if scale is None
+                       else _positive_finite("attention scale", scale))
+        out = _ops.attention_layer_step_paged(
+            query_gate.reshape(batch, query_heads, 2 * width), key, value, query_norm, key_norm,
+            key_pages, value_pages, block_table, position=position, sections=section,
+            frequency_base=base, eps=eps, positions=positions, scale=scale_value,
+            out_dtype=out_dtype)
+        return out, position + 1
+
     def paged_attention_prefill(self, query: Any, key_pages: Any, value_pages: Any,
                                 block_table: Any, *, position: int, batch_index: int = 0,
                                 scale: float | None = None, gate: Any = None) -> Any:

@@ -442,6 +442,27 @@ int alpx_attention_layer_step(const void* query_gate, const void* key, const voi
                               int64_t position, const int32_t* positions, const int* sections,
                               double frequency_base, float eps, float scale, void* stream);
 
+/* alpx_attention_layer_step over a paged K/V pool (an extension, as
+ * alpx_decode_gqa_paged): pages [num_pages, page_size, Hkv, D],
+ * block_table [batch, max_pages] (device int32), page_size a power of two
+ * of at least 32.  Sequence b's rotated key and value land at logical row
+ * pos_b (row pos_b % page_size of page block_table[b][pos_b / page_size]);
+ * a table entry outside [0, num_pages) writes no row (reads clamp such an
+ * entry into the pool, as alpx_decode_gqa_paged does).  `position` must be
+ * below max_pages * page_size.  Same launches, split plan and arithmetic as
+ * alpx_attention_layer_step, so the same rows give the same output bits.
+ * fp16 / bf16 pages, head_dim in {64, 128, 256} (others:
+ * ALPX_EUNSUPPORTED).  workspace: alpx_decode_workspace_bytes(batch,
+ * q_heads, kv_heads, head_dim, position + 1) bytes. */
+int alpx_attention_layer_step_paged(const void* query_gate, const void* key, const void* value,
+                                    const float* q_norm, const float* k_norm, void* key_pages,
+                                    void* value_pages, const int32_t* block_table, int max_pages,
+                                    int page_size, int num_pages, void* out, void* workspace,
+                                    size_t workspace_bytes, int dtype, int out_dtype, int batch,
+                                    int q_heads, int kv_heads, int head_dim, int64_t position,
+                                    const int32_t* positions, const int* sections,
+                                    double frequency_base, float eps, float scale, void* stream);
+
 /* Workspace bytes for alpx_recurrent_step. */
 size_t alpx_recurrent_step_workspace_bytes(int batch, int key_heads, int value_heads, int key_dim,
                                            int value_dim);

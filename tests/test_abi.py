@@ -167,6 +167,23 @@ def test_layer_entry_points_validate_without_gpu(pkg):
     rc = lib.alpx_attention_layer_step(*f9, 1 << 20, 2, 2, 64, 1, 16, 2, 96, 10, None, sec, 1e7,
                                        1e-6, 0.0625, None)
     assert rc == L.EUNSUPPORTED and "fused attention step" in L.last_error()
+    # paged layer step: pool geometry, capacity, table and fused-shape checks
+    f7 = (fake,) * 7
+    rc = lib.alpx_attention_layer_step_paged(*f7, fake, 4, 16, 8, fake, fake, 1 << 20, 2, 2, 1, 16,
+                                             2, 256, 10, None, sec, 1e7, 1e-6, 0.0625, None)
+    assert rc == L.EINVAL and "power of two" in L.last_error()
+    rc = lib.alpx_attention_layer_step_paged(*f7, fake, 4, 64, 8, fake, fake, 1 << 20, 2, 2, 1, 16,
+                                             2, 256, 256, None, sec, 1e7, 1e-6, 0.0625, None)
+    assert rc == L.ERANGE and "exceeds capacity" in L.last_error()
+    rc = lib.alpx_attention_layer_step_paged(*f7, None, 4, 64, 8, fake, fake, 1 << 20, 2, 2, 1, 16,
+                                             2, 256, 10, None, sec, 1e7, 1e-6, 0.0625, None)
+    assert rc == L.EINVAL and "null" in L.last_error()
+    rc = lib.alpx_attention_layer_step_paged(*f7, fake, 0, 64, 8, fake, fake, 1 << 20, 2, 2, 1, 16,
+                                             2, 256, 10, None, sec, 1e7, 1e-6, 0.0625, None)
+    assert rc == L.EINVAL and "sizes must be positive" in L.last_error()
+    rc = lib.alpx_attention_layer_step_paged(*f7, fake, 4, 64, 8, fake, fake, 1 << 20, 0, 0, 1, 16,
+                                             2, 256, 10, None, sec, 1e7, 1e-6, 0.0625, None)
+    assert rc == L.EUNSUPPORTED and "fused attention step" in L.last_error()
     assert lib.alpx_recurrent_step_workspace_bytes(1, 16, 32, 128, 128) > 0
     assert lib.alpx_recurrent_step_workspace_bytes(1, 0, 32, 128, 128) == 0
     rc = lib.alpx_recurrent_step(fake, fake, 4, 1, fake, 4, fake, fake, fake, fake, fake, fake,

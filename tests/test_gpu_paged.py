@@ -184,3 +184,109 @@ def test_paged_prefill_rejects_unsupported(gpu, ops):
         ops.paged_attention_prefill(q, pw.key_pages, pw.value_pages, table, position=8)
     with pytest.raises(ValueError):
         ops.paged_attention_prefill(q, pw.key_pages, pw.value_pages, table, position=125)
+
+
+def _step_inputs(torch, rng, gpu, dtype, b, hq, hkv, d):
+    qg = I.round_to(rng.standard_normal((b, hq * 2 * d)) * 3, dtype)
+    k = I.round_to(rng.standard_normal((b, hkv * d)) * 3, dtype)
+    v = I.round_to(rng.standard_normal((b, hkv * d)), dtype)
+    td = _td(torch, dtype)
+    qw = torch.from_numpy(rng.uniform(0.5, 1.5, d).astype(np.float32)).to(gpu)
+    kw = torch.from_numpy(rng.uniform(0.5, 1.5, d).astype(np.float32)).to(gpu)
+    dev = [torch.from_numpy(x.astype(np.float32)).to(gpu).to(td) for x in (qg, k, v)]
+    return (*dev, qw, kw)
+
+
+def _pool_rows(torch, pages, perm, bb, length):
+    return A.paged_rows(pages.view(torch.int16).cpu().numpy(), perm, bb, length)
+
+
+@pytest.mark.parametrize("dtype,d,page,hq,hkv,b,cap,pos", [
+    ("bf16", 128, 64, 32, 8, 3, 512, 300), ("f16", 256, 32, 16, 2, 2, 256, 255),
+    ("bf16", 64, 128, 8, 2, 4, 512, 0), ("f16", 128, 32, 12, 4, 1, 96, 64)])
+def test_paged_layer_step_equals_contiguous_bit_for_bit(gpu, ops, dtype, d, page, hq, hkv, b,
+                                                        cap, pos):
+    """paged_attention_layer_step_ (alpx_attention_layer_step_paged: the
+    prologue inside the paged split-K launch) against the contiguous step on
+    the same rows in a shuffled page pool: the same output bits and the same
+    rows written (gathered through the table), for one position shared by
+    the batch and then for per-sequence device positions (a ragged batch,
+    each at most the bound)."""
+    import torch
+    rng = np.random.default_rng(d + page + pos)
+    sections, base, eps = (11, 11, 10, 0), 10000000.0, 1e-6
+    if 2 * sum(sections) > d:
+        sections = (4, 4, 2, 0)
+    ws, pw, table, perm = _fill(torch, ops, gpu, rng, dtype, b, cap, hkv, d, page, None)
+    kw_args = dict(sections=sections, frequency_base=base, epsilon=eps)
+    ragged = torch.tensor([(pos * (i + 1)) // b for i in range(b)], dtype=torch.int32,
+                          device=gpu)
+    for positions in (None, ragged):
+        args = _step_inputs(torch, rng, gpu, dtype, b, hq, hkv, d)
+        out_c, n_c = ops.attention_layer_step_(*args, ws.key_cache, ws.value_cache, position=pos,
+                                               positions=positions, **kw_args)
+        out_p, n_p = ops.paged_attention_layer_step_(*args, pw.key_pages, pw.value_pages, table,
+                                                     position=pos, positions=positions,
+                                                     **kw_args)
+        out_c32, _ = ops.attention_layer_step_(*args, ws.key_cache, ws.value_cache, position=pos,
+                                               positions=positions, out_dtype=torch.float32,
+                                               **kw_args)
+        out_p32, _ = ops.paged_attention_layer_step_(*args, pw.key_pages, pw.value_pages, table,
+                                                     position=pos, positions=positions,
+                                                     out_dtype=torch.float32, **kw_args)
+        torch.cuda.synchronize()
+        assert n_c == n_p == pos + 1
+        assert torch.equal(out_p.view(torch.int16), out_c.view(torch.int16))
+        assert torch.equal(out_p32, out_c32)
+        kc = ws.key_cache.view(torch.int16).cpu().numpy()
+        vc = ws.value_cache.view(torch.int16).cpu().numpy()
+        for bb in range(b):
+            assert np.array_equal(_pool_rows(torch, pw.key_pages, perm, bb, cap), kc[:, bb])
+            assert np.array_equal(_pool_rows(torch, pw.value_pages, perm, bb, cap), vc[:, bb])
+
+
+def test_paged_layer_step_skips_rows_outside_the_pool(gpu, ops):
+    """A block-table entry outside [0, num_pages) for the page of the new
+    row writes nothing (the pool keeps its bits); the other sequences'
+    rows land as in the contiguous step."""
+    import torch
+    rng = np.random.default_rng(9)
+    dtype, d, page, hq, hkv, b, cap, pos = "bf16", 128, 64, 16, 4, 3, 256, 130
+    ws, pw, table, perm = _fill(torch, ops, gpu, rng, dtype, b, cap, hkv, d, page, None)
+    bad = table.clone()
+    bad[1, pos // page] = -1
+    bad[2, pos // page] = pw.key_pages.shape[0] + 5
+    before_k = pw.key_pages.view(torch.int16).clone()
+    before_v = pw.value_pages.view(torch.int16).clone()
+    args = _step_inputs(torch, rng, gpu, dtype, b, hq, hkv, d)
+    kw_args = dict(position=pos, sections=(11, 11, 10, 0), frequency_base=1e7, epsilon=1e-6)
+    ops.paged_attention_layer_step_(*args, pw.key_pages, pw.value_pages, bad, **kw_args)
+    ops.attention_layer_step_(*args, ws.key_cache, ws.value_cache, **kw_args)
+    torch.cuda.synchronize()
+    changed = (pw.key_pages.view(torch.int16) != before_k).any(dim=(2, 3)).nonzero().tolist()
+    row0 = [int(perm[0, pos // page]), pos % page]
+    assert changed == [row0]  # only sequence 0's new key row
+    assert torch.equal(pw.key_pages.view(torch.int16)[row0[0], row0[1]],
+                       ws.key_cache.view(torch.int16)[pos, 0])
+    vchanged = (pw.value_pages.view(torch.int16) != before_v).any(dim=(2, 3)).nonzero().tolist()
+    assert vchanged in ([row0], [])  # a value row equal to the old one would not show
+
+
+def test_paged_layer_step_rejects_unsupported(gpu, ops):
+    import torch
+    pw = ops.initialize_paged_attention_workspace(num_pages=4, page_size=64, kv_heads=2,
+                                                  key_dimension=96, value_dimension=96,
+                                                  dtype=torch.bfloat16)
+    table = torch.zeros((1, 4), dtype=torch.int32, device=gpu)
+    args = _step_inputs(torch, np.random.default_rng(1), gpu, "bf16", 1, 4, 2, 96)
+    with pytest.raises(ValueError, match="widths of 64, 128 or 256"):
+        ops.paged_attention_layer_step_(*args, pw.key_pages, pw.value_pages, table, position=3,
+                                        sections=(4, 4, 2, 0), frequency_base=1e7, epsilon=1e-6)
+    pw2 = ops.initialize_paged_attention_workspace(num_pages=4, page_size=64, kv_heads=2,
+                                                   key_dimension=64, value_dimension=64,
+                                                   dtype=torch.bfloat16)
+    args2 = _step_inputs(torch, np.random.default_rng(2), gpu, "bf16", 1, 4, 2, 64)
+    with pytest.raises(ValueError, match="exceeds capacity"):
+        ops.paged_attention_layer_step_(*args2, pw2.key_pages, pw2.value_pages, table,
+                                        position=256, sections=(4, 4, 2, 0),
+                                        frequency_base=1e7, epsilon=1e-6)
