@@ -39,6 +39,16 @@ SIGNATURES = {
                                 _c_int, _c_int, _c_int, _c_i64, _c_i64, _c_ptr]),
     "alpx_kv_import": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_int, _c_int,
                                 _c_int, _c_int, _c_int, _c_i64, _c_i64, _c_ptr]),
+    # pages, pages, block_table, batch, max_pages, page_size, num_pages, rows, rows, dtype,
+    # kv_heads, key_dim, value_dim, batch_index, row0, rows, stream
+    "alpx_kv_export_paged": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_int, _c_int, _c_int, _c_int,
+                                      _c_ptr, _c_ptr, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                      _c_i64, _c_i64, _c_ptr]),
+    # rows, rows, pages, pages, block_table, batch, max_pages, page_size, num_pages, dtype,
+    # kv_heads, key_dim, value_dim, batch_index, row0, rows, stream
+    "alpx_kv_import_paged": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_int,
+                                      _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                      _c_i64, _c_i64, _c_ptr]),
     "alpx_decode_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int]),
     "alpx_decode_gqa": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_ptr, _c_ptr,
                                  _c_ptr, _c_size, _c_int, _c_int, _c_int, _c_int, _c_int,

@@ -174,6 +174,44 @@ def kv_import(key_rows, value_rows, key_cache, value_cache, *, batch_index, row0
     _lib.check(rc)
 
 
+def kv_export_paged(key_pages, value_pages, block_table, *, batch_index, row0, rows):
+    """Logical rows ``[row0, row0 + rows)`` of sequence ``batch_index`` of a
+    paged pool (``block_table [B, max_pages]`` int32) as contiguous fp32
+    ``(key [rows, Hkv, D], value [rows, Hkv, Dv])``; rows whose table entry
+    lies outside the pool read as zero."""
+    torch = _torch()
+    num_pages, page_size, kv_heads, dim = (int(x) for x in key_pages.shape)
+    value_dim = int(value_pages.shape[3])
+    batch, max_pages = (int(x) for x in block_table.shape)
+    dev = key_pages.device
+    k = torch.empty((rows, kv_heads, dim), dtype=torch.float32, device=dev)
+    v = torch.empty((rows, kv_heads, value_dim), dtype=torch.float32, device=dev)
+    rc = _lib.lib().alpx_kv_export_paged(
+        key_pages.data_ptr(), value_pages.data_ptr(), block_table.data_ptr(), batch, max_pages,
+        page_size, num_pages, k.data_ptr(), v.data_ptr(), _lib.dtype_code(torch, key_pages.dtype),
+        kv_heads, dim, value_dim, int(batch_index), int(row0), int(rows),
+        _lib.stream_handle(torch, dev))
+    _lib.check(rc)
+    return k, v
+
+
+def kv_import_paged(key_rows, value_rows, key_pages, value_pages, block_table, *, batch_index,
+                    row0):
+    """Writes fp32 rows ``[rows, Hkv, D|Dv]`` into sequence ``batch_index`` of a
+    paged pool from logical row ``row0`` (rounded to the page dtype; rows
+    whose table entry lies outside the pool are skipped)."""
+    torch = _torch()
+    num_pages, page_size, kv_heads, dim = (int(x) for x in key_pages.shape)
+    value_dim = int(value_pages.shape[3])
+    batch, max_pages = (int(x) for x in block_table.shape)
+    rc = _lib.lib().alpx_kv_import_paged(
+        key_rows.data_ptr(), value_rows.data_ptr(), key_pages.data_ptr(), value_pages.data_ptr(),
+        block_table.data_ptr(), batch, max_pages, page_size, num_pages,
+        _lib.dtype_code(torch, key_pages.dtype), kv_heads, dim, value_dim, int(batch_index),
+        int(row0), int(key_rows.shape[0]), _lib.stream_handle(torch, key_pages.device))
+    _lib.check(rc)
+
+
 def decode(q, key_cache, value_cache, *, length, k_strides, v_strides, batch, kv_heads,
            seq_lens=None, gate=None, scale=None, out_dtype=None, out=None):
     """Split-K GQA decode.  ``q [B, Hq, D]`` contiguous; K/V addressed by

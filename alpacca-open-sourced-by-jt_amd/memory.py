@@ -8,6 +8,8 @@ that lives in device buffers:
   bf16 as the reference's half-precision device mirror, cuda.py:1729-1738)
   for one sequence, with the logical length on the host, as
   ``FullAttentionState`` keeps them in host arrays.
+* ``DevicePagedAttentionState`` is the same for one sequence of a paged
+  pool (pages + block table; an extension), with the same records.
 * ``DeviceRecurrentState`` views one sequence of a ``RocmRecurrentWorkspace``
   (convolution history and delta matrix, fp32) as ``RecurrentState``.
 
@@ -213,28 +215,9 @@ class DeviceFullAttentionState:
         """Validate a record as _validate_layer_snapshot does
         (memory.py:640-690) and write its rows into the cache (rounded to
         the cache dtype)."""
-        import torch
-        if getattr(snapshot, "kind", None) != "attention":
-            raise SnapshotMismatchError("snapshot record is not an attention record")
-        if getattr(snapshot, "layer_index", None) != self.layer_index:
-            raise SnapshotMismatchError(f"snapshot layer index mismatch at layer {self.layer_index}")
-        if snapshot.dtype != "f32-le":
-            raise SnapshotMismatchError(f"snapshot has unsupported dtype {snapshot.dtype!r}")
-        length = snapshot.logical_length
-        _strict_nonnegative("logical_length", length)
-        if (snapshot.kv_heads, snapshot.key_dim, snapshot.value_dim) != (
-                self.kv_heads, self.key_dim, self.value_dim):
-            raise SnapshotMismatchError("snapshot attention shape differs")
-        if length > self.capacity:
-            raise SnapshotMismatchError("snapshot length exceeds the cache capacity")
-        dev = self.key_cache.device
-        k = _from_le_bytes(torch, snapshot.key, length * self.kv_heads * self.key_dim,
-                           "snapshot key", dev)
-        v = _from_le_bytes(torch, snapshot.value, length * self.kv_heads * self.value_dim,
-                           "snapshot value", dev)
-        _ops.kv_import(k.reshape(length, self.kv_heads, self.key_dim),
-                       v.reshape(length, self.kv_heads, self.value_dim), self.key_cache,
-                       self.value_cache, batch_index=self.batch_index, row0=0)
+        length, k, v = _attention_record_rows(self, snapshot)
+        _ops.kv_import(k, v, self.key_cache, self.value_cache, batch_index=self.batch_index,
+                       row0=0)
         self.logical_length = length
 
     def memory_bytes(self) -> int:
@@ -250,6 +233,122 @@ class DeviceFullAttentionState:
             "value_shape": [self.logical_length, self.kv_heads, self.value_dim],
             "memory_bytes": self.memory_bytes(),
         }
+
+
+def _attention_record_rows(state, snapshot):
+    """Checks of an attention record against ``state`` (kind, layer, dtype,
+    shape, capacity; _validate_layer_snapshot, memory.py:640-690) and its
+    rows as fp32 device tensors ``(length, key [L, Hkv, D], value [L, Hkv, Dv])``."""
+    import torch
+    if getattr(snapshot, "kind", None) != "attention":
+        raise SnapshotMismatchError("snapshot record is not an attention record")
+    if getattr(snapshot, "layer_index", None) != state.layer_index:
+        raise SnapshotMismatchError(f"snapshot layer index mismatch at layer {state.layer_index}")
+    if snapshot.dtype != "f32-le":
+        raise SnapshotMismatchError(f"snapshot has unsupported dtype {snapshot.dtype!r}")
+    length = snapshot.logical_length
+    _strict_nonnegative("logical_length", length)
+    if (snapshot.kv_heads, snapshot.key_dim, snapshot.value_dim) != (
+            state.kv_heads, state.key_dim, state.value_dim):
+        raise SnapshotMismatchError("snapshot attention shape differs")
+    if length > state.capacity:
+        raise SnapshotMismatchError("snapshot length exceeds the cache capacity")
+    dev = state.key_cache.device
+    k = _from_le_bytes(torch, snapshot.key, length * state.kv_heads * state.key_dim,
+                       "snapshot key", dev)
+    v = _from_le_bytes(torch, snapshot.value, length * state.kv_heads * state.value_dim,
+                       "snapshot value", dev)
+    return (length, k.reshape(length, state.kv_heads, state.key_dim),
+            v.reshape(length, state.kv_heads, state.value_dim))
+
+
+class DevicePagedAttentionState(DeviceFullAttentionState):
+    """``DeviceFullAttentionState`` for sequence ``batch_index`` of a paged
+    pool (extension): pages ``[num_pages, page_size, kv_heads, dim]`` held in
+    ``key_cache`` / ``value_cache`` and the pool's ``block_table [batch,
+    max_pages]`` (device int32); logical row j lives at row j % page_size of
+    page ``block_table[batch_index][j // page_size]``.  The capacity is
+    ``max_pages * page_size``.  Appends, snapshots and restores move rows
+    through the table (``alpx_kv_append_paged``, ``alpx_kv_export_paged`` /
+    ``alpx_kv_import_paged``), with the same record bytes as the contiguous
+    state."""
+
+    __slots__ = ("block_table",)
+
+    def __init__(self, key_pages: Any, value_pages: Any, block_table: Any, *,
+                 layer_index: int = 0, batch_index: int = 0, logical_length: int = 0) -> None:
+        import torch
+        _strict_nonnegative("logical_length", logical_length)
+        _strict_nonnegative("batch_index", batch_index)
+        if key_pages.dim() != 4 or value_pages.dim() != 4:
+            raise StateError("attention pages must be [num_pages, page_size, kv_heads, dim]")
+        if tuple(key_pages.shape[:3]) != tuple(value_pages.shape[:3]):
+            raise StateError("attention K/V pages differ in count, size or heads")
+        if key_pages.dtype != value_pages.dtype:
+            raise StateError("attention K/V pages must share a dtype")
+        if not (key_pages.is_contiguous() and value_pages.is_contiguous()):
+            raise StateError("attention pages must be contiguous")
+        if (block_table.dim() != 2 or block_table.dtype != torch.int32
+                or not block_table.is_contiguous() or block_table.device != key_pages.device):
+            raise StateError("block table must be a contiguous [batch, max_pages] int32 tensor "
+                             "on the pages' device")
+        size = int(key_pages.shape[1])
+        if size <= 0 or size & (size - 1):
+            raise StateError("page size must be a power of two")
+        if batch_index >= int(block_table.shape[0]):
+            raise StateError("batch_index exceeds the block table batch")
+        if logical_length > int(block_table.shape[1]) * size:
+            raise StateError("logical_length exceeds the cache capacity")
+        self.key_cache = key_pages
+        self.value_cache = value_pages
+        self.block_table = block_table
+        self.layer_index = layer_index
+        self.batch_index = batch_index
+        self.logical_length = logical_length
+
+    @property
+    def capacity(self) -> int:
+        return int(self.block_table.shape[1]) * int(self.key_cache.shape[1])
+
+    def append(self, key: Any, value: Any) -> None:
+        """Append one token's rows at the logical length through the block
+        table (bit-exact copy; FullAttentionState.append, memory.py:419-428)."""
+        import torch
+        if self.logical_length >= self.capacity:
+            raise StateError("attention cache capacity exhausted")
+        if key.numel() != self.kv_heads * self.key_dim or (
+                value.numel() != self.kv_heads * self.value_dim):
+            raise StateError("attention rows must hold kv_heads * dim values")
+        if key.dtype != self.key_cache.dtype or value.dtype != self.value_cache.dtype:
+            raise StateError("attention rows must use the cache dtype")
+        batch = int(self.block_table.shape[0])
+        pos = torch.full((batch,), -1, dtype=torch.int32, device=self.key_cache.device)
+        pos[self.batch_index] = self.logical_length
+        rows_k = self.key_cache.new_zeros((1, batch, self.kv_heads, self.key_dim))
+        rows_v = self.value_cache.new_zeros((1, batch, self.kv_heads, self.value_dim))
+        rows_k[0, self.batch_index] = key.reshape(self.kv_heads, self.key_dim)
+        rows_v[0, self.batch_index] = value.reshape(self.kv_heads, self.value_dim)
+        _ops.kv_append_paged(self.key_cache, self.value_cache, self.block_table, rows_k, rows_v,
+                             positions=pos)
+        self.logical_length += 1
+
+    def snapshot(self) -> FullAttentionSnapshot:
+        """The reference's record of this state (memory.py:451-460)."""
+        k, v = _ops.kv_export_paged(self.key_cache, self.value_cache, self.block_table,
+                                    batch_index=self.batch_index, row0=0,
+                                    rows=self.logical_length)
+        return FullAttentionSnapshot(
+            layer_index=self.layer_index, logical_length=self.logical_length,
+            kv_heads=self.kv_heads, key_dim=self.key_dim, value_dim=self.value_dim,
+            key=_le_bytes(k), value=_le_bytes(v))
+
+    def restore(self, snapshot: FullAttentionSnapshot) -> None:
+        """Validate a record (memory.py:640-690) and write its rows into the
+        sequence's pages (rounded to the page dtype)."""
+        length, k, v = _attention_record_rows(self, snapshot)
+        _ops.kv_import_paged(k, v, self.key_cache, self.value_cache, self.block_table,
+                             batch_index=self.batch_index, row0=0)
+        self.logical_length = length
 
 
 class DeviceRecurrentState:
@@ -340,6 +439,7 @@ class DeviceRecurrentState:
 
 __all__ = [
     "DeviceFullAttentionState",
+    "DevicePagedAttentionState",
     "DeviceRecurrentState",
     "FullAttentionSnapshot",
     "RecurrentSnapshot",

@@ -135,6 +135,24 @@ int alpx_kv_import(const float* key_rows, const float* value_rows, void* key_cac
                    void* value_cache, int dtype, int64_t capacity, int batch, int kv_heads,
                    int key_dim, int value_dim, int batch_index, int64_t row0, int64_t rows,
                    void* stream);
+/* The same transfers for one sequence of a paged pool (an extension):
+ * pages [num_pages, page_size, kv_heads, key_dim|value_dim], block_table
+ * [batch, max_pages] (device int32, page_size a power of two); logical row
+ * j of sequence batch_index is row j % page_size of page
+ * block_table[batch_index][j / page_size].  A table entry outside
+ * [0, num_pages) exports zeros and imports nothing.  Rows outside
+ * [0, max_pages * page_size) fail with ALPX_ERANGE.  Same values as the
+ * contiguous calls on the same rows. */
+int alpx_kv_export_paged(const void* key_pages, const void* value_pages,
+                         const int32_t* block_table, int batch, int max_pages, int page_size,
+                         int num_pages, float* key_rows, float* value_rows, int dtype,
+                         int kv_heads, int key_dim, int value_dim, int batch_index, int64_t row0,
+                         int64_t rows, void* stream);
+int alpx_kv_import_paged(const float* key_rows, const float* value_rows, void* key_pages,
+                         void* value_pages, const int32_t* block_table, int batch, int max_pages,
+                         int page_size, int num_pages, int dtype, int kv_heads, int key_dim,
+                         int value_dim, int batch_index, int64_t row0, int64_t rows,
+                         void* stream);
 
 /*
  * Workspace size in bytes needed by alpx_decode_gqa for these sizes

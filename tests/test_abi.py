@@ -167,6 +167,19 @@ def test_layer_entry_points_validate_without_gpu(pkg):
     rc = lib.alpx_attention_layer_step(*f9, 1 << 20, 2, 2, 64, 1, 16, 2, 96, 10, None, sec, 1e7,
                                        1e-6, 0.0625, None)
     assert rc == L.EUNSUPPORTED and "fused attention step" in L.last_error()
+    # paged state transfer: table, page size and range checks
+    rc = lib.alpx_kv_export_paged(fake, fake, None, 2, 4, 32, 8, fake, fake, 2, 2, 64, 64, 0, 0,
+                                  8, None)
+    assert rc == L.EINVAL and "null block table" in L.last_error()
+    rc = lib.alpx_kv_import_paged(fake, fake, fake, fake, fake, 2, 4, 48, 8, 2, 2, 64, 64, 0, 0,
+                                  8, None)
+    assert rc == L.EINVAL and "power of two" in L.last_error()
+    rc = lib.alpx_kv_export_paged(fake, fake, fake, 2, 4, 32, 8, fake, fake, 2, 2, 64, 64, 1, 100,
+                                  40, None)
+    assert rc == L.ERANGE and "exceed" in L.last_error()
+    rc = lib.alpx_kv_export_paged(fake, fake, fake, 2, 4, 32, 8, fake, fake, 2, 2, 64, 64, 2, 0,
+                                  8, None)
+    assert rc == L.EINVAL and "batch_index" in L.last_error()
     # paged layer step: pool geometry, capacity, table and fused-shape checks
     f7 = (fake,) * 7
     rc = lib.alpx_attention_layer_step_paged(*f7, fake, 4, 16, 8, fake, fake, 1 << 20, 2, 2, 1, 16,

@@ -173,3 +173,124 @@ def test_recurrent_snapshot_restore_round_trip(gpu):
     assert st0.logical_position == 12
     assert torch.equal(ws.convolution_history[0], ws.convolution_history[1])
     assert torch.equal(ws.delta_state[0], ws.delta_state[1])
+
+
+# --------------------------------------------------------- paged pools
+
+def _paged_pool(torch, device, td, rng, num_pages, page, hkv, d, dv, batch, max_pages):
+    """A shuffled, shared page pool (each sequence its own pages) and its
+    table; the pages hold random bits so untouched pages can be checked."""
+    perm = rng.permutation(num_pages)[:batch * max_pages].reshape(batch, max_pages)
+    table = torch.from_numpy(perm.astype(np.int32)).to(device)
+    kp = torch.from_numpy(rng.standard_normal((num_pages, page, hkv, d)).astype(np.float32))
+    vp = torch.from_numpy(rng.standard_normal((num_pages, page, hkv, dv)).astype(np.float32))
+    return kp.to(td).to(device), vp.to(td).to(device), table, perm
+
+
+def test_paged_state_validation_and_records_before_touching_the_device():
+    import torch
+    M = _mem()
+    rng = np.random.default_rng(2)
+    kp, vp, table, _ = _paged_pool(torch, "cpu", torch.float32, rng, 8, 4, 2, 4, 3, 2, 3)
+    st = M.DevicePagedAttentionState(kp, vp, table, layer_index=3, batch_index=1)
+    assert st.capacity == 12 and (st.kv_heads, st.key_dim, st.value_dim) == (2, 4, 3)
+    good = dict(layer_index=3, logical_length=2, kv_heads=2, key_dim=4, value_dim=3,
+                key=bytes(2 * 2 * 4 * 4), value=bytes(2 * 2 * 3 * 4))
+    for change, err in [({"layer_index": 2}, "layer index"), ({"value_dim": 4}, "shape"),
+                        ({"logical_length": 13}, "capacity"), ({"value": bytes(5)}, "bytes")]:
+        with pytest.raises(M.SnapshotMismatchError, match=err):
+            st.restore(M.FullAttentionSnapshot(**{**good, **change}))
+    assert st.logical_length == 0
+    with pytest.raises(M.StateError, match="batch_index"):
+        M.DevicePagedAttentionState(kp, vp, table, batch_index=2)
+    with pytest.raises(M.StateError, match="int32"):
+        M.DevicePagedAttentionState(kp, vp, table.to(torch.int64))
+    with pytest.raises(M.StateError, match="power of two"):
+        M.DevicePagedAttentionState(kp[:, :3].contiguous(), vp[:, :3].contiguous(), table)
+    with pytest.raises(M.StateError, match="capacity"):
+        M.DevicePagedAttentionState(kp, vp, table, logical_length=13)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", ["f32", "f16", "bf16"])
+def test_paged_snapshot_equals_contiguous_and_restores_across(gpu, dtype):
+    """Rows appended to a paged sequence give the reference's record bytes,
+    the same record as a contiguous state holding the same rows; a record
+    restores from either layout into the other with identical bits; pages
+    of other sequences keep their bits; truncate + append continues at the
+    new length."""
+    import torch
+    M = _mem()
+    rng = np.random.default_rng(3 + len(dtype))
+    td = _td(torch, dtype)
+    num_pages, page, hkv, d, dv, batch, max_pages, bi, n = 20, 8, 2, 32, 24, 3, 5, 1, 29
+    kp, vp, table, perm = _paged_pool(torch, gpu, td, rng, num_pages, page, hkv, d, dv, batch,
+                                      max_pages)
+    kp0, vp0 = kp.clone(), vp.clone()
+    kc = torch.zeros((page * max_pages, batch, hkv, d), dtype=td, device=gpu)
+    vc = torch.zeros((page * max_pages, batch, hkv, dv), dtype=td, device=gpu)
+    sp = M.DevicePagedAttentionState(kp, vp, table, layer_index=4, batch_index=bi)
+    sc = M.DeviceFullAttentionState(kc, vc, layer_index=4, batch_index=bi)
+    rows_k = I.round_to(rng.standard_normal((n, hkv * d)), dtype)
+    rows_v = I.round_to(rng.standard_normal((n, hkv * dv)), dtype)
+    for t in range(n):
+        k = torch.from_numpy(rows_k[t].astype(np.float32)).to(gpu).to(td)
+        v = torch.from_numpy(rows_v[t].astype(np.float32)).to(gpu).to(td)
+        sp.append(k, v)
+        sc.append(k, v)
+    snap = sp.snapshot()
+    assert snap.key == np.asarray(rows_k, dtype="<f4").tobytes()
+    assert snap.value == np.asarray(rows_v, dtype="<f4").tobytes()
+    csnap = sc.snapshot()
+    assert (snap.key, snap.value, snap.logical_length) == (csnap.key, csnap.value, n)
+    # only sequence bi's first ceil(n / page) pages changed
+    used = {int(perm[bi, j]) for j in range((n + page - 1) // page)}
+    for p in range(num_pages):
+        if p not in used:
+            assert torch.equal(_bits_t(kp[p]), _bits_t(kp0[p]))
+            assert torch.equal(_bits_t(vp[p]), _bits_t(vp0[p]))
+    # contiguous record -> paged sequence 0 of a fresh pool, paged -> contiguous
+    kp2, vp2, table2, perm2 = _paged_pool(torch, gpu, td, rng, num_pages, page, hkv, d, dv,
+                                          batch, max_pages)
+    M.DevicePagedAttentionState(kp2, vp2, table2, layer_index=4, batch_index=0).restore(csnap)
+    kc2, vc2 = torch.zeros_like(kc), torch.zeros_like(vc)
+    M.DeviceFullAttentionState(kc2, vc2, layer_index=4, batch_index=2).restore(snap)
+    for j in range(n):
+        pg, r = int(perm2[0, j // page]), j % page
+        assert torch.equal(_bits_t(kp2[pg, r]), _bits_t(kc[j, bi]))
+        assert torch.equal(_bits_t(vp2[pg, r]), _bits_t(vc[j, bi]))
+    assert torch.equal(_bits_t(kc2[:n, 2]), _bits_t(kc[:n, bi]))
+    # truncate drops rows; the next append lands at the new length
+    sp.truncate(9)
+    sp.append(torch.zeros(hkv * d, dtype=td, device=gpu), torch.ones(hkv * dv, dtype=td, device=gpu))
+    snap10 = sp.snapshot()
+    want_v = np.concatenate([rows_v[:9], np.ones((1, hkv * dv))]).astype("<f4").tobytes()
+    assert snap10.logical_length == 10 and snap10.value == want_v
+
+
+@pytest.mark.gpu
+def test_paged_transfer_rows_outside_the_pool(gpu):
+    """A table entry outside [0, num_pages) exports zeros and imports
+    nothing; rows past the table fail with a range error."""
+    import torch
+    O = importlib.import_module("alpacca-open-sourced-by-jt_amd._ops")
+    rng = np.random.default_rng(5)
+    kp, vp, table, perm = _paged_pool(torch, gpu, torch.bfloat16, rng, 6, 32, 2, 64, 64, 2, 3)
+    bad = table.clone()
+    bad[0, 1] = -3
+    bad[0, 2] = 6
+    k, v = O.kv_export_paged(kp, vp, bad, batch_index=0, row0=0, rows=96)
+    assert torch.equal(k[:32], kp[int(perm[0, 0])].float()) and not k[32:].any()
+    assert not v[32:].any()
+    before = kp.clone()
+    O.kv_import_paged(torch.ones_like(k), torch.ones_like(v), kp, vp, bad, batch_index=0, row0=0)
+    changed = {int(p) for p in (kp.view(torch.int16) != before.view(torch.int16))
+               .reshape(6, -1).any(dim=1).nonzero().flatten().tolist()}
+    assert changed == {int(perm[0, 0])}
+    with pytest.raises(Exception, match="exceed"):
+        O.kv_export_paged(kp, vp, table, batch_index=1, row0=90, rows=7)
+
+
+def _bits_t(t):
+    import torch
+    return t.view(torch.int16) if t.element_size() == 2 else t.view(torch.int32)
