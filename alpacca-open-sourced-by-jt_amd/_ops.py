@@ -9,6 +9,7 @@ in libalpx.so.  Nothing here computes on the CPU.
 from __future__ import annotations
 
 import math
+import os
 
 from . import _lib
 
@@ -573,12 +574,18 @@ def attention_prologue_chunk(query_gate, key, value, q_norm, k_norm, key_cache, 
 
 def attention_layer_prefill(query_gate, key, value, q_norm, k_norm, key_cache, value_cache, *,
                             batch_index, position, sections, frequency_base, eps, scale=None,
-                            out_dtype=None):
+                            out_dtype=None, fused_query=None):
     """Qwen3.5 attention-layer prefill chunk (``alpx_attention_layer_prefill``):
     the chunk prologue for ``query_gate [T, Hq, 2D]``, ``key [T, Hkv, D]``,
     ``value [T, Hkv, D]`` of cache sequence ``batch_index`` at positions
     ``position ..``, then the causal prefill over the cache with the sigmoid
-    gate read from ``query_gate``.  Returns the gated output ``[T, Hq, D]``."""
+    gate read from ``query_gate``.  Returns the gated output ``[T, Hq, D]``.
+
+    ``fused_query`` picks the form: True has the prefill form the query
+    rows from ``query_gate`` itself (no query buffer; fp16 / bf16, D in
+    {64, 128, 256}, rotary sections summing to a multiple of 32), False
+    writes them to a query buffer first, None takes the first where it
+    applies.  Both give the same bits."""
     torch = _torch()
     capacity, cache_batch, kv_heads, dim = (int(x) for x in key_cache.shape)
     tokens, q_heads = int(query_gate.shape[0]), int(query_gate.shape[1])
@@ -586,11 +593,19 @@ def attention_layer_prefill(query_gate, key, value, q_norm, k_norm, key_cache, v
     if scale is None:
         scale = 1.0 / math.sqrt(dim)
     out_dtype = key_cache.dtype if out_dtype is None else out_dtype
-    query = torch.empty((tokens, q_heads, dim), dtype=key_cache.dtype, device=dev)
     out = torch.empty((tokens, q_heads, dim), dtype=out_dtype, device=dev)
     L = _lib.lib()
     fast = key_cache.dtype != torch.float32 and dim in (64, 128, 256)
+    pairs = sum(int(x) for x in sections)
+    if fused_query is None:
+        fused_query = (fast and pairs % 32 == 0 and 2 * pairs <= dim
+                       and os.environ.get("ALPX_PREFILL_GENERIC") is None)
+    query = None
     ws = None
+    if fused_query:
+        ws = _lib.workspace(torch, dev, max(tokens * pairs * 8, 1))
+    else:
+        query = torch.empty((tokens, q_heads, dim), dtype=key_cache.dtype, device=dev)
     if not fast:
         nbytes = L.alpx_prefill_workspace_bytes(tokens, q_heads, kv_heads, dim,
                                                 int(position) + tokens)
@@ -599,10 +614,11 @@ def attention_layer_prefill(query_gate, key, value, q_norm, k_norm, key_cache, v
         ws = _lib.workspace(torch, dev, nbytes)
     rc = L.alpx_attention_layer_prefill(
         query_gate.data_ptr(), key.data_ptr(), value.data_ptr(), q_norm.data_ptr(),
-        k_norm.data_ptr(), query.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(),
-        out.data_ptr(), None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(),
-        _lib.dtype_code(torch, key_cache.dtype), _lib.dtype_code(torch, out.dtype), capacity,
-        cache_batch, int(batch_index), tokens, q_heads, kv_heads, dim, int(position),
+        k_norm.data_ptr(), None if query is None else query.data_ptr(), key_cache.data_ptr(),
+        value_cache.data_ptr(), out.data_ptr(), None if ws is None else ws.data_ptr(),
+        0 if ws is None else ws.numel(), _lib.dtype_code(torch, key_cache.dtype),
+        _lib.dtype_code(torch, out.dtype), capacity, cache_batch, int(batch_index), tokens,
+        q_heads, kv_heads, dim, int(position),
         _sections(sections), float(frequency_base), float(eps), float(scale),
         _lib.stream_handle(torch, dev))
     _lib.check(rc)

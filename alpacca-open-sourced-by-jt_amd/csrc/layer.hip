@@ -223,6 +223,8 @@ struct ProArgs {
   int bsel;          // < 0: row r is cache sequence r; else every row is cache sequence bsel
   int sec[4];
   float eps;
+  int slot0;         // first slot processed (Hq: key and value heads only)
+  float2* rot_out;   // null, or [B, R]: (cos, sin) of each row's rotary pairs
   double inv[kMaxPairs];  // base^(-2 p / (2 R)) per pair p
 };
 
@@ -235,11 +237,11 @@ __global__ void __launch_bounds__(256) attn_prologue_kernel(ProArgs a) {
   __shared__ float stage[4][kMaxDim];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int slots = a.Hq + 2 * a.Hkv;
+  const int slots = a.Hq + 2 * a.Hkv - a.slot0;
   const int64_t id = (int64_t)blockIdx.x * 4 + wave;
   if (id >= (int64_t)a.B * slots) return;
   const int b = (int)(id / slots);
-  const int j = (int)(id - (int64_t)b * slots);
+  const int j = a.slot0 + (int)(id - (int64_t)b * slots);
   const int64_t pos = a.positions ? (int64_t)a.positions[b] : a.position + b * a.pos_step;
   const bool in_cache = pos >= 0 && pos < a.capacity;
   const int64_t crow = pos * a.CB + (a.bsel < 0 ? b : a.bsel);  // cache row of this token
@@ -250,6 +252,15 @@ __global__ void __launch_bounds__(256) attn_prologue_kernel(ProArgs a) {
     T* dst = (T*)a.vc + (crow * a.Hkv + h) * a.Dv;
     for (int i = lane; i < a.Dv; i += 64) dst[i] = src[i];
     return;
+  }
+  if (a.rot_out != nullptr && j == a.Hq) {
+    // the rotation of this row's pairs, as norm_rope forms it, for a
+    // kernel that rotates the query heads itself
+    for (int pr = lane; pr < a.R; pr += 64) {
+      float c, sn;
+      rope_cs(imrope_lane(pr, a.sec, a.R) == 3 ? 0.0 : (double)pos, a.inv[pr], c, sn);
+      a.rot_out[(int64_t)b * a.R + pr] = make_float2(c, sn);
+    }
   }
   const bool is_q = j < a.Hq;
   const int h = is_q ? j : j - a.Hq;
@@ -983,9 +994,10 @@ int attention_prologue_launch(const char* what, const void* query_gate, const vo
                               int cache_batch, int bsel, int64_t pos_step, int q_heads,
                               int kv_heads, int head_dim, int value_dim, int64_t position,
                               const int32_t* positions, const int* sections,
-                              double frequency_base, float eps, void* stream) {
+                              double frequency_base, float eps, void* stream,
+                              bool kv_only = false, float2* rot_out = nullptr) {
   using namespace alpx;
-  if (!query_gate || !key || !value || !q_norm || !k_norm || !query_out ||
+  if (!query_gate || !key || !value || !q_norm || !k_norm || (!query_out && !kv_only) ||
       (!gate_out && pos_step == 0) || !key_cache || !value_cache)
     return fail(ALPX_EINVAL, "%s: null buffer", what);
   if (!dtype_ok(dtype)) return fail(ALPX_EINVAL, "%s: unknown dtype", what);
@@ -1028,9 +1040,11 @@ int attention_prologue_launch(const char* what, const void* query_gate, const vo
   for (int i = 0; i < 4; ++i) a.sec[i] = sections[i];
   inverse_frequencies(a.inv, R, frequency_base, 1.0);
   a.eps = eps;
+  a.slot0 = kv_only ? q_heads : 0;
+  a.rot_out = rot_out;
   hipStream_t s = (hipStream_t)stream;
   TimedRegion timed(ALPX_T_LAYER, s);
-  const int64_t waves = (int64_t)rows * (q_heads + 2 * kv_heads);
+  const int64_t waves = (int64_t)rows * (q_heads + 2 * kv_heads - a.slot0);
   const dim3 grid((unsigned)((waves + 3) / 4));
   switch (dtype) {
     case ALPX_F32: hipLaunchKernelGGL(attn_prologue_kernel<float>, grid, dim3(256), 0, s, a); break;
@@ -1074,6 +1088,26 @@ extern "C" int alpx_attention_prologue_chunk(const void* query_gate, const void*
                                    kv_heads, head_dim, value_dim, position, nullptr, sections,
                                    frequency_base, eps, stream);
 }
+
+namespace alpx {
+// The chunk prologue's key and value heads only (the query heads are
+// formed by the prefill kernel that reads them): cache rows written as
+// alpx_attention_prologue_chunk writes them.
+int attention_prologue_chunk_kv(const void* query_gate, const void* key, const void* value,
+                                const float* q_norm, const float* k_norm, void* key_cache,
+                                void* value_cache, int dtype, int64_t capacity, int cache_batch,
+                                int batch_index, int tokens, int q_heads, int kv_heads,
+                                int head_dim, int value_dim, int64_t position, const int* sections,
+                                double frequency_base, float eps, float2* rot_out, void* stream) {
+  if (batch_index < 0 || batch_index >= cache_batch)
+    return fail(ALPX_EINVAL, "batch_index exceeds the cache batch");
+  return attention_prologue_launch("alpx_attention_layer_prefill", query_gate, key, value,
+                                   q_norm, k_norm, nullptr, nullptr, key_cache, value_cache,
+                                   dtype, capacity, tokens, cache_batch, batch_index, 1, q_heads,
+                                   kv_heads, head_dim, value_dim, position, nullptr, sections,
+                                   frequency_base, eps, stream, true, rot_out);
+}
+}  // namespace alpx
 
 namespace {
 

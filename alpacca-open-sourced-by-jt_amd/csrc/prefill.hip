@@ -65,6 +65,17 @@ struct PrefillArgs {
   const void* kn;
   const void* vn;
   int new0;
+  // Fused query prologue (qw != null; the Qwen3.5 attention-layer chunk):
+  // q holds the joint projection rows [T, Hq, 2 D], and each query row is
+  // RMS-normalised with qw and rotated (IMROPE, q_R pairs, a multiple of
+  // 32) with the attention prologue's arithmetic, then rounded to T, before
+  // the softmax scale is applied.  q_rot [T, q_R] holds the (cos, sin) of
+  // token t's pairs, formed by the prologue launch that writes the keys.
+  int64_t q_stride;  // elements between the (token, head) rows of q
+  const float* qw;
+  const float2* q_rot;
+  float q_eps;
+  int q_R;
 };
 
 constexpr int kXcds = 8;  // MI355X: workgroup b is dispatched to XCD b % 8
@@ -283,6 +294,82 @@ constexpr int kRunWrite = 0, kRunPartial = 1, kRunMerge = 2;
 // prefill_mfma runs one per block; prefill_pair runs two groups per block.
 // part_o / part_st: the partial's LDS home (written by kRunPartial, read by
 // kRunMerge).
+// The attention prologue's query half (norm_rope) for one column whose row
+// a lane holds as q[ks] = channels 32 ks + 8 quad + 0..7 (the four lanes
+// of a column hold quads 0..3), giving the prologue's bits.  The prologue
+// wave sums squares per lane l over channels l + 64 e (e ascending) and
+// then across lanes with xor offsets 32, 16, 8, 4, 2, 1; here lane
+// l = 32 h + 8 quad + j lives in slot j of this lane's registers with
+// ks = 2 e + h, offset 32 pairs h = 0 / 1 in place, 16 and 8 pair the lanes
+// of quads quad ^ 2 and quad ^ 1 (this kernel's lanes ^ 32 and ^ 16), and
+// 4, 2, 1 pair slots.  With q_R a multiple of 32 a channel's rotation
+// partner (d +- q_R) sits in the same lane, q_R / 32 registers away; the
+// (cos, sin) of its pair come from q_rot.
+template <typename T, int D>
+__device__ __forceinline__ void fused_query(const PrefillArgs& a, typename Vec8<T>::type (&q)[D / 32],
+                                            int tok, int quad) {
+  constexpr int KS = D / 32, E = D / 64;
+  float x[KS][8];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[ks][j] = to_f32(q[ks][j]);
+  float v[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      s0 = fmaf(x[2 * e][j], x[2 * e][j], s0);
+      s1 = fmaf(x[2 * e + 1][j], x[2 * e + 1][j], s1);
+    }
+    v[j] = s0 + s1;
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = v[j] + __shfl_xor(v[j], 32);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = v[j] + __shfl_xor(v[j], 16);
+  float w4[8], w2[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) w4[j] = v[j] + v[j ^ 4];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) w2[j] = w4[j] + w4[j ^ 2];
+  const float ss = w2[0] + w2[1];
+  const float inv = 1.f / sqrtf(ss / (float)D + a.q_eps);
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    const f32x4 w0 = *(const f32x4*)(a.qw + 32 * ks + 8 * quad);
+    const f32x4 w1 = *(const f32x4*)(a.qw + 32 * ks + 8 * quad + 4);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[ks][j] = x[ks][j] * inv * (j < 4 ? w0[j] : w1[j - 4]);
+  }
+  const int R = a.q_R, RK = R / 32;
+  const float2* rot = a.q_rot + (int64_t)tok * R;
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    const bool rotated = 32 * ks < 2 * R;  // whole 32-channel groups rotate or not
+    const bool first = 32 * ks < R;
+    float2 cs[8];
+    if (rotated) {
+      const int pr0 = (first ? 32 * ks : 32 * ks - R) + 8 * quad;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) cs[j] = rot[pr0 + j];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float y = x[ks][j];
+      if (rotated) {
+        float xp = 0.f;  // the partner, RK registers away
+#pragma unroll
+        for (int k2 = 0; k2 < KS; ++k2)
+          if (k2 == (first ? ks + RK : ks - RK)) xp = x[k2][j];
+        y = rope_pair(first, x[ks][j], xp, cs[j].x, cs[j].y);
+      }
+      q[ks][j] = from_f32<T>(y);
+    }
+  }
+}
+
 template <typename T, typename TO, int D, int BK, int NQB, bool PAGED, int MODE, int NW,
           typename Bar>
 __device__ __forceinline__ void prefill_run(const PrefillArgs& a, int kvh, int ctile, int tb,
@@ -360,14 +447,9 @@ __device__ __forceinline__ void prefill_run(const PrefillArgs& a, int kvh, int c
   V8 qv[NQB][KS];
 #pragma unroll
   for (int qb = 0; qb < NQB; ++qb) {
-    const T* qp = (const T*)a.q + ((int64_t)tok[qb] * a.q_heads + hq[qb]) * D + 8 * quad;
+    const T* qp = (const T*)a.q + ((int64_t)tok[qb] * a.q_heads + hq[qb]) * a.q_stride + 8 * quad;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      V8 x = *(const V8*)(qp + 32 * ks);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] = from_f32<T>(to_f32(x[e]) * c2);
-      qv[qb][ks] = cok[qb] ? x : (V8){};
-    }
+    for (int ks = 0; ks < KS; ++ks) qv[qb][ks] = *(const V8*)(qp + 32 * ks);
   }
 
   f32x4 o[NQB][MB];   // O^T[d = 16 mb + 4 quad + i][column]
@@ -738,6 +820,22 @@ __device__ __forceinline__ void prefill_run(const PrefillArgs& a, int kvh, int c
     if constexpr (PAGED) kpage[1] = tile_page(1);
     load_tile(kg, kgn, a.ks_pos, a.ks_page, kofs, 1, 1, kpage[1]);
   }
+  // The query columns' own work (the fused prologue, the scale) after the
+  // first tile loads are issued, so that it overlaps their flight.
+  if (a.qw != nullptr) {
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb) fused_query<T, D>(a, qv[qb], tok[qb], quad);
+  }
+#pragma unroll
+  for (int qb = 0; qb < NQB; ++qb) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      V8 x = qv[qb][ks];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = from_f32<T>(to_f32(x[e]) * c2);
+      qv[qb][ks] = cok[qb] ? x : (V8){};
+    }
+  }
   __builtin_amdgcn_s_waitcnt(0);
   bar();
   qk_first();
@@ -1100,6 +1198,7 @@ PrefillKernelChoice choose_prefill(int q_tokens, int kv_tokens, int kv_heads, in
     return one_stream ? kSharedKernel : kSingleKernel;
   const int64_t pairs = (int64_t)kv_heads * ((col_tiles + 1) / 2);
   const int resident = alpx::resident_blocks(pair_kernel, 512, 0);
+  if (resident <= 0) return kSingleKernel;
   const bool one_round = pairs <= resident && pairs * 10 >= (int64_t)resident * 9;
   if (!one_round && !(key_dim == 256 && pairs > resident)) return kSingleKernel;
   const int first = host_tile_keys(q_tokens, kv_tokens, group, rel0, window, cols_per_block, rows, 0);
@@ -1111,13 +1210,23 @@ PrefillKernelChoice choose_prefill(int q_tokens, int kv_tokens, int kv_heads, in
   return ratio10 >= r10 ? kPairKernel : kSingleKernel;
 }
 
+// The query prologue a prefill forms itself (alpx_attention_layer_prefill
+// with no query_out): q is then the joint projection [T, Hq, 2 D].
+struct QueryPrologue {
+  const float* qw;
+  const float2* rot;  // [T, R] (cos, sin) per token and pair
+  float eps;
+  int R;
+};
+
 int prefill_impl(const void* q, const void* key, const void* value, const void* gate, void* out,
                  void* workspace, size_t workspace_bytes, int q_tokens, int kv_tokens,
                  int q_heads, int kv_heads, int key_dim, int value_dim, int64_t k_pos_stride,
                  int64_t v_pos_stride, int64_t q_pos0, int window, int64_t kv_start, float scale,
                  int dtype, int out_dtype, void* stream, const int32_t* pages = nullptr,
                  int page_shift = 0, int num_pages = 0, const void* kn = nullptr,
-                 const void* vn = nullptr, int64_t gate_stride = 0) {
+                 const void* vn = nullptr, int64_t gate_stride = 0,
+                 const QueryPrologue* qpro = nullptr) {
   using namespace alpx;
   if (!q || !key || !value || !out) return fail(ALPX_EINVAL, "alpx_prefill_causal: null buffer");
   if (!dtype_ok(dtype) || !dtype_ok(out_dtype))
@@ -1144,7 +1253,9 @@ int prefill_impl(const void* q, const void* key, const void* value, const void* 
                         v_pos_stride != (int64_t)kv_heads * value_dim))
     return fail(ALPX_EINVAL, "alpx_prefill_append: cache rows must be contiguous");
   if (gate_stride == 0) gate_stride = value_dim;
-  const uintptr_t align = (uintptr_t)q | (uintptr_t)key | (uintptr_t)value | (uintptr_t)gate |
+  const int64_t q_stride = qpro != nullptr ? 2 * (int64_t)key_dim : key_dim;
+  const uintptr_t align = (uintptr_t)q | (uintptr_t)(q_stride * es) | (uintptr_t)key |
+                          (uintptr_t)value | (uintptr_t)gate |
                           (uintptr_t)(gate_stride * es) |
                           (uintptr_t)kn | (uintptr_t)vn | (uintptr_t)(k_pos_stride * es) |
                           (uintptr_t)(v_pos_stride * es);
@@ -1195,6 +1306,13 @@ int prefill_impl(const void* q, const void* key, const void* value, const void* 
     a.ks_page = ((int64_t)1 << page_shift) * k_pos_stride;
     a.vs_page = ((int64_t)1 << page_shift) * v_pos_stride;
     a.q = q;
+    a.q_stride = q_stride;
+    if (qpro != nullptr) {
+      a.qw = qpro->qw;
+      a.q_rot = qpro->rot;
+      a.q_eps = qpro->eps;
+      a.q_R = qpro->R;
+    }
     a.k = key;
     a.v = value;
     a.gate = gate;
@@ -1224,6 +1342,8 @@ int prefill_impl(const void* q, const void* key, const void* value, const void* 
     return check_launch("prefill_mfma");
   }
 
+  if (qpro != nullptr)  // callers check the MFMA conditions before any launch
+    return fail(ALPX_EUNSUPPORTED, "fused query prologue: MFMA prefill shapes only");
   if (!workspace) return fail(ALPX_EINVAL, "alpx_prefill_causal: null workspace");
   if (kn != nullptr) {  // append mode off the MFMA path: the append kernel first
     const int rc = alpx_kv_append(const_cast<void*>(key), const_cast<void*>(value), kn, vn, dtype,
@@ -1330,19 +1450,62 @@ extern "C" int alpx_attention_layer_prefill(
     return fail(ALPX_EINVAL, "alpx_prefill_causal: null workspace");
   if (!(scale > 0.0f) || !isfinite(scale))
     return fail(ALPX_EINVAL, "attention scale must be positive and finite");
+  const size_t es = dtype_size(dtype);
+  const int64_t row = (int64_t)cache_batch * kv_heads * head_dim;
+  const int64_t seq = (int64_t)batch_index * kv_heads * head_dim;
+  const void* kseq = (const char*)key_cache + seq * es;
+  const void* vseq = (const char*)value_cache + seq * es;
+  const void* gate = (const char*)query_gate + head_dim * es;
+  if (query_out == nullptr) {
+    // The prefill forms the query rows from query_gate (its Q load runs the
+    // prologue's norm and rotation); the prologue launch writes the key and
+    // value rows only.  Needs the MFMA prefill and rotary pairs in whole
+    // 32-channel groups; checked before any launch.
+    int R = 0;
+    if (!query_gate || !q_norm || bad_sections(sections, R) || R % 32 != 0 || 2 * R > head_dim ||
+        !(frequency_base > 0.0) || !isfinite(frequency_base))
+      return fail(ALPX_EUNSUPPORTED,
+                  "alpx_attention_layer_prefill without query_out: needs rotary sections summing "
+                  "to a multiple of 32 and a valid frequency base");
+    const uintptr_t align = (uintptr_t)query_gate | (uintptr_t)kseq | (uintptr_t)vseq |
+                            (uintptr_t)q_norm | (uintptr_t)(row * es) |
+                            (uintptr_t)(2 * head_dim * es);
+    if (!((dtype == ALPX_F16 || dtype == ALPX_BF16) &&
+          (head_dim == 64 || head_dim == 128 || head_dim == 256) && (align & 15) == 0 &&
+          getenv("ALPX_PREFILL_GENERIC") == nullptr &&
+          (position + tokens) * row * (int64_t)es < ((int64_t)1 << 31)))
+      return fail(ALPX_EUNSUPPORTED,
+                  "alpx_attention_layer_prefill without query_out: needs fp16/bf16, head_dim in "
+                  "{64, 128, 256}, 16-byte aligned rows and q_norm, and a cache under 2 GiB per "
+                  "tensor");
+    const size_t need = (size_t)tokens * R * sizeof(float2);
+    if (!workspace || workspace_bytes < need)
+      return fail(ALPX_EINVAL, "alpx_attention_layer_prefill: workspace of %zu bytes, %zu needed",
+                  workspace ? workspace_bytes : (size_t)0, need);
+    QueryPrologue qp = {};
+    qp.qw = q_norm;
+    qp.rot = (const float2*)workspace;
+    qp.eps = eps;
+    qp.R = R;
+    const int rc = attention_prologue_chunk_kv(
+        query_gate, key, value, q_norm, k_norm, key_cache, value_cache, dtype, capacity,
+        cache_batch, batch_index, tokens, q_heads, kv_heads, head_dim, head_dim, position,
+        sections, frequency_base, eps, (float2*)workspace, stream);
+    if (rc != ALPX_OK) return rc;
+    return prefill_impl(query_gate, kseq, vseq, gate, out, workspace, workspace_bytes, tokens,
+                        (int)(position + tokens), q_heads, kv_heads, head_dim, head_dim, row, row,
+                        position, 0, 0, scale, dtype, out_dtype, stream, nullptr, 0, 0, nullptr,
+                        nullptr, 2 * (int64_t)head_dim, &qp);
+  }
   const int rc = alpx_attention_prologue_chunk(
       query_gate, key, value, q_norm, k_norm, query_out, nullptr, key_cache, value_cache, dtype,
       capacity, cache_batch, batch_index, tokens, q_heads, kv_heads, head_dim, head_dim, position,
       sections, frequency_base, eps, stream);
   if (rc != ALPX_OK) return rc;
-  const size_t es = dtype_size(dtype);
-  const int64_t row = (int64_t)cache_batch * kv_heads * head_dim;
-  const int64_t seq = (int64_t)batch_index * kv_heads * head_dim;
-  return prefill_impl(query_out, (const char*)key_cache + seq * es,
-                      (const char*)value_cache + seq * es, (const char*)query_gate + head_dim * es,
-                      out, workspace, workspace_bytes, tokens, (int)(position + tokens), q_heads,
-                      kv_heads, head_dim, head_dim, row, row, position, 0, 0, scale, dtype,
-                      out_dtype, stream, nullptr, 0, 0, nullptr, nullptr, 2 * (int64_t)head_dim);
+  return prefill_impl(query_out, kseq, vseq, gate, out, workspace, workspace_bytes, tokens,
+                      (int)(position + tokens), q_heads, kv_heads, head_dim, head_dim, row, row,
+                      position, 0, 0, scale, dtype, out_dtype, stream, nullptr, 0, 0, nullptr,
+                      nullptr, 2 * (int64_t)head_dim);
 }
 
 extern "C" int alpx_prefill_causal_paged(const void* q, const void* key_pages,

@@ -33,6 +33,15 @@ __device__ __forceinline__ void rope_cs(double pos, double inv, float& c, float&
   sincosf((float)r, &s, &c);
 }
 
+// One rotated channel of an IMROPE pair: x c - xp s in the first half,
+// xp s + x c in the second (xp: the pair partner), with the fused
+// multiply-adds written out so every kernel that rotates forms the same
+// bits (the prologue kernels, the split kernel's prelude and the prefill
+// kernel's fused query prologue).
+__device__ __forceinline__ float rope_pair(bool first, float x, float xp, float c, float s) {
+  return first ? fmaf(x, c, -(xp * s)) : fmaf(xp, s, x * c);
+}
+
 __device__ __forceinline__ float rope_wave_sum(float v) {
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off);
@@ -40,7 +49,10 @@ __device__ __forceinline__ float rope_wave_sum(float v) {
 }
 
 // One head row by one wave: x (lane-strided, channel lane + 64 e, already
-// loaded) is RMS-normalised over D with per-channel weights wt, then the
+// loaded) is RMS-normalised over D with per-channel weights wt -- x times
+// one correctly rounded 1 / sqrt(mean(x^2) + eps) per row, times wt (the
+// reference divides each channel by the root, qwen35_cuda.py:920-931, which
+// differs by at most an fp32 rounding before the T rounding) -- then the
 // first 2 R channels are rotated as IMROPE pairs (p, p + R) at text
 // position p (the last section's lane uses position 0); st is a D-float
 // LDS row for the pair partners.  Channel i of the result goes to dst[i],
@@ -55,12 +67,12 @@ __device__ __forceinline__ void norm_rope(float (&x)[kPer], const float (&wt)[kP
   for (int e = 0; e < kPer; ++e)
     if (lane + 64 * e < D) ss = fmaf(x[e], x[e], ss);
   ss = rope_wave_sum(ss);
-  const float den = sqrtf(ss / (float)D + eps);
+  const float rinv = 1.f / sqrtf(ss / (float)D + eps);
 #pragma unroll
   for (int e = 0; e < kPer; ++e) {
     const int i = lane + 64 * e;
     if (i < D) {
-      x[e] = x[e] / den * wt[e];
+      x[e] = x[e] * rinv * wt[e];
       st[i] = x[e];
     }
   }
@@ -77,7 +89,7 @@ __device__ __forceinline__ void norm_rope(float (&x)[kPer], const float (&wt)[kP
       const int ln = imrope_lane(pr, sec, R);
       float c, sn;
       rope_cs(ln == 3 ? 0.0 : p, inv[pr], c, sn);
-      y = i < R ? x[e] * c - st[i + R] * sn : st[pr] * sn + x[e] * c;
+      y = rope_pair(i < R, x[e], i < R ? st[i + R] : st[pr], c, sn);
     }
     dst[i] = from_f32<T>(y);
   }
@@ -85,6 +97,15 @@ __device__ __forceinline__ void norm_rope(float (&x)[kPer], const float (&wt)[kP
 
 // scale * base^(-2 p / (2 R)) for p < R, in double precision (host).
 void inverse_frequencies(double* inv, int R, double base, double scale);
+// The attention chunk prologue's key / value heads only (layer.hip), and
+// rot_out [tokens, R] = the (cos, sin) of each token's rotary pairs: the
+// caller forms the query rows itself with the same arithmetic.
+int attention_prologue_chunk_kv(const void* query_gate, const void* key, const void* value,
+                                const float* q_norm, const float* k_norm, void* key_cache,
+                                void* value_cache, int dtype, int64_t capacity, int cache_batch,
+                                int batch_index, int tokens, int q_heads, int kv_heads,
+                                int head_dim, int value_dim, int64_t position, const int* sections,
+                                double frequency_base, float eps, float2* rot_out, void* stream);
 // R = the sum of the four IMROPE sections; true when they are unusable.
 bool bad_sections(const int* sections, int& R);
 

@@ -1035,7 +1035,10 @@ class Qwen35RocmOps:
         positions ``position .. position + T - 1`` as one fused prologue
         (split, Q/K RMSNorm, IMROPE, cache append) and one causal prefill
         attention over the cache with the sigmoid gate in its epilogue, read in
-        place from ``query_gate`` (alpx_attention_layer_prefill).  Returns
+        place from ``query_gate`` (alpx_attention_layer_prefill).  Where the
+        rotary sections sum to a multiple of 32 (Qwen3.5: 32), the prefill
+        forms the query heads itself from ``query_gate`` (same bits) and the
+        prologue launch writes only the key / value rows.  Returns
         ``(gated output [T, Hq, Dv], position + T)``."""
         key_cache = self._tensor(key_cache, "attention key cache", dimensions=4)
         value_cache = self._tensor(value_cache, "attention value cache", dimensions=4)

@@ -513,6 +513,9 @@ def bench_layer_prefill(torch, ops, lib, *, steps, warmup, seed=7):
     * Attention layer, Qwen3.5 head geometry (16 q / 2 kv heads, head_dim
       256, bf16), one sequence: a 2048-token chunk at position 2048 of a
       4096-row cache -- chunk prologue + causal prefill + sigmoid gate.
+      Timed in both forms: the query heads normed and rotated inside the
+      prefill's query load (chunk_ms), and through a query buffer
+      (query_buffer_chunk_ms).
       FLOPs count causal-valid pairs (4 D Hq per pair).  Token path: 2048
       attention-layer decode steps (prologue in the split-K launch, gated
       combine).
@@ -536,6 +539,14 @@ def bench_layer_prefill(torch, ops, lib, *, steps, warmup, seed=7):
         epsilon=eps)
     _warm(torch, chunk, 0.1)
     a_ms = _timed_steps(torch, chunk, max(10, steps // 2), 2)
+    # the same chunk with the query rows written to a buffer by the prologue
+    # launch and read back by the prefill (the form for rotary sections that
+    # are not whole groups of 32)
+    qg3 = qg.reshape(T, hq, 2 * d)
+    qbuf = lambda: _mod("_ops").attention_layer_prefill(  # noqa: E731
+        qg3, kn, vn, qw, kw, K, V, batch_index=0, position=prefix, sections=sec,
+        frequency_base=base, eps=eps, fused_query=False)
+    qb_ms = _timed_steps(torch, qbuf, max(10, steps // 2), 2)
 
     def tokens_attn():
         for t in range(T):
@@ -574,8 +585,8 @@ def bench_layer_prefill(torch, ops, lib, *, steps, warmup, seed=7):
     rt_ms = _timed_steps(torch, tokens_rec, 2, 1)
     return {
         "attention_layer_prefill_qwen35_2k_on_2k": {
-            "chunk_ms": round(a_ms, 4), "token_path_ms": round(at_ms, 3),
-            "speedup": round(at_ms / a_ms, 1), "flops": a_flops,
+            "chunk_ms": round(a_ms, 4), "query_buffer_chunk_ms": round(qb_ms, 4),
+            "token_path_ms": round(at_ms, 3), "speedup": round(at_ms / a_ms, 1), "flops": a_flops,
             "chunk_tflops": round(a_flops / (a_ms * 1e-3) / 1e12, 1)},
         "recurrent_layer_prefill_c5_1024": {
             "chunk_ms": round(r_ms, 4), "token_path_ms": round(rt_ms, 3),

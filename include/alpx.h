@@ -537,7 +537,16 @@ int alpx_attention_prologue_chunk(const void* query_gate, const void* key, const
  * token-sequential Qwen35Model._attention calls of a prefill
  * (qwen35_runtime.py:597-665, prefill_state qwen35_runtime.py:777-810).
  * value_dim must equal head_dim (the gate has head_dim values per head);
- * workspace as alpx_prefill_causal (only its fallback path uses it). */
+ * workspace as alpx_prefill_causal (only its fallback path uses it).
+ *
+ * query_out may be null: the prefill then forms the query rows itself from
+ * query_gate (the prologue's RMSNorm and IMROPE in its query load, same
+ * bits) and the prologue launch writes only the key / value rows and each
+ * token's rotary (cos, sin) pairs into workspace, which must hold
+ * tokens x R x 8 bytes (R = the section sum).  Needs fp16 / bf16,
+ * head_dim 64, 128 or 256, R a multiple of 32 with 2 R <= head_dim,
+ * 16-byte aligned query_gate, q_norm and cache rows; otherwise
+ * ALPX_EUNSUPPORTED before any launch. */
 int alpx_attention_layer_prefill(const void* query_gate, const void* key, const void* value,
                                  const float* q_norm, const float* k_norm, void* query_out,
                                  void* key_cache, void* value_cache, void* out, void* workspace,

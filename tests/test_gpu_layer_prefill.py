@@ -108,22 +108,34 @@ def test_attention_layer_prefill_matches_token_chain(gpu, ops, hq, hkv, d, secti
     assert np.abs(_np(KC)[:prefix + tokens, bi] - kco[:prefix + tokens]).max() <= 2e-2
 
 
-@pytest.mark.parametrize("hq,hkv,d,prefix,tokens,batch,bi,dtype", [
-    (16, 2, 256, 300, 130, 2, 1, "bf16"), (8, 2, 128, 0, 70, 1, 0, "f16"),
-    (4, 2, 64, 40, 33, 1, 0, "f32")])
+@pytest.mark.parametrize("hq,hkv,d,prefix,tokens,batch,bi,dtype,sec", [
+    (16, 2, 256, 300, 130, 2, 1, "bf16", (11, 11, 10, 0)),
+    (8, 2, 128, 0, 70, 1, 0, "f16", (11, 11, 10, 0)),
+    (4, 2, 64, 40, 33, 1, 0, "f32", (11, 11, 10, 0)),
+    (8, 2, 128, 17, 1, 1, 0, "bf16", (16, 16, 16, 16)),     # 2 R = D, one token
+    (4, 2, 64, 90, 45, 3, 2, "bf16", (8, 8, 8, 8)),         # 2 R = D at D = 64
+    (16, 2, 256, 2500, 384, 1, 0, "bf16", (11, 11, 10, 0)),  # long prefix, shared kernel
+    (16, 2, 256, 0, 1000, 1, 0, "f16", (24, 20, 20, 0)),    # R = 64, multi-round pairs
+    (8, 2, 128, 30, 50, 1, 0, "bf16", (10, 10, 10, 0)),     # R = 30: query buffer only
+])
 def test_attention_layer_prefill_equals_prologue_then_gated_prefill(gpu, hq, hkv, d, prefix,
-                                                                    tokens, batch, bi, dtype):
-    """alpx_attention_layer_prefill (prologue without the gate copy, the
-    prefill reading the gate in place from the joint projection, row stride
-    2 D) gives the bits of alpx_attention_prologue_chunk (gate copied) +
-    alpx_prefill_causal_gated: output and both caches (fp32 runs the split-K
-    fallback, whose combine applies the gate)."""
+                                                                    tokens, batch, bi, dtype,
+                                                                    sec):
+    """alpx_attention_layer_prefill in both of its forms gives the bits of
+    alpx_attention_prologue_chunk (gate copied) + alpx_prefill_causal_gated:
+    output and both caches.  The query-buffer form writes the query rows
+    and has the prefill read the gate in place from the joint projection
+    (row stride 2 D; fp32 runs the split-K fallback, whose combine applies
+    the gate); the fused form (fp16 / bf16, rotary pairs in whole groups of
+    32) has the prefill form the query rows from the joint projection
+    itself, with the prologue's RMS reduction order and rotation table."""
     import torch
     P = _mod("_ops")
+    Lib = _mod("_lib")
     td = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[dtype]
     rng = np.random.default_rng(hq + d + prefix)
     cap = prefix + tokens + 5
-    sec, base, eps = (11, 11, 10, 0), 1e6, 1e-6
+    base, eps = 1e6, 1e-6
     t = lambda a: torch.from_numpy(I.round_to(a, dtype).astype(np.float32)).to(gpu).to(td)  # noqa: E731
     kc0 = t(rng.standard_normal((cap, batch, hkv, d)))
     vc0 = t(rng.standard_normal((cap, batch, hkv, d)))
@@ -132,18 +144,29 @@ def test_attention_layer_prefill_equals_prologue_then_gated_prefill(gpu, hq, hkv
     v = t(rng.standard_normal((tokens, hkv, d)))
     qw = torch.from_numpy(rng.uniform(0.5, 1.5, d).astype(np.float32)).to(gpu)
     kw = torch.from_numpy(rng.uniform(0.5, 1.5, d).astype(np.float32)).to(gpu)
-    KA, VA = kc0.clone(), vc0.clone()
-    out_a = P.attention_layer_prefill(qg, k, v, qw, kw, KA, VA, batch_index=bi, position=prefix,
-                                      sections=sec, frequency_base=base, eps=eps)
     KB, VB = kc0.clone(), vc0.clone()
     q, g = P.attention_prologue_chunk(qg, k, v, qw, kw, KB, VB, batch_index=bi, position=prefix,
                                       sections=sec, frequency_base=base, eps=eps)
     out_b = P.prefill(q, KB[:, bi], VB[:, bi], pos0=prefix, kv_tokens=prefix + tokens,
                       k_pos_stride=batch * hkv * d, v_pos_stride=batch * hkv * d, gate=g)
     torch.cuda.synchronize()
-    assert torch.equal(KA, KB) and torch.equal(VA, VB)
-    assert torch.equal(out_a, out_b)
     assert torch.equal(g, qg[:, :, d:])  # the copied gate is the joint row's second half
+    fusable = dtype != "f32" and sum(sec) % 32 == 0
+    for fused in (None, False, True):
+        KA, VA = kc0.clone(), vc0.clone()
+        call = lambda: P.attention_layer_prefill(  # noqa: E731
+            qg, k, v, qw, kw, KA, VA, batch_index=bi, position=prefix, sections=sec,
+            frequency_base=base, eps=eps, fused_query=fused)
+        if fused and not fusable:
+            with pytest.raises(Lib.AlpxUnsupported, match="without query_out"):
+                call()
+            # refused before any launch: the caches are untouched
+            assert torch.equal(KA, kc0) and torch.equal(VA, vc0)
+            continue
+        out_a = call()
+        torch.cuda.synchronize()
+        assert torch.equal(KA, KB) and torch.equal(VA, VB), fused
+        assert torch.equal(out_a, out_b), fused
 
 
 def test_attention_layer_prefill_rejects_bad_shapes(gpu, ops):
