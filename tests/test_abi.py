@@ -109,6 +109,31 @@ def test_facade_validation_mirrors_reference(pkg):
         ops.zeros((0, 2))
 
 
+def test_layer_prefill_without_query_buffer_refusals_without_gpu(pkg):
+    """alpx_attention_layer_prefill with query_out = NULL (the prefill forms
+    the query heads itself) refuses what that form cannot do -- fp32, rotary
+    sections that are not whole groups of 32, a head_dim it has no kernel
+    for, a workspace too small for the rotation table -- before any launch."""
+    L = pkg._lib
+    lib = L.lib()
+    fake = ctypes.c_void_p(256)  # never dereferenced: validation fails first
+    sec = (ctypes.c_int * 4)(11, 11, 10, 0)   # R = 32
+    odd = (ctypes.c_int * 4)(10, 10, 10, 0)   # R = 30
+
+    def call(dtype, sections, head_dim=256, ws=fake, ws_bytes=1 << 20, tokens=64):
+        return lib.alpx_attention_layer_prefill(
+            fake, fake, fake, fake, fake, None, fake, fake, fake, ws, ws_bytes, dtype, dtype,
+            4096, 1, 0, tokens, 16, 2, head_dim, 0, sections, 1e7, 1e-6, 0.0625, None)
+
+    assert call(L.F32, sec) == L.EUNSUPPORTED and "without query_out" in L.last_error()
+    assert call(L.BF16, odd) == L.EUNSUPPORTED and "multiple of 32" in L.last_error()
+    assert call(L.F16, sec, head_dim=96) == L.EUNSUPPORTED and "head_dim" in L.last_error()
+    # 64 tokens x 32 pairs x 8 bytes = 16 KiB of rotation table
+    assert call(L.BF16, sec, ws_bytes=16383) == L.EINVAL
+    assert "16384 needed" in L.last_error()
+    assert call(L.BF16, sec, ws=None) == L.EINVAL and "workspace" in L.last_error()
+
+
 def test_layer_entry_points_validate_without_gpu(pkg):
     lib = pkg._lib.lib()
     L = pkg._lib
