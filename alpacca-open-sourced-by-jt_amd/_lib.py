@@ -76,6 +76,12 @@ SIGNATURES = {
                                               _c_int, _c_int, _c_i64,
                                               ctypes.POINTER(ctypes.c_int), ctypes.c_double,
                                               _c_float, _c_float, _c_ptr]),
+    "alpx_attention_layer_prefill_paged": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
+                                                    _c_ptr, _c_ptr, _c_ptr, _c_int, _c_int,
+                                                    _c_int, _c_int, _c_ptr, _c_ptr, _c_size,
+                                                    _c_int, _c_int, _c_int, _c_int, _c_int,
+                                                    _c_i64, ctypes.POINTER(ctypes.c_int),
+                                                    ctypes.c_double, _c_float, _c_float, _c_ptr]),
     "alpx_gdn_step": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int,
                                _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_ptr]),
     "alpx_gdn_chunk_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int]),

@@ -549,6 +549,36 @@ def attention_layer_step_paged(query_gate, key, value, q_norm, k_norm, key_pages
     return out
 
 
+def attention_layer_prefill_paged(query_gate, key, value, q_norm, k_norm, key_pages, value_pages,
+                                  block_table, *, batch_index, position, sections,
+                                  frequency_base, eps, scale=None):
+    """``attention_layer_prefill`` (the form without a query buffer) over a
+    paged pool: pages ``[P, page_size, Hkv, D]`` (fp16 / bf16, D in 64, 128,
+    256, page_size a power of two >= 64) and ``block_table [B, max_pages]``
+    (device int32); the chunk's rotated keys and values land at logical
+    rows ``position ..`` of sequence ``batch_index`` through the table.
+    Returns the gated output ``[T, Hq, D]`` in the pages' dtype."""
+    torch = _torch()
+    num_pages, page_size, kv_heads, dim = (int(x) for x in key_pages.shape)
+    max_pages = int(block_table.shape[1])
+    tokens, q_heads = int(query_gate.shape[0]), int(query_gate.shape[1])
+    dev = key_pages.device
+    if scale is None:
+        scale = 1.0 / math.sqrt(dim)
+    out = torch.empty((tokens, q_heads, dim), dtype=key_pages.dtype, device=dev)
+    pairs = sum(int(x) for x in sections)
+    ws = _lib.workspace(torch, dev, max(tokens * pairs * 8, 1))
+    rc = _lib.lib().alpx_attention_layer_prefill_paged(
+        query_gate.data_ptr(), key.data_ptr(), value.data_ptr(), q_norm.data_ptr(),
+        k_norm.data_ptr(), key_pages.data_ptr(), value_pages.data_ptr(), block_table.data_ptr(),
+        max_pages, page_size, num_pages, int(batch_index), out.data_ptr(), ws.data_ptr(),
+        ws.numel(), _lib.dtype_code(torch, key_pages.dtype), tokens, q_heads, kv_heads, dim,
+        int(position), _sections(sections), float(frequency_base), float(eps), float(scale),
+        _lib.stream_handle(torch, dev))
+    _lib.check(rc)
+    return out
+
+
 def attention_prologue_chunk(query_gate, key, value, q_norm, k_norm, key_cache, value_cache, *,
                              batch_index, position, sections, frequency_base, eps):
     """Attention prologue for ``T`` consecutive tokens of cache sequence

@@ -225,6 +225,12 @@ struct ProArgs {
   float eps;
   int slot0;         // first slot processed (Hq: key and value heads only)
   float2* rot_out;   // null, or [B, R]: (cos, sin) of each row's rotary pairs
+  // Paged caches (table non-null): logical row pos of the one sequence is
+  // row pos % 2^page_shift of page table[pos >> page_shift] of a pool
+  // [num_pages, 2^page_shift, Hkv, D]; an entry outside the pool writes
+  // nothing.
+  const int32_t* table;
+  int page_shift, num_pages;
   double inv[kMaxPairs];  // base^(-2 p / (2 R)) per pair p
 };
 
@@ -243,8 +249,13 @@ __global__ void __launch_bounds__(256) attn_prologue_kernel(ProArgs a) {
   const int b = (int)(id / slots);
   const int j = a.slot0 + (int)(id - (int64_t)b * slots);
   const int64_t pos = a.positions ? (int64_t)a.positions[b] : a.position + b * a.pos_step;
-  const bool in_cache = pos >= 0 && pos < a.capacity;
-  const int64_t crow = pos * a.CB + (a.bsel < 0 ? b : a.bsel);  // cache row of this token
+  bool in_cache = pos >= 0 && pos < a.capacity;
+  int64_t crow = pos * a.CB + (a.bsel < 0 ? b : a.bsel);  // cache row of this token
+  if (a.table != nullptr && in_cache) {
+    const int pg = a.table[pos >> a.page_shift];
+    in_cache = pg >= 0 && pg < a.num_pages;
+    crow = ((int64_t)pg << a.page_shift) + (pos & ((1 << a.page_shift) - 1));
+  }
   if (j >= a.Hq + a.Hkv) {  // value head
     const int h = j - a.Hq - a.Hkv;
     if (!in_cache) return;
@@ -995,7 +1006,9 @@ int attention_prologue_launch(const char* what, const void* query_gate, const vo
                               int kv_heads, int head_dim, int value_dim, int64_t position,
                               const int32_t* positions, const int* sections,
                               double frequency_base, float eps, void* stream,
-                              bool kv_only = false, float2* rot_out = nullptr) {
+                              bool kv_only = false, float2* rot_out = nullptr,
+                              const int32_t* table = nullptr, int page_shift = 0,
+                              int num_pages = 0) {
   using namespace alpx;
   if (!query_gate || !key || !value || !q_norm || !k_norm || (!query_out && !kv_only) ||
       (!gate_out && pos_step == 0) || !key_cache || !value_cache)
@@ -1042,6 +1055,9 @@ int attention_prologue_launch(const char* what, const void* query_gate, const vo
   a.eps = eps;
   a.slot0 = kv_only ? q_heads : 0;
   a.rot_out = rot_out;
+  a.table = table;
+  a.page_shift = page_shift;
+  a.num_pages = num_pages;
   hipStream_t s = (hipStream_t)stream;
   TimedRegion timed(ALPX_T_LAYER, s);
   const int64_t waves = (int64_t)rows * (q_heads + 2 * kv_heads - a.slot0);
@@ -1098,14 +1114,17 @@ int attention_prologue_chunk_kv(const void* query_gate, const void* key, const v
                                 void* value_cache, int dtype, int64_t capacity, int cache_batch,
                                 int batch_index, int tokens, int q_heads, int kv_heads,
                                 int head_dim, int value_dim, int64_t position, const int* sections,
-                                double frequency_base, float eps, float2* rot_out, void* stream) {
+                                double frequency_base, float eps, float2* rot_out, void* stream,
+                                const int32_t* table, int page_shift, int num_pages) {
   if (batch_index < 0 || batch_index >= cache_batch)
     return fail(ALPX_EINVAL, "batch_index exceeds the cache batch");
-  return attention_prologue_launch("alpx_attention_layer_prefill", query_gate, key, value,
-                                   q_norm, k_norm, nullptr, nullptr, key_cache, value_cache,
-                                   dtype, capacity, tokens, cache_batch, batch_index, 1, q_heads,
-                                   kv_heads, head_dim, value_dim, position, nullptr, sections,
-                                   frequency_base, eps, stream, true, rot_out);
+  return attention_prologue_launch(table ? "alpx_attention_layer_prefill_paged"
+                                         : "alpx_attention_layer_prefill",
+                                   query_gate, key, value, q_norm, k_norm, nullptr, nullptr,
+                                   key_cache, value_cache, dtype, capacity, tokens, cache_batch,
+                                   batch_index, 1, q_heads, kv_heads, head_dim, value_dim,
+                                   position, nullptr, sections, frequency_base, eps, stream, true,
+                                   rot_out, table, page_shift, num_pages);
 }
 }  // namespace alpx
 

@@ -1508,6 +1508,70 @@ extern "C" int alpx_attention_layer_prefill(
                       nullptr, 2 * (int64_t)head_dim);
 }
 
+extern "C" int alpx_attention_layer_prefill_paged(
+    const void* query_gate, const void* key, const void* value, const float* q_norm,
+    const float* k_norm, void* key_pages, void* value_pages, const int32_t* block_table,
+    int max_pages, int page_size, int num_pages, int batch_index, void* out, void* workspace,
+    size_t workspace_bytes, int dtype, int tokens, int q_heads, int kv_heads, int head_dim,
+    int64_t position, const int* sections, double frequency_base, float eps, float scale,
+    void* stream) {
+  using namespace alpx;
+  const char* what = "alpx_attention_layer_prefill_paged";
+  if (!query_gate || !key || !value || !q_norm || !k_norm || !key_pages || !value_pages ||
+      !block_table || !out)
+    return fail(ALPX_EINVAL, "%s: null buffer", what);
+  if (!dtype_ok(dtype)) return fail(ALPX_EINVAL, "%s: unknown dtype", what);
+  if (tokens <= 0 || q_heads <= 0 || kv_heads <= 0 || head_dim <= 0 || max_pages <= 0 ||
+      num_pages <= 0 || batch_index < 0)
+    return fail(ALPX_EINVAL, "%s: sizes must be positive", what);
+  if (page_size < 64 || (page_size & (page_size - 1)) != 0)
+    return fail(ALPX_EINVAL, "%s: page_size must be a power of two >= 64", what);
+  if (position < 0 || position + tokens > (int64_t)max_pages * page_size)
+    return fail(ALPX_ERANGE, "attention cache position exceeds capacity");
+  if (!(scale > 0.0f) || !isfinite(scale))
+    return fail(ALPX_EINVAL, "attention scale must be positive and finite");
+  // Everything the two launches check, first: a failing call writes no page.
+  int R = 0;
+  if (bad_sections(sections, R) || R % 32 != 0 || 2 * R > head_dim ||
+      !(frequency_base > 0.0) || !isfinite(frequency_base))
+    return fail(ALPX_EUNSUPPORTED,
+                "%s: needs rotary sections summing to a multiple of 32 (at most head_dim / 2) "
+                "and a valid frequency base", what);
+  const size_t es = dtype_size(dtype);
+  const int64_t row = (int64_t)kv_heads * head_dim;
+  const uintptr_t align = (uintptr_t)query_gate | (uintptr_t)key_pages | (uintptr_t)value_pages |
+                          (uintptr_t)q_norm | (uintptr_t)(row * es) |
+                          (uintptr_t)(2 * head_dim * es);
+  if (!((dtype == ALPX_F16 || dtype == ALPX_BF16) &&
+        (head_dim == 64 || head_dim == 128 || head_dim == 256) && (align & 15) == 0 &&
+        getenv("ALPX_PREFILL_GENERIC") == nullptr && position < ((int64_t)1 << 30) &&
+        (position + tokens) * row * (int64_t)es < ((int64_t)1 << 31)))
+    return fail(ALPX_EUNSUPPORTED,
+                "%s: needs fp16/bf16 pages, head_dim in {64, 128, 256}, 16-byte aligned rows and "
+                "q_norm, and under 2 GiB of logical rows", what);
+  const size_t need = (size_t)tokens * R * sizeof(float2);
+  if (!workspace || workspace_bytes < need)
+    return fail(ALPX_EINVAL, "%s: workspace of %zu bytes, %zu needed", what,
+                workspace ? workspace_bytes : (size_t)0, need);
+  const int page_shift = __builtin_ctz((unsigned)page_size);
+  const int32_t* table = block_table + (int64_t)batch_index * max_pages;
+  QueryPrologue qp = {};
+  qp.qw = q_norm;
+  qp.rot = (const float2*)workspace;
+  qp.eps = eps;
+  qp.R = R;
+  const int rc = attention_prologue_chunk_kv(
+      query_gate, key, value, q_norm, k_norm, key_pages, value_pages, dtype,
+      (int64_t)max_pages * page_size, 1, 0, tokens, q_heads, kv_heads, head_dim, head_dim,
+      position, sections, frequency_base, eps, (float2*)workspace, stream, table, page_shift,
+      num_pages);
+  if (rc != ALPX_OK) return rc;
+  return prefill_impl(query_gate, key_pages, value_pages, (const char*)query_gate + head_dim * es,
+                      out, nullptr, 0, tokens, (int)(position + tokens), q_heads, kv_heads,
+                      head_dim, head_dim, row, row, position, 0, 0, scale, dtype, dtype, stream,
+                      table, page_shift, num_pages, nullptr, nullptr, 2 * (int64_t)head_dim, &qp);
+}
+
 extern "C" int alpx_prefill_causal_paged(const void* q, const void* key_pages,
                                          const void* value_pages, const int32_t* block_table,
                                          int max_pages, int page_size, int num_pages,

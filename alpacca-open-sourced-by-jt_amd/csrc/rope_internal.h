@@ -99,13 +99,18 @@ __device__ __forceinline__ void norm_rope(float (&x)[kPer], const float (&wt)[kP
 void inverse_frequencies(double* inv, int R, double base, double scale);
 // The attention chunk prologue's key / value heads only (layer.hip), and
 // rot_out [tokens, R] = the (cos, sin) of each token's rotary pairs: the
-// caller forms the query rows itself with the same arithmetic.
+// caller forms the query rows itself with the same arithmetic.  With a
+// table (the sequence's block-table row), the caches are page pools
+// [num_pages, 2^page_shift, Hkv, D], capacity = max_pages << page_shift,
+// cache_batch 1 and batch_index 0.
 int attention_prologue_chunk_kv(const void* query_gate, const void* key, const void* value,
                                 const float* q_norm, const float* k_norm, void* key_cache,
                                 void* value_cache, int dtype, int64_t capacity, int cache_batch,
                                 int batch_index, int tokens, int q_heads, int kv_heads,
                                 int head_dim, int value_dim, int64_t position, const int* sections,
-                                double frequency_base, float eps, float2* rot_out, void* stream);
+                                double frequency_base, float eps, float2* rot_out, void* stream,
+                                const int32_t* table = nullptr, int page_shift = 0,
+                                int num_pages = 0);
 // R = the sum of the four IMROPE sections; true when they are unusable.
 bool bad_sections(const int* sections, int& R);
 

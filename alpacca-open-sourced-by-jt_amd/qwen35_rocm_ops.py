@@ -917,6 +917,71 @@ class Qwen35RocmOps:
                                  seq_lens=seq_lens, gate=gate, scale=scale_value,
                                  out_dtype=out_dtype)
 
+    def paged_attention_layer_prefill_(self, query_gate: Any, key: Any, value: Any,
+                                       query_norm: Any, key_norm: Any, key_pages: Any,
+                                       value_pages: Any, block_table: Any, *, position: int,
+                                       sections: Sequence[int], frequency_base: float,
+                                       epsilon: float, batch_index: int = 0,
+                                       scale: float | None = None) -> tuple[Any, int]:
+        """``attention_layer_prefill_`` over a paged pool (extension): the
+        ``T`` tokens of sequence ``batch_index`` at logical rows
+        ``position .. position + T - 1`` (through ``block_table``), with the
+        same prologue arithmetic and prefill kernel as the contiguous chunk,
+        so the same rows give its bits.  A table entry outside the pool
+        writes no row.  fp16 / bf16 pages with equal key and value widths of
+        64, 128 or 256, pages of a power-of-two size >= 64 rows, rotary
+        sections summing to a multiple of 32.  Returns ``(gated output
+        [T, Hq, D], position + T)``."""
+        key_pages, value_pages = self._paged(key_pages, value_pages, block_table)
+        num_pages, size, kv_heads, width = _shape(key_pages)
+        batch, max_pages = (int(x) for x in block_table.shape)
+        if (key_pages.dtype not in (self.torch.float16, self.torch.bfloat16)
+                or int(value_pages.shape[3]) != width or width not in (64, 128, 256)):
+            raise ValueError("paged attention layer prefill needs fp16/bf16 pages with equal key "
+                             "and value widths of 64, 128 or 256")
+        if size < 64 or size & (size - 1):
+            raise ValueError("paged attention layer prefill needs pages of a power-of-two size "
+                             ">= 64 rows")
+        query_gate = self._tensor(query_gate, "joint Q/gate projection", dimensions=2)
+        key = self._tensor(key, "attention key", dimensions=2)
+        value = self._tensor(value, "attention value", dimensions=2)
+        query_norm = self._fp32(query_norm, "query RMSNorm weight", dimensions=1)
+        key_norm = self._fp32(key_norm, "key RMSNorm weight", dimensions=1)
+        position = _nonnegative_integer("attention cache position", position)
+        batch_index = _nonnegative_integer("batch_index", batch_index)
+        tokens = int(query_gate.shape[0])
+        if tokens <= 0:
+            raise ValueError("prefill chunk must hold at least one token")
+        if batch_index >= batch:
+            raise ValueError("batch_index exceeds the block table")
+        if position + tokens > max_pages * size:
+            raise ValueError("attention cache position exceeds capacity")
+        if int(query_gate.shape[1]) % (2 * width):
+            raise ValueError("joint Q/gate projection does not match the page head width")
+        query_heads = int(query_gate.shape[1]) // (2 * width)
+        if query_heads % kv_heads:
+            raise ValueError("attention query heads must be a multiple of KV heads")
+        if _shape(key) != (tokens, kv_heads * width) or _shape(value) != (tokens,
+                                                                           kv_heads * width):
+            raise ValueError("attention key/value do not match the page token shape")
+        if _shape(query_norm) != (width,) or _shape(key_norm) != (width,):
+            raise ValueError("RMSNorm weight must match the head dimension")
+        self._same_dtype("paged attention prefill", query_gate, key, value, key_pages)
+        if len(sections) != 4:
+            raise ValueError("IMRoPE requires four sections")
+        section = tuple(_nonnegative_integer("IMRoPE section", item) for item in sections)
+        if sum(section) % 32 or 2 * sum(section) > width:
+            raise ValueError("paged attention layer prefill needs rotary sections summing to a "
+                             "multiple of 32, at most half the head width")
+        scale_value = (1.0 / math.sqrt(width) if scale is None
+                       else _positive_finite("attention scale", scale))
+        gated = _ops.attention_layer_prefill_paged(
+            query_gate.reshape(tokens, query_heads, 2 * width), key, value, query_norm, key_norm,
+            key_pages, value_pages, block_table, batch_index=batch_index, position=position,
+            sections=section, frequency_base=_positive_finite("frequency_base", frequency_base),
+            eps=_positive_finite("epsilon", epsilon), scale=scale_value)
+        return gated, position + tokens
+
     def paged_attention_layer_step_(self, query_gate: Any, key: Any, value: Any,
                                     query_norm: Any, key_norm: Any, key_pages: Any,
                                     value_pages: Any, block_table: Any, *, position: int,

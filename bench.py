@@ -515,7 +515,8 @@ def bench_layer_prefill(torch, ops, lib, *, steps, warmup, seed=7):
       4096-row cache -- chunk prologue + causal prefill + sigmoid gate.
       Timed in both forms: the query heads normed and rotated inside the
       prefill's query load (chunk_ms), and through a query buffer
-      (query_buffer_chunk_ms).
+      (query_buffer_chunk_ms); and over a pool of 256-row pages in shuffled
+      order (paged_256_rows_chunk_ms).
       FLOPs count causal-valid pairs (4 D Hq per pair).  Token path: 2048
       attention-layer decode steps (prologue in the split-K launch, gated
       combine).
@@ -547,6 +548,21 @@ def bench_layer_prefill(torch, ops, lib, *, steps, warmup, seed=7):
         qg3, kn, vn, qw, kw, K, V, batch_index=0, position=prefix, sections=sec,
         frequency_base=base, eps=eps, fused_query=False)
     qb_ms = _timed_steps(torch, qbuf, max(10, steps // 2), 2)
+    # the same chunk over a pool of 256-row pages in shuffled order
+    import numpy as np
+    page = 256
+    npg = (prefix + T) // page
+    perm = torch.from_numpy(np.random.default_rng(seed).permutation(npg).astype(np.int32))
+    table = perm.to(dev).reshape(1, npg)
+    kp = torch.empty((npg, page, hkv, d), dtype=bf, device=dev)
+    vp = torch.empty_like(kp)
+    kp[perm.long().to(dev)] = K.reshape(npg, page, hkv, d)
+    vp[perm.long().to(dev)] = V.reshape(npg, page, hkv, d)
+    pchunk = lambda: ops.paged_attention_layer_prefill_(  # noqa: E731
+        qg, kn, vn, qw, kw, kp, vp, table, position=prefix, sections=sec, frequency_base=base,
+        epsilon=eps)
+    _warm(torch, pchunk, 0.1)
+    pg_ms = _timed_steps(torch, pchunk, max(10, steps // 2), 2)
 
     def tokens_attn():
         for t in range(T):
@@ -586,6 +602,7 @@ def bench_layer_prefill(torch, ops, lib, *, steps, warmup, seed=7):
     return {
         "attention_layer_prefill_qwen35_2k_on_2k": {
             "chunk_ms": round(a_ms, 4), "query_buffer_chunk_ms": round(qb_ms, 4),
+            "paged_256_rows_chunk_ms": round(pg_ms, 4),
             "token_path_ms": round(at_ms, 3), "speedup": round(at_ms / a_ms, 1), "flops": a_flops,
             "chunk_tflops": round(a_flops / (a_ms * 1e-3) / 1e12, 1)},
         "recurrent_layer_prefill_c5_1024": {

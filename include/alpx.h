@@ -556,6 +556,30 @@ int alpx_attention_layer_prefill(const void* query_gate, const void* key, const 
                                  const int* sections, double frequency_base, float eps,
                                  float scale, void* stream);
 
+/* alpx_attention_layer_prefill over a paged pool (the form without a query
+ * buffer): the key / value rows of the chunk's T tokens land at logical
+ * rows position .. position + T - 1 of sequence batch_index, i.e. row
+ * pos % page_size of page block_table[batch_index][pos / page_size] of
+ * key_pages / value_pages [num_pages, page_size, Hkv, D] (a table entry
+ * outside [0, num_pages) writes no row; the prefill's reads clamp it into
+ * the pool, as alpx_prefill_causal_paged does), then the gated causal
+ * prefill runs over logical rows 0 .. position + t, forming the query
+ * heads from query_gate itself.  Same kernels and arithmetic as the
+ * contiguous call, so the same rows give the same bits.  fp16 / bf16,
+ * head_dim 64, 128 or 256, rotary sections summing to a multiple of 32
+ * (at most head_dim / 2), page_size a power of two >= 64, out in dtype;
+ * workspace: tokens x R x 8 bytes (R = the section sum).  Every check
+ * runs before the first launch. */
+int alpx_attention_layer_prefill_paged(const void* query_gate, const void* key,
+                                       const void* value, const float* q_norm,
+                                       const float* k_norm, void* key_pages, void* value_pages,
+                                       const int32_t* block_table, int max_pages, int page_size,
+                                       int num_pages, int batch_index, void* out, void* workspace,
+                                       size_t workspace_bytes, int dtype, int tokens, int q_heads,
+                                       int kv_heads, int head_dim, int64_t position,
+                                       const int* sections, double frequency_base, float eps,
+                                       float scale, void* stream);
+
 /* Qwen3.5 recurrent-layer inputs for a prefill chunk of one sequence: the
  * depthwise causal convolution + SiLU of current [T, C] (C = 2 Hk Dk +
  * Hv Dv; weights strided as alpx_conv_step) continuing conv_history

@@ -133,6 +133,17 @@ def test_layer_prefill_without_query_buffer_refusals_without_gpu(pkg):
     assert "16384 needed" in L.last_error()
     assert call(L.BF16, sec, ws=None) == L.EINVAL and "workspace" in L.last_error()
 
+    def paged(dtype, sections, page=64, position=0, ws_bytes=1 << 20, head_dim=128):
+        return lib.alpx_attention_layer_prefill_paged(
+            fake, fake, fake, fake, fake, fake, fake, fake, 4, page, 8, 0, fake, fake, ws_bytes,
+            dtype, 64, 16, 2, head_dim, position, sections, 1e7, 1e-6, 0.0625, None)
+
+    assert paged(L.BF16, sec, page=32) == L.EINVAL and "power of two" in L.last_error()
+    assert paged(L.BF16, sec, position=200) == L.ERANGE and "capacity" in L.last_error()
+    assert paged(L.F32, sec) == L.EUNSUPPORTED and "fp16/bf16" in L.last_error()
+    assert paged(L.BF16, odd) == L.EUNSUPPORTED and "multiple of 32" in L.last_error()
+    assert paged(L.BF16, sec, ws_bytes=100) == L.EINVAL and "16384 needed" in L.last_error()
+
 
 def test_layer_entry_points_validate_without_gpu(pkg):
     lib = pkg._lib.lib()

@@ -290,3 +290,85 @@ def test_paged_layer_step_rejects_unsupported(gpu, ops):
         ops.paged_attention_layer_step_(*args2, pw2.key_pages, pw2.value_pages, table,
                                         position=256, sections=(4, 4, 2, 0),
                                         frequency_base=1e7, epsilon=1e-6)
+
+
+@pytest.mark.parametrize("dtype,d,page,hq,hkv,b,bi,cap,prefix,tokens,sections", [
+    ("bf16", 256, 64, 16, 2, 2, 1, 1024, 300, 130, (11, 11, 10, 0)),   # Qwen3.5 heads
+    ("f16", 128, 128, 8, 2, 1, 0, 512, 0, 70, (16, 16, 16, 16)),       # empty prefix, 2 R = D
+    ("bf16", 64, 64, 4, 2, 3, 2, 256, 100, 45, (8, 8, 8, 8)),          # third sequence
+    ("bf16", 128, 256, 32, 8, 1, 0, 4096, 2048, 2048, (11, 11, 10, 0)),  # C3-sized chunk
+])
+def test_paged_layer_prefill_equals_contiguous_bit_for_bit(gpu, ops, dtype, d, page, hq, hkv, b,
+                                                           bi, cap, prefix, tokens, sections):
+    """paged_attention_layer_prefill_ (alpx_attention_layer_prefill_paged:
+    the K/V chunk prologue writing through the block table, then the paged
+    gated prefill forming the query heads itself) against the contiguous
+    chunk on the same rows in a shuffled page pool: the same output bits and
+    the same rows written, for every sequence of the pool."""
+    import torch
+    rng = np.random.default_rng(d + page + prefix + tokens)
+    ws, pw, table, perm = _fill(torch, ops, gpu, rng, dtype, b, cap, hkv, d, page, None)
+    print(f"paged layer prefill {dtype} D={d} page={page} prefix={prefix} T={tokens}", flush=True)
+    args = _step_inputs(torch, rng, gpu, dtype, tokens, hq, hkv, d)
+    kw_args = dict(position=prefix, batch_index=bi, sections=sections, frequency_base=1e7,
+                   epsilon=1e-6)
+    out_c, n_c = ops.attention_layer_prefill_(*args, ws.key_cache, ws.value_cache, **kw_args)
+    out_p, n_p = ops.paged_attention_layer_prefill_(*args, pw.key_pages, pw.value_pages, table,
+                                                    **kw_args)
+    torch.cuda.synchronize()
+    assert n_c == n_p == prefix + tokens
+    assert torch.equal(out_p.view(torch.int16), out_c.view(torch.int16))
+    kc = ws.key_cache.view(torch.int16).cpu().numpy()
+    vc = ws.value_cache.view(torch.int16).cpu().numpy()
+    for bb in range(b):
+        assert np.array_equal(_pool_rows(torch, pw.key_pages, perm, bb, cap), kc[:, bb])
+        assert np.array_equal(_pool_rows(torch, pw.value_pages, perm, bb, cap), vc[:, bb])
+
+
+def test_paged_layer_prefill_skips_pages_outside_the_pool(gpu, ops):
+    """The chunk's rows on a page whose table entry lies outside
+    [0, num_pages) are not written: the pool page the valid table maps there
+    keeps its bits, and the chunk's other pages take the contiguous rows."""
+    import torch
+    rng = np.random.default_rng(11)
+    dtype, d, page, hq, hkv, b, cap, prefix, tokens = "bf16", 128, 64, 16, 4, 2, 512, 64, 256
+    ws, pw, table, perm = _fill(torch, ops, gpu, rng, dtype, b, cap, hkv, d, page, None)
+    bad = table.clone()
+    bad[1, 2] = -1                       # rows 128 .. 191 of sequence 1 (inside the chunk)
+    bad[1, 3] = pw.key_pages.shape[0]    # rows 192 .. 255, one past the pool
+    before_k = pw.key_pages.view(torch.int16).clone()
+    args = _step_inputs(torch, rng, gpu, dtype, tokens, hq, hkv, d)
+    kw_args = dict(position=prefix, batch_index=1, sections=(11, 11, 10, 0), frequency_base=1e7,
+                   epsilon=1e-6)
+    ops.paged_attention_layer_prefill_(*args, pw.key_pages, pw.value_pages, bad, **kw_args)
+    ops.attention_layer_prefill_(*args, ws.key_cache, ws.value_cache, **kw_args)
+    torch.cuda.synchronize()
+    after = pw.key_pages.view(torch.int16)
+    for lp in (2, 3):   # the pages the valid table maps there: untouched
+        assert torch.equal(after[int(perm[1, lp])], before_k[int(perm[1, lp])])
+    kc = ws.key_cache.view(torch.int16)
+    for lp in (1, 4):   # the chunk's other pages: the contiguous rows
+        assert torch.equal(after[int(perm[1, lp])], kc[lp * page:(lp + 1) * page, 1])
+    changed = (after != before_k).any(dim=(1, 2, 3)).nonzero().flatten().tolist()
+    assert sorted(changed) == sorted(int(perm[1, lp]) for lp in (1, 4))
+
+
+def test_paged_layer_prefill_rejects_unsupported(gpu, ops):
+    import torch
+    args = _step_inputs(torch, np.random.default_rng(3), gpu, "bf16", 8, 4, 2, 64)
+    pw = ops.initialize_paged_attention_workspace(num_pages=4, page_size=32, kv_heads=2,
+                                                  key_dimension=64, value_dimension=64,
+                                                  dtype=torch.bfloat16)
+    table = torch.zeros((1, 4), dtype=torch.int32, device=gpu)
+    kw = dict(position=0, sections=(11, 11, 10, 0), frequency_base=1e7, epsilon=1e-6)
+    with pytest.raises(ValueError, match="power-of-two size >= 64"):
+        ops.paged_attention_layer_prefill_(*args, pw.key_pages, pw.value_pages, table, **kw)
+    pw2 = ops.initialize_paged_attention_workspace(num_pages=4, page_size=64, kv_heads=2,
+                                                   key_dimension=64, value_dimension=64,
+                                                   dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="multiple of 32"):
+        ops.paged_attention_layer_prefill_(*args, pw2.key_pages, pw2.value_pages, table,
+                                           **dict(kw, sections=(10, 10, 10, 0)))
+    with pytest.raises(ValueError, match="exceeds capacity"):
+        ops.paged_attention_layer_prefill_(*args, pw2.key_pages, pw2.value_pages, table,
+                                           **dict(kw, position=250))
