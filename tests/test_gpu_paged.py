@@ -136,17 +136,20 @@ def test_paged_append_one_token_per_sequence_and_bad_arguments(gpu, ops):
         ops.paged_online_attention(q, pw.key_pages, pw.value_pages, table, length=129)
 
 
+@pytest.mark.parametrize("kind", ["single", "pair", "shared"])
 @pytest.mark.parametrize("dtype,d,page,hq,hkv,tq,prefix,gated", [
     ("bf16", 128, 64, 32, 8, 200, 300, False), ("f16", 256, 128, 16, 2, 130, 190, True),
     ("bf16", 64, 256, 8, 2, 70, 0, False), ("bf16", 256, 64, 16, 2, 64, 448, True)])
 def test_paged_prefill_equals_contiguous_bit_for_bit(gpu, ops, monkeypatch, dtype, d, page, hq,
-                                                     hkv, tq, prefix, gated):
+                                                     hkv, tq, prefix, gated, kind):
     """Causal prefill of one sequence's chunk over its pages (shuffled pool,
-    two sequences sharing it) returns the bytes of the contiguous prefill's
-    one-tile-per-block kernel (the kernel the paged path shares), with and
-    without the sigmoid gate, and matches the oracle."""
+    two sequences sharing it; the paged path runs the one-tile-per-block
+    kernel) returns the bytes of the contiguous prefill with each of its
+    kernels forced (one tile per block, paired light / heavy tiles, shared
+    tile stream: every kernel gives the same bits), with and without the
+    sigmoid gate, and matches the oracle."""
     import torch
-    monkeypatch.setenv("ALPX_PREFILL_KERNEL", "single")
+    monkeypatch.setenv("ALPX_PREFILL_KERNEL", kind)
     rng = np.random.default_rng(d + tq + page)
     batch = 2
     cap = ((prefix + tq + page - 1) // page) * page
