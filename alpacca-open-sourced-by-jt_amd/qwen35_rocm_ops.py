@@ -926,8 +926,9 @@ class Qwen35RocmOps:
         """``attention_layer_prefill_`` over a paged pool (extension): the
         ``T`` tokens of sequence ``batch_index`` at logical rows
         ``position .. position + T - 1`` (through ``block_table``), with the
-        same prologue arithmetic and prefill kernel as the contiguous chunk,
-        so the same rows give its bits.  A table entry outside the pool
+        contiguous chunk's prologue arithmetic and single-tile prefill
+        kernel: the same rows give its bits on that kernel (within rounding
+        of the paired kernel it may pick).  A table entry outside the pool
         writes no row.  fp16 / bf16 pages with equal key and value widths of
         64, 128 or 256, pages of a power-of-two size >= 64 rows, rotary
         sections summing to a multiple of 32.  Returns ``(gated output

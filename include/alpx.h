@@ -97,8 +97,9 @@ int alpx_kv_append_paged(void* key_pages, void* value_pages, const void* key, co
  * null = no gate) of q [q_tokens, Hq, D] at positions q_pos0 .. over the
  * first kv_tokens logical rows of sequence batch_index of a paged cache
  * (pages and block_table as above; page_size a power of two >= 64, so a
- * key tile never crosses a page).  Same kernel, tiling and arithmetic as
- * the contiguous call, so the same rows give the same bits.  fp16 / bf16
+ * key tile never crosses a page).  The contiguous call's single-tile
+ * kernel, tiling and arithmetic, so the same rows give its bits (and its
+ * shared-stream kernel's; its paired kernel agrees within rounding).  fp16 / bf16
  * pages, head_dim = value width in {64, 128, 256}, output in `dtype`
  * (others: ALPX_EUNSUPPORTED).  No workspace. */
 int alpx_prefill_causal_paged(const void* q, const void* key_pages, const void* value_pages,
@@ -564,8 +565,10 @@ int alpx_attention_layer_prefill(const void* query_gate, const void* key, const 
  * outside [0, num_pages) writes no row; the prefill's reads clamp it into
  * the pool, as alpx_prefill_causal_paged does), then the gated causal
  * prefill runs over logical rows 0 .. position + t, forming the query
- * heads from query_gate itself.  Same kernels and arithmetic as the
- * contiguous call, so the same rows give the same bits.  fp16 / bf16,
+ * heads from query_gate itself, on the prefill's single-tile kernel: the
+ * same rows give the bits of the contiguous call on that kernel (within
+ * rounding of its paired kernel, which splits a heavy tile's keys over two
+ * wave groups and merges them).  fp16 / bf16,
  * head_dim 64, 128 or 256, rotary sections summing to a multiple of 32
  * (at most head_dim / 2), page_size a power of two >= 64, out in dtype;
  * workspace: tokens x R x 8 bytes (R = the section sum).  Every check

@@ -136,7 +136,7 @@ def test_paged_append_one_token_per_sequence_and_bad_arguments(gpu, ops):
         ops.paged_online_attention(q, pw.key_pages, pw.value_pages, table, length=129)
 
 
-@pytest.mark.parametrize("kind", ["single", "pair", "shared"])
+@pytest.mark.parametrize("kind", ["single", "shared", "pair"])
 @pytest.mark.parametrize("dtype,d,page,hq,hkv,tq,prefix,gated", [
     ("bf16", 128, 64, 32, 8, 200, 300, False), ("f16", 256, 128, 16, 2, 130, 190, True),
     ("bf16", 64, 256, 8, 2, 70, 0, False), ("bf16", 256, 64, 16, 2, 64, 448, True)])
@@ -144,10 +144,11 @@ def test_paged_prefill_equals_contiguous_bit_for_bit(gpu, ops, monkeypatch, dtyp
                                                      hkv, tq, prefix, gated, kind):
     """Causal prefill of one sequence's chunk over its pages (shuffled pool,
     two sequences sharing it; the paged path runs the one-tile-per-block
-    kernel) returns the bytes of the contiguous prefill with each of its
-    kernels forced (one tile per block, paired light / heavy tiles, shared
-    tile stream: every kernel gives the same bits), with and without the
-    sigmoid gate, and matches the oracle."""
+    kernel) returns the bytes of the contiguous prefill's single-tile and
+    shared-stream kernels (the same arithmetic) and agrees within bf16 /
+    fp16 rounding with its paired kernel (a heavy tile's keys split over
+    two wave groups and merged), with and without the sigmoid gate, and
+    matches the oracle."""
     import torch
     monkeypatch.setenv("ALPX_PREFILL_KERNEL", kind)
     rng = np.random.default_rng(d + tq + page)
@@ -168,7 +169,10 @@ def test_paged_prefill_equals_contiguous_bit_for_bit(gpu, ops, monkeypatch, dtyp
                                           position=prefix, batch_index=bi, gate=gate)
         torch.cuda.synchronize()
         assert got.dtype == td and got.shape == (tq, hq, d)
-        assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), bi
+        if kind == "pair":
+            assert (got.float() - ref.float()).abs().max().item() <= 2e-2, bi
+        else:
+            assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), bi
         K = ws.key_cache[:prefix + tq, bi].float().cpu().numpy()
         V = ws.value_cache[:prefix + tq, bi].float().cpu().numpy()
         expect = A.full_attention_prefill(q.float().cpu().numpy(), K, V, prefix_length=prefix)
@@ -301,14 +305,17 @@ def test_paged_layer_step_rejects_unsupported(gpu, ops):
     ("bf16", 64, 64, 4, 2, 3, 2, 256, 100, 45, (8, 8, 8, 8)),          # third sequence
     ("bf16", 128, 256, 32, 8, 1, 0, 4096, 2048, 2048, (11, 11, 10, 0)),  # C3-sized chunk
 ])
-def test_paged_layer_prefill_equals_contiguous_bit_for_bit(gpu, ops, dtype, d, page, hq, hkv, b,
-                                                           bi, cap, prefix, tokens, sections):
+def test_paged_layer_prefill_equals_contiguous_bit_for_bit(gpu, ops, monkeypatch, dtype, d, page,
+                                                           hq, hkv, b, bi, cap, prefix, tokens,
+                                                           sections):
     """paged_attention_layer_prefill_ (alpx_attention_layer_prefill_paged:
     the K/V chunk prologue writing through the block table, then the paged
     gated prefill forming the query heads itself) against the contiguous
-    chunk on the same rows in a shuffled page pool: the same output bits and
-    the same rows written, for every sequence of the pool."""
+    chunk on the same rows in a shuffled page pool, with the contiguous
+    prefill on the single-tile kernel the paged one runs: the same output
+    bits and the same rows written, for every sequence of the pool."""
     import torch
+    monkeypatch.setenv("ALPX_PREFILL_KERNEL", "single")
     rng = np.random.default_rng(d + page + prefix + tokens)
     ws, pw, table, perm = _fill(torch, ops, gpu, rng, dtype, b, cap, hkv, d, page, None)
     print(f"paged layer prefill {dtype} D={d} page={page} prefix={prefix} T={tokens}", flush=True)
