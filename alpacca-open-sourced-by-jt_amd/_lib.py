@@ -85,6 +85,7 @@ SIGNATURES = {
     "alpx_gdn_step": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int,
                                _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_ptr]),
     "alpx_gdn_chunk_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int]),
+    "alpx_gdn_chunk_uses_mfma": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
     "alpx_gdn_chunk_prefill": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
                                         _c_ptr, _c_size, _c_int, _c_int, _c_int, _c_int, _c_int,
                                         _c_int, _c_int, _c_int, _c_ptr]),
@@ -136,6 +137,8 @@ SIGNATURES = {
                                      _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr,
                                      _c_ptr, _c_size, _c_int, _c_int, _c_int, _c_int, _c_int,
                                      _c_float, _c_int, _c_ptr]),
+    "alpx_set_override": (_c_int, [_c_int, _c_int]),
+    "alpx_get_override": (_c_int, [_c_int]),
     "alpx_timing_enable": (_c_int, [_c_int]),
     "alpx_timing_read": (_c_int, [_c_int, ctypes.POINTER(ctypes.c_double),
                                   ctypes.POINTER(ctypes.c_int64)]),
@@ -147,6 +150,28 @@ SIGNATURES = {
 
 # alpx_row_norm modes
 NORM_L2, NORM_RMS, NORM_RMS_GATE = 0, 1, 2
+
+# alpx_override ids and the ALPX_OVERRIDE_PREFILL_KERNEL values
+(OVERRIDE_DECODE_GENERIC, OVERRIDE_PREFILL_GENERIC, OVERRIDE_PREFILL_KERNEL,
+ OVERRIDE_GDN_SEQUENTIAL, OVERRIDE_RECURRENT_UNFUSED) = range(5)
+PREFILL_KERNELS = {"auto": 0, "single": 1, "pair": 2, "shared": 3}
+
+
+def set_override(which: int, value: int) -> int:
+    """Sets a kernel-choice override of the library (tests and A/B timing;
+    the library reads the environment only once, at load) and returns the
+    previous value."""
+    previous = lib().alpx_set_override(int(which), int(value))
+    if previous < 0:
+        check(previous)
+    return previous
+
+
+def get_override(which: int) -> int:
+    value = lib().alpx_get_override(int(which))
+    if value < 0:
+        check(value)
+    return value
 
 
 def timing_enable(on: bool) -> None:

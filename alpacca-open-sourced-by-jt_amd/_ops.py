@@ -9,7 +9,6 @@ in libalpx.so.  Nothing here computes on the CPU.
 from __future__ import annotations
 
 import math
-import os
 
 from . import _lib
 
@@ -103,21 +102,29 @@ def prefill_append(q, key, value, key_cache, value_cache, *, position, scale=Non
     out_dtype = q.dtype if out_dtype is None else out_dtype
     out = torch.empty((q_tokens, q_heads, value_dim), dtype=out_dtype, device=q.device)
     L = _lib.lib()
+    nbytes = L.alpx_prefill_workspace_bytes(q_tokens, q_heads, kv_heads, value_dim,
+                                            int(position) + q_tokens)
+    if nbytes == 0:
+        raise ValueError("invalid prefill sizes")
     fast = (q.dtype != torch.float32 and key_dim == value_dim and key_dim in (64, 128, 256))
-    ws = None
-    if not fast:
-        nbytes = L.alpx_prefill_workspace_bytes(q_tokens, q_heads, kv_heads, value_dim,
-                                                int(position) + q_tokens)
-        if nbytes == 0:
-            raise ValueError("invalid prefill sizes")
+    ws = None if fast else _lib.workspace(torch, q.device, nbytes)
+
+    def call(workspace):
+        return L.alpx_prefill_append(
+            q.data_ptr(), key.data_ptr(), value.data_ptr(), key_cache.data_ptr(),
+            value_cache.data_ptr(), None if gate is None else gate.data_ptr(), out.data_ptr(),
+            None if workspace is None else workspace.data_ptr(),
+            0 if workspace is None else workspace.numel(), q_tokens, capacity, q_heads, kv_heads,
+            key_dim, value_dim, int(position), int(window), float(scale),
+            _lib.dtype_code(torch, q.dtype), _lib.dtype_code(torch, out.dtype),
+            _lib.stream_handle(torch, q.device))
+
+    rc = call(ws)
+    # unaligned rows or a cache of 2 GiB or more leave the MFMA kernels; the
+    # split-K path refuses a null workspace before its append
+    if rc == _lib.EINVAL and ws is None:
         ws = _lib.workspace(torch, q.device, nbytes)
-    rc = L.alpx_prefill_append(
-        q.data_ptr(), key.data_ptr(), value.data_ptr(), key_cache.data_ptr(),
-        value_cache.data_ptr(), None if gate is None else gate.data_ptr(), out.data_ptr(),
-        None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), q_tokens,
-        capacity, q_heads, kv_heads, key_dim, value_dim, int(position), int(window),
-        float(scale), _lib.dtype_code(torch, q.dtype), _lib.dtype_code(torch, out.dtype),
-        _lib.stream_handle(torch, q.device))
+        rc = call(ws)
     _lib.check(rc)
     return out
 
@@ -335,13 +342,16 @@ def gdn_chunk(state, q, k, v, beta, log_decay, out_dtype=None):
     out = torch.empty((bsz, tokens, hv, dv), dtype=q.dtype if out_dtype is None else out_dtype,
                       device=state.device)
     L = _lib.lib()
-    nbytes = L.alpx_gdn_chunk_workspace_bytes(bsz, tokens, hv, dk)
-    ws = _lib.workspace(torch, state.device, nbytes)
+    dtype = _lib.dtype_code(torch, q.dtype)
+    ws = None
+    if L.alpx_gdn_chunk_uses_mfma(dtype, tokens, hk, hv, dk, dv):
+        ws = _lib.workspace(torch, state.device,
+                            L.alpx_gdn_chunk_workspace_bytes(bsz, tokens, hv, dk))
     rc = L.alpx_gdn_chunk_prefill(
         state.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(),
-        log_decay.data_ptr(), out.data_ptr(), ws.data_ptr(), ws.numel(), bsz, tokens, hk, hv,
-        dk, dv, _lib.dtype_code(torch, q.dtype), _lib.dtype_code(torch, out.dtype),
-        _lib.stream_handle(torch, state.device))
+        log_decay.data_ptr(), out.data_ptr(), None if ws is None else ws.data_ptr(),
+        0 if ws is None else ws.numel(), bsz, tokens, hk, hv, dk, dv, dtype,
+        _lib.dtype_code(torch, out.dtype), _lib.stream_handle(torch, state.device))
     _lib.check(rc)
     return out
 
@@ -627,30 +637,37 @@ def attention_layer_prefill(query_gate, key, value, q_norm, k_norm, key_cache, v
     L = _lib.lib()
     fast = key_cache.dtype != torch.float32 and dim in (64, 128, 256)
     pairs = sum(int(x) for x in sections)
-    if fused_query is None:
+    auto = fused_query is None
+    if auto:
         fused_query = (fast and pairs % 32 == 0 and 2 * pairs <= dim
-                       and os.environ.get("ALPX_PREFILL_GENERIC") is None)
-    query = None
-    ws = None
+                       and _lib.get_override(_lib.OVERRIDE_PREFILL_GENERIC) == 0)
+
+    def call(query, ws):
+        return L.alpx_attention_layer_prefill(
+            query_gate.data_ptr(), key.data_ptr(), value.data_ptr(), q_norm.data_ptr(),
+            k_norm.data_ptr(), None if query is None else query.data_ptr(),
+            key_cache.data_ptr(), value_cache.data_ptr(), out.data_ptr(),
+            None if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(),
+            _lib.dtype_code(torch, key_cache.dtype), _lib.dtype_code(torch, out.dtype), capacity,
+            cache_batch, int(batch_index), tokens, q_heads, kv_heads, dim, int(position),
+            _sections(sections), float(frequency_base), float(eps), float(scale),
+            _lib.stream_handle(torch, dev))
+
+    # Every refusal below comes before the library's first launch, so a
+    # refused form has written nothing and the next form may run.
     if fused_query:
-        ws = _lib.workspace(torch, dev, max(tokens * pairs * 8, 1))
-    else:
-        query = torch.empty((tokens, q_heads, dim), dtype=key_cache.dtype, device=dev)
-    if not fast:
+        rc = call(None, _lib.workspace(torch, dev, max(tokens * pairs * 8, 1)))
+        if not (auto and rc == _lib.EUNSUPPORTED):  # e.g. a cache of 2 GiB or more
+            _lib.check(rc)
+            return out
+    query = torch.empty((tokens, q_heads, dim), dtype=key_cache.dtype, device=dev)
+    rc = call(query, None)
+    if rc == _lib.EINVAL:  # the split-K prefill (fp32, unaligned, >= 2 GiB) needs a workspace
         nbytes = L.alpx_prefill_workspace_bytes(tokens, q_heads, kv_heads, dim,
                                                 int(position) + tokens)
         if nbytes == 0:
             raise ValueError("invalid prefill sizes")
-        ws = _lib.workspace(torch, dev, nbytes)
-    rc = L.alpx_attention_layer_prefill(
-        query_gate.data_ptr(), key.data_ptr(), value.data_ptr(), q_norm.data_ptr(),
-        k_norm.data_ptr(), None if query is None else query.data_ptr(), key_cache.data_ptr(),
-        value_cache.data_ptr(), out.data_ptr(), None if ws is None else ws.data_ptr(),
-        0 if ws is None else ws.numel(), _lib.dtype_code(torch, key_cache.dtype),
-        _lib.dtype_code(torch, out.dtype), capacity, cache_batch, int(batch_index), tokens,
-        q_heads, kv_heads, dim, int(position),
-        _sections(sections), float(frequency_base), float(eps), float(scale),
-        _lib.stream_handle(torch, dev))
+        rc = call(query, _lib.workspace(torch, dev, nbytes))
     _lib.check(rc)
     return out
 

@@ -116,4 +116,8 @@ inline bool dtype_ok(int dtype) {
 int fail(int status, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 int check_launch(const char* what);
 
+// Current value of kernel-choice override `which` (enum alpx_override):
+// the environment as read at load, or the last alpx_set_override.
+int override_value(int which);
+
 }  // namespace alpx

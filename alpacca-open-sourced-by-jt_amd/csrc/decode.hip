@@ -1076,7 +1076,7 @@ int run_decode(DecodeArgs a, int dtype, int out_dtype, void* workspace, size_t w
   const int64_t max_pos = a.ks_pos > a.vs_pos ? a.ks_pos : a.vs_pos;
   const bool mfma = D == a.value_dim && (D == 64 || D == 128 || D == 256) && (align & 15) == 0 &&
                     (int64_t)kTile * max_pos * (int64_t)es < ((int64_t)1 << 31) &&
-                    getenv("ALPX_DECODE_GENERIC") == nullptr;
+                    override_value(ALPX_OVERRIDE_DECODE_GENERIC) == 0;
   const size_t need = decode_workspace(a.batch, a.q_heads, a.kv_heads, a.value_dim, a.length);
   if (fixed_scratch == nullptr && workspace_bytes < need)
     return fail(ALPX_EINVAL, "decode workspace holds %zu bytes, needs %zu", workspace_bytes,

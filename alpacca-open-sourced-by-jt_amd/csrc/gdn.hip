@@ -37,6 +37,8 @@
 // beta = 0, g = 0, which leaves every real quantity unchanged.
 #include <math.h>
 
+#include <type_traits>
+
 #include "alpx_common.h"
 #include "gdn_internal.h"
 #include "timing.h"
@@ -177,24 +179,67 @@ gdn_step_kernel(GdnArgs a) {
 
 // ------------------------------------------------------------ helpers
 
-__device__ __forceinline__ void split8(const float* x, bf16x8& hi, bf16x8& lo) {
+// Operand planes.  An fp32 value x enters the bf16 MFMAs as N bf16 planes
+// p0 = bf16(x), p1 = bf16(x - p0), p2 = bf16(x - p0 - p1): two planes hold
+// x to about 2^-17 relative, three hold any fp32 value exactly (8 + 8 + 8
+// significant bits).  Plane n is about 2^-8n of x, so a product of planed
+// operands keeps the terms a_i b_j with i + j <= its order.
+template <int N>
+__device__ __forceinline__ void split_planes8(const float* x, bf16x8 (&p)[N]) {
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    const float v = x[j];
-    const bf16_t h = static_cast<bf16_t>(v);
-    hi[j] = h;
-    lo[j] = static_cast<bf16_t>(v - static_cast<float>(h));
+    float r = x[j];
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+      const bf16_t h = static_cast<bf16_t>(r);
+      p[n][j] = h;
+      if (n + 1 < N) r = r - static_cast<float>(h);
+    }
   }
 }
 
-__device__ __forceinline__ void split4(f32x4 x, bf16x4& hi, bf16x4& lo) {
+template <int N>
+__device__ __forceinline__ void split_planes4(f32x4 x, bf16x4 (&p)[N]) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const bf16_t h = static_cast<bf16_t>(x[j]);
-    hi[j] = h;
-    lo[j] = static_cast<bf16_t>(x[j] - static_cast<float>(h));
+    float r = x[j];
+#pragma unroll
+    for (int n = 0; n < N; ++n) {
+      const bf16_t h = static_cast<bf16_t>(r);
+      p[n][j] = h;
+      if (n + 1 < N) r = r - static_cast<float>(h);
+    }
   }
 }
+
+// acc + sum of a_i b_j over i + j <= ORD, accumulated in (i, j) order.
+template <int NA, int NB, int ORD>
+__device__ __forceinline__ f32x4 mfma_planes(const bf16x8 (&a)[NA], const bf16x8 (&b)[NB],
+                                             f32x4 acc) {
+#pragma unroll
+  for (int i = 0; i < NA; ++i)
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+      if (i + j <= ORD) acc = mfma16x16x32(a[i], b[j], acc);
+  return acc;
+}
+
+// Planes per operand by input type.  bf16 inputs (q, k, v) are one exact
+// plane and the fp32 quantities derived from them (state, P, W, X, Y) two,
+// products keeping the terms to order 1.  fp32 inputs take three planes
+// everywhere, products to order 2: in a CPU model of the kernels on the
+// Qwen3.5 recurrent-layer chain (small GDN outputs, formed with heavy
+// cancellation, then RMS-normalised) two planes left 1.3e-4 after the gated
+// norm against the fp64 chain, three planes 3e-5 (plain fp32 token by
+// token: 5e-6).
+template <typename TI>
+struct Planes {
+  static constexpr int in = 1, der = 2;
+};
+template <>
+struct Planes<float> {
+  static constexpr int in = 3, der = 3;
+};
 
 // Rows in the order the transposing LDS read delivers them: k-slot j of
 // lane group `quad` is row 16 (j / 4) + 4 quad + j % 4.
@@ -206,34 +251,42 @@ __device__ __forceinline__ void wave_sync_lds() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Per-chunk workspace (fp32 words), in order: Gc * log2(e) [kC], then the hi
-// and lo bf16 planes of P and of W [kC x kC each].  Both are causal (row t
-// is zero past column t), so of the eight 16 x 32 A-operand tiles (m tile
-// mt, k step ks) only the six with 32 ks <= 16 mt + 15 are stored, in the
-// order (0,0) (1,0) (2,0) (2,1) (3,0) (3,1).  Each tile is stored
+// Per-chunk workspace (fp32 words), in order: Gc * log2(e) [kC], then the NS
+// bf16 planes of P and the NS planes of W [kC x kC each].  Both are causal
+// (row t is zero past column t), so of the eight 16 x 32 A-operand tiles (m
+// tile mt, k step ks) only the six with 32 ks <= 16 mt + 15 are stored, in
+// the order (0,0) (1,0) (2,0) (2,1) (3,0) (3,1).  Each tile is stored
 // fragment-major: lane 16 quad + i holds row 16 mt + i, columns
 // 32 ks + 8 quad + 0..7, as 16 contiguous bytes, and the 64 lanes follow
 // each other, so a wave's operand load is one contiguous 1 KiB access.
 constexpr int kTiles = 6;
 constexpr int kTileElems = 64 * 8;
-__host__ __device__ inline int64_t ws_per_chunk() { return kC + 4 * kTiles * kTileElems / 2; }
+template <int NS>
+__host__ __device__ constexpr int64_t ws_per_chunk() {
+  return kC + 2 * NS * kTiles * kTileElems / 2;
+}
 __device__ __forceinline__ int tile_slot(int mt, int ks) { return mt < 2 ? mt : 2 * mt - 2 + ks; }
 // Whether A-operand tile (mt, ks) of a causal kC x kC matrix is stored.
 __device__ __forceinline__ bool tile_live(int mt, int ks) { return ks == 0 || mt >= 2; }
 
+template <int NS>
 struct ChunkWs {
   float* g;
-  bf16_t *p_hi, *p_lo, *w_hi, *w_lo;
+  bf16_t* p[NS];
+  bf16_t* w[NS];
 };
 
-__device__ __forceinline__ ChunkWs chunk_ws(float* base) {
-  ChunkWs w;
-  w.g = base;
-  w.p_hi = (bf16_t*)(base + kC);
-  w.p_lo = w.p_hi + kTiles * kTileElems;
-  w.w_hi = w.p_lo + kTiles * kTileElems;
-  w.w_lo = w.w_hi + kTiles * kTileElems;
-  return w;
+template <int NS>
+__device__ __forceinline__ ChunkWs<NS> chunk_ws(float* base) {
+  ChunkWs<NS> c;
+  c.g = base;
+  bf16_t* const planes = (bf16_t*)(base + kC);
+#pragma unroll
+  for (int n = 0; n < NS; ++n) {
+    c.p[n] = planes + n * kTiles * kTileElems;
+    c.w[n] = planes + (NS + n) * kTiles * kTileElems;
+  }
+  return c;
 }
 
 // Element offset of `lane`'s 16 bytes in stored tile (mt, ks).
@@ -245,18 +298,23 @@ __device__ __forceinline__ int tile_off(int mt, int ks, int lane) {
 
 // NG value heads of one key head per block (the value heads h with
 // h % Hk = kh share K and Q): four waves per value head, one load of the
-// chunk's K and Q rows for all of them.
-template <int DK, int NG>
+// chunk's K and Q rows for all of them.  bf16 inputs: the K and Q rows are
+// staged in LDS as they are.  fp32 inputs: the K rows are staged as their
+// three planes and each wave reads its own Q rows from global memory as A
+// operands.
+template <typename TI, int DK, int NG>
 __global__ void __launch_bounds__(256 * NG)
 gdn_prep(GdnArgs a) {
+  constexpr bool F32IN = std::is_same<TI, float>::value;
+  constexpr int NI = Planes<TI>::in, NS = Planes<TI>::der, ORD = NS - 1;
   constexpr int kS = DK + 8;   // bf16 LDS row stride
   constexpr int kF = kC + 4;   // fp32 LDS row stride
   constexpr int KS = DK / 32;
   constexpr int kUnits = DK / 8;
   constexpr int kUPT = kC * kUnits / (256 * NG);
   static_assert(kUPT * 256 * NG == kC * kUnits, "K / Q rows must split evenly over the block");
-  __shared__ __attribute__((aligned(16))) bf16_t Ks[kC * kS];
-  __shared__ __attribute__((aligned(16))) bf16_t Qs[kC * kS];
+  __shared__ __attribute__((aligned(16))) bf16_t Ks[NI][kC * kS];             // K rows
+  __shared__ __attribute__((aligned(16))) bf16_t Qs[F32IN ? 8 : kC * kS];     // Q rows
   // Per value head: diag(beta) A, then (per wave, its own 16 rows) M, P and
   // a staging tile; T; the block-recursion exchange; Gc; beta.
   __shared__ __attribute__((aligned(16))) float Bm_[NG][kC * kF];
@@ -282,14 +340,37 @@ gdn_prep(GdnArgs a) {
   // K, Q rows of the chunk, g and beta: every load reads a clamped row and
   // is issued before any is used, so they are all in flight together; rows
   // past the end are zeroed when stored.
-  bf16x8 kv[kUPT], qv[kUPT];
+  bf16x8 kv[F32IN ? 1 : kUPT], qv[F32IN ? 1 : kUPT];
+  f32x4 kf[F32IN ? kUPT : 1][2], qf[F32IN ? KS : 1][2];
+  if constexpr (F32IN) {
 #pragma unroll
-  for (int u = 0; u < kUPT; ++u) {
-    const int idx = u * 256 * NG + gtid;
-    const int r = idx / kUnits, cc = idx - (idx / kUnits) * kUnits;
-    const int64_t off = (((int64_t)b * a.T + min(t0 + r, a.T - 1)) * a.Hk + kh) * DK + 8 * cc;
-    kv[u] = *(const bf16x8*)((const bf16_t*)a.k + off);
-    qv[u] = *(const bf16x8*)((const bf16_t*)a.q + off);
+    for (int u = 0; u < kUPT; ++u) {
+      const int idx = u * 256 * NG + gtid;
+      const int r = idx / kUnits, cc = idx - (idx / kUnits) * kUnits;
+      const float* p =
+          (const float*)a.k + (((int64_t)b * a.T + min(t0 + r, a.T - 1)) * a.Hk + kh) * DK + 8 * cc;
+      kf[u][0] = *(const f32x4*)p;
+      kf[u][1] = *(const f32x4*)(p + 4);
+    }
+    // this wave's Q rows in A-operand order: row 16 wave + hl, columns
+    // 32 ks + 8 quad + 0..7
+    const float* p = (const float*)a.q +
+                     (((int64_t)b * a.T + min(t0 + 16 * wave + hl, a.T - 1)) * a.Hk + kh) * DK +
+                     8 * quad;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      qf[ks][0] = *(const f32x4*)(p + 32 * ks);
+      qf[ks][1] = *(const f32x4*)(p + 32 * ks + 4);
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < kUPT; ++u) {
+      const int idx = u * 256 * NG + gtid;
+      const int r = idx / kUnits, cc = idx - (idx / kUnits) * kUnits;
+      const int64_t off = (((int64_t)b * a.T + min(t0 + r, a.T - 1)) * a.Hk + kh) * DK + 8 * cc;
+      kv[u] = *(const bf16x8*)((const bf16_t*)a.k + off);
+      qv[u] = *(const bf16x8*)((const bf16_t*)a.q + off);
+    }
   }
   const bool tok_ok = t0 + lane < a.T;
   const int64_t goff = ((int64_t)b * a.T + min(t0 + lane, a.T - 1)) * a.Hv + h;
@@ -308,8 +389,17 @@ gdn_prep(GdnArgs a) {
     const int idx = u * 256 * NG + gtid;
     const int r = idx / kUnits, cc = idx - (idx / kUnits) * kUnits;
     const bool ok = t0 + r < a.T;
-    *(bf16x8*)(Ks + r * kS + 8 * cc) = ok ? kv[u] : zero8;
-    *(bf16x8*)(Qs + r * kS + 8 * cc) = ok ? qv[u] : zero8;
+    if constexpr (F32IN) {
+      const float x[8] = {kf[u][0][0], kf[u][0][1], kf[u][0][2], kf[u][0][3],
+                          kf[u][1][0], kf[u][1][1], kf[u][1][2], kf[u][1][3]};
+      bf16x8 pl[NI];
+      split_planes8<NI>(x, pl);
+#pragma unroll
+      for (int n = 0; n < NI; ++n) *(bf16x8*)(Ks[n] + r * kS + 8 * cc) = ok ? pl[n] : zero8;
+    } else {
+      *(bf16x8*)(Ks[0] + r * kS + 8 * cc) = ok ? kv[u] : zero8;
+      *(bf16x8*)(Qs + r * kS + 8 * cc) = ok ? qv[u] : zero8;
+    }
   }
   if (wave == 0) {
     float gv = tok_ok ? graw : 0.f;
@@ -323,7 +413,8 @@ gdn_prep(GdnArgs a) {
   }
   __syncthreads();
 
-  const ChunkWs out = chunk_ws(a.ws + (((int64_t)b * a.Hv + h) * a.nchunks + c) * ws_per_chunk());
+  const ChunkWs<NS> out =
+      chunk_ws<NS>(a.ws + (((int64_t)b * a.Hv + h) * a.nchunks + c) * ws_per_chunk<NS>());
   if (tid < kC) out.g[tid] = Gs[tid] * kLog2e;
 
   // Bm = diag(beta) (exp(Gc_t - Gc_i) k_t.k_i)_{i<t} and
@@ -334,15 +425,32 @@ gdn_prep(GdnArgs a) {
     f32x4 kk[4];
 #pragma unroll
     for (int ib = 0; ib < 4; ++ib) kk[ib] = mq[ib] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    const bool qok = t0 + 16 * wave + hl < a.T;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      const bf16x8 ka = *(const bf16x8*)(Ks + (16 * wave + hl) * kS + 32 * ks + 8 * quad);
-      const bf16x8 qa = *(const bf16x8*)(Qs + (16 * wave + hl) * kS + 32 * ks + 8 * quad);
+      bf16x8 ka[NI], qa[NI];
+#pragma unroll
+      for (int n = 0; n < NI; ++n)
+        ka[n] = *(const bf16x8*)(Ks[n] + (16 * wave + hl) * kS + 32 * ks + 8 * quad);
+      if constexpr (F32IN) {
+        float x[8];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          x[j] = qok ? qf[ks][0][j] : 0.f;
+          x[4 + j] = qok ? qf[ks][1][j] : 0.f;
+        }
+        split_planes8<NI>(x, qa);
+      } else {
+        qa[0] = *(const bf16x8*)(Qs + (16 * wave + hl) * kS + 32 * ks + 8 * quad);
+      }
 #pragma unroll
       for (int ib = 0; ib < 4; ++ib) {
-        const bf16x8 kb = *(const bf16x8*)(Ks + (16 * ib + hl) * kS + 32 * ks + 8 * quad);
-        kk[ib] = mfma16x16x32(ka, kb, kk[ib]);
-        mq[ib] = mfma16x16x32(qa, kb, mq[ib]);
+        bf16x8 kb[NI];
+#pragma unroll
+        for (int n = 0; n < NI; ++n)
+          kb[n] = *(const bf16x8*)(Ks[n] + (16 * ib + hl) * kS + 32 * ks + 8 * quad);
+        kk[ib] = mfma_planes<NI, NI, ORD>(ka, kb, kk[ib]);
+        mq[ib] = mfma_planes<NI, NI, ORD>(qa, kb, mq[ib]);
       }
     }
     // Decays and masks as selects over values already in registers (Gc is
@@ -441,11 +549,12 @@ gdn_prep(GdnArgs a) {
           x[j] = rowf * x0[j] * b0[j];
           x[4 + j] = rowf * x1[j] * b1[j];
         }
-        bf16x8 hi, lo;
-        split8(x, hi, lo);
+        bf16x8 pl[NS];
+        split_planes8<NS>(x, pl);
         const int o = tile_off(wave, ks, lane);
-        __builtin_nontemporal_store(__builtin_bit_cast(u32x4, hi), (u32x4*)(out.w_hi + o));
-        __builtin_nontemporal_store(__builtin_bit_cast(u32x4, lo), (u32x4*)(out.w_lo + o));
+#pragma unroll
+        for (int n = 0; n < NS; ++n)
+          __builtin_nontemporal_store(__builtin_bit_cast(u32x4, pl[n]), (u32x4*)(out.w[n] + o));
       }
     }
   }
@@ -481,17 +590,15 @@ gdn_prep(GdnArgs a) {
       const f32x4 m0 = *(const f32x4*)(Mw + hl * kF + 32 * ks + 4 * quad);
       const f32x4 m1 = *(const f32x4*)(Mw + hl * kF + 32 * ks + 16 + 4 * quad);
       const float mrow[8] = {m0[0], m0[1], m0[2], m0[3], m1[0], m1[1], m1[2], m1[3]};
-      bf16x8 mh, ml;
-      split8(mrow, mh, ml);
+      bf16x8 mp[NS];
+      split_planes8<NS>(mrow, mp);
       if (ks == 0 || wave >= 2) {
 #pragma unroll
         for (int nt = 0; nt < 4; ++nt) {
           if (ks == 1 || nt < 2) {
-            bf16x8 th, tl;
-            split8(tc[nt][ks], th, tl);
-            pacc[nt] = mfma16x16x32(mh, th, pacc[nt]);
-            pacc[nt] = mfma16x16x32(mh, tl, pacc[nt]);
-            pacc[nt] = mfma16x16x32(ml, th, pacc[nt]);
+            bf16x8 tp[NS];
+            split_planes8<NS>(tc[nt][ks], tp);
+            pacc[nt] = mfma_planes<NS, NS, ORD>(mp, tp, pacc[nt]);
           }
         }
       }
@@ -504,7 +611,7 @@ gdn_prep(GdnArgs a) {
       for (int e = 0; e < 4; ++e) Mw[(4 * quad + e) * kF + 16 * nt + hl] = f * pacc[nt][e];
     }
     wave_sync_lds();
-    // P as hi / lo fragments: the wave's live tiles, one unit per lane each.
+    // P as planed fragments: the wave's live tiles, one unit per lane each.
     // Workspace stores are nontemporal: every block writes its fragments at
     // about the same late point, and streaming them out rather than leaving
     // them dirty in L2 shortens the drain at the end of the kernel.
@@ -514,11 +621,12 @@ gdn_prep(GdnArgs a) {
         const f32x4 x0 = *(const f32x4*)(Mw + hl * kF + 32 * ks + 8 * quad);
         const f32x4 x1 = *(const f32x4*)(Mw + hl * kF + 32 * ks + 8 * quad + 4);
         const float x[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-        bf16x8 hi, lo;
-        split8(x, hi, lo);
+        bf16x8 pl[NS];
+        split_planes8<NS>(x, pl);
         const int o = tile_off(wave, ks, lane);
-        __builtin_nontemporal_store(__builtin_bit_cast(u32x4, hi), (u32x4*)(out.p_hi + o));
-        __builtin_nontemporal_store(__builtin_bit_cast(u32x4, lo), (u32x4*)(out.p_lo + o));
+#pragma unroll
+        for (int n = 0; n < NS; ++n)
+          __builtin_nontemporal_store(__builtin_bit_cast(u32x4, pl[n]), (u32x4*)(out.p[n] + o));
       }
     }
   }
@@ -544,25 +652,54 @@ __device__ __forceinline__ void apply_block(const GdnArgs& a, int& slice, int& h
 // Global inputs of one chunk, in three groups: what the K S^T / Q S^T step
 // reads as A operands (K and Q rows of the lane's token), the P and W
 // fragments of the wave's token rows, and the V rows and decays that waves
-// 0..2 stage in LDS for everyone.
-template <int DK>
+// 0..2 stage in LDS for everyone.  fp32 inputs keep the loaded fp32 values
+// until their use, where they are split into planes.
+template <typename TI, int DK>
 struct KqIn {
   bf16x8 k[DK / 32], q[DK / 32];
 };
-struct PwIn {
-  bf16x8 p_hi[2], p_lo[2], w_hi[2], w_lo[2];
+template <int DK>
+struct KqIn<float, DK> {
+  f32x4 k[DK / 16], q[DK / 16];  // 32 ks + 8 quad + 0..3 in [2 ks], + 4..7 in [2 ks + 1]
 };
+template <int NS>
+struct PwIn {
+  bf16x8 p[2][NS], w[2][NS];  // [k step][plane]
+};
+template <typename TI>
 struct VgIn {
   bf16x8 v;  // waves 0, 1: V[token tid / 2][16-column slice half tid % 2]
   f32x4 g;   // wave 2, lanes 0..15: Gc * log2(e) of tokens 4 lane .. 4 lane + 3
 };
+// fp32 V: one pair of registers holds either a wave's V halves (waves 0,
+// 1) or the decays (wave 2, in v[0]), so no field is chosen by a branch
+// (a branch-selected field is stored through a selected pointer, in
+// scratch memory).
+template <>
+struct VgIn<float> {
+  f32x4 v[2];
+};
+__device__ __forceinline__ f32x4& vg_decay(VgIn<bf16_t>& in) { return in.g; }
+__device__ __forceinline__ f32x4& vg_decay(VgIn<float>& in) { return in.v[0]; }
+__device__ __forceinline__ const f32x4& vg_decay(const VgIn<bf16_t>& in) { return in.g; }
+__device__ __forceinline__ const f32x4& vg_decay(const VgIn<float>& in) { return in.v[0]; }
 
-template <typename TO, int DK>
+// The planes of fp32 operand elements 8 j .. 8 j + 7 held as two f32x4.
+template <int N>
+__device__ __forceinline__ void split_pair(const f32x4& x0, const f32x4& x1, bf16x8 (&p)[N]) {
+  const float x[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+  split_planes8<N>(x, p);
+}
+
+template <typename TI, typename TO, int DK>
 __global__ void __launch_bounds__(256)
 gdn_apply(GdnArgs a) {
+  constexpr bool F32IN = std::is_same<TI, float>::value;
+  constexpr int NI = Planes<TI>::in, NS = Planes<TI>::der, ORD = NS - 1;
   constexpr int KS = DK / 32;
   constexpr int MT = DK / 64;     // state d tiles per wave
-  constexpr int PF = DK <= 128 ? 2 : 1;  // chunks of operands in flight
+  // chunks of operands in flight (fp32 operands take twice the registers)
+  constexpr int PF = !F32IN && DK <= 128 ? 2 : 1;
   constexpr int kSB = DK + 8;     // bf16 row stride of the state planes
   // bf16 row stride of the K tile: 8 dwords past a multiple of 64 banks, so
   // the transposing reads of step (3) (four rows x four column groups per
@@ -570,15 +707,14 @@ gdn_apply(GdnArgs a) {
   constexpr int kSK = DK + 16;
   constexpr int kXB = kC + 8;     // bf16 row stride of the X^T and Y^T planes
   constexpr int kVB = 24;         // bf16 row stride of the V tile
+  constexpr int kVF = 20;         // fp32 row stride of the V tile (fp32 inputs)
   constexpr int kOB = 16 + 16 / (int)sizeof(TO);  // TO row stride of the output tile
-  __shared__ __attribute__((aligned(16))) bf16_t Sh[16 * kSB];  // S [r][d], hi
-  __shared__ __attribute__((aligned(16))) bf16_t Sl[16 * kSB];  // S [r][d], lo
-  __shared__ __attribute__((aligned(16))) bf16_t Ks[kC * kSK];  // K [t][d]
-  __shared__ __attribute__((aligned(16))) bf16_t Xh[16 * kXB];  // X^T [r][t], hi
-  __shared__ __attribute__((aligned(16))) bf16_t Xl[16 * kXB];  // X^T [r][t], lo
-  __shared__ __attribute__((aligned(16))) bf16_t Yh[16 * kXB];  // Y^T [r][t], hi
-  __shared__ __attribute__((aligned(16))) bf16_t Yl[16 * kXB];  // Y^T [r][t], lo
-  __shared__ __attribute__((aligned(16))) bf16_t Vs[kC * kVB];  // V [t][r]
+  __shared__ __attribute__((aligned(16))) bf16_t Sp[NS][16 * kSB];  // S [r][d]
+  __shared__ __attribute__((aligned(16))) bf16_t Kt[NI][kC * kSK];  // K [t][d]
+  __shared__ __attribute__((aligned(16))) bf16_t Xp[NS][16 * kXB];  // X^T [r][t]
+  __shared__ __attribute__((aligned(16))) bf16_t Yp[NS][16 * kXB];  // Y^T [r][t]
+  __shared__ __attribute__((aligned(16))) bf16_t Vs[F32IN ? 8 : kC * kVB];  // V [t][r]
+  __shared__ __attribute__((aligned(16))) float Vf[F32IN ? kC * kVF : 4];   // V [t][r], fp32
   __shared__ __attribute__((aligned(16))) TO Os[kC * kOB];      // O [t][r]
   __shared__ __attribute__((aligned(16))) float Gs[kC];
 
@@ -595,7 +731,7 @@ gdn_apply(GdnArgs a) {
 
   // The wave keeps d tiles mt = wave + 4 i of S^T in fp32 (lane: state row
   // r0 + hl, d = 16 mt + 4 quad + e) and publishes them to every wave as
-  // hi / lo bf16 planes.
+  // NS bf16 planes.
   float* const srow = a.state + (bh * a.Dv + r0 + hl) * DK;
   f32x4 sown[MT];
 #pragma unroll
@@ -603,60 +739,83 @@ gdn_apply(GdnArgs a) {
   auto put_state = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
-      bf16x4 hi, lo;
-      split4(sown[i], hi, lo);
-      *(bf16x4*)(Sh + hl * kSB + 16 * (wave + 4 * i) + 4 * quad) = hi;
-      *(bf16x4*)(Sl + hl * kSB + 16 * (wave + 4 * i) + 4 * quad) = lo;
+      bf16x4 pl[NS];
+      split_planes4<NS>(sown[i], pl);
+#pragma unroll
+      for (int n = 0; n < NS; ++n)
+        *(bf16x4*)(Sp[n] + hl * kSB + 16 * (wave + 4 * i) + 4 * quad) = pl[n];
     }
   };
 
   // Every load reads a clamped row and is issued unconditionally (per
   // wave); the rows of tokens past the end are zeroed where X^T is formed
   // and never stored, and their rows of W are zero.
-  // Per-block bases; the per-token offsets are 24-bit products (token index
-  // times a row of at most 2^24 elements, checked on the host), so address
-  // arithmetic stays off the quarter-rate 32 / 64-bit multiplies.
+  // Per-block bases; the per-token offsets are 24-bit products (a token
+  // index below 2^24 times a row of fewer than 2^24 elements, whose product
+  // the host also keeps below 2^32), so address arithmetic stays off the
+  // quarter-rate 32 / 64-bit multiplies.
   const int krow = a.Hk * DK, vrow = a.Hv * a.Dv;
-  const bf16_t* const kbase = (const bf16_t*)a.k + (int64_t)b * a.T * krow + kh * DK + 8 * quad;
-  const bf16_t* const qbase = (const bf16_t*)a.q + (int64_t)b * a.T * krow + kh * DK + 8 * quad;
-  const bf16_t* const vbase = (const bf16_t*)a.v + (int64_t)b * a.T * vrow + h * a.Dv + r0;
+  const TI* const kbase = (const TI*)a.k + (int64_t)b * a.T * krow + kh * DK + 8 * quad;
+  const TI* const qbase = (const TI*)a.q + (int64_t)b * a.T * krow + kh * DK + 8 * quad;
+  const TI* const vbase = (const TI*)a.v + (int64_t)b * a.T * vrow + h * a.Dv + r0;
   TO* const obase = (TO*)a.out + (int64_t)b * a.T * vrow + h * a.Dv + r0;
-  float* const wsbase = a.ws + bh * a.nchunks * ws_per_chunk();
-  auto fetch_kq = [&](KqIn<DK>& in, int c) __attribute__((always_inline)) {
+  float* const wsbase = a.ws + bh * a.nchunks * ws_per_chunk<NS>();
+  auto fetch_kq = [&](KqIn<TI, DK>& in, int c) __attribute__((always_inline)) {
     const unsigned off = __umul24((unsigned)min(c * kC + tw + hl, a.T - 1), (unsigned)krow);
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      in.k[ks] = *(const bf16x8*)(kbase + off + 32 * ks);
-      in.q[ks] = *(const bf16x8*)(qbase + off + 32 * ks);
+      if constexpr (F32IN) {
+        in.k[2 * ks] = *(const f32x4*)(kbase + off + 32 * ks);
+        in.k[2 * ks + 1] = *(const f32x4*)(kbase + off + 32 * ks + 4);
+        in.q[2 * ks] = *(const f32x4*)(qbase + off + 32 * ks);
+        in.q[2 * ks + 1] = *(const f32x4*)(qbase + off + 32 * ks + 4);
+      } else {
+        in.k[ks] = *(const bf16x8*)(kbase + off + 32 * ks);
+        in.q[ks] = *(const bf16x8*)(qbase + off + 32 * ks);
+      }
     }
   };
-  auto fetch_pw = [&](PwIn& in, int c) __attribute__((always_inline)) {
-    const ChunkWs w = chunk_ws(wsbase + c * (int)ws_per_chunk());
+  auto fetch_pw = [&](PwIn<NS>& in, int c) __attribute__((always_inline)) {
+    const ChunkWs<NS> w = chunk_ws<NS>(wsbase + c * (int)ws_per_chunk<NS>());
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       if (tile_live(wave, ks)) {
         const int o = tile_off(wave, ks, lane);
-        in.p_hi[ks] = *(const bf16x8*)(w.p_hi + o);
-        in.p_lo[ks] = *(const bf16x8*)(w.p_lo + o);
-        in.w_hi[ks] = *(const bf16x8*)(w.w_hi + o);
-        in.w_lo[ks] = *(const bf16x8*)(w.w_lo + o);
+#pragma unroll
+        for (int n = 0; n < NS; ++n) in.p[ks][n] = *(const bf16x8*)(w.p[n] + o);
+#pragma unroll
+        for (int n = 0; n < NS; ++n) in.w[ks][n] = *(const bf16x8*)(w.w[n] + o);
       }
     }
   };
-  auto fetch_vg = [&](VgIn& in, int c) __attribute__((always_inline)) {
+  auto fetch_vg = [&](VgIn<TI>& in, int c) __attribute__((always_inline)) {
     if (wave < 2) {
       const unsigned t = (unsigned)min(c * kC + (tid >> 1), a.T - 1);
-      in.v = *(const bf16x8*)(vbase + __umul24(t, (unsigned)vrow) + 8 * (tid & 1));
+      const TI* p = vbase + __umul24(t, (unsigned)vrow) + 8 * (tid & 1);
+      if constexpr (F32IN) {
+        in.v[0] = *(const f32x4*)p;
+        in.v[1] = *(const f32x4*)(p + 4);
+      } else {
+        in.v = *(const bf16x8*)p;
+      }
     } else if (wave == 2 && lane < 16) {
-      in.g = *(const f32x4*)(wsbase + c * (int)ws_per_chunk() + 4 * lane);
+      vg_decay(in) = *(const f32x4*)(wsbase + c * (int)ws_per_chunk<NS>() + 4 * lane);
     }
   };
-  auto stage_vg = [&](const VgIn& in, int c) __attribute__((always_inline)) {
+  auto stage_vg = [&](const VgIn<TI>& in, int c) __attribute__((always_inline)) {
     if (wave < 2) {
-      const bf16x8 zero = {};
-      *(bf16x8*)(Vs + (tid >> 1) * kVB + 8 * (tid & 1)) = c * kC + (tid >> 1) < a.T ? in.v : zero;
+      const bool ok = c * kC + (tid >> 1) < a.T;
+      if constexpr (F32IN) {
+        const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+        float* p = Vf + (tid >> 1) * kVF + 8 * (tid & 1);
+        *(f32x4*)p = ok ? in.v[0] : zero;
+        *(f32x4*)(p + 4) = ok ? in.v[1] : zero;
+      } else {
+        const bf16x8 zero = {};
+        *(bf16x8*)(Vs + (tid >> 1) * kVB + 8 * (tid & 1)) = ok ? in.v : zero;
+      }
     } else if (wave == 2 && lane < 16) {
-      *(f32x4*)(Gs + 4 * lane) = in.g;
+      *(f32x4*)(Gs + 4 * lane) = vg_decay(in);
     }
   };
   // Output tile of chunk c (staged in LDS) -> global, 16 bytes per lane.
@@ -677,9 +836,9 @@ gdn_apply(GdnArgs a) {
   // last use, into the same registers, so the loads overlap the following
   // chunks.  Chunks past the end re-read the last chunk (unused) rather
   // than branching.
-  KqIn<DK> kq[PF];
-  PwIn pw[PF];
-  VgIn vg[PF];
+  KqIn<TI, DK> kq[PF];
+  PwIn<NS> pw[PF];
+  VgIn<TI> vg[PF];
 #pragma unroll
   for (int p = 0; p < PF; ++p) {
     const int c = min(p, a.nchunks - 1);
@@ -692,36 +851,58 @@ gdn_apply(GdnArgs a) {
   fetch_vg(vg[0], min(PF, a.nchunks - 1));
   __syncthreads();
 
-  auto chunk = [&](int c, KqIn<DK>& kqc, PwIn& pwc, VgIn& vgn) __attribute__((always_inline)) {
+  auto chunk = [&](int c, KqIn<TI, DK>& kqc, PwIn<NS>& pwc, VgIn<TI>& vgn)
+                   __attribute__((always_inline)) {
     const int t0 = c * kC;
     const int cf = min(c + PF, a.nchunks - 1);
 
     // (1) K S^T and Q S^T for this wave's tokens (B = S^T: lane holds
     // S[r0 + hl][32 ks + 8 quad + 0..7]); X^T = V - diag(exp Gc) K S^T.  The
     // wave's K rows also go to the K tile for step (3).
-    bf16x8 shi[KS], slo[KS];
+    bf16x8 sp[KS][NS];
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      shi[ks] = *(const bf16x8*)(Sh + hl * kSB + 32 * ks + 8 * quad);
-      slo[ks] = *(const bf16x8*)(Sl + hl * kSB + 32 * ks + 8 * quad);
-    }
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int n = 0; n < NS; ++n) sp[ks][n] = *(const bf16x8*)(Sp[n] + hl * kSB + 32 * ks + 8 * quad);
     f32x4 kst = {0.f, 0.f, 0.f, 0.f}, qst = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      kst = mfma16x16x32(kqc.k[ks], shi[ks], kst);
-      kst = mfma16x16x32(kqc.k[ks], slo[ks], kst);
+      bf16x8 kp[NI];
+      if constexpr (F32IN) {
+        split_pair<NI>(kqc.k[2 * ks], kqc.k[2 * ks + 1], kp);
+#pragma unroll
+        for (int n = 0; n < NI; ++n) *(bf16x8*)(Kt[n] + (tw + hl) * kSK + 32 * ks + 8 * quad) = kp[n];
+      } else {
+        kp[0] = kqc.k[ks];
+      }
+      kst = mfma_planes<NI, NS, ORD>(kp, sp[ks], kst);
     }
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      qst = mfma16x16x32(kqc.q[ks], shi[ks], qst);
-      qst = mfma16x16x32(kqc.q[ks], slo[ks], qst);
+      bf16x8 qp[NI];
+      if constexpr (F32IN)
+        split_pair<NI>(kqc.q[2 * ks], kqc.q[2 * ks + 1], qp);
+      else
+        qp[0] = kqc.q[ks];
+      qst = mfma_planes<NI, NS, ORD>(qp, sp[ks], qst);
     }
     // The previous chunk's output tile goes out while the products run.
     if (c > 0) flush_out(c - 1);
+    if constexpr (!F32IN) {
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) *(bf16x8*)(Ks + (tw + hl) * kSK + 32 * ks + 8 * quad) = kqc.k[ks];
+      for (int ks = 0; ks < KS; ++ks)
+        *(bf16x8*)(Kt[0] + (tw + hl) * kSK + 32 * ks + 8 * quad) = kqc.k[ks];
+    }
     fetch_kq(kqc, cf);
-    const bf16x4 v4 = lds_read_tr4(Vs + (tw + tr_row) * kVB + tr_col);
+    f32x4 v4;
+    if constexpr (F32IN) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v4[e] = Vf[(tw + 4 * quad + e) * kVF + hl];
+    } else {
+      const bf16x4 vb = lds_read_tr4(Vs + (tw + tr_row) * kVB + tr_col);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v4[e] = static_cast<float>(vb[e]);
+    }
     const f32x4 g4 = *(const f32x4*)(Gs + tw + 4 * quad);
     const float glin = fast_exp2(Gs[kC - 1]);
     f32x4 gam, xt;
@@ -729,47 +910,36 @@ gdn_apply(GdnArgs a) {
     for (int e = 0; e < 4; ++e) {
       gam[e] = fast_exp2(g4[e]);
       const bool ok = t0 + tw + 4 * quad + e < a.T;
-      xt[e] = ok ? static_cast<float>(v4[e]) - gam[e] * kst[e] : 0.f;
+      xt[e] = ok ? v4[e] - gam[e] * kst[e] : 0.f;
     }
     {
-      bf16x4 hi, lo;
-      split4(xt, hi, lo);
-      *(bf16x4*)(Xh + hl * kXB + tw + 4 * quad) = hi;
-      *(bf16x4*)(Xl + hl * kXB + tw + 4 * quad) = lo;
+      bf16x4 pl[NS];
+      split_planes4<NS>(xt, pl);
+#pragma unroll
+      for (int n = 0; n < NS; ++n) *(bf16x4*)(Xp[n] + hl * kXB + tw + 4 * quad) = pl[n];
     }
     __syncthreads();  // X^T and the K tile complete; every wave has read S, V and Gc
 
     // (2) Y^T = W X^T and O = scale exp(Gc) Q S^T + P X^T for this wave's
     // tokens (W and P are causal: waves 0 and 1, tokens < 32, skip tokens
     // 32..63).
-    bf16x8 xhi[2], xlo[2];
+    bf16x8 xp[2][NS];
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      xhi[ks] = *(const bf16x8*)(Xh + hl * kXB + 32 * ks + 8 * quad);
-      xlo[ks] = *(const bf16x8*)(Xl + hl * kXB + 32 * ks + 8 * quad);
-    }
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int n = 0; n < NS; ++n) xp[ks][n] = *(const bf16x8*)(Xp[n] + hl * kXB + 32 * ks + 8 * quad);
     f32x4 yt = {0.f, 0.f, 0.f, 0.f}, po = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      if (tile_live(wave, ks)) {
-        yt = mfma16x16x32(pwc.w_hi[ks], xhi[ks], yt);
-        yt = mfma16x16x32(pwc.w_hi[ks], xlo[ks], yt);
-        yt = mfma16x16x32(pwc.w_lo[ks], xhi[ks], yt);
-      }
-    }
+    for (int ks = 0; ks < 2; ++ks)
+      if (tile_live(wave, ks)) yt = mfma_planes<NS, NS, ORD>(pwc.w[ks], xp[ks], yt);
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      if (tile_live(wave, ks)) {
-        po = mfma16x16x32(pwc.p_hi[ks], xhi[ks], po);
-        po = mfma16x16x32(pwc.p_hi[ks], xlo[ks], po);
-        po = mfma16x16x32(pwc.p_lo[ks], xhi[ks], po);
-      }
-    }
+    for (int ks = 0; ks < 2; ++ks)
+      if (tile_live(wave, ks)) po = mfma_planes<NS, NS, ORD>(pwc.p[ks], xp[ks], po);
     {
-      bf16x4 hi, lo;
-      split4(yt, hi, lo);
-      *(bf16x4*)(Yh + hl * kXB + tw + 4 * quad) = hi;
-      *(bf16x4*)(Yl + hl * kXB + tw + 4 * quad) = lo;
+      bf16x4 pl[NS];
+      split_planes4<NS>(yt, pl);
+#pragma unroll
+      for (int n = 0; n < NS; ++n) *(bf16x4*)(Yp[n] + hl * kXB + tw + 4 * quad) = pl[n];
     }
     stage_vg(vgn, c + 1);
     fetch_vg(vgn, min(c + 1 + PF, a.nchunks - 1));
@@ -781,15 +951,15 @@ gdn_apply(GdnArgs a) {
     // (3) S^T <- exp(Gc_last) S^T + K^T Y^T: A = K^T through the transposing
     // read (k-slot j of lane group quad is token 32 ks + tr_slot(quad, j)),
     // B = Y^T in the same token order; then publish the new state.
-    bf16x8 yhi[2], ylo[2];
+    bf16x8 yp[2][NS];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      const bf16x4 h0 = *(const bf16x4*)(Yh + hl * kXB + 32 * ks + 4 * quad);
-      const bf16x4 h1 = *(const bf16x4*)(Yh + hl * kXB + 32 * ks + 16 + 4 * quad);
-      const bf16x4 l0 = *(const bf16x4*)(Yl + hl * kXB + 32 * ks + 4 * quad);
-      const bf16x4 l1 = *(const bf16x4*)(Yl + hl * kXB + 32 * ks + 16 + 4 * quad);
-      yhi[ks] = __builtin_shufflevector(h0, h1, 0, 1, 2, 3, 4, 5, 6, 7);
-      ylo[ks] = __builtin_shufflevector(l0, l1, 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+      for (int n = 0; n < NS; ++n) {
+        const bf16x4 h0 = *(const bf16x4*)(Yp[n] + hl * kXB + 32 * ks + 4 * quad);
+        const bf16x4 h1 = *(const bf16x4*)(Yp[n] + hl * kXB + 32 * ks + 16 + 4 * quad);
+        yp[ks][n] = __builtin_shufflevector(h0, h1, 0, 1, 2, 3, 4, 5, 6, 7);
+      }
     }
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
@@ -797,11 +967,14 @@ gdn_apply(GdnArgs a) {
       f32x4 acc = glin * sown[i];
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        const bf16x4 k0 = lds_read_tr4(Ks + (32 * ks + tr_row) * kSK + 16 * mt + tr_col);
-        const bf16x4 k1 = lds_read_tr4(Ks + (32 * ks + 16 + tr_row) * kSK + 16 * mt + tr_col);
-        const bf16x8 ka = __builtin_shufflevector(k0, k1, 0, 1, 2, 3, 4, 5, 6, 7);
-        acc = mfma16x16x32(ka, yhi[ks], acc);
-        acc = mfma16x16x32(ka, ylo[ks], acc);
+        bf16x8 ka[NI];
+#pragma unroll
+        for (int n = 0; n < NI; ++n) {
+          const bf16x4 k0 = lds_read_tr4(Kt[n] + (32 * ks + tr_row) * kSK + 16 * mt + tr_col);
+          const bf16x4 k1 = lds_read_tr4(Kt[n] + (32 * ks + 16 + tr_row) * kSK + 16 * mt + tr_col);
+          ka[n] = __builtin_shufflevector(k0, k1, 0, 1, 2, 3, 4, 5, 6, 7);
+        }
+        acc = mfma_planes<NI, NS, ORD>(ka, yp[ks], acc);
       }
       sown[i] = acc;
     }
@@ -822,24 +995,45 @@ gdn_apply(GdnArgs a) {
   for (int i = 0; i < MT; ++i) *(f32x4*)(srow + 16 * (wave + 4 * i) + 4 * quad) = sown[i];
 }
 
-template <int DK, typename TO>
+template <typename TI, int DK, typename TO>
 int launch_chunk(const GdnArgs& a, hipStream_t s) {
-  if ((a.Hv / a.Hk) % 2 == 0)
-    hipLaunchKernelGGL((gdn_prep<DK, 2>), dim3(a.nchunks, a.Hv / 2, a.B), dim3(512), 0, s, a);
-  else
-    hipLaunchKernelGGL((gdn_prep<DK, 1>), dim3(a.nchunks, a.Hv, a.B), dim3(256), 0, s, a);
+  // two value heads per phase-A block where the key head has an even
+  // number of them; fp32 inputs at head_dim 256 stage three K planes, which
+  // leave LDS for one head's matrices only
+  constexpr bool kPairs = !(std::is_same<TI, float>::value && DK == 256);
+  if constexpr (kPairs) {
+    if ((a.Hv / a.Hk) % 2 == 0) {
+      hipLaunchKernelGGL((gdn_prep<TI, DK, 2>), dim3(a.nchunks, a.Hv / 2, a.B), dim3(512), 0, s,
+                         a);
+      const int rc = check_launch("gdn_prep");
+      if (rc != ALPX_OK) return rc;
+      hipLaunchKernelGGL((gdn_apply<TI, TO, DK>), dim3(a.Dv / 16 * a.Hv * a.B), dim3(256), 0, s,
+                         a);
+      return check_launch("gdn_apply");
+    }
+  }
+  hipLaunchKernelGGL((gdn_prep<TI, DK, 1>), dim3(a.nchunks, a.Hv, a.B), dim3(256), 0, s, a);
   int rc = check_launch("gdn_prep");
   if (rc != ALPX_OK) return rc;
-  hipLaunchKernelGGL((gdn_apply<TO, DK>), dim3(a.Dv / 16 * a.Hv * a.B), dim3(256), 0, s, a);
+  hipLaunchKernelGGL((gdn_apply<TI, TO, DK>), dim3(a.Dv / 16 * a.Hv * a.B), dim3(256), 0, s, a);
   return check_launch("gdn_apply");
 }
 
-template <typename TO>
+template <typename TI, typename TO>
 int launch_chunk_dk(const GdnArgs& a, hipStream_t s) {
   switch (a.Dk) {
-    case 64: return launch_chunk<64, TO>(a, s);
-    case 128: return launch_chunk<128, TO>(a, s);
-    default: return launch_chunk<256, TO>(a, s);
+    case 64: return launch_chunk<TI, 64, TO>(a, s);
+    case 128: return launch_chunk<TI, 128, TO>(a, s);
+    default: return launch_chunk<TI, 256, TO>(a, s);
+  }
+}
+
+template <typename TI>
+int launch_chunk_ti(const GdnArgs& a, int out_dtype, hipStream_t s) {
+  switch (out_dtype) {
+    case ALPX_F32: return launch_chunk_dk<TI, float>(a, s);
+    case ALPX_F16: return launch_chunk_dk<TI, f16_t>(a, s);
+    default: return launch_chunk_dk<TI, bf16_t>(a, s);
   }
 }
 
@@ -934,12 +1128,31 @@ extern "C" int alpx_gdn_step(float* state, const void* q, const void* k, const v
                          key_dim, value_dim, dtype, out_dtype, s);
 }
 
+extern "C" int alpx_gdn_chunk_uses_mfma(int dtype, int tokens, int key_heads, int value_heads,
+                                        int key_dim, int value_dim) {
+  using namespace alpx;
+  if (tokens <= 0 || key_heads <= 0 || value_heads <= 0 || key_dim <= 0 || value_dim <= 0 ||
+      value_heads % key_heads != 0)
+    return 0;
+  const int64_t krow = (int64_t)key_heads * key_dim, vrow = (int64_t)value_heads * value_dim;
+  // phase B forms per-token element offsets as unsigned 24 x 24-bit
+  // products: token < 2^24, row < 2^24 and token x row < 2^32
+  const bool offsets_fit = tokens < (1 << 24) && krow < (1 << 24) && vrow < (1 << 24) &&
+                           (int64_t)tokens * (krow > vrow ? krow : vrow) <= (int64_t)UINT32_MAX;
+  return (dtype == ALPX_BF16 || dtype == ALPX_F32) &&
+                 (key_dim == 64 || key_dim == 128 || key_dim == 256) && value_dim % 16 == 0 &&
+                 offsets_fit && override_value(ALPX_OVERRIDE_GDN_SEQUENTIAL) == 0
+             ? 1
+             : 0;
+}
+
 extern "C" size_t alpx_gdn_chunk_workspace_bytes(int batch, int tokens, int value_heads,
                                                  int key_dim) {
   using namespace alpx;
   if (batch <= 0 || tokens <= 0 || value_heads <= 0 || key_dim <= 0) return 0;
   const int64_t chunks = (tokens + kC - 1) / kC;
-  return (size_t)batch * value_heads * chunks * ws_per_chunk() * sizeof(float);
+  // the fp32-input kernels' three planes of P and W (bf16 inputs use two)
+  return (size_t)batch * value_heads * chunks * ws_per_chunk<3>() * sizeof(float);
 }
 
 extern "C" int alpx_gdn_chunk_prefill(float* state, const void* q, const void* k, const void* v,
@@ -971,11 +1184,9 @@ extern "C" int alpx_gdn_chunk_prefill(float* state, const void* q, const void* k
   a.scale = gdn_output_scale(key_dim);
   const uintptr_t align =
       (uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)state | (uintptr_t)out;
-  const bool chunked = dtype == ALPX_BF16 && (key_dim == 64 || key_dim == 128 || key_dim == 256) &&
-                       value_dim % 16 == 0 && (align & 15) == 0 &&
-                       tokens < (1 << 24) && key_heads * key_dim < (1 << 24) &&
-                       (int64_t)value_heads * value_dim < (1 << 24) &&
-                       getenv("ALPX_GDN_SEQUENTIAL") == nullptr;
+  const bool chunked =
+      alpx_gdn_chunk_uses_mfma(dtype, tokens, key_heads, value_heads, key_dim, value_dim) == 1 &&
+      (align & 15) == 0;
   TimedRegion timed(ALPX_T_GDN_CHUNK, s);
   if (chunked) {
     const size_t need = alpx_gdn_chunk_workspace_bytes(batch, tokens, value_heads, key_dim);
@@ -983,14 +1194,11 @@ extern "C" int alpx_gdn_chunk_prefill(float* state, const void* q, const void* k
       return fail(ALPX_EINVAL, "alpx_gdn_chunk_prefill: workspace holds %zu bytes, needs %zu",
                   workspace_bytes, need);
     a.ws = (float*)workspace;
-    switch (out_dtype) {
-      case ALPX_F32: return launch_chunk_dk<float>(a, s);
-      case ALPX_F16: return launch_chunk_dk<f16_t>(a, s);
-      default: return launch_chunk_dk<bf16_t>(a, s);
-    }
+    return dtype == ALPX_F32 ? launch_chunk_ti<float>(a, out_dtype, s)
+                             : launch_chunk_ti<bf16_t>(a, out_dtype, s);
   }
-  // Token-sequential form (fp32/fp16 inputs, other shapes): the decode step
-  // per token, exactly the reference's recurrence order.
+  // Token-sequential form (fp16 inputs, other shapes): the decode step per
+  // token, exactly the reference's recurrence order.
   const size_t es = dtype_size(dtype);
   const size_t os = dtype_size(out_dtype);
   for (int t = 0; t < tokens; ++t) {

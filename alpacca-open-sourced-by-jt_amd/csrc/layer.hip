@@ -1319,7 +1319,7 @@ extern "C" int alpx_recurrent_step(const float* current, const float* conv_weigh
   // Two launches (recurrent_rows_kernel, recurrent_finish_kernel) when the
   // heads fit launch A; otherwise prep, GDN step and norm separately.
   const bool rows_path = key_dim % 4 == 0 && key_dim <= kRowsDim && ((uintptr_t)state & 15) == 0 &&
-                         getenv("ALPX_RECURRENT_UNFUSED") == nullptr;
+                         override_value(ALPX_OVERRIDE_RECURRENT_UNFUSED) == 0;
   if (rows_path) {
     RowsArgs ra;
     ra.p = a;

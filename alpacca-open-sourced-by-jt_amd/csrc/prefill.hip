@@ -1181,8 +1181,9 @@ int host_tile_keys(int q_tokens, int kv_tokens, int group, int rel0, int window,
 // head_dim 128 at prefix 2048: 104.7 / 105.4 / 100.8, head_dim 64: 72.1 /
 // 65.2 / 66.4), so it takes one round of pairs below a ratio of
 // kSharedBelow10 / 10.
-// ALPX_PREFILL_KERNEL=pair, =shared or =single overrides the choice
-// (=shared falls back to the single kernel where one stream cannot serve).
+// ALPX_OVERRIDE_PREFILL_KERNEL (1 single, 2 paired, 3 shared-stream)
+// overrides the choice (shared falls back to the single kernel where one
+// stream cannot serve).
 enum PrefillKernelChoice { kSingleKernel, kPairKernel, kSharedKernel };
 constexpr int kSharedBelow10 = 16;
 
@@ -1191,11 +1192,10 @@ PrefillKernelChoice choose_prefill(int q_tokens, int kv_tokens, int kv_heads, in
                                    int key_dim, const void* pair_kernel) {
   // both tiles of a pair walk the key rows from 0 when no window starts inside the chunk
   const bool one_stream = window <= 0 || (int64_t)window > (int64_t)rel0 + q_tokens;
-  const char* force = getenv("ALPX_PREFILL_KERNEL");
-  if (force != nullptr && strcmp(force, "pair") == 0) return kPairKernel;
-  if (force != nullptr && strcmp(force, "single") == 0) return kSingleKernel;
-  if (force != nullptr && strcmp(force, "shared") == 0)
-    return one_stream ? kSharedKernel : kSingleKernel;
+  const int force = alpx::override_value(ALPX_OVERRIDE_PREFILL_KERNEL);
+  if (force == 2) return kPairKernel;
+  if (force == 1) return kSingleKernel;
+  if (force == 3) return one_stream ? kSharedKernel : kSingleKernel;
   const int64_t pairs = (int64_t)kv_heads * ((col_tiles + 1) / 2);
   const int resident = alpx::resident_blocks(pair_kernel, 512, 0);
   if (resident <= 0) return kSingleKernel;
@@ -1208,6 +1208,23 @@ PrefillKernelChoice choose_prefill(int q_tokens, int kv_tokens, int kv_heads, in
   if (key_dim == 256 && one_round && one_stream && ratio10 < kSharedBelow10) return kSharedKernel;
   const int r10 = key_dim == 128 ? 30 : 18;  // R x 10
   return ratio10 >= r10 ? kPairKernel : kSingleKernel;
+}
+
+// Whether prefill_impl runs these operands on the MFMA kernels: fp16 /
+// bf16, equal head dims of 64, 128 or 256, 16-byte aligned buffers and row
+// strides (`align` ORs their addresses and byte strides), and per-tile row
+// offsets that fit 32 bits.  Otherwise it takes the split-K path, which
+// needs a workspace of alpx_prefill_workspace_bytes.
+bool mfma_prefill_applies(int dtype, int key_dim, int value_dim, uintptr_t align,
+                          int64_t kv_tokens, int64_t k_pos_stride, int64_t v_pos_stride,
+                          int64_t rel0) {
+  const int64_t es = (int64_t)alpx::dtype_size(dtype);
+  return dtype != ALPX_F32 && key_dim == value_dim &&
+         (key_dim == 64 || key_dim == 128 || key_dim == 256) && (align & 15) == 0 &&
+         alpx::override_value(ALPX_OVERRIDE_PREFILL_GENERIC) == 0 &&
+         kv_tokens * k_pos_stride * es < ((int64_t)1 << 31) &&
+         kv_tokens * v_pos_stride * es < ((int64_t)1 << 31) && rel0 < ((int64_t)1 << 30) &&
+         rel0 > -((int64_t)1 << 30);
 }
 
 // The query prologue a prefill forms itself (alpx_attention_layer_prefill
@@ -1259,18 +1276,13 @@ int prefill_impl(const void* q, const void* key, const void* value, const void* 
                           (uintptr_t)(gate_stride * es) |
                           (uintptr_t)kn | (uintptr_t)vn | (uintptr_t)(k_pos_stride * es) |
                           (uintptr_t)(v_pos_stride * es);
-  const bool mfma = dtype != ALPX_F32 && key_dim == value_dim &&
-                    (key_dim == 64 || key_dim == 128 || key_dim == 256) && (align & 15) == 0 &&
-                    getenv("ALPX_PREFILL_GENERIC") == nullptr;
-  // the MFMA kernel forms per-tile row offsets in 32 bits
-  const bool offsets_fit = (int64_t)kv_tokens * k_pos_stride * (int64_t)es < ((int64_t)1 << 31) &&
-                           (int64_t)kv_tokens * v_pos_stride * (int64_t)es < ((int64_t)1 << 31) &&
-                           q_pos0 - kv_start < ((int64_t)1 << 30) && q_pos0 - kv_start > -((int64_t)1 << 30);
-  if (pages != nullptr && !(mfma && offsets_fit && out_dtype == dtype))
+  const bool mfma = mfma_prefill_applies(dtype, key_dim, value_dim, align, kv_tokens, k_pos_stride,
+                                         v_pos_stride, q_pos0 - kv_start);
+  if (pages != nullptr && !(mfma && out_dtype == dtype))
     return fail(ALPX_EUNSUPPORTED,
                 "alpx_prefill_causal_paged: needs fp16/bf16 pages, head_dim in {64, 128, 256}, "
                 "16-byte aligned rows and out_dtype == dtype");
-  if (mfma && offsets_fit) {
+  if (mfma) {
     const int cols_per_block = key_dim == 256 ? 64 : 128;
     const int tile_rows = key_dim == 256 ? 32 : 64;
     const int col_tiles = (int)(((int64_t)q_tokens * group + cols_per_block - 1) / cols_per_block);
@@ -1472,7 +1484,7 @@ extern "C" int alpx_attention_layer_prefill(
                             (uintptr_t)(2 * head_dim * es);
     if (!((dtype == ALPX_F16 || dtype == ALPX_BF16) &&
           (head_dim == 64 || head_dim == 128 || head_dim == 256) && (align & 15) == 0 &&
-          getenv("ALPX_PREFILL_GENERIC") == nullptr &&
+          override_value(ALPX_OVERRIDE_PREFILL_GENERIC) == 0 &&
           (position + tokens) * row * (int64_t)es < ((int64_t)1 << 31)))
       return fail(ALPX_EUNSUPPORTED,
                   "alpx_attention_layer_prefill without query_out: needs fp16/bf16, head_dim in "
@@ -1496,6 +1508,23 @@ extern "C" int alpx_attention_layer_prefill(
                         (int)(position + tokens), q_heads, kv_heads, head_dim, head_dim, row, row,
                         position, 0, 0, scale, dtype, out_dtype, stream, nullptr, 0, 0, nullptr,
                         nullptr, 2 * (int64_t)head_dim, &qp);
+  }
+  // The query-buffer form: where the prefill will not take the MFMA
+  // kernels, its split-K path needs a workspace, checked before the
+  // prologue writes the caches.
+  const uintptr_t qalign = (uintptr_t)query_out | (uintptr_t)(head_dim * es) | (uintptr_t)kseq |
+                           (uintptr_t)vseq | (uintptr_t)gate | (uintptr_t)(2 * head_dim * es) |
+                           (uintptr_t)(row * es);
+  if (!mfma_prefill_applies(dtype, head_dim, head_dim, qalign, position + tokens, row, row,
+                            position)) {
+    const size_t need =
+        alpx_prefill_workspace_bytes(tokens, q_heads, kv_heads, head_dim, (int)(position + tokens));
+    if (need == 0) return fail(ALPX_EINVAL, "alpx_attention_layer_prefill: invalid sizes");
+    if (!workspace || workspace_bytes < need)
+      return fail(ALPX_EINVAL,
+                  "alpx_attention_layer_prefill: the split-K prefill needs a workspace of %zu "
+                  "bytes, %zu given (null workspace)",
+                  need, workspace ? workspace_bytes : (size_t)0);
   }
   const int rc = alpx_attention_prologue_chunk(
       query_gate, key, value, q_norm, k_norm, query_out, nullptr, key_cache, value_cache, dtype,
@@ -1544,7 +1573,7 @@ extern "C" int alpx_attention_layer_prefill_paged(
                           (uintptr_t)(2 * head_dim * es);
   if (!((dtype == ALPX_F16 || dtype == ALPX_BF16) &&
         (head_dim == 64 || head_dim == 128 || head_dim == 256) && (align & 15) == 0 &&
-        getenv("ALPX_PREFILL_GENERIC") == nullptr && position < ((int64_t)1 << 30) &&
+        override_value(ALPX_OVERRIDE_PREFILL_GENERIC) == 0 && position < ((int64_t)1 << 30) &&
         (position + tokens) * row * (int64_t)es < ((int64_t)1 << 31)))
     return fail(ALPX_EUNSUPPORTED,
                 "%s: needs fp16/bf16 pages, head_dim in {64, 128, 256}, 16-byte aligned rows and "

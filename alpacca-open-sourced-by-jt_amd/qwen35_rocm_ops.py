@@ -1155,7 +1155,8 @@ class Qwen35RocmOps:
                                  convolution_weights: Any, gate: Any, beta_logits: Any,
                                  alpha_logits: Any, dt_bias: Any, ssm_a: Any, norm_weight: Any,
                                  *, key_heads: int, key_dimension: int, epsilon: float,
-                                 batch_index: int = 0, out_dtype: Any = None) -> Any:
+                                 batch_index: int = 0, out_dtype: Any = None,
+                                 operand_dtype: Any = None) -> Any:
         """A prefill chunk of the Qwen3.5 recurrent (GDN) layer after its
         projections (extension): the reference runs the per-token chain of
         qwen35_numpy.py:63-131 / Qwen35Model._recurrent once per token
@@ -1164,9 +1165,13 @@ class Qwen35RocmOps:
         ``[T, Hv]`` of workspace sequence ``batch_index`` as one convolution
         prep (conv + SiLU over the chunk, split, Q/K L2 norm, beta / decay,
         history moved on), the chunked GDN on the sequence's delta state and
-        one gated RMSNorm.  The chunked GDN takes its q / k / v in bf16 when
-        the MFMA path covers the shape (key_dimension 64 / 128 / 256, value
-        width a multiple of 16) and in fp32, token by token, otherwise.
+        one gated RMSNorm.  The chain is fp32 like the reference's: q / k / v
+        stay fp32 and the chunked GDN (key_dimension 64 / 128 / 256, value
+        width a multiple of 16; token by token otherwise) splits them into
+        hi + lo bf16 MFMA operands, which keeps output and state within 1e-4
+        of the fp64 token chain.  ``operand_dtype=torch.bfloat16`` (opt-in)
+        rounds q / k / v to bf16 instead (fewer MFMAs), with the state within
+        about 2e-3 and the output within 2e-2 of the fp32 chain.
         Returns ``[T, Hv * Dv]``."""
         torch = self.torch
         history = self._fp32(workspace.convolution_history, "convolution history",
@@ -1211,8 +1216,11 @@ class Qwen35RocmOps:
         if _shape(norm_weight) != (value_width,):
             raise ValueError("RMSNorm weight must match the input's final dimension")
         eps = _positive_finite("epsilon", epsilon)
+        if operand_dtype not in (None, torch.float32, torch.bfloat16):
+            raise TypeError("operand_dtype must be torch.float32 or torch.bfloat16")
         mfma = key_width in (64, 128, 256) and value_width % 16 == 0
-        qkv_dtype = torch.bfloat16 if mfma else torch.float32
+        qkv_dtype = (torch.bfloat16 if mfma and operand_dtype == torch.bfloat16
+                     else torch.float32)
         q, k, v, beta, g = _ops.recurrent_prefill_prep(
             mixed, weights, history[batch_index] if kernel > 1 else None, beta_logits,
             alpha_logits, dt_bias, ssm_a, key_heads=key_heads, key_dim=key_width,

@@ -122,6 +122,37 @@ def _graph_replay_ms(torch, fn, steps, warmup):
     return ms
 
 
+def _graph_event_ms(torch, fn, replays=8):
+    """Device ms per call of ``fn`` run back to back: ``GRAPH_CALLS`` calls
+    captured in one graph, ``replays`` replays bracketed by one pair of
+    events on the replay stream.  For kernels of a few microseconds a pair
+    of events around every launch (``_event_kernel_ms``) adds about as much
+    as the kernel takes; this figure includes no host time and no event per
+    launch, only the gaps between consecutive kernels of the graph, so it
+    bounds a single kernel's duration from above."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(GRAPH_CALLS):
+            fn()
+    for _ in range(2):
+        graph.replay()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / (replays * GRAPH_CALLS)
+    del graph
+    return ms
+
+
 def _event_kernel_ms(torch, lib, fn, steps, kernels):
     """Average HIP-event duration (ms) of each library kernel id in
     ``kernels`` over ``steps`` calls of ``fn`` (events recorded by the
@@ -243,6 +274,7 @@ def bench_decode(torch, ops, lib, *, batch, ctx, hq, hkv, d, dtype, gate, steps,
     split_ms, comb_ms = _event_kernel_ms(torch, lib, fn, steps, (lib.T_DECODE,
                                                                  lib.T_DECODE_COMBINE))
     graph_ms = _graph_replay_ms(torch, fn, steps, warmup) if graph else None
+    device_ms = _graph_event_ms(torch, fn) if graph else None
     es = q.element_size()
     rows = batch * ctx if seq_lens is None else int(sum(seq_lens))
     kv_bytes = 2 * rows * hkv * d * es
@@ -254,6 +286,7 @@ def bench_decode(torch, ops, lib, *, batch, ctx, hq, hkv, d, dtype, gate, steps,
         "split_ms": split_ms,
         "combine_ms": comb_ms,
         "graph_ms": graph_ms,
+        "device_ms": device_ms,
         "split_alg_bytes": kv_bytes + q_bytes,
         "split_gbs": (kv_bytes + q_bytes) / (split_ms * 1e-3) / 1e9,
         "step_bytes": step_bytes,
@@ -323,11 +356,18 @@ def _gdn_chunk_flops(hv, T, C, dk, dv):
     return hv * (T // C) * (2 * C * C * (2 * dk + 2 * dv + C) + 6 * C * dk * dv)
 
 
+# C5 prefill FLOPs as the baseline counts them: per (head,
+# chunk) 2 C^2 (3 Dk + 2 Dv) + 6 C Dk Dv, 32 heads x 16 chunks of 64
+C5_BASELINE_FLOPS = 32 * 16 * (2 * 64 * 64 * (3 * 128 + 2 * 128) + 6 * 64 * 128 * 128)
+
+
 def bench_gdn(torch, ops, lib, *, steps, warmup, seed=5):
     """C5: gated delta rule, 16 q/k heads, 32 v heads, Dk = Dv = 128, fp32
     state; a 1024-token chunked prefill, then 256 single-token decode steps.
     Prefill FLOPs follow the chunked form (2 C^2 (3 Dk + 2 Dv) + 6 C Dk Dv per
-    head-chunk); decode bytes are the state read + write plus q/k/v/o."""
+    head-chunk, the baseline's count); decode bytes are the state read +
+    write plus q/k/v/o.  Also timed: the same prefill with fp32 q / k / v
+    (the three-plane kernels that keep fp32 accuracy)."""
     g = torch.Generator(device="cuda").manual_seed(seed)
     dev = torch.device("cuda")
     T, hk, hv, dk, dv, C = 1024, 16, 32, 128, 128, 64
@@ -341,9 +381,17 @@ def bench_gdn(torch, ops, lib, *, steps, warmup, seed=5):
         torch.randn((1, T, hv), generator=g, device=dev))).contiguous()
     S = torch.zeros((1, hv, dv, dk), dtype=torch.float32, device=dev)
     fn = lambda: ops.gated_delta_net_chunk_(S, q, k, v, beta, gl)  # noqa: E731
+    _warm(torch, fn, 0.1)
     ms = _timed_steps(torch, fn, steps, warmup)
     (k_ms,) = _event_kernel_ms(torch, lib, fn, steps, (lib.T_GDN_CHUNK,))
     flops = _gdn_chunk_flops(hv, T, C, dk, dv)
+    # the same prefill on fp32 q / k / v
+    qf, kf, vf = q.float(), k.float(), v.float()
+    S32 = torch.zeros_like(S)
+    fn32 = lambda: ops.gated_delta_net_chunk_(S32, qf, kf, vf, beta, gl)  # noqa: E731
+    _warm(torch, fn32, 0.1)
+    ms32 = _timed_steps(torch, fn32, steps, warmup)
+    (k_ms32,) = _event_kernel_ms(torch, lib, fn32, steps, (lib.T_GDN_CHUNK,))
     # decode: 256 steps on the carried state
     q1, k1, v1 = q[:, 0].contiguous(), k[:, 0].contiguous(), v[:, 0].contiguous()
     b1, g1 = beta[:, 0].contiguous(), gl[:, 0].contiguous()
@@ -352,13 +400,16 @@ def bench_gdn(torch, ops, lib, *, steps, warmup, seed=5):
     dec_ms = _timed_steps(torch, step, n_dec, 16)
     (dk_ms,) = _event_kernel_ms(torch, lib, step, n_dec, (lib.T_GDN_STEP,))
     dec_graph_ms = _graph_replay_ms(torch, step, n_dec, 16)
+    dec_device_ms = _graph_event_ms(torch, step)
     step_bytes = 2 * hv * dv * dk * 4 + (2 * hk * dk + 2 * hv * dv) * 2
     return {"prefill_ms": ms, "prefill_kernel_ms": k_ms, "prefill_flops": flops,
             "prefill_tflops": flops / (k_ms * 1e-3) / 1e12,
+            "prefill_f32_inputs_ms": ms32, "prefill_f32_inputs_kernel_ms": k_ms32,
             "decode_us_per_step": dec_ms * 1e3, "decode_kernel_us": dk_ms * 1e3,
             "decode_graph_us_per_step": dec_graph_ms * 1e3,
+            "decode_device_us_per_step": dec_device_ms * 1e3,
             "decode_step_bytes": step_bytes,
-            "decode_kernel_gbs": step_bytes / (dk_ms * 1e-3) / 1e9}
+            "decode_kernel_gbs": step_bytes / (dec_device_ms * 1e-3) / 1e9}
 
 
 def bench_layers(torch, ops, lib, *, steps, warmup, seed=6):
@@ -591,6 +642,11 @@ def bench_layer_prefill(torch, ops, lib, *, steps, warmup, seed=7):
         ws, mixed, cw, gate, bl, al, dt, ssm, nw, key_heads=hk, key_dimension=dk, epsilon=eps)
     _warm(torch, rchunk, 0.1)
     r_ms = _timed_steps(torch, rchunk, max(10, steps // 2), 2)
+    rchunk16 = lambda: ops.recurrent_layer_prefill_(  # noqa: E731
+        ws, mixed, cw, gate, bl, al, dt, ssm, nw, key_heads=hk, key_dimension=dk, epsilon=eps,
+        operand_dtype=torch.bfloat16)
+    _warm(torch, rchunk16, 0.1)
+    r16_ms = _timed_steps(torch, rchunk16, max(10, steps // 2), 2)
 
     def tokens_rec():
         for t in range(R):
@@ -606,7 +662,9 @@ def bench_layer_prefill(torch, ops, lib, *, steps, warmup, seed=7):
             "token_path_ms": round(at_ms, 3), "speedup": round(at_ms / a_ms, 1), "flops": a_flops,
             "chunk_tflops": round(a_flops / (a_ms * 1e-3) / 1e12, 1)},
         "recurrent_layer_prefill_c5_1024": {
-            "chunk_ms": round(r_ms, 4), "token_path_ms": round(rt_ms, 3),
+            "chunk_ms": round(r_ms, 4), "chunk": "fp32 end to end (q / k / v in three bf16 "
+                                                 "planes on the MFMA products)",
+            "bf16_operands_chunk_ms": round(r16_ms, 4), "token_path_ms": round(rt_ms, 3),
             "speedup": round(rt_ms / r_ms, 1)},
     }
 
@@ -1032,16 +1090,24 @@ def main() -> int:
         entry = {
             "prefill_1024_ms": round(c5["prefill_ms"], 4),
             "prefill_kernel_ms": round(c5["prefill_kernel_ms"], 4),
-            "prefill_flops_chunked": c5["prefill_flops"],
+            "prefill_flops_baseline": C5_BASELINE_FLOPS,
+            "prefill_flops_products_once": c5["prefill_flops"],
             "prefill_flops_sequential": 1024 * 32 * 7 * 128 * 128,
+            "prefill_f32_inputs_ms": round(c5["prefill_f32_inputs_ms"], 4),
+            "prefill_f32_inputs_kernel_ms": round(c5["prefill_f32_inputs_kernel_ms"], 4),
             "decode_us_per_step": round(c5["decode_us_per_step"], 2),
             "decode_graph_us_per_step": round(c5["decode_graph_us_per_step"], 2),
-            "decode_kernel_us": round(c5["decode_kernel_us"], 2),
-            "roofline": _roofline("gdn_prep<128> + gdn_apply<bf16,128>", "mfma",
-                                  c5["prefill_flops"], c5["prefill_kernel_ms"],
+            "decode_event_pair_us": round(c5["decode_kernel_us"], 2),
+            "decode_device_us_per_step": round(c5["decode_device_us_per_step"], 2),
+            "roofline": _roofline("gdn_prep<bf16,128,2> + gdn_apply<bf16,bf16,128>", "mfma",
+                                  C5_BASELINE_FLOPS, c5["prefill_kernel_ms"],
                                   work_name="flops"),
+            # a kernel of ~3 us: per-launch event pairs add about its own
+            # duration, so the device time of back-to-back launches in a
+            # graph (events around the replays only) is the duration used
             "decode_roofline": _roofline("gdn_step_kernel<bf16>", "hbm",
-                                         c5["decode_step_bytes"], c5["decode_kernel_us"] * 1e-3)}
+                                         c5["decode_step_bytes"],
+                                         c5["decode_device_us_per_step"] * 1e-3)}
         if host:
             entry["cpu_baseline"] = cpu_c5(host)
         extra["c5_gdn_bf16"] = entry
@@ -1052,10 +1118,14 @@ def main() -> int:
         entry = {
             "us_per_step": round(c1["ms_per_step"] * 1e3, 2),
             "graph_us_per_step": round(c1["graph_ms"] * 1e3, 2),
-            "split_us": round(c1["split_ms"] * 1e3, 2),
-            "combine_us": round(c1["combine_ms"] * 1e3, 2),
-            "roofline": _roofline("decode_split_f32<64>", "hbm", c1["split_alg_bytes"],
-                                  c1["split_ms"])}
+            "device_us_per_step": round(c1["device_ms"] * 1e3, 2),
+            "split_event_pair_us": round(c1["split_ms"] * 1e3, 2),
+            "combine_event_pair_us": round(c1["combine_ms"] * 1e3, 2),
+            # kernels of a few microseconds: the device time of the step run
+            # back to back in a graph (split + combine) bounds the split's
+            # duration from above; per-launch event pairs add about as much
+            "roofline": _roofline("decode_split_f32<64> + decode_combine (step device time)",
+                                  "hbm", c1["split_alg_bytes"], c1["device_ms"])}
         if host:
             entry["cpu_baseline"] = cpu_c1(c1["tensors"], host)
         c1.pop("tensors")

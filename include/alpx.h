@@ -316,6 +316,13 @@ int alpx_gdn_step(float* state, const void* q, const void* k, const void* v, con
 /* Workspace bytes for alpx_gdn_chunk_prefill (chunked path). */
 size_t alpx_gdn_chunk_workspace_bytes(int batch, int tokens, int value_heads, int key_dim);
 
+/* 1 when alpx_gdn_chunk_prefill runs these sizes on the chunked MFMA
+ * kernels (given 16-byte aligned buffers), 0 when it runs them token by
+ * token.  Host-only: no device work.  (No reference counterpart: it tells
+ * a caller whether the call needs the chunk workspace.) */
+int alpx_gdn_chunk_uses_mfma(int dtype, int tokens, int key_heads, int value_heads, int key_dim,
+                             int value_dim);
+
 /*
  * GDN over a `tokens`-long prefill, in place on the state: the same result
  * as `tokens` calls of alpx_gdn_step (the reference's only form, the
@@ -325,10 +332,13 @@ size_t alpx_gdn_chunk_workspace_bytes(int batch, int tokens, int value_heads, in
  *
  * q, k [batch, tokens, key_heads, key_dim]; v and out [batch, tokens,
  * value_heads, value_dim]; beta, log_decay [batch, tokens, value_heads] fp32;
- * state as in alpx_gdn_step.  bf16 inputs with key_dim in {64, 128, 256},
- * value_dim a multiple of 16 and 16-byte aligned rows run the chunked
- * MFMA kernels (workspace of alpx_gdn_chunk_workspace_bytes needed);
- * anything else runs the step kernel token by token (workspace unused).
+ * state as in alpx_gdn_step.  bf16 or fp32 inputs with key_dim in {64,
+ * 128, 256}, value_dim a multiple of 16 and 16-byte aligned rows run the
+ * chunked MFMA kernels (workspace of alpx_gdn_chunk_workspace_bytes
+ * needed; alpx_gdn_chunk_uses_mfma tells); fp32 inputs enter those
+ * products as hi + lo bf16 pairs, so their result stays within fp32
+ * accuracy (1e-4) of the token-sequential recurrence.  Anything else runs
+ * the step kernel token by token (workspace unused).
  */
 int alpx_gdn_chunk_prefill(float* state, const void* q, const void* k, const void* v,
                            const float* beta, const float* log_decay, void* out, void* workspace,
@@ -626,6 +636,29 @@ enum alpx_timed_kernel {
 #define ALPX_TIMING_KERNELS 9
 int alpx_timing_enable(int enable);
 int alpx_timing_read(int kernel, double* total_ms, int64_t* launches);
+
+/*
+ * Kernel-choice overrides (test and A/B measurement support, no reference
+ * counterpart).  Each starts from its environment variable, read once when
+ * the library loads -- ALPX_DECODE_GENERIC, ALPX_PREFILL_GENERIC,
+ * ALPX_PREFILL_KERNEL (single | pair | shared), ALPX_GDN_SEQUENTIAL,
+ * ALPX_RECURRENT_UNFUSED -- and afterwards changes only through
+ * alpx_set_override: no entry point reads the environment per call.
+ * alpx_set_override returns the previous value, or ALPX_EINVAL for an
+ * unknown override or value; alpx_get_override returns the value or
+ * ALPX_EINVAL.  Set them between calls, not while calls are in flight on
+ * another host thread.
+ */
+enum alpx_override {
+  ALPX_OVERRIDE_DECODE_GENERIC = 0,    /* 1: decode on the VALU split kernel */
+  ALPX_OVERRIDE_PREFILL_GENERIC = 1,   /* 1: prefill on the split-K decode path */
+  ALPX_OVERRIDE_PREFILL_KERNEL = 2,    /* 0 auto, 1 single, 2 paired, 3 shared-stream */
+  ALPX_OVERRIDE_GDN_SEQUENTIAL = 3,    /* 1: chunked GDN runs token by token */
+  ALPX_OVERRIDE_RECURRENT_UNFUSED = 4  /* 1: recurrent step in three launches */
+};
+#define ALPX_OVERRIDES 5
+int alpx_set_override(int which, int value);
+int alpx_get_override(int which);
 
 #ifdef __cplusplus
 }

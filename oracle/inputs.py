@@ -124,11 +124,12 @@ def c4_decode_gated_bf16(seed=4, batch=4, ctx=32768, n_head=16, n_kv=2, hd=256):
             "scale": 1.0 / math.sqrt(hd), "dtype": "bf16"}
 
 
-def c5_gdn_bf16(seed=5, tokens=1280, hk=16, hv=32, dk=128, dv=128, eps=1e-6):
+def c5_gdn_bf16(seed=5, tokens=1280, hk=16, hv=32, dk=128, dv=128, eps=1e-6, dtype="bf16"):
     """C5: gated delta rule inputs.  Draw order: q ``[T, Hk, Dk]``, k, v
     ``[T, Hv, Dv]``, beta logits ``[T, Hv]``, a ``[Hv]`` ~ U(-1, 1),
     x ``[T, Hv]``.  q/k are L2-normalised per head (qwen35_normalize_qk,
-    qwen35_kernels.py:277-287) then rounded to bf16; v is rounded to bf16;
+    qwen35_kernels.py:277-287) then rounded to ``dtype`` (bf16 for C5;
+    "f32" keeps the fp32 values); v is rounded likewise;
     ``beta = sigmoid(logits)`` and ``g = -exp(a) * softplus(x)``
     (qwen35_beta_decay with dt_bias = 0, qwen35_kernels.py:290-307) stay
     float32."""
@@ -142,6 +143,6 @@ def c5_gdn_bf16(seed=5, tokens=1280, hk=16, hv=32, dk=128, dv=128, eps=1e-6):
     qn, kn = _gdn.normalize_qk(q, k, eps)
     ssm_a = -np.exp(a.astype(np.float64)).astype(np.float32)
     beta, g = _gdn.beta_decay(b, x, np.zeros(hv, np.float32), ssm_a[None, :])
-    return {"q": round_to(qn, "bf16"), "k": round_to(kn, "bf16"),
-            "v": round_to(v, "bf16"), "beta": beta.astype(np.float32),
-            "g": g.astype(np.float32), "dtype": "bf16"}
+    return {"q": round_to(qn, dtype), "k": round_to(kn, dtype),
+            "v": round_to(v, dtype), "beta": beta.astype(np.float32),
+            "g": g.astype(np.float32), "dtype": dtype}

@@ -26,3 +26,23 @@ def gpu():
     if not torch.cuda.is_available():
         pytest.skip("no GPU visible")
     return torch.device("cuda:0")
+
+
+@pytest.fixture
+def override():
+    """Sets kernel-choice overrides of the library (alpx_set_override: the
+    library reads its environment only once, at load) for one test, and
+    restores the previous values afterwards.  ``override("prefill_kernel",
+    "pair")``, ``override("recurrent_unfused", 1)``."""
+    lib = importlib.import_module(PACKAGE + "._lib")
+    saved = []
+
+    def set_(name, value):
+        which = getattr(lib, "OVERRIDE_" + name.upper())
+        if isinstance(value, str):
+            value = lib.PREFILL_KERNELS[value]
+        saved.append((which, lib.set_override(which, int(value))))
+
+    yield set_
+    for which, previous in reversed(saved):
+        lib.set_override(which, previous)

@@ -242,3 +242,75 @@ def test_layer_entry_points_validate_without_gpu(pkg):
                                  fake, fake, fake, 1 << 30, 1, 16, 30, 128, 128, 1e-6, 0, None)
     assert rc == L.EINVAL and "multiple of key heads" in L.last_error()
     assert lib.alpx_silu(None, fake, 4, 0, 0, None) == L.EINVAL
+
+
+def test_overrides_read_once_and_set_by_hook_without_gpu(pkg, monkeypatch):
+    """Kernel-choice overrides come from the environment once, at load, and
+    afterwards only from alpx_set_override: a variable set later changes
+    nothing, and the hook validates its arguments."""
+    L = pkg._lib
+    lib = L.lib()
+    before = lib.alpx_gdn_chunk_uses_mfma(L.BF16, 1024, 16, 32, 128, 128)
+    monkeypatch.setenv("ALPX_GDN_SEQUENTIAL", "1")
+    assert lib.alpx_gdn_chunk_uses_mfma(L.BF16, 1024, 16, 32, 128, 128) == before == 1
+    prev = L.set_override(L.OVERRIDE_PREFILL_KERNEL, L.PREFILL_KERNELS["pair"])
+    try:
+        assert L.get_override(L.OVERRIDE_PREFILL_KERNEL) == 2
+    finally:
+        assert L.set_override(L.OVERRIDE_PREFILL_KERNEL, prev) == 2
+    assert lib.alpx_set_override(99, 0) == L.EINVAL and "unknown override" in L.last_error()
+    assert lib.alpx_set_override(L.OVERRIDE_GDN_SEQUENTIAL, 2) == L.EINVAL
+    assert "out of range" in L.last_error()
+    assert lib.alpx_get_override(-1) == L.EINVAL
+
+
+def test_gdn_chunk_form_predicate_without_gpu(pkg, override):
+    """alpx_gdn_chunk_uses_mfma: bf16 and fp32 inputs with key_dim 64 / 128
+    / 256 and value_dim a multiple of 16 run the chunked kernels; phase B's
+    unsigned 24 x 24-bit token offsets need token x row < 2^32, so longer
+    calls run token by token instead of wrapping."""
+    L = pkg._lib
+    f = L.lib().alpx_gdn_chunk_uses_mfma
+    assert f(L.BF16, 1024, 16, 32, 128, 128) == 1
+    assert f(L.F32, 1024, 16, 32, 128, 128) == 1
+    assert f(L.F16, 1024, 16, 32, 128, 128) == 0
+    assert f(L.BF16, 1024, 16, 32, 100, 128) == 0
+    assert f(L.BF16, 1024, 16, 32, 128, 40) == 0
+    assert f(L.BF16, 1024, 16, 24, 128, 128) == 0
+    assert f(L.BF16, 0, 16, 32, 128, 128) == 0
+    # the wider row here is the value row, 32 x 128 = 2^12 elements
+    assert f(L.BF16, (1 << 20) - 1, 16, 32, 128, 128) == 1
+    assert f(L.BF16, 1 << 20, 16, 32, 128, 128) == 0
+    # the key row: 2^14 x 256 = 2^22 elements, at most 1023 tokens
+    assert f(L.F32, 1023, 1 << 14, 1 << 14, 256, 16) == 1
+    assert f(L.F32, 1024, 1 << 14, 1 << 14, 256, 16) == 0
+    override("gdn_sequential", 1)
+    assert f(L.BF16, 1024, 16, 32, 128, 128) == 0
+
+
+def test_layer_prefill_query_buffer_checks_workspace_first_without_gpu(pkg):
+    """The query-buffer form of alpx_attention_layer_prefill refuses, before
+    its prologue launch writes the caches, a call whose prefill leaves the
+    MFMA kernels -- a cache of 2 GiB or more per tensor, an fp32 cache --
+    without a large enough split-K workspace; the form without a query
+    buffer refuses the 2 GiB cache outright."""
+    L = pkg._lib
+    lib = L.lib()
+    fake = ctypes.c_void_p(256)  # never dereferenced: validation fails first
+    sec = (ctypes.c_int * 4)(11, 11, 10, 0)
+    # 16 sequences x 2 heads x 256 dims of bf16: 16 KiB per cache row, so
+    # 131072 rows make 2 GiB
+    cap = 131072
+
+    def call(query_out, ws, ws_bytes, dtype=L.BF16, position=cap - 64):
+        return lib.alpx_attention_layer_prefill(
+            fake, fake, fake, fake, fake, query_out, fake, fake, fake, ws, ws_bytes, dtype, dtype,
+            cap, 16, 3, 64, 16, 2, 256, position, sec, 1e7, 1e-6, 0.0625, None)
+
+    assert call(fake, None, 0) == L.EINVAL and "null workspace" in L.last_error()
+    need = lib.alpx_prefill_workspace_bytes(64, 16, 2, 256, cap)
+    assert need > 0
+    assert call(fake, fake, need - 1) == L.EINVAL and f"{need} bytes" in L.last_error()
+    assert call(None, fake, 1 << 20) == L.EUNSUPPORTED and "2 GiB" in L.last_error()
+    assert call(fake, None, 0, dtype=L.F32, position=0) == L.EINVAL
+    assert "workspace" in L.last_error()

@@ -1,6 +1,8 @@
 """GPU parity: gated delta-rule decode step and chunked prefill against the
 token-sequential fp64 oracle (qwen35_kernels.py:322-331 restated).
-Tolerances: outputs fp32 1e-4 / bf16 2e-2; state (fp32) 1e-4."""
+Tolerances: outputs fp32 1e-4 / bf16 2e-2; state (fp32) 1e-4.  fp32 inputs
+run the chunked MFMA kernels with hi + lo bf16 operands and keep the fp32
+bars."""
 
 import importlib
 
@@ -72,13 +74,16 @@ def test_qwen35_gdn_step_numpy_in_place(gpu):
     assert np.abs(state - ref_state).max() <= 1e-4  # mutated in place, like the reference
 
 
-def _c5_run(ops, gpu, tokens, prefill, hk=16, hv=32, dk=128, dv=128, seed=5):
+def _c5_run(ops, gpu, tokens, prefill, hk=16, hv=32, dk=128, dv=128, seed=5, dtype="bf16",
+            s0=None):
     import torch
-    c = I.c5_gdn_bf16(seed=seed, tokens=tokens, hk=hk, hv=hv, dk=dk, dv=dv)
+    c = I.c5_gdn_bf16(seed=seed, tokens=tokens, hk=hk, hv=hv, dk=dk, dv=dv, dtype=dtype)
     S = torch.zeros((1, hv, dv, dk), dtype=torch.float32, device=gpu)
-    q = _dev(torch, c["q"], "bf16", gpu)[None]
-    k = _dev(torch, c["k"], "bf16", gpu)[None]
-    v = _dev(torch, c["v"], "bf16", gpu)[None]
+    if s0 is not None:
+        S.copy_(torch.from_numpy(s0.astype(np.float32))[None])
+    q = _dev(torch, c["q"], dtype, gpu)[None]
+    k = _dev(torch, c["k"], dtype, gpu)[None]
+    v = _dev(torch, c["v"], dtype, gpu)[None]
     beta = torch.from_numpy(c["beta"]).to(gpu)[None]
     g = torch.from_numpy(c["g"]).to(gpu)[None]
     outs = [ops.gated_delta_net_chunk_(S, q[:, :prefill].contiguous(), k[:, :prefill].contiguous(),
@@ -89,7 +94,7 @@ def _c5_run(ops, gpu, tokens, prefill, hk=16, hv=32, dk=128, dv=128, seed=5):
                                               v[:, t].contiguous(), beta[:, t].contiguous(),
                                               g[:, t].contiguous())[:, None])
     out = torch.cat(outs, dim=1)[0]
-    ref_state = np.zeros((hv, dv, dk))
+    ref_state = np.zeros((hv, dv, dk)) if s0 is None else s0.astype(np.float32).astype(np.float64)
     ref = G.gdn_scan(ref_state, c["q"], c["k"], c["v"], c["beta"], c["g"])
     return out, S[0], ref, ref_state
 
@@ -124,3 +129,48 @@ def test_chunk_sequential_fallback_fp32(gpu, ops):
     ref = G.gdn_scan(ref_state, c["q"], c["k"], c["v"], c["beta"], c["g"])
     assert np.abs(out[0].cpu().numpy() - ref).max() <= 1e-4
     assert np.abs(S[0].cpu().numpy() - ref_state).max() <= 1e-4
+
+
+def test_c5_chunked_prefill_fp32_inputs_full(gpu, ops):
+    # C5 geometry with fp32 q / k / v (no bf16 rounding anywhere): the
+    # chunked kernels' hi + lo operands keep the fp32 bar on the output as
+    # well as on the state
+    L = _mod("_lib").lib()
+    assert L.alpx_gdn_chunk_uses_mfma(_mod("_lib").F32, 1024, 16, 32, 128, 128) == 1
+    out, S, ref, ref_state = _c5_run(ops, gpu, tokens=1280, prefill=1024, dtype="f32")
+    err_o = np.abs(out.float().cpu().numpy() - ref).max()
+    err_s = np.abs(S.cpu().numpy() - ref_state).max()
+    assert out.dtype == __import__("torch").float32
+    assert err_o <= 1e-4, err_o
+    assert err_s <= 1e-4, err_s
+
+
+@pytest.mark.parametrize("tokens,dk,dv,hk,hv", [(100, 128, 128, 2, 4), (64, 64, 32, 1, 2),
+                                                (150, 256, 64, 2, 2), (37, 128, 16, 1, 1),
+                                                (70, 128, 32, 1, 4), (40, 64, 16, 2, 6),
+                                                (300, 256, 256, 1, 2)])
+def test_chunked_fp32_shapes_from_nonzero_state(gpu, ops, tokens, dk, dv, hk, hv):
+    # fp32 inputs on the chunked kernels (every head dim, partial chunks,
+    # odd and even head groups) from a nonzero state, at the fp32 bars
+    rng = np.random.default_rng(tokens + dk)
+    s0 = rng.standard_normal((hv, dv, dk)) * 0.3
+    out, S, ref, ref_state = _c5_run(ops, gpu, tokens=tokens, prefill=tokens, hk=hk, hv=hv,
+                                     dk=dk, dv=dv, seed=tokens, dtype="f32", s0=s0)
+    assert np.abs(out.float().cpu().numpy() - ref).max() <= 1e-4
+    assert np.abs(S.cpu().numpy() - ref_state).max() <= 1e-4
+
+
+def test_chunked_fp32_agrees_with_token_by_token(gpu, ops, override):
+    # the same fp32 call through the chunked kernels and through the step
+    # kernel token by token (ALPX_OVERRIDE_GDN_SEQUENTIAL)
+    import torch
+    c = I.c5_gdn_bf16(seed=9, tokens=200, hk=4, hv=8, dk=128, dv=128, dtype="f32")
+    args = [torch.from_numpy(c[n]).to(gpu)[None] for n in ("q", "k", "v", "beta", "g")]
+    S1 = torch.full((1, 8, 128, 128), 0.05, dtype=torch.float32, device=gpu)
+    S2 = S1.clone()
+    o1 = ops.gated_delta_net_chunk_(S1, *args, out_dtype=torch.float32)
+    override("gdn_sequential", 1)
+    o2 = ops.gated_delta_net_chunk_(S2, *args, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert (o1 - o2).abs().max().item() <= 1e-4
+    assert (S1 - S2).abs().max().item() <= 1e-4

@@ -595,7 +595,7 @@ def _recurrent_run(ops, torch, gpu, rng_seed, batch, hk, hv, dk, dv, kernel, out
                                                       (2, 2, 4, 64, 96, 4),
                                                       (3, 1, 2, 256, 40, 4),
                                                       (1, 2, 6, 32, 48, 1)])
-def test_recurrent_layer_step_one_launch_matches_three_launches(gpu, ops, monkeypatch, out_name,
+def test_recurrent_layer_step_one_launch_matches_three_launches(gpu, ops, override, out_name,
                                                                 batch, hk, hv, dk, dv, kernel):
     """The one-launch step (one block per key head) performs the prep / GDN
     step / gated-norm arithmetic of the three-launch path in the same order,
@@ -604,7 +604,7 @@ def test_recurrent_layer_step_one_launch_matches_three_launches(gpu, ops, monkey
     args = (ops, torch, gpu, 7 + hk * 3 + kernel, batch, hk, hv, dk, dv, kernel,
             _td(torch, out_name), 4)
     fused = _recurrent_run(*args)
-    monkeypatch.setenv("ALPX_RECURRENT_UNFUSED", "1")
+    override("recurrent_unfused", 1)
     split = _recurrent_run(*args)
     for a, b in zip(fused[0], split[0]):
         assert np.array_equal(a, b)

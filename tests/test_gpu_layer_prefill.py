@@ -4,11 +4,13 @@ where the reference runs one token at a time) against the fp64
 token-sequential oracle (oracle/layer.py) and against the device's own
 per-token path.
 
-Tolerances: bf16 results 2e-2; the recurrent chunk's fp32 prep outputs
-1e-5 (fp32 arithmetic); GDN state 1e-4 when the oracle is fed the device's
-own bf16 q / k / v, 2e-3 when it rounds its own (a value on a bf16
-rounding boundary may round to the neighbouring bf16 on one side); pure
-copies (value rows, convolution history) bit-exact."""
+Tolerances: bf16 results 2e-2; the recurrent chunk (fp32 end to end, as
+the reference's chain) 1e-4 on output and state against the unrounded fp64
+chain; its fp32 prep outputs 1e-5 (fp32 arithmetic); with the opt-in bf16
+q / k / v operands, the GDN state 1e-4 when the oracle is fed the device's
+own bf16 q / k / v and 2e-3 when it rounds its own (a value on a bf16
+rounding boundary may round to the neighbouring bf16 on one side), the
+output 2e-2; pure copies (value rows, convolution history) bit-exact."""
 
 import importlib
 
@@ -169,6 +171,46 @@ def test_attention_layer_prefill_equals_prologue_then_gated_prefill(gpu, hq, hkv
         assert torch.equal(out_a, out_b), fused
 
 
+def test_attention_layer_prefill_cache_of_2gib_or_more(gpu, ops):
+    """A chunk over caches of 2 GiB per tensor (16 sequences x 131072 rows of
+    2 x 256 bf16): the MFMA prefill's 32-bit row offsets do not reach, so
+    the form without a query buffer refuses before any launch and the call
+    runs the query-buffer form on the split-K prefill with a workspace.  Its
+    output agrees with the same chunk over a batch-1 copy of the sequence
+    (MFMA kernels), the written rows bit for bit, and the other sequences
+    stay untouched."""
+    import torch
+    hq, hkv, d, cache_batch, cap, tokens, bi = 16, 2, 256, 16, 131072, 64, 5
+    assert cap * cache_batch * hkv * d * 2 == 1 << 31
+    pos = cap - tokens
+    gen = torch.Generator(device=gpu).manual_seed(11)
+    seq_k = torch.randn((pos, hkv, d), device=gpu, generator=gen).to(torch.bfloat16)
+    seq_v = torch.randn((pos, hkv, d), device=gpu, generator=gen).to(torch.bfloat16)
+    KC = torch.zeros((cap, cache_batch, hkv, d), dtype=torch.bfloat16, device=gpu)
+    VC = torch.zeros_like(KC)
+    KC[:pos, bi] = seq_k
+    VC[:pos, bi] = seq_v
+    KS = torch.zeros((cap, 1, hkv, d), dtype=torch.bfloat16, device=gpu)
+    VS = torch.zeros_like(KS)
+    KS[:pos, 0] = seq_k
+    VS[:pos, 0] = seq_v
+    del seq_k, seq_v
+    qg = (torch.randn((tokens, hq * 2 * d), device=gpu, generator=gen) * 3).to(torch.bfloat16)
+    k = (torch.randn((tokens, hkv * d), device=gpu, generator=gen) * 3).to(torch.bfloat16)
+    v = torch.randn((tokens, hkv * d), device=gpu, generator=gen).to(torch.bfloat16)
+    w = torch.linspace(0.5, 1.5, d, device=gpu)
+    kwargs = dict(position=pos, sections=(11, 11, 10, 0), frequency_base=1e7, epsilon=1e-6)
+    big, nxt = ops.attention_layer_prefill_(qg, k, v, w, w, KC, VC, batch_index=bi, **kwargs)
+    small, _ = ops.attention_layer_prefill_(qg, k, v, w, w, KS, VS, batch_index=0, **kwargs)
+    torch.cuda.synchronize()
+    assert nxt == cap
+    assert torch.equal(KC[pos:, bi], KS[pos:, 0]) and torch.equal(VC[pos:, bi], VS[pos:, 0])
+    assert (big.float() - small.float()).abs().max().item() <= 2e-2
+    others = [b for b in range(cache_batch) if b != bi]
+    assert KC[pos - 8:, others].abs().sum().item() == 0
+    assert VC[:, others[:3]].abs().sum().item() == 0
+
+
 def test_attention_layer_prefill_rejects_bad_shapes(gpu, ops):
     import torch
     KC = torch.zeros((16, 1, 2, 64), dtype=torch.bfloat16, device=gpu)
@@ -231,13 +273,12 @@ def test_recurrent_prefill_prep_matches_oracle(gpu, tokens, kernel, hk, hv, dk, 
         assert np.array_equal(H.cpu().numpy(), hist[0].astype(np.float32))
 
 
-@pytest.mark.parametrize("tokens,hk,hv,dk,dv", [(200, 16, 32, 128, 128), (70, 2, 4, 64, 64),
-                                                (33, 2, 2, 40, 24)])
-def test_recurrent_layer_prefill_matches_token_chain(gpu, ops, tokens, hk, hv, dk, dv):
-    # the chunk (prep -> chunked GDN -> gated norm) against the fp64
-    # token-sequential chain, from a nonzero state and history, for the
-    # second sequence of a batch-2 workspace; (40, 24) takes the fp32
-    # token-by-token recurrence instead of the bf16 MFMA one
+def _recurrent_prefill_vs_chain(ops, gpu, tokens, hk, hv, dk, dv, operand_dtype):
+    # the chunk (prep -> chunked GDN -> gated norm) of the second sequence of
+    # a batch-2 workspace, from a nonzero state and history, and the fp64
+    # token-sequential chain; returns (device output, device state,
+    # reference output, reference state), the oracle rounding q / k / v to
+    # bf16 where the device is asked to
     import torch
     rng = np.random.default_rng(tokens + hk + dk)
     kernel, eps, bi = 4, 1e-6, 1
@@ -252,20 +293,45 @@ def test_recurrent_layer_prefill_matches_token_chain(gpu, ops, tokens, hk, hv, d
         ws, _f32(torch, x["mixed"], gpu), _f32(torch, x["w"], gpu), _f32(torch, x["gate"], gpu),
         _f32(torch, x["bl"], gpu), _f32(torch, x["al"], gpu), _f32(torch, x["dt"], gpu),
         _f32(torch, x["ssm"], gpu), _f32(torch, x["nw"], gpu), key_heads=hk,
-        key_dimension=dk, epsilon=eps, batch_index=bi)
+        key_dimension=dk, epsilon=eps, batch_index=bi, operand_dtype=operand_dtype)
     torch.cuda.synchronize()
-    mfma = dk in (64, 128, 256) and dv % 16 == 0
+    rounded = operand_dtype == torch.bfloat16 and dk in (64, 128, 256) and dv % 16 == 0
     state = x["s0"].astype(np.float64)
     ref, hist = L.recurrent_layer_prefill(
         x["mixed"], x["w"], x["hist"], x["gate"], x["bl"], x["al"], x["dt"], x["ssm"], x["nw"],
         state, key_heads=hk, key_dim=dk, value_heads=hv, value_dim=dv, eps=eps,
-        round_qkv=(lambda a: I.round_to(a, "bf16")) if mfma else None)
+        round_qkv=(lambda a: I.round_to(a, "bf16")) if rounded else None)
     assert tuple(out.shape) == (tokens, hv * dv)
-    assert np.abs(_np(out) - ref).max() <= (2e-2 if mfma else 1e-4)
-    assert np.abs(ws.delta_state[bi].cpu().numpy() - state).max() <= (2e-3 if mfma else 1e-4)
     assert np.array_equal(ws.convolution_history[bi].cpu().numpy(), hist.astype(np.float32))
     # the other sequence is untouched
     assert not ws.delta_state[0].any() and not ws.convolution_history[0].any()
+    return _np(out), ws.delta_state[bi].cpu().numpy(), ref, state
+
+
+@pytest.mark.parametrize("tokens,hk,hv,dk,dv", [(200, 16, 32, 128, 128), (1024, 16, 32, 128, 128),
+                                                (70, 2, 4, 64, 64), (130, 1, 2, 256, 128),
+                                                (33, 2, 2, 40, 24)])
+def test_recurrent_layer_prefill_matches_token_chain(gpu, ops, tokens, hk, hv, dk, dv):
+    # the fp32 chunk against the unrounded fp64 token chain at the fp32 bar:
+    # the chunked GDN takes q / k / v as hi + lo bf16 operands (head dims
+    # 64 / 128 / 256), (40, 24) runs it token by token; (1024, C5 heads) is
+    # a full C5-geometry chunk
+    out, state, ref, ref_state = _recurrent_prefill_vs_chain(ops, gpu, tokens, hk, hv, dk, dv,
+                                                              None)
+    assert np.abs(out - ref).max() <= 1e-4
+    assert np.abs(state - ref_state).max() <= 1e-4
+
+
+@pytest.mark.parametrize("tokens,hk,hv,dk,dv", [(200, 16, 32, 128, 128), (70, 2, 4, 64, 64)])
+def test_recurrent_layer_prefill_bf16_operands(gpu, ops, tokens, hk, hv, dk, dv):
+    # the opt-in bf16 q / k / v operands: against the chain whose oracle
+    # rounds its own q / k / v to bf16, output 2e-2, state 2e-3 (a value on
+    # a rounding boundary may land on the neighbouring bf16)
+    import torch
+    out, state, ref, ref_state = _recurrent_prefill_vs_chain(ops, gpu, tokens, hk, hv, dk, dv,
+                                                              torch.bfloat16)
+    assert np.abs(out - ref).max() <= 2e-2
+    assert np.abs(state - ref_state).max() <= 2e-3
 
 
 def test_recurrent_prefill_state_with_device_qkv(gpu):

@@ -140,7 +140,7 @@ def test_paged_append_one_token_per_sequence_and_bad_arguments(gpu, ops):
 @pytest.mark.parametrize("dtype,d,page,hq,hkv,tq,prefix,gated", [
     ("bf16", 128, 64, 32, 8, 200, 300, False), ("f16", 256, 128, 16, 2, 130, 190, True),
     ("bf16", 64, 256, 8, 2, 70, 0, False), ("bf16", 256, 64, 16, 2, 64, 448, True)])
-def test_paged_prefill_equals_contiguous_bit_for_bit(gpu, ops, monkeypatch, dtype, d, page, hq,
+def test_paged_prefill_equals_contiguous_bit_for_bit(gpu, ops, override, dtype, d, page, hq,
                                                      hkv, tq, prefix, gated, kind):
     """Causal prefill of one sequence's chunk over its pages (shuffled pool,
     two sequences sharing it; the paged path runs the one-tile-per-block
@@ -150,7 +150,7 @@ def test_paged_prefill_equals_contiguous_bit_for_bit(gpu, ops, monkeypatch, dtyp
     two wave groups and merged), with and without the sigmoid gate, and
     matches the oracle."""
     import torch
-    monkeypatch.setenv("ALPX_PREFILL_KERNEL", kind)
+    override("prefill_kernel", kind)
     rng = np.random.default_rng(d + tq + page)
     batch = 2
     cap = ((prefix + tq + page - 1) // page) * page
@@ -305,7 +305,7 @@ def test_paged_layer_step_rejects_unsupported(gpu, ops):
     ("bf16", 64, 64, 4, 2, 3, 2, 256, 100, 45, (8, 8, 8, 8)),          # third sequence
     ("bf16", 128, 256, 32, 8, 1, 0, 4096, 2048, 2048, (11, 11, 10, 0)),  # C3-sized chunk
 ])
-def test_paged_layer_prefill_equals_contiguous_bit_for_bit(gpu, ops, monkeypatch, dtype, d, page,
+def test_paged_layer_prefill_equals_contiguous_bit_for_bit(gpu, ops, override, dtype, d, page,
                                                            hq, hkv, b, bi, cap, prefix, tokens,
                                                            sections):
     """paged_attention_layer_prefill_ (alpx_attention_layer_prefill_paged:
@@ -315,7 +315,7 @@ def test_paged_layer_prefill_equals_contiguous_bit_for_bit(gpu, ops, monkeypatch
     prefill on the single-tile kernel the paged one runs: the same output
     bits and the same rows written, for every sequence of the pool."""
     import torch
-    monkeypatch.setenv("ALPX_PREFILL_KERNEL", "single")
+    override("prefill_kernel", "single")
     rng = np.random.default_rng(d + page + prefix + tokens)
     ws, pw, table, perm = _fill(torch, ops, gpu, rng, dtype, b, cap, hkv, d, page, None)
     print(f"paged layer prefill {dtype} D={d} page={page} prefix={prefix} T={tokens}", flush=True)

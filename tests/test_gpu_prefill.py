@@ -34,14 +34,14 @@ def ops(gpu):
 
 
 @pytest.mark.parametrize("kernel", ["auto", "pair", "shared"])
-def test_c3_append_then_prefill_bf16_full_size(gpu, ops, monkeypatch, kernel):
+def test_c3_append_then_prefill_bf16_full_size(gpu, ops, override, kernel):
     """C3 at full size through append_prefill_attention_ (one launch: the
     chunk's rows read from k_new / v_new and written to the cache by the
     kernel), with the kernel the host picks (one tile per block at C3) and
     with the paired and the shared-stream kernels forced."""
     import torch
     if kernel != "auto":
-        monkeypatch.setenv("ALPX_PREFILL_KERNEL", kernel)
+        override("prefill_kernel", kernel)
     c = I.c3_prefill_bf16()
     cap = 4096
     ws = ops.initialize_attention_workspace(capacity=cap, batch_size=1, kv_heads=8,
@@ -72,7 +72,7 @@ def test_c3_append_then_prefill_bf16_full_size(gpu, ops, monkeypatch, kernel):
 
 
 @pytest.mark.parametrize("tq,prefix", [(2048, 2048), (4096, 0)])
-def test_qwen35_geometry_full_size_kernels_agree(gpu, monkeypatch, tq, prefix):
+def test_qwen35_geometry_full_size_kernels_agree(gpu, override, tq, prefix):
     """The Qwen3.5 attention-layer chunk at full size (2048 queries on a
     2048-row prefix, 16/2 heads, head_dim 256, gated; the host picks the
     paired kernel here) and 4096 queries at prefix 0 (two rounds of pairs,
@@ -92,10 +92,10 @@ def test_qwen35_geometry_full_size_kernels_agree(gpu, monkeypatch, tq, prefix):
     ops = _mod("qwen35_rocm_ops").Qwen35RocmOps()
     outs = {}
     for kernel in ("pair", "single", "shared"):
-        monkeypatch.setenv("ALPX_PREFILL_KERNEL", kernel)
+        override("prefill_kernel", kernel)
         outs[kernel] = ops.attention_prefill(q, K, V, position=prefix, gate=gate,
                                              out_dtype=torch.float32)
-    monkeypatch.delenv("ALPX_PREFILL_KERNEL")
+    override("prefill_kernel", "auto")
     outs["auto"] = ops.attention_prefill(q, K, V, position=prefix, gate=gate,
                                          out_dtype=torch.float32)
     torch.cuda.synchronize()
@@ -112,7 +112,7 @@ def test_qwen35_geometry_full_size_kernels_agree(gpu, monkeypatch, tq, prefix):
     (1, 5, 4, 4, 64, 0), (96, 250, 8, 2, 128, 70), (64, 64, 32, 8, 128, 0),
     (300, 17, 3, 1, 128, 0), (45, 100, 24, 2, 256, 40)])
 @pytest.mark.parametrize("kernel", ["pair", "single", "shared"])
-def test_prefill_append_equals_append_then_prefill(gpu, monkeypatch, kernel, dtype, tq, prefix, hq,
+def test_prefill_append_equals_append_then_prefill(gpu, override, kernel, dtype, tq, prefix, hq,
                                                    hkv, d, window):
     """alpx_prefill_append (one launch on the MFMA path, each contiguous kernel: the chunk's rows
     read from key / value, each block writing its own tokens' rows) gives
@@ -122,7 +122,7 @@ def test_prefill_append_equals_append_then_prefill(gpu, monkeypatch, kernel, dty
     tile), no prefix, a group size that does not divide a block's columns
     (tokens whose columns span two blocks), head_dim 256 and windows."""
     import torch
-    monkeypatch.setenv("ALPX_PREFILL_KERNEL", kernel)  # fp32 takes the split-K path either way
+    override("prefill_kernel", kernel)  # fp32 takes the split-K path either way
     P = _mod("_ops")
     rng = np.random.default_rng(tq * 13 + prefix + d + window)
     cap = prefix + tq + 9
@@ -188,7 +188,7 @@ def test_prefill_shapes(gpu, ops, dtype, tq, prefix, hq, hkv, d):
     (161, 7, 8, 2, 256, 0, True), (40, 500, 8, 8, 128, 0, False),
     (700, 300, 16, 4, 128, 200, False), (513, 0, 2, 1, 64, 0, True),
     (96, 33, 48, 2, 256, 50, False), (300, 100, 8, 2, 256, 1000, True)])
-def test_prefill_kernels_match_oracle(gpu, monkeypatch, kernel, tq, prefix, hq, hkv, d, window,
+def test_prefill_kernels_match_oracle(gpu, override, kernel, tq, prefix, hq, hkv, d, window,
                                       gated):
     """The three contiguous MFMA kernels -- the paired one (a light and a
     heavy column tile per block, the heavy tile's key tiles split between
@@ -202,7 +202,7 @@ def test_prefill_kernels_match_oracle(gpu, monkeypatch, kernel, tq, prefix, hq, 
     light tile's key range not a prefix of the heavy one's), head_dim
     64/128/256, gated and not."""
     import torch
-    monkeypatch.setenv("ALPX_PREFILL_KERNEL", kernel)
+    override("prefill_kernel", kernel)
     rng = np.random.default_rng(tq + prefix + d + window)
     q = I.round_to(rng.standard_normal((tq, hq, d)), "bf16")
     K = I.round_to(rng.standard_normal((prefix + tq, hkv, d)), "bf16")
