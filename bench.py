@@ -775,14 +775,35 @@ def _c2_tensors(torch, seed=2):
     return q, K, V
 
 
+def _c2_ragged_lens():
+    """C2 ragged lengths: the survey's draw rule, rng(2).integers(1024, 8193, 16)."""
+    import numpy as np
+    return np.random.default_rng(2).integers(1024, 8192 + 1, 16).astype(np.int32).tolist()
+
+
+# Decode workloads of the traffic summaries: (label, algorithmic bytes of
+# one split launch = K + V of every valid row + q).
+def _decode_traffic_workloads():
+    b, c, hq, hkv, d = (C2_SHAPE[k] for k in ("batch", "ctx", "hq", "hkv", "d"))
+    return {
+        "c2": ("C2 uniform 8192, fp16", 2 * c * b * hkv * d * 2 + b * hq * d * 2),
+        "ragged": ("C2 ragged lengths (rng(2) in [1024, 8192]), fp16",
+                   2 * sum(_c2_ragged_lens()) * hkv * d * 2 + b * hq * d * 2),
+        "c4": ("C4 4 x 32768, 16/2 heads, head_dim 256, bf16, gated",
+               2 * 4 * 32768 * 2 * 256 * 2 + 4 * 16 * 256 * 2),
+    }
+
+
 def pmc_probe(torch, ops, lib, steps, workload="c2") -> int:
     """Workload for the counter runs: 3 plain copies of known size (the
     library's append kernel writing a whole C2-sized K and V cache: it reads
     and writes 2 x 268,435,456 bytes per launch), then ``steps`` steps of
-    ``workload``: C2 decode (c2), C3 append + prefill (c3) or the C5
-    chunked GDN prefill (c5).  Prints the copy's byte count for the summary
-    step."""
+    ``workload``: C2 decode (c2), C2 ragged decode (ragged), C4 gated decode
+    (c4), C3 append + prefill (c3) or the C5 chunked GDN prefill, bf16 and
+    fp32 inputs, plus decode steps (c5).  Prints the copy's byte count for
+    the summary step."""
     q, K, V = _c2_tensors(torch)
+    copy_bytes = 2 * K.numel() * K.element_size()
     Kc, Vc = torch.empty_like(K), torch.empty_like(V)
     ops_mod = _mod("_ops")
     for _ in range(3):
@@ -790,6 +811,20 @@ def pmc_probe(torch, ops, lib, steps, workload="c2") -> int:
     if workload == "c2":
         for _ in range(steps):
             ops.online_attention(q, K, V, length=C2_SHAPE["ctx"])
+    elif workload == "ragged":
+        lens = torch.tensor(_c2_ragged_lens(), dtype=torch.int32, device=q.device)
+        for _ in range(steps):
+            ops.online_attention(q, K, V, length=C2_SHAPE["ctx"], seq_lens=lens)
+    elif workload == "c4":
+        del Kc, Vc, K, V
+        g = torch.Generator(device="cuda").manual_seed(4)
+        bf = torch.bfloat16
+        q4 = torch.randn((4, 16, 256), generator=g, device="cuda").to(bf)
+        K4 = torch.randn((32768, 4, 2, 256), generator=g, device="cuda").to(bf)
+        V4 = torch.randn((32768, 4, 2, 256), generator=g, device="cuda").to(bf)
+        g4 = torch.randn((4, 16, 256), generator=g, device="cuda").to(bf)
+        for _ in range(steps):
+            ops.online_attention(q4, K4, V4, length=32768, gate=g4)
     elif workload == "c3":
         del Kc, Vc
         bench_prefill(torch, ops, lib, steps=steps, warmup=1)
@@ -799,7 +834,6 @@ def pmc_probe(torch, ops, lib, steps, workload="c2") -> int:
     else:
         raise SystemExit(f"unknown probe workload {workload!r}")
     torch.cuda.synchronize()
-    copy_bytes = 2 * K.numel() * K.element_size()
     print(json.dumps({"copy_kernel": COPY_KERNEL, "copy_read_bytes": copy_bytes,
                       "copy_write_bytes": copy_bytes, "split_kernel": SPLIT_KERNEL,
                       "decode_steps": steps}))
@@ -808,7 +842,8 @@ def pmc_probe(torch, ops, lib, steps, workload="c2") -> int:
 
 def _counter_means(run_dir, counter):
     """Mean per-dispatch value of ``counter`` for the copy and split kernels
-    in one rocprofv3 CSV run directory (rows of one dispatch are summed)."""
+    in one rocprofv3 CSV run directory (rows of one dispatch are summed;
+    the split kernel is the MFMA split kernel without a prologue)."""
     import csv
     import glob
     files = glob.glob(os.path.join(run_dir, "**", "*counter_collection.csv"), recursive=True)
@@ -821,7 +856,7 @@ def _counter_means(run_dir, counter):
                 if r["Counter_Name"] != counter:
                     continue
                 for key, acc in per.items():
-                    if key in r["Kernel_Name"]:
+                    if key in r["Kernel_Name"] and "_pro" not in r["Kernel_Name"]:
                         did = (f, r["Dispatch_Id"])
                         acc[did] = acc.get(did, 0.0) + float(r["Counter_Value"])
     out = {}
@@ -832,8 +867,9 @@ def _counter_means(run_dir, counter):
     return out
 
 
-def traffic_summary(fetch_dir, write_dir) -> int:
-    """Print the profiles/ summary (markdown) from the two counter runs."""
+def traffic_summary(fetch_dir, write_dir, workload="c2") -> int:
+    """Print the profiles/ summary (markdown) from the two counter runs of
+    ``--pmc-probe workload`` (c2, ragged or c4)."""
     copy_bytes = 2 * C2_SHAPE["ctx"] * C2_SHAPE["batch"] * C2_SHAPE["hkv"] * C2_SHAPE["d"] * 2
     fetch = _counter_means(fetch_dir, "FETCH_SIZE")
     write = _counter_means(write_dir, "WRITE_SIZE")
@@ -841,21 +877,21 @@ def traffic_summary(fetch_dir, write_dir) -> int:
     w_scale = copy_bytes / (write[COPY_KERNEL][0] * 1024.0)
     fetch_b = fetch[SPLIT_KERNEL][0] * 1024.0 * f_scale
     write_b = write[SPLIT_KERNEL][0] * 1024.0 * w_scale
-    b, c, hq, hkv, d = (C2_SHAPE[k] for k in ("batch", "ctx", "hq", "hkv", "d"))
-    alg = 2 * c * b * hkv * d * 2 + b * hq * d * 2
-    rec = {"kernel": SPLIT_KERNEL + "<f16,128>", "workload": "C2 uniform 8192, fp16",
+    label, alg = _decode_traffic_workloads()[workload]
+    kernel = {"c4": "<bf16,256>"}.get(workload, "<f16,128>")
+    rec = {"kernel": SPLIT_KERNEL + kernel, "workload": label,
            "traffic_bytes_per_launch": round(fetch_b + write_b),
            "fetch_bytes_per_launch": round(fetch_b), "write_bytes_per_launch": round(write_b),
            "alg_bytes_per_launch": alg,
            "traffic_over_alg": round((fetch_b + write_b) / alg, 4),
            "fetch_scale": round(f_scale, 5), "write_scale": round(w_scale, 5)}
-    print("# HBM traffic of the decode split kernel (C2 uniform-8192, fp16)\n")
+    print(f"# HBM traffic of the decode split kernel ({label})\n")
     print("Counter runs (one rocprofv3 run per counter, from the repository root):\n")
     print("```")
     for ctr, dname in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
         print(f"rocprofv3 --pmc {ctr} --output-format csv -d {dname} -o run -- "
-              "python3 bench.py --pmc-probe c2")
-    print(f"python3 bench.py --traffic-summary {fetch_dir} {write_dir}")
+              f"python3 bench.py --pmc-probe {workload}")
+    print(f"python3 bench.py --traffic-summary {fetch_dir} {write_dir} {workload}")
     print("```\n")
     print("| kernel | counter | mean KiB / dispatch | dispatches |")
     print("|---|---|---|---|")
@@ -918,6 +954,9 @@ def counter_summary(pattern, dirs) -> int:
         if "SQ_VALU_MFMA_BUSY_CYCLES" in mean and mean.get("SQ_BUSY_CU_CYCLES"):
             ratios.append(("MFMA pipe busy per busy-CU cycle (x4 SIMDs)",
                            mean["SQ_VALU_MFMA_BUSY_CYCLES"] / (4 * mean["SQ_BUSY_CU_CYCLES"])))
+        if "SQ_ACTIVE_INST_VALU" in mean and mean.get("SQ_BUSY_CU_CYCLES"):
+            ratios.append(("VALU issue cycles (all waves) per busy-CU cycle (x4 SIMDs)",
+                           mean["SQ_ACTIVE_INST_VALU"] / (4 * mean["SQ_BUSY_CU_CYCLES"])))
         if mean.get("SQ_INSTS_MFMA") and "SQ_INSTS_VALU" in mean:
             ratios.append(("non-MFMA VALU instructions per MFMA",
                            (mean["SQ_INSTS_VALU"] - mean["SQ_INSTS_MFMA"]) / mean["SQ_INSTS_MFMA"]))
@@ -994,14 +1033,17 @@ def main() -> int:
     ap.add_argument("--pmc-probe", nargs="?", const="c2", default=None, metavar="WORKLOAD",
                     help="run the counter-run workload: copy calibration + c2 (default), c3 "
                          "or c5 steps")
-    ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
-                    help="summarise two rocprofv3 counter runs of --pmc-probe")
+    ap.add_argument("--traffic-summary", nargs="+", metavar="FETCH_DIR WRITE_DIR [WORKLOAD]",
+                    help="summarise two rocprofv3 counter runs of --pmc-probe WORKLOAD "
+                         "(c2, ragged or c4; default c2)")
     ap.add_argument("--counter-summary", nargs="+", metavar=("KERNEL", "RUN_DIR"),
                     help="summarise rocprofv3 --pmc runs for kernels whose name contains KERNEL")
     ap.add_argument("--trace-summary", metavar="TRACE_DIR",
                     help="summarise a rocprofv3 --kernel-trace run")
     args = ap.parse_args()
     if args.traffic_summary:
+        if len(args.traffic_summary) not in (2, 3):
+            ap.error("--traffic-summary takes FETCH_DIR WRITE_DIR [WORKLOAD]")
         return traffic_summary(*args.traffic_summary)
     if args.counter_summary:
         return counter_summary(args.counter_summary[0], args.counter_summary[1:])
@@ -1031,8 +1073,7 @@ def main() -> int:
     wl = set() if args.only_headline else set(args.workloads.split(","))
     if "ragged" in wl:
         # C2 ragged: the survey's draw rule, rng(seed 2).integers(1024, 8193, 16)
-        import numpy as np
-        lens = np.random.default_rng(2).integers(1024, 8192 + 1, 16).astype(np.int32).tolist()
+        lens = _c2_ragged_lens()
         cr = bench_decode(torch, ops, lib, batch=16, ctx=8192, hq=32, hkv=8, d=128,
                           dtype=torch.float16, gate=False, steps=steps, warmup=warmup, seed=2,
                           seq_lens=lens)
