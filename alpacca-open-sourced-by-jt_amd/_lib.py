@@ -26,6 +26,7 @@ SIGNATURES = {
     "alpx_abi_version": (_c_int, []),
     "alpx_last_error": (ctypes.c_char_p, []),
     "alpx_device_arch": (_c_int, [_c_int, ctypes.c_char_p, _c_int]),
+    "alpx_host_device_pointer": (_c_int, [_c_ptr, ctypes.POINTER(_c_ptr)]),
     "alpx_kv_append": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_i64, _c_int, _c_int,
                                 _c_int, _c_int, _c_int, _c_i64, _c_ptr, _c_ptr]),
     "alpx_kv_append_paged": (_c_int, [_c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_ptr, _c_int, _c_int,
@@ -250,23 +251,54 @@ def device_arch(index: int) -> str:
     return buf.value.decode()
 
 
+_dtype_codes: dict = {}
+
+
+def host_device_pointer(host_address: int):
+    """Device address of page-locked host memory, or None when the runtime
+    does not map it (alpx_host_device_pointer)."""
+    dev = ctypes.c_void_p()
+    if lib().alpx_host_device_pointer(host_address, ctypes.byref(dev)) != OK or not dev.value:
+        return None
+    return dev.value
+
+
 def dtype_code(torch, dtype) -> int:
-    if dtype == torch.float32:
-        return F32
-    if dtype == torch.float16:
-        return F16
-    if dtype == torch.bfloat16:
-        return BF16
+    code = _dtype_codes.get(dtype)
+    if code is not None:
+        return code
+    if not _dtype_codes:
+        _dtype_codes.update({torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16})
+        if dtype in _dtype_codes:
+            return _dtype_codes[dtype]
     raise TypeError(f"unsupported dtype {dtype}")
 
 
+_raw_stream = None
+
+
+def current_stream(index: int) -> int:
+    """hipStream_t of torch's current stream on device ``index`` (an int)."""
+    global _raw_stream
+    if _raw_stream is None:
+        import torch
+        _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", False)
+    if _raw_stream is not False:
+        return _raw_stream(index)
+    import torch
+    return int(torch.cuda.current_stream(index).cuda_stream)
+
+
 def stream_handle(torch, device) -> int:
-    """hipStream_t of torch's current stream on ``device``.  Uses torch's raw
-    stream query (no Stream object per call) when this torch build has it."""
-    raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)
-    if raw is not None:
-        index = device.index if hasattr(device, "index") else device
-        return int(raw(torch.cuda.current_device() if index is None else int(index)))
+    """hipStream_t of torch's current stream on ``device`` (a torch.device,
+    an index or a device string).  Uses torch's raw stream query (no Stream
+    object per call) when this torch build has it."""
+    global _raw_stream
+    index = getattr(device, "index", device)
+    if _raw_stream is None:
+        _raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", False)
+    if _raw_stream is not False and (index is None or type(index) is int):
+        return _raw_stream(torch.cuda.current_device() if index is None else index)
     return int(torch.cuda.current_stream(device).cuda_stream)
 
 
@@ -289,11 +321,18 @@ def workspace(torch, device, nbytes: int):
     graphs should be captured after the largest workspace a process needs
     has been sized (one eager call of each shape), though a later growth
     never frees the buffer a graph holds."""
-    key = str(device)
+    key = _device_keys.get(device)
+    if key is None:
+        key = _device_keys.setdefault(device, str(device))
     buf = _workspaces.get(key)
-    if buf is None or buf.numel() < nbytes:
+    if buf is None or _workspace_bytes[key] < nbytes:
         if buf is not None:
             _retired.setdefault(key, []).append(buf)
         buf = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device)
         _workspaces[key] = buf
+        _workspace_bytes[key] = buf.numel()
     return buf
+
+
+_device_keys: dict = {}     # device (object or string) -> str(device)
+_workspace_bytes: dict = {}  # str(device) -> bytes of _workspaces[str(device)]

@@ -18,23 +18,79 @@ def _torch():
     return torch
 
 
+def _run(fn, args, device, out):
+    """Enqueues one C-ABI call (argument list with the stream last) on torch's
+    current stream of ``device`` and returns ``out``."""
+    args[-1] = _lib.stream_handle(_torch(), device)
+    rc = fn(*args)
+    if rc:
+        _lib.check(rc)
+    return out
+
+
+class PreparedCall:
+    """One library call whose buffers were validated and whose C-ABI argument
+    list was packed once, for decode loops that call a step many times
+    without capturing a graph.  Each call enqueues the same launch as the
+    immediate entry point on torch's current stream of the device (read at
+    call time) and returns ``out``.  The object holds a reference to every
+    buffer it was prepared with (including the library workspace it was
+    sized for), so their device pointers stay valid: their contents may
+    change between calls (new query rows, device lengths, an advanced
+    state), their shapes, dtypes and storage must not (no ``resize_`` or
+    ``set_``).  Calls of one object must be ordered on one stream, as the
+    immediate calls sharing a workspace are."""
+
+    __slots__ = ("_fn", "_args", "_index", "_buffers", "out")
+
+    def __init__(self, fn, args, device, buffers, out):
+        self._fn = fn
+        self._args = list(args)
+        self._index = device.index
+        self._buffers = buffers
+        self.out = out
+
+    def __call__(self):
+        args = self._args
+        args[-1] = _lib.current_stream(self._index)
+        rc = self._fn(*args)
+        if rc:
+            _lib.check(rc)
+        return self.out
+
+
+def _kv_append_call(key_cache, value_cache, key, value, *, position=None, positions=None):
+    torch = _torch()
+    capacity, batch, kv_heads, key_dim = key_cache.shape
+    value_dim = value_cache.shape[3]
+    device = key_cache.device
+    pos_ptr = None
+    if positions is not None:
+        if positions.dtype != torch.int32 or positions.device != device or \
+                not positions.is_contiguous():
+            positions = positions.to(device=device, dtype=torch.int32).contiguous()
+        pos_ptr = positions.data_ptr()
+    args = [key_cache.data_ptr(), value_cache.data_ptr(), key.data_ptr(), value.data_ptr(),
+            _lib.dtype_code(torch, key_cache.dtype), capacity, batch, kv_heads, key_dim,
+            value_dim, key.shape[0], 0 if position is None else int(position), pos_ptr, None]
+    return (_lib.lib().alpx_kv_append, args, device, None,
+            (key_cache, value_cache, key, value, positions))
+
+
 def kv_append(key_cache, value_cache, key, value, *, position=None, positions=None):
     """Append ``tokens`` rows ``key/value [T, B, Hkv, D]`` to caches
     ``[C, B, Hkv, D]`` at ``position + t`` (or ``positions[b] + t``)."""
-    torch = _torch()
-    capacity, batch, kv_heads, key_dim = (int(x) for x in key_cache.shape)
-    value_dim = int(value_cache.shape[3])
-    tokens = int(key.shape[0])
-    pos_ptr = None
-    if positions is not None:
-        positions = positions.to(device=key_cache.device, dtype=torch.int32).contiguous()
-        pos_ptr = positions.data_ptr()
-    rc = _lib.lib().alpx_kv_append(
-        key_cache.data_ptr(), value_cache.data_ptr(), key.data_ptr(), value.data_ptr(),
-        _lib.dtype_code(torch, key_cache.dtype), capacity, batch, kv_heads, key_dim,
-        value_dim, tokens, 0 if position is None else int(position), pos_ptr,
-        _lib.stream_handle(torch, key_cache.device))
-    _lib.check(rc)
+    fn, args, device, _, _ = _kv_append_call(key_cache, value_cache, key, value,
+                                             position=position, positions=positions)
+    _run(fn, args, device, None)
+
+
+def prepare_kv_append(key_cache, value_cache, key, value, *, position=None, positions=None):
+    """``kv_append`` as a PreparedCall (device ``positions`` may change
+    between calls)."""
+    fn, args, device, _, buffers = _kv_append_call(key_cache, value_cache, key, value,
+                                                   position=position, positions=positions)
+    return PreparedCall(fn, args, device, buffers, None)
 
 
 def kv_append_paged(key_pages, value_pages, block_table, key, value, *, position=None,
@@ -220,35 +276,82 @@ def kv_import_paged(key_rows, value_rows, key_pages, value_pages, block_table, *
     _lib.check(rc)
 
 
-def decode(q, key_cache, value_cache, *, length, k_strides, v_strides, batch, kv_heads,
-           seq_lens=None, gate=None, scale=None, out_dtype=None, out=None):
-    """Split-K GQA decode.  ``q [B, Hq, D]`` contiguous; K/V addressed by
-    (pos, batch, head) element strides; returns ``[B, Hq, Dv]``."""
+def _decode_call(q, key_cache, value_cache, *, length, k_strides, v_strides, batch, kv_heads,
+                 seq_lens=None, gate=None, scale=None, out_dtype=None, out=None,
+                 out_address=None):
+    """(C function, argument list with the stream last, device, out, buffers)
+    of one alpx_decode_gqa call.  ``out_address``: the device address the
+    output is written to when it is not ``out``'s own (page-locked host
+    memory mapped for the device, alpx_host_device_pointer)."""
     torch = _torch()
-    bsz, q_heads, key_dim = (int(x) for x in q.shape)
-    value_dim = int(value_cache.shape[-1])
+    bsz, q_heads, key_dim = q.shape
+    value_dim = value_cache.shape[-1]
+    device = q.device
     if scale is None:
         scale = 1.0 / math.sqrt(key_dim)
-    out_dtype = q.dtype if out_dtype is None else out_dtype
     if out is None:
-        out = torch.empty((bsz, q_heads, value_dim), dtype=out_dtype, device=q.device)
+        out = torch.empty((bsz, q_heads, value_dim), dtype=q.dtype if out_dtype is None
+                          else out_dtype, device=device)
     lens_ptr = None
     if seq_lens is not None:
-        seq_lens = seq_lens.to(device=q.device, dtype=torch.int32).contiguous()
+        if seq_lens.dtype != torch.int32 or seq_lens.device != device or \
+                not seq_lens.is_contiguous():
+            seq_lens = seq_lens.to(device=device, dtype=torch.int32).contiguous()
         lens_ptr = seq_lens.data_ptr()
     L = _lib.lib()
-    nbytes = L.alpx_decode_workspace_bytes(batch, q_heads, kv_heads, value_dim, int(length))
-    if nbytes == 0:
-        raise ValueError("invalid decode sizes")
-    ws = _lib.workspace(torch, q.device, nbytes)
-    rc = L.alpx_decode_gqa(
-        q.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(), lens_ptr, int(length),
-        None if gate is None else gate.data_ptr(), out.data_ptr(), ws.data_ptr(), ws.numel(),
-        batch, q_heads, kv_heads, key_dim, value_dim, *k_strides, *v_strides, float(scale),
-        _lib.dtype_code(torch, q.dtype), _lib.dtype_code(torch, out.dtype),
-        _lib.stream_handle(torch, q.device))
-    _lib.check(rc)
-    return out
+    length = int(length)
+    sizes = (batch, q_heads, kv_heads, value_dim, length)
+    nbytes = _decode_ws_bytes.get(sizes)
+    if nbytes is None:
+        nbytes = L.alpx_decode_workspace_bytes(*sizes)
+        if nbytes == 0:
+            raise ValueError("invalid decode sizes")
+        _decode_ws_bytes[sizes] = nbytes
+    ws = _lib.workspace(torch, device, nbytes)
+    args = [q.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(), lens_ptr, length,
+            None if gate is None else gate.data_ptr(),
+            out.data_ptr() if out_address is None else out_address, ws.data_ptr(), ws.numel(),
+            batch, q_heads, kv_heads, key_dim, value_dim, *k_strides, *v_strides, float(scale),
+            _lib.dtype_code(torch, q.dtype), _lib.dtype_code(torch, out.dtype), None]
+    return L.alpx_decode_gqa, args, device, out, (q, key_cache, value_cache, seq_lens, gate, ws)
+
+
+def decode(q, key_cache, value_cache, **kwargs):
+    """Split-K GQA decode.  ``q [B, Hq, D]`` contiguous; K/V addressed by
+    (pos, batch, head) element strides (keywords: length, k_strides,
+    v_strides, batch, kv_heads, seq_lens, gate, scale, out_dtype, out);
+    returns ``[B, Hq, Dv]``."""
+    fn, args, device, out, _ = _decode_call(q, key_cache, value_cache, **kwargs)
+    return _run(fn, args, device, out)
+
+
+class PreparedDecode(PreparedCall):
+    """A prepared ``decode`` whose call may name the rows to attend:
+    ``call(length)`` attends rows ``0 .. length - 1`` (at most the length it
+    was prepared with, which sized its workspace) from this call on."""
+
+    __slots__ = ("_max_length",)
+
+    def __call__(self, length=None):
+        if length is not None:
+            length = int(length)
+            if not 0 < length <= self._max_length:
+                raise ValueError(f"attention length {length} outside [1, {self._max_length}]")
+            self._args[4] = length
+        return PreparedCall.__call__(self)
+
+
+def prepare_decode(q, key_cache, value_cache, **kwargs):
+    """``decode`` as a PreparedDecode (same keywords)."""
+    fn, args, device, out, buffers = _decode_call(q, key_cache, value_cache, **kwargs)
+    call = PreparedDecode(fn, args, device, buffers + (out,), out)
+    call._max_length = args[4]
+    return call
+
+
+# alpx_decode_workspace_bytes per (batch, q_heads, kv_heads, value_dim, length):
+# a pure function of the sizes, asked once per shape.
+_decode_ws_bytes: dict = {}
 
 
 def sigmoid_gate(values, gate, out_dtype=None):
@@ -314,22 +417,33 @@ def prefill(q, key, value, *, pos0, scale=None, window=0, kv_start=0, kv_tokens=
     return out
 
 
-def gdn_step(state, q, k, v, beta, log_decay, out_dtype=None):
+def _gdn_step_call(state, q, k, v, beta, log_decay, out_dtype=None, out=None):
+    torch = _torch()
+    bsz, hv, dv, dk = state.shape
+    device = state.device
+    if out is None:
+        out = torch.empty((bsz, hv, dv), dtype=q.dtype if out_dtype is None else out_dtype,
+                          device=device)
+    args = [state.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(),
+            log_decay.data_ptr(), out.data_ptr(), bsz, q.shape[1], hv, dk, dv,
+            _lib.dtype_code(torch, q.dtype), _lib.dtype_code(torch, out.dtype), None]
+    return _lib.lib().alpx_gdn_step, args, device, out, (state, q, k, v, beta, log_decay)
+
+
+def gdn_step(state, q, k, v, beta, log_decay, out_dtype=None, out=None):
     """One GDN decode step in place on ``state [B, Hv, Dv, Dk]`` (fp32);
     q/k ``[B, Hk, Dk]``, v ``[B, Hv, Dv]``, beta/log_decay ``[B, Hv]`` fp32.
-    Returns ``[B, Hv, Dv]``."""
-    torch = _torch()
-    bsz, hv, dv, dk = (int(x) for x in state.shape)
-    hk = int(q.shape[1])
-    out = torch.empty((bsz, hv, dv), dtype=q.dtype if out_dtype is None else out_dtype,
-                      device=state.device)
-    rc = _lib.lib().alpx_gdn_step(
-        state.data_ptr(), q.data_ptr(), k.data_ptr(), v.data_ptr(), beta.data_ptr(),
-        log_decay.data_ptr(), out.data_ptr(), bsz, hk, hv, dk, dv,
-        _lib.dtype_code(torch, q.dtype), _lib.dtype_code(torch, out.dtype),
-        _lib.stream_handle(torch, state.device))
-    _lib.check(rc)
-    return out
+    Returns ``[B, Hv, Dv]`` (``out`` when given: a contiguous buffer of
+    that shape, already checked by the caller)."""
+    fn, args, device, out, _ = _gdn_step_call(state, q, k, v, beta, log_decay, out_dtype, out)
+    return _run(fn, args, device, out)
+
+
+def prepare_gdn_step(state, q, k, v, beta, log_decay, out_dtype=None, out=None):
+    """``gdn_step`` as a PreparedCall."""
+    fn, args, device, out, buffers = _gdn_step_call(state, q, k, v, beta, log_decay, out_dtype,
+                                                    out)
+    return PreparedCall(fn, args, device, buffers + (out,), out)
 
 
 def gdn_chunk(state, q, k, v, beta, log_decay, out_dtype=None):
@@ -704,34 +818,51 @@ def recurrent_prefill_prep(current, conv_weight, conv_history, beta_logits, alph
     return q, k, v, beta, g
 
 
-def recurrent_step(current, conv_weight, conv_history, gate, beta_logits, alpha_logits, dt_bias,
-                   ssm_a, norm_weight, state, *, key_heads, key_dim, eps, weight_layout="kc",
-                   out_dtype=None):
-    """Fused Qwen3.5 recurrent-layer token (all fp32 inputs); updates
-    ``conv_history [B, K-1, C]`` and ``state [B, Hv, Dv, Dk]`` in place and
-    returns ``[B, Hv * Dv]``."""
+def _recurrent_step_call(current, conv_weight, conv_history, gate, beta_logits, alpha_logits,
+                         dt_bias, ssm_a, norm_weight, state, *, key_heads, key_dim, eps,
+                         weight_layout="kc", out_dtype=None, out=None):
     torch = _torch()
-    bsz, hv, dv, dk = (int(x) for x in state.shape)
-    channels = int(current.shape[1])
+    bsz, hv, dv, dk = state.shape
+    channels = current.shape[1]
     if weight_layout == "kc":
-        kernel = int(conv_weight.shape[0])
+        kernel = conv_weight.shape[0]
         tap_stride, ch_stride = channels, 1
     else:
-        kernel = int(conv_weight.shape[1])
+        kernel = conv_weight.shape[1]
         tap_stride, ch_stride = 1, kernel
-    out = torch.empty((bsz, hv * dv), dtype=torch.float32 if out_dtype is None else out_dtype,
-                      device=state.device)
+    device = state.device
+    if out is None:
+        out = torch.empty((bsz, hv * dv),
+                          dtype=torch.float32 if out_dtype is None else out_dtype, device=device)
     L = _lib.lib()
-    nbytes = L.alpx_recurrent_step_workspace_bytes(bsz, int(key_heads), hv, int(key_dim), dv)
+    key_heads, key_dim = int(key_heads), int(key_dim)
+    nbytes = L.alpx_recurrent_step_workspace_bytes(bsz, key_heads, hv, key_dim, dv)
     if nbytes == 0:
         raise ValueError("invalid recurrent step sizes")
-    ws = _lib.workspace(torch, state.device, nbytes)
-    rc = L.alpx_recurrent_step(
-        current.data_ptr(), conv_weight.data_ptr(), tap_stride, ch_stride,
-        None if conv_history is None else conv_history.data_ptr(), kernel, gate.data_ptr(),
-        beta_logits.data_ptr(), alpha_logits.data_ptr(), dt_bias.data_ptr(), ssm_a.data_ptr(),
-        norm_weight.data_ptr(), state.data_ptr(), out.data_ptr(), ws.data_ptr(), ws.numel(),
-        bsz, int(key_heads), hv, int(key_dim), dv, float(eps),
-        _lib.dtype_code(torch, out.dtype), _lib.stream_handle(torch, state.device))
-    _lib.check(rc)
-    return out
+    ws = _lib.workspace(torch, device, nbytes)
+    args = [current.data_ptr(), conv_weight.data_ptr(), tap_stride, ch_stride,
+            None if conv_history is None else conv_history.data_ptr(), kernel, gate.data_ptr(),
+            beta_logits.data_ptr(), alpha_logits.data_ptr(), dt_bias.data_ptr(),
+            ssm_a.data_ptr(), norm_weight.data_ptr(), state.data_ptr(), out.data_ptr(),
+            ws.data_ptr(), ws.numel(), bsz, key_heads, hv, key_dim, dv, float(eps),
+            _lib.dtype_code(torch, out.dtype), None]
+    buffers = (current, conv_weight, conv_history, gate, beta_logits, alpha_logits, dt_bias,
+               ssm_a, norm_weight, state, ws)
+    return L.alpx_recurrent_step, args, device, out, buffers
+
+
+def recurrent_step(*args, **kwargs):
+    """Fused Qwen3.5 recurrent-layer token (all fp32 inputs): arguments
+    current, conv_weight, conv_history, gate, beta_logits, alpha_logits,
+    dt_bias, ssm_a, norm_weight, state and the keywords key_heads, key_dim,
+    eps, weight_layout ("kc": [K, C] weights, else [C, K]), out_dtype, out.
+    Updates ``conv_history [B, K-1, C]`` and ``state [B, Hv, Dv, Dk]`` in
+    place and returns ``[B, Hv * Dv]``."""
+    fn, call_args, device, out, _ = _recurrent_step_call(*args, **kwargs)
+    return _run(fn, call_args, device, out)
+
+
+def prepare_recurrent_step(*args, **kwargs):
+    """``recurrent_step`` as a PreparedCall (same arguments)."""
+    fn, call_args, device, out, buffers = _recurrent_step_call(*args, **kwargs)
+    return PreparedCall(fn, call_args, device, buffers + (out,), out)

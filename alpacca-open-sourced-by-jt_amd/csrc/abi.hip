@@ -113,4 +113,18 @@ int alpx_device_arch(int device, char* buf, int buf_len) {
   return ALPX_OK;
 }
 
+int alpx_host_device_pointer(void* host, void** device_pointer) {
+  if (host == nullptr || device_pointer == nullptr)
+    return alpx::fail(ALPX_EINVAL, "alpx_host_device_pointer: null pointer");
+  void* dev = nullptr;
+  hipError_t err = hipHostGetDevicePointer(&dev, host, 0);
+  if (err != hipSuccess || dev == nullptr) {
+    (void)hipGetLastError();  // leave no sticky error for the caller's next HIP call
+    return alpx::fail(ALPX_EINVAL, "alpx_host_device_pointer: %p is not page-locked HIP host "
+                                   "memory (%s)", host, hipGetErrorString(err));
+  }
+  *device_pointer = dev;
+  return ALPX_OK;
+}
+
 }  // extern "C"

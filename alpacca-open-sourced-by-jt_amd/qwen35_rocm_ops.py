@@ -227,6 +227,15 @@ class Qwen35RocmOps:
             raise ValueError(f"{name} must be contiguous")
         return value
 
+    def _out_buffer(self, out: Any, shape: tuple, dtype: Any, name: str) -> None:
+        """An ``out=`` buffer: a contiguous tensor of ``shape`` and ``dtype`` on
+        this device."""
+        self._tensor(out, name)
+        if out.dtype != dtype:
+            raise TypeError(f"{name} must use {dtype}")
+        if out.shape != shape:
+            raise ValueError(f"{name} has {_shape(out)}, expected {tuple(shape)}")
+
     @staticmethod
     def _same_shape(left: Any, right: Any, what: str) -> None:
         if _shape(left) != _shape(right):
@@ -342,7 +351,31 @@ class Qwen35RocmOps:
 
     def online_attention(self, query: Any, key_cache: Any, value_cache: Any, *, length: int,
                          scale: float | None = None, seq_lens: Any = None, gate: Any = None,
-                         out_dtype: Any = None) -> Any:
+                         out_dtype: Any = None, out: Any = None) -> Any:
+        """Single-token GQA decode over the ROCm cache layout
+        (qwen35_rocm_ops.py:502-564).  Extensions: fp16 / bf16 tensors,
+        device ``seq_lens [B]`` (ragged batch), the sigmoid output ``gate``,
+        ``out_dtype`` and an ``out`` buffer."""
+        return _ops.decode(query, key_cache, value_cache,
+                           **self._online_attention_args(query, key_cache, value_cache, length,
+                                                         scale, seq_lens, gate, out_dtype, out))
+
+    def prepare_online_attention(self, query: Any, key_cache: Any, value_cache: Any, *,
+                                 length: int, scale: float | None = None, seq_lens: Any = None,
+                                 gate: Any = None, out_dtype: Any = None,
+                                 out: Any = None) -> Any:
+        """``online_attention`` validated and packed once (extension): returns a
+        call object whose every call runs the decode on the buffers given here
+        (their contents, e.g. the query row and device ``seq_lens``, may change
+        between calls; their shapes and storage may not) and returns the
+        output buffer.  For decode loops that do not capture graphs."""
+        return _ops.prepare_decode(
+            query, key_cache, value_cache,
+            **self._online_attention_args(query, key_cache, value_cache, length, scale, seq_lens,
+                                          gate, out_dtype, out))
+
+    def _online_attention_args(self, query, key_cache, value_cache, length, scale, seq_lens,
+                               gate, out_dtype, out):
         query = self._tensor(query, "attention query", dimensions=3)
         key_cache = self._tensor(key_cache, "attention key cache", dimensions=4)
         value_cache = self._tensor(value_cache, "attention value cache", dimensions=4)
@@ -374,12 +407,15 @@ class Qwen35RocmOps:
                 seq_lens = self.torch.tensor(host, dtype=self.torch.int32, device=self.device)
             elif _shape(seq_lens) != (batch,):
                 raise ValueError("seq_lens must hold one length per sequence")
+        if out is not None:
+            self._out_buffer(out, (batch, query_heads, value_shape[3]),
+                             query.dtype if out_dtype is None else out_dtype,
+                             "attention output")
         c, b, h = batch * kv_heads * key_width, kv_heads * key_width, key_width
         cv, bv, hv = batch * kv_heads * value_shape[3], kv_heads * value_shape[3], value_shape[3]
-        return _ops.decode(query, key_cache, value_cache, length=length, k_strides=(c, b, h),
-                           v_strides=(cv, bv, hv), batch=batch, kv_heads=kv_heads,
-                           seq_lens=seq_lens, gate=gate, scale=scale_value,
-                           out_dtype=out_dtype)
+        return dict(length=length, k_strides=(c, b, h), v_strides=(cv, bv, hv), batch=batch,
+                    kv_heads=kv_heads, seq_lens=seq_lens, gate=gate, scale=scale_value,
+                    out_dtype=out_dtype, out=out)
 
     def append_online_attention_(self, query: Any, key: Any, value: Any, key_cache: Any,
                                  value_cache: Any, *, position: int,
@@ -508,11 +544,30 @@ class Qwen35RocmOps:
         return state, query, key, value, beta, log_decay
 
     def gated_delta_net_step_(self, state: Any, query: Any, key: Any, value: Any, beta: Any,
-                              log_decay: Any) -> Any:
+                              log_decay: Any, *, out: Any = None) -> Any:
         """One GDN step in place on ``state [B, Hv, Dv, Dk]``
-        (qwen35_rocm_ops.py:362-407); value head h reads key head h % Hk."""
+        (qwen35_rocm_ops.py:362-407); value head h reads key head h % Hk.
+        ``out`` (extension): a contiguous ``[B, Hv, Dv]`` buffer of the
+        query dtype on the same device that receives the result (no
+        allocation per step); it is returned."""
         args = self._gdn_checks(state, query, key, value, beta, log_decay, chunk=False)
-        return _ops.gdn_step(*args)
+        if out is not None:
+            self._out_buffer(out, (state.shape[0], state.shape[1], state.shape[2]), query.dtype,
+                             "GDN output")
+        return _ops.gdn_step(*args, out=out)
+
+    def prepare_gated_delta_net_step_(self, state: Any, query: Any, key: Any, value: Any,
+                                      beta: Any, log_decay: Any, *, out: Any = None) -> Any:
+        """``gated_delta_net_step_`` validated and packed once (extension):
+        returns a call object whose every call advances ``state`` in place by
+        one step from the current contents of the buffers given here and
+        returns the output buffer (allocated once when ``out`` is None).  For
+        decode loops that do not capture graphs."""
+        args = self._gdn_checks(state, query, key, value, beta, log_decay, chunk=False)
+        if out is not None:
+            self._out_buffer(out, (state.shape[0], state.shape[1], state.shape[2]), query.dtype,
+                             "GDN output")
+        return _ops.prepare_gdn_step(*args, out=out)
 
     def gated_delta_net_chunk_(self, state: Any, query: Any, key: Any, value: Any, beta: Any,
                                log_decay: Any, *, out_dtype: Any = None) -> Any:
@@ -776,7 +831,7 @@ class Qwen35RocmOps:
                               convolution_weights: Any, gate: Any, beta_logits: Any,
                               alpha_logits: Any, dt_bias: Any, ssm_a: Any, norm_weight: Any, *,
                               key_heads: int, key_dimension: int, epsilon: float,
-                              out_dtype: Any = None) -> Any:
+                              out_dtype: Any = None, out: Any = None) -> Any:
         """One token of the Qwen3.5 recurrent (GDN) layer after its
         projections, fused (extension; the chain of qwen35_numpy.py:63-131):
         convolution + SiLU of ``mixed [B, 2 Hk Dk + Hv Dv]`` against the
@@ -784,6 +839,30 @@ class Qwen35RocmOps:
         GDN step on the workspace's delta state and the gated RMSNorm with
         ``gate [B, Hv * Dv]``.  Both workspace tensors advance in place.
         Returns ``[B, Hv * Dv]``."""
+        args, kwargs = self._recurrent_step_args(
+            workspace, mixed, convolution_weights, gate, beta_logits, alpha_logits, dt_bias,
+            ssm_a, norm_weight, key_heads, key_dimension, epsilon, out_dtype, out)
+        return _ops.recurrent_step(*args, **kwargs)
+
+    def prepare_recurrent_layer_step_(self, workspace: RocmRecurrentWorkspace, mixed: Any,
+                                      convolution_weights: Any, gate: Any, beta_logits: Any,
+                                      alpha_logits: Any, dt_bias: Any, ssm_a: Any,
+                                      norm_weight: Any, *, key_heads: int, key_dimension: int,
+                                      epsilon: float, out_dtype: Any = None,
+                                      out: Any = None) -> Any:
+        """``recurrent_layer_step_`` validated and packed once (extension):
+        returns a call object whose every call runs one token from the current
+        contents of the buffers given here (advancing the workspace in place)
+        and returns the output buffer.  For decode loops that do not capture
+        graphs."""
+        args, kwargs = self._recurrent_step_args(
+            workspace, mixed, convolution_weights, gate, beta_logits, alpha_logits, dt_bias,
+            ssm_a, norm_weight, key_heads, key_dimension, epsilon, out_dtype, out)
+        return _ops.prepare_recurrent_step(*args, **kwargs)
+
+    def _recurrent_step_args(self, workspace, mixed, convolution_weights, gate, beta_logits,
+                             alpha_logits, dt_bias, ssm_a, norm_weight, key_heads,
+                             key_dimension, epsilon, out_dtype, out):
         history = self._fp32(workspace.convolution_history, "convolution history",
                              dimensions=3)
         state = self._fp32(workspace.delta_state, "GDN state", dimensions=4)
@@ -819,11 +898,14 @@ class Qwen35RocmOps:
             raise ValueError("time-step bias and ssm_a must match value heads")
         if _shape(norm_weight) != (value_width,):
             raise ValueError("RMSNorm weight must match the input's final dimension")
-        return _ops.recurrent_step(mixed, weights, history if kernel > 1 else None, gate,
-                                   beta_logits, alpha_logits, dt_bias, ssm_a, norm_weight, state,
-                                   key_heads=key_heads, key_dim=key_dimension,
-                                   eps=_positive_finite("epsilon", epsilon),
-                                   out_dtype=out_dtype)
+        if out is not None:
+            self._out_buffer(out, (batch, value_heads * value_width),
+                             self.torch.float32 if out_dtype is None else out_dtype,
+                             "recurrent output")
+        return ((mixed, weights, history if kernel > 1 else None, gate, beta_logits,
+                 alpha_logits, dt_bias, ssm_a, norm_weight, state),
+                dict(key_heads=key_heads, key_dim=key_dimension,
+                     eps=_positive_finite("epsilon", epsilon), out_dtype=out_dtype, out=out))
 
     # ------------------------------------------------------------ paged K/V
 

@@ -275,6 +275,10 @@ def bench_decode(torch, ops, lib, *, batch, ctx, hq, hkv, d, dtype, gate, steps,
                                                                  lib.T_DECODE_COMBINE))
     graph_ms = _graph_replay_ms(torch, fn, steps, warmup) if graph else None
     device_ms = _graph_event_ms(torch, fn) if graph else None
+    prepared_ms = None
+    if graph:  # the latency-bound step as a decode loop without graphs runs it
+        prepared = ops.prepare_online_attention(q, K, V, length=ctx, gate=gt, seq_lens=lens_dev)
+        prepared_ms = _timed_steps(torch, prepared, steps, warmup)
     es = q.element_size()
     rows = batch * ctx if seq_lens is None else int(sum(seq_lens))
     kv_bytes = 2 * rows * hkv * d * es
@@ -287,6 +291,7 @@ def bench_decode(torch, ops, lib, *, batch, ctx, hq, hkv, d, dtype, gate, steps,
         "combine_ms": comb_ms,
         "graph_ms": graph_ms,
         "device_ms": device_ms,
+        "prepared_ms": prepared_ms,
         "split_alg_bytes": kv_bytes + q_bytes,
         "split_gbs": (kv_bytes + q_bytes) / (split_ms * 1e-3) / 1e9,
         "step_bytes": step_bytes,
@@ -401,12 +406,15 @@ def bench_gdn(torch, ops, lib, *, steps, warmup, seed=5):
     (dk_ms,) = _event_kernel_ms(torch, lib, step, n_dec, (lib.T_GDN_STEP,))
     dec_graph_ms = _graph_replay_ms(torch, step, n_dec, 16)
     dec_device_ms = _graph_event_ms(torch, step)
+    prepared = ops.prepare_gated_delta_net_step_(S, q1, k1, v1, b1, g1)
+    dec_prepared_ms = _timed_steps(torch, prepared, n_dec, 16)
     step_bytes = 2 * hv * dv * dk * 4 + (2 * hk * dk + 2 * hv * dv) * 2
     return {"prefill_ms": ms, "prefill_kernel_ms": k_ms, "prefill_flops": flops,
             "prefill_tflops": flops / (k_ms * 1e-3) / 1e12,
             "prefill_f32_inputs_ms": ms32, "prefill_f32_inputs_kernel_ms": k_ms32,
             "decode_us_per_step": dec_ms * 1e3, "decode_kernel_us": dk_ms * 1e3,
             "decode_graph_us_per_step": dec_graph_ms * 1e3,
+            "decode_prepared_us_per_step": dec_prepared_ms * 1e3,
             "decode_device_us_per_step": dec_device_ms * 1e3,
             "decode_step_bytes": step_bytes,
             "decode_kernel_gbs": step_bytes / (dec_device_ms * 1e-3) / 1e9}
@@ -481,6 +489,10 @@ def bench_layers(torch, ops, lib, *, steps, warmup, seed=6):
     r_ms = _timed_steps(torch, rec_step, steps, warmup)
     (rk_ms,) = _event_kernel_ms(torch, lib, rec_step, steps, (lib.T_RECURRENT_STEP,))
     rg_ms = _graph_replay_ms(torch, rec_step, steps, warmup)
+    rec_prepared = ops.prepare_recurrent_layer_step_(ws, mixed, cw, gate, bl, al, dt, ssm, nw,
+                                                     key_heads=hk, key_dimension=dk,
+                                                     epsilon=1e-6)
+    rp_ms = _timed_steps(torch, rec_prepared, steps, warmup)
     r_bytes = (2 * bsz * hv * dv * dk * 4 + 2 * bsz * (kern - 1) * chn * 4 + kern * chn * 4
                + bsz * chn * 4 + 2 * bsz * hv * dv * 4 + 2 * bsz * hv * 4 + 2 * hv * 4 + dv * 4)
     return {
@@ -496,6 +508,7 @@ def bench_layers(torch, ops, lib, *, steps, warmup, seed=6):
                                   a_bytes, ak_ms)},
         "recurrent_layer_c5": {
             "us_per_step": round(r_ms * 1e3, 2),
+            "prepared_us_per_step": round(rp_ms * 1e3, 2),
             "graph_us_per_step": round(rg_ms * 1e3, 2),
             "kernel_us": round(rk_ms * 1e3, 2),
             "step_bytes": r_bytes,
@@ -504,6 +517,65 @@ def bench_layers(torch, ops, lib, *, steps, warmup, seed=6):
             "roofline": _roofline("recurrent_rows_kernel + recurrent_finish_kernel", "hbm",
                                   r_bytes, rk_ms)},
     }
+
+
+def bench_dropin(torch, ops, *, steps, warmup, seed=9):
+    """The NumPy-facing llama decode drop-in (kernels.attention_decode,
+    kernels.py:1183-1200) for one C2-shaped token: one sequence, 32 query /
+    8 kv heads, head_dim 128, 8192 rows, fp32 host cache (the reference's
+    cache dtype).  PCIe included: (1) the upload form, which copies the
+    host K/V rows to the device on every call; (2) the mirror form
+    (``DeviceKVMirror``, rows kept on the device; per token one pinned
+    upload of q, the new K/V row and the device position and length, the
+    append, the decode, one download of the output); beside them (3) the
+    same decode on device-resident tensors (``online_attention``)."""
+    import numpy as np
+    kern = _mod("kernels")
+    rng = np.random.default_rng(seed)
+    t, n_kv, hd, group = 8192, 8, 128, 4
+    K = rng.standard_normal((t, n_kv, hd)).astype(np.float32)
+    V = rng.standard_normal((t, n_kv, hd)).astype(np.float32)
+    q = rng.standard_normal(n_kv * group * hd).astype(np.float32)
+    inv = 1.0 / math.sqrt(hd)
+
+    def per_call(fn, n, w):
+        for _ in range(w):
+            fn()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        return (time.perf_counter() - t0) / n * 1e3
+
+    upload_ms = per_call(lambda: kern.attention_decode(q, K, V, group, inv), 5, 1)
+    mirror = kern.DeviceKVMirror(t, n_kv, hd)
+    mirror_ms = per_call(lambda: kern.attention_decode(q, K, V, group, inv, mirror=mirror),
+                         steps, warmup)
+    dev = torch.device("cuda")
+    Kd = torch.from_numpy(K).to(dev).reshape(t, 1, n_kv, hd)
+    Vd = torch.from_numpy(V).to(dev).reshape(t, 1, n_kv, hd)
+    qd = torch.from_numpy(q).to(dev).reshape(1, n_kv * group, hd)
+    device_ms = _timed_steps(torch, lambda: ops.online_attention(qd, Kd, Vd, length=t),
+                             steps, warmup)
+
+    def device_token():  # one token whose result the caller waits for
+        ops.online_attention(qd, Kd, Vd, length=t)
+        torch.cuda.synchronize()
+
+    device_sync_ms = per_call(device_token, steps, warmup)
+    step_state = next(iter(mirror._steps.values()))
+    return {"llama_dropin_c2_token_fp32": {
+        "upload_form_ms": round(upload_ms, 4),
+        "mirror_form_ms": round(mirror_ms, 4),
+        "device_step_ms": round(device_ms, 4),
+        "device_step_awaited_ms": round(device_sync_ms, 4),
+        "mirror_over_device": round(mirror_ms / device_ms, 2),
+        "mirror_over_device_awaited": round(mirror_ms / device_sync_ms, 2),
+        "output_written_to_host_by_kernel": bool(step_state["out_mapped"]),
+        "kv_bytes": 2 * t * n_kv * hd * 4,
+        "note": "one sequence, 32/8 heads, head_dim 128, 8192 rows, fp32 host cache; upload "
+                "and mirror forms include PCIe transfers and the host round trip; "
+                "device_step_ms is a back-to-back loop on device tensors, "
+                "device_step_awaited_ms the same decode waited for after each call"}}
 
 
 def bench_paged(torch, ops, lib, c2, *, steps, warmup, seed=8):
@@ -1027,9 +1099,10 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--only-headline", action="store_true",
                     help="C2 uniform only (no other workloads)")
-    ap.add_argument("--workloads", default="ragged,c4,c3,c5,c1,layers,lprefill,paged,append",
+    ap.add_argument("--workloads",
+                    default="ragged,c4,c3,c5,c1,layers,lprefill,paged,append,dropin",
                     help="comma list of secondary workloads to run "
-                         "(ragged, c1, c3, c4, c5, layers, lprefill, paged, append)")
+                         "(ragged, c1, c3, c4, c5, layers, lprefill, paged, append, dropin)")
     ap.add_argument("--pmc-probe", nargs="?", const="c2", default=None, metavar="WORKLOAD",
                     help="run the counter-run workload: copy calibration + c2 (default), c3 "
                          "or c5 steps")
@@ -1137,6 +1210,7 @@ def main() -> int:
             "prefill_f32_inputs_ms": round(c5["prefill_f32_inputs_ms"], 4),
             "prefill_f32_inputs_kernel_ms": round(c5["prefill_f32_inputs_kernel_ms"], 4),
             "decode_us_per_step": round(c5["decode_us_per_step"], 2),
+            "decode_prepared_us_per_step": round(c5["decode_prepared_us_per_step"], 2),
             "decode_graph_us_per_step": round(c5["decode_graph_us_per_step"], 2),
             "decode_event_pair_us": round(c5["decode_kernel_us"], 2),
             "decode_device_us_per_step": round(c5["decode_device_us_per_step"], 2),
@@ -1158,6 +1232,7 @@ def main() -> int:
                           graph=True)
         entry = {
             "us_per_step": round(c1["ms_per_step"] * 1e3, 2),
+            "prepared_us_per_step": round(c1["prepared_ms"] * 1e3, 2),
             "graph_us_per_step": round(c1["graph_ms"] * 1e3, 2),
             "device_us_per_step": round(c1["device_ms"] * 1e3, 2),
             "split_event_pair_us": round(c1["split_ms"] * 1e3, 2),
@@ -1179,6 +1254,8 @@ def main() -> int:
         extra.update(bench_append(torch, lib, c2, steps=steps, warmup=warmup))
     if "lprefill" in wl:
         extra.update(bench_layer_prefill(torch, ops, lib, steps=steps, warmup=warmup))
+    if "dropin" in wl:
+        extra.update(bench_dropin(torch, ops, steps=steps, warmup=warmup))
     extra["c2_combine_ms"] = round(c2["combine_ms"], 5)
 
     cpu = None

@@ -55,6 +55,14 @@ const char* alpx_last_error(void);
 /* gcnArchName of `device` (e.g. "gfx950:sramecc+:xnack-") into a host buffer. */
 int alpx_device_arch(int device, char* buf, int buf_len);
 
+/* Device address of page-locked host memory allocated by the HIP runtime
+ * (hipHostMalloc; torch's pin_memory), so that an entry point can write
+ * its output straight to host memory over PCIe (the NumPy-facing decode
+ * drop-in's mirror writes its 16-KiB output that way instead of a copy
+ * back).  No counterpart in the reference.  ALPX_EINVAL for any other
+ * pointer. */
+int alpx_host_device_pointer(void* host, void** device_pointer);
+
 /*
  * KV-cache append.
  * Replaces Qwen35RocmOps.attention_append_ (qwen35_rocm_ops.py:475-500),

@@ -52,6 +52,14 @@ def test_null_buffers_rejected_without_gpu(pkg):
     assert rc == pkg._lib.EINVAL and "multiple of KV heads" in pkg._lib.last_error()
 
 
+def test_host_device_pointer_rejects_null_without_gpu(pkg):
+    lib = pkg._lib.lib()
+    dev = ctypes.c_void_p()
+    assert lib.alpx_host_device_pointer(None, ctypes.byref(dev)) == pkg._lib.EINVAL
+    assert "null" in pkg._lib.last_error()
+    assert lib.alpx_host_device_pointer(ctypes.c_void_p(64), None) == pkg._lib.EINVAL
+
+
 def test_gated_prefill_rejects_null_gate_without_gpu(pkg):
     lib = pkg._lib.lib()
     fake = ctypes.c_void_p(256)  # never dereferenced: validation fails first
