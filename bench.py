@@ -55,6 +55,7 @@ METRIC = ("decode attn HBM GB/s (% of peak) @8K ctx; "
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "pmc_traffic_decode_split_c2_f16.md")
+TRACE_FILE = os.path.join(ROOT, "profiles", "kernel_trace_all_workloads.md")
 C2_SHAPE = dict(batch=16, ctx=8192, hq=32, hkv=8, d=128)
 SPLIT_KERNEL = "decode_split_mfma"
 COPY_KERNEL = "kv_copy_kernel"
@@ -179,6 +180,25 @@ def _roofline(kernel, bound, work, ms, *, peak=None, traffic=None, work_name="by
     return {"kernel": kernel, "bound": bound, "achieved": round(achieved, 1), "peak": peak,
             "unit": unit, "frac": round(achieved / peak, 4), "traffic": traffic,
             "avg_launch_ms": round(ms, 5), f"alg_{work_name}_per_launch": work}
+
+
+def _trace_avg_ms(name_part, grid):
+    """Average duration (ms) of the kernel whose label contains ``name_part``
+    on ``grid`` (x, y, z blocks) in the committed rocprofv3 kernel-trace
+    summary of the current build, or None.  Kernels of a few microseconds
+    take their roofline from it: a HIP-event pair around each launch adds
+    about the kernel's own duration, and back-to-back launches in a graph
+    overlap a kernel's start with its predecessor's end."""
+    want = ", ".join(str(g) for g in grid)
+    try:
+        with open(TRACE_FILE) as fh:
+            for line in fh:
+                cells = [c.strip() for c in line.strip().strip("|").split("|")]
+                if len(cells) == 6 and name_part in cells[0] and cells[1] == want:
+                    return float(cells[3]) * 1e-3
+    except (OSError, ValueError):
+        return None
+    return None
 
 
 # ------------------------------------------------------------ CPU baselines
@@ -514,8 +534,14 @@ def bench_layers(torch, ops, lib, *, steps, warmup, seed=6):
             "step_bytes": r_bytes,
             "kernel_gbs": round(r_bytes / (rk_ms * 1e-3) / 1e9, 1),
             "frac_hbm": round(r_bytes / (rk_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "roofline": _roofline("recurrent_rows_kernel + recurrent_finish_kernel", "hbm",
-                                  r_bytes, rk_ms)},
+            # two kernels of a few microseconds: durations from the committed
+            # kernel trace of this build, the HIP-event span beside them
+            "roofline": _roofline(
+                "recurrent_rows_kernel + recurrent_finish_kernel (kernel trace)", "hbm",
+                r_bytes, (_trace_avg_ms("recurrent_rows_kernel<1>", (8, 32, 1)) or 0)
+                + (_trace_avg_ms("recurrent_finish_kernel<float>", (24, 1, 1)) or 0) or rk_ms),
+            "roofline_events": _roofline("recurrent_rows_kernel + recurrent_finish_kernel "
+                                         "(event span)", "hbm", r_bytes, rk_ms)},
     }
 
 
@@ -1217,12 +1243,16 @@ def main() -> int:
             "roofline": _roofline("gdn_prep<bf16,128,2> + gdn_apply<bf16,bf16,128>", "mfma",
                                   C5_BASELINE_FLOPS, c5["prefill_kernel_ms"],
                                   work_name="flops"),
-            # a kernel of ~3 us: per-launch event pairs add about its own
-            # duration, so the device time of back-to-back launches in a
-            # graph (events around the replays only) is the duration used
-            "decode_roofline": _roofline("gdn_step_kernel<bf16>", "hbm",
+            # a kernel of ~3 us: its duration comes from the committed kernel
+            # trace of this build; the device time of back-to-back launches
+            # in a graph (events around the replays only) stands beside it
+            "decode_roofline": _roofline("gdn_step_kernel<bf16> (kernel trace)", "hbm",
                                          c5["decode_step_bytes"],
-                                         c5["decode_device_us_per_step"] * 1e-3)}
+                                         _trace_avg_ms("gdn_step_kernel", (8, 32, 1))
+                                         or c5["decode_device_us_per_step"] * 1e-3),
+            "decode_roofline_graph": _roofline("gdn_step_kernel<bf16> (graph, back to back)",
+                                               "hbm", c5["decode_step_bytes"],
+                                               c5["decode_device_us_per_step"] * 1e-3)}
         if host:
             entry["cpu_baseline"] = cpu_c5(host)
         extra["c5_gdn_bf16"] = entry
@@ -1237,11 +1267,17 @@ def main() -> int:
             "device_us_per_step": round(c1["device_ms"] * 1e3, 2),
             "split_event_pair_us": round(c1["split_ms"] * 1e3, 2),
             "combine_event_pair_us": round(c1["combine_ms"] * 1e3, 2),
-            # kernels of a few microseconds: the device time of the step run
-            # back to back in a graph (split + combine) bounds the split's
-            # duration from above; per-launch event pairs add about as much
-            "roofline": _roofline("decode_split_f32<64> + decode_combine (step device time)",
-                                  "hbm", c1["split_alg_bytes"], c1["device_ms"])}
+            # kernels of a few microseconds: split + combine durations from the
+            # committed kernel trace of this build; the device time of the
+            # step run back to back in a graph stands beside it
+            "roofline": _roofline(
+                "decode_split_f32<64> + decode_combine (kernel trace)", "hbm",
+                c1["split_alg_bytes"],
+                (_trace_avg_ms("decode_split_f32<64, 32, false>", (4, 8, 1)) or 0)
+                + (_trace_avg_ms("decode_combine<float, float, 1>", (32, 1, 1)) or 0)
+                or c1["device_ms"]),
+            "roofline_graph": _roofline("decode_split_f32<64> + decode_combine (graph step)",
+                                        "hbm", c1["split_alg_bytes"], c1["device_ms"])}
         if host:
             entry["cpu_baseline"] = cpu_c1(c1["tensors"], host)
         c1.pop("tensors")
