@@ -117,6 +117,36 @@ def test_chunked_shapes_and_partial_chunks(gpu, ops, tokens, dk, dv, hk, hv):
     assert np.abs(S.cpu().numpy() - ref_state).max() <= 1e-4
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_chunked_batch_of_sequences_from_nonzero_states(gpu, ops, dtype):
+    """Three sequences in one chunked call (partial last chunk), each from its
+    own nonzero state, each against the fp64 scan of its own tokens: the
+    chunked kernels keep the sequences apart (workspace slots, state rows,
+    token offsets)."""
+    import torch
+    B, T, hk, hv, dk, dv = 3, 130, 2, 4, 128, 64
+    print(f"chunked GDN batch: B={B} T={T} Hk={hk} Hv={hv} Dk={dk} Dv={dv} {dtype}", flush=True)
+    cs = [I.c5_gdn_bf16(seed=40 + b, tokens=T, hk=hk, hv=hv, dk=dk, dv=dv, dtype=dtype)
+          for b in range(B)]
+    s0 = np.random.default_rng(77).standard_normal((B, hv, dv, dk)) * 0.3
+    S = torch.from_numpy(s0.astype(np.float32)).to(gpu)
+
+    def stack(key):
+        return np.stack([c[key] for c in cs])
+
+    out = ops.gated_delta_net_chunk_(
+        S, _dev(torch, stack("q"), dtype, gpu), _dev(torch, stack("k"), dtype, gpu),
+        _dev(torch, stack("v"), dtype, gpu), torch.from_numpy(stack("beta")).to(gpu),
+        torch.from_numpy(stack("g")).to(gpu))
+    tol = 1e-4 if dtype == "f32" else 2e-2
+    for b in range(B):
+        ref_state = s0[b].astype(np.float32).astype(np.float64)
+        ref = G.gdn_scan(ref_state, cs[b]["q"], cs[b]["k"], cs[b]["v"], cs[b]["beta"],
+                         cs[b]["g"])
+        assert np.abs(out[b].float().cpu().numpy() - ref).max() <= tol, b
+        assert np.abs(S[b].cpu().numpy() - ref_state).max() <= 1e-4, b
+
+
 def test_chunk_sequential_fallback_fp32(gpu, ops):
     import torch
     c = I.c5_gdn_bf16(tokens=20, hk=2, hv=4, dk=32, dv=8)
