@@ -55,6 +55,21 @@ int override_value(int which) {
                                               : 0;
 }
 
+int multiprocessor_count() {
+  static thread_local int cached_device = -1, cached = 0;
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess) device = 0;
+  if (device != cached_device) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    cached_device = device;
+    cached = cus;
+  }
+  return cached;
+}
+
 int resident_blocks(const void* kernel, int block, size_t lds) {
   struct Entry {
     const void* kernel;
@@ -67,14 +82,11 @@ int resident_blocks(const void* kernel, int block, size_t lds) {
   if (hipGetDevice(&device) != hipSuccess) device = 0;
   for (int i = 0; i < used; ++i)
     if (cache[i].kernel == kernel && cache[i].device == device) return cache[i].value;
-  int per_cu = 0, cus = 0;
+  int per_cu = 0;
   if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, block, lds) != hipSuccess ||
       per_cu <= 0)
     per_cu = 1;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
-      cus <= 0)
-    cus = 256;
-  const int value = per_cu * cus;
+  const int value = per_cu * multiprocessor_count();
   if (used < 32) cache[used++] = {kernel, device, value};
   return value;
 }

@@ -103,6 +103,8 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
 // one CU at once, times the CU count of the current device (cached per
 // kernel and device).
 int resident_blocks(const void* kernel, int block, size_t lds);
+// CU count of the current device (cached per device).
+int multiprocessor_count();
 
 inline size_t dtype_size(int dtype) {
   return dtype == ALPX_F32 ? 4 : 2;

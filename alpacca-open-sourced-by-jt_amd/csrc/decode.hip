@@ -6,7 +6,9 @@
 // unnormalised accumulator acc[Dv]) for every query head of the GQA group.
 // K and V are read exactly once per group, so the 4 (Llama-3-8B) or 8
 // (Qwen3.5) query heads of a group share each byte.  The grid is sized from
-// the occupancy API so that all blocks are resident in a single round.
+// the occupancy API: one round of resident blocks, or (16-bit caches, two
+// or more blocks per CU, long chunks) several rounds of shorter chunks that
+// the dispatcher balances over the CUs.
 //
 //  * fp16/bf16, head_dim 64/128/256 (decode_split_mfma): 4 wavefronts per
 //    block, 32 rows per wave step.  K and V rows are fetched row-major with
@@ -912,6 +914,36 @@ Plan plan_split(int pairs, int length, int resident, int unit) {
   return p;
 }
 
+// Several rounds of short chunks, for the 16-bit split kernels when two or
+// more of their blocks fit on a CU.  With one round of long chunks the
+// slowest CU sets the end of the launch (CUs, and whole XCDs, stream at
+// rates up to ~20% apart under full load, and a CU that finishes its blocks
+// early then idles).  Chunks of kRoundChunkUnits block steps, several per
+// resident slot, let the dispatcher give a CU that finishes early the next
+// block of its XCD.  At most kRoundMaxSlots partials per (sequence, head)
+// keep the combine short, and plans whose one-round chunks are already
+// short (fewer than kRoundMinUnits block steps) keep them: a block's start
+// and merge would then weigh more than the balance gained.
+constexpr int kRoundChunkUnits = 3;
+constexpr int kRoundMinUnits = 8;
+constexpr int kRoundMaxSlots = 32;
+
+Plan plan_rounds(const Plan& one, int length, int unit, int bound) {
+  if (one.chunk < kRoundMinUnits * unit) return one;
+  const int cap = bound < kRoundMaxSlots ? bound : kRoundMaxSlots;
+  int chunk = kRoundChunkUnits * unit;
+  int n = (length + chunk - 1) / chunk;
+  if (n > cap) {
+    chunk = ((length + cap - 1) / cap + unit - 1) / unit * unit;
+    n = (length + chunk - 1) / chunk;
+  }
+  if (n <= one.nsplit) return one;
+  Plan p;
+  p.nsplit = n;
+  p.chunk = chunk;
+  return p;
+}
+
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 int slot_bound(int pairs, int length) {
@@ -1124,7 +1156,10 @@ int run_decode(DecodeArgs a, int dtype, int out_dtype, void* workspace, size_t w
     n = (size_t)a.batch * a.q_heads * a.nsplit;
     grid = dim3(a.items_max, rows_y, 1);
   } else {
-    const Plan p = plan_split(a.batch * rows_y, a.length, resident, unit);
+    Plan p = plan_split(a.batch * rows_y, a.length, resident, unit);
+    if (mfma && dtype != ALPX_F32 && pro == nullptr && a.causal_pos0 < 0 &&
+        resident >= 2 * multiprocessor_count())
+      p = plan_rounds(p, a.length, unit, slot_bound(a.batch * rows_y, a.length));
     a.balanced = 0;
     a.nsplit = p.nsplit;
     a.chunk = p.chunk;
