@@ -171,9 +171,13 @@ __device__ __forceinline__ void block_rows(const DecodeArgs& a, int& b, int& sta
   } else {
     b = blockIdx.z;
     const int len = seq_len(a, b);
-    start = max((int)blockIdx.x * a.chunk, seq_lo(a, b, len));
-    end = min((int)blockIdx.x * a.chunk + a.chunk, len);
-    slot = blockIdx.x;
+    const int x = blockIdx.x;
+    // with a skew, the even slot of each pair takes chunk + skew rows
+    const int s0 = x * a.chunk + ((x & 1) ? a.skew : 0);
+    const int e0 = x * a.chunk + a.chunk + ((x & 1) ? 0 : a.skew);
+    start = max(s0, seq_lo(a, b, len));
+    end = min(e0, len);
+    slot = x;
   }
   b = __builtin_amdgcn_readfirstlane(b);
   start = __builtin_amdgcn_readfirstlane(start);
@@ -914,6 +918,20 @@ Plan plan_split(int pairs, int length, int resident, int unit) {
   return p;
 }
 
+// One-round plans: the blocks a launch places on odd-numbered XCDs (block
+// L of the grid runs on XCD L mod 8, and with an even split count the
+// slot's parity is L's) streamed 7-11% slower than those on even XCDs in
+// every per-block timing taken on MI355X boxes here (C4 shape: the odd XCDs'
+// blocks end 3-4 us later on a 44 us split).  The even slot of each pair
+// therefore takes a tenth of a chunk more rows (whole 32-row tiles) and the
+// odd slot as many fewer, for chunks of at least kSkewMinUnits block steps.
+constexpr int kSkewMinUnits = 4;
+
+int plan_skew(const Plan& p, int unit) {
+  if (p.nsplit % 2 != 0 || p.chunk < kSkewMinUnits * unit) return 0;
+  return p.chunk / 10 / kDecodeWaveRows * kDecodeWaveRows;
+}
+
 // Several rounds of short chunks, for the 16-bit split kernels when two or
 // more of their blocks fit on a CU.  With one round of long chunks the
 // slowest CU sets the end of the launch (CUs, and whole XCDs, stream at
@@ -1157,9 +1175,10 @@ int run_decode(DecodeArgs a, int dtype, int out_dtype, void* workspace, size_t w
     grid = dim3(a.items_max, rows_y, 1);
   } else {
     Plan p = plan_split(a.batch * rows_y, a.length, resident, unit);
-    if (mfma && dtype != ALPX_F32 && pro == nullptr && a.causal_pos0 < 0 &&
-        resident >= 2 * multiprocessor_count())
+    const bool mfma16 = mfma && dtype != ALPX_F32 && a.causal_pos0 < 0;
+    if (mfma16 && pro == nullptr && resident >= 2 * multiprocessor_count())
       p = plan_rounds(p, a.length, unit, slot_bound(a.batch * rows_y, a.length));
+    a.skew = mfma16 && (int64_t)p.nsplit * a.batch * rows_y <= resident ? plan_skew(p, unit) : 0;
     a.balanced = 0;
     a.nsplit = p.nsplit;
     a.chunk = p.chunk;

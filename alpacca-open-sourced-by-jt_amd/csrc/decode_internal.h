@@ -32,6 +32,10 @@ struct DecodeArgs {
   int head_chunks;  // ceil(group / 16): 16 query heads per MFMA column block
   int nsplit;       // partial slots per (b, h)
   int chunk;        // rows per slot
+  // Uniform plan, one round, even nsplit: rows moved from each odd slot to
+  // the even slot before it (slot 2i covers chunk + skew rows, slot 2i + 1
+  // chunk - skew); 0 = equal chunks.
+  int skew;
   float scale_log2; // softmax scale * log2(e)
   // Paged caches (pages != null): cache row j of sequence b lives in page
   // pages[b * max_pages + (j >> page_shift)] (clamped to [0, num_pages)),
