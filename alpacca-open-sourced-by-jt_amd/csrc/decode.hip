@@ -800,11 +800,11 @@ decode_split_generic(DecodeArgs a) {
 // are then merged through LDS by wave 0.  NW = 1 (uniform plans of at most
 // four splits, and every balanced plan, whose sequences hold a handful of
 // items) folds groups of 16 in one wave with no LDS merge.
-template <typename T, typename TO, int NW>
+template <typename T, typename TO, int NW, int kGroup>
 __global__ void __launch_bounds__(256)
 decode_combine(DecodeArgs a) {
-  // partials whose loads are issued together (one memory round trip)
-  constexpr int kGroup = NW == 1 ? 16 : 4;
+  // kGroup: partials per wave whose loads are issued together (one memory
+  // round trip)
   __shared__ float red[3][NW > 1 ? NW - 1 : 1][64];
   const int64_t bh = blockIdx.x;
   const int lane = threadIdx.x & 63;
@@ -1055,13 +1055,13 @@ const void* split_kernel(bool mfma, bool paged, int D) {
   return (const void*)decode_split_generic<T>;
 }
 
-template <typename T, int NW>
+template <typename T, int NW, int G>
 void launch_combine_nw(int out_dtype, const DecodeArgs& a, hipStream_t s) {
   const dim3 grid(a.batch * a.q_heads, (a.value_dim + 63) / 64), block(64 * NW);
   switch (out_dtype) {
-    case ALPX_F32: hipLaunchKernelGGL((decode_combine<T, float, NW>), grid, block, 0, s, a); break;
-    case ALPX_F16: hipLaunchKernelGGL((decode_combine<T, f16_t, NW>), grid, block, 0, s, a); break;
-    default: hipLaunchKernelGGL((decode_combine<T, bf16_t, NW>), grid, block, 0, s, a); break;
+    case ALPX_F32: hipLaunchKernelGGL((decode_combine<T, float, NW, G>), grid, block, 0, s, a); break;
+    case ALPX_F16: hipLaunchKernelGGL((decode_combine<T, f16_t, NW, G>), grid, block, 0, s, a); break;
+    default: hipLaunchKernelGGL((decode_combine<T, bf16_t, NW, G>), grid, block, 0, s, a); break;
   }
 }
 
@@ -1070,11 +1070,16 @@ int launch_combine(int out_dtype, const DecodeArgs& a, hipStream_t s) {
   // One wave folds up to four partials from one group of loads; with more
   // (uniform plans of many splits, balanced plans) four waves share them
   // (C2 ragged: the combine 0.6 us shorter than with one wave of 16-slot
-  // groups, same box).
+  // groups, same box).  Uniform plans of more than 16 splits fold eight
+  // partials per wave per group (C4's 32 in one round trip: step 0.3 us
+  // shorter, same box); balanced plans keep groups of four (eight measured
+  // 0.8 us slower on C2 ragged).
   if (a.nsplit <= 4)
-    launch_combine_nw<T, 1>(out_dtype, a, s);
+    launch_combine_nw<T, 1, 16>(out_dtype, a, s);
+  else if (a.nsplit > 16 && !a.balanced)
+    launch_combine_nw<T, kWaves, 8>(out_dtype, a, s);
   else
-    launch_combine_nw<T, kWaves>(out_dtype, a, s);
+    launch_combine_nw<T, kWaves, 4>(out_dtype, a, s);
   return check_launch("decode_combine");
 }
 

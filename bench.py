@@ -1274,7 +1274,7 @@ def main() -> int:
                 "decode_split_f32<64> + decode_combine (kernel trace)", "hbm",
                 c1["split_alg_bytes"],
                 (_trace_avg_ms("decode_split_f32<64, 32, false>", (4, 8, 1)) or 0)
-                + (_trace_avg_ms("decode_combine<float, float, 1>", (32, 1, 1)) or 0)
+                + (_trace_avg_ms("decode_combine<float, float, 1, 16>", (32, 1, 1)) or 0)
                 or c1["device_ms"]),
             "roofline_graph": _roofline("decode_split_f32<64> + decode_combine (graph step)",
                                         "hbm", c1["split_alg_bytes"], c1["device_ms"])}

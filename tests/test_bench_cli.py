@@ -29,7 +29,7 @@ def test_committed_profiles_cover_what_the_bench_reads():
     # small kernels whose roofline comes from the committed kernel trace
     for name, grid in (("gdn_step_kernel", (8, 32, 1)),
                        ("decode_split_f32<64, 32, false>", (4, 8, 1)),
-                       ("decode_combine<float, float, 1>", (32, 1, 1)),
+                       ("decode_combine<float, float, 1, 16>", (32, 1, 1)),
                        ("recurrent_rows_kernel<1>", (8, 32, 1)),
                        ("recurrent_finish_kernel<float>", (24, 1, 1))):
         ms = b._trace_avg_ms(name, grid)
