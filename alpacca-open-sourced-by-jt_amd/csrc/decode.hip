@@ -1182,8 +1182,14 @@ int run_decode(DecodeArgs a, int dtype, int out_dtype, void* workspace, size_t w
   } else {
     Plan p = plan_split(a.batch * rows_y, a.length, resident, unit);
     const bool mfma16 = mfma && dtype != ALPX_F32 && a.causal_pos0 < 0;
-    if (mfma16 && pro == nullptr && resident >= 2 * multiprocessor_count())
-      p = plan_rounds(p, a.length, unit, slot_bound(a.batch * rows_y, a.length));
+    if (mfma16 && pro == nullptr && resident >= 2 * multiprocessor_count()) {
+      const Plan r = plan_rounds(p, a.length, unit, slot_bound(a.batch * rows_y, a.length));
+      // a fixed scratch that holds the one-round partials but not these
+      // keeps the one-round plan
+      if (fixed_scratch == nullptr ||
+          partial_bytes((size_t)a.batch * a.q_heads * r.nsplit, a.value_dim) <= workspace_bytes)
+        p = r;
+    }
     a.skew = mfma16 && (int64_t)p.nsplit * a.batch * rows_y <= resident ? plan_skew(p, unit) : 0;
     a.balanced = 0;
     a.nsplit = p.nsplit;

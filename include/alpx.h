@@ -216,13 +216,16 @@ int alpx_decode_gqa(const void* q, const void* key_cache, const void* value_cach
  * No counterpart in the reference: it is for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  Same arguments (minus workspace),
- * kernels, split plan and result (bit for bit) as alpx_decode_gqa.  The
- * split partials live in a static device array of
- * ALPX_DECODE_SCRATCH_BYTES per GPU, held from the library's load until
- * the process ends; its address on each device is looked up on the first
- * call there.  A call whose split plan needs more partial bytes than that
- * (many sequences x query heads x splits) fails with ALPX_ERANGE before
- * anything is enqueued; use alpx_decode_gqa then.  Every call on one GPU
+ * kernels, split plan and result (bit for bit) as alpx_decode_gqa, except
+ * where alpx_decode_gqa's several-rounds plan (long 16-bit caches) needs
+ * more partial bytes than the array: the call then keeps the one-round
+ * plan (same result within rounding).  The split partials live in a
+ * static device array of ALPX_DECODE_SCRATCH_BYTES per GPU, held from the
+ * library's load until the process ends; its address on each device is
+ * looked up on the first call there.  A call whose one-round plan needs
+ * more partial bytes than that (many sequences x query heads x splits)
+ * fails with ALPX_ERANGE before anything is enqueued; use alpx_decode_gqa
+ * then.  Every call on one GPU
  * shares the array, so calls that overlap on one GPU (unordered streams)
  * race; calls ordered on one stream are safe.  Nothing in the array needs
  * initial contents.
