@@ -103,6 +103,23 @@ def test_paged_c2_full_size_equals_contiguous(gpu, ops):
         assert torch.equal(got, want)
 
 
+def test_paged_c4_full_size_equals_contiguous(gpu, ops):
+    # BASELINE C4 (4 x 32768 rows, 16/2 heads, D 256, bf16, gated) through
+    # 256-row pages: a one-round plan of unequal even / odd chunks
+    import torch
+    rng = np.random.default_rng(4)
+    batch, cap, hq, hkv, d, page = 4, 32768, 16, 2, 256, 256
+    print(f"paged C4: B={batch} cap={cap} Hq={hq} Hkv={hkv} D={d} page={page} bf16", flush=True)
+    ws, pw, table, _ = _fill(torch, ops, gpu, rng, "bf16", batch, cap, hkv, d, page, False)
+    q = torch.randn((batch, hq, d), device=gpu).to(torch.bfloat16)
+    gate = torch.randn((batch, hq, d), device=gpu).to(torch.bfloat16)
+    want = ops.online_attention(q, ws.key_cache, ws.value_cache, length=cap, gate=gate)
+    got = ops.paged_online_attention(q, pw.key_pages, pw.value_pages, table, length=cap,
+                                     gate=gate)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+
+
 def test_paged_append_one_token_per_sequence_and_bad_arguments(gpu, ops):
     import torch
     rng = np.random.default_rng(7)
