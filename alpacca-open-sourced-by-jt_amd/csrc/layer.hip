@@ -56,9 +56,49 @@ struct NormArgs {
   float eps;
 };
 
-// Row r of a row norm, by one wave.
+// Row r of a row norm, by one wave, rows of at most 64 NPL values: every
+// load of the row (x, and the weight and gate it needs) is issued from a
+// clamped index before the reduction, so the row costs one memory round
+// trip, and x stays in registers.  Lane l owns elements l + 64 j, summed in
+// j order, as the strided loop below sums them: both forms give the same
+// bits.
+template <typename T, typename TO, int MODE, int NPL>
+__device__ __forceinline__ void norm_row_regs(const NormArgs& a, int64_t r, int lane) {
+  const T* x = (const T*)a.x + (r / a.grp_rows) * a.grp_stride + (r % a.grp_rows) * a.n;
+  const T* g = (const T*)a.gate + r * a.n;
+  float xv[NPL], wv[NPL], gv[NPL];
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) {
+    const int i = min(lane + 64 * j, a.n - 1);
+    xv[j] = to_f32(x[i]);
+    if constexpr (MODE != kNormL2) wv[j] = a.w[i];
+    if constexpr (MODE == kNormRmsGate) gv[j] = to_f32(g[i]);
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < NPL; ++j)
+    if (lane + 64 * j < a.n) ss = fmaf(xv[j], xv[j], ss);
+  ss = wave_sum(ss);
+  const float den = MODE == kNormL2 ? fmaxf(sqrtf(ss), a.eps) : sqrtf(ss / (float)a.n + a.eps);
+  TO* o = (TO*)a.out + r * a.n;
+#pragma unroll
+  for (int j = 0; j < NPL; ++j) {
+    const int i = lane + 64 * j;
+    if (i < a.n) {
+      float v = xv[j] / den;
+      if constexpr (MODE != kNormL2) v *= wv[j];
+      if constexpr (MODE == kNormRmsGate) v *= silu_f(gv[j]);
+      o[i] = from_f32<TO>(v);
+    }
+  }
+}
+
+// Row r of a row norm, by one wave (any width).
 template <typename T, typename TO, int MODE>
 __device__ __forceinline__ void norm_row(const NormArgs& a, int64_t r, int lane) {
+  if (a.n <= 128) return norm_row_regs<T, TO, MODE, 2>(a, r, lane);
+  if (a.n <= 256) return norm_row_regs<T, TO, MODE, 4>(a, r, lane);
+  if (a.n <= 512) return norm_row_regs<T, TO, MODE, 8>(a, r, lane);
   const T* x = (const T*)a.x + (r / a.grp_rows) * a.grp_stride + (r % a.grp_rows) * a.n;
   float ss = 0.f;
   for (int i = lane; i < a.n; i += 64) {
