@@ -114,8 +114,16 @@ __device__ __forceinline__ int balanced_chunk(const DecodeArgs& a, int lane, int
     if (b < a.batch) total += seq_len(a, b);
   }
   total = wave_sum(total);
-  int64_t c = (total + a.items_target - 1) / a.items_target;
-  c = (c + a.unit - 1) / a.unit * a.unit;
+  // 32-bit divisions where the row total allows (the 64-bit ones are long
+  // instruction sequences on the path to every block's first tile loads)
+  int64_t c;
+  if (total <= 0x7fffffff - a.items_target) {
+    const unsigned q = ((unsigned)total + (unsigned)a.items_target - 1u) / (unsigned)a.items_target;
+    c = (q + (unsigned)a.unit - 1u) / (unsigned)a.unit * (unsigned)a.unit;
+  } else {
+    c = (total + a.items_target - 1) / a.items_target;
+    c = (c + a.unit - 1) / a.unit * a.unit;
+  }
   return c < a.unit ? a.unit : (int)c;
 }
 
