@@ -257,6 +257,28 @@ def test_sigmoid_gate(gpu, ops, dtype):
     assert np.abs(out.float().cpu().numpy() - ref).max() <= tol
 
 
+@pytest.mark.parametrize("B,length,hq,hkv,d,dtype", [
+    (32, 4096, 16, 4, 128, "bf16"),   # several rounds of 384-row chunks
+    (8, 4096, 32, 8, 128, "f16"),     # one round, even / odd chunks of 544 / 480 rows
+    (2, 32768, 8, 2, 256, "bf16")])   # one round at head_dim 256, 544 / 480 rows
+def test_decode_split_plans_against_oracle(gpu, ops, B, length, hq, hkv, d, dtype):
+    """Uniform plans of the 16-bit kernels: several rounds of short chunks
+    for long caches of small-register kernels, unequal even / odd chunks in
+    one-round plans; every row attended once, against the oracle."""
+    import torch
+    rng = np.random.default_rng(B * 7 + d)
+    print(f"decode plan: B={B} len={length} Hq={hq} Hkv={hkv} D={d} {dtype}", flush=True)
+    q = I.round_to(rng.standard_normal((B, hq, d)), dtype)
+    K = I.round_to(rng.standard_normal((length, B, hkv, d)), dtype)
+    V = I.round_to(rng.standard_normal((length, B, hkv, d)), dtype)
+    out = ops.online_attention(_dev(torch, q, dtype, gpu), _dev(torch, K, dtype, gpu),
+                               _dev(torch, V, dtype, gpu), length=length,
+                               out_dtype=torch.float32)
+    ref = A.online_attention(q, K, V, length)
+    err = np.abs(out.cpu().numpy() - ref).max()
+    assert err <= TOL[dtype], err
+
+
 def test_decode_repeatable_across_plans(gpu, ops):
     import torch
     rng = np.random.default_rng(11)
