@@ -273,6 +273,39 @@ def test_recurrent_prefill_prep_matches_oracle(gpu, tokens, kernel, hk, hv, dk, 
         assert np.array_equal(H.cpu().numpy(), hist[0].astype(np.float32))
 
 
+@pytest.mark.parametrize("tokens,hk,hv,d,layout,qkv", [
+    (70, 2, 4, 64, "kc", "f32"), (130, 1, 2, 128, "kc", "f32"), (65, 1, 1, 256, "kc", "f32"),
+    (100, 2, 4, 128, "ck", "f32"), (37, 2, 4, 128, "kc", "bf16")])
+def test_recurrent_prefill_prep_four_taps_equal_dims(gpu, tokens, hk, hv, d, layout, qkv):
+    # 4-tap convolution with equal key / value head dims (the Qwen3.5
+    # shapes) through the tiled kernel, for weights laid out [K, C] (tap rows
+    # of consecutive channels) and [C, K], fp32 and bf16 outputs
+    import torch
+    P = _mod("_ops")
+    rng = np.random.default_rng(tokens * 3 + d)
+    eps, kernel = 1e-6, 4
+    x = _rec_inputs(rng, tokens, hk, hv, d, d, kernel)
+    w_dev = _f32(torch, x["w"], gpu) if layout == "kc" else _f32(torch, x["w"].T.copy(), gpu)
+    H = _f32(torch, x["hist"], gpu)
+    td = torch.float32 if qkv == "f32" else torch.bfloat16
+    q, k, v, beta, g = P.recurrent_prefill_prep(
+        _f32(torch, x["mixed"], gpu), w_dev, H, _f32(torch, x["bl"], gpu),
+        _f32(torch, x["al"], gpu), _f32(torch, x["dt"], gpu), _f32(torch, x["ssm"], gpu),
+        key_heads=hk, key_dim=d, value_heads=hv, value_dim=d, eps=eps, qkv_dtype=td,
+        weight_layout=layout)
+    tol = 1e-5 if qkv == "f32" else 1e-2
+    hist = x["hist"].astype(np.float64)[None]
+    w = hk * d
+    for t in range(tokens):
+        act, hist = L.conv_step(x["mixed"][t:t + 1], x["w"], hist, apply_silu=True)
+        assert np.abs(_np(q[t]) - L.l2_normalize(act[0, :w].reshape(hk, d), eps)).max() <= tol
+        assert np.abs(_np(k[t]) - L.l2_normalize(act[0, w:2 * w].reshape(hk, d), eps)).max() <= tol
+        assert np.abs(_np(v[t]) - act[0, 2 * w:].reshape(hv, d)).max() <= tol * (1 if qkv == "f32" else 10)
+    rb, rg = L.recurrent_parameters(x["bl"], x["al"], x["dt"], x["ssm"])
+    assert np.abs(_np(beta) - rb).max() <= 1e-6 and np.abs(_np(g) - rg).max() <= 1e-5
+    assert np.array_equal(H.cpu().numpy(), hist[0].astype(np.float32))
+
+
 def _recurrent_prefill_vs_chain(ops, gpu, tokens, hk, hv, dk, dv, operand_dtype):
     # the chunk (prep -> chunked GDN -> gated norm) of the second sequence of
     # a batch-2 workspace, from a nonzero state and history, and the fp64
