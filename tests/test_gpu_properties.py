@@ -14,6 +14,8 @@ below 1e-30, where a flushed denormal would break the exact scaling):
   * causal prefill (C3): rewriting the chunk's last 512 K/V rows leaves the
     outputs of the first 1536 query tokens unchanged (keys past a token's
     position enter with weight exactly zero);
+  * ragged decode (C2 ragged) never reads a row at or past a sequence's
+    length: rewriting those rows leaves the outputs unchanged;
   * KV append is idempotent: appending the same rows again leaves the
     caches unchanged.
 """
@@ -61,6 +63,27 @@ def test_decode_scales_with_values_c2_and_c4(gpu, ops):
         torch.cuda.synchronize()
         assert torch.equal(_bits(o2), _bits(o1 * 2)), name
         del K, V
+
+
+def test_ragged_decode_reads_no_row_past_a_length_c2(gpu, ops):
+    # C2 ragged (16 sequences of 1024..8192 of 8192 rows, length-balanced
+    # plan): rows at or past a sequence's length rewritten, outputs unchanged
+    import torch
+    g = torch.Generator(device=gpu).manual_seed(54)
+    B, cap, hq, hkv, d = 16, 8192, 32, 8, 128
+    print(f"ragged decode: B={B} cap={cap} Hq={hq} Hkv={hkv} D={d} fp16", flush=True)
+    lens_np = np.random.default_rng(2).integers(1024, cap + 1, B)
+    lens = torch.from_numpy(lens_np.astype(np.int32)).to(gpu)
+    q = torch.randn((B, hq, d), generator=g, device=gpu).half()
+    K = torch.randn((cap, B, hkv, d), generator=g, device=gpu).half()
+    V = torch.randn((cap, B, hkv, d), generator=g, device=gpu).half()
+    o1 = ops.online_attention(q, K, V, length=cap, seq_lens=lens, out_dtype=torch.float32)
+    for b, n in enumerate(lens_np.tolist()):
+        K[n:, b] = torch.randn((cap - n, hkv, d), generator=g, device=gpu).half() * 100
+        V[n:, b] = torch.randn((cap - n, hkv, d), generator=g, device=gpu).half() * 100
+    o2 = ops.online_attention(q, K, V, length=cap, seq_lens=lens, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(o1), _bits(o2))
 
 
 def test_prefill_scales_with_values_and_is_causal_c3(gpu, ops):
