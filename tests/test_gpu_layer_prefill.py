@@ -306,15 +306,16 @@ def test_recurrent_prefill_prep_four_taps_equal_dims(gpu, tokens, hk, hv, d, lay
     assert np.array_equal(H.cpu().numpy(), hist[0].astype(np.float32))
 
 
-def _recurrent_prefill_vs_chain(ops, gpu, tokens, hk, hv, dk, dv, operand_dtype):
+def _recurrent_prefill_vs_chain(ops, gpu, tokens, hk, hv, dk, dv, operand_dtype, seed=None,
+                                kernel=4):
     # the chunk (prep -> chunked GDN -> gated norm) of the second sequence of
     # a batch-2 workspace, from a nonzero state and history, and the fp64
     # token-sequential chain; returns (device output, device state,
     # reference output, reference state), the oracle rounding q / k / v to
     # bf16 where the device is asked to
     import torch
-    rng = np.random.default_rng(tokens + hk + dk)
-    kernel, eps, bi = 4, 1e-6, 1
+    rng = np.random.default_rng(tokens + hk + dk if seed is None else seed)
+    eps, bi = 1e-6, 1
     x = _rec_inputs(rng, tokens, hk, hv, dk, dv, kernel)
     c = 2 * hk * dk + hv * dv
     ws = ops.initialize_recurrent_workspace(batch_size=2, convolution_kernel=kernel,
@@ -388,3 +389,111 @@ def test_recurrent_prefill_state_with_device_qkv(gpu):
     ro = G.gdn_scan(s64, _np(q), _np(k), _np(v), _np(beta), _np(g))
     assert np.abs(S[0].cpu().numpy() - s64).max() <= 1e-4
     assert np.abs(_np(o[0]) - np.asarray(ro)).max() <= 2e-2
+
+
+# ------------------------------------------------ seeded random geometry
+
+def _pick(rng, values):
+    return values[int(rng.integers(len(values)))]
+
+
+def _random_attention_layer_cases(n=16):
+    rng = np.random.default_rng(9400)
+    cases = []
+    for i in range(n):
+        dtype = _pick(rng, ["bf16", "f16", "bf16", "f32"])
+        d = _pick(rng, [64, 128, 256, 128, 96])
+        sec = _pick(rng, [s for s in ((11, 11, 10, 0), (16, 16, 16, 16), (8, 12, 12, 0),
+                                      (24, 20, 20, 0), (5, 5, 6, 0), (10, 10, 10, 2))
+                          if sum(s) <= d // 2])
+        hkv = int(rng.integers(1, 4))
+        hq = hkv * _pick(rng, [1, 2, 4, 8])
+        tokens = int(rng.integers(1, 161))
+        prefix = int(rng.integers(0, 601))
+        batch = int(rng.integers(1, 4))
+        c = dict(seed=9400 + i, dtype=dtype, d=d, sec=sec, hkv=hkv, hq=hq, tokens=tokens,
+                 prefix=prefix, batch=batch, bi=int(rng.integers(batch)))
+        c["id"] = (f"att{i:02d}-{dtype}-d{d}-q{hq}kv{hkv}-R{sum(sec)}-T{tokens}at{prefix}"
+                   f"-B{batch}s{c['bi']}")
+        cases.append(c)
+    return cases
+
+
+def _random_recurrent_cases(n=12):
+    rng = np.random.default_rng(9450)
+    cases = []
+    for i in range(n):
+        dk = _pick(rng, [64, 128, 256, 128, 40])
+        dv = _pick(rng, [32, 64, 128, 256, 24])
+        hk = int(rng.integers(1, 4))
+        hv = hk * int(rng.integers(1, 4))
+        tokens = max(1, min(int(rng.integers(1, 301)), 1200 // hv))
+        c = dict(seed=9450 + i, dk=dk, dv=dv, hk=hk, hv=hv, tokens=tokens,
+                 kernel=_pick(rng, [4, 4, 3, 2]))
+        c["id"] = f"rec{i:02d}-k{dk}v{dv}-hk{hk}hv{hv}-T{tokens}-taps{c['kernel']}"
+        cases.append(c)
+    return cases
+
+
+ATT_CASES = _random_attention_layer_cases()
+REC_CASES = _random_recurrent_cases()
+
+
+@pytest.mark.parametrize("c", ATT_CASES, ids=[c["id"] for c in ATT_CASES])
+def test_random_attention_layer_prefill_against_token_chain(gpu, ops, c):
+    """Seeded random geometry (dtype, head dim, rotary sections, heads,
+    chunk, prefix, batch, sequence) of the chunked attention layer against
+    the fp64 token-sequential oracle: gated output at the dtype's bar, the
+    appended key rows within it, value rows copied bit for bit, the other
+    sequences' rows untouched."""
+    import torch
+    print("random attention layer prefill:", c["id"], flush=True)
+    rng = np.random.default_rng(c["seed"])
+    dt, d, hq, hkv, T, P0, B, bi = (c["dtype"], c["d"], c["hq"], c["hkv"], c["tokens"],
+                                    c["prefix"], c["batch"], c["bi"])
+    td = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[dt]
+    r = lambda a: I.round_to(a, dt).astype(np.float64)  # noqa: E731
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(gpu).to(td)  # noqa: E731
+    base, eps, cap = 1e6, 1e-6, P0 + T + 3
+    kc0 = np.zeros((cap, B, hkv, d))
+    vc0 = np.zeros((cap, B, hkv, d))
+    kc0[:P0] = r(rng.standard_normal((P0, B, hkv, d)))
+    vc0[:P0] = r(rng.standard_normal((P0, B, hkv, d)))
+    qg = r(rng.standard_normal((T, hq * 2 * d)) * 3)
+    k = r(rng.standard_normal((T, hkv * d)) * 3)
+    v = r(rng.standard_normal((T, hkv * d)))
+    qw = rng.uniform(0.5, 1.5, d).astype(np.float32)
+    kw = rng.uniform(0.5, 1.5, d).astype(np.float32)
+    KC, VC = dev(kc0), dev(vc0)
+    out, nxt = ops.attention_layer_prefill_(
+        dev(qg), dev(k), dev(v), _f32(torch, qw, gpu), _f32(torch, kw, gpu), KC, VC,
+        position=P0, batch_index=bi, sections=c["sec"], frequency_base=base, epsilon=eps)
+    torch.cuda.synchronize()
+    assert nxt == P0 + T and tuple(out.shape) == (T, hq, d)
+    kco, vco = kc0[:, bi].copy(), vc0[:, bi].copy()
+    ref = L.attention_layer_prefill(qg, k, v, qw, kw, eps, P0, c["sec"], base, kco, vco,
+                                    round_rows=None if dt == "f32" else r)
+    tol = 1e-4 if dt == "f32" else 2e-2
+    err = float(np.abs(_np(out) - ref).max())
+    err_k = float(np.abs(_np(KC)[:P0 + T, bi] - kco[:P0 + T]).max())
+    print(f"  output {err:.3g}, key rows {err_k:.3g} (bar {tol:g})", flush=True)
+    assert err <= tol and err_k <= tol, (c["id"], err, err_k)
+    assert np.array_equal(_np(VC)[P0:P0 + T, bi], v.reshape(T, hkv, d))
+    others = np.arange(B) != bi
+    assert np.array_equal(_np(KC)[:, others], kc0[:, others])
+    assert np.array_equal(_np(VC)[:, others], vc0[:, others])
+
+
+@pytest.mark.parametrize("c", REC_CASES, ids=[c["id"] for c in REC_CASES])
+def test_random_recurrent_layer_prefill_against_token_chain(gpu, ops, c):
+    """Seeded random geometry (head dims, head counts, chunk length,
+    convolution taps) of the fp32 recurrent-layer chunk against the
+    unrounded fp64 token chain at the fp32 bars (output and state 1e-4)."""
+    print("random recurrent layer prefill:", c["id"], flush=True)
+    out, state, ref, ref_state = _recurrent_prefill_vs_chain(
+        ops, gpu, c["tokens"], c["hk"], c["hv"], c["dk"], c["dv"], None, seed=c["seed"],
+        kernel=c["kernel"])
+    err_o = float(np.abs(out - ref).max())
+    err_s = float(np.abs(state - ref_state).max())
+    print(f"  output {err_o:.3g}, state {err_s:.3g} (bar 1e-4)", flush=True)
+    assert err_o <= 1e-4 and err_s <= 1e-4, (c["id"], err_o, err_s)
