@@ -642,3 +642,141 @@ def test_split_query_gate(gpu, ops):
     q, g = ops.split_query_gate(p, query_heads=3, head_dimension=4)
     rq, rg = L.split_query_gate(p.cpu().numpy(), 3, 4)
     assert np.array_equal(q.cpu().numpy(), rq) and np.array_equal(g.cpu().numpy(), rg)
+
+
+# ------------------------------------------------ seeded random geometry
+
+def _pick(rng, values):
+    return values[int(rng.integers(len(values)))]
+
+
+def _random_step_cases(n=24):
+    rng = np.random.default_rng(9600)
+    cases = []
+    for i in range(n):
+        dtype = _pick(rng, ["bf16", "f16", "bf16", "f32"])
+        d = _pick(rng, [64, 128, 256, 128, 96])
+        sections = _pick(rng, [s for s in ((11, 11, 10, 0), (16, 16, 16, 16), (8, 12, 12, 0),
+                                           (4, 4, 2, 0), (10, 10, 10, 2))
+                               if 2 * sum(s) <= d])
+        b = int(rng.integers(1, 6))
+        hkv = int(rng.integers(1, 4))
+        hq = hkv * _pick(rng, [1, 2, 4, 8])
+        cap = int(rng.integers(1, 2049))
+        ragged = bool(b > 1 and rng.random() < 0.4)
+        rows = (rng.integers(0, cap, b) if ragged else np.full(b, int(rng.integers(0, cap))))
+        c = dict(seed=9600 + i, dtype=dtype, d=d, sections=sections, b=b, hkv=hkv, hq=hq,
+                 cap=cap, rows=[int(x) for x in rows], ragged=ragged,
+                 out32=bool(dtype != "f32" and rng.random() < 0.4))
+        c["id"] = (f"step{i:02d}-{dtype}-d{d}-q{hq}kv{hkv}-B{b}-cap{cap}-R{sum(sections)}"
+                   f"{'-ragged' if ragged else '-at%d' % rows[0]}{'-o32' if c['out32'] else ''}")
+        cases.append(c)
+    return cases
+
+
+def _random_recurrent_step_cases(n=12):
+    rng = np.random.default_rng(9650)
+    cases = []
+    for i in range(n):
+        hk = int(rng.integers(1, 4))
+        c = dict(seed=9650 + i, batch=int(rng.integers(1, 4)), hk=hk,
+                 hv=hk * int(rng.integers(1, 4)), dk=_pick(rng, [32, 64, 128, 256, 40]),
+                 dv=_pick(rng, [32, 48, 96, 128, 24]), kernel=_pick(rng, [4, 4, 3, 2, 1, 6]),
+                 steps=int(rng.integers(2, 9)))
+        c["id"] = (f"rstep{i:02d}-B{c['batch']}-hk{hk}hv{c['hv']}-k{c['dk']}v{c['dv']}"
+                   f"-taps{c['kernel']}-x{c['steps']}")
+        cases.append(c)
+    return cases
+
+
+STEP_CASES = _random_step_cases()
+RSTEP_CASES = _random_recurrent_step_cases()
+
+
+@pytest.mark.parametrize("c", STEP_CASES, ids=[c["id"] for c in STEP_CASES])
+def test_random_attention_layer_step_against_oracle(gpu, ops, c):
+    """Seeded random geometry (dtype, head dim, rotary sections, batch,
+    heads, capacity, uniform or per-sequence rows, output dtype) of the
+    fused attention-layer step against the oracle prologue and decode: key
+    rows at the dtype's bar, value rows copied bit for bit, the gated
+    output of each sequence over its rows 0 .. row, every other cache row
+    untouched."""
+    import torch
+    print("random attention layer step:", c["id"], flush=True)
+    rng = np.random.default_rng(c["seed"])
+    dt, d, b, hq, hkv, cap, rows = (c["dtype"], c["d"], c["b"], c["hq"], c["hkv"], c["cap"],
+                                    c["rows"])
+    base, eps = 10000000.0, 1e-6
+    kc = I.round_to(rng.standard_normal((cap, b, hkv, d)), dt)
+    vc = I.round_to(rng.standard_normal((cap, b, hkv, d)), dt)
+    qg = I.round_to(rng.standard_normal((b, hq * 2 * d)) * 3, dt)
+    k = I.round_to(rng.standard_normal((b, hkv * d)) * 3, dt)
+    v = I.round_to(rng.standard_normal((b, hkv * d)), dt)
+    qw = rng.uniform(0.5, 1.5, d).astype(np.float32)
+    kw = rng.uniform(0.5, 1.5, d).astype(np.float32)
+    KC, VC = _dev(torch, kc, dt, gpu), _dev(torch, vc, dt, gpu)
+    bound = max(rows)
+    out, n = ops.attention_layer_step_(
+        _dev(torch, qg, dt, gpu), _dev(torch, k, dt, gpu), _dev(torch, v, dt, gpu),
+        torch.from_numpy(qw).to(gpu), torch.from_numpy(kw).to(gpu), KC, VC, position=bound,
+        positions=rows if c["ragged"] else None, sections=c["sections"], frequency_base=base,
+        epsilon=eps, out_dtype=torch.float32 if c["out32"] else None)
+    torch.cuda.synchronize()
+    assert n == bound + 1 and tuple(out.shape) == (b, hq, d)
+    assert out.dtype == (torch.float32 if c["out32"] else _td(torch, dt))
+    rq, rg, rk, rv = L.attention_prologue(qg, k, v, qw, kw, eps, np.array(rows), c["sections"],
+                                          base)
+    tol = _tol(dt)
+    got_k, got_v = _np(KC), _np(VC)
+    worst = 0.0
+    for bb, p in enumerate(rows):
+        assert np.abs(got_k[p, bb] - rk[bb]).max() <= tol, (c["id"], bb)
+        assert np.array_equal(got_v[p, bb], rv[bb]), (c["id"], bb)
+        ref = A.attention_decode_twopass(rq[bb], got_k[:p + 1, bb], got_v[:p + 1, bb],
+                                         hq // hkv, 1.0 / np.sqrt(d))
+        ref = ref * (1.0 / (1.0 + np.exp(-rg[bb])))
+        worst = max(worst, float(np.abs(_np(out[bb]) - ref).max()))
+    print(f"  output {worst:.3g} (bar {tol:g})", flush=True)
+    assert worst <= tol, (c["id"], worst)
+    mask = np.ones((cap, b), bool)
+    mask[rows, np.arange(b)] = False
+    assert np.array_equal(got_k[mask], kc[mask]) and np.array_equal(got_v[mask], vc[mask])
+
+
+@pytest.mark.parametrize("c", RSTEP_CASES, ids=[c["id"] for c in RSTEP_CASES])
+def test_random_recurrent_layer_step_against_oracle(gpu, ops, c):
+    """Seeded random geometry (batch, head counts, head dims, convolution
+    taps, number of tokens) of the recurrent-layer step against the fp64
+    token chain: output and state 1e-4, convolution history bit for bit."""
+    import torch
+    print("random recurrent layer step:", c["id"], flush=True)
+    rng = np.random.default_rng(c["seed"])
+    batch, hk, hv, dk, dv, kernel = c["batch"], c["hk"], c["hv"], c["dk"], c["dv"], c["kernel"]
+    eps = 1e-6
+    chn = 2 * hk * dk + hv * dv
+    w = (rng.standard_normal((kernel, chn)) * 0.5).astype(np.float32)
+    dt = rng.standard_normal(hv).astype(np.float32)
+    ssm = (-np.exp(rng.uniform(-1, 1, hv))).astype(np.float32)
+    nw = rng.uniform(0.5, 1.5, dv).astype(np.float32)
+    ws = ops.initialize_recurrent_workspace(batch_size=batch, convolution_kernel=kernel,
+                                            convolution_channels=chn, value_heads=hv,
+                                            value_dimension=dv, key_dimension=dk)
+    hist = np.zeros((batch, kernel - 1, chn))
+    state = np.zeros((batch, hv, dv, dk))
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(gpu)  # noqa: E731
+    worst = 0.0
+    for _ in range(c["steps"]):
+        mixed = rng.standard_normal((batch, chn)).astype(np.float32)
+        gate = rng.standard_normal((batch, hv * dv)).astype(np.float32)
+        bl = rng.standard_normal((batch, hv)).astype(np.float32)
+        al = rng.standard_normal((batch, hv)).astype(np.float32)
+        out = ops.recurrent_layer_step_(ws, T(mixed), T(w), T(gate), T(bl), T(al), T(dt), T(ssm),
+                                        T(nw), key_heads=hk, key_dimension=dk, epsilon=eps)
+        ref, hist = L.recurrent_layer_step(mixed, w, hist, gate, bl, al, dt, ssm, nw, state,
+                                           key_heads=hk, key_dim=dk, value_heads=hv,
+                                           value_dim=dv, eps=eps)
+        worst = max(worst, float(np.abs(out.cpu().numpy() - ref).max()))
+    err_s = float(np.abs(ws.delta_state.cpu().numpy() - state).max())
+    print(f"  output {worst:.3g}, state {err_s:.3g} (bar 1e-4)", flush=True)
+    assert worst <= 1e-4 and err_s <= 1e-4, (c["id"], worst, err_s)
+    assert np.array_equal(ws.convolution_history.cpu().numpy(), hist.astype(np.float32))
