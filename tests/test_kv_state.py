@@ -294,3 +294,108 @@ def test_paged_transfer_rows_outside_the_pool(gpu):
 def _bits_t(t):
     import torch
     return t.view(torch.int16) if t.element_size() == 2 else t.view(torch.int32)
+
+
+# --------------------------------------------------------------- GPU: random geometry
+
+def _pick(rng, values):
+    return values[int(rng.integers(len(values)))]
+
+
+def _random_transfer_cases(n=16):
+    rng = np.random.default_rng(9700)
+    cases = []
+    for i in range(n):
+        paged = bool(rng.random() < 0.5)
+        page = _pick(rng, [1, 4, 8, 16, 64]) if paged else 0
+        cap = page * int(rng.integers(1, 9)) if paged else int(rng.integers(1, 301))
+        c = dict(seed=9700 + i, dtype=_pick(rng, ["f32", "f16", "bf16"]), paged=paged, page=page,
+                 cap=cap, hkv=int(rng.integers(1, 5)), d=_pick(rng, [8, 32, 64, 128, 256, 40]),
+                 dv=_pick(rng, [8, 24, 64, 128, 256]), batch=int(rng.integers(1, 4)),
+                 n=int(rng.integers(1, cap + 1)), rounded=bool(rng.random() < 0.5))
+        c["bi"] = int(rng.integers(c["batch"]))
+        c["id"] = (f"xfer{i:02d}-{c['dtype']}-{'paged%d' % page if paged else 'contig'}"
+                   f"-cap{cap}-kv{c['hkv']}-d{c['d']}x{c['dv']}-B{c['batch']}s{c['bi']}-n{c['n']}"
+                   f"{'' if c['rounded'] else '-fp32rows'}")
+        cases.append(c)
+    return cases
+
+
+XFER_CASES = _random_transfer_cases()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("c", XFER_CASES, ids=[c["id"] for c in XFER_CASES])
+def test_random_state_transfer_round_trips(gpu, c):
+    """Seeded random geometry (dtype, contiguous or paged with random page
+    size, capacity, heads, head dims, batch, sequence, row count; records of
+    values already in the cache dtype or of raw fp32 values): restore then
+    snapshot gives the reference's encoding of the rounded rows, bit for
+    bit; the other sequences' rows keep their bits; truncate + append
+    continues at the new length; a record restores across layouts."""
+    import torch
+    M = _mem()
+    print("random state transfer:", c["id"], flush=True)
+    rng = np.random.default_rng(c["seed"])
+    dt, hkv, d, dv, n, bi, B = c["dtype"], c["hkv"], c["d"], c["dv"], c["n"], c["bi"], c["batch"]
+    td = _td(torch, dt)
+    raw_k = rng.standard_normal((n, hkv * d))
+    raw_v = rng.standard_normal((n, hkv * dv))
+    if c["rounded"]:
+        raw_k, raw_v = I.round_to(raw_k, dt), I.round_to(raw_v, dt)
+    rec = M.FullAttentionSnapshot(layer_index=2, logical_length=n, kv_heads=hkv, key_dim=d,
+                                  value_dim=dv, key=np.asarray(raw_k, dtype="<f4").tobytes(),
+                                  value=np.asarray(raw_v, dtype="<f4").tobytes())
+    want_k = np.asarray(I.round_to(np.asarray(raw_k, dtype=np.float32), dt), dtype="<f4")
+    want_v = np.asarray(I.round_to(np.asarray(raw_v, dtype=np.float32), dt), dtype="<f4")
+    if c["paged"]:
+        max_pages = c["cap"] // c["page"]
+        kp, vp, table, perm = _paged_pool(torch, gpu, td, rng, B * max_pages + 2, c["page"], hkv,
+                                          d, dv, B, max_pages)
+        k0, v0 = kp.clone(), vp.clone()
+        st = M.DevicePagedAttentionState(kp, vp, table, layer_index=2, batch_index=bi)
+    else:
+        kc = torch.from_numpy(rng.standard_normal((c["cap"], B, hkv, d)).astype(np.float32)).to(
+            td).to(gpu)
+        vc = torch.from_numpy(rng.standard_normal((c["cap"], B, hkv, dv)).astype(np.float32)).to(
+            td).to(gpu)
+        k0, v0 = kc.clone(), vc.clone()
+        st = M.DeviceFullAttentionState(kc, vc, layer_index=2, batch_index=bi)
+    st.restore(rec)
+    snap = st.snapshot()
+    assert st.logical_length == n
+    assert snap.key == want_k.tobytes() and snap.value == want_v.tobytes(), c["id"]
+    if c["paged"]:
+        # only sequence bi's first ceil(n / page) pages changed
+        used = {int(perm[bi, j]) for j in range((n + c["page"] - 1) // c["page"])}
+        for p in range(kp.shape[0]):
+            if p not in used:
+                assert torch.equal(_bits_t(kp[p]), _bits_t(k0[p]))
+                assert torch.equal(_bits_t(vp[p]), _bits_t(v0[p]))
+    else:
+        others = [b for b in range(B) if b != bi]
+        assert torch.equal(_bits_t(kc[:, others]), _bits_t(k0[:, others]))
+        assert torch.equal(_bits_t(vc[n:, bi]), _bits_t(v0[n:, bi]))
+    # truncate to m rows, append one row: the record holds m rows + the new one
+    m = int(rng.integers(0, n))
+    st.truncate(m)
+    krow = I.round_to(rng.standard_normal(hkv * d), dt).astype(np.float32)
+    vrow = I.round_to(rng.standard_normal(hkv * dv), dt).astype(np.float32)
+    st.append(torch.from_numpy(krow).to(gpu).to(td), torch.from_numpy(vrow).to(gpu).to(td))
+    snap2 = st.snapshot()
+    assert snap2.logical_length == m + 1
+    assert snap2.key == np.concatenate([want_k[:m], krow[None]]).astype("<f4").tobytes()
+    assert snap2.value == np.concatenate([want_v[:m], vrow[None]]).astype("<f4").tobytes()
+    # the record restores into the other layout with the same bytes back
+    if c["paged"]:
+        other = M.DeviceFullAttentionState(
+            torch.zeros((c["cap"], 1, hkv, d), dtype=td, device=gpu),
+            torch.zeros((c["cap"], 1, hkv, dv), dtype=td, device=gpu), layer_index=2)
+    else:
+        page = 8
+        pages = (c["cap"] + page - 1) // page
+        kp2, vp2, table2, _ = _paged_pool(torch, gpu, td, rng, pages, page, hkv, d, dv, 1, pages)
+        other = M.DevicePagedAttentionState(kp2, vp2, table2, layer_index=2)
+    other.restore(snap2)
+    back = other.snapshot()
+    assert (back.key, back.value, back.logical_length) == (snap2.key, snap2.value, m + 1)
