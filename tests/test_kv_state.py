@@ -145,7 +145,8 @@ def test_restore_of_fp32_rows_rounds_to_nearest_even(gpu, dtype):
     if dtype == "bf16":
         want = I.f32_to_bf16_bits(k).view(np.int16)
     else:
-        want = k.astype(np.float16).view(np.int16)
+        with np.errstate(over="ignore"):  # 70000 rounds to +inf in fp16, as on the device
+            want = k.astype(np.float16).view(np.int16)
     assert np.array_equal(_bits(kc[:n, 0]), want)
 
 
