@@ -307,9 +307,9 @@ _workspaces: dict = {}
 # a HIP graph captured while one of them was current keeps its address in
 # its kernel arguments, and replays of that graph still write there.  Were
 # the buffer returned to torch's caching allocator, those replays would
-# overwrite whatever tensor torch handed the memory to next.  Each retired
-# buffer is smaller than its successor, so at most about as much again as
-# the largest workspace is held.
+# overwrite whatever tensor torch handed the memory to next.  Each
+# replacement at least doubles, so the retired buffers together hold less
+# than the current workspace.
 _retired: dict = {}
 
 
@@ -326,9 +326,14 @@ def workspace(torch, device, nbytes: int):
         key = _device_keys.setdefault(device, str(device))
     buf = _workspaces.get(key)
     if buf is None or _workspace_bytes[key] < nbytes:
+        size = max(int(nbytes), 256)
         if buf is not None:
             _retired.setdefault(key, []).append(buf)
-        buf = torch.zeros(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+            # at least double, so the retired buffers together stay below
+            # the current one (a decode loop asks for a little more as its
+            # split count grows with the length)
+            size = max(size, 2 * _workspace_bytes[key])
+        buf = torch.zeros(size, dtype=torch.uint8, device=device)
         _workspaces[key] = buf
         _workspace_bytes[key] = buf.numel()
     return buf

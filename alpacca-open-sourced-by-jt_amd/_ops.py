@@ -306,6 +306,8 @@ def _decode_call(q, key_cache, value_cache, *, length, k_strides, v_strides, bat
         nbytes = L.alpx_decode_workspace_bytes(*sizes)
         if nbytes == 0:
             raise ValueError("invalid decode sizes")
+        if len(_decode_ws_bytes) >= _DECODE_WS_CACHE_MAX:  # a decode loop asks per length
+            _decode_ws_bytes.clear()
         _decode_ws_bytes[sizes] = nbytes
     ws = _lib.workspace(torch, device, nbytes)
     args = [q.data_ptr(), key_cache.data_ptr(), value_cache.data_ptr(), lens_ptr, length,
@@ -350,8 +352,11 @@ def prepare_decode(q, key_cache, value_cache, **kwargs):
 
 
 # alpx_decode_workspace_bytes per (batch, q_heads, kv_heads, value_dim, length):
-# a pure function of the sizes, asked once per shape.
+# a pure function of the sizes, asked once per shape; cleared when it holds
+# _DECODE_WS_CACHE_MAX entries (the length changes every token of a decode
+# loop, so the cache would otherwise grow for the life of the process).
 _decode_ws_bytes: dict = {}
+_DECODE_WS_CACHE_MAX = 1024
 
 
 def sigmoid_gate(values, gate, out_dtype=None):

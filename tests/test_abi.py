@@ -3,6 +3,7 @@ the header declares, and rejects contract violations before touching the
 GPU (no compute calls are made here)."""
 
 import ctypes
+import importlib
 import os
 import re
 
@@ -97,6 +98,41 @@ def test_decode_workspace_sizes(pkg):
     # grows with the number of partial slots, never below the 1-slot size
     one = 3 * 256
     assert lib.alpx_decode_workspace_bytes(1, 1, 1, 64, 1) >= one
+
+
+def test_workspace_growth_is_geometric_and_caches_are_bounded(pkg):
+    # the facade's grow-only workspace (host memory stands in for a device
+    # here): small growth steps, as a decode loop's lengthening plan asks
+    # for, at least double the buffer, so the retired buffers kept for
+    # captured graphs hold less than the current one
+    import torch
+    lib = pkg._lib
+    dev = torch.device("cpu")
+    key = str(dev)
+    try:
+        for n in range(1000, 60000, 700):
+            buf = lib.workspace(torch, dev, n)
+            assert buf.numel() >= n
+        held = sum(b.numel() for b in lib._retired.get(key, []))
+        assert held < lib._workspace_bytes[key]
+        assert len(lib._retired.get(key, [])) <= 7
+        # the decode call's workspace-size cache, asked with a new length
+        # per token as a decode loop does, stays within its bound (the call
+        # is only packed here, never launched)
+        ops = importlib.import_module(pkg.__name__ + "._ops")
+        ops._decode_ws_bytes.clear()
+        q = torch.zeros((1, 8, 64))
+        kc = torch.zeros((3000, 1, 2, 64))
+        for length in range(1, ops._DECODE_WS_CACHE_MAX + 200):
+            ops._decode_call(q, kc, kc, length=length, k_strides=(128, 128, 64),
+                             v_strides=(128, 128, 64), batch=1, kv_heads=2)
+            assert len(ops._decode_ws_bytes) <= ops._DECODE_WS_CACHE_MAX
+    finally:
+        importlib.import_module(pkg.__name__ + "._ops")._decode_ws_bytes.clear()
+        lib._workspaces.pop(key, None)
+        lib._workspace_bytes.pop(key, None)
+        lib._retired.pop(key, None)
+        lib._device_keys.pop(dev, None)
 
 
 def test_facade_validation_mirrors_reference(pkg):
