@@ -399,3 +399,101 @@ def test_paged_layer_prefill_rejects_unsupported(gpu, ops):
     with pytest.raises(ValueError, match="exceeds capacity"):
         ops.paged_attention_layer_prefill_(*args, pw2.key_pages, pw2.value_pages, table,
                                            **dict(kw, position=250))
+
+
+# ------------------------------------------------ seeded random geometry
+
+def _pick(rng, values):
+    return values[int(rng.integers(len(values)))]
+
+
+def _random_paged_cases(n=16):
+    rng = np.random.default_rng(9800)
+    cases = []
+    for i in range(n):
+        dtype = _pick(rng, ["bf16", "f16"])
+        d = _pick(rng, [64, 128, 256])
+        page = _pick(rng, [64, 128, 256])
+        hkv = int(rng.integers(1, 4))
+        batch = int(rng.integers(1, 4))
+        cap = page * int(rng.integers(1, max(2, 1537 // page)))
+        tokens = int(rng.integers(1, min(cap, 300) + 1))
+        sections = _pick(rng, [s for s in ((11, 11, 10, 0), (16, 16, 16, 16), (8, 8, 8, 8),
+                                           (24, 20, 20, 0)) if 2 * sum(s) <= d])
+        c = dict(seed=9800 + i, dtype=dtype, d=d, page=page, hkv=hkv,
+                 hq=hkv * _pick(rng, [1, 2, 4, 8]), batch=batch, bi=int(rng.integers(batch)),
+                 cap=cap, tokens=tokens, prefix=int(rng.integers(0, cap - tokens + 1)),
+                 pos=int(rng.integers(0, cap)), ragged=bool(batch > 1 and rng.random() < 0.5),
+                 gated=bool(rng.random() < 0.5), sections=sections)
+        c["id"] = (f"pg{i:02d}-{dtype}-d{d}-p{page}-q{c['hq']}kv{hkv}-B{batch}s{c['bi']}"
+                   f"-cap{cap}-T{tokens}at{c['prefix']}-step{c['pos']}"
+                   f"{'-ragged' if c['ragged'] else ''}{'-gate' if c['gated'] else ''}")
+        cases.append(c)
+    return cases
+
+
+PAGED_CASES = _random_paged_cases()
+
+
+@pytest.mark.parametrize("c", PAGED_CASES, ids=[c["id"] for c in PAGED_CASES])
+def test_random_paged_paths_equal_contiguous(gpu, ops, override, c):
+    """Seeded random geometry (dtype, head dim, page size, heads, batch,
+    sequence, capacity, chunk, prefix, step position, ragged positions,
+    gate, rotary sections) of the paged extension against the contiguous
+    paths on the same rows of a shuffled page pool, with the contiguous
+    prefill on the single-tile kernel the paged one runs: prefill (oracle
+    too), attention-layer step and attention-layer prefill give the same
+    output bits and write the same rows."""
+    import torch
+    override("prefill_kernel", "single")
+    print("random paged paths:", c["id"], flush=True)
+    rng = np.random.default_rng(c["seed"])
+    dt, d, page, hq, hkv, B, bi, cap = (c["dtype"], c["d"], c["page"], c["hq"], c["hkv"],
+                                        c["batch"], c["bi"], c["cap"])
+    td = _td(torch, dt)
+    ws, pw, table, perm = _fill(torch, ops, gpu, rng, dt, B, cap, hkv, d, page, None)
+    T, P0 = c["tokens"], c["prefix"]
+    # prefill of rows already in both caches
+    q = torch.from_numpy(I.round_to(rng.standard_normal((T, hq, d)), dt)
+                         .astype(np.float32)).to(gpu).to(td)
+    gate = (torch.from_numpy(I.round_to(rng.standard_normal((T, hq, d)) * 2, dt)
+                             .astype(np.float32)).to(gpu).to(td) if c["gated"] else None)
+    want = ops.attention_prefill(q, ws.key_cache, ws.value_cache, position=P0, batch_index=bi,
+                                 gate=gate)
+    got = ops.paged_attention_prefill(q, pw.key_pages, pw.value_pages, table, position=P0,
+                                      batch_index=bi, gate=gate)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16)), c["id"]
+    K = ws.key_cache[:P0 + T, bi].float().cpu().numpy()
+    V = ws.value_cache[:P0 + T, bi].float().cpu().numpy()
+    expect = A.full_attention_prefill(q.float().cpu().numpy(), K, V, prefix_length=P0)
+    if gate is not None:
+        expect = expect / (1.0 + np.exp(-gate.float().cpu().numpy()))
+    assert np.abs(got.float().cpu().numpy() - expect).max() <= 2e-2, c["id"]
+    kw_args = dict(sections=c["sections"], frequency_base=1e7, epsilon=1e-6)
+    # one attention-layer decode step (one row per sequence)
+    pos = c["pos"]
+    positions = (torch.from_numpy(rng.integers(0, pos + 1, B).astype(np.int32)).to(gpu)
+                 if c["ragged"] else None)
+    args = _step_inputs(torch, rng, gpu, dt, B, hq, hkv, d)
+    out_c, n_c = ops.attention_layer_step_(*args, ws.key_cache, ws.value_cache, position=pos,
+                                           positions=positions, **kw_args)
+    out_p, n_p = ops.paged_attention_layer_step_(*args, pw.key_pages, pw.value_pages, table,
+                                                 position=pos, positions=positions, **kw_args)
+    torch.cuda.synchronize()
+    assert n_c == n_p == pos + 1
+    assert torch.equal(out_p.view(torch.int16), out_c.view(torch.int16)), c["id"]
+    # an attention-layer prefill chunk of sequence bi
+    args = _step_inputs(torch, rng, gpu, dt, T, hq, hkv, d)
+    out_c, n_c = ops.attention_layer_prefill_(*args, ws.key_cache, ws.value_cache, position=P0,
+                                              batch_index=bi, **kw_args)
+    out_p, n_p = ops.paged_attention_layer_prefill_(*args, pw.key_pages, pw.value_pages, table,
+                                                    position=P0, batch_index=bi, **kw_args)
+    torch.cuda.synchronize()
+    assert n_c == n_p == P0 + T
+    assert torch.equal(out_p.view(torch.int16), out_c.view(torch.int16)), c["id"]
+    kc = ws.key_cache.view(torch.int16).cpu().numpy()
+    vc = ws.value_cache.view(torch.int16).cpu().numpy()
+    for bb in range(B):
+        assert np.array_equal(_pool_rows(torch, pw.key_pages, perm, bb, cap), kc[:, bb])
+        assert np.array_equal(_pool_rows(torch, pw.value_pages, perm, bb, cap), vc[:, bb])
