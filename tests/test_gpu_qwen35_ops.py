@@ -106,3 +106,77 @@ def test_causal_gqa_step_one_token_returns_its_value_row(q35):
     for h in range(8):
         assert _worst(out[h], V[0][h // 4]) <= 1e-6
     assert all(math.isfinite(x) for row in out for x in row)
+
+
+# ------------------------------------------------ seeded random geometry
+
+def _random_q35_cases():
+    rng = np.random.default_rng(9900)
+    pick = lambda vals: vals[int(rng.integers(len(vals)))]  # noqa: E731
+    steps = [dict(kind="step", seed=9900 + i, dv=int(rng.integers(1, 129)),
+                  dk=int(rng.integers(1, 129))) for i in range(10)]
+    scans = [dict(kind="scan", seed=9920 + i, dv=pick([8, 24, 32, 64]),
+                  dk=pick([64, 128, 40, 7]), t=int(rng.integers(0, 81))) for i in range(8)]
+    gqas = []
+    for i in range(10):
+        hkv = int(rng.integers(1, 5))
+        gqas.append(dict(kind="gqa", seed=9940 + i, hkv=hkv, hq=hkv * pick([1, 2, 4, 5]),
+                         d=pick([3, 16, 64, 100, 128]), dv=pick([5, 16, 64, 128]),
+                         t=int(rng.integers(1, 301)), scale=pick([None, 0.05, 0.3])))
+    for c in steps + scans + gqas:
+        c["id"] = "-".join([c["kind"]] + [f"{k}{v}" for k, v in c.items()
+                                          if k not in ("seed", "kind")])
+    return steps + scans + gqas
+
+
+Q35_CASES = _random_q35_cases()
+
+
+@pytest.mark.parametrize("c", Q35_CASES, ids=[c["id"] for c in Q35_CASES])
+def test_random_list_adapters_against_scalar_oracle(q35, c):
+    """Seeded random sizes of the three list adapters (GDN step, GDN scan --
+    chunked kernels where the key width allows, token by token otherwise --
+    and the causal GQA step with and without a custom scale) against the
+    oracle's scalar fsum forms at the fp32 bar; inputs untouched."""
+    print("random qwen35_ops:", c["id"], flush=True)
+    rng = np.random.default_rng(c["seed"])
+
+    def unit_rows(n, d):
+        x = rng.standard_normal((n, d))
+        return _f32_lists(x / np.linalg.norm(x, axis=1, keepdims=True))
+
+    if c["kind"] == "step":
+        dv, dk = c["dv"], c["dk"]
+        state = _f32_lists(rng.standard_normal((dv, dk)) * 0.3)
+        q, k = unit_rows(1, dk)[0], unit_rows(1, dk)[0]
+        v = _f32_lists(rng.standard_normal(dv))
+        beta = float(np.float32(rng.uniform(0, 1)))
+        g = float(np.float32(-rng.uniform(0, 1.5)))
+        before = copy.deepcopy((state, q, k, v))
+        out, new = q35.gated_delta_net_step(state, q, k, v, beta=beta, log_decay=g)
+        assert (state, q, k, v) == before
+        ref_out, ref_new = G.gdn_step_scalar(state, q, k, v, beta, g)
+        assert _worst(out, ref_out) <= TOL and _worst(new, ref_new) <= TOL
+    elif c["kind"] == "scan":
+        dv, dk, t = c["dv"], c["dk"], c["t"]
+        state = _f32_lists(rng.standard_normal((dv, dk)) * 0.2)
+        qs, ks = unit_rows(t, dk), unit_rows(t, dk)
+        vs = _f32_lists(rng.standard_normal((t, dv)))
+        betas = _f32_lists(rng.uniform(0, 1, t))
+        gs = _f32_lists(-np.exp(rng.uniform(-1, 1, t)) * np.log1p(np.exp(rng.standard_normal(t))))
+        before = copy.deepcopy(state)
+        outs, final = q35.gated_delta_net_scan(state, qs, ks, vs, betas, gs)
+        assert state == before and len(outs) == t
+        ref, worst = state, 0.0
+        for i in range(t):
+            o, ref = G.gdn_step_scalar(ref, qs[i], ks[i], vs[i], betas[i], gs[i])
+            worst = max(worst, _worst(outs[i], o))
+        assert worst <= TOL and _worst(final, ref) <= TOL
+    else:
+        q = _f32_lists(rng.standard_normal((c["hq"], c["d"])))
+        K = _f32_lists(rng.standard_normal((c["t"], c["hkv"], c["d"])))
+        V = _f32_lists(rng.standard_normal((c["t"], c["hkv"], c["dv"])))
+        before = copy.deepcopy((q, K, V))
+        out = q35.causal_gqa_step(q, K, V, scale=c["scale"])
+        assert (q, K, V) == before
+        assert _worst(out, A.causal_gqa_step_scalar(q, K, V, scale=c["scale"])) <= TOL
