@@ -780,3 +780,84 @@ def test_random_recurrent_layer_step_against_oracle(gpu, ops, c):
     print(f"  output {worst:.3g}, state {err_s:.3g} (bar 1e-4)", flush=True)
     assert worst <= 1e-4 and err_s <= 1e-4, (c["id"], worst, err_s)
     assert np.array_equal(ws.convolution_history.cpu().numpy(), hist.astype(np.float32))
+
+
+def _random_norm_cases(n=24):
+    rng = np.random.default_rng(9700)
+    widths = [int(rng.integers(1, 129)), int(rng.integers(129, 257)),
+              int(rng.integers(257, 513)), int(rng.integers(513, 1200))]
+    cases = []
+    for i in range(n):
+        c = dict(seed=9700 + i, dtype=_pick(rng, ["f32", "bf16", "f16"]),
+                 n=widths[i % 4] if i < 8 else int(rng.integers(1, 1200)),
+                 rows=int(rng.integers(1, 70)), eps=_pick(rng, [1e-6, 1e-5]))
+        c["id"] = f"norm{i:02d}-{c['dtype']}-n{c['n']}-rows{c['rows']}"
+        cases.append(c)
+    return cases
+
+
+NORM_CASES = _random_norm_cases()
+
+
+@pytest.mark.parametrize("c", NORM_CASES, ids=[c["id"] for c in NORM_CASES])
+def test_random_row_norms_against_oracle(gpu, ops, c):
+    """Seeded random row widths (every width class the kernel dispatches on:
+    up to 128, 256 and 512 values per row held in registers, wider rows in a
+    strided loop), row counts and dtypes of the L2, RMS and gated RMS norms
+    against the oracle, at the dtype's bar plus one unit in the last place
+    of the output's format (|2^-7 x| for bf16, |2^-10 x| for fp16)."""
+    import torch
+    print("random row norms:", c["id"], flush=True)
+    rng = np.random.default_rng(c["seed"])
+    dt, n = c["dtype"], c["n"]
+    x = I.round_to(rng.standard_normal((c["rows"], n)) * 2.0, dt)
+    w = rng.uniform(0.5, 1.5, n).astype(np.float32)
+    gt = I.round_to(rng.standard_normal((c["rows"], n)), dt)
+    X, G_ = _dev(torch, x, dt, gpu), _dev(torch, gt, dt, gpu)
+    W = torch.from_numpy(w).to(gpu)
+    tol = _tol(dt)
+    # normalised rows reach |4-8| (RMS x weight) and past 16 (x silu(gate)),
+    # where one unit in the last place of bf16 is 2^-5 to 2^-3: the bar is
+    # the dtype's tolerance plus one unit in the last place of the output
+    ulp = {"f32": 0.0, "f16": 2.0 ** -10, "bf16": 2.0 ** -7}[dt]
+
+    def err(got, ref):
+        return float((np.abs(_np(got) - ref) - ulp * np.abs(ref)).max())
+    errs = (err(ops.rms_norm(X, W, c["eps"]), L.rms_norm(x, w, c["eps"])),
+            err(ops.l2_normalize(X, c["eps"]), L.l2_normalize(x, c["eps"])),
+            err(ops.recurrent_gate(X, W, G_, c["eps"]), L.gated_rms_norm(x, w, gt, c["eps"])))
+    print("  beyond one output ulp: rms %.3g, l2 %.3g, gated %.3g (bar %g)" % (*errs, tol),
+          flush=True)
+    assert max(errs) <= tol, (c["id"], errs)
+
+
+def _random_conv_cases(n=12):
+    rng = np.random.default_rng(9750)
+    return [dict(seed=9750 + i, kernel=int(rng.integers(1, 7)), batch=int(rng.integers(1, 5)),
+                 channels=int(rng.integers(1, 9000)),
+                 id=f"conv{i:02d}") for i in range(n)]
+
+
+CONV_CASES = _random_conv_cases()
+for _c in CONV_CASES:
+    _c["id"] += f"-taps{_c['kernel']}-B{_c['batch']}-C{_c['channels']}"
+
+
+@pytest.mark.parametrize("c", CONV_CASES, ids=[c["id"] for c in CONV_CASES])
+def test_random_conv_step_against_oracle(gpu, ops, c):
+    """Seeded random taps (1-6), batch and channel counts of the depthwise
+    causal convolution step: output at 1e-4, the history shift bit for
+    bit."""
+    import torch
+    print("random conv step:", c["id"], flush=True)
+    rng = np.random.default_rng(c["seed"])
+    b, ch, kernel = c["batch"], c["channels"], c["kernel"]
+    cur = rng.standard_normal((b, ch)).astype(np.float32)
+    w = rng.standard_normal((kernel, ch)).astype(np.float32)
+    hist = rng.standard_normal((b, kernel - 1, ch)).astype(np.float32)
+    H = torch.from_numpy(hist).to(gpu)
+    out = ops.causal_convolution_step_(torch.from_numpy(cur).to(gpu),
+                                       torch.from_numpy(w).to(gpu), H)
+    ref, new_hist = L.conv_step(cur, w, hist)
+    assert np.abs(out.cpu().numpy() - ref).max() <= 1e-4, c["id"]
+    assert np.array_equal(H.cpu().numpy(), new_hist.astype(np.float32)), c["id"]
