@@ -14,6 +14,8 @@ Same names, argument order and layouts as the reference (qwen35_kernels.py):
   (:261-274), ``qwen35_normalize_qk`` (:277-287), ``qwen35_beta_decay``
   (:290-307), ``qwen35_gated_rms`` (:335-352) and
   ``qwen35_recurrent_layer`` (:349-360)
+* ``qwen35_state_copy_restore(source, target)`` (:414-425) and
+  ``diagnostics()`` (:428-445)
 
 NumPy in -> NumPy out (upload, compute on the device, download); torch
 device tensors in -> device tensor out.  All arithmetic runs in libalpx.so.
@@ -179,6 +181,45 @@ def qwen35_recurrent_layer(state_matrix, queries, keys, values, beta_logits, alp
     return qwen35_gated_rms(output, norm_weight, gates, epsilon), queries, keys
 
 
-__all__ = ["available", "backend_name", "qwen35_beta_decay", "qwen35_conv_step",
+def qwen35_state_copy_restore(source, target):
+    """Copy a recurrent state into ``target`` and return it
+    (qwen35_kernels.py:414-425, same checks and messages): ``target`` is a
+    float32 NumPy array of ``source``'s shape, overwritten in place.  The
+    state lives in host memory, so the copy stays there (the reference's
+    accelerated path is the same copy, spread over threads).  Extension: a
+    float32 torch device tensor as ``target`` is filled on its device."""
+    import numpy as np
+    torch = _host.torch_mod() if not isinstance(target, np.ndarray) else None
+    if torch is not None and torch.is_tensor(target) and target.dtype == torch.float32:
+        src = source if torch.is_tensor(source) else torch.from_numpy(
+            np.ascontiguousarray(source, dtype=np.float32))
+        if tuple(src.shape) != tuple(target.shape):
+            raise ValueError(f"state restore shapes differ: {tuple(src.shape)} != "
+                             f"{tuple(target.shape)}")
+        target.copy_(src.to(device=target.device, dtype=torch.float32))
+        return target
+    src = np.ascontiguousarray(source, dtype=np.float32)
+    if getattr(target, "dtype", None) is None or target.dtype.name != "float32":
+        raise ValueError("state restore target must be a float32 NumPy array")
+    if src.shape != target.shape:
+        raise ValueError(f"state restore shapes differ: {src.shape} != {target.shape}")
+    np.copyto(target, src)
+    return target
+
+
+def diagnostics() -> dict:
+    """What this backend runs on (qwen35_kernels.py:428-445 reports its
+    numba build the same way): availability, backend name, the library and
+    its ABI version, and the device architecture when a device is there."""
+    info = {"available": available(), "backend": backend_name(), "library": _lib.LIB_PATH,
+            "abi_version": _lib.ABI_VERSION}
+    if info["available"]:
+        torch = _host.torch_mod()
+        info["device"] = _lib.device_arch(torch.cuda.current_device())
+    return info
+
+
+__all__ = ["available", "backend_name", "diagnostics", "qwen35_beta_decay", "qwen35_conv_step",
            "qwen35_full_attention_decode", "qwen35_full_attention_prefill", "qwen35_gated_rms",
-           "qwen35_gdn_step", "qwen35_normalize_qk", "qwen35_recurrent_layer"]
+           "qwen35_gdn_step", "qwen35_normalize_qk", "qwen35_recurrent_layer",
+           "qwen35_state_copy_restore"]

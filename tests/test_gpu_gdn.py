@@ -204,3 +204,16 @@ def test_chunked_fp32_agrees_with_token_by_token(gpu, ops, override):
     torch.cuda.synchronize()
     assert (o1 - o2).abs().max().item() <= 1e-4
     assert (S1 - S2).abs().max().item() <= 1e-4
+
+
+def test_qwen35_kernels_diagnostics_and_device_state_restore(gpu):
+    # on the device the drop-in reports itself available on gfx950, and a
+    # state restore into a device tensor copies the bits
+    import torch
+    K = importlib.import_module("alpacca-open-sourced-by-jt_amd.qwen35_kernels")
+    info = K.diagnostics()
+    assert info["available"] is True and info["device"].startswith("gfx950")
+    src = np.random.default_rng(3).standard_normal((4, 16, 8)).astype(np.float32)
+    tgt = torch.zeros((4, 16, 8), device=gpu)
+    assert K.qwen35_state_copy_restore(src, tgt) is tgt
+    assert np.array_equal(tgt.cpu().numpy(), src)

@@ -1,6 +1,7 @@
 """CPU checks of the ``qwen35_ops`` drop-in's contract validation: the same
 exception types and messages as the reference (qwen35_ops.py:318-345,
-381-390, 436-460), raised before any device work (no GPU needed)."""
+381-390, 436-460), raised before any device work (no GPU needed); and the
+``qwen35_kernels`` state copy / diagnostics helpers, which need no device."""
 
 import importlib
 
@@ -67,3 +68,30 @@ def test_causal_gqa_step_validation(q35):
         q35.causal_gqa_step(q, K, [[[1.0]] * 2] * 2 + [[[1.0, 2.0]] * 2])
     with pytest.raises(ValueError, match="scale must be positive and finite"):
         q35.causal_gqa_step(q, K, V, scale=0.0)
+
+
+def test_qwen35_kernels_state_copy_restore_and_diagnostics():
+    """qwen35_kernels.qwen35_state_copy_restore keeps the reference's checks
+    and messages (qwen35_kernels.py:414-425) and copies in place;
+    diagnostics() reports the backend whether or not a device is there."""
+    import numpy as np
+    import torch
+    K = importlib.import_module("alpacca-open-sourced-by-jt_amd.qwen35_kernels")
+    src = np.arange(24, dtype=np.float64).reshape(2, 3, 4) / 7.0
+    tgt = np.zeros((2, 3, 4), dtype=np.float32)
+    assert K.qwen35_state_copy_restore(src, tgt) is tgt
+    assert np.array_equal(tgt, src.astype(np.float32))
+    with pytest.raises(ValueError, match="must be a float32 NumPy array"):
+        K.qwen35_state_copy_restore(src, np.zeros((2, 3, 4), dtype=np.float64))
+    with pytest.raises(ValueError, match="must be a float32 NumPy array"):
+        K.qwen35_state_copy_restore(src, [[0.0]])
+    with pytest.raises(ValueError, match="shapes differ"):
+        K.qwen35_state_copy_restore(src, np.zeros((2, 3, 5), dtype=np.float32))
+    t = torch.zeros((2, 3, 4))
+    assert K.qwen35_state_copy_restore(src, t) is t
+    assert np.array_equal(t.numpy(), src.astype(np.float32))
+    info = K.diagnostics()
+    assert info["backend"] == K.backend_name() and isinstance(info["available"], bool)
+    assert info["abi_version"] == importlib.import_module(
+        "alpacca-open-sourced-by-jt_amd._lib").ABI_VERSION
+    assert "diagnostics" in K.__all__ and "qwen35_state_copy_restore" in K.__all__
