@@ -381,8 +381,8 @@ def _gdn_chunk_flops(hv, T, C, dk, dv):
     return hv * (T // C) * (2 * C * C * (2 * dk + 2 * dv + C) + 6 * C * dk * dv)
 
 
-# C5 prefill FLOPs as the baseline counts them: per (head,
-# chunk) 2 C^2 (3 Dk + 2 Dv) + 6 C Dk Dv, 32 heads x 16 chunks of 64
+# C5 prefill FLOPs as the headline metric's baseline counts them: per
+# (head, chunk) 2 C^2 (3 Dk + 2 Dv) + 6 C Dk Dv, 32 heads x 16 chunks of 64
 C5_BASELINE_FLOPS = 32 * 16 * (2 * 64 * 64 * (3 * 128 + 2 * 128) + 6 * 64 * 128 * 128)
 
 
