@@ -295,3 +295,60 @@ def test_numpy_drop_ins_fp32(gpu):
     assert np.abs(seam.reshape(24, 8, 64) - ref).max() <= 1e-4
     # non-contiguous positions: the seam declines, as the reference's does
     assert _mod("cuda").attention_batch(c["q"], K, V, np.arange(24) * 2, 4, 0.125) is None
+
+
+# ------------------------------------------------ seeded random geometry
+
+def _random_seam_cases(n=20):
+    rng = np.random.default_rng(9850)
+    pick = lambda vals: vals[int(rng.integers(len(vals)))]  # noqa: E731
+    cases = []
+    for i in range(n):
+        t_kv = int(rng.integers(1, 600))
+        kv_start = int(rng.integers(0, 300)) if rng.random() < 0.4 else 0
+        t_q = int(rng.integers(1, 200))
+        c = dict(seed=9850 + i, dtype=pick(["f32", "f32", "f16"]), hd=pick([16, 40, 64, 128, 256]),
+                 n_kv=int(rng.integers(1, 5)), group=int(rng.integers(1, 6)), t_kv=t_kv,
+                 t_q=t_q, kv_start=kv_start,
+                 p0=int(rng.integers(max(0, kv_start - 20), kv_start + t_kv + 5)),
+                 window=0 if rng.random() < 0.6 else int(rng.integers(1, 400)),
+                 inv_sqrt=pick([None, 0.05, 0.2]))
+        c["id"] = (f"seam{i:02d}-{c['dtype']}-hd{c['hd']}-kv{c['n_kv']}x{c['group']}-Tq{t_q}"
+                   f"-Tkv{t_kv}-p{c['p0']}-s{kv_start}-w{c['window']}")
+        cases.append(c)
+    return cases
+
+
+SEAM_CASES = _random_seam_cases()
+
+
+@pytest.mark.parametrize("c", SEAM_CASES, ids=[c["id"] for c in SEAM_CASES])
+def test_random_attention_batch_seam_against_oracle(gpu, c):
+    """Seeded random geometry of the llama batched-attention seam
+    (cuda.attention_batch, cuda.py:1186-1244 / model.py:1254-1272,
+    1567-1592): NumPy fp32 or fp16 caches, head dims from 16 to 256, GQA
+    groups, absolute positions that start before, inside or past the keys,
+    kv_start and sliding windows (rows with no visible key are zeros)
+    against the oracle; positions that are not contiguous and head dims past
+    256 are declined with None."""
+    print("random attention_batch seam:", c["id"], flush=True)
+    rng = np.random.default_rng(c["seed"])
+    seam = _mod("cuda")
+    nd = np.float16 if c["dtype"] == "f16" else np.float32
+    n_head = c["n_kv"] * c["group"]
+    q = rng.standard_normal((c["t_q"], n_head, c["hd"])).astype(nd)
+    K = rng.standard_normal((c["t_kv"], c["n_kv"], c["hd"])).astype(nd)
+    V = rng.standard_normal((c["t_kv"], c["n_kv"], c["hd"])).astype(nd)
+    inv = c["inv_sqrt"] if c["inv_sqrt"] is not None else 1.0 / np.sqrt(c["hd"])
+    pos = c["p0"] + np.arange(c["t_q"])
+    out = seam.attention_batch(q, K, V, pos, c["group"], inv, window=c["window"],
+                               kv_start=c["kv_start"])
+    assert out is not None and out.shape == (c["t_q"], n_head * c["hd"]), c["id"]
+    ref = A.attention_batch(q.astype(np.float32), K.astype(np.float32), V.astype(np.float32), pos,
+                            c["group"], inv, window=c["window"], kv_start=c["kv_start"])
+    tol = 1e-4 if c["dtype"] == "f32" else 2e-2
+    err = float(np.abs(np.asarray(out, dtype=np.float64) - ref.reshape(c["t_q"], -1)).max())
+    print(f"  max abs error {err:.3g} (bar {tol:g})", flush=True)
+    assert err <= tol, (c["id"], err)
+    if c["t_q"] > 1:
+        assert seam.attention_batch(q, K, V, pos[::-1].copy(), c["group"], inv) is None
