@@ -117,21 +117,96 @@ __device__ __forceinline__ void norm_row(const NormArgs& a, int64_t r, int lane)
   }
 }
 
+// kNormRows consecutive rows of at most 128 values by one wave: the loads of
+// every row (and the weight, once) are issued before the first reduction,
+// then each row is reduced and written with norm_row_regs's arithmetic
+// (lane l owns elements l and l + 64, summed in that order): the same bits
+// with a quarter of the waves, each with four rows' loads in flight.
+constexpr int kNormRows = 4;
+
 template <typename T, typename TO, int MODE>
+__device__ __forceinline__ void norm_rows_128(const NormArgs& a, int64_t r0, int lane) {
+  constexpr int NPL = 2, R = kNormRows;
+  float xv[R][NPL], wv[NPL], gv[R][NPL];
+#pragma unroll
+  for (int j = 0; j < NPL; ++j)
+    if constexpr (MODE != kNormL2) wv[j] = a.w[min(lane + 64 * j, a.n - 1)];
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    const int64_t r = min(r0 + k, a.rows - 1);
+    const T* x = (const T*)a.x + (r / a.grp_rows) * a.grp_stride + (r % a.grp_rows) * a.n;
+    const T* g = (const T*)a.gate + r * a.n;
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) {
+      const int i = min(lane + 64 * j, a.n - 1);
+      xv[k][j] = to_f32(x[i]);
+      if constexpr (MODE == kNormRmsGate) gv[k][j] = to_f32(g[i]);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    const int64_t r = r0 + k;
+    if (r >= a.rows) break;  // uniform across the wave
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < NPL; ++j)
+      if (lane + 64 * j < a.n) ss = fmaf(xv[k][j], xv[k][j], ss);
+    ss = wave_sum(ss);
+    const float den =
+        MODE == kNormL2 ? fmaxf(sqrtf(ss), a.eps) : sqrtf(ss / (float)a.n + a.eps);
+    TO* o = (TO*)a.out + r * a.n;
+#pragma unroll
+    for (int j = 0; j < NPL; ++j) {
+      const int i = lane + 64 * j;
+      if (i < a.n) {
+        float v = xv[k][j] / den;
+        if constexpr (MODE != kNormL2) v *= wv[j];
+        if constexpr (MODE == kNormRmsGate) v *= silu_f(gv[k][j]);
+        o[i] = from_f32<TO>(v);
+      }
+    }
+  }
+}
+
+// ROWS = 1: one row per wave, any width; ROWS = kNormRows: rows of at most
+// 128 values, kNormRows per wave (many-row calls: a prefill chunk's norms).
+template <typename T, typename TO, int MODE, int ROWS>
 __global__ void __launch_bounds__(256) row_norm_kernel(NormArgs a) {
-  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t r = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * ROWS;
   if (r >= a.rows) return;  // the whole wave leaves together
-  norm_row<T, TO, MODE>(a, r, threadIdx.x & 63);
+  if constexpr (ROWS == 1)
+    norm_row<T, TO, MODE>(a, r, threadIdx.x & 63);
+  else
+    norm_rows_128<T, TO, MODE>(a, r, threadIdx.x & 63);
+}
+
+// Calls with at least this many rows of at most 128 values take the
+// several-rows-per-wave kernel (fewer rows keep one row per wave, for
+// parallelism).
+constexpr int64_t kNormManyRows = 4096;
+
+template <typename T, typename TO, int ROWS>
+void launch_norm_rows(const NormArgs& a, int mode, hipStream_t s) {
+  const dim3 grid((unsigned)((a.rows + 4 * ROWS - 1) / (4 * ROWS)));
+  switch (mode) {
+    case kNormL2:
+      hipLaunchKernelGGL((row_norm_kernel<T, TO, kNormL2, ROWS>), grid, dim3(256), 0, s, a);
+      break;
+    case kNormRms:
+      hipLaunchKernelGGL((row_norm_kernel<T, TO, kNormRms, ROWS>), grid, dim3(256), 0, s, a);
+      break;
+    default:
+      hipLaunchKernelGGL((row_norm_kernel<T, TO, kNormRmsGate, ROWS>), grid, dim3(256), 0, s, a);
+      break;
+  }
 }
 
 template <typename T, typename TO>
 int launch_norm(const NormArgs& a, int mode, hipStream_t s) {
-  const dim3 grid((unsigned)((a.rows + 3) / 4));
-  switch (mode) {
-    case kNormL2: hipLaunchKernelGGL((row_norm_kernel<T, TO, kNormL2>), grid, dim3(256), 0, s, a); break;
-    case kNormRms: hipLaunchKernelGGL((row_norm_kernel<T, TO, kNormRms>), grid, dim3(256), 0, s, a); break;
-    default: hipLaunchKernelGGL((row_norm_kernel<T, TO, kNormRmsGate>), grid, dim3(256), 0, s, a); break;
-  }
+  if (a.n <= 128 && a.rows >= kNormManyRows)
+    launch_norm_rows<T, TO, kNormRows>(a, mode, s);
+  else
+    launch_norm_rows<T, TO, 1>(a, mode, s);
   return check_launch("alpx_row_norm");
 }
 

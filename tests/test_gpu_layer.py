@@ -861,3 +861,35 @@ def test_random_conv_step_against_oracle(gpu, ops, c):
     ref, new_hist = L.conv_step(cur, w, hist)
     assert np.abs(out.cpu().numpy() - ref).max() <= 1e-4, c["id"]
     assert np.array_equal(H.cpu().numpy(), new_hist.astype(np.float32)), c["id"]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_many_row_norms_equal_one_row_per_wave(gpu, dtype):
+    """Calls of many rows of at most 128 values run four rows per wave; the
+    same rows in calls of fewer rows run one row per wave.  The per-row
+    arithmetic is the same, so every mode gives the same bits either way."""
+    import torch
+    ops_mod = _mod("_ops")
+    lib = _mod("_lib")
+    rng = np.random.default_rng(31)
+    rows, n = 8192 + 3, 128
+    x = _dev(torch, I.round_to(rng.standard_normal((rows, n)) * 2.0, dtype), dtype, gpu)
+    g = _dev(torch, I.round_to(rng.standard_normal((rows, n)), dtype), dtype, gpu)
+    w = torch.from_numpy(rng.uniform(0.5, 1.5, n).astype(np.float32)).to(gpu)
+    for mode in (lib.NORM_L2, lib.NORM_RMS, lib.NORM_RMS_GATE):
+        kw = dict(mode=mode, eps=1e-6, n=n)
+        if mode != lib.NORM_L2:
+            kw["weight"] = w
+        if mode == lib.NORM_RMS_GATE:
+            kw["gate"] = g
+        whole = ops_mod.row_norm(x, rows=rows, **kw)
+        parts = []
+        for r0 in range(0, rows, 2048):
+            r1 = min(rows, r0 + 2048)
+            kp = dict(kw)
+            if mode == lib.NORM_RMS_GATE:
+                kp["gate"] = g[r0:r1]
+            parts.append(ops_mod.row_norm(x[r0:r1], rows=r1 - r0, **kp))
+        torch.cuda.synchronize()
+        bits = torch.int32 if dtype == "f32" else torch.int16
+        assert torch.equal(whole.view(bits), torch.cat(parts).view(bits)), mode
