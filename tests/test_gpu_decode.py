@@ -6,7 +6,6 @@ Tolerances: fp32 max abs error <= 1e-4; fp16/bf16 <= 2e-2 (fp32 accumulation).
 """
 
 import importlib
-import math
 
 import numpy as np
 import pytest

@@ -17,7 +17,6 @@ import importlib
 import numpy as np
 import pytest
 
-from oracle import attention as A
 from oracle import gdn as G
 from oracle import inputs as I
 from oracle import layer as L
