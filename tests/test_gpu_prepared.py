@@ -160,3 +160,112 @@ def test_prepared_decode_per_call_length(gpu):
         assert torch.equal(got, want), n
     with pytest.raises(ValueError, match="outside"):
         step(cap + 1)
+
+
+# ------------------------------------------------ seeded random geometry
+
+def _random_prepared_cases():
+    rng = np.random.default_rng(9960)
+    pick = lambda vals: vals[int(rng.integers(len(vals)))]  # noqa: E731
+    cases = []
+    for i in range(6):
+        hkv = int(rng.integers(1, 4))
+        cases.append(dict(kind="decode", seed=9960 + i, dtype=pick(["bf16", "f16", "f32"]),
+                          d=pick([64, 128, 256, 80]), hkv=hkv, hq=hkv * pick([1, 4, 8]),
+                          batch=int(rng.integers(1, 5)), cap=int(rng.integers(64, 3000)),
+                          gated=bool(rng.random() < 0.5)))
+    for i in range(4):
+        hk = int(rng.integers(1, 4))
+        cases.append(dict(kind="gdn", seed=9970 + i, dtype=("bf16", "f32")[i % 2],
+                          dk=pick([64, 128, 40]), dv=pick([32, 64, 128]), hk=hk,
+                          hv=hk * int(rng.integers(1, 3)), batch=int(rng.integers(1, 4))))
+    for i in range(4):
+        hk = int(rng.integers(1, 3))
+        cases.append(dict(kind="recurrent", seed=9980 + i, dk=pick([64, 128]), dv=pick([32, 64]),
+                          hk=hk, hv=hk * int(rng.integers(1, 3)), batch=int(rng.integers(1, 3)),
+                          taps=pick([2, 4])))
+    for c in cases:
+        c["id"] = "-".join([c["kind"]] + [f"{k}{v}" for k, v in c.items()
+                                          if k not in ("kind", "seed")])
+    return cases
+
+
+PREP_CASES = _random_prepared_cases()
+
+
+@pytest.mark.parametrize("c", PREP_CASES, ids=[c["id"] for c in PREP_CASES])
+def test_random_prepared_calls_equal_immediate(gpu, ops, c):
+    """Seeded random geometry of the three prepared step calls against the
+    immediate methods over five steps with fresh inputs copied into the
+    bound buffers (the decode also attends a different row count and fresh
+    device lengths each step): outputs and advanced states bit for bit."""
+    import torch
+    print("random prepared call:", c["id"], flush=True)
+    rng = np.random.default_rng(c["seed"])
+    g = torch.Generator(device=gpu).manual_seed(c["seed"])
+    td = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}.get(
+        c.get("dtype", "f32"))
+
+    def bits(t):
+        return t.view(torch.int16) if t.element_size() == 2 else t.view(torch.int32)
+
+    if c["kind"] == "decode":
+        B, cap, hq, hkv, d = c["batch"], c["cap"], c["hq"], c["hkv"], c["d"]
+        K = torch.randn((cap, B, hkv, d), generator=g, device=gpu).to(td)
+        V = torch.randn((cap, B, hkv, d), generator=g, device=gpu).to(td)
+        q = torch.empty((B, hq, d), device=gpu, dtype=td)
+        gate = torch.empty((B, hq, d), device=gpu, dtype=td) if c["gated"] else None
+        lens = torch.full((B,), cap, dtype=torch.int32, device=gpu)
+        step = ops.prepare_online_attention(q, K, V, length=cap, seq_lens=lens, gate=gate)
+        for t in range(5):
+            q.copy_(torch.randn(q.shape, generator=g, device=gpu))
+            if gate is not None:
+                gate.copy_(torch.randn(gate.shape, generator=g, device=gpu))
+            lens.copy_(torch.from_numpy(rng.integers(1, cap + 1, B).astype(np.int32)).to(gpu))
+            want = ops.online_attention(q, K, V, length=cap, seq_lens=lens, gate=gate)
+            got = step()
+            torch.cuda.synchronize()
+            assert torch.equal(bits(got), bits(want)), (c["id"], t)
+        return
+    if c["kind"] == "gdn":
+        B, hk, hv, dk, dv = c["batch"], c["hk"], c["hv"], c["dk"], c["dv"]
+        S_a = torch.randn((B, hv, dv, dk), generator=g, device=gpu) * 0.1
+        S_b = S_a.clone()
+        q = torch.empty((B, hk, dk), device=gpu, dtype=td)
+        k, v = torch.empty_like(q), torch.empty((B, hv, dv), device=gpu, dtype=td)
+        beta, gl = torch.empty((B, hv), device=gpu), torch.empty((B, hv), device=gpu)
+        step = ops.prepare_gated_delta_net_step_(S_b, q, k, v, beta, gl)
+        for t in range(5):
+            for x in (q, k):
+                x.copy_(torch.nn.functional.normalize(
+                    torch.randn(x.shape, generator=g, device=gpu), dim=-1))
+            v.copy_(torch.randn(v.shape, generator=g, device=gpu))
+            beta.copy_(torch.rand(beta.shape, generator=g, device=gpu))
+            gl.copy_(-torch.rand(gl.shape, generator=g, device=gpu))
+            want = ops.gated_delta_net_step_(S_a, q, k, v, beta, gl)
+            got = step()
+            torch.cuda.synchronize()
+            assert torch.equal(bits(got), bits(want)) and torch.equal(S_a, S_b), (c["id"], t)
+        return
+    B, hk, hv, dk, dv, taps = c["batch"], c["hk"], c["hv"], c["dk"], c["dv"], c["taps"]
+    chn = 2 * hk * dk + hv * dv
+    wss = [ops.initialize_recurrent_workspace(batch_size=B, convolution_kernel=taps,
+                                              convolution_channels=chn, value_heads=hv,
+                                              value_dimension=dv, key_dimension=dk)
+           for _ in range(2)]
+    f = lambda *s: torch.randn(s, generator=g, device=gpu)  # noqa: E731
+    w, dt = f(taps, chn) * 0.5, f(hv)
+    ssm = -torch.exp(torch.rand(hv, generator=g, device=gpu) * 2 - 1)
+    nw = torch.rand(dv, generator=g, device=gpu) + 0.5
+    mixed, gate, bl, al = f(B, chn), f(B, hv * dv), f(B, hv), f(B, hv)
+    kw = dict(key_heads=hk, key_dimension=dk, epsilon=1e-6)
+    step = ops.prepare_recurrent_layer_step_(wss[1], mixed, w, gate, bl, al, dt, ssm, nw, **kw)
+    for t in range(5):
+        for x in (mixed, gate, bl, al):
+            x.copy_(torch.randn(x.shape, generator=g, device=gpu))
+        want = ops.recurrent_layer_step_(wss[0], mixed, w, gate, bl, al, dt, ssm, nw, **kw)
+        got = step()
+        torch.cuda.synchronize()
+        assert torch.equal(bits(got), bits(want)), (c["id"], t)
+        assert torch.equal(wss[0].delta_state, wss[1].delta_state), (c["id"], t)
+        assert torch.equal(wss[0].convolution_history, wss[1].convolution_history), (c["id"], t)
