@@ -115,3 +115,45 @@ def test_noalloc_decode_rejects_plans_beyond_the_scratch(gpu):
     assert "static" in L.last_error()
     torch.cuda.synchronize()
     assert bool((out == 0).all())  # nothing was enqueued
+
+
+def _random_noalloc_cases(n=10):
+    rng = np.random.default_rng(9995)
+    pick = lambda vals: vals[int(rng.integers(len(vals)))]  # noqa: E731
+    cases = []
+    for i in range(n):
+        hkv = int(rng.integers(1, 5))
+        cases.append(dict(seed=9995 + i, dtype=pick(["f16", "bf16", "f32"]),
+                          d=pick([64, 128, 256, 80]), hkv=hkv, hq=hkv * pick([1, 2, 4, 8]),
+                          batch=int(rng.integers(1, 9)), cap=int(rng.integers(1, 4097)),
+                          ragged=bool(rng.random() < 0.5), gated=bool(rng.random() < 0.4)))
+    return cases
+
+
+NA_CASES = _random_noalloc_cases()
+
+
+@pytest.mark.parametrize("c", NA_CASES, ids=[
+    f"na{i}-{c['dtype']}-d{c['d']}-q{c['hq']}kv{c['hkv']}-B{c['batch']}-cap{c['cap']}"
+    f"{'-ragged' if c['ragged'] else ''}{'-gate' if c['gated'] else ''}"
+    for i, c in enumerate(NA_CASES)])
+def test_random_noalloc_calls_equal_workspace_calls(gpu, c):
+    """Seeded random geometry, one call after another on the shared static
+    array (sizes of at most 8 sequences x 4096 rows, whose partials of any
+    plan fit the array, so both entry points plan the same split): the
+    no-alloc output equals the workspace entry point's bit for bit."""
+    import torch
+    L = _lib()
+    print("random no-alloc:", c, flush=True)
+    g = torch.Generator(device=gpu).manual_seed(c["seed"])
+    td = {"f16": torch.float16, "bf16": torch.bfloat16, "f32": torch.float32}[c["dtype"]]
+    b, hq, hkv, d, cap = c["batch"], c["hq"], c["hkv"], c["d"], c["cap"]
+    K = torch.randn((cap, b, hkv, d), generator=g, device=gpu).to(td)
+    V = torch.randn((cap, b, hkv, d), generator=g, device=gpu).to(td)
+    q = torch.randn((b, hq, d), generator=g, device=gpu).to(td)
+    gate = torch.randn((b, hq, d), generator=g, device=gpu).to(td) if c["gated"] else None
+    lens = (torch.randint(1, cap + 1, (b,), generator=g, device=gpu, dtype=torch.int32)
+            if c["ragged"] else None)
+    ws_out, na_out = _decode_both(torch, L, q, K, V, lens, cap, gate, hkv)
+    assert torch.equal(ws_out.view(torch.int32), na_out.view(torch.int32))
+    assert bool(torch.isfinite(na_out).all())
